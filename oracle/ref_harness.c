@@ -1,0 +1,106 @@
+/*
+ * ref_harness.c — exposes the reference's static MoE functions for golden
+ * vectors. TEST INFRASTRUCTURE ONLY, built into oracle/_ref/ by
+ * oracle/Makefile from the reference sources where they lie (nothing is
+ * copied): this file includes the reference's src/model.c so that its
+ * static vq_build_lut, vq_apply, vq_matvec, moe_layer and moe_chunk can be
+ * called on a model loaded by waste_model_load from a synthetic container.
+ * Built with the flags the reference gives model.c (-O2 -std=gnu11).
+ */
+#include "model.c"
+
+void *ref_open(const char *dir, size_t cache_bytes)
+{
+    waste_model *m = (waste_model *)calloc(1, sizeof *m);
+    if (!m) return NULL;
+    waste_load_opts o;
+    memset(&o, 0, sizeof o);
+    o.cache_bytes = cache_bytes;
+    o.direct_io = 0;
+    o.n_threads = 1;
+    if (waste_model_load(m, dir, 64, &o) != 0) { free(m); return NULL; }
+    /* the router's scratch must still hold this layer's logits and scores
+     * when moe_layer returns, so no lookahead into it; set after the load,
+     * whose one-time option parsing would otherwise reset it */
+    waste_model_set_lookahead(0);
+    return m;
+}
+
+void ref_close(void *p)
+{
+    waste_model *m = (waste_model *)p;
+    if (m) { waste_model_free(m); free(m); }
+}
+
+const char *ref_backend(void) { return waste_backend_name(); }
+
+int ref_read_error(void *p) { return ((waste_model *)p)->read_error; }
+
+/* moe_layer for one token. logits/scores get n_experts floats each. */
+int ref_moe_layer(void *p, int L, const float *in, float *out, int *routed,
+                  float *logits, float *scores)
+{
+    waste_model *m = (waste_model *)p;
+    const int E = m->cfg.n_experts;
+    moe_layer(m, L, in, out, routed);
+    const float *sc = m->att + WASTE_ATT_ROUTER_OFF;
+    if (logits) memcpy(logits, sc, (size_t)E * sizeof(float));
+    if (scores) memcpy(scores, sc + E, (size_t)E * sizeof(float));
+    return m->read_error;
+}
+
+/* moe_chunk over nT tokens; route/rw receive [nT][top_k]. */
+int ref_moe_chunk(void *p, int L, const float *in, float *out, int nT, int *route,
+                  float *rw)
+{
+    waste_model *m = (waste_model *)p;
+    if (prefill_alloc(m, nT) != 0) return -1;
+    moe_chunk(m, L, in, out, nT);
+    const int K = m->cfg.top_k;
+    memcpy(route, m->croute, (size_t)nT * K * sizeof(int));
+    memcpy(rw, m->crw, (size_t)nT * K * sizeof(float));
+    return m->read_error;
+}
+
+/* The LUT of one matrix kind (0 gate, 1 up, 2 down) for input x of width N,
+ * built with the layer's codebook base. lut gets N/vd * stages * entries. */
+int ref_build_lut(void *p, int L, int kind, const float *x, int N, float *lut)
+{
+    waste_model *m = (waste_model *)p;
+    const int cb = m->bank[L].cb_base + kind * m->stages;
+    vq_build_lut(m, lut, cb, x, N, m->stages, m->cb_entries, m->vec_dim, NULL, NULL);
+    return 0;
+}
+
+/* vq_matvec of one matrix of one expert record: y = W_kind(expert) x. */
+int ref_vq_matvec(void *p, int L, int expert, int kind, const float *x, float *y)
+{
+    waste_model *m = (waste_model *)p;
+    const uint8_t *rec = read_expert(m, L, expert);
+    if (!rec) return -1;
+    const waste_expert_hdr *h = (const waste_expert_hdr *)rec;
+    const uint16_t *sc = (const uint16_t *)(rec + h->chan_corr_off);
+    const int inter = m->cfg.moe_inter, hid = m->cfg.hidden;
+    const uint32_t off = kind == 0 ? h->gate_off : kind == 1 ? h->up_off : h->down_off;
+    const int M = kind == 2 ? hid : inter, N = kind == 2 ? inter : hid;
+    const uint16_t *s = sc + (kind == 0 ? 0 : kind == 1 ? inter : 2 * inter);
+    const size_t lsz = (size_t)(N / m->vec_dim) * m->stages * m->cb_entries;
+    float *lut = (float *)malloc(lsz * sizeof(float));
+    int8_t *q = m->index_bits == 6 ? (int8_t *)malloc(lsz) : NULL;
+    float *qs = m->index_bits == 6 ? (float *)malloc((lsz / (m->stages * m->cb_entries) / WASTE_VQ_LUT_BLK + 2) * sizeof(float)) : NULL;
+    if (!lut || (m->index_bits == 6 && (!q || !qs))) { free(lut); free(q); free(qs); return -1; }
+    vq_matvec(m, y, rec + off, s, x, M, N, h->codebook_id + kind * m->stages, lut, q, qs);
+    free(lut); free(q); free(qs);
+    return 0;
+}
+
+/* The shared expert's three projections through matvec_t, as moe_layer
+ * runs them (the backend's mvq_rows_f32 for a quantised trunk). */
+int ref_trunk_matvec(void *p, const char *name, const float *x, float *y, int out, int in)
+{
+    waste_model *m = (waste_model *)p;
+    const waste_tensor *t = waste_find(m, name);
+    if (!t) return -1;
+    matvec_t(m, y, t, x, out, in);
+    return 0;
+}
