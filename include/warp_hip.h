@@ -1,0 +1,240 @@
+/*
+ * warp_hip.h — C ABI of the MI355X (gfx950) backend for WARP's routed-expert
+ * MoE path. Plain C, plain pointers and sizes.
+ *
+ * Two halves:
+ *
+ *  1. The reference's dispatch table (src/waste_backend.h:67-94) and a
+ *     registration function in its style (src/waste_backend.h:116-120,
+ *     called from src/backend.c:198-211 under WASTE_ENABLE_HIP). It fills
+ *     the mvq_rows_f32 slot with a device implementation and sets
+ *     on_device, so run_rows hands it whole row ranges (src/model.c:356-360).
+ *
+ *  2. The MoE slots the table does not have. The gather apply, routing,
+ *     combine and chunk loop are static functions of src/model.c
+ *     (vq_apply :2264, moe_layer :2713, moe_chunk :3512); these entry points
+ *     replace them behind a context that keeps the codebooks, routers,
+ *     shared experts and an expert cache resident in HBM.
+ *
+ * Device pointers are named *_dev and live in the memory of the context's
+ * device; everything else is host memory borrowed for the duration of the
+ * call. Functions returning int return 0 on success or a negative
+ * WARP_HIP_E_* code; the reason is available from warp_hip_error().
+ * A context is not thread-safe (as a waste_ctx is not, src/waste.h:25-26);
+ * distinct contexts are independent.
+ */
+#ifndef WARP_HIP_H
+#define WARP_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- 1. the reference's dispatch table ---------------------------------- */
+
+#ifndef WASTE_BACKEND_H
+/* Identical layout to src/waste_backend.h:67-90 for a build that does not
+ * include the reference's header. */
+typedef struct {
+    void (*kda_step)(int H, int K, int V, const float *q, const float *k, const float *v,
+                     const float *g_log, const float *beta, float *S, float *o, float *scratch);
+    void (*short_conv_step)(int C, int KS, const float *w, const float *bias, float *ring,
+                            const float *x, float *y);
+    void (*rmsnorm_gated)(int C, const float *x, const float *gate, const float *weight,
+                          float eps, float *y);
+    void (*mvq_rows_f32)(int b, int e, void *arg);
+    void (*lutb_range)(int lo, int hi, void *arg);
+    int on_device;
+} waste_kernels;
+#endif
+
+/* Replaces: the registration shape of src/waste_backend.h:116-120 (a new
+ * waste_register_hip beside waste_register_metal, src/metal.m). Probes for a
+ * gfx950 device and returns NULL (declines) without one; otherwise fills
+ * mvq_rows_f32 (argument struct mvq_arg, src/simd.h:35-39, host pointers) and
+ * sets on_device = 1, and returns "HIP gfx950". The slot keeps the table's
+ * previous mvq_rows_f32 and calls it with the same arguments if a device call
+ * fails, as the reference's accelerator contract requires (src/metal.m:177-181);
+ * warp_hip_table_stats() reports how many calls ran where. */
+const char *waste_register_hip(waste_kernels *t);
+
+/* Replaces: src/waste_backend.h:112-114 for this backend. Drops the device
+ * mirrors of trunk tensors keyed by host pointer; call before the model frees
+ * its host buffers. */
+void waste_hip_release_host_buffers(void);
+
+/* Calls of the mvq_rows_f32 slot that ran on the device / fell back. */
+void warp_hip_table_stats(uint64_t *device_calls, uint64_t *fallback_calls);
+
+/* ---- 2. MoE slots ---------------------------------------------------------- */
+
+/* Expert formats: waste_fmt codes (src/waste_format.h:41-71) plus one. */
+enum {
+    WARP_HIP_VQ3R = 4,   /* 3 stages x 256 entries, byte codes                 */
+    WARP_HIP_VQ2R = 5,   /* 2 stages x 256 entries, byte codes                 */
+    WARP_HIP_VQ4P = 8,   /* 4 stages x 64 entries, 4x6 bits in 3 bytes         */
+    WARP_HIP_VQ12 = 9,   /* extension: 2 stages x 4096, two 12-bit codes in the
+                          * little-endian 3-byte word s0 | s1 << 12; same
+                          * blocked layout, same 3.00 bits per weight          */
+};
+
+enum {
+    WARP_HIP_OK = 0,
+    WARP_HIP_E_ARG = -1,       /* a size or pointer the call cannot accept     */
+    WARP_HIP_E_DEVICE = -2,    /* a HIP call failed                            */
+    WARP_HIP_E_NOMEM = -3,     /* device or pinned allocation failed           */
+    WARP_HIP_E_READ = -4,      /* fetch short or failed   (REC_E_READ)         */
+    WARP_HIP_E_HEADER = -5,    /* record header invalid   (REC_E_HEADER)       */
+    WARP_HIP_E_CRC = -6,       /* record payload checksum (REC_E_CRC)          */
+    WARP_HIP_E_NOSLOT = -7,    /* cache could not free a slot (REC_E_NOSLOT)   */
+    WARP_HIP_E_MISSING = -8,   /* a selected expert is neither resident nor
+                                * fetchable: the layer was not computed       */
+};
+
+enum { WARP_HIP_ROUTE_SIGMOID = 0, WARP_HIP_ROUTE_SOFTMAX = 1 };
+
+typedef struct {
+    int hidden;            /* H (the expert input width; no latent path)       */
+    int inter;             /* moe_intermediate_size                            */
+    int n_experts;         /* E                                                */
+    int top_k;             /* K <= 64                                          */
+    int n_layers;
+    int fmt;               /* WARP_HIP_VQ*                                     */
+    int renorm;            /* moe_renormalize present (src/model.c:977-978)    */
+    float routed_scale;    /* routed_scaling_factor                            */
+    int router_act;        /* WARP_HIP_ROUTE_SIGMOID is the reference; SOFTMAX
+                            * is the extension                                 */
+    int router_strict;     /* 1: F32 router logits in the reference's
+                            * sequential fp32 order (bit-identical logits)     */
+    int act_situ;          /* hidden_act == "situ"                             */
+    float situ_beta, situ_linear_beta;
+    int max_tokens;        /* largest chunk warp_hip_moe_chunk will be given   */
+    size_t rec_bytes;      /* expert record stride, a 4 KiB multiple           */
+    size_t cache_bytes;    /* HBM budget for expert records                    */
+    int verify;            /* crc32 every record entering the cache
+                            * (WASTE_VERIFY, src/model.c:1742-1744)            */
+    int lookahead;         /* experts of layer L+1 to prefetch from layer L's
+                            * input (WASTE_LOOKAHEAD, src/model.c:2680-2711)   */
+    int device;            /* HIP device ordinal                               */
+} warp_hip_cfg;
+
+typedef struct warp_hip_ctx warp_hip_ctx;
+
+/* Fills `rec_bytes` at dst with record (layer, expert) and returns 0; the
+ * reference's waste_fetch_fn (src/ecache.h:35-38), e.g. bank_fetch. */
+typedef int (*warp_hip_fetch_fn)(void *user, int layer, int expert, uint8_t *dst);
+
+typedef struct {
+    uint64_t hits, misses, bytes_read, evictions;
+    uint64_t prefetched, spec_issued;      /* as waste_ecache (src/ecache.h:69-71) */
+    int n_slots, resident;
+} warp_hip_cache_stats;
+
+/* Replaces the MoE half of waste_model_load (src/model.c:1058-1493) for
+ * this backend: a context with device scratch for cfg->max_tokens tokens and
+ * an expert cache of cfg->cache_bytes / cfg->rec_bytes slots. */
+int warp_hip_open(const warp_hip_cfg *cfg, warp_hip_ctx **out);
+void warp_hip_close(warp_hip_ctx *c);
+
+/* Replaces waste_model_read_error (src/model.c:1815): the last failure, and
+ * the layer and expert it concerns (-1 when none). Never NULL. */
+const char *warp_hip_error(const warp_hip_ctx *c, int *layer, int *expert);
+
+/* The context's compute stream (a hipStream_t) for callers that enqueue
+ * around it. */
+void *warp_hip_stream(warp_hip_ctx *c);
+
+/* Layer weights, copied to HBM once.
+ * books: the layer's 3*stages codebooks as codebooks.bin stores them without
+ * headers, [3][stages][entries][8] fp16 (gate, up, down), ids cb_base..;
+ * fp16 subnormals are flushed to signed zero on upload (src/model.c:1277-1286).
+ * Replaces the codebook load of src/model.c:1269-1304. */
+int warp_hip_set_codebooks(warp_hip_ctx *c, int layer, int cb_base, const uint16_t *books);
+/* F32 router [E][H] and optional e_score_correction_bias [E]
+ * (block_sparse_moe.gate.weight / .e_score_correction_bias). */
+int warp_hip_set_router(warp_hip_ctx *c, int layer, const float *w, const float *bias);
+/* Quantised router: Q8G (bits 8), Q4G (4) or Q3G (3) rows as the trunk stores
+ * them (src/model.c:601-625). */
+int warp_hip_set_router_q(warp_hip_ctx *c, int layer, int bits, int group, const int8_t *q,
+                          const uint16_t *scales, size_t rowbytes, const float *bias);
+/* Shared expert (block_sparse_moe.shared_experts.{gate,up,down}_proj), quantised
+ * trunk rows; inter_shared = moe_inter * n_shared. q/scales/rowbytes: gate, up, down. */
+int warp_hip_set_shared(warp_hip_ctx *c, int layer, int bits, int group, int inter_shared,
+                        const int8_t *const q[3], const uint16_t *const scales[3],
+                        const size_t rowbytes[3]);
+
+/* Expert records. put copies one record into the cache now (checked as
+ * record_check does, src/model.c:1698-1745, plus the offsets the kernels
+ * rely on). fetch is how misses are filled. */
+int warp_hip_set_fetch(warp_hip_ctx *c, warp_hip_fetch_fn fetch, void *user);
+int warp_hip_put_expert(warp_hip_ctx *c, int layer, int expert, const uint8_t *rec);
+/* Replaces waste_ecache_prefetch (src/ecache.h:160-164): speculative fills on
+ * the copy stream; not counted as misses. */
+int warp_hip_prefetch(warp_hip_ctx *c, int layer, const int *ids, int n);
+void warp_hip_get_cache_stats(const warp_hip_ctx *c, warp_hip_cache_stats *st);
+
+/* Replaces moe_layer (src/model.c:2713-2940) for one token: router, top-k,
+ * K expert FFNs, combine in selection order, shared expert. x_dev, out_dev:
+ * [H] f32; resid_dev (may be NULL) is added to out (the caller's residual).
+ * idx/w (host, may be NULL) receive the selection; passing them costs a
+ * device->host copy and a wait. Experts not resident are fetched. */
+int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *out_dev,
+                        const float *resid_dev, int *idx, float *w);
+/* The same on host buffers: the drop-in for moe_layer's call site
+ * (src/model.c:3929-3934). `routed` (may be NULL) gets the K ids. */
+int warp_hip_moe_decode_host(warp_hip_ctx *c, int layer, const float *x, float *out, int *routed);
+
+/* Replaces moe_chunk (src/model.c:3512-3693) for T <= max_tokens tokens:
+ * per-token routing, pairs grouped by expert on the GPU, matrix-core
+ * matvecs over tiles of up to 8 tokens per expert, per-token combine in
+ * ascending expert id, shared expert. route/rw (host, may be NULL) get
+ * [T][K]. */
+int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *out_dev, int T,
+                       int *route, float *rw);
+int warp_hip_moe_chunk_host(warp_hip_ctx *c, int layer, const float *X, float *out, int T,
+                            int *route, float *rw);
+
+/* ---- finer-grained entry points (device pointers) -------------------------- */
+
+/* Replaces vq_matvec (src/model.c:2282-2289) on one matrix of one record:
+ * kind 0 gate, 1 up, 2 down; rec_dev is a record in device memory; x_dev
+ * [N] f32, y_dev [M] f32 with (M, N) = (inter, hidden) for gate/up and
+ * (hidden, inter) for down. Uses the layer's codebooks. */
+int warp_hip_vq_matvec(warp_hip_ctx *c, int layer, int kind, const uint8_t *rec_dev,
+                       const float *x_dev, float *y_dev);
+/* Decoded weights of one matrix, W_dev [M][N] f32, bit for bit the closed
+ * form of docs/FORMAT.md:186-189 (stage sum in fp32 from stage 0, then the
+ * subnormal-keeping row scale); the reference never materialises it. */
+int warp_hip_decode_weights(warp_hip_ctx *c, int layer, int kind, const uint8_t *rec_dev,
+                            float *W_dev);
+/* Router logits of the layer for T tokens: logits_dev [T][E]
+ * (matvec_t on the gate tensor, src/model.c:2721). */
+int warp_hip_router_logits(warp_hip_ctx *c, int layer, const float *x_dev, int T,
+                           float *logits_dev);
+/* Scoring, top-k and weights (src/model.c:2720-2747) on given logits:
+ * idx_dev/w_dev [T][K]. */
+int warp_hip_route(warp_hip_ctx *c, int layer, const float *logits_dev, int T, int *idx_dev,
+                   float *w_dev);
+/* Quantised rows times f32 activations on the device (the mvq_rows_f32 slot's
+ * arithmetic): y_dev [T][M]. */
+int warp_hip_mvq(warp_hip_ctx *c, int bits, int group, const int8_t *q_dev,
+                 const uint16_t *scales_dev, size_t rowbytes, const float *x_dev, int M, int N,
+                 int T, float *y_dev);
+
+/* Fill n bytes of device memory with deterministic noise (synthetic expert
+ * data for benchmarks that cannot afford host generation). */
+int warp_hip_fill_random(warp_hip_ctx *c, void *dev, size_t n, uint64_t seed);
+/* Direct pointer to the cache slot holding (layer, expert), NULL if not
+ * resident; and making a slot resident from bytes already in device memory. */
+const uint8_t *warp_hip_resident(warp_hip_ctx *c, int layer, int expert);
+int warp_hip_put_expert_dev(warp_hip_ctx *c, int layer, int expert, const uint8_t *rec_dev);
+/* Blocks until the context's streams are idle. */
+int warp_hip_sync(warp_hip_ctx *c);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* WARP_HIP_H */

@@ -1,0 +1,159 @@
+"""Parity of the HIP path (through the C ABI) with the oracle, on the same
+synthetic container bytes.
+
+Bars: decoded weights, code unpacking and expert selection bit-exact;
+VQ4P (whose reference arithmetic is integer plus a fixed float order) and
+the strict router bit-exact; everything else max|d|/max|ref| <= 1e-4 with
+fp32 accumulation.
+"""
+import numpy as np
+import pytest
+
+import container as ct
+from gpu_util import dev, empty, host, log, open_ctx, rel_err
+from oracle import pyoracle as po
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+FMTS = ["VQ3R", "VQ2R", "VQ4P", "VQ12"]
+
+
+def small_spec(fmt, **kw):
+    base = dict(hidden=128, inter=64, experts=8, top_k=2, layers=2, fmt=fmt, seed=7)
+    base.update(kw)
+    return ct.Spec(**base)
+
+
+@pytest.fixture(scope="module", params=FMTS)
+def loaded(request):
+    import warp_amd
+    fmt = request.param
+    model = ct.build(small_spec(fmt))
+    ctx = open_ctx(model, max_tokens=16)
+    warp_amd.load_container_model(ctx, model)
+    log(f"[{fmt}] context loaded, rec_bytes {model.rec_bytes}")
+    yield fmt, model, ctx
+    ctx.close()
+
+
+def test_decode_weights_bitexact(loaded):
+    fmt, model, ctx = loaded
+    spec = model.spec
+    books = po.books_flat(model.books_raw)
+    for L in range(spec.layers):
+        for e in (0, spec.experts - 1):
+            rec = ctx.resident(L, e)
+            assert rec
+            for kind in range(3):
+                M, N = (spec.inter, spec.hidden) if kind < 2 else (spec.hidden, spec.inter)
+                W = empty((M, N))
+                ctx.decode_weights(L, kind, rec, W)
+                r = np.frombuffer(model.layers[L].records[e], np.uint8)
+                hdr = np.frombuffer(model.layers[L].records[e][:48], np.uint32)
+                off = int(hdr[5 + kind])
+                corr = int(hdr[8])
+                soff = [0, spec.inter, 2 * spec.inter][kind]
+                scale = r[corr + 2 * soff: corr + 2 * (soff + M)].view(np.uint16)
+                S = ct.FMT_STAGES[fmt]
+                Wr = po.decode_weights(fmt, r[off:].copy(), scale.copy(), books, L * 3 * S + kind * S, M, N)
+                assert np.array_equal(host(W).view(np.uint32), Wr.view(np.uint32)), (L, e, kind)
+    log(f"[{fmt}] decoded weights bit-exact")
+
+
+def test_vq_matvec(loaded):
+    fmt, model, ctx = loaded
+    spec = model.spec
+    S = {"VQ3R": 3, "VQ2R": 2, "VQ4P": 4, "VQ12": 2}[fmt]
+    bT = po.books_T(model.books_raw)
+    rng = np.random.default_rng(3)
+    for L in range(spec.layers):
+        for e in range(0, spec.experts, 3):
+            rec = ctx.resident(L, e)
+            r = np.frombuffer(model.layers[L].records[e], np.uint8)
+            hdr = np.frombuffer(model.layers[L].records[e][:48], np.uint32)
+            for kind in range(3):
+                M, N = (spec.inter, spec.hidden) if kind < 2 else (spec.hidden, spec.inter)
+                x = rng.normal(size=N).astype(np.float32)
+                y = empty(M)
+                ctx.vq_matvec(L, kind, rec, dev(x), y)
+                off, corr = int(hdr[5 + kind]), int(hdr[8])
+                soff = [0, spec.inter, 2 * spec.inter][kind]
+                scale = r[corr + 2 * soff: corr + 2 * (soff + M)].view(np.uint16).copy()
+                yr = po.vq_matvec(fmt, r[off:].copy(), scale, x, bT, L * 3 * S + kind * S, M, N)
+                yg = host(y)
+                if fmt == "VQ4P":
+                    assert np.array_equal(yg, yr), (L, e, kind, rel_err(yg, yr))
+                else:
+                    assert rel_err(yg, yr) <= TOL, (L, e, kind, rel_err(yg, yr))
+    log(f"[{fmt}] vq_matvec within bar")
+
+
+def test_router_strict_and_route(loaded):
+    import warp_amd
+    fmt, model, ctx0 = loaded
+    spec = model.spec
+    ctx = open_ctx(model, max_tokens=16, router_strict=True)
+    warp_amd.load_container_model(ctx, model)
+    rng = np.random.default_rng(11)
+    T = 16
+    for L in range(spec.layers):
+        X = rng.normal(size=(T, spec.hidden)).astype(np.float32)
+        lg = empty((T, spec.experts))
+        ctx.router_logits(L, dev(X), T, lg)
+        W = model.layers[L].router
+        ref = np.array([[po.lib().or_dotf(W[e].ctypes.data, X[t].ctypes.data, spec.hidden)
+                         for e in range(spec.experts)] for t in range(T)], np.float32)
+        assert np.array_equal(host(lg), ref), "strict router logits are not bit-exact"
+        # selection and weights on identical logits
+        idx = empty((T, spec.top_k), np.int32)
+        w = empty((T, spec.top_k))
+        ctx.route(L, dev(ref), T, idx, w)
+        for t in range(T):
+            ri, rw, _ = po.route(ref[t], model.layers[L].bias, spec.top_k, 0, int(spec.renorm), spec.routed_scale)
+            assert np.array_equal(host(idx)[t], ri)
+            assert np.array_equal(host(w)[t], rw), (host(w)[t], rw)
+    ctx.close()
+    log(f"[{fmt}] strict router bit-exact, selection and weights bit-exact")
+
+
+def test_moe_decode(loaded):
+    fmt, model, ctx = loaded
+    spec = model.spec
+    rng = np.random.default_rng(5)
+    worst = 0.0
+    for L in range(spec.layers):
+        lv = po.LayerView(model, L)
+        for t in range(6):
+            x = rng.normal(size=spec.hidden).astype(np.float32)
+            out = empty(spec.hidden)
+            idx, w = ctx.moe_decode(L, dev(x), out, want_route=True)
+            ro, ri, rw, _ = lv.moe_layer(x)
+            assert np.array_equal(idx, ri), (idx, ri)
+            e = rel_err(host(out), ro)
+            worst = max(worst, e)
+            assert e <= TOL, (L, t, e)
+    log(f"[{fmt}] moe_decode worst rel err {worst:.2e}")
+
+
+def test_moe_decode_host_matches_device(loaded):
+    fmt, model, ctx = loaded
+    x = np.random.default_rng(9).normal(size=model.spec.hidden).astype(np.float32)
+    out = empty(model.spec.hidden)
+    ctx.moe_decode(1, dev(x), out)
+    oh, _ = ctx.moe_decode_host(1, x)
+    assert np.array_equal(host(out), oh)
+
+
+def test_moe_chunk(loaded):
+    fmt, model, ctx = loaded
+    spec = model.spec
+    rng = np.random.default_rng(21)
+    for L in range(spec.layers):
+        lv = po.LayerView(model, L)
+        X = rng.normal(size=(13, spec.hidden)).astype(np.float32)
+        out, route, rw = ctx.moe_chunk_host(L, X)
+        ro, rr, rrw = lv.moe_chunk(X)
+        assert np.array_equal(route, rr)
+        e = rel_err(out, ro)
+        assert e <= TOL, (L, e)
+        log(f"[{fmt}] moe_chunk L{L} rel err {e:.2e}")

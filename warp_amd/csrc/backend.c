@@ -1,0 +1,1229 @@
+/*
+ * backend.c — host side of the MI355X backend, in C, over the HIP runtime
+ * API. Implements include/warp_hip.h: the reference's dispatch-table
+ * registration, the device context that keeps codebooks, routers, shared
+ * experts and an expert cache resident in HBM, the miss path (pinned
+ * staging, copies on a side stream, lookahead prefetch), and the layer and
+ * chunk orchestration over the kernels of kernels.hip.
+ */
+#define _GNU_SOURCE
+#include <hip/hip_runtime_api.h>
+
+#include <pthread.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "warp_hip.h"
+#include "warp_internal.h"
+
+#define HIPOK(x) ((x) == hipSuccess)
+
+/* ---- small utilities ----------------------------------------------------- */
+
+static uint32_t crc_table[256];
+static pthread_once_t crc_once = PTHREAD_ONCE_INIT;
+
+static void crc_init(void)
+{
+    for (uint32_t i = 0; i < 256; i++) {
+        uint32_t c = i;
+        for (int k = 0; k < 8; k++) c = (c >> 1) ^ (0xEDB88320u & (0u - (c & 1u)));
+        crc_table[i] = c;
+    }
+}
+
+/* zlib's crc32, as the record checksum is defined (src/waste_format.h:116-127) */
+static uint32_t crc32_buf(const uint8_t *p, size_t n)
+{
+    pthread_once(&crc_once, crc_init);
+    uint32_t c = 0xFFFFFFFFu;
+    for (size_t i = 0; i < n; i++) c = crc_table[(c ^ p[i]) & 0xFF] ^ (c >> 8);
+    return c ^ 0xFFFFFFFFu;
+}
+
+static int fmt_stages(int fmt)
+{
+    switch (fmt) {
+    case WARP_HIP_VQ3R: return 3;
+    case WARP_HIP_VQ2R: return 2;
+    case WARP_HIP_VQ4P: return 4;
+    case WARP_HIP_VQ12: return 2;
+    }
+    return 0;
+}
+
+static int fmt_entries(int fmt)
+{
+    switch (fmt) {
+    case WARP_HIP_VQ3R: case WARP_HIP_VQ2R: return 256;
+    case WARP_HIP_VQ4P: return 64;
+    case WARP_HIP_VQ12: return 4096;
+    }
+    return 0;
+}
+
+static int fmt_slot(int fmt)
+{
+    switch (fmt) {
+    case WARP_HIP_VQ3R: return 3;
+    case WARP_HIP_VQ2R: return 2;
+    case WARP_HIP_VQ4P: return 3;
+    case WARP_HIP_VQ12: return 3;
+    }
+    return 0;
+}
+
+static size_t index_bytes(int fmt, int M, int N)
+{
+    return ((size_t)(M + WARP_TILE - 1) / WARP_TILE) * (size_t)(N / 8) * WARP_TILE * fmt_slot(fmt);
+}
+
+/* ---- 1. the dispatch-table slot ---------------------------------------------- */
+
+/* mvq_arg, src/simd.h:35-39 (same member order and types) */
+typedef struct {
+    float *y; const int8_t *W; const uint16_t *ws;
+    const int8_t *xq; const float *xs; int in, ng, group, bits;
+    size_t rowbytes;
+} mvq_arg_t;
+
+typedef struct {
+    const void *host;
+    size_t bytes;
+    void *dev;
+} mirror_t;
+
+static pthread_mutex_t g_tab_mu = PTHREAD_MUTEX_INITIALIZER;
+static void (*g_prev_mvq)(int, int, void *);
+static mirror_t *g_mirrors;
+static int g_n_mirrors, g_cap_mirrors;
+static hipStream_t g_tab_stream;
+static float *g_tab_x, *g_tab_y;
+static size_t g_tab_x_cap, g_tab_y_cap;
+static uint64_t g_dev_calls, g_fallback_calls;
+
+/* Device copy of a host buffer, keyed by its pointer (the Metal backend's
+ * no-copy buffers, src/metal.m:98-150, are the precedent: trunk tensors do
+ * not change while a model is open). Grows when a longer range is asked. */
+static void *mirror_of(const void *host, size_t bytes)
+{
+    for (int i = 0; i < g_n_mirrors; i++)
+        if (g_mirrors[i].host == host) {
+            if (g_mirrors[i].bytes >= bytes) return g_mirrors[i].dev;
+            (void)hipFree(g_mirrors[i].dev);
+            g_mirrors[i] = g_mirrors[--g_n_mirrors];
+            break;
+        }
+    if (g_n_mirrors == g_cap_mirrors) {
+        const int cap = g_cap_mirrors ? 2 * g_cap_mirrors : 64;
+        mirror_t *m = (mirror_t *)realloc(g_mirrors, (size_t)cap * sizeof *m);
+        if (!m) return NULL;
+        g_mirrors = m;
+        g_cap_mirrors = cap;
+    }
+    void *dev = NULL;
+    if (!HIPOK(hipMalloc(&dev, bytes))) return NULL;
+    if (!HIPOK(hipMemcpy(dev, host, bytes, hipMemcpyHostToDevice))) { (void)hipFree(dev); return NULL; }
+    g_mirrors[g_n_mirrors++] = (mirror_t){ host, bytes, dev };
+    return dev;
+}
+
+static int grow(float **p, size_t *cap, size_t n)
+{
+    if (*cap >= n) return 0;
+    if (*p) (void)hipFree(*p);
+    *p = NULL;
+    *cap = 0;
+    if (!HIPOK(hipMalloc((void **)p, n * sizeof(float)))) return -1;
+    *cap = n;
+    return 0;
+}
+
+static int mvq_on_device(int b, int e, const mvq_arg_t *a)
+{
+    if (!g_tab_stream && !HIPOK(hipStreamCreate(&g_tab_stream))) return -1;
+    const size_t rows = (size_t)e;
+    const int8_t *W = (const int8_t *)mirror_of(a->W, rows * a->rowbytes);
+    const uint16_t *ws = (const uint16_t *)mirror_of(a->ws, rows * (size_t)a->ng * sizeof(uint16_t));
+    if (!W || !ws) return -1;
+    if (grow(&g_tab_x, &g_tab_x_cap, (size_t)a->in) || grow(&g_tab_y, &g_tab_y_cap, rows)) return -1;
+    if (!HIPOK(hipMemcpyAsync(g_tab_x, a->xs, (size_t)a->in * sizeof(float), hipMemcpyHostToDevice, g_tab_stream)))
+        return -1;
+    if (wk_mvq(W + (size_t)b * a->rowbytes, ws + (size_t)b * a->ng, a->rowbytes, a->group, a->bits, g_tab_x,
+               e - b, a->in, 1, g_tab_y, g_tab_stream))
+        return -1;
+    if (!HIPOK(hipMemcpyAsync(a->y + b, g_tab_y, (size_t)(e - b) * sizeof(float), hipMemcpyDeviceToHost,
+                              g_tab_stream)))
+        return -1;
+    return HIPOK(hipStreamSynchronize(g_tab_stream)) ? 0 : -1;
+}
+
+/* The mvq_rows_f32 slot (src/simd.h:15-19, src/model.c:385-399). */
+static void hip_mvq_rows_f32(int b, int e, void *p)
+{
+    const mvq_arg_t *a = (const mvq_arg_t *)p;
+    if (e <= b) return;
+    pthread_mutex_lock(&g_tab_mu);
+    const int rc = mvq_on_device(b, e, a);
+    if (rc == 0) g_dev_calls++; else g_fallback_calls++;
+    pthread_mutex_unlock(&g_tab_mu);
+    if (rc != 0 && g_prev_mvq) g_prev_mvq(b, e, p);
+}
+
+static int device_is_gfx950(int dev)
+{
+    char arch[64];
+    if (wk_device_arch(dev, arch, sizeof arch)) return 0;
+    return strncmp(arch, "gfx950", 6) == 0;
+}
+
+const char *waste_register_hip(waste_kernels *t)
+{
+    int n = 0;
+    if (!HIPOK(hipGetDeviceCount(&n)) || n < 1) return NULL;
+    if (!device_is_gfx950(0)) return NULL;
+    pthread_mutex_lock(&g_tab_mu);
+    if (t->mvq_rows_f32 != hip_mvq_rows_f32) g_prev_mvq = t->mvq_rows_f32;
+    pthread_mutex_unlock(&g_tab_mu);
+    t->mvq_rows_f32 = hip_mvq_rows_f32;
+    t->on_device = 1;
+    return "HIP gfx950";
+}
+
+void waste_hip_release_host_buffers(void)
+{
+    pthread_mutex_lock(&g_tab_mu);
+    for (int i = 0; i < g_n_mirrors; i++) (void)hipFree(g_mirrors[i].dev);
+    g_n_mirrors = 0;
+    pthread_mutex_unlock(&g_tab_mu);
+}
+
+void warp_hip_table_stats(uint64_t *device_calls, uint64_t *fallback_calls)
+{
+    pthread_mutex_lock(&g_tab_mu);
+    if (device_calls) *device_calls = g_dev_calls;
+    if (fallback_calls) *fallback_calls = g_fallback_calls;
+    pthread_mutex_unlock(&g_tab_mu);
+}
+
+/* ---- 2. the context ---------------------------------------------------------------- */
+
+typedef struct {
+    uint16_t *books;            /* [3][S][E][8] fp16, flushed              */
+    int cb_base, has_books;
+    float *router;              /* [E][H] or NULL                          */
+    int8_t *rq; uint16_t *rs;   /* quantised router                        */
+    size_t r_rowbytes; int r_bits, r_group;
+    float *bias;                /* [E] or NULL                             */
+    int8_t *sq[3]; uint16_t *ss[3];
+    size_t s_rowbytes[3]; int s_bits, s_group, s_inter;
+    int resident;               /* records of this layer in the cache      */
+} layer_t;
+
+#define N_STAGE 32
+
+struct warp_hip_ctx {
+    warp_hip_cfg cfg;
+    int S, En, SB, P6, P_max, max_jobs;
+    size_t gate_bytes, down_bytes;
+    hipStream_t st, cp, la;
+    hipEvent_t ev_copy, ev_before, ev_after, ev_la, ev_x, ev_stage[N_STAGE];
+    int copy_pending;
+    layer_t *L;
+    /* expert cache */
+    uint8_t *pool;
+    int n_slots, next_free;
+    int *slot_key, *key_slot;
+    uint32_t *hits;
+    uint64_t *last, clock;
+    unsigned rng;
+    const uint8_t **table_dev;
+    uint8_t *staging;           /* pinned, N_STAGE records                 */
+    int stage_next, stage_used[N_STAGE];
+    warp_hip_fetch_fn fetch;
+    void *fetch_user;
+    warp_hip_cache_stats stats;
+    int *pin, n_pin, pin_layer;     /* experts of the layer in flight      */
+    /* device scratch */
+    float *logits;
+    int *idx;
+    float *w;
+    warp_job *jobs;
+    int *njobs, *missing;
+    uint16_t *xs;
+    float *xscale;
+    float *yg, *yu, *yd;
+    uint16_t *xsh;
+    float *xscaleh, *hbuf;
+    float *shg, *shu, *shh, *sho;
+    int sh_cap;
+    int8_t *lut8, *lut8d;
+    float *lscale, *lscaled;
+    int *counts, *offsets, *pair_tok, *pair_exp;
+    float *pair_w;
+    float *xin, *xout;
+    float *la_logits;
+    int *la_idx;
+    float *la_w;
+    /* pinned host */
+    int *h_idx, *h_la_idx, *h_missing;
+    float *h_w;
+    char err[256];
+    int err_layer, err_expert;
+};
+
+static int set_err(warp_hip_ctx *c, int code, int layer, int expert, const char *fmt, ...)
+{
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(c->err, sizeof c->err, fmt, ap);
+    va_end(ap);
+    c->err_layer = layer;
+    c->err_expert = expert;
+    return code;
+}
+
+static int dev_err(warp_hip_ctx *c, const char *what, hipError_t e)
+{
+    return set_err(c, WARP_HIP_E_DEVICE, -1, -1, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define DEV(c, call)                                               \
+    do {                                                           \
+        hipError_t e__ = (call);                                   \
+        if (e__ != hipSuccess) return dev_err((c), #call, e__);    \
+    } while (0)
+
+#define KRN(c, call)                                                          \
+    do {                                                                      \
+        int r__ = (call);                                                     \
+        if (r__) return set_err((c), r__ == -1 ? WARP_HIP_E_ARG : WARP_HIP_E_DEVICE, -1, -1, \
+                                "%s failed (%d)", #call, r__);                \
+    } while (0)
+
+const char *warp_hip_error(const warp_hip_ctx *c, int *layer, int *expert)
+{
+    if (layer) *layer = c ? c->err_layer : -1;
+    if (expert) *expert = c ? c->err_expert : -1;
+    return c ? c->err : "no context";
+}
+
+void *warp_hip_stream(warp_hip_ctx *c) { return c ? (void *)c->st : NULL; }
+
+static int dmalloc(warp_hip_ctx *c, void **p, size_t bytes)
+{
+    *p = NULL;
+    if (!bytes) bytes = 16;
+    hipError_t e = hipMalloc(p, bytes);
+    if (e != hipSuccess) {
+        *p = NULL;
+        return set_err(c, WARP_HIP_E_NOMEM, -1, -1, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+    }
+    return 0;
+}
+
+#define DMALLOC(c, p, bytes) do { if (dmalloc((c), (void **)&(p), (bytes))) return WARP_HIP_E_NOMEM; } while (0)
+
+static int ctx_alloc(warp_hip_ctx *c)
+{
+    const warp_hip_cfg *g = &c->cfg;
+    const int E = g->n_experts, K = g->top_k, H = g->hidden, I = g->inter, T = g->max_tokens;
+    const size_t P = (size_t)T * K;
+    c->P_max = (int)P;
+    c->max_jobs = (int)(P / WARP_TPJ + (size_t)E + 1);
+    if (c->max_jobs < K) c->max_jobs = K;
+    const size_t nvH = (size_t)H / 8, nvI = (size_t)I / 8;
+    const size_t nblkH = (nvH + WARP_LUT_BLK - 1) / WARP_LUT_BLK, nblkI = (nvI + WARP_LUT_BLK - 1) / WARP_LUT_BLK;
+    DMALLOC(c, c->logits, (size_t)T * E * 4);
+    DMALLOC(c, c->idx, P * 4);
+    DMALLOC(c, c->w, P * 4);
+    DMALLOC(c, c->jobs, (size_t)3 * c->max_jobs * sizeof(warp_job));
+    DMALLOC(c, c->njobs, 4 * sizeof(int));
+    DMALLOC(c, c->missing, sizeof(int));
+    DMALLOC(c, c->xs, (size_t)T * H * 2 * 2);
+    DMALLOC(c, c->xscale, (size_t)T * 4);
+    DMALLOC(c, c->yg, P * I * 4);
+    DMALLOC(c, c->yu, P * I * 4);
+    DMALLOC(c, c->yd, P * H * 4);
+    DMALLOC(c, c->xsh, P * I * 2 * 2);
+    DMALLOC(c, c->xscaleh, P * 4);
+    DMALLOC(c, c->hbuf, P * I * 4);
+    DMALLOC(c, c->sho, (size_t)T * H * 4);
+    DMALLOC(c, c->xin, (size_t)T * H * 4);
+    DMALLOC(c, c->xout, (size_t)T * H * 4);
+    DMALLOC(c, c->counts, ((size_t)E + 1) * 4);
+    DMALLOC(c, c->offsets, ((size_t)E + 1) * 4);
+    DMALLOC(c, c->pair_tok, P * 4);
+    DMALLOC(c, c->pair_exp, P * 4);
+    DMALLOC(c, c->pair_w, P * 4);
+    DMALLOC(c, c->la_logits, (size_t)E * 4);
+    DMALLOC(c, c->la_idx, (size_t)WARP_MAX_K * 4);
+    DMALLOC(c, c->la_w, (size_t)WARP_MAX_K * 4);
+    if (c->P6) {
+        DMALLOC(c, c->lut8, (size_t)T * 2 * nvH * 256);
+        DMALLOC(c, c->lscale, (size_t)T * 2 * nblkH * 4);
+        DMALLOC(c, c->lut8d, P * nvI * 256);
+        DMALLOC(c, c->lscaled, P * nblkI * 4);
+    }
+    DEV(c, hipMemset(c->missing, 0, sizeof(int)));
+    DEV(c, hipHostMalloc((void **)&c->h_idx, P * 4, 0));
+    DEV(c, hipHostMalloc((void **)&c->h_w, P * 4, 0));
+    DEV(c, hipHostMalloc((void **)&c->h_la_idx, WARP_MAX_K * 4, 0));
+    DEV(c, hipHostMalloc((void **)&c->h_missing, 4 * sizeof(int), 0));
+    /* expert cache */
+    c->n_slots = g->rec_bytes ? (int)(g->cache_bytes / g->rec_bytes) : 0;
+    const size_t nkeys = (size_t)g->n_layers * E;
+    c->key_slot = (int *)malloc(nkeys * sizeof(int));
+    c->slot_key = (int *)malloc(((size_t)c->n_slots + 1) * sizeof(int));
+    c->hits = (uint32_t *)calloc((size_t)c->n_slots + 1, sizeof(uint32_t));
+    c->pin = (int *)calloc((size_t)E + 1, sizeof(int));
+    c->last = (uint64_t *)calloc((size_t)c->n_slots + 1, sizeof(uint64_t));
+    if (!c->key_slot || !c->slot_key || !c->hits || !c->last || !c->pin)
+        return set_err(c, WARP_HIP_E_NOMEM, -1, -1, "host allocation failed");
+    for (size_t i = 0; i < nkeys; i++) c->key_slot[i] = -1;
+    for (int i = 0; i < c->n_slots; i++) c->slot_key[i] = -1;
+    DMALLOC(c, c->table_dev, nkeys * sizeof(void *));
+    DEV(c, hipMemset(c->table_dev, 0, nkeys * sizeof(void *)));
+    if (c->n_slots > 0) DMALLOC(c, c->pool, (size_t)c->n_slots * g->rec_bytes);
+    DEV(c, hipHostMalloc((void **)&c->staging, (size_t)N_STAGE * g->rec_bytes, 0));
+    return 0;
+}
+
+int warp_hip_open(const warp_hip_cfg *cfg, warp_hip_ctx **out)
+{
+    *out = NULL;
+    warp_hip_ctx *c = (warp_hip_ctx *)calloc(1, sizeof *c);
+    if (!c) return WARP_HIP_E_NOMEM;
+    c->cfg = *cfg;
+    c->err_layer = c->err_expert = -1;
+    c->pin_layer = -1;
+    c->rng = 0x9E3779B9u;
+    warp_hip_cfg *g = &c->cfg;
+    c->S = fmt_stages(g->fmt);
+    c->En = fmt_entries(g->fmt);
+    c->SB = fmt_slot(g->fmt);
+    c->P6 = g->fmt == WARP_HIP_VQ4P;
+    if (g->max_tokens < 1) g->max_tokens = 1;
+    int rc = WARP_HIP_E_ARG;
+    if (!c->S || g->hidden <= 0 || g->inter <= 0 || g->n_experts <= 0 || g->top_k <= 0 ||
+        g->top_k > WARP_MAX_K || g->top_k > g->n_experts || g->n_layers <= 0 || g->n_layers > 65535 ||
+        g->n_experts > 65535 || (g->rec_bytes % 4096) != 0 || g->lookahead < 0) {
+        set_err(c, rc, -1, -1, "configuration out of range");
+        goto fail;
+    }
+    if (!c->P6 && (g->hidden % 32 || g->inter % 32)) {
+        set_err(c, rc, -1, -1, "hidden and inter must be multiples of 32 (4 vector positions)");
+        goto fail;
+    }
+    if (g->hidden % 8 || g->inter % 8) {
+        set_err(c, rc, -1, -1, "hidden and inter must be multiples of vec_dim 8");
+        goto fail;
+    }
+    c->gate_bytes = index_bytes(g->fmt, g->inter, g->hidden);
+    c->down_bytes = index_bytes(g->fmt, g->hidden, g->inter);
+    if (g->rec_bytes && WARP_HDR_BYTES + 2 * c->gate_bytes + c->down_bytes +
+                            2 * (2 * (size_t)g->inter + g->hidden) > g->rec_bytes) {
+        set_err(c, rc, -1, -1, "rec_bytes %zu cannot hold a record of this shape", g->rec_bytes);
+        goto fail;
+    }
+    int ndev = 0;
+    if (!HIPOK(hipGetDeviceCount(&ndev)) || g->device < 0 || g->device >= ndev) {
+        set_err(c, WARP_HIP_E_DEVICE, -1, -1, "no HIP device %d", g->device);
+        rc = WARP_HIP_E_DEVICE;
+        goto fail;
+    }
+    if (!device_is_gfx950(g->device)) {
+        set_err(c, WARP_HIP_E_DEVICE, -1, -1, "device %d is not gfx950", g->device);
+        rc = WARP_HIP_E_DEVICE;
+        goto fail;
+    }
+    if (!HIPOK(hipSetDevice(g->device)) || !HIPOK(hipStreamCreateWithFlags(&c->st, hipStreamNonBlocking)) ||
+        !HIPOK(hipStreamCreateWithFlags(&c->cp, hipStreamNonBlocking)) ||
+        !HIPOK(hipStreamCreateWithFlags(&c->la, hipStreamNonBlocking)) ||
+        !HIPOK(hipEventCreateWithFlags(&c->ev_copy, hipEventDisableTiming)) ||
+        !HIPOK(hipEventCreateWithFlags(&c->ev_before, hipEventDisableTiming)) ||
+        !HIPOK(hipEventCreateWithFlags(&c->ev_after, hipEventDisableTiming)) ||
+        !HIPOK(hipEventCreateWithFlags(&c->ev_la, hipEventDisableTiming)) ||
+        !HIPOK(hipEventCreateWithFlags(&c->ev_x, hipEventDisableTiming))) {
+        set_err(c, WARP_HIP_E_DEVICE, -1, -1, "stream/event creation failed");
+        rc = WARP_HIP_E_DEVICE;
+        goto fail;
+    }
+    for (int i = 0; i < N_STAGE; i++)
+        if (!HIPOK(hipEventCreateWithFlags(&c->ev_stage[i], hipEventDisableTiming))) {
+            rc = WARP_HIP_E_DEVICE;
+            goto fail;
+        }
+    c->L = (layer_t *)calloc((size_t)g->n_layers, sizeof(layer_t));
+    if (!c->L) { rc = WARP_HIP_E_NOMEM; goto fail; }
+    if ((rc = ctx_alloc(c)) != 0) goto fail;
+    *out = c;
+    return 0;
+fail:
+    fprintf(stderr, "warp_hip_open: %s\n", c->err);
+    warp_hip_close(c);
+    return rc;
+}
+
+static void hfree(void *p) { if (p) (void)hipFree(p); }
+static void hhfree(void *p) { if (p) (void)hipHostFree(p); }
+
+void warp_hip_close(warp_hip_ctx *c)
+{
+    if (!c) return;
+    if (c->st) (void)hipStreamSynchronize(c->st);
+    if (c->cp) (void)hipStreamSynchronize(c->cp);
+    if (c->la) (void)hipStreamSynchronize(c->la);
+    if (c->L)
+        for (int l = 0; l < c->cfg.n_layers; l++) {
+            layer_t *L = &c->L[l];
+            hfree(L->books); hfree(L->router); hfree(L->rq); hfree(L->rs); hfree(L->bias);
+            for (int k = 0; k < 3; k++) { hfree(L->sq[k]); hfree(L->ss[k]); }
+        }
+    free(c->L);
+    void *d[] = { c->logits, c->idx, c->w, c->jobs, c->njobs, c->missing, c->xs, c->xscale, c->yg, c->yu,
+                  c->yd, c->xsh, c->xscaleh, c->hbuf, c->shg, c->shu, c->shh, c->sho, c->lut8, c->lut8d,
+                  c->lscale, c->lscaled, c->counts, c->offsets, c->pair_tok, c->pair_exp, c->pair_w,
+                  c->xin, c->xout, c->la_logits, c->la_idx, c->la_w, c->table_dev, c->pool };
+    for (size_t i = 0; i < sizeof d / sizeof d[0]; i++) hfree(d[i]);
+    hhfree(c->h_idx); hhfree(c->h_w); hhfree(c->h_la_idx); hhfree(c->h_missing); hhfree(c->staging);
+    free(c->key_slot); free(c->slot_key); free(c->hits); free(c->last); free(c->pin);
+    for (int i = 0; i < N_STAGE; i++) if (c->ev_stage[i]) (void)hipEventDestroy(c->ev_stage[i]);
+    if (c->ev_copy) (void)hipEventDestroy(c->ev_copy);
+    if (c->ev_before) (void)hipEventDestroy(c->ev_before);
+    if (c->ev_after) (void)hipEventDestroy(c->ev_after);
+    if (c->ev_la) (void)hipEventDestroy(c->ev_la);
+    if (c->ev_x) (void)hipEventDestroy(c->ev_x);
+    if (c->st) (void)hipStreamDestroy(c->st);
+    if (c->cp) (void)hipStreamDestroy(c->cp);
+    if (c->la) (void)hipStreamDestroy(c->la);
+    free(c);
+}
+
+int warp_hip_sync(warp_hip_ctx *c)
+{
+    DEV(c, hipStreamSynchronize(c->la));
+    DEV(c, hipStreamSynchronize(c->cp));
+    DEV(c, hipStreamSynchronize(c->st));
+    return 0;
+}
+
+/* ---- layer weights ------------------------------------------------------------------ */
+
+static int check_layer(warp_hip_ctx *c, int layer)
+{
+    if (!c || layer < 0 || layer >= c->cfg.n_layers)
+        return c ? set_err(c, WARP_HIP_E_ARG, layer, -1, "layer %d out of range", layer) : WARP_HIP_E_ARG;
+    return 0;
+}
+
+static int upload(warp_hip_ctx *c, void **dst, const void *src, size_t bytes)
+{
+    if (*dst) { (void)hipFree(*dst); *dst = NULL; }
+    if (dmalloc(c, dst, bytes)) return WARP_HIP_E_NOMEM;
+    DEV(c, hipMemcpy(*dst, src, bytes, hipMemcpyHostToDevice));
+    return 0;
+}
+
+int warp_hip_set_codebooks(warp_hip_ctx *c, int layer, int cb_base, const uint16_t *books)
+{
+    int rc = check_layer(c, layer);
+    if (rc) return rc;
+    const size_t n = (size_t)3 * c->S * c->En * 8;
+    uint16_t *tmp = (uint16_t *)malloc(n * sizeof(uint16_t));
+    if (!tmp) return set_err(c, WARP_HIP_E_NOMEM, layer, -1, "host allocation failed");
+    /* fp16 subnormals flush to signed zero, as the codebook load does
+     * (src/model.c:1277-1286); exponent-31 values keep their bits and the
+     * kernels rebias them as the reference does. */
+    for (size_t i = 0; i < n; i++) tmp[i] = ((books[i] >> 10) & 0x1f) ? books[i] : (uint16_t)(books[i] & 0x8000);
+    rc = upload(c, (void **)&c->L[layer].books, tmp, n * sizeof(uint16_t));
+    free(tmp);
+    if (rc) return rc;
+    c->L[layer].cb_base = cb_base;
+    c->L[layer].has_books = 1;
+    return 0;
+}
+
+int warp_hip_set_router(warp_hip_ctx *c, int layer, const float *w, const float *bias)
+{
+    int rc = check_layer(c, layer);
+    if (rc) return rc;
+    if (!w) return set_err(c, WARP_HIP_E_ARG, layer, -1, "router weights missing");
+    layer_t *L = &c->L[layer];
+    if ((rc = upload(c, (void **)&L->router, w, (size_t)c->cfg.n_experts * c->cfg.hidden * 4))) return rc;
+    hfree(L->rq); hfree(L->rs);
+    L->rq = NULL; L->rs = NULL;
+    if (bias) return upload(c, (void **)&L->bias, bias, (size_t)c->cfg.n_experts * 4);
+    hfree(L->bias);
+    L->bias = NULL;
+    return 0;
+}
+
+int warp_hip_set_router_q(warp_hip_ctx *c, int layer, int bits, int group, const int8_t *q,
+                          const uint16_t *scales, size_t rowbytes, const float *bias)
+{
+    int rc = check_layer(c, layer);
+    if (rc) return rc;
+    if ((bits != 8 && bits != 4 && bits != 3) || group <= 0 || !q || !scales)
+        return set_err(c, WARP_HIP_E_ARG, layer, -1, "quantised router arguments");
+    layer_t *L = &c->L[layer];
+    const int E = c->cfg.n_experts, ng = (c->cfg.hidden + group - 1) / group;
+    if ((rc = upload(c, (void **)&L->rq, q, (size_t)E * rowbytes))) return rc;
+    if ((rc = upload(c, (void **)&L->rs, scales, (size_t)E * ng * 2))) return rc;
+    L->r_rowbytes = rowbytes;
+    L->r_bits = bits;
+    L->r_group = group;
+    hfree(L->router);
+    L->router = NULL;
+    if (bias) return upload(c, (void **)&L->bias, bias, (size_t)E * 4);
+    hfree(L->bias);
+    L->bias = NULL;
+    return 0;
+}
+
+int warp_hip_set_shared(warp_hip_ctx *c, int layer, int bits, int group, int inter_shared,
+                        const int8_t *const q[3], const uint16_t *const scales[3], const size_t rowbytes[3])
+{
+    int rc = check_layer(c, layer);
+    if (rc) return rc;
+    if ((bits != 8 && bits != 4 && bits != 3) || group <= 0 || inter_shared <= 0)
+        return set_err(c, WARP_HIP_E_ARG, layer, -1, "shared expert arguments");
+    layer_t *L = &c->L[layer];
+    const int H = c->cfg.hidden, Is = inter_shared;
+    const int rows[3] = { Is, Is, H }, cols[3] = { H, H, Is };
+    for (int k = 0; k < 3; k++) {
+        const int ng = (cols[k] + group - 1) / group;
+        if ((rc = upload(c, (void **)&L->sq[k], q[k], (size_t)rows[k] * rowbytes[k]))) return rc;
+        if ((rc = upload(c, (void **)&L->ss[k], scales[k], (size_t)rows[k] * ng * 2))) return rc;
+        L->s_rowbytes[k] = rowbytes[k];
+    }
+    L->s_bits = bits;
+    L->s_group = group;
+    L->s_inter = Is;
+    /* scratch for the shared expert, sized for the widest one set so far */
+    int max_is = 0;
+    for (int l = 0; l < c->cfg.n_layers; l++) if (c->L[l].s_inter > max_is) max_is = c->L[l].s_inter;
+    if (max_is > c->sh_cap) {
+        hfree(c->shg); hfree(c->shu); hfree(c->shh);
+        c->shg = c->shu = c->shh = NULL;
+        c->sh_cap = 0;
+        const size_t bytes = (size_t)c->cfg.max_tokens * max_is * 4;
+        DMALLOC(c, c->shg, bytes);
+        DMALLOC(c, c->shu, bytes);
+        DMALLOC(c, c->shh, bytes);
+        c->sh_cap = max_is;
+    }
+    return 0;
+}
+
+/* ---- expert cache ----------------------------------------------------------------------- */
+
+/* record_check (src/model.c:1698-1745), plus the offsets the kernels index
+ * with: every index block at least as long as its shape needs, the scales
+ * after them, all inside the record, so no kernel read leaves the slot. */
+static int check_record(warp_hip_ctx *c, const uint8_t *rec, int layer, int expert)
+{
+    const warp_hip_cfg *g = &c->cfg;
+    uint32_t magic, blocks, off[4], crc;
+    uint16_t lay, eid, cbid, lowrank;
+    uint8_t fmt;
+    memcpy(&magic, rec + 0, 4);
+    memcpy(&lay, rec + 4, 2);
+    memcpy(&eid, rec + 6, 2);
+    memcpy(&fmt, rec + 8, 1);
+    memcpy(&cbid, rec + 10, 2);
+    memcpy(&lowrank, rec + 12, 2);
+    memcpy(&blocks, rec + 16, 4);
+    memcpy(off, rec + 20, 16);
+    memcpy(&crc, rec + 36, 4);
+    if (magic != 0x50584557u || lay != (uint16_t)layer || eid != (uint16_t)expert ||
+        (size_t)blocks * 4096u != g->rec_bytes || lowrank != 0)
+        return set_err(c, WARP_HIP_E_HEADER, layer, expert, "record header: magic/identity/size");
+    if (fmt != g->fmt) return set_err(c, WARP_HIP_E_HEADER, layer, expert, "record fmt %d, context fmt %d", fmt, g->fmt);
+    if (c->L[layer].has_books && cbid != (uint16_t)c->L[layer].cb_base)
+        return set_err(c, WARP_HIP_E_HEADER, layer, expert, "record codebook_id %u, layer base %d", cbid,
+                       c->L[layer].cb_base);
+    const size_t scales = 2u * (2 * (size_t)g->inter + g->hidden);
+    if (!(off[0] == WARP_HDR_BYTES && (size_t)off[0] + c->gate_bytes <= off[1] &&
+          (size_t)off[1] + c->gate_bytes <= off[2] && (size_t)off[2] + c->down_bytes <= off[3] &&
+          (size_t)off[3] + scales <= g->rec_bytes))
+        return set_err(c, WARP_HIP_E_HEADER, layer, expert, "record offsets do not fit the shape");
+    if (g->verify && crc32_buf(rec + WARP_HDR_BYTES, (size_t)off[3] + scales - WARP_HDR_BYTES) != crc)
+        return set_err(c, WARP_HIP_E_CRC, layer, expert, "record payload checksum");
+    return 0;
+}
+
+static int is_pinned(const warp_hip_ctx *c, int key)
+{
+    const int E = c->cfg.n_experts;
+    if (c->pin_layer < 0 || key / E != c->pin_layer) return 0;
+    for (int i = 0; i < c->n_pin; i++) if (c->pin[i] == key % E) return 1;
+    return 0;
+}
+
+/* A slot to fill: a never-used one, else the least-frequent (then least
+ * recent) of 16 sampled slots, skipping the layer in flight
+ * (the LFRU sampled victim of src/ecache.c:432-460). */
+static int pick_victim(warp_hip_ctx *c)
+{
+    if (c->next_free < c->n_slots) return c->next_free++;
+    int best = -1;
+    for (int tries = 0; tries < 64 && best < 0; tries++)
+        for (int k = 0; k < 16; k++) {
+            c->rng = c->rng * 1664525u + 1013904223u;
+            const int s = (int)((c->rng >> 8) % (unsigned)c->n_slots);
+            if (c->slot_key[s] >= 0 && is_pinned(c, c->slot_key[s])) continue;
+            if (best < 0 || c->hits[s] < c->hits[best] || (c->hits[s] == c->hits[best] && c->last[s] < c->last[best]))
+                best = s;
+        }
+    return best;
+}
+
+/* Assign (layer, expert) a slot, evicting if needed. Returns the slot or a
+ * negative code. The caller fills it. */
+static int claim_slot(warp_hip_ctx *c, int layer, int expert)
+{
+    const int E = c->cfg.n_experts, key = layer * E + expert;
+    if (c->n_slots <= 0) return set_err(c, WARP_HIP_E_NOSLOT, layer, expert, "no cache slots");
+    const int s = pick_victim(c);
+    if (s < 0) return set_err(c, WARP_HIP_E_NOSLOT, layer, expert, "every sampled slot is in use");
+    const int old = c->slot_key[s];
+    if (old >= 0) {
+        c->key_slot[old] = -1;
+        c->L[old / E].resident--;
+        c->stats.evictions++;
+        if (wk_set_ptr(c->table_dev + old, NULL, c->cp))
+            return set_err(c, WARP_HIP_E_DEVICE, layer, expert, "table update");
+    }
+    c->slot_key[s] = key;
+    c->key_slot[key] = s;
+    c->hits[s] = 0;
+    c->last[s] = ++c->clock;
+    c->L[layer].resident++;
+    return s;
+}
+
+static int publish_slot(warp_hip_ctx *c, int layer, int expert, int s)
+{
+    const int key = layer * c->cfg.n_experts + expert;
+    if (wk_set_ptr(c->table_dev + key, c->pool + (size_t)s * c->cfg.rec_bytes, c->cp))
+        return set_err(c, WARP_HIP_E_DEVICE, layer, expert, "table update");
+    DEV(c, hipEventRecord(c->ev_copy, c->cp));
+    c->copy_pending = 1;
+    return 0;
+}
+
+int warp_hip_put_expert(warp_hip_ctx *c, int layer, int expert, const uint8_t *rec)
+{
+    int rc = check_layer(c, layer);
+    if (rc) return rc;
+    if (expert < 0 || expert >= c->cfg.n_experts || !rec)
+        return set_err(c, WARP_HIP_E_ARG, layer, expert, "expert id");
+    if ((rc = check_record(c, rec, layer, expert))) return rc;
+    const int key = layer * c->cfg.n_experts + expert;
+    int s = c->key_slot[key];
+    if (s < 0 && (s = claim_slot(c, layer, expert)) < 0) return s;
+    /* the overwrite waits for everything already queued on the compute
+     * stream, which may still read the slot's previous record */
+    DEV(c, hipEventRecord(c->ev_before, c->st));
+    DEV(c, hipStreamWaitEvent(c->cp, c->ev_before, 0));
+    DEV(c, hipMemcpyAsync(c->pool + (size_t)s * c->cfg.rec_bytes, rec, c->cfg.rec_bytes, hipMemcpyHostToDevice, c->cp));
+    DEV(c, hipStreamSynchronize(c->cp));
+    return publish_slot(c, layer, expert, s);
+}
+
+int warp_hip_put_expert_dev(warp_hip_ctx *c, int layer, int expert, const uint8_t *rec_dev)
+{
+    int rc = check_layer(c, layer);
+    if (rc) return rc;
+    if (expert < 0 || expert >= c->cfg.n_experts || !rec_dev)
+        return set_err(c, WARP_HIP_E_ARG, layer, expert, "expert id");
+    const int key = layer * c->cfg.n_experts + expert;
+    int s = c->key_slot[key];
+    if (s < 0 && (s = claim_slot(c, layer, expert)) < 0) return s;
+    DEV(c, hipEventRecord(c->ev_before, c->st));
+    DEV(c, hipStreamWaitEvent(c->cp, c->ev_before, 0));
+    DEV(c, hipMemcpyAsync(c->pool + (size_t)s * c->cfg.rec_bytes, rec_dev, c->cfg.rec_bytes,
+                          hipMemcpyDeviceToDevice, c->cp));
+    /* the header is checked on a host copy of its first bytes */
+    uint8_t hdr[WARP_HDR_BYTES];
+    DEV(c, hipMemcpyAsync(hdr, rec_dev, sizeof hdr, hipMemcpyDeviceToHost, c->cp));
+    DEV(c, hipStreamSynchronize(c->cp));
+    const int v = c->cfg.verify;
+    c->cfg.verify = 0;                 /* the payload is not on the host */
+    rc = check_record(c, hdr, layer, expert);
+    c->cfg.verify = v;
+    if (rc) {
+        c->key_slot[key] = -1;
+        c->slot_key[s] = -1;
+        c->L[layer].resident--;
+        return rc;
+    }
+    return publish_slot(c, layer, expert, s);
+}
+
+const uint8_t *warp_hip_resident(warp_hip_ctx *c, int layer, int expert)
+{
+    if (!c || layer < 0 || layer >= c->cfg.n_layers || expert < 0 || expert >= c->cfg.n_experts) return NULL;
+    const int s = c->key_slot[layer * c->cfg.n_experts + expert];
+    return s < 0 ? NULL : c->pool + (size_t)s * c->cfg.rec_bytes;
+}
+
+int warp_hip_set_fetch(warp_hip_ctx *c, warp_hip_fetch_fn fetch, void *user)
+{
+    if (!c) return WARP_HIP_E_ARG;
+    c->fetch = fetch;
+    c->fetch_user = user;
+    return 0;
+}
+
+void warp_hip_get_cache_stats(const warp_hip_ctx *c, warp_hip_cache_stats *st)
+{
+    if (!c || !st) return;
+    *st = c->stats;
+    st->n_slots = c->n_slots;
+    int r = 0;
+    for (int l = 0; l < c->cfg.n_layers; l++) r += c->L[l].resident;
+    st->resident = r;
+}
+
+/* Fetch (layer, expert) through the caller's fetch function into a pinned
+ * staging buffer, check it, and copy it into a slot on the copy stream.
+ * `after` is an event the copy must wait for (the compute that may still
+ * read the victim), or NULL. */
+static int fill_from_fetch(warp_hip_ctx *c, int layer, int expert, hipEvent_t after)
+{
+    if (!c->fetch)
+        return set_err(c, WARP_HIP_E_MISSING, layer, expert, "expert not resident and no fetch function");
+    const int i = c->stage_next;
+    c->stage_next = (c->stage_next + 1) % N_STAGE;
+    if (c->stage_used[i]) DEV(c, hipEventSynchronize(c->ev_stage[i]));
+    uint8_t *dst = c->staging + (size_t)i * c->cfg.rec_bytes;
+    if (c->fetch(c->fetch_user, layer, expert, dst) != 0)
+        return set_err(c, WARP_HIP_E_READ, layer, expert, "fetch failed");
+    int rc = check_record(c, dst, layer, expert);
+    if (rc) return rc;
+    const int s = claim_slot(c, layer, expert);
+    if (s < 0) return s;
+    if (after) DEV(c, hipStreamWaitEvent(c->cp, after, 0));
+    DEV(c, hipMemcpyAsync(c->pool + (size_t)s * c->cfg.rec_bytes, dst, c->cfg.rec_bytes, hipMemcpyHostToDevice, c->cp));
+    DEV(c, hipEventRecord(c->ev_stage[i], c->cp));
+    c->stage_used[i] = 1;
+    c->stats.bytes_read += c->cfg.rec_bytes;
+    return publish_slot(c, layer, expert, s);
+}
+
+static int prefetch_after(warp_hip_ctx *c, int layer, const int *ids, int n, hipEvent_t after)
+{
+    int rc;
+    for (int i = 0; i < n; i++) {
+        if (ids[i] < 0 || ids[i] >= c->cfg.n_experts) continue;
+        if (c->key_slot[layer * c->cfg.n_experts + ids[i]] >= 0) continue;
+        /* a guess: not a miss, and never allowed to stall on a full cache */
+        if ((rc = fill_from_fetch(c, layer, ids[i], after)) != 0) {
+            if (rc == WARP_HIP_E_NOSLOT) return 0;
+            return rc;
+        }
+        c->stats.spec_issued++;
+    }
+    return 0;
+}
+
+int warp_hip_prefetch(warp_hip_ctx *c, int layer, const int *ids, int n)
+{
+    int rc = check_layer(c, layer);
+    if (rc) return rc;
+    /* everything queued so far may still read the slots it would evict */
+    DEV(c, hipEventRecord(c->ev_after, c->st));
+    return prefetch_after(c, layer, ids, n, c->ev_after);
+}
+
+/* Demand residency for `n` experts of `layer`, all pinned against eviction
+ * until the next layer pins its own. Hits and misses are counted per record
+ * asked for, as waste_ecache_get counts them (src/ecache.c:596-669). */
+static int ensure_selected(warp_hip_ctx *c, int layer, const int *ids, int n)
+{
+    const int E = c->cfg.n_experts;
+    c->pin_layer = layer;
+    c->n_pin = 0;
+    for (int j = 0; j < n; j++) {
+        if (ids[j] < 0 || ids[j] >= E) return set_err(c, WARP_HIP_E_ARG, layer, ids[j], "expert id from the router");
+        c->pin[c->n_pin++] = ids[j];
+    }
+    for (int j = 0; j < n; j++) {
+        const int e = ids[j];
+        const int s = c->key_slot[layer * E + e];
+        if (s >= 0) {
+            c->stats.hits++;
+            c->hits[s]++;
+            c->last[s] = ++c->clock;
+            continue;
+        }
+        c->stats.misses++;
+        int rc = fill_from_fetch(c, layer, e, NULL);
+        if (rc) return rc;
+    }
+    return 0;
+}
+
+static int wait_copies(warp_hip_ctx *c)
+{
+    if (c->copy_pending) {
+        DEV(c, hipStreamWaitEvent(c->st, c->ev_copy, 0));
+        c->copy_pending = 0;
+    }
+    return 0;
+}
+
+/* ---- the layer ------------------------------------------------------------------------------ */
+
+static const uint16_t *books_kind(const warp_hip_ctx *c, const layer_t *L, int kind)
+{
+    return L->books + (size_t)kind * c->S * c->En * 8;
+}
+
+static int logits_of(warp_hip_ctx *c, const layer_t *L, const float *x, int T, float *logits, hipStream_t s)
+{
+    const warp_hip_cfg *g = &c->cfg;
+    if (L->router)
+        return wk_router_logits(L->router, x, g->n_experts, g->hidden, T, g->router_strict, logits, s);
+    if (L->rq)
+        return wk_mvq(L->rq, L->rs, L->r_rowbytes, L->r_group, L->r_bits, x, g->n_experts, g->hidden, T, logits, s);
+    return -1;
+}
+
+static int shared_ffn(warp_hip_ctx *c, const layer_t *L, const float *x, int T)
+{
+    const warp_hip_cfg *g = &c->cfg;
+    const int H = g->hidden, Is = L->s_inter;
+    KRN(c, wk_mvq(L->sq[0], L->ss[0], L->s_rowbytes[0], L->s_group, L->s_bits, x, Is, H, T, c->shg, c->st));
+    KRN(c, wk_mvq(L->sq[1], L->ss[1], L->s_rowbytes[1], L->s_group, L->s_bits, x, Is, H, T, c->shu, c->st));
+    KRN(c, wk_act(c->shg, c->shu, T, Is, g->act_situ, g->situ_beta, g->situ_linear_beta, c->shh, c->st));
+    KRN(c, wk_mvq(L->sq[2], L->ss[2], L->s_rowbytes[2], L->s_group, L->s_bits, c->shh, H, Is, T, c->sho, c->st));
+    return 0;
+}
+
+/* Lookahead (src/model.c:2680-2711, 2923-2931): layer L+1's router on layer
+ * L's input, top-n by biased sigmoid score, issued as speculative fills. The
+ * router runs on its own stream from the start of the layer; the fills are
+ * issued after this layer's expert kernels are queued and may not evict
+ * this layer's experts. */
+static int lookahead_launch(warp_hip_ctx *c, int layer, const float *x_dev)
+{
+    const warp_hip_cfg *g = &c->cfg;
+    if (!g->lookahead || !c->fetch || layer + 1 >= g->n_layers) return 0;
+    const layer_t *N = &c->L[layer + 1];
+    if (!N->router && !N->rq) return 0;
+    if (N->resident == g->n_experts) return 0;
+    const int n = g->lookahead < g->n_experts ? (g->lookahead < WARP_MAX_K ? g->lookahead : WARP_MAX_K) : g->n_experts;
+    DEV(c, hipEventRecord(c->ev_x, c->st));
+    DEV(c, hipStreamWaitEvent(c->la, c->ev_x, 0));
+    KRN(c, logits_of(c, N, x_dev, 1, c->la_logits, c->la));
+    KRN(c, wk_route(c->la_logits, N->bias, g->n_experts, n, 1, WARP_HIP_ROUTE_SIGMOID, 0, 1.0f, c->la_idx, c->la_w,
+                    NULL, NULL, NULL, NULL, c->la));
+    DEV(c, hipMemcpyAsync(c->h_la_idx, c->la_idx, (size_t)n * sizeof(int), hipMemcpyDeviceToHost, c->la));
+    DEV(c, hipEventRecord(c->ev_la, c->la));
+    return n;
+}
+
+/* When this layer's selection is pinned (it went through the host), the
+ * fills need only wait for the work queued before this layer's expert
+ * kernels, and so overlap them; otherwise they wait for the whole layer. */
+static int lookahead_issue(warp_hip_ctx *c, int layer, int n)
+{
+    if (n <= 0) return 0;
+    DEV(c, hipEventSynchronize(c->ev_la));
+    return prefetch_after(c, layer + 1, c->h_la_idx, n, c->pin_layer == layer ? c->ev_before : c->ev_after);
+}
+
+int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *out_dev, const float *resid_dev,
+                        int *idx, float *w)
+{
+    int rc = check_layer(c, layer);
+    if (rc) return rc;
+    const warp_hip_cfg *g = &c->cfg;
+    const layer_t *L = &c->L[layer];
+    const int E = g->n_experts, K = g->top_k, H = g->hidden, I = g->inter;
+    if (!L->has_books || (!L->router && !L->rq))
+        return set_err(c, WARP_HIP_E_ARG, layer, -1, "layer %d has no codebooks or router", layer);
+    const uint8_t *const *table = c->table_dev + (size_t)layer * E;
+
+    /* inputs for the gate/up matvecs, then the router */
+    if (c->P6) {
+        const size_t nvH = (size_t)H / 8, nblkH = (nvH + WARP_LUT_BLK - 1) / WARP_LUT_BLK;
+        KRN(c, wk_lut_p6(x_dev, 1, H, books_kind(c, L, 0), c->lut8, c->lscale, c->st));
+        KRN(c, wk_lut_p6(x_dev, 1, H, books_kind(c, L, 1), c->lut8 + nvH * 256, c->lscale + nblkH, c->st));
+    } else {
+        KRN(c, wk_split(x_dev, 1, H, c->xs, c->xscale, c->st));
+    }
+    KRN(c, logits_of(c, L, x_dev, 1, c->logits, c->st));
+    const int n_la = lookahead_launch(c, layer, x_dev);
+    if (n_la < 0) return n_la;
+
+    if (L->resident == E) {
+        /* everything resident: route and build the jobs on the device, no
+         * host round trip */
+        KRN(c, wait_copies(c));
+        KRN(c, wk_route(c->logits, L->bias, E, K, 1, g->router_act, g->renorm, g->routed_scale, c->idx, c->w, table,
+                        c->jobs, c->njobs, c->missing, c->st));
+        c->stats.hits += (uint64_t)K;
+        if (c->pin_layer == layer) c->pin_layer = -1;
+    } else if (!c->fetch) {
+        /* nothing to fetch with: the device reports a selected expert that is
+         * not resident, and the layer is refused rather than summed short */
+        KRN(c, wait_copies(c));
+        DEV(c, hipMemsetAsync(c->missing, 0, sizeof(int), c->st));
+        KRN(c, wk_route(c->logits, L->bias, E, K, 1, g->router_act, g->renorm, g->routed_scale, c->idx, c->w, table,
+                        c->jobs, c->njobs, c->missing, c->st));
+        DEV(c, hipMemcpyAsync(c->h_missing, c->missing, sizeof(int), hipMemcpyDeviceToHost, c->st));
+        DEV(c, hipStreamSynchronize(c->st));
+        if (*c->h_missing) return set_err(c, WARP_HIP_E_MISSING, layer, -1, "a selected expert is not resident");
+        if (c->pin_layer == layer) c->pin_layer = -1;
+    } else {
+        KRN(c, wk_route(c->logits, L->bias, E, K, 1, g->router_act, g->renorm, g->routed_scale, c->idx, c->w, NULL,
+                        NULL, NULL, NULL, c->st));
+        DEV(c, hipMemcpyAsync(c->h_idx, c->idx, (size_t)K * sizeof(int), hipMemcpyDeviceToHost, c->st));
+        DEV(c, hipStreamSynchronize(c->st));
+        if ((rc = ensure_selected(c, layer, c->h_idx, K))) return rc;
+        KRN(c, wait_copies(c));
+        KRN(c, wk_route(c->logits, L->bias, E, K, 1, g->router_act, g->renorm, g->routed_scale, c->idx, c->w, table,
+                        c->jobs, c->njobs, c->missing, c->st));
+    }
+    DEV(c, hipEventRecord(c->ev_before, c->st));
+
+    /* gate and up, activation, down */
+    float *yk[3] = { c->yg, c->yu, c->yd };
+    if (c->P6) {
+        const size_t nvH = (size_t)H / 8, nblkH = (nvH + WARP_LUT_BLK - 1) / WARP_LUT_BLK;
+        KRN(c, wk_apply_p6(c->jobs, c->njobs, K, 0, c->lut8, c->lscale, c->yg, I, H, c->st));
+        KRN(c, wk_apply_p6(c->jobs, c->njobs, K, 1, c->lut8 + nvH * 256, c->lscale + nblkH, c->yu, I, H, c->st));
+        KRN(c, wk_act(c->yg, c->yu, K, I, g->act_situ, g->situ_beta, g->situ_linear_beta, c->hbuf, c->st));
+        KRN(c, wk_lut_p6(c->hbuf, K, I, books_kind(c, L, 2), c->lut8d, c->lscaled, c->st));
+        KRN(c, wk_apply_p6(c->jobs, c->njobs, K, 2, c->lut8d, c->lscaled, c->yd, H, I, c->st));
+    } else {
+        KRN(c, wk_vq_matvec(g->fmt, c->jobs, c->njobs, K, 0, 2, L->books, c->xs, c->xscale, yk, I, H, 1, c->st));
+        KRN(c, wk_act_split(c->yg, c->yu, K, I, g->act_situ, g->situ_beta, g->situ_linear_beta, c->xsh, c->xscaleh,
+                            NULL, c->st));
+        KRN(c, wk_vq_matvec(g->fmt, c->jobs, c->njobs, K, 2, 1, L->books, c->xsh, c->xscaleh, yk, H, I, 1, c->st));
+    }
+    if (L->sq[0] && (rc = shared_ffn(c, L, x_dev, 1))) return rc;
+    KRN(c, wk_combine(c->yd, c->w, K, H, L->sq[0] ? c->sho : NULL, resid_dev, out_dev, c->st));
+    DEV(c, hipEventRecord(c->ev_after, c->st));
+
+    if ((rc = lookahead_issue(c, layer, n_la))) return rc;
+    if (idx || w) {
+        if (idx) DEV(c, hipMemcpyAsync(c->h_idx, c->idx, (size_t)K * sizeof(int), hipMemcpyDeviceToHost, c->st));
+        if (w) DEV(c, hipMemcpyAsync(c->h_w, c->w, (size_t)K * sizeof(float), hipMemcpyDeviceToHost, c->st));
+        DEV(c, hipStreamSynchronize(c->st));
+        if (idx) memcpy(idx, c->h_idx, (size_t)K * sizeof(int));
+        if (w) memcpy(w, c->h_w, (size_t)K * sizeof(float));
+    }
+    return 0;
+}
+
+int warp_hip_moe_decode_host(warp_hip_ctx *c, int layer, const float *x, float *out, int *routed)
+{
+    if (!c) return WARP_HIP_E_ARG;
+    const int H = c->cfg.hidden;
+    DEV(c, hipMemcpyAsync(c->xin, x, (size_t)H * 4, hipMemcpyHostToDevice, c->st));
+    int rc = warp_hip_moe_decode(c, layer, c->xin, c->xout, NULL, routed, NULL);
+    if (rc) return rc;
+    DEV(c, hipMemcpyAsync(out, c->xout, (size_t)H * 4, hipMemcpyDeviceToHost, c->st));
+    DEV(c, hipStreamSynchronize(c->st));
+    return 0;
+}
+
+int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *out_dev, int T, int *route, float *rw)
+{
+    int rc = check_layer(c, layer);
+    if (rc) return rc;
+    const warp_hip_cfg *g = &c->cfg;
+    const layer_t *L = &c->L[layer];
+    const int E = g->n_experts, K = g->top_k, H = g->hidden, I = g->inter;
+    if (T < 1 || T > g->max_tokens) return set_err(c, WARP_HIP_E_ARG, layer, -1, "T = %d, max_tokens = %d", T, g->max_tokens);
+    if (!L->has_books || (!L->router && !L->rq))
+        return set_err(c, WARP_HIP_E_ARG, layer, -1, "layer %d has no codebooks or router", layer);
+    const uint8_t *const *table = c->table_dev + (size_t)layer * E;
+    const int P = T * K;
+
+    KRN(c, logits_of(c, L, X_dev, T, c->logits, c->st));
+    KRN(c, wk_route(c->logits, L->bias, E, K, T, g->router_act, g->renorm, g->routed_scale, c->idx, c->w, NULL, NULL,
+                    NULL, NULL, c->st));
+    if (L->resident != E && c->fetch) {
+        DEV(c, hipMemcpyAsync(c->h_idx, c->idx, (size_t)P * sizeof(int), hipMemcpyDeviceToHost, c->st));
+        DEV(c, hipStreamSynchronize(c->st));
+        /* each distinct record once, ascending (src/model.c:3595-3603) */
+        int *ids = (int *)malloc((size_t)E * sizeof(int));
+        if (!ids) return set_err(c, WARP_HIP_E_NOMEM, layer, -1, "host allocation failed");
+        char *used = (char *)calloc((size_t)E, 1);
+        if (!used) { free(ids); return set_err(c, WARP_HIP_E_NOMEM, layer, -1, "host allocation failed"); }
+        for (int q = 0; q < P; q++)
+            if (c->h_idx[q] >= 0 && c->h_idx[q] < E) used[c->h_idx[q]] = 1;
+        int n = 0;
+        for (int e = 0; e < E; e++) if (used[e]) ids[n++] = e;
+        rc = ensure_selected(c, layer, ids, n);
+        free(ids);
+        free(used);
+        if (rc) return rc;
+    }
+    KRN(c, wait_copies(c));
+    DEV(c, hipMemsetAsync(c->missing, 0, sizeof(int), c->st));
+    KRN(c, wk_plan_chunk(c->idx, c->w, T, K, E, table, c->counts, c->offsets, c->pair_tok, c->pair_exp, c->pair_w,
+                         c->jobs, c->max_jobs, c->njobs, c->missing, c->st));
+    DEV(c, hipEventRecord(c->ev_before, c->st));
+    float *yk[3] = { c->yg, c->yu, c->yd };
+    if (c->P6) {
+        const size_t nvH = (size_t)H / 8, nblkH = (nvH + WARP_LUT_BLK - 1) / WARP_LUT_BLK;
+        /* per token: gate LUT at [t][0], up LUT at [t][1] */
+        KRN(c, wk_lut_p6(X_dev, T, H, books_kind(c, L, 0), c->lut8, c->lscale, c->st));
+        KRN(c, wk_lut_p6(X_dev, T, H, books_kind(c, L, 1), c->lut8 + (size_t)T * nvH * 256, c->lscale + (size_t)T * nblkH,
+                         c->st));
+        KRN(c, wk_apply_p6(c->jobs, c->njobs, c->max_jobs, 0, c->lut8, c->lscale, c->yg, I, H, c->st));
+        KRN(c, wk_apply_p6(c->jobs, c->njobs, c->max_jobs, 1, c->lut8 + (size_t)T * nvH * 256,
+                           c->lscale + (size_t)T * nblkH, c->yu, I, H, c->st));
+        KRN(c, wk_act(c->yg, c->yu, P, I, g->act_situ, g->situ_beta, g->situ_linear_beta, c->hbuf, c->st));
+        KRN(c, wk_lut_p6(c->hbuf, P, I, books_kind(c, L, 2), c->lut8d, c->lscaled, c->st));
+        KRN(c, wk_apply_p6(c->jobs, c->njobs, c->max_jobs, 2, c->lut8d, c->lscaled, c->yd, H, I, c->st));
+    } else {
+        KRN(c, wk_split(X_dev, T, H, c->xs, c->xscale, c->st));
+        KRN(c, wk_vq_matvec(g->fmt, c->jobs, c->njobs, c->max_jobs, 0, 2, L->books, c->xs, c->xscale, yk, I, H,
+                            WARP_TPJ, c->st));
+        KRN(c, wk_act_split(c->yg, c->yu, P, I, g->act_situ, g->situ_beta, g->situ_linear_beta, c->xsh, c->xscaleh,
+                            NULL, c->st));
+        KRN(c, wk_vq_matvec(g->fmt, c->jobs, c->njobs, c->max_jobs, 2, 1, L->books, c->xsh, c->xscaleh, yk, H, I,
+                            WARP_TPJ, c->st));
+    }
+    if (L->sq[0] && (rc = shared_ffn(c, L, X_dev, T))) return rc;
+    KRN(c, wk_combine_chunk(c->yd, c->offsets, c->pair_tok, c->pair_w, T, K, E, H, L->sq[0] ? c->sho : NULL, out_dev,
+                            c->st));
+    DEV(c, hipMemcpyAsync(c->h_missing, c->missing, sizeof(int), hipMemcpyDeviceToHost, c->st));
+    if (route) DEV(c, hipMemcpyAsync(c->h_idx, c->idx, (size_t)P * sizeof(int), hipMemcpyDeviceToHost, c->st));
+    if (rw) DEV(c, hipMemcpyAsync(c->h_w, c->w, (size_t)P * sizeof(float), hipMemcpyDeviceToHost, c->st));
+    DEV(c, hipStreamSynchronize(c->st));
+    if (*c->h_missing)
+        return set_err(c, WARP_HIP_E_MISSING, layer, -1,
+                       *c->h_missing == 2 ? "chunk needs more jobs than planned" : "a selected expert is not resident");
+    if (route) memcpy(route, c->h_idx, (size_t)P * sizeof(int));
+    if (rw) memcpy(rw, c->h_w, (size_t)P * sizeof(float));
+    return 0;
+}
+
+int warp_hip_moe_chunk_host(warp_hip_ctx *c, int layer, const float *X, float *out, int T, int *route, float *rw)
+{
+    if (!c) return WARP_HIP_E_ARG;
+    if (T < 1 || T > c->cfg.max_tokens) return set_err(c, WARP_HIP_E_ARG, layer, -1, "T out of range");
+    const size_t bytes = (size_t)T * c->cfg.hidden * 4;
+    DEV(c, hipMemcpyAsync(c->xin, X, bytes, hipMemcpyHostToDevice, c->st));
+    int rc = warp_hip_moe_chunk(c, layer, c->xin, c->xout, T, route, rw);
+    if (rc) return rc;
+    DEV(c, hipMemcpyAsync(out, c->xout, bytes, hipMemcpyDeviceToHost, c->st));
+    DEV(c, hipStreamSynchronize(c->st));
+    return 0;
+}
+
+/* ---- finer-grained entry points -------------------------------------------------------------- */
+
+static int matrix_shape(const warp_hip_ctx *c, int kind, int *M, int *N)
+{
+    if (kind < 0 || kind > 2) return -1;
+    *M = kind == 2 ? c->cfg.hidden : c->cfg.inter;
+    *N = kind == 2 ? c->cfg.inter : c->cfg.hidden;
+    return 0;
+}
+
+int warp_hip_vq_matvec(warp_hip_ctx *c, int layer, int kind, const uint8_t *rec_dev, const float *x_dev, float *y_dev)
+{
+    int rc = check_layer(c, layer);
+    if (rc) return rc;
+    const layer_t *L = &c->L[layer];
+    int M, N;
+    if (matrix_shape(c, kind, &M, &N) || !rec_dev || !L->has_books)
+        return set_err(c, WARP_HIP_E_ARG, layer, -1, "vq_matvec arguments");
+    warp_job jb;
+    memset(&jb, 0, sizeof jb);
+    jb.rec = rec_dev;
+    jb.kind = kind;
+    jb.n = 1;
+    int nj[3] = { 0, 0, 0 };
+    nj[kind] = 1;
+    /* one job of this kind, list stride 1 */
+    warp_job jl[3];
+    memset(jl, 0, sizeof jl);
+    jl[kind] = jb;
+    DEV(c, hipMemcpyAsync(c->jobs, jl, sizeof jl, hipMemcpyHostToDevice, c->st));
+    DEV(c, hipMemcpyAsync(c->njobs, nj, sizeof nj, hipMemcpyHostToDevice, c->st));
+    /* scratch sized for the input width: hidden for gate/up, inter for down */
+    if (c->P6) {
+        int8_t *lut = kind == 2 ? c->lut8d : c->lut8;
+        float *ls = kind == 2 ? c->lscaled : c->lscale;
+        KRN(c, wk_lut_p6(x_dev, 1, N, books_kind(c, L, kind), lut, ls, c->st));
+        KRN(c, wk_apply_p6(c->jobs, c->njobs, 1, kind, lut, ls, y_dev, M, N, c->st));
+    } else {
+        float *yk[3] = { y_dev, y_dev, y_dev };
+        uint16_t *xs = kind == 2 ? c->xsh : c->xs;
+        float *xsc = kind == 2 ? c->xscaleh : c->xscale;
+        KRN(c, wk_split(x_dev, 1, N, xs, xsc, c->st));
+        KRN(c, wk_vq_matvec(c->cfg.fmt, c->jobs, c->njobs, 1, kind, 1, L->books, xs, xsc, yk, M, N, 1, c->st));
+    }
+    DEV(c, hipStreamSynchronize(c->st));
+    return 0;
+}
+
+int warp_hip_decode_weights(warp_hip_ctx *c, int layer, int kind, const uint8_t *rec_dev, float *W_dev)
+{
+    int rc = check_layer(c, layer);
+    if (rc) return rc;
+    const layer_t *L = &c->L[layer];
+    int M, N;
+    if (matrix_shape(c, kind, &M, &N) || !rec_dev || !L->has_books)
+        return set_err(c, WARP_HIP_E_ARG, layer, -1, "decode_weights arguments");
+    uint8_t hdr[WARP_HDR_BYTES];
+    DEV(c, hipMemcpy(hdr, rec_dev, sizeof hdr, hipMemcpyDeviceToHost));
+    uint32_t off[4];
+    memcpy(off, hdr + 20, 16);
+    const size_t soff = kind == 0 ? 0 : kind == 1 ? (size_t)c->cfg.inter : 2 * (size_t)c->cfg.inter;
+    if (off[3] + 2 * (2 * (size_t)c->cfg.inter + c->cfg.hidden) > c->cfg.rec_bytes || off[kind] >= off[3])
+        return set_err(c, WARP_HIP_E_HEADER, layer, -1, "record offsets");
+    KRN(c, wk_decode_weights(c->cfg.fmt, rec_dev + off[kind], (const uint16_t *)(rec_dev + off[3]) + soff,
+                             books_kind(c, L, kind), M, N, W_dev, c->st));
+    DEV(c, hipStreamSynchronize(c->st));
+    return 0;
+}
+
+int warp_hip_router_logits(warp_hip_ctx *c, int layer, const float *x_dev, int T, float *logits_dev)
+{
+    int rc = check_layer(c, layer);
+    if (rc) return rc;
+    KRN(c, logits_of(c, &c->L[layer], x_dev, T, logits_dev, c->st));
+    DEV(c, hipStreamSynchronize(c->st));
+    return 0;
+}
+
+int warp_hip_route(warp_hip_ctx *c, int layer, const float *logits_dev, int T, int *idx_dev, float *w_dev)
+{
+    int rc = check_layer(c, layer);
+    if (rc) return rc;
+    const warp_hip_cfg *g = &c->cfg;
+    KRN(c, wk_route(logits_dev, c->L[layer].bias, g->n_experts, g->top_k, T, g->router_act, g->renorm, g->routed_scale,
+                    idx_dev, w_dev, NULL, NULL, NULL, NULL, c->st));
+    DEV(c, hipStreamSynchronize(c->st));
+    return 0;
+}
+
+int warp_hip_mvq(warp_hip_ctx *c, int bits, int group, const int8_t *q_dev, const uint16_t *scales_dev,
+                 size_t rowbytes, const float *x_dev, int M, int N, int T, float *y_dev)
+{
+    if (!c) return WARP_HIP_E_ARG;
+    KRN(c, wk_mvq(q_dev, scales_dev, rowbytes, group, bits, x_dev, M, N, T, y_dev, c->st));
+    DEV(c, hipStreamSynchronize(c->st));
+    return 0;
+}
+
+int warp_hip_fill_random(warp_hip_ctx *c, void *dev, size_t n, uint64_t seed)
+{
+    if (!c) return WARP_HIP_E_ARG;
+    KRN(c, wk_fill_random((uint8_t *)dev, n, seed, c->st));
+    return 0;
+}

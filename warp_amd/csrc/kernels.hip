@@ -1,0 +1,950 @@
+// kernels.hip — gfx950 kernels for the routed-expert MoE path, and their
+// launchers (extern "C", declared in warp_internal.h).
+//
+// The expert matvec is decode-then-dot on the matrix cores: each lane reads
+// the code word of 4 rows at one vector position (12 bytes, coalesced across
+// the wave), gathers the 8-dim fp16 codebook vector of every stage from LDS
+// and feeds it as the A operand of v_mfma_f32_16x16x32_f16, whose B operand
+// holds the input split into two fp16 halves (hi, lo) per token slot. fp16 x
+// fp16 products are exact in fp32, so the result is the fp32 dot product of
+// the decoded weights with x to ~22 bits of x. The reference computes the
+// same sum through a float LUT (src/model.c:1843-2024); the two agree within
+// fp32 rounding.
+//
+// Built with -ffp-contract=off: every multiply-add that must be fused is an
+// explicit __builtin_fmaf, every one that must not be is left as two
+// operations, matching the reference's x86 build where it matters (VQ4P).
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "warp_internal.h"
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef unsigned u2v __attribute__((ext_vector_type(2)));
+typedef unsigned u3v __attribute__((ext_vector_type(3)));
+
+#define CHECK_LAUNCH()                                   \
+    do {                                                 \
+        hipError_t e_ = hipGetLastError();               \
+        if (e_ != hipSuccess) return -(int)e_ - 1000;    \
+    } while (0)
+
+// ---- scalar helpers ---------------------------------------------------------
+
+// fp16 bits -> f32 keeping subnormals (src/simd.h:49-67, exponent 31 rebiased
+// as a normal number, exactly as the reference does).
+__device__ __forceinline__ float f16_keep(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h >> 15) << 31;
+    const uint32_t e = (h >> 10) & 0x1f, mn = h & 0x3ff;
+    if (e == 0) {
+        const float f = (float)mn * 5.9604644775390625e-08f;
+        return sign ? -f : f;
+    }
+    return __uint_as_float(sign | ((e + 112u) << 23) | (mn << 13));
+}
+
+// fp16 bits (already flushed on upload) -> f32 with the same rebiasing.
+__device__ __forceinline__ float f16_flushed(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h >> 15) << 31;
+    const uint32_t e = (h >> 10) & 0x1f, mn = h & 0x3ff;
+    return __uint_as_float(e ? (sign | ((e + 112u) << 23) | (mn << 13)) : sign);
+}
+
+// expf rounded from a double-precision exp: the correctly rounded value in
+// all but a vanishing fraction of inputs.
+__device__ __forceinline__ float exp_cr(float x) { return (float)exp((double)x); }
+
+__device__ __forceinline__ float silu_ref(float v) {
+    // src/model.c:501: v / (1 + expf(-v))
+    return __fdiv_rn(v, __fadd_rn(1.0f, exp_cr(-v)));
+}
+
+__device__ __forceinline__ float act_pair(float g, float u, int situ, float beta, float lbeta) {
+    if (!situ) return __fmul_rn(silu_ref(g), u);
+    // src/model.c:505-509
+    const float a = __fdiv_rn(__fmul_rn(beta, tanhf(__fdiv_rn(g, beta))), __fadd_rn(1.0f, exp_cr(-g)));
+    return __fmul_rn(a, lbeta > 0.0f ? __fmul_rn(lbeta, tanhf(__fdiv_rn(u, lbeta))) : u);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+// block-wide max of |v| over blockDim.x (a multiple of 64, <= 1024)
+__device__ float block_absmax(float v) {
+    __shared__ float red[16];
+    v = wave_max(fabsf(v));
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float m = 0.0f;
+    for (int i = 0; i < (int)(blockDim.x >> 6); i++) m = fmaxf(m, red[i]);
+    __syncthreads();
+    return m;
+}
+
+// Scale exponent k for the split: max|x| * 2^k in [2^14, 2^15).
+__device__ __forceinline__ int split_exp(float mx) {
+    if (!(mx > 0.0f) || !isfinite(mx)) return 0;
+    int e;
+    (void)frexpf(mx, &e);
+    return 15 - e;
+}
+
+__device__ __forceinline__ void split_store(float x, int k, _Float16 *hi, _Float16 *lo) {
+    const float xs = ldexpf(x, k);
+    const _Float16 h = (_Float16)xs;
+    *hi = h;
+    *lo = (_Float16)(xs - (float)h);
+}
+
+// ---- split -------------------------------------------------------------------
+
+__global__ __launch_bounds__(256) void k_split(const float *__restrict__ x, int N,
+                                               _Float16 *__restrict__ xs, float *__restrict__ xscale) {
+    const int t = blockIdx.x;
+    const float *xt = x + (size_t)t * N;
+    float m = 0.0f;
+    for (int i = threadIdx.x; i < N; i += blockDim.x) m = fmaxf(m, fabsf(xt[i]));
+    m = block_absmax(m);
+    const int k = split_exp(m);
+    _Float16 *o = xs + (size_t)t * N * 2;
+    for (int i = threadIdx.x; i < N; i += blockDim.x) {
+        const int v = i >> 3, d = i & 7;
+        split_store(xt[i], k, &o[v * 16 + d], &o[v * 16 + 8 + d]);
+    }
+    if (threadIdx.x == 0) xscale[t] = ldexpf(1.0f, -k);
+}
+
+extern "C" int wk_split(const float *x, int T, int N, uint16_t *xs, float *xscale, void *stream) {
+    if (T <= 0 || N <= 0 || (N & 7)) return -1;
+    hipLaunchKernelGGL(k_split, dim3(T), dim3(256), 0, (hipStream_t)stream, x, N, (_Float16 *)xs, xscale);
+    CHECK_LAUNCH();
+    return 0;
+}
+
+// ---- router logits --------------------------------------------------------------
+
+// One wave per (token, row): float4 loads, lane partials, fixed xor tree.
+__global__ __launch_bounds__(256) void k_router_fast(const float *__restrict__ W, const float *__restrict__ x,
+                                                     int E, int H, int T, float *__restrict__ logits) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= E * T) return;
+    const int t = row / E, e = row % E;
+    const float *w = W + (size_t)e * H, *xt = x + (size_t)t * H;
+    float acc = 0.0f;
+    if ((H & 3) == 0) {
+        const float4 *w4 = (const float4 *)w, *x4 = (const float4 *)xt;
+        for (int i = lane; i < H / 4; i += 64) {
+            const float4 a = w4[i], b = x4[i];
+            acc = __builtin_fmaf(a.x, b.x, acc);
+            acc = __builtin_fmaf(a.y, b.y, acc);
+            acc = __builtin_fmaf(a.z, b.z, acc);
+            acc = __builtin_fmaf(a.w, b.w, acc);
+        }
+    } else {
+        for (int i = lane; i < H; i += 64) acc = __builtin_fmaf(w[i], xt[i], acc);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) logits[row] = acc;
+}
+
+// The reference's dotf on x86 (src/model.c:155-160): one sequential, unfused
+// sum per row, bit for bit.
+__global__ __launch_bounds__(64) void k_router_strict(const float *__restrict__ W, const float *__restrict__ x,
+                                                      int E, int H, int T, float *__restrict__ logits) {
+    const int row = blockIdx.x * 64 + threadIdx.x;
+    if (row >= E * T) return;
+    const int t = row / E, e = row % E;
+    const float *w = W + (size_t)e * H, *xt = x + (size_t)t * H;
+    float acc = 0.0f;
+    for (int i = 0; i < H; i++) acc = __fadd_rn(acc, __fmul_rn(w[i], xt[i]));
+    logits[row] = acc;
+}
+
+extern "C" int wk_router_logits(const float *W, const float *x, int E, int H, int T, int strict,
+                                float *logits, void *stream) {
+    if (E <= 0 || H <= 0 || T <= 0) return -1;
+    const int rows = E * T;
+    if (strict)
+        hipLaunchKernelGGL(k_router_strict, dim3((rows + 63) / 64), dim3(64), 0, (hipStream_t)stream, W, x, E, H,
+                           T, logits);
+    else
+        hipLaunchKernelGGL(k_router_fast, dim3((rows + 3) / 4), dim3(256), 0, (hipStream_t)stream, W, x, E, H, T,
+                           logits);
+    CHECK_LAUNCH();
+    return 0;
+}
+
+// ---- quantised rows (Q8G / Q4G / Q3G) ------------------------------------------------
+
+__device__ __forceinline__ int q_at(const int8_t *row, int bits, int i) {
+    if (bits == 8) return row[i];
+    if (bits == 4) {
+        const uint8_t b = ((const uint8_t *)row)[i >> 1];
+        return (i & 1) ? (int)(b >> 4) - 8 : (int)(b & 0x0F) - 8;
+    }
+    const uint8_t *p = (const uint8_t *)row;
+    const long off = (long)i * 3;
+    const int v = (p[off >> 3] >> (off & 7)) | (p[(off >> 3) + 1] << (8 - (off & 7)));
+    return (v & 7) - 4;
+}
+
+// One wave per (token, output row). Lanes take whole groups; a group's
+// partial dot is scaled by its fp16 scale, then the lanes' sums are reduced.
+__global__ __launch_bounds__(256) void k_mvq(const int8_t *__restrict__ W, const uint16_t *__restrict__ ws,
+                                             size_t rowbytes, int g, int bits, const float *__restrict__ x,
+                                             int M, int N, int T, float *__restrict__ y) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= M * T) return;
+    const int t = row / M, o = row % M;
+    const int ng = (N + g - 1) / g;
+    const int8_t *wr = W + (size_t)o * rowbytes;
+    const uint16_t *sr = ws + (size_t)o * ng;
+    const float *xt = x + (size_t)t * N;
+    float acc = 0.0f;
+    for (int k = lane; k < ng; k += 64) {
+        const int lim = (k * g + g <= N) ? g : N - k * g;
+        float part = 0.0f;
+        for (int i = 0; i < lim; i++) part = __builtin_fmaf((float)q_at(wr, bits, k * g + i), xt[k * g + i], part);
+        acc = __builtin_fmaf(f16_keep(sr[k]), part, acc);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) y[row] = acc;
+}
+
+extern "C" int wk_mvq(const int8_t *W, const uint16_t *ws, size_t rowbytes, int group, int bits,
+                      const float *x, int M, int N, int T, float *y, void *stream) {
+    if (M <= 0 || N <= 0 || T <= 0 || group <= 0 || (bits != 8 && bits != 4 && bits != 3)) return -1;
+    hipLaunchKernelGGL(k_mvq, dim3((M * T + 3) / 4), dim3(256), 0, (hipStream_t)stream, W, ws, rowbytes, group,
+                       bits, x, M, N, T, y);
+    CHECK_LAUNCH();
+    return 0;
+}
+
+// ---- routing -----------------------------------------------------------------------
+
+// One 64-lane block per token. Scores in LDS; K rounds of a wave argmax
+// where the larger biased score wins and, on equal scores, the lower expert
+// id (the reference scans ids upwards with strict >, src/model.c:2729-2742).
+__global__ __launch_bounds__(64) void k_route(const float *__restrict__ logits, const float *__restrict__ bias,
+                                              int E, int K, int act, int renorm, float routed_scale,
+                                              int *__restrict__ idx, float *__restrict__ w,
+                                              const uint8_t *const *__restrict__ table, warp_job *__restrict__ jobs,
+                                              int *__restrict__ njobs, int *__restrict__ missing) {
+    extern __shared__ float lds_route[];
+    float *score = lds_route;             // [E]
+    float *biased = lds_route + E;        // [E], -inf once taken
+    __shared__ int sel[WARP_MAX_K];
+    __shared__ float wsel[WARP_MAX_K];
+    const int t = blockIdx.x, lane = threadIdx.x;
+    const float *lt = logits + (size_t)t * E;
+    if (act == 1) {
+        float mx = -INFINITY;
+        for (int e = lane; e < E; e += 64) mx = fmaxf(mx, lt[e]);
+        mx = wave_max(mx);
+        for (int e = lane; e < E; e += 64) score[e] = exp_cr(__fsub_rn(lt[e], mx));
+        __syncthreads();
+        if (lane == 0) {
+            float s = 0.0f;
+            for (int e = 0; e < E; e++) s = __fadd_rn(s, score[e]);
+            biased[0] = s;
+        }
+        __syncthreads();
+        const float s = biased[0];
+        __syncthreads();
+        for (int e = lane; e < E; e += 64) score[e] = __fdiv_rn(score[e], s);
+    } else {
+        for (int e = lane; e < E; e += 64) score[e] = __fdiv_rn(1.0f, __fadd_rn(1.0f, exp_cr(-lt[e])));
+    }
+    __syncthreads();
+    for (int e = lane; e < E; e += 64) biased[e] = __fadd_rn(score[e], bias ? bias[e] : 0.0f);
+    __syncthreads();
+    for (int j = 0; j < K; j++) {
+        float bv = -1e30f;
+        int be = 0x7fffffff;
+        for (int e = lane; e < E; e += 64) {
+            const float v = biased[e];
+            if (v > bv) { bv = v; be = e; }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(bv, o);
+            const int oe = __shfl_xor(be, o);
+            if (ov > bv || (ov == bv && oe < be)) { bv = ov; be = oe; }
+        }
+        if (be == 0x7fffffff) be = 0;     // nothing above -1e30: degenerate input
+        if (lane == 0) {
+            sel[j] = be;
+            wsel[j] = score[be];
+            biased[be] = -INFINITY;
+        }
+        __syncthreads();
+    }
+    if (lane == 0) {
+        if (renorm && K > 1) {
+            float s = 0.0f;
+            for (int j = 0; j < K; j++) s = __fadd_rn(s, wsel[j]);
+            const float d = __fadd_rn(s, 1e-20f);
+            for (int j = 0; j < K; j++) wsel[j] = __fdiv_rn(wsel[j], d);
+        }
+        for (int j = 0; j < K; j++) {
+            wsel[j] = __fmul_rn(wsel[j], routed_scale);
+            idx[(size_t)t * K + j] = sel[j];
+            w[(size_t)t * K + j] = wsel[j];
+        }
+    }
+    if (table) {
+        __syncthreads();
+        int miss = 0;
+        for (int j = lane; j < K; j += 64) {
+            const uint8_t *rec = table[sel[j]];
+            miss |= rec == nullptr;
+            for (int kind = 0; kind < 3; kind++) {
+                warp_job jb;
+                jb.rec = rec;
+                jb.kind = kind;
+                jb.n = 1;
+                for (int s = 0; s < WARP_TPJ; s++) { jb.xi[s] = 0; jb.yi[s] = 0; }
+                jb.xi[0] = kind == 2 ? j : 0;
+                jb.yi[0] = j;
+                jobs[kind * K + j] = jb;
+            }
+        }
+        miss = __any(miss);
+        if (lane == 0) {
+            for (int kind = 0; kind < 3; kind++) njobs[kind] = miss ? 0 : K;
+            if (miss) *missing = 1;
+        }
+    }
+}
+
+extern "C" int wk_route(const float *logits, const float *bias, int E, int K, int T, int act, int renorm,
+                        float routed_scale, int *idx, float *w, const uint8_t *const *table, warp_job *jobs,
+                        int *njobs, int *missing, void *stream) {
+    if (E <= 0 || K <= 0 || K > WARP_MAX_K || K > E || T <= 0 || E > 8192) return -1;
+    if (table && T != 1) return -1;
+    hipLaunchKernelGGL(k_route, dim3(T), dim3(64), (size_t)E * 2 * sizeof(float), (hipStream_t)stream, logits,
+                       bias, E, K, act, renorm, routed_scale, idx, w, table, jobs, njobs, missing);
+    CHECK_LAUNCH();
+    return 0;
+}
+
+// ---- the MFMA expert matvec --------------------------------------------------------------
+
+template <int FMT> struct FmtT;
+template <> struct FmtT<WARP_FMT_VQ3R> { static constexpr int S = 3, E = 256, SB = 3; };
+template <> struct FmtT<WARP_FMT_VQ2R> { static constexpr int S = 2, E = 256, SB = 2; };
+template <> struct FmtT<WARP_FMT_VQ12> { static constexpr int S = 2, E = 4096, SB = 3; };
+
+// Code word of 4 consecutive rows at one position, as loaded by a lane.
+template <int SB> struct Word;
+template <> struct Word<3> {
+    u3v w;
+    __device__ __forceinline__ void load(const uint8_t *p) {
+        const unsigned *q = (const unsigned *)p;
+        w = u3v{__builtin_nontemporal_load(q), __builtin_nontemporal_load(q + 1), __builtin_nontemporal_load(q + 2)};
+    }
+    // 24-bit slot of row t (0..3)
+    __device__ __forceinline__ unsigned slot(int t) const {
+        switch (t) {
+        case 0: return w.x & 0xFFFFFFu;
+        case 1: return __builtin_amdgcn_alignbit(w.y, w.x, 24) & 0xFFFFFFu;
+        case 2: return __builtin_amdgcn_alignbit(w.z, w.y, 16) & 0xFFFFFFu;
+        default: return w.z >> 8;
+        }
+    }
+};
+template <> struct Word<2> {
+    u2v w;
+    __device__ __forceinline__ void load(const uint8_t *p) {
+        const unsigned *q = (const unsigned *)p;
+        w = u2v{__builtin_nontemporal_load(q), __builtin_nontemporal_load(q + 1)};
+    }
+    __device__ __forceinline__ unsigned slot(int t) const {
+        switch (t) {
+        case 0: return w.x & 0xFFFFu;
+        case 1: return w.x >> 16;
+        case 2: return w.y & 0xFFFFu;
+        default: return w.y >> 16;
+        }
+    }
+};
+
+// Byte offset in LDS of the codebook vector for (stage, code of this slot).
+template <int FMT>
+__device__ __forceinline__ unsigned cb_off(unsigned slot, int s) {
+    if (FMT == WARP_FMT_VQ12) {
+        const unsigned c = s == 0 ? (slot & 0xFFFu) : (slot >> 12);
+        return ((unsigned)s * 4096u + c) * 16u;
+    }
+    const unsigned c = (slot >> (8 * s)) & 0xFFu;
+    return ((unsigned)s * 256u + c) * 16u;
+}
+
+struct VqArgs {
+    const warp_job *jobs;
+    const int *njobs;
+    int max_jobs;
+    int kind_lo;
+    const uint16_t *books;      // [3][S][E][8] fp16
+    const _Float16 *xs;         // [nx][nv][2][8]
+    const float *xscale;        // [nx]
+    float *y[3];                // per kind: [ny][M]
+    int M, N;
+};
+
+#define VQ_NW 16   // waves per block
+#define VQ_D 4     // code words in flight per wave
+
+// Block = 16 waves, grid.y = kind. A unit is (job, 64-row block); WPU waves
+// share one unit, each over a contiguous range of 4-position groups, and
+// their partial sums meet in LDS (fixed order, so results are deterministic).
+template <int FMT, int TPJ, int WPU>
+__global__ __launch_bounds__(1024) void k_vq_mfma(VqArgs a) {
+    typedef FmtT<FMT> F;
+    constexpr int UPW = VQ_NW / WPU;
+    extern __shared__ __attribute__((aligned(16))) unsigned char lds_vq[];
+    const int kind = a.kind_lo + blockIdx.y;
+    const int nj = a.njobs[kind];
+    const warp_job *jobs = a.jobs + (size_t)kind * a.max_jobs;
+    const int M = a.M, N = a.N, nv = N >> 3, npg = nv >> 2, nrb = (M + 63) >> 6;
+    const int units = nj * nrb;
+    if ((int)(blockIdx.x * UPW) >= units) return;   // uniform per block
+
+    // codebook of this kind -> LDS
+    {
+        const uint4 *src = (const uint4 *)(a.books + (size_t)kind * F::S * F::E * 8);
+        uint4 *dst = (uint4 *)lds_vq;
+        for (int i = threadIdx.x; i < F::S * F::E; i += blockDim.x) dst[i] = src[i];
+    }
+    float *red = (float *)(lds_vq + (size_t)F::S * F::E * 16);   // [VQ_NW][TPJ][64]
+    __syncthreads();
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, jc = lane & 15;
+    const int sub = wave / WPU, part = wave % WPU;
+    const int pg0 = part * npg / WPU, pg1 = (part + 1) * npg / WPU;
+    const int ts = jc >> 1, hl = jc & 1;
+    const uint32_t hdr_off = WARP_HDR_GATE_OFF + 4 * kind;
+
+    for (int ub = blockIdx.x * UPW; ub < units; ub += gridDim.x * UPW) {
+        const int u = ub + sub;
+        f4 acc[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+        if (u < units && pg0 < pg1) {
+            const warp_job &jb = jobs[u / nrb];
+            const int rb = u % nrb;
+            const uint8_t *rec = jb.rec;
+            const uint32_t moff = *(const uint32_t *)(rec + hdr_off);
+            const uint8_t *cp = rec + moff + ((size_t)rb * nv) * 64 * F::SB + (size_t)lane * 4 * F::SB;
+            const bool bvalid = ts < jb.n && ts < TPJ;
+            const _Float16 *xrow = a.xs + (size_t)(bvalid ? jb.xi[ts] : 0) * nv * 16 + hl * 8;
+            half8 b = {0, 0, 0, 0, 0, 0, 0, 0};
+            Word<F::SB> buf[VQ_D];
+#pragma unroll
+            for (int k = 0; k < VQ_D; k++)
+                if (pg0 + k < pg1) buf[k].load(cp + (size_t)(pg0 + k) * 256 * F::SB);
+            for (int pgb = pg0; pgb < pg1; pgb += VQ_D) {
+#pragma unroll
+                for (int k = 0; k < VQ_D; k++) {
+                    const int pg = pgb + k;
+                    if (pg < pg1) {
+                        const Word<F::SB> wd = buf[k];
+                        if (pg + VQ_D < pg1) buf[k].load(cp + (size_t)(pg + VQ_D) * 256 * F::SB);
+                        if (bvalid) b = *(const half8 *)(xrow + (size_t)(pg * 4 + g) * 16);
+#pragma unroll
+                        for (int t = 0; t < 4; t++) {
+                            const unsigned sl = wd.slot(t);
+#pragma unroll
+                            for (int s = 0; s < F::S; s++) {
+                                const half8 av = *(const half8 *)(lds_vq + cb_off<FMT>(sl, s));
+                                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b, acc[t], 0, 0, 0);
+                            }
+                        }
+                    }
+                }
+            }
+        }
+        // lane (g, jc) holds C[4g + r][jc] of tile t, i.e. block row 16g + 4r + t,
+        // token slot jc/2, half jc%2: fold the halves, park per-wave partials.
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float v = acc[t][r] + __shfl_xor(acc[t][r], 1);
+                if (hl == 0 && ts < TPJ) red[(wave * TPJ + ts) * 64 + 16 * g + 4 * r + t] = v;
+            }
+        __syncthreads();
+        for (int q = threadIdx.x; q < UPW * TPJ * 64; q += blockDim.x) {
+            const int s = q / (TPJ * 64), tsl = (q / 64) % TPJ, row = q % 64;
+            const int uu = ub + s;
+            if (uu >= units) continue;
+            const warp_job &jb = jobs[uu / nrb];
+            const int rg = (uu % nrb) * 64 + row;
+            if (tsl >= jb.n || rg >= M) continue;
+            float v = 0.0f;
+            for (int p = 0; p < WPU; p++) v += red[((s * WPU + p) * TPJ + tsl) * 64 + row];
+            const uint8_t *rec = jb.rec;
+            const uint16_t *sc = (const uint16_t *)(rec + *(const uint32_t *)(rec + WARP_HDR_CORR_OFF));
+            const int soff = kind == 0 ? 0 : kind == 1 ? M : 2 * N;
+            v = (v * a.xscale[jb.xi[tsl]]) * f16_keep(sc[soff + rg]);
+            a.y[kind][(size_t)jb.yi[tsl] * M + rg] = v;
+        }
+        __syncthreads();
+    }
+}
+
+template <int FMT, int TPJ, int WPU>
+static int launch_vq(const VqArgs &a, int nkinds, int max_units, void *stream) {
+    typedef FmtT<FMT> F;
+    constexpr int UPW = VQ_NW / WPU;
+    const size_t lds = (size_t)F::S * F::E * 16 + (size_t)VQ_NW * TPJ * 64 * 4;
+    if (lds > 163840) return -2;
+    static bool attr = false;
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute((const void *)k_vq_mfma<FMT, TPJ, WPU>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return -(int)e - 1000;
+        attr = true;
+    }
+    int grid = (max_units + UPW - 1) / UPW;
+    if (grid > 256) grid = 256;
+    if (grid < 1) grid = 1;
+    hipLaunchKernelGGL((k_vq_mfma<FMT, TPJ, WPU>), dim3(grid, nkinds), dim3(1024), lds, (hipStream_t)stream, a);
+    CHECK_LAUNCH();
+    return 0;
+}
+
+template <int FMT, int TPJ>
+static int launch_vq_w(const VqArgs &a, int nkinds, int max_units, int npg, void *stream) {
+    if (npg >= 128) return launch_vq<FMT, TPJ, 16>(a, nkinds, max_units, stream);
+    if (npg >= 32) return launch_vq<FMT, TPJ, 8>(a, nkinds, max_units, stream);
+    if (npg >= 16) return launch_vq<FMT, TPJ, 4>(a, nkinds, max_units, stream);
+    if (npg >= 4) return launch_vq<FMT, TPJ, 2>(a, nkinds, max_units, stream);
+    return launch_vq<FMT, TPJ, 1>(a, nkinds, max_units, stream);
+}
+
+template <int FMT>
+static int launch_vq_t(const VqArgs &a, int nkinds, int max_units, int npg, int tpj, void *stream) {
+    if (tpj == 1) return launch_vq_w<FMT, 1>(a, nkinds, max_units, npg, stream);
+    return launch_vq_w<FMT, WARP_TPJ>(a, nkinds, max_units, npg, stream);
+}
+
+extern "C" int wk_vq_matvec(int fmt, const warp_job *jobs, const int *njobs, int max_jobs, int kind_lo,
+                            int nkinds, const uint16_t *books, const uint16_t *xs, const float *xscale,
+                            float *const *y, int M, int N, int tokens_per_job, void *stream) {
+    if (M <= 0 || N <= 0 || (N % 32) || max_jobs <= 0 || kind_lo < 0 || nkinds < 1 || kind_lo + nkinds > 3)
+        return -1;
+    if (tokens_per_job != 1 && tokens_per_job != WARP_TPJ) return -1;
+    VqArgs a;
+    a.jobs = jobs;
+    a.njobs = njobs;
+    a.max_jobs = max_jobs;
+    a.kind_lo = kind_lo;
+    a.books = books;
+    a.xs = (const _Float16 *)xs;
+    a.xscale = xscale;
+    for (int k = 0; k < 3; k++) a.y[k] = y[k];
+    a.M = M;
+    a.N = N;
+    const int npg = N / 32, nrb = (M + 63) / 64, max_units = max_jobs * nrb;
+    switch (fmt) {
+    case WARP_FMT_VQ3R: return launch_vq_t<WARP_FMT_VQ3R>(a, nkinds, max_units, npg, tokens_per_job, stream);
+    case WARP_FMT_VQ2R: return launch_vq_t<WARP_FMT_VQ2R>(a, nkinds, max_units, npg, tokens_per_job, stream);
+    case WARP_FMT_VQ12: return launch_vq_t<WARP_FMT_VQ12>(a, nkinds, max_units, npg, tokens_per_job, stream);
+    }
+    return -1;
+}
+
+// ---- decoded weights ------------------------------------------------------------------
+
+template <int FMT>
+__device__ __forceinline__ unsigned code_at(const uint8_t *p, int s) {
+    if (FMT == WARP_FMT_VQ12) {
+        const unsigned w = (unsigned)p[0] | ((unsigned)p[1] << 8) | ((unsigned)p[2] << 16);
+        return s == 0 ? (w & 0xFFFu) : (w >> 12);
+    }
+    if (FMT == WARP_FMT_VQ4P) {
+        const unsigned b0 = p[0], b1 = p[1], b2 = p[2];
+        switch (s) {
+        case 0: return b0 & 0x3f;
+        case 1: return ((b0 >> 6) | (b1 << 2)) & 0x3f;
+        case 2: return ((b1 >> 4) | (b2 << 4)) & 0x3f;
+        default: return (b2 >> 2) & 0x3f;
+        }
+    }
+    return p[s];
+}
+
+template <int FMT, int S, int E, int SB>
+__global__ __launch_bounds__(256) void k_decode(const uint8_t *__restrict__ idx, const uint16_t *__restrict__ scale,
+                                                const uint16_t *__restrict__ books, int M, int N,
+                                                float *__restrict__ W) {
+    const int nv = N >> 3;
+    const long q = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= (long)M * nv) return;
+    const int r = (int)(q / nv), v = (int)(q % nv);
+    const uint8_t *p = idx + (((size_t)(r >> 6) * nv + v) * 64 + (r & 63)) * SB;
+    const float sr = f16_keep(scale[r]);
+    for (int d = 0; d < 8; d++) {
+        float t = f16_flushed(books[((size_t)0 * E + code_at<FMT>(p, 0)) * 8 + d]);
+        for (int s = 1; s < S; s++) t = __fadd_rn(t, f16_flushed(books[((size_t)s * E + code_at<FMT>(p, s)) * 8 + d]));
+        W[(size_t)r * N + 8 * v + d] = __fmul_rn(t, sr);
+    }
+}
+
+extern "C" int wk_decode_weights(int fmt, const uint8_t *idx, const uint16_t *scale, const uint16_t *books, int M,
+                                 int N, float *W, void *stream) {
+    if (M <= 0 || N <= 0 || (N & 7)) return -1;
+    const long n = (long)M * (N / 8);
+    const dim3 grid((unsigned)((n + 255) / 256)), blk(256);
+    hipStream_t s = (hipStream_t)stream;
+    switch (fmt) {
+    case WARP_FMT_VQ3R: hipLaunchKernelGGL((k_decode<WARP_FMT_VQ3R, 3, 256, 3>), grid, blk, 0, s, idx, scale, books, M, N, W); break;
+    case WARP_FMT_VQ2R: hipLaunchKernelGGL((k_decode<WARP_FMT_VQ2R, 2, 256, 2>), grid, blk, 0, s, idx, scale, books, M, N, W); break;
+    case WARP_FMT_VQ4P: hipLaunchKernelGGL((k_decode<WARP_FMT_VQ4P, 4, 64, 3>), grid, blk, 0, s, idx, scale, books, M, N, W); break;
+    case WARP_FMT_VQ12: hipLaunchKernelGGL((k_decode<WARP_FMT_VQ12, 2, 4096, 3>), grid, blk, 0, s, idx, scale, books, M, N, W); break;
+    default: return -1;
+    }
+    CHECK_LAUNCH();
+    return 0;
+}
+
+// ---- activation --------------------------------------------------------------------------
+
+__global__ __launch_bounds__(256) void k_act_split(const float *__restrict__ g, const float *__restrict__ u, int I,
+                                                   int situ, float beta, float lbeta, _Float16 *__restrict__ xs,
+                                                   float *__restrict__ xscale, float *__restrict__ h_out) {
+    const int p = blockIdx.x;
+    extern __shared__ float lds_h[];
+    const float *gp = g + (size_t)p * I, *up = u + (size_t)p * I;
+    float m = 0.0f;
+    for (int i = threadIdx.x; i < I; i += blockDim.x) {
+        const float h = act_pair(gp[i], up[i], situ, beta, lbeta);
+        lds_h[i] = h;
+        m = fmaxf(m, fabsf(h));
+    }
+    m = block_absmax(m);
+    const int k = split_exp(m);
+    _Float16 *o = xs + (size_t)p * I * 2;
+    for (int i = threadIdx.x; i < I; i += blockDim.x) {
+        const float h = lds_h[i];
+        split_store(h, k, &o[(i >> 3) * 16 + (i & 7)], &o[(i >> 3) * 16 + 8 + (i & 7)]);
+        if (h_out) h_out[(size_t)p * I + i] = h;
+    }
+    if (threadIdx.x == 0) xscale[p] = ldexpf(1.0f, -k);
+}
+
+extern "C" int wk_act_split(const float *g, const float *u, int P, int I, int act_situ, float beta, float lbeta,
+                            uint16_t *xs, float *xscale, float *h_out, void *stream) {
+    if (P <= 0 || I <= 0 || (I & 7) || I > 16384) return -1;
+    hipLaunchKernelGGL(k_act_split, dim3(P), dim3(256), (size_t)I * sizeof(float), (hipStream_t)stream, g, u, I,
+                       act_situ, beta, lbeta, (_Float16 *)xs, xscale, h_out);
+    CHECK_LAUNCH();
+    return 0;
+}
+
+__global__ __launch_bounds__(256) void k_act(const float *__restrict__ g, const float *__restrict__ u, long n,
+                                             int situ, float beta, float lbeta, float *__restrict__ h) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) h[i] = act_pair(g[i], u[i], situ, beta, lbeta);
+}
+
+extern "C" int wk_act(const float *g, const float *u, int P, int I, int act_situ, float beta, float lbeta, float *h,
+                      void *stream) {
+    if (P <= 0 || I <= 0) return -1;
+    const long n = (long)P * I;
+    hipLaunchKernelGGL(k_act, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, g, u, n, act_situ,
+                       beta, lbeta, h);
+    CHECK_LAUNCH();
+    return 0;
+}
+
+// ---- combine ---------------------------------------------------------------------------------
+
+__global__ __launch_bounds__(256) void k_combine(const float *__restrict__ y, const float *__restrict__ w, int K,
+                                                 int H, const float *__restrict__ add0,
+                                                 const float *__restrict__ add1, float *__restrict__ out) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= H) return;
+    float s = 0.0f;
+    for (int j = 0; j < K; j++) s = __fadd_rn(s, __fmul_rn(w[j], y[(size_t)j * H + i]));
+    if (add0) s = __fadd_rn(s, add0[i]);
+    if (add1) s = __fadd_rn(s, add1[i]);
+    out[i] = s;
+}
+
+extern "C" int wk_combine(const float *y, const float *w, int K, int H, const float *add0, const float *add1,
+                          float *out, void *stream) {
+    if (K <= 0 || H <= 0) return -1;
+    hipLaunchKernelGGL(k_combine, dim3((H + 255) / 256), dim3(256), 0, (hipStream_t)stream, y, w, K, H, add0, add1,
+                       out);
+    CHECK_LAUNCH();
+    return 0;
+}
+
+// ---- VQ4P: int8 LUT and its apply ------------------------------------------------------------
+
+// One block per (vector, 32-position block): the fp32 LUT entries with the
+// fused d-ascending chain of the reference's AVX-512 build
+// (src/simd_avx512.c:90-123), then max|.|, scale = max/127, ties-to-even
+// rounding and the +-127 clamp (src/model.c:2048-2109).
+__global__ __launch_bounds__(256) void k_lut_p6(const float *__restrict__ x, int N,
+                                                const uint16_t *__restrict__ books, int8_t *__restrict__ lut8,
+                                                float *__restrict__ lscale) {
+    __shared__ float lut[WARP_LUT_BLK * 256];
+    __shared__ float xsh[WARP_LUT_BLK * 8];
+    const int vec = blockIdx.y, blk = blockIdx.x, nv = N >> 3;
+    const int v0 = blk * WARP_LUT_BLK, v1 = min(v0 + WARP_LUT_BLK, nv), nvb = v1 - v0;
+    const float *xv = x + (size_t)vec * N;
+    for (int i = threadIdx.x; i < nvb * 8; i += blockDim.x) xsh[i] = xv[v0 * 8 + i];
+    __syncthreads();
+    float m = 0.0f;
+    for (int q = threadIdx.x; q < nvb * 256; q += blockDim.x) {
+        const int v = q >> 8, s = (q >> 6) & 3, c = q & 63;
+        float t = 0.0f;
+        for (int d = 0; d < 8; d++)
+            t = __builtin_fmaf(xsh[v * 8 + d], f16_flushed(books[((size_t)s * 64 + c) * 8 + d]), t);
+        lut[q] = t;
+        m = fmaxf(m, fabsf(t));
+    }
+    m = block_absmax(m);
+    const float inv = m > 0.0f ? __fdiv_rn(127.0f, m) : 0.0f;
+    int8_t *dst = lut8 + ((size_t)vec * nv + v0) * 256;
+    for (int q = threadIdx.x; q < nvb * 256; q += blockDim.x) {
+        int t = (int)rintf(__fmul_rn(lut[q], inv));
+        t = t > 127 ? 127 : (t < -127 ? -127 : t);
+        dst[q] = (int8_t)t;
+    }
+    if (threadIdx.x == 0) lscale[(size_t)vec * ((nv + WARP_LUT_BLK - 1) / WARP_LUT_BLK) + blk] = __fdiv_rn(m, 127.0f);
+}
+
+extern "C" int wk_lut_p6(const float *x, int V, int N, const uint16_t *books_kind, int8_t *lut8, float *lscale,
+                         void *stream) {
+    if (V <= 0 || N <= 0 || (N & 7)) return -1;
+    const int nv = N / 8, nblk = (nv + WARP_LUT_BLK - 1) / WARP_LUT_BLK;
+    hipLaunchKernelGGL(k_lut_p6, dim3(nblk, V), dim3(256), 0, (hipStream_t)stream, x, N, books_kind, lut8, lscale);
+    CHECK_LAUNCH();
+    return 0;
+}
+
+// One wave per (job, 64-row block), lane = row: integer block sums of the
+// four int8 lookups, folded into fp32 once per 32 positions in the
+// reference's order (src/model.c:2136-2229, portable branch).
+__global__ __launch_bounds__(256) void k_apply_p6(const warp_job *__restrict__ jobs, const int *__restrict__ njobs,
+                                                  int kind, const int8_t *__restrict__ lut8,
+                                                  const float *__restrict__ lscale, float *__restrict__ y, int M,
+                                                  int N) {
+    const int nv = N >> 3, nrb = (M + 63) >> 6, nblk = (nv + WARP_LUT_BLK - 1) / WARP_LUT_BLK;
+    const int unit = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (unit >= njobs[kind] * nrb) return;
+    const warp_job &jb = jobs[unit / nrb];
+    const int rb = unit % nrb, r = rb * 64 + lane;
+    const uint8_t *rec = jb.rec;
+    const uint8_t *idx = rec + *(const uint32_t *)(rec + WARP_HDR_GATE_OFF + 4 * kind);
+    for (int ts = 0; ts < jb.n; ts++) {
+    const int8_t *T0 = lut8 + (size_t)jb.xi[ts] * nv * 256;
+    const float *ls = lscale + (size_t)jb.xi[ts] * nblk;
+    float acc = 0.0f;
+    for (int b = 0; b < nblk; b++) {
+        const int v0 = b * WARP_LUT_BLK, v1 = min(v0 + WARP_LUT_BLK, nv);
+        int sum = 0;
+        for (int v = v0; v < v1; v++) {
+            const uint8_t *p = idx + (((size_t)rb * nv + v) * 64 + lane) * 3;
+            const int8_t *T = T0 + (size_t)v * 256;
+            sum += T[code_at<WARP_FMT_VQ4P>(p, 0)] + T[64 + code_at<WARP_FMT_VQ4P>(p, 1)] +
+                   T[128 + code_at<WARP_FMT_VQ4P>(p, 2)] + T[192 + code_at<WARP_FMT_VQ4P>(p, 3)];
+        }
+        acc = __fadd_rn(acc, __fmul_rn(ls[b], (float)sum));
+    }
+    if (r < M) {
+        const uint16_t *sc = (const uint16_t *)(rec + *(const uint32_t *)(rec + WARP_HDR_CORR_OFF));
+        const int soff = kind == 0 ? 0 : kind == 1 ? M : 2 * N;
+        y[(size_t)jb.yi[ts] * M + r] = __fmul_rn(acc, f16_keep(sc[soff + r]));
+    }
+    }
+}
+
+extern "C" int wk_apply_p6(const warp_job *jobs, const int *njobs, int max_jobs, int kind, const int8_t *lut8,
+                           const float *lscale, float *y, int M, int N, void *stream) {
+    if (M <= 0 || N <= 0 || (N & 7) || kind < 0 || kind > 2 || max_jobs <= 0) return -1;
+    const int nrb = (M + 63) / 64, units = max_jobs * nrb;
+    hipLaunchKernelGGL(k_apply_p6, dim3((units + 3) / 4), dim3(256), 0, (hipStream_t)stream,
+                       jobs + (size_t)kind * max_jobs, njobs, kind, lut8, lscale, y, M, N);
+    CHECK_LAUNCH();
+    return 0;
+}
+
+// ---- prefill grouping ----------------------------------------------------------------------------
+
+// One block. Counts per expert, exclusive scan, then one thread per expert
+// places its pairs in token order and cuts them into jobs of WARP_TPJ.
+__global__ __launch_bounds__(1024) void k_plan_chunk(const int *__restrict__ idx, const float *__restrict__ w, int T,
+                                                     int K, int E, const uint8_t *const *__restrict__ table,
+                                                     int *__restrict__ counts, int *__restrict__ offsets,
+                                                     int *__restrict__ pair_tok, int *__restrict__ pair_exp,
+                                                     float *__restrict__ pair_w, warp_job *__restrict__ jobs,
+                                                     int max_jobs, int *__restrict__ njobs, int *__restrict__ missing) {
+    __shared__ int s_tiles_total;
+    const int P = T * K;
+    for (int e = threadIdx.x; e < E; e += blockDim.x) counts[e] = 0;
+    __syncthreads();
+    for (int q = threadIdx.x; q < P; q += blockDim.x) atomicAdd(&counts[idx[q]], 1);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int run = 0, tiles = 0, miss = 0;
+        for (int e = 0; e < E; e++) {
+            offsets[e] = run;
+            run += counts[e];
+            tiles += (counts[e] + WARP_TPJ - 1) / WARP_TPJ;
+            if (counts[e] && !table[e]) miss = 1;
+        }
+        offsets[E] = run;
+        s_tiles_total = tiles;
+        if (miss) *missing = 1;
+        const int nj = (miss || tiles > max_jobs) ? 0 : tiles;
+        njobs[0] = njobs[1] = njobs[2] = nj;
+        if (tiles > max_jobs) *missing = 2;
+    }
+    __syncthreads();
+    if (njobs[0] == 0) return;
+    // job index of expert e's first tile = number of tiles of experts < e
+    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+        const int c = counts[e];
+        if (!c) continue;
+        int tile0 = 0;
+        for (int e2 = 0; e2 < e; e2++) tile0 += (counts[e2] + WARP_TPJ - 1) / WARP_TPJ;
+        int pos = offsets[e];
+        for (int t = 0; t < T; t++)
+            for (int k = 0; k < K; k++)
+                if (idx[t * K + k] == e) {
+                    pair_tok[pos] = t;
+                    pair_exp[pos] = e;
+                    pair_w[pos] = w[t * K + k];
+                    pos++;
+                }
+        const int ntile = (c + WARP_TPJ - 1) / WARP_TPJ;
+        for (int i = 0; i < ntile; i++) {
+            const int base = offsets[e] + i * WARP_TPJ, n = min(WARP_TPJ, c - i * WARP_TPJ);
+            for (int kind = 0; kind < 3; kind++) {
+                warp_job jb;
+                jb.rec = table[e];
+                jb.kind = kind;
+                jb.n = n;
+                for (int s = 0; s < WARP_TPJ; s++) {
+                    const int slot = base + (s < n ? s : 0);
+                    jb.xi[s] = kind == 2 ? slot : pair_tok[slot];
+                    jb.yi[s] = slot;
+                }
+                jobs[(size_t)kind * max_jobs + tile0 + i] = jb;
+            }
+        }
+    }
+}
+
+extern "C" int wk_plan_chunk(const int *idx, const float *w, int T, int K, int E, const uint8_t *const *table,
+                             int *counts, int *offsets, int *pair_tok, int *pair_exp, float *pair_w, warp_job *jobs,
+                             int max_jobs, int *njobs, int *missing, void *stream) {
+    if (T <= 0 || K <= 0 || E <= 0 || max_jobs <= 0) return -1;
+    hipLaunchKernelGGL(k_plan_chunk, dim3(1), dim3(1024), 0, (hipStream_t)stream, idx, w, T, K, E, table, counts,
+                       offsets, pair_tok, pair_exp, pair_w, jobs, max_jobs, njobs, missing);
+    CHECK_LAUNCH();
+    return 0;
+}
+
+// Per token: the pairs of that token in ascending expert id, each weighted
+// and added in that order (moe_chunk's loop order, src/model.c:3601-3656).
+__global__ __launch_bounds__(256) void k_combine_chunk(const float *__restrict__ y, const int *__restrict__ offsets,
+                                                       const int *__restrict__ pair_tok,
+                                                       const float *__restrict__ pair_w, int T, int K, int E, int H,
+                                                       const float *__restrict__ add0, float *__restrict__ out) {
+    __shared__ int slots[WARP_MAX_K];
+    __shared__ int nsl;
+    const int t = blockIdx.y;
+    if (threadIdx.x == 0) {
+        int n = 0;
+        for (int e = 0; e < E && n < K; e++)
+            for (int p = offsets[e]; p < offsets[e + 1]; p++)
+                if (pair_tok[p] == t) {
+                    slots[n++] = p;
+                    break;
+                }
+        nsl = n;
+    }
+    __syncthreads();
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= H) return;
+    float s = 0.0f;
+    for (int q = 0; q < nsl; q++) {
+        const int p = slots[q];
+        const float wj = pair_w[p];
+        if (wj == 0.0f) continue;
+        s = __fadd_rn(s, __fmul_rn(wj, y[(size_t)p * H + i]));
+    }
+    if (add0) s = __fadd_rn(s, add0[(size_t)t * H + i]);
+    out[(size_t)t * H + i] = s;
+}
+
+extern "C" int wk_combine_chunk(const float *y, const int *offsets, const int *pair_tok, const float *pair_w, int T,
+                                int K, int E, int H, const float *add0, float *out, void *stream) {
+    if (T <= 0 || K <= 0 || K > WARP_MAX_K || E <= 0 || H <= 0) return -1;
+    hipLaunchKernelGGL(k_combine_chunk, dim3((H + 255) / 256, T), dim3(256), 0, (hipStream_t)stream, y, offsets,
+                       pair_tok, pair_w, T, K, E, H, add0, out);
+    CHECK_LAUNCH();
+    return 0;
+}
+
+// ---- synthetic data ---------------------------------------------------------------------------
+
+__device__ __forceinline__ uint64_t splitmix(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__global__ __launch_bounds__(256) void k_fill(uint8_t *__restrict__ p, size_t n, uint64_t seed) {
+    const size_t nw = n / 8;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < nw; i += (size_t)gridDim.x * blockDim.x)
+        ((uint64_t *)p)[i] = splitmix(seed ^ (i * 0xD1B54A32D192ED03ull));
+    if (blockIdx.x == 0 && threadIdx.x < (n & 7)) p[nw * 8 + threadIdx.x] = (uint8_t)splitmix(seed + n + threadIdx.x);
+}
+
+extern "C" int wk_fill_random(uint8_t *p, size_t n, uint64_t seed, void *stream) {
+    if (!n) return 0;
+    if (((uintptr_t)p) & 7) return -1;
+    hipLaunchKernelGGL(k_fill, dim3(4096), dim3(256), 0, (hipStream_t)stream, p, n, seed);
+    CHECK_LAUNCH();
+    return 0;
+}
+
+__global__ void k_set_ptr(const uint8_t **dst, const uint8_t *val) { *dst = val; }
+
+extern "C" int wk_set_ptr(const uint8_t **dst, const uint8_t *val, void *stream) {
+    hipLaunchKernelGGL(k_set_ptr, dim3(1), dim3(1), 0, (hipStream_t)stream, dst, val);
+    CHECK_LAUNCH();
+    return 0;
+}
+
+extern "C" int wk_device_arch(int device, char *buf, int n) {
+    hipDeviceProp_t pr;
+    if (hipGetDeviceProperties(&pr, device) != hipSuccess) return -1;
+    int i = 0;
+    for (; i < n - 1 && pr.gcnArchName[i]; i++) buf[i] = pr.gcnArchName[i];
+    if (n > 0) buf[i] = 0;
+    return 0;
+}

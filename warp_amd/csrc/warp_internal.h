@@ -1,0 +1,154 @@
+/*
+ * warp_internal.h — the interface between the C host backend (backend.c)
+ * and the HIP kernels (kernels.hip). Not installed; include/warp_hip.h is
+ * the public ABI.
+ *
+ * Device data the kernels read:
+ *   - expert records, byte for byte as the container stores them: a 48-byte
+ *     header, then the gate, up and down index blocks in the blocked
+ *     [row_block=64][position][row_in_block][slot] layout, then one fp16 row
+ *     scale per output row of each matrix;
+ *   - per layer codebooks as fp16 [3 kinds][stages][entries][8], with fp16
+ *     subnormals already flushed to signed zero (the reference flushes them
+ *     when it loads codebooks.bin);
+ *   - activations split for the fp16 matrix cores: a vector x of width N is
+ *     stored as [N/8][2][8] fp16 (hi = fp16(x*2^k), lo = fp16(x*2^k - hi))
+ *     with one float 2^-k per vector, so that the products on the matrix
+ *     cores are exact and the sum keeps about 22 bits of x.
+ */
+#ifndef WARP_INTERNAL_H
+#define WARP_INTERNAL_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Formats (the reference's waste_fmt codes plus the 12-bit extension). */
+#define WARP_FMT_VQ3R 4
+#define WARP_FMT_VQ2R 5
+#define WARP_FMT_VQ4P 8
+#define WARP_FMT_VQ12 9
+
+#define WARP_TILE 64          /* index_block of the container format     */
+#define WARP_LUT_BLK 32       /* positions per int8 LUT scale (VQ4P)     */
+#define WARP_TPJ 8            /* token slots per matvec job              */
+#define WARP_MAX_K 64         /* top-k bound (the reference's cfg_sane)  */
+
+/* One matvec job: one matrix (kind) of one expert record against up to
+ * WARP_TPJ input vectors. xi[t] indexes the split inputs, yi[t] the output
+ * rows block ([y_index][M]). */
+typedef struct {
+    const uint8_t *rec;
+    int kind;                 /* 0 gate, 1 up, 2 down                    */
+    int n;                    /* token slots in use, 1..WARP_TPJ         */
+    int xi[WARP_TPJ];
+    int yi[WARP_TPJ];
+} warp_job;
+
+/* Byte offsets of the header fields the kernels read (waste_expert_hdr). */
+#define WARP_HDR_GATE_OFF 20
+#define WARP_HDR_UP_OFF 24
+#define WARP_HDR_DOWN_OFF 28
+#define WARP_HDR_CORR_OFF 32
+#define WARP_HDR_BYTES 48
+
+/* Every launcher returns 0 or a negative hipError_t-derived code, and
+ * launches on `stream` (a hipStream_t). */
+
+/* x [T][N] f32 -> xs [T][N/8][2][8] fp16, xscale [T]. */
+int wk_split(const float *x, int T, int N, uint16_t *xs, float *xscale, void *stream);
+
+/* Router logits [T][E] = W [E][H] . x [T][H]. strict = 1 reproduces the
+ * reference's sequential, unfused fp32 sum (dotf on x86); 0 is a parallel
+ * fixed-order tree. */
+int wk_router_logits(const float *W, const float *x, int E, int H, int T, int strict,
+                     float *logits, void *stream);
+
+/* Quantised router / dense trunk rows (Q8G, Q4G, Q3G with the reference's
+ * packing): y [T][M] = dequant(W) [M][N] . x [T][N]. */
+int wk_mvq(const int8_t *W, const uint16_t *ws, size_t rowbytes, int group, int bits,
+           const float *x, int M, int N, int T, float *y, void *stream);
+
+/* Routing for T tokens: scores, top-k by score + bias (strict >, lowest
+ * index wins), weights, renorm, scale. When `table` is not NULL (decode,
+ * T == 1) it also writes the decode job lists: jobs[0..K) gate, [K..2K) up,
+ * [2K..3K) down, and njobs[3] = {K, K, K}, or {0, 0, 0} plus *missing = 1
+ * when a selected expert has no resident record. */
+int wk_route(const float *logits, const float *bias, int E, int K, int T, int act,
+             int renorm, float routed_scale, int *idx, float *w,
+             const uint8_t *const *table, warp_job *jobs, int *njobs, int *missing,
+             void *stream);
+
+/* The MFMA decode-then-dot matvec over a job list, one launch per group of
+ * kinds: kind_lo..kind_lo+nkinds-1. jobs[k] / njobs[k] are the lists of
+ * kind kind_lo + k, at most max_jobs each. books: the layer's fp16 codebooks.
+ * y[k] gets the outputs of kind kind_lo + k: [y_index][M]. The output is
+ * the full matvec, scaled by the row scale and the input's xscale. */
+int wk_vq_matvec(int fmt, const warp_job *jobs, const int *njobs, int max_jobs,
+                 int kind_lo, int nkinds, const uint16_t *books, const uint16_t *xs,
+                 const float *xscale, float *const *y, int M, int N, int tokens_per_job,
+                 void *stream);
+
+/* Decoded weights of one matrix, bit for bit the reference's closed form
+ * (stage sum in fp32 from stage 0, then times the subnormal-keeping fp16
+ * row scale). books: fp16 [stages][entries][8] of this kind. W [M][N]. */
+int wk_decode_weights(int fmt, const uint8_t *idx, const uint16_t *scale,
+                      const uint16_t *books, int M, int N, float *W, void *stream);
+
+/* h = act(g, u) per pair, then split: g, u [P][I] -> xs [P][I/8][2][8],
+ * xscale [P]; h_out (may be NULL) gets h in f32. act_situ selects SiTU. */
+int wk_act_split(const float *g, const float *u, int P, int I, int act_situ,
+                 float beta, float lbeta, uint16_t *xs, float *xscale, float *h_out,
+                 void *stream);
+
+/* out [H] = sum_j w[j] * y[j][H] in j order (unfused, as the reference's
+ * combine), then + add0[H] and + add1[H] when given. */
+int wk_combine(const float *y, const float *w, int K, int H, const float *add0,
+               const float *add1, float *out, void *stream);
+
+/* VQ4P: int8 LUT of x for one kind (4 stages x 64 entries, one scale per 32
+ * positions), bit-identical to the reference's fused LUT build and
+ * quantisation. x [V][N] f32 -> lut8 [V][N/8][4][64], lscale [V][nblk]. */
+int wk_lut_p6(const float *x, int V, int N, const uint16_t *books_kind, int8_t *lut8,
+              float *lscale, void *stream);
+/* VQ4P apply over a job list of one kind: y[yi] = apply(rec kind, lut8[xi]). */
+int wk_apply_p6(const warp_job *jobs, const int *njobs, int max_jobs, int kind,
+                const int8_t *lut8, const float *lscale, float *y, int M, int N,
+                void *stream);
+/* silu/SiTU pairs for VQ4P: h [P][I] = act(g, u), exactly as the reference. */
+int wk_act(const float *g, const float *u, int P, int I, int act_situ, float beta,
+           float lbeta, float *h, void *stream);
+
+/* Prefill: token-to-expert grouping on the GPU. From route idx/w [T][K]:
+ * counts per expert, exclusive scan, pairs sorted by (expert, token) into
+ * pair_tok/pair_exp/pair_w [T*K]; gate/up jobs (tiles of WARP_TPJ tokens of
+ * one expert; xi = token, yi = pair slot) and down jobs (xi = yi = pair
+ * slot) written to jobs[kind*max_jobs ..], counts to njobs[3]. Pairs whose
+ * expert has no resident record set *missing. */
+int wk_plan_chunk(const int *idx, const float *w, int T, int K, int E,
+                  const uint8_t *const *table, int *counts, int *offsets,
+                  int *pair_tok, int *pair_exp, float *pair_w, warp_job *jobs,
+                  int max_jobs, int *njobs, int *missing, void *stream);
+/* out [T][H] = per token, sum over its pairs in ascending expert id of
+ * w * y[pair], then + add0 [T][H] when given. */
+int wk_combine_chunk(const float *y, const int *offsets, const int *pair_tok,
+                     const float *pair_w, int T, int K, int E, int H, const float *add0,
+                     float *out, void *stream);
+
+/* Synthetic device data for benchmarks: fill n bytes with a counter-based
+ * hash of (seed, offset). */
+int wk_fill_random(uint8_t *p, size_t n, uint64_t seed, void *stream);
+
+/* *dst = val, ordered on `stream` (device table updates). */
+int wk_set_ptr(const uint8_t **dst, const uint8_t *val, void *stream);
+
+/* Device properties the host needs: returns the gfx name into buf. */
+int wk_device_arch(int device, char *buf, int n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* WARP_INTERNAL_H */
