@@ -1,0 +1,232 @@
+#!/usr/bin/env python3
+"""bench.py — routed-expert MoE decode at K3 scale on one MI355X.
+
+Workload (one "step" = one decode token through the whole stack):
+  a 60-layer stack of MoE layers, hidden 7168, 384 experts of intermediate
+  2048, top-16 sigmoid routing from fp32 routers ~N(0, 0.02), experts in the
+  2-stage x 4096-entry residual VQ with 12-bit codes (3.00 bits per weight),
+  fp16 codebooks ~N(0, 0.02), fp16 row scales ~U(0.01, 0.05), uniformly
+  random codes. Each layer keeps 64 of its 384 expert records resident in
+  HBM (60 x 64 records, about 63.5 GB), and its e_score_correction_bias
+  lifts those 64 so that every selection hits the cache. The token's hidden
+  state enters layer L+1 as h + moe_L(h). Inputs live in HBM before timing.
+
+Reported:
+  value        MoE-layer tokens/s (tokens x layers / wall time of the
+               timed steps, HIP events on the compute stream)
+  roofline     the expert matvec kernel: algorithmic bytes (codes + row
+               scales of the 16 selected experts) / its launch time from HIP
+               events bracketing each launch, against 8 TB/s
+  cpu_baseline the reference's own CPU path (oracle/_ref, all host cores)
+               on the VQ3R twin of one K3 layer (3 x 256 entries, the same
+               3.00 bits per weight), 16 routed experts per token
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import tempfile
+import time
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, HERE)
+sys.path.insert(0, os.path.join(HERE, "tests", "golden"))
+
+METRIC = "MoE-layer tokens/s + achieved HBM GB/s (% of peak), K3-scale RVQ, 1 MI355X"
+HBM_PEAK_GBS = 8000.0
+H, I, E, K = 7168, 2048, 384, 16
+S, EN = 2, 4096
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def rec_layout():
+    gate = (I // 64) * (H // 8) * 64 * 3
+    down = (H // 64) * (I // 8) * 64 * 3
+    scales = 2 * (2 * I + H)
+    raw = 48 + 2 * gate + down + scales
+    return gate, down, scales, (raw + 4095) // 4096 * 4096
+
+
+def pair_bytes():
+    gate, down, scales, _ = rec_layout()
+    return 2 * gate + down + scales            # codes + row scales per (token, expert)
+
+
+def layer_bytes():
+    # codes+scales of K experts, the fp32 router, the layer's codebooks,
+    # the bias, x in and y out
+    return K * pair_bytes() + E * H * 4 + 3 * S * EN * 8 * 2 + E * 4 + 2 * H * 4
+
+
+def setup(layers, resident, seed=1234):
+    import warp_amd
+    gate, down, scales_b, rec_bytes = rec_layout()
+    ctx = warp_amd.Context(hidden=H, inter=I, n_experts=E, top_k=K, n_layers=layers, fmt="VQ12",
+                           renorm=True, routed_scale=1.0, max_tokens=1, rec_bytes=rec_bytes,
+                           cache_bytes=layers * resident * rec_bytes)
+    rng = np.random.Generator(np.random.PCG64(seed))
+    t0 = time.time()
+    for L in range(layers):
+        books = rng.normal(0.0, 0.02, size=(3 * S, EN, 8)).astype(np.float16).view(np.uint16)
+        ctx.set_codebooks(L, L * 3 * S, books)
+        router = rng.standard_normal((E, H), dtype=np.float32) * np.float32(0.02)
+        res_ids = rng.permutation(E)[:resident]
+        bias = np.zeros(E, np.float32)
+        bias[res_ids] = 1.0                         # resident experts always win
+        ctx.set_router(L, router, bias)
+        for e in res_ids:
+            sc = rng.uniform(0.01, 0.05, size=2 * I + H).astype(np.float16).view(np.uint16)
+            ctx.put_expert_synth(L, int(e), int(rng.integers(1 << 62)), sc)
+        if L % 10 == 9:
+            log(f"bench: {L + 1}/{layers} layers resident ({time.time() - t0:.1f}s)")
+    ctx.sync()
+    return ctx, rec_bytes
+
+
+def run_gpu(args):
+    from warp_amd.device import Buf, Event
+    ctx, rec_bytes = setup(args.layers, args.resident)
+    n_in = max(args.steps, args.warmup, 1)
+    X = Buf.of(np.random.default_rng(7).standard_normal((n_in, H), dtype=np.float32))
+    bufs = [Buf.empty(H), Buf.empty(H)]
+    stream = ctx.stream
+
+    def step(s):
+        # token s enters from its own staged input; h <- h + moe_L(h)
+        x = X.ptr + (s % n_in) * H * 4
+        for L in range(args.layers):
+            out = bufs[L & 1]
+            ctx.moe_decode(L, x, out, resid_dev=x)
+            x = out.ptr
+
+    log(f"bench: warmup {args.warmup} steps")
+    for s in range(args.warmup):
+        step(s)
+    ctx.sync()
+    ctx.set_timing(True)
+    e0, e1 = Event(), Event()
+    log(f"bench: timing {args.steps} steps of {args.layers} layers")
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for s in range(args.steps):
+        step(s)
+    e1.record(stream)
+    e1.synchronize()
+    ctx.sync()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_ms(e1)
+    kms, kn = ctx.get_timing()
+    ctx.set_timing(False)
+    out = bufs[(args.layers - 1) & 1].numpy()
+    assert np.isfinite(out).all(), "non-finite hidden state after the stack"
+    st = ctx.cache_stats()
+    ctx.close()
+    return ms, wall, kms, kn, st
+
+
+def cpu_baseline(seconds):
+    """The reference's CPU path on the VQ3R twin of one K3 layer."""
+    from oracle import pyoracle as po
+    import container as ct
+    if not os.path.exists(po.REF_LIB):
+        return None
+    spec = ct.Spec(hidden=H, inter=I, experts=K, top_k=K, layers=1, fmt="VQ3R", bias=False,
+                   renorm=True, routed_scale=1.0, shared_bits=4, shared_group=128, subnormals=False,
+                   keep_codes=False, seed=99)
+    log("bench: writing the VQ3R twin container for the CPU baseline")
+    model = ct.build(spec)
+    tmp = tempfile.mkdtemp(prefix="warp_k3_twin_")
+    ct.write(model, tmp)
+    del model
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+    ref = po.Ref(tmp, cache_bytes=2 * K * 17_000_000, n_threads=threads)
+    threads = ref.threads()
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal(H, dtype=np.float32)
+    ref.moe_layer(0, x, K, K, H)                   # first token fills the reference's cache
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        ref.moe_layer(0, rng.standard_normal(H, dtype=np.float32), K, K, H)
+        n += 1
+    dt = time.perf_counter() - t0
+    ref.close()
+    return {"value": n / dt, "unit": "MoE-layer tokens/s", "cores": threads, "kind": "reference",
+            "sample": f"{n} decode tokens through one K3-shape layer (H {H}, I {I}, top-16 of 16 "
+                      f"routed experts) in the reference's VQ3R format (3x256, 3.00 bits/weight, the "
+                      f"twin of the 2x4096 format it cannot load), its own LUT build + gather apply "
+                      f"over {threads} threads, {dt:.1f}s, records cache-resident; the reference loader "
+                      f"requires a shared expert, so each token also runs a Q4G shared expert (about 8% "
+                      f"of the bytes) that the GPU workload does not have"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--layers", type=int, default=60)
+    ap.add_argument("--resident", type=int, default=64, help="expert records per layer kept in HBM")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported by this build "
+              "(the path is single-GPU; multi-GPU sharding is described in DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    ms, wall, kms, kn, st = run_gpu(args)
+    steps, layers = args.steps, args.layers
+    layer_tokens = steps * layers
+    value = layer_tokens / (ms / 1e3)
+    # the expert matvec: class 0 gate+up launches, class 1 down launches
+    gate, down, scales_b, _ = rec_layout()
+    b0 = K * (2 * gate + 2 * 2 * I)               # codes + gate/up row scales per gate/up launch
+    b1 = K * (down + 2 * H)                       # codes + down row scales per down launch
+    kern_ms = kms[0] + kms[1]
+    kern_bytes = kn[0] * b0 + kn[1] * b1
+    achieved = kern_bytes / (kern_ms / 1e3) / 1e9
+    layer_gbs = layer_bytes() * layer_tokens / (ms / 1e3) / 1e9
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+    rec = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "MoE-layer tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms / steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32 accumulate (fp16 codebooks x hi/lo fp16 activations on MFMA)",
+        "data": "synthetic (random codes, codebooks, scales and routers of the K3 shapes)",
+        "config": {"workload": "K3-scale MoE decode layer, batch 1, 60-layer stack",
+                   "hidden": H, "inter": I, "experts": E, "top_k": K, "layers": layers,
+                   "format": "RVQ 2x4096 12-bit codes (3.00 b/w)", "resident_per_layer": args.resident,
+                   "parallelism": "single GPU"},
+        "layer_hbm_gbs": round(layer_gbs, 1),
+        "layer_hbm_frac": round(layer_gbs / HBM_PEAK_GBS, 4),
+        "layer_bytes": layer_bytes(),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_vq_mfma (expert matvec, gate/up and down launches)",
+                     "bytes_per_launch": {"gate_up": b0, "down": b1},
+                     "avg_launch_us": {"gate_up": round(kms[0] / max(kn[0], 1) * 1e3, 2),
+                                       "down": round(kms[1] / max(kn[1], 1) * 1e3, 2)},
+                     "router_avg_us": round(kms[2] / max(kn[2], 1) * 1e3, 2)},
+        "cache": {"hits": st["hits"], "misses": st["misses"], "resident": st["resident"]},
+        "wall_s": round(wall, 3),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec))
+
+
+if __name__ == "__main__":
+    main()

@@ -231,6 +231,18 @@ int warp_hip_fill_random(warp_hip_ctx *c, void *dev, size_t n, uint64_t seed);
  * resident; and making a slot resident from bytes already in device memory. */
 const uint8_t *warp_hip_resident(warp_hip_ctx *c, int layer, int expert);
 int warp_hip_put_expert_dev(warp_hip_ctx *c, int layer, int expert, const uint8_t *rec_dev);
+/* A resident record of synthetic content for benchmarks: a valid header for
+ * the context's shape, codes drawn on the device from `seed`, the given row
+ * scales ((2*inter + hidden) fp16, gate then up then down). */
+int warp_hip_put_expert_synth(warp_hip_ctx *c, int layer, int expert, uint64_t seed,
+                              const uint16_t *scales);
+/* Per-launch timing with HIP events on the compute stream: when on, every
+ * warp_hip_moe_decode brackets its launches of class 0 (gate/up expert
+ * matvec), 1 (down expert matvec) and 2 (router logits). get returns the
+ * summed milliseconds and launch counts per class since timing was turned
+ * on (waiting for the events). */
+int warp_hip_set_timing(warp_hip_ctx *c, int on);
+int warp_hip_get_timing(warp_hip_ctx *c, double ms[4], uint64_t launches[4]);
 /* Blocks until the context's streams are idle. */
 int warp_hip_sync(warp_hip_ctx *c);
 

@@ -198,14 +198,15 @@ def route(logits, bias, K, act=0, renorm=1, routed_scale=1.0):
 class Ref:
     """oracle/_ref/libwaste_ref.so over one container directory."""
 
-    def __init__(self, container_dir: str, cache_bytes: int = 0):
+    def __init__(self, container_dir: str, cache_bytes: int = 0, n_threads: int = 1):
         if not os.path.exists(REF_LIB):
             raise RuntimeError(f"{REF_LIB} is not built")
         self.L = C.CDLL(REF_LIB)
         L = self.L
         vp, i = C.c_void_p, C.c_int
         L.ref_open.restype = vp
-        L.ref_open.argtypes = [C.c_char_p, C.c_size_t]
+        L.ref_open.argtypes = [C.c_char_p, C.c_size_t, C.c_int]
+        L.ref_threads.restype = C.c_int
         L.ref_close.argtypes = [vp]
         L.ref_backend.restype = C.c_char_p
         L.ref_moe_layer.restype = i
@@ -217,7 +218,7 @@ class Ref:
         L.ref_vq_matvec.argtypes = [vp, i, i, i, vp, vp]
         L.ref_trunk_matvec.restype = i
         L.ref_trunk_matvec.argtypes = [vp, C.c_char_p, vp, vp, i, i]
-        self.m = L.ref_open(container_dir.encode(), cache_bytes)
+        self.m = L.ref_open(container_dir.encode(), cache_bytes, n_threads)
         if not self.m:
             raise RuntimeError(f"reference refused {container_dir}")
 
@@ -228,6 +229,9 @@ class Ref:
 
     def backend(self) -> str:
         return self.L.ref_backend().decode()
+
+    def threads(self) -> int:
+        return self.L.ref_threads()
 
     def moe_layer(self, L, x, E, K, H):
         x = np.ascontiguousarray(x, np.float32)

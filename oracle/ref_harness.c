@@ -9,7 +9,7 @@
  */
 #include "model.c"
 
-void *ref_open(const char *dir, size_t cache_bytes)
+void *ref_open(const char *dir, size_t cache_bytes, int n_threads)
 {
     waste_model *m = (waste_model *)calloc(1, sizeof *m);
     if (!m) return NULL;
@@ -17,7 +17,7 @@ void *ref_open(const char *dir, size_t cache_bytes)
     memset(&o, 0, sizeof o);
     o.cache_bytes = cache_bytes;
     o.direct_io = 0;
-    o.n_threads = 1;
+    o.n_threads = n_threads;   /* 0: the reference's default, one per CPU */
     if (waste_model_load(m, dir, 64, &o) != 0) { free(m); return NULL; }
     /* the router's scratch must still hold this layer's logits and scores
      * when moe_layer returns, so no lookahead into it; set after the load,
@@ -33,6 +33,8 @@ void ref_close(void *p)
 }
 
 const char *ref_backend(void) { return waste_backend_name(); }
+
+int ref_threads(void) { return waste_pool_threads(); }
 
 int ref_read_error(void *p) { return ((waste_model *)p)->read_error; }
 

@@ -65,6 +65,8 @@ class Spec:
     subnormals: bool = True      # plant fp16 subnormals in codebooks and scales
     vocab: int = 64
     seed: int = 0
+    keep_codes: bool = True      # keep the per-matrix code arrays (small shapes)
+    dup_rows: tuple = ()         # (a, b): router row b is a copy of row a (exact ties)
 
 
 def index_bytes(fmt: str, M: int, N: int) -> int:
@@ -75,7 +77,7 @@ def pack_indices(fmt: str, codes: np.ndarray, M: int, N: int) -> bytes:
     """codes: [S][M][nv] ints -> blocked index block."""
     S, nv = FMT_STAGES[fmt], N // 8
     nb = (M + TILE - 1) // TILE
-    full = np.zeros((S, nb * TILE, nv), dtype=np.uint32)
+    full = np.zeros((S, nb * TILE, nv), dtype=np.uint32 if fmt in ("VQ4P", "VQ12") else np.uint8)
     full[:, :M, :] = codes
     # [S][nb][64][nv] -> [nb][nv][64][S]
     c = full.reshape(S, nb, TILE, nv).transpose(1, 3, 2, 0)
@@ -87,7 +89,7 @@ def pack_indices(fmt: str, codes: np.ndarray, M: int, N: int) -> bytes:
         b1 = ((s1 >> 2) | (s2 << 4)) & 0xFF
         b2 = ((s2 >> 4) | (s3 << 2)) & 0xFF
     else:  # VQ12
-        w = (c[..., 0] & 0xFFF) | ((c[..., 1] & 0xFFF) << 12)
+        w = (c[..., 0].astype(np.uint32) & 0xFFF) | ((c[..., 1].astype(np.uint32) & 0xFFF) << 12)
         b0, b1, b2 = w & 0xFF, (w >> 8) & 0xFF, (w >> 16) & 0xFF
     return np.stack([b0, b1, b2], axis=-1).astype(np.uint8).tobytes()
 
@@ -157,6 +159,9 @@ def build(spec: Spec) -> Model:
         if spec.router != "f32":
             bits = 8 if spec.router == "q8" else 4
             router_q = quant_rows(rng, spec.experts, H, bits, 128) + (bits, 128)
+        if spec.dup_rows:
+            a, b = spec.dup_rows
+            router[b] = router[a]
         bias = rng.normal(0.0, 0.01, size=spec.experts).astype(np.float32) if spec.bias else None
         shared = []
         if spec.shared_bits:
@@ -169,8 +174,9 @@ def build(spec: Spec) -> Model:
             offs = []
             codes_e, scales_e = [], []
             for (M, N) in shapes:
-                c = rng.integers(0, E, size=(S, M, N // 8), dtype=np.int64)
-                codes_e.append(c)
+                c = rng.integers(0, E, size=(S, M, N // 8), dtype=np.uint16)
+                if spec.keep_codes:
+                    codes_e.append(c)
                 offs.append(HDR + len(body))
                 body += pack_indices(spec.fmt, c, M, N)
             corr = HDR + len(body)
@@ -216,6 +222,27 @@ class _Trunk:
         self.index.append({"name": name, "fmt": 2 if bits == 8 else 3, "off": off,
                            "shape": list(shape), "group": group, "scale_off": soff,
                            "bytes": len(self.buf) - off})
+
+
+def digest(model: Model) -> str:
+    """sha256 over every byte the model defines (codebooks, routers, biases,
+    shared experts, records), to catch a generator that drifted."""
+    import hashlib
+    h = hashlib.sha256()
+    h.update(model.books_raw.tobytes())
+    for lay in model.layers:
+        h.update(np.ascontiguousarray(lay.router).tobytes())
+        if lay.router_q is not None:
+            h.update(lay.router_q[0].tobytes())
+            h.update(lay.router_q[1].tobytes())
+        if lay.bias is not None:
+            h.update(lay.bias.tobytes())
+        for q in lay.shared:
+            h.update(q[0].tobytes())
+            h.update(q[1].tobytes())
+        for r in lay.records:
+            h.update(r)
+    return h.hexdigest()
 
 
 def write(model: Model, out: str) -> str:

@@ -1,0 +1,133 @@
+"""Pins for what the compiled reference cannot run or does not check: the
+2 x 4096 12-bit format, the fp16 conversions' edge cases, the encoder, the
+crc32 and the routing rules. Each check is an independent computation (a
+closed form, a library routine, brute force), not the oracle's own formula."""
+import zlib
+
+import numpy as np
+import pytest
+
+import container as ct
+from oracle import pyoracle as po
+
+
+def test_crc32_known_answer():
+    assert po.lib().or_crc32(b"123456789", 9) == 0xCBF43926
+    data = np.random.default_rng(0).integers(0, 256, 5000, dtype=np.uint8).tobytes()
+    assert po.lib().or_crc32(data, len(data)) == zlib.crc32(data)
+
+
+def test_f16_conversions():
+    L = po.lib()
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    f = h.view(np.float16).astype(np.float64)
+    keep = np.array([L.or_f16_keep(int(v)) for v in h[::7]])
+    flush = np.array([L.or_f16_flush(int(v)) for v in h[::7]])
+    ff = f[::7]
+    exp = (h[::7] >> 10) & 0x1F
+    normal = (exp > 0) & (exp < 31)
+    sub = exp == 0
+    # normal numbers are exact in both; subnormals kept exactly or flushed to 0
+    assert np.array_equal(keep[normal], ff[normal])
+    assert np.array_equal(flush[normal], ff[normal])
+    assert np.array_equal(keep[sub], ff[sub])
+    assert np.all(flush[sub] == 0.0)
+    # exponent 31 is rebiased as a normal number, not inf/nan (src/simd.h:64)
+    assert L.or_f16_keep(0x7C00) == 65536.0 and L.or_f16_flush(0x7C01) == 65536.0 * (1 + 2 ** -10)
+
+
+def _vq12_case(seed, M=64, N=128):
+    spec = ct.Spec(hidden=N, inter=M, experts=1, top_k=1, layers=1, fmt="VQ12", seed=seed,
+                   shared_bits=0, subnormals=True)
+    return spec, ct.build(spec)
+
+
+def test_vq12_matvec_against_float64_decode():
+    spec, model = _vq12_case(5)
+    books = po.books_flat(model.books_raw)                      # flushed, [book][entry][8]
+    rec = np.frombuffer(model.layers[0].records[0], np.uint8)
+    hdr = np.frombuffer(model.layers[0].records[0][:48], np.uint32)
+    codes = model.layers[0].codes[0]
+    for kind in range(3):
+        M, N = (spec.inter, spec.hidden) if kind < 2 else (spec.hidden, spec.inter)
+        soff = [0, spec.inter, 2 * spec.inter][kind]
+        scale = rec[int(hdr[8]) + 2 * soff:int(hdr[8]) + 2 * (soff + M)].view(np.uint16).copy()
+        c = codes[kind]                                          # [2][M][nv]
+        W = (books[kind * 2 + 0][c[0]].astype(np.float64) + books[kind * 2 + 1][c[1]]).reshape(M, N)
+        s = scale.view(np.float16).astype(np.float64)
+        x = np.random.default_rng(kind).normal(size=N).astype(np.float32)
+        ref = (W * s[:, None]) @ x.astype(np.float64)
+        y = po.vq_matvec("VQ12", rec[int(hdr[5 + kind]):].copy(), scale, x, po.books_T(model.books_raw),
+                         kind * 2, M, N)
+        assert np.max(np.abs(y - ref)) <= 1e-5 * np.max(np.abs(ref))
+        # the decoded weights are the closed form, bit for bit
+        Wd = po.decode_weights("VQ12", rec[int(hdr[5 + kind]):].copy(), scale, books, kind * 2, M, N)
+        W32 = (books[kind * 2 + 0][c[0]] + books[kind * 2 + 1][c[1]]).reshape(M, N).astype(np.float32)
+        Wexp = (W32 * s.astype(np.float32)[:, None]).astype(np.float32)
+        assert np.array_equal(Wd.view(np.uint32), Wexp.view(np.uint32))
+
+
+def test_vq12_reduces_to_vq2r_for_byte_codes():
+    """With every code < 256 and the first 256 entries of each 4096-entry book
+    equal to a VQ2R book, the 12-bit path must give VQ2R's result bit for bit
+    (VQ2R is a format the reference runs)."""
+    rng = np.random.default_rng(9)
+    M, N = 64, 128
+    nv = N // 8
+    b256 = rng.normal(0, 0.02, size=(2, 256, 8)).astype(np.float16).view(np.uint16)
+    b4096 = rng.normal(0, 0.02, size=(2, 4096, 8)).astype(np.float16).view(np.uint16)
+    b4096[:, :256] = b256
+    codes = rng.integers(0, 256, size=(2, M, nv))
+    idx2 = np.frombuffer(ct.pack_indices("VQ2R", codes, M, N), np.uint8).copy()
+    idx12 = np.frombuffer(ct.pack_indices("VQ12", codes, M, N), np.uint8).copy()
+    scale = rng.uniform(0.01, 0.05, M).astype(np.float16).view(np.uint16)
+    x = rng.normal(size=N).astype(np.float32)
+    y2 = po.vq_matvec("VQ2R", idx2, scale, x, po.books_T(b256), 0, M, N)
+    y12 = po.vq_matvec("VQ12", idx12, scale, x, po.books_T(b4096), 0, M, N)
+    assert np.array_equal(y2.view(np.uint32), y12.view(np.uint32))
+
+
+@pytest.mark.parametrize("fmt", ["VQ3R", "VQ2R", "VQ4P", "VQ12"])
+def test_code_packing_round_trip(fmt):
+    rng = np.random.default_rng(1)
+    M, N = 70, 64                                                 # a ragged row block
+    S, E = ct.FMT_STAGES[fmt], ct.FMT_ENTRIES[fmt]
+    codes = rng.integers(0, E, size=(S, M, N // 8))
+    idx = np.frombuffer(ct.pack_indices(fmt, codes, M, N), np.uint8).copy()
+    assert idx.nbytes == po.lib().or_index_bytes(po.FMT[fmt], M, N)
+    for r in (0, 63, 64, 69):
+        for v in (0, N // 8 - 1):
+            for s in range(S):
+                assert po.lib().or_code_at(po.FMT[fmt], idx.ctypes.data, N, r, v, s) == codes[s, r, v]
+
+
+def test_encoder_first_minimum_and_residual():
+    """waste_vq_encode semantics: per stage the nearest entry (strict <, so a
+    duplicate later entry never wins), then the residual feeds the next stage."""
+    rng = np.random.default_rng(4)
+    E, S = 64, 2
+    books = rng.normal(0, 1, size=(S, E, 8)).astype(np.float32)
+    books[0, 40] = books[0, 7]                                    # duplicate: 7 must win
+    a, b = 7, 19
+    X = (books[0, a] + books[1, b] * np.float32(1e-3))[None, :].astype(np.float32)
+    out = np.empty((1, S), np.uint16)
+    po.lib().or_vq_encode(X.ctypes.data, 1, books.ctypes.data, S, E, 8, out.ctypes.data)
+    assert out[0, 0] == a
+    # brute force over stage 1 on the exact residual
+    resid = X[0] - books[0, a]
+    d = ((resid[None, :] - books[1]) ** 2).sum(1)
+    assert out[0, 1] == int(np.argmin(d))
+
+
+def test_route_rules():
+    logits = np.array([0.5, 2.0, 2.0, -1.0, 2.0, 0.1], np.float32)
+    idx, w, sc = po.route(logits, None, 3, 0, 1, 1.0)
+    assert list(idx) == [1, 2, 4]                                 # equal scores: lowest id first
+    s = 1 / (1 + np.exp(-np.float64(2.0)))
+    assert np.allclose(w, [1 / 3] * 3, rtol=1e-6) and abs(sc[1] - s) < 1e-7
+    bias = np.array([3.0, 0, 0, 0, 0, 0], np.float32)             # bias selects, weight stays unbiased
+    idx, w, sc = po.route(logits, bias, 1, 0, 0, 2.0)
+    assert idx[0] == 0 and np.isclose(w[0], 2.0 * sc[0])
+    # softmax extension: same order for monotone scores, weights are probabilities
+    idx, w, sc = po.route(logits, None, 2, 1, 0, 1.0)
+    assert list(idx) == [1, 2] and abs(sc.sum() - 1.0) < 1e-6

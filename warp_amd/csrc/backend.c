@@ -223,6 +223,8 @@ typedef struct {
 } layer_t;
 
 #define N_STAGE 32
+#define WARP_TIMING_N 2048
+#define WARP_TIMING_CLS 4
 
 struct warp_hip_ctx {
     warp_hip_cfg cfg;
@@ -270,6 +272,14 @@ struct warp_hip_ctx {
     /* pinned host */
     int *h_idx, *h_la_idx, *h_missing;
     float *h_w;
+    /* optional per-launch timing of the expert matvecs (HIP events on the
+     * compute stream) */
+    int missing_pending;          /* a sticky device flag may be set        */
+    int timing;
+    hipEvent_t *tev;              /* [WARP_TIMING_N][2]                    */
+    int tev_cls[WARP_TIMING_N], tev_n;
+    double t_ms[WARP_TIMING_CLS];
+    uint64_t t_cnt[WARP_TIMING_CLS];
     char err[256];
     int err_layer, err_expert;
 };
@@ -490,6 +500,10 @@ void warp_hip_close(warp_hip_ctx *c)
     for (size_t i = 0; i < sizeof d / sizeof d[0]; i++) hfree(d[i]);
     hhfree(c->h_idx); hhfree(c->h_w); hhfree(c->h_la_idx); hhfree(c->h_missing); hhfree(c->staging);
     free(c->key_slot); free(c->slot_key); free(c->hits); free(c->last); free(c->pin);
+    if (c->tev) {
+        for (int i = 0; i < 2 * WARP_TIMING_N; i++) if (c->tev[i]) (void)hipEventDestroy(c->tev[i]);
+        free(c->tev);
+    }
     for (int i = 0; i < N_STAGE; i++) if (c->ev_stage[i]) (void)hipEventDestroy(c->ev_stage[i]);
     if (c->ev_copy) (void)hipEventDestroy(c->ev_copy);
     if (c->ev_before) (void)hipEventDestroy(c->ev_before);
@@ -502,12 +516,27 @@ void warp_hip_close(warp_hip_ctx *c)
     free(c);
 }
 
+/* Reads and clears the sticky missing-expert flag once the compute stream
+ * is idle. */
+static int take_missing(warp_hip_ctx *c)
+{
+    if (!c->missing_pending) return 0;
+    DEV(c, hipMemcpy(c->h_missing, c->missing, sizeof(int), hipMemcpyDeviceToHost));
+    c->missing_pending = 0;
+    if (*c->h_missing) {
+        DEV(c, hipMemset(c->missing, 0, sizeof(int)));
+        return set_err(c, WARP_HIP_E_MISSING, -1, -1,
+                       "a selected expert was not resident: the affected layers were not computed");
+    }
+    return 0;
+}
+
 int warp_hip_sync(warp_hip_ctx *c)
 {
     DEV(c, hipStreamSynchronize(c->la));
     DEV(c, hipStreamSynchronize(c->cp));
     DEV(c, hipStreamSynchronize(c->st));
-    return 0;
+    return take_missing(c);
 }
 
 /* ---- layer weights ------------------------------------------------------------------ */
@@ -764,6 +793,44 @@ int warp_hip_put_expert_dev(warp_hip_ctx *c, int layer, int expert, const uint8_
     return publish_slot(c, layer, expert, s);
 }
 
+int warp_hip_put_expert_synth(warp_hip_ctx *c, int layer, int expert, uint64_t seed, const uint16_t *scales)
+{
+    int rc = check_layer(c, layer);
+    if (rc) return rc;
+    const warp_hip_cfg *g = &c->cfg;
+    if (expert < 0 || expert >= g->n_experts || !scales) return set_err(c, WARP_HIP_E_ARG, layer, expert, "expert id");
+    /* header of waste_expert_hdr (src/waste_format.h:98-130) for this shape */
+    uint8_t hdr[WARP_HDR_BYTES];
+    memset(hdr, 0, sizeof hdr);
+    const uint32_t magic = 0x50584557u, blocks = (uint32_t)(g->rec_bytes / 4096u);
+    const uint16_t lay = (uint16_t)layer, eid = (uint16_t)expert, cb = (uint16_t)c->L[layer].cb_base;
+    const uint8_t fmt = (uint8_t)g->fmt;
+    uint32_t off[4];
+    off[0] = WARP_HDR_BYTES;
+    off[1] = off[0] + (uint32_t)c->gate_bytes;
+    off[2] = off[1] + (uint32_t)c->gate_bytes;
+    off[3] = off[2] + (uint32_t)c->down_bytes;
+    memcpy(hdr, &magic, 4);
+    memcpy(hdr + 4, &lay, 2);
+    memcpy(hdr + 6, &eid, 2);
+    memcpy(hdr + 8, &fmt, 1);
+    memcpy(hdr + 10, &cb, 2);
+    memcpy(hdr + 16, &blocks, 4);
+    memcpy(hdr + 20, off, 16);
+    if ((rc = check_record(c, hdr, layer, expert))) return rc;
+    const int key = layer * g->n_experts + expert;
+    int s = c->key_slot[key];
+    if (s < 0 && (s = claim_slot(c, layer, expert)) < 0) return s;
+    uint8_t *slot = c->pool + (size_t)s * g->rec_bytes;
+    DEV(c, hipEventRecord(c->ev_before, c->st));
+    DEV(c, hipStreamWaitEvent(c->cp, c->ev_before, 0));
+    KRN(c, wk_fill_random(slot, g->rec_bytes, seed, c->cp));
+    DEV(c, hipMemcpyAsync(slot, hdr, sizeof hdr, hipMemcpyHostToDevice, c->cp));
+    DEV(c, hipMemcpyAsync(slot + off[3], scales, 2 * (2 * (size_t)g->inter + g->hidden), hipMemcpyHostToDevice, c->cp));
+    DEV(c, hipStreamSynchronize(c->cp));
+    return publish_slot(c, layer, expert, s);
+}
+
 const uint8_t *warp_hip_resident(warp_hip_ctx *c, int layer, int expert)
 {
     if (!c || layer < 0 || layer >= c->cfg.n_layers || expert < 0 || expert >= c->cfg.n_experts) return NULL;
@@ -877,6 +944,69 @@ static int wait_copies(warp_hip_ctx *c)
     return 0;
 }
 
+/* ---- launch timing ---------------------------------------------------------------------------- */
+
+static int timing_fold(warp_hip_ctx *c)
+{
+    for (int i = 0; i < c->tev_n; i++) {
+        float ms = 0.0f;
+        DEV(c, hipEventSynchronize(c->tev[2 * i + 1]));
+        DEV(c, hipEventElapsedTime(&ms, c->tev[2 * i], c->tev[2 * i + 1]));
+        c->t_ms[c->tev_cls[i]] += ms;
+        c->t_cnt[c->tev_cls[i]]++;
+    }
+    c->tev_n = 0;
+    return 0;
+}
+
+/* Bracket one launch of class `cls` with events on the compute stream. */
+static int timing_begin(warp_hip_ctx *c, int cls)
+{
+    if (!c->timing) return 0;
+    if (c->tev_n == WARP_TIMING_N) {
+        int rc = timing_fold(c);
+        if (rc) return rc;
+    }
+    c->tev_cls[c->tev_n] = cls;
+    DEV(c, hipEventRecord(c->tev[2 * c->tev_n], c->st));
+    return 0;
+}
+
+static int timing_end(warp_hip_ctx *c)
+{
+    if (!c->timing) return 0;
+    DEV(c, hipEventRecord(c->tev[2 * c->tev_n + 1], c->st));
+    c->tev_n++;
+    return 0;
+}
+
+int warp_hip_set_timing(warp_hip_ctx *c, int on)
+{
+    if (!c) return WARP_HIP_E_ARG;
+    if (on && !c->tev) {
+        c->tev = (hipEvent_t *)calloc(2 * WARP_TIMING_N, sizeof(hipEvent_t));
+        if (!c->tev) return set_err(c, WARP_HIP_E_NOMEM, -1, -1, "host allocation failed");
+        for (int i = 0; i < 2 * WARP_TIMING_N; i++) DEV(c, hipEventCreate(&c->tev[i]));
+    }
+    c->timing = on;
+    c->tev_n = 0;
+    memset(c->t_ms, 0, sizeof c->t_ms);
+    memset(c->t_cnt, 0, sizeof c->t_cnt);
+    return 0;
+}
+
+int warp_hip_get_timing(warp_hip_ctx *c, double ms[4], uint64_t launches[4])
+{
+    if (!c) return WARP_HIP_E_ARG;
+    int rc = timing_fold(c);
+    if (rc) return rc;
+    for (int k = 0; k < WARP_TIMING_CLS; k++) {
+        if (ms) ms[k] = c->t_ms[k];
+        if (launches) launches[k] = c->t_cnt[k];
+    }
+    return 0;
+}
+
 /* ---- the layer ------------------------------------------------------------------------------ */
 
 static const uint16_t *books_kind(const warp_hip_ctx *c, const layer_t *L, int kind)
@@ -958,7 +1088,9 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
     } else {
         KRN(c, wk_split(x_dev, 1, H, c->xs, c->xscale, c->st));
     }
+    if ((rc = timing_begin(c, 2))) return rc;
     KRN(c, logits_of(c, L, x_dev, 1, c->logits, c->st));
+    if ((rc = timing_end(c))) return rc;
     const int n_la = lookahead_launch(c, layer, x_dev);
     if (n_la < 0) return n_la;
 
@@ -971,15 +1103,13 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
         c->stats.hits += (uint64_t)K;
         if (c->pin_layer == layer) c->pin_layer = -1;
     } else if (!c->fetch) {
-        /* nothing to fetch with: the device reports a selected expert that is
-         * not resident, and the layer is refused rather than summed short */
+        /* nothing to fetch with: the device flags a selected expert that is
+         * not resident (sticky), the combine poisons this layer's output with
+         * NaN, and the next synchronising call reports E_MISSING */
         KRN(c, wait_copies(c));
-        DEV(c, hipMemsetAsync(c->missing, 0, sizeof(int), c->st));
         KRN(c, wk_route(c->logits, L->bias, E, K, 1, g->router_act, g->renorm, g->routed_scale, c->idx, c->w, table,
                         c->jobs, c->njobs, c->missing, c->st));
-        DEV(c, hipMemcpyAsync(c->h_missing, c->missing, sizeof(int), hipMemcpyDeviceToHost, c->st));
-        DEV(c, hipStreamSynchronize(c->st));
-        if (*c->h_missing) return set_err(c, WARP_HIP_E_MISSING, layer, -1, "a selected expert is not resident");
+        c->missing_pending = 1;
         if (c->pin_layer == layer) c->pin_layer = -1;
     } else {
         KRN(c, wk_route(c->logits, L->bias, E, K, 1, g->router_act, g->renorm, g->routed_scale, c->idx, c->w, NULL,
@@ -1003,13 +1133,17 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
         KRN(c, wk_lut_p6(c->hbuf, K, I, books_kind(c, L, 2), c->lut8d, c->lscaled, c->st));
         KRN(c, wk_apply_p6(c->jobs, c->njobs, K, 2, c->lut8d, c->lscaled, c->yd, H, I, c->st));
     } else {
+        if ((rc = timing_begin(c, 0))) return rc;
         KRN(c, wk_vq_matvec(g->fmt, c->jobs, c->njobs, K, 0, 2, L->books, c->xs, c->xscale, yk, I, H, 1, c->st));
+        if ((rc = timing_end(c))) return rc;
         KRN(c, wk_act_split(c->yg, c->yu, K, I, g->act_situ, g->situ_beta, g->situ_linear_beta, c->xsh, c->xscaleh,
                             NULL, c->st));
+        if ((rc = timing_begin(c, 1))) return rc;
         KRN(c, wk_vq_matvec(g->fmt, c->jobs, c->njobs, K, 2, 1, L->books, c->xsh, c->xscaleh, yk, H, I, 1, c->st));
+        if ((rc = timing_end(c))) return rc;
     }
     if (L->sq[0] && (rc = shared_ffn(c, L, x_dev, 1))) return rc;
-    KRN(c, wk_combine(c->yd, c->w, K, H, L->sq[0] ? c->sho : NULL, resid_dev, out_dev, c->st));
+    KRN(c, wk_combine(c->yd, c->w, K, H, L->sq[0] ? c->sho : NULL, resid_dev, c->missing, out_dev, c->st));
     DEV(c, hipEventRecord(c->ev_after, c->st));
 
     if ((rc = lookahead_issue(c, layer, n_la))) return rc;
@@ -1017,6 +1151,7 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
         if (idx) DEV(c, hipMemcpyAsync(c->h_idx, c->idx, (size_t)K * sizeof(int), hipMemcpyDeviceToHost, c->st));
         if (w) DEV(c, hipMemcpyAsync(c->h_w, c->w, (size_t)K * sizeof(float), hipMemcpyDeviceToHost, c->st));
         DEV(c, hipStreamSynchronize(c->st));
+        if ((rc = take_missing(c))) return rc;
         if (idx) memcpy(idx, c->h_idx, (size_t)K * sizeof(int));
         if (w) memcpy(w, c->h_w, (size_t)K * sizeof(float));
     }
@@ -1032,7 +1167,7 @@ int warp_hip_moe_decode_host(warp_hip_ctx *c, int layer, const float *x, float *
     if (rc) return rc;
     DEV(c, hipMemcpyAsync(out, c->xout, (size_t)H * 4, hipMemcpyDeviceToHost, c->st));
     DEV(c, hipStreamSynchronize(c->st));
-    return 0;
+    return take_missing(c);
 }
 
 int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *out_dev, int T, int *route, float *rw)

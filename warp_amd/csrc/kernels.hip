@@ -678,9 +678,14 @@ extern "C" int wk_act(const float *g, const float *u, int P, int I, int act_situ
 
 __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ y, const float *__restrict__ w, int K,
                                                  int H, const float *__restrict__ add0,
-                                                 const float *__restrict__ add1, float *__restrict__ out) {
+                                                 const float *__restrict__ add1, const int *__restrict__ missing,
+                                                 float *__restrict__ out) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= H) return;
+    if (missing && *missing) {          // a selected expert was not computed
+        out[i] = __builtin_nanf("");
+        return;
+    }
     float s = 0.0f;
     for (int j = 0; j < K; j++) s = __fadd_rn(s, __fmul_rn(w[j], y[(size_t)j * H + i]));
     if (add0) s = __fadd_rn(s, add0[i]);
@@ -689,10 +694,10 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ y, co
 }
 
 extern "C" int wk_combine(const float *y, const float *w, int K, int H, const float *add0, const float *add1,
-                          float *out, void *stream) {
+                          const int *missing, float *out, void *stream) {
     if (K <= 0 || H <= 0) return -1;
     hipLaunchKernelGGL(k_combine, dim3((H + 255) / 256), dim3(256), 0, (hipStream_t)stream, y, w, K, H, add0, add1,
-                       out);
+                       missing, out);
     CHECK_LAUNCH();
     return 0;
 }

@@ -105,9 +105,10 @@ int wk_act_split(const float *g, const float *u, int P, int I, int act_situ,
                  void *stream);
 
 /* out [H] = sum_j w[j] * y[j][H] in j order (unfused, as the reference's
- * combine), then + add0[H] and + add1[H] when given. */
+ * combine), then + add0[H] and + add1[H] when given; NaN everywhere when
+ * *missing is set (a selected expert was not computed). */
 int wk_combine(const float *y, const float *w, int K, int H, const float *add0,
-               const float *add1, float *out, void *stream);
+               const float *add1, const int *missing, float *out, void *stream);
 
 /* VQ4P: int8 LUT of x for one kind (4 stages x 64 entries, one scale per 32
  * positions), bit-identical to the reference's fused LUT build and

@@ -84,6 +84,9 @@ SIGNATURES = {
     "warp_hip_fill_random": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_uint64]),
     "warp_hip_resident": (C.c_void_p, [C.c_void_p, C.c_int, C.c_int]),
     "warp_hip_put_expert_dev": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p]),
+    "warp_hip_put_expert_synth": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_uint64, C.c_void_p]),
+    "warp_hip_set_timing": (C.c_int, [C.c_void_p, C.c_int]),
+    "warp_hip_get_timing": (C.c_int, [C.c_void_p, C.POINTER(C.c_double), C.POINTER(C.c_uint64)]),
     "warp_hip_sync": (C.c_int, [C.c_void_p]),
 }
 
@@ -262,6 +265,18 @@ class Context:
     def mvq(self, bits, group, q_dev, s_dev, rowbytes, x_dev, M, N, T, y_dev):
         self._check(lib().warp_hip_mvq(self.h, bits, group, _addr(q_dev), _addr(s_dev), rowbytes, _addr(x_dev),
                                        M, N, T, _addr(y_dev)))
+
+    def put_expert_synth(self, layer, expert, seed, scales_u16):
+        self._check(lib().warp_hip_put_expert_synth(self.h, layer, expert, seed, _addr(scales_u16)))
+
+    def set_timing(self, on):
+        self._check(lib().warp_hip_set_timing(self.h, int(on)))
+
+    def get_timing(self):
+        ms = (C.c_double * 4)()
+        n = (C.c_uint64 * 4)()
+        self._check(lib().warp_hip_get_timing(self.h, ms, n))
+        return list(ms), list(n)
 
     def fill_random(self, dev, nbytes, seed):
         self._check(lib().warp_hip_fill_random(self.h, _addr(dev), nbytes, seed))
