@@ -106,6 +106,13 @@ def run_gpu(args):
             ctx.moe_decode(L, x, out, resid_dev=x)
             x = out.ptr
 
+    if args.calibrate_copy_mib:
+        from warp_amd.device import D2D, check, rt
+        n = args.calibrate_copy_mib << 20
+        src, dst = Buf(n), Buf(n)
+        check(rt().hipMemcpy(dst.ptr, src.ptr, n, D2D), "calibration copy")
+        src.free()
+        dst.free()
     log(f"bench: warmup {args.warmup} steps")
     for s in range(args.warmup):
         step(s)
@@ -175,6 +182,9 @@ def main():
     ap.add_argument("--resident", type=int, default=64, help="expert records per layer kept in HBM")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="before timing, one device-to-device copy of this many MiB (a known-size "
+                         "kernel for scaling the profiler's traffic counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported by this build "

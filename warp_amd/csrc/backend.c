@@ -1052,7 +1052,7 @@ static int lookahead_launch(warp_hip_ctx *c, int layer, const float *x_dev)
     DEV(c, hipStreamWaitEvent(c->la, c->ev_x, 0));
     KRN(c, logits_of(c, N, x_dev, 1, c->la_logits, c->la));
     KRN(c, wk_route(c->la_logits, N->bias, g->n_experts, n, 1, WARP_HIP_ROUTE_SIGMOID, 0, 1.0f, c->la_idx, c->la_w,
-                    NULL, NULL, NULL, NULL, c->la));
+                    NULL, NULL, NULL, NULL, 0, c->la));
     DEV(c, hipMemcpyAsync(c->h_la_idx, c->la_idx, (size_t)n * sizeof(int), hipMemcpyDeviceToHost, c->la));
     DEV(c, hipEventRecord(c->ev_la, c->la));
     return n;
@@ -1099,7 +1099,7 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
          * host round trip */
         KRN(c, wait_copies(c));
         KRN(c, wk_route(c->logits, L->bias, E, K, 1, g->router_act, g->renorm, g->routed_scale, c->idx, c->w, table,
-                        c->jobs, c->njobs, c->missing, c->st));
+                        c->jobs, c->njobs, c->missing, I, c->st));
         c->stats.hits += (uint64_t)K;
         if (c->pin_layer == layer) c->pin_layer = -1;
     } else if (!c->fetch) {
@@ -1108,18 +1108,18 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
          * NaN, and the next synchronising call reports E_MISSING */
         KRN(c, wait_copies(c));
         KRN(c, wk_route(c->logits, L->bias, E, K, 1, g->router_act, g->renorm, g->routed_scale, c->idx, c->w, table,
-                        c->jobs, c->njobs, c->missing, c->st));
+                        c->jobs, c->njobs, c->missing, I, c->st));
         c->missing_pending = 1;
         if (c->pin_layer == layer) c->pin_layer = -1;
     } else {
         KRN(c, wk_route(c->logits, L->bias, E, K, 1, g->router_act, g->renorm, g->routed_scale, c->idx, c->w, NULL,
-                        NULL, NULL, NULL, c->st));
+                        NULL, NULL, NULL, 0, c->st));
         DEV(c, hipMemcpyAsync(c->h_idx, c->idx, (size_t)K * sizeof(int), hipMemcpyDeviceToHost, c->st));
         DEV(c, hipStreamSynchronize(c->st));
         if ((rc = ensure_selected(c, layer, c->h_idx, K))) return rc;
         KRN(c, wait_copies(c));
         KRN(c, wk_route(c->logits, L->bias, E, K, 1, g->router_act, g->renorm, g->routed_scale, c->idx, c->w, table,
-                        c->jobs, c->njobs, c->missing, c->st));
+                        c->jobs, c->njobs, c->missing, I, c->st));
     }
     DEV(c, hipEventRecord(c->ev_before, c->st));
 
@@ -1185,7 +1185,7 @@ int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *ou
 
     KRN(c, logits_of(c, L, X_dev, T, c->logits, c->st));
     KRN(c, wk_route(c->logits, L->bias, E, K, T, g->router_act, g->renorm, g->routed_scale, c->idx, c->w, NULL, NULL,
-                    NULL, NULL, c->st));
+                    NULL, NULL, 0, c->st));
     if (L->resident != E && c->fetch) {
         DEV(c, hipMemcpyAsync(c->h_idx, c->idx, (size_t)P * sizeof(int), hipMemcpyDeviceToHost, c->st));
         DEV(c, hipStreamSynchronize(c->st));
@@ -1206,7 +1206,7 @@ int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *ou
     KRN(c, wait_copies(c));
     DEV(c, hipMemsetAsync(c->missing, 0, sizeof(int), c->st));
     KRN(c, wk_plan_chunk(c->idx, c->w, T, K, E, table, c->counts, c->offsets, c->pair_tok, c->pair_exp, c->pair_w,
-                         c->jobs, c->max_jobs, c->njobs, c->missing, c->st));
+                         c->jobs, c->max_jobs, c->njobs, c->missing, I, c->st));
     DEV(c, hipEventRecord(c->ev_before, c->st));
     float *yk[3] = { c->yg, c->yu, c->yd };
     if (c->P6) {
@@ -1276,10 +1276,16 @@ int warp_hip_vq_matvec(warp_hip_ctx *c, int layer, int kind, const uint8_t *rec_
     int M, N;
     if (matrix_shape(c, kind, &M, &N) || !rec_dev || !L->has_books)
         return set_err(c, WARP_HIP_E_ARG, layer, -1, "vq_matvec arguments");
+    uint8_t hdr[WARP_HDR_BYTES];
+    DEV(c, hipMemcpy(hdr, rec_dev, sizeof hdr, hipMemcpyDeviceToHost));
+    uint32_t off[4];
+    memcpy(off, hdr + 20, 16);
+    if (off[3] + 2 * (2 * (size_t)c->cfg.inter + c->cfg.hidden) > c->cfg.rec_bytes || off[kind] >= off[3])
+        return set_err(c, WARP_HIP_E_HEADER, layer, -1, "record offsets");
     warp_job jb;
     memset(&jb, 0, sizeof jb);
-    jb.rec = rec_dev;
-    jb.kind = kind;
+    jb.idx = rec_dev + off[kind];
+    jb.scale = (const uint16_t *)(rec_dev + off[3]) + (kind == 0 ? 0 : kind == 1 ? c->cfg.inter : 2 * c->cfg.inter);
     jb.n = 1;
     int nj[3] = { 0, 0, 0 };
     nj[kind] = 1;
@@ -1342,7 +1348,7 @@ int warp_hip_route(warp_hip_ctx *c, int layer, const float *logits_dev, int T, i
     if (rc) return rc;
     const warp_hip_cfg *g = &c->cfg;
     KRN(c, wk_route(logits_dev, c->L[layer].bias, g->n_experts, g->top_k, T, g->router_act, g->renorm, g->routed_scale,
-                    idx_dev, w_dev, NULL, NULL, NULL, NULL, c->st));
+                    idx_dev, w_dev, NULL, NULL, NULL, NULL, 0, c->st));
     DEV(c, hipStreamSynchronize(c->st));
     return 0;
 }

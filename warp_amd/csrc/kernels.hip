@@ -17,6 +17,7 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 #include "warp_internal.h"
 
@@ -110,43 +111,69 @@ __device__ __forceinline__ void split_store(float x, int k, _Float16 *hi, _Float
 
 // ---- split -------------------------------------------------------------------
 
-__global__ __launch_bounds__(256) void k_split(const float *__restrict__ x, int N,
-                                               _Float16 *__restrict__ xs, float *__restrict__ xscale) {
+// One block per vector. Up to 8 values per thread stay in registers between
+// the max pass and the store pass (N <= 8192 at 1024 threads).
+__global__ __launch_bounds__(1024) void k_split(const float *__restrict__ x, int N,
+                                                _Float16 *__restrict__ xs, float *__restrict__ xscale) {
     const int t = blockIdx.x;
     const float *xt = x + (size_t)t * N;
-    float m = 0.0f;
-    for (int i = threadIdx.x; i < N; i += blockDim.x) m = fmaxf(m, fabsf(xt[i]));
-    m = block_absmax(m);
-    const int k = split_exp(m);
     _Float16 *o = xs + (size_t)t * N * 2;
-    for (int i = threadIdx.x; i < N; i += blockDim.x) {
-        const int v = i >> 3, d = i & 7;
-        split_store(xt[i], k, &o[v * 16 + d], &o[v * 16 + 8 + d]);
+    float v[8];
+    float m = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const int i = threadIdx.x + k * 1024;
+        v[k] = i < N ? xt[i] : 0.0f;
+        m = fmaxf(m, fabsf(v[k]));
     }
-    if (threadIdx.x == 0) xscale[t] = ldexpf(1.0f, -k);
+    for (int i = threadIdx.x + 8 * 1024; i < N; i += 1024) m = fmaxf(m, fabsf(xt[i]));
+    m = block_absmax(m);
+    const int e = split_exp(m);
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const int i = threadIdx.x + k * 1024;
+        if (i < N) split_store(v[k], e, &o[(i >> 3) * 16 + (i & 7)], &o[(i >> 3) * 16 + 8 + (i & 7)]);
+    }
+    for (int i = threadIdx.x + 8 * 1024; i < N; i += 1024)
+        split_store(xt[i], e, &o[(i >> 3) * 16 + (i & 7)], &o[(i >> 3) * 16 + 8 + (i & 7)]);
+    if (threadIdx.x == 0) xscale[t] = ldexpf(1.0f, -e);
 }
 
 extern "C" int wk_split(const float *x, int T, int N, uint16_t *xs, float *xscale, void *stream) {
     if (T <= 0 || N <= 0 || (N & 7)) return -1;
-    hipLaunchKernelGGL(k_split, dim3(T), dim3(256), 0, (hipStream_t)stream, x, N, (_Float16 *)xs, xscale);
+    hipLaunchKernelGGL(k_split, dim3(T), dim3(1024), 0, (hipStream_t)stream, x, N, (_Float16 *)xs, xscale);
     CHECK_LAUNCH();
     return 0;
 }
 
 // ---- router logits --------------------------------------------------------------
 
-// One wave per (token, row): float4 loads, lane partials, fixed xor tree.
+// One 256-thread block per (token, row): eight float4 loads in flight per
+// thread, lane partials, then a fixed-order block sum (deterministic).
 __global__ __launch_bounds__(256) void k_router_fast(const float *__restrict__ W, const float *__restrict__ x,
                                                      int E, int H, int T, float *__restrict__ logits) {
-    const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= E * T) return;
+    __shared__ float part[4];
+    const int row = blockIdx.x;
     const int t = row / E, e = row % E;
     const float *w = W + (size_t)e * H, *xt = x + (size_t)t * H;
     float acc = 0.0f;
     if ((H & 3) == 0) {
         const float4 *w4 = (const float4 *)w, *x4 = (const float4 *)xt;
-        for (int i = lane; i < H / 4; i += 64) {
+        const int n4 = H >> 2;
+        int i = threadIdx.x;
+        for (; i + 7 * 256 < n4; i += 8 * 256) {
+            float4 a[8], b[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) { a[k] = w4[i + k * 256]; b[k] = x4[i + k * 256]; }
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                acc = __builtin_fmaf(a[k].x, b[k].x, acc);
+                acc = __builtin_fmaf(a[k].y, b[k].y, acc);
+                acc = __builtin_fmaf(a[k].z, b[k].z, acc);
+                acc = __builtin_fmaf(a[k].w, b[k].w, acc);
+            }
+        }
+        for (; i < n4; i += 256) {
             const float4 a = w4[i], b = x4[i];
             acc = __builtin_fmaf(a.x, b.x, acc);
             acc = __builtin_fmaf(a.y, b.y, acc);
@@ -154,10 +181,12 @@ __global__ __launch_bounds__(256) void k_router_fast(const float *__restrict__ W
             acc = __builtin_fmaf(a.w, b.w, acc);
         }
     } else {
-        for (int i = lane; i < H; i += 64) acc = __builtin_fmaf(w[i], xt[i], acc);
+        for (int i = threadIdx.x; i < H; i += 256) acc = __builtin_fmaf(w[i], xt[i], acc);
     }
     acc = wave_sum(acc);
-    if (lane == 0) logits[row] = acc;
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) logits[row] = (part[0] + part[1]) + (part[2] + part[3]);
 }
 
 // The reference's dotf on x86 (src/model.c:155-160): one sequential, unfused
@@ -181,8 +210,7 @@ extern "C" int wk_router_logits(const float *W, const float *x, int E, int H, in
         hipLaunchKernelGGL(k_router_strict, dim3((rows + 63) / 64), dim3(64), 0, (hipStream_t)stream, W, x, E, H,
                            T, logits);
     else
-        hipLaunchKernelGGL(k_router_fast, dim3((rows + 3) / 4), dim3(256), 0, (hipStream_t)stream, W, x, E, H, T,
-                           logits);
+        hipLaunchKernelGGL(k_router_fast, dim3(rows), dim3(256), 0, (hipStream_t)stream, W, x, E, H, T, logits);
     CHECK_LAUNCH();
     return 0;
 }
@@ -234,66 +262,80 @@ extern "C" int wk_mvq(const int8_t *W, const uint16_t *ws, size_t rowbytes, int 
     return 0;
 }
 
+// ---- jobs -----------------------------------------------------------------------------
+
+// Pointers of one matrix inside a record (header fields of waste_expert_hdr,
+// src/waste_format.h:98-130). Row scales are gate [I], up [I], down [H].
+__device__ __forceinline__ void job_ptrs(warp_job &jb, const uint8_t *rec, int kind, int inter) {
+    const uint32_t *h = (const uint32_t *)rec;
+    jb.idx = rec + h[WARP_HDR_GATE_OFF / 4 + kind];
+    const int soff = kind == 0 ? 0 : kind == 1 ? inter : 2 * inter;
+    jb.scale = (const uint16_t *)(rec + h[WARP_HDR_CORR_OFF / 4]) + soff;
+}
+
 // ---- routing -----------------------------------------------------------------------
 
-// One 64-lane block per token. Scores in LDS; K rounds of a wave argmax
-// where the larger biased score wins and, on equal scores, the lower expert
-// id (the reference scans ids upwards with strict >, src/model.c:2729-2742).
-__global__ __launch_bounds__(64) void k_route(const float *__restrict__ logits, const float *__restrict__ bias,
-                                              int E, int K, int act, int renorm, float routed_scale,
-                                              int *__restrict__ idx, float *__restrict__ w,
-                                              const uint8_t *const *__restrict__ table, warp_job *__restrict__ jobs,
-                                              int *__restrict__ njobs, int *__restrict__ missing) {
+// One 256-thread block per token: the logits are read in one pass and
+// scored into LDS, then every candidate ranks itself against all others in
+// the reference's order (larger biased score first, on equal scores the
+// lower id: it scans ids upwards with strict >, src/model.c:2729-2742).
+__global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits, const float *__restrict__ bias,
+                                               int E, int K, int act, int renorm, float routed_scale,
+                                               int *__restrict__ idx, float *__restrict__ w,
+                                               const uint8_t *const *__restrict__ table, warp_job *__restrict__ jobs,
+                                               int *__restrict__ njobs, int *__restrict__ missing, int inter) {
     extern __shared__ float lds_route[];
     float *score = lds_route;             // [E]
     float *biased = lds_route + E;        // [E], -inf once taken
     __shared__ int sel[WARP_MAX_K];
     __shared__ float wsel[WARP_MAX_K];
-    const int t = blockIdx.x, lane = threadIdx.x;
+    __shared__ float red[4];
+    const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid < WARP_MAX_K) { sel[tid] = 0; wsel[tid] = 0.0f; }
     const float *lt = logits + (size_t)t * E;
+    for (int e = tid; e < E; e += 256) score[e] = lt[e];
+    __syncthreads();
     if (act == 1) {
         float mx = -INFINITY;
-        for (int e = lane; e < E; e += 64) mx = fmaxf(mx, lt[e]);
+        for (int e = tid; e < E; e += 256) mx = fmaxf(mx, score[e]);
         mx = wave_max(mx);
-        for (int e = lane; e < E; e += 64) score[e] = exp_cr(__fsub_rn(lt[e], mx));
+        if (lane == 0) red[wave] = mx;
         __syncthreads();
-        if (lane == 0) {
-            float s = 0.0f;
+        mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        for (int e = tid; e < E; e += 256) score[e] = exp_cr(__fsub_rn(score[e], mx));
+        __syncthreads();
+        if (tid == 0) {
+            float s = 0.0f;                   // sequential, as the reference sums
             for (int e = 0; e < E; e++) s = __fadd_rn(s, score[e]);
-            biased[0] = s;
+            red[0] = s;
         }
         __syncthreads();
-        const float s = biased[0];
-        __syncthreads();
-        for (int e = lane; e < E; e += 64) score[e] = __fdiv_rn(score[e], s);
+        const float s = red[0];
+        for (int e = tid; e < E; e += 256) score[e] = __fdiv_rn(score[e], s);
     } else {
-        for (int e = lane; e < E; e += 64) score[e] = __fdiv_rn(1.0f, __fadd_rn(1.0f, exp_cr(-lt[e])));
+        for (int e = tid; e < E; e += 256) score[e] = __fdiv_rn(1.0f, __fadd_rn(1.0f, exp_cr(-score[e])));
     }
     __syncthreads();
-    for (int e = lane; e < E; e += 64) biased[e] = __fadd_rn(score[e], bias ? bias[e] : 0.0f);
+    for (int e = tid; e < E; e += 256) biased[e] = __fadd_rn(score[e], bias ? bias[e] : 0.0f);
     __syncthreads();
-    for (int j = 0; j < K; j++) {
-        float bv = -1e30f;
-        int be = 0x7fffffff;
-        for (int e = lane; e < E; e += 64) {
-            const float v = biased[e];
-            if (v > bv) { bv = v; be = e; }
+    // Rank selection: candidate e takes place r = #{e' beating e}, where e'
+    // beats e if its biased score is larger, or equal with a lower id. The
+    // first K places are the K picks of the reference's repeated strict-max
+    // scan, in its order. Values at or below -1e30 are never picked there.
+    for (int e = tid; e < E; e += 256) {
+        const float v = biased[e];
+        int r = 0;
+        for (int q = 0; q < E; q++) {
+            const float o = biased[q];
+            r += (o > v) || (o == v && q < e);
         }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const float ov = __shfl_xor(bv, o);
-            const int oe = __shfl_xor(be, o);
-            if (ov > bv || (ov == bv && oe < be)) { bv = ov; be = oe; }
+        if (r < K && v > -1e30f) {
+            sel[r] = e;
+            wsel[r] = score[e];
         }
-        if (be == 0x7fffffff) be = 0;     // nothing above -1e30: degenerate input
-        if (lane == 0) {
-            sel[j] = be;
-            wsel[j] = score[be];
-            biased[be] = -INFINITY;
-        }
-        __syncthreads();
     }
-    if (lane == 0) {
+    __syncthreads();
+    if (tid == 0) {
         if (renorm && K > 1) {
             float s = 0.0f;
             for (int j = 0; j < K; j++) s = __fadd_rn(s, wsel[j]);
@@ -309,22 +351,24 @@ __global__ __launch_bounds__(64) void k_route(const float *__restrict__ logits, 
     if (table) {
         __syncthreads();
         int miss = 0;
-        for (int j = lane; j < K; j += 64) {
+        for (int j = tid; j < K; j += 256) {
             const uint8_t *rec = table[sel[j]];
             miss |= rec == nullptr;
             for (int kind = 0; kind < 3; kind++) {
                 warp_job jb;
-                jb.rec = rec;
-                jb.kind = kind;
+                jb.idx = nullptr;
+                jb.scale = nullptr;
+                if (rec) job_ptrs(jb, rec, kind, inter);
                 jb.n = 1;
+                jb.rsv = 0;
                 for (int s = 0; s < WARP_TPJ; s++) { jb.xi[s] = 0; jb.yi[s] = 0; }
                 jb.xi[0] = kind == 2 ? j : 0;
                 jb.yi[0] = j;
                 jobs[kind * K + j] = jb;
             }
         }
-        miss = __any(miss);
-        if (lane == 0) {
+        miss = __syncthreads_or(miss);
+        if (tid == 0) {
             for (int kind = 0; kind < 3; kind++) njobs[kind] = miss ? 0 : K;
             if (miss) *missing = 1;
         }
@@ -333,11 +377,11 @@ __global__ __launch_bounds__(64) void k_route(const float *__restrict__ logits, 
 
 extern "C" int wk_route(const float *logits, const float *bias, int E, int K, int T, int act, int renorm,
                         float routed_scale, int *idx, float *w, const uint8_t *const *table, warp_job *jobs,
-                        int *njobs, int *missing, void *stream) {
+                        int *njobs, int *missing, int inter, void *stream) {
     if (E <= 0 || K <= 0 || K > WARP_MAX_K || K > E || T <= 0 || E > 8192) return -1;
     if (table && T != 1) return -1;
-    hipLaunchKernelGGL(k_route, dim3(T), dim3(64), (size_t)E * 2 * sizeof(float), (hipStream_t)stream, logits,
-                       bias, E, K, act, renorm, routed_scale, idx, w, table, jobs, njobs, missing);
+    hipLaunchKernelGGL(k_route, dim3(T), dim3(256), (size_t)E * 2 * sizeof(float), (hipStream_t)stream, logits,
+                       bias, E, K, act, renorm, routed_scale, idx, w, table, jobs, njobs, missing, inter);
     CHECK_LAUNCH();
     return 0;
 }
@@ -412,6 +456,7 @@ struct VqArgs {
 // Block = 16 waves, grid.y = kind. A unit is (job, 64-row block); WPU waves
 // share one unit, each over a contiguous range of 4-position groups, and
 // their partial sums meet in LDS (fixed order, so results are deterministic).
+// Code words and B operands run VQ_D groups ahead of their use.
 template <int FMT, int TPJ, int WPU>
 __global__ __launch_bounds__(1024) void k_vq_mfma(VqArgs a) {
     typedef FmtT<FMT> F;
@@ -438,7 +483,6 @@ __global__ __launch_bounds__(1024) void k_vq_mfma(VqArgs a) {
     const int sub = wave / WPU, part = wave % WPU;
     const int pg0 = part * npg / WPU, pg1 = (part + 1) * npg / WPU;
     const int ts = jc >> 1, hl = jc & 1;
-    const uint32_t hdr_off = WARP_HDR_GATE_OFF + 4 * kind;
 
     for (int ub = blockIdx.x * UPW; ub < units; ub += gridDim.x * UPW) {
         const int u = ub + sub;
@@ -448,24 +492,30 @@ __global__ __launch_bounds__(1024) void k_vq_mfma(VqArgs a) {
         if (u < units && pg0 < pg1) {
             const warp_job &jb = jobs[u / nrb];
             const int rb = u % nrb;
-            const uint8_t *rec = jb.rec;
-            const uint32_t moff = *(const uint32_t *)(rec + hdr_off);
-            const uint8_t *cp = rec + moff + ((size_t)rb * nv) * 64 * F::SB + (size_t)lane * 4 * F::SB;
+            const uint8_t *cp = jb.idx + ((size_t)rb * nv) * 64 * F::SB + (size_t)lane * 4 * F::SB;
             const bool bvalid = ts < jb.n && ts < TPJ;
-            const _Float16 *xrow = a.xs + (size_t)(bvalid ? jb.xi[ts] : 0) * nv * 16 + hl * 8;
-            half8 b = {0, 0, 0, 0, 0, 0, 0, 0};
+            const _Float16 *xrow = a.xs + (size_t)(bvalid ? jb.xi[ts] : 0) * nv * 16 + hl * 8 + (size_t)g * 16;
             Word<F::SB> buf[VQ_D];
+            half8 bb[VQ_D];
 #pragma unroll
-            for (int k = 0; k < VQ_D; k++)
-                if (pg0 + k < pg1) buf[k].load(cp + (size_t)(pg0 + k) * 256 * F::SB);
+            for (int k = 0; k < VQ_D; k++) {
+                bb[k] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+                if (pg0 + k < pg1) {
+                    buf[k].load(cp + (size_t)(pg0 + k) * 256 * F::SB);
+                    if (bvalid) bb[k] = *(const half8 *)(xrow + (size_t)(pg0 + k) * 64);
+                }
+            }
             for (int pgb = pg0; pgb < pg1; pgb += VQ_D) {
 #pragma unroll
                 for (int k = 0; k < VQ_D; k++) {
                     const int pg = pgb + k;
                     if (pg < pg1) {
                         const Word<F::SB> wd = buf[k];
-                        if (pg + VQ_D < pg1) buf[k].load(cp + (size_t)(pg + VQ_D) * 256 * F::SB);
-                        if (bvalid) b = *(const half8 *)(xrow + (size_t)(pg * 4 + g) * 16);
+                        const half8 b = bb[k];
+                        if (pg + VQ_D < pg1) {
+                            buf[k].load(cp + (size_t)(pg + VQ_D) * 256 * F::SB);
+                            if (bvalid) bb[k] = *(const half8 *)(xrow + (size_t)(pg + VQ_D) * 64);
+                        }
 #pragma unroll
                         for (int t = 0; t < 4; t++) {
                             const unsigned sl = wd.slot(t);
@@ -498,10 +548,7 @@ __global__ __launch_bounds__(1024) void k_vq_mfma(VqArgs a) {
             if (tsl >= jb.n || rg >= M) continue;
             float v = 0.0f;
             for (int p = 0; p < WPU; p++) v += red[((s * WPU + p) * TPJ + tsl) * 64 + row];
-            const uint8_t *rec = jb.rec;
-            const uint16_t *sc = (const uint16_t *)(rec + *(const uint32_t *)(rec + WARP_HDR_CORR_OFF));
-            const int soff = kind == 0 ? 0 : kind == 1 ? M : 2 * N;
-            v = (v * a.xscale[jb.xi[tsl]]) * f16_keep(sc[soff + rg]);
+            v = (v * a.xscale[jb.xi[tsl]]) * f16_keep(jb.scale[rg]);
             a.y[kind][(size_t)jb.yi[tsl] * M + rg] = v;
         }
         __syncthreads();
@@ -529,12 +576,28 @@ static int launch_vq(const VqArgs &a, int nkinds, int max_units, void *stream) {
     return 0;
 }
 
+// Waves per unit: enough position groups per wave (>= 16) to amortise the
+// unit's start-up, at most 16. WARP_VQ_WPU overrides it (tuning).
+static int choose_wpu(int npg) {
+    static int forced = -1;
+    if (forced < 0) {
+        const char *e = getenv("WARP_VQ_WPU");
+        forced = e ? atoi(e) : 0;
+    }
+    if (forced == 1 || forced == 2 || forced == 4 || forced == 8 || forced == 16) return forced;
+    int w = 16;
+    while (w > 1 && npg / w < 16) w >>= 1;
+    return w;
+}
+
 template <int FMT, int TPJ>
 static int launch_vq_w(const VqArgs &a, int nkinds, int max_units, int npg, void *stream) {
-    if (npg >= 128) return launch_vq<FMT, TPJ, 16>(a, nkinds, max_units, stream);
-    if (npg >= 32) return launch_vq<FMT, TPJ, 8>(a, nkinds, max_units, stream);
-    if (npg >= 16) return launch_vq<FMT, TPJ, 4>(a, nkinds, max_units, stream);
-    if (npg >= 4) return launch_vq<FMT, TPJ, 2>(a, nkinds, max_units, stream);
+    switch (choose_wpu(npg)) {
+    case 16: return launch_vq<FMT, TPJ, 16>(a, nkinds, max_units, stream);
+    case 8: return launch_vq<FMT, TPJ, 8>(a, nkinds, max_units, stream);
+    case 4: return launch_vq<FMT, TPJ, 4>(a, nkinds, max_units, stream);
+    case 2: return launch_vq<FMT, TPJ, 2>(a, nkinds, max_units, stream);
+    }
     return launch_vq<FMT, TPJ, 1>(a, nkinds, max_units, stream);
 }
 
@@ -626,14 +689,30 @@ extern "C" int wk_decode_weights(int fmt, const uint8_t *idx, const uint16_t *sc
 
 // ---- activation --------------------------------------------------------------------------
 
-__global__ __launch_bounds__(256) void k_act_split(const float *__restrict__ g, const float *__restrict__ u, int I,
-                                                   int situ, float beta, float lbeta, _Float16 *__restrict__ xs,
-                                                   float *__restrict__ xscale, float *__restrict__ h_out) {
+__global__ __launch_bounds__(1024) void k_act_split(const float *__restrict__ g, const float *__restrict__ u, int I,
+                                                    int situ, float beta, float lbeta, _Float16 *__restrict__ xs,
+                                                    float *__restrict__ xscale, float *__restrict__ h_out) {
     const int p = blockIdx.x;
     extern __shared__ float lds_h[];
     const float *gp = g + (size_t)p * I, *up = u + (size_t)p * I;
+    float gv[4], uv[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int i = threadIdx.x + k * 1024;
+        gv[k] = i < I ? gp[i] : 0.0f;
+        uv[k] = i < I ? up[i] : 0.0f;
+    }
     float m = 0.0f;
-    for (int i = threadIdx.x; i < I; i += blockDim.x) {
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int i = threadIdx.x + k * 1024;
+        if (i < I) {
+            const float h = act_pair(gv[k], uv[k], situ, beta, lbeta);
+            lds_h[i] = h;
+            m = fmaxf(m, fabsf(h));
+        }
+    }
+    for (int i = threadIdx.x + 4 * 1024; i < I; i += 1024) {
         const float h = act_pair(gp[i], up[i], situ, beta, lbeta);
         lds_h[i] = h;
         m = fmaxf(m, fabsf(h));
@@ -652,7 +731,7 @@ __global__ __launch_bounds__(256) void k_act_split(const float *__restrict__ g, 
 extern "C" int wk_act_split(const float *g, const float *u, int P, int I, int act_situ, float beta, float lbeta,
                             uint16_t *xs, float *xscale, float *h_out, void *stream) {
     if (P <= 0 || I <= 0 || (I & 7) || I > 16384) return -1;
-    hipLaunchKernelGGL(k_act_split, dim3(P), dim3(256), (size_t)I * sizeof(float), (hipStream_t)stream, g, u, I,
+    hipLaunchKernelGGL(k_act_split, dim3(P), dim3(1024), (size_t)I * sizeof(float), (hipStream_t)stream, g, u, I,
                        act_situ, beta, lbeta, (_Float16 *)xs, xscale, h_out);
     CHECK_LAUNCH();
     return 0;
@@ -759,8 +838,7 @@ __global__ __launch_bounds__(256) void k_apply_p6(const warp_job *__restrict__ j
     if (unit >= njobs[kind] * nrb) return;
     const warp_job &jb = jobs[unit / nrb];
     const int rb = unit % nrb, r = rb * 64 + lane;
-    const uint8_t *rec = jb.rec;
-    const uint8_t *idx = rec + *(const uint32_t *)(rec + WARP_HDR_GATE_OFF + 4 * kind);
+    const uint8_t *idx = jb.idx;
     for (int ts = 0; ts < jb.n; ts++) {
     const int8_t *T0 = lut8 + (size_t)jb.xi[ts] * nv * 256;
     const float *ls = lscale + (size_t)jb.xi[ts] * nblk;
@@ -776,11 +854,7 @@ __global__ __launch_bounds__(256) void k_apply_p6(const warp_job *__restrict__ j
         }
         acc = __fadd_rn(acc, __fmul_rn(ls[b], (float)sum));
     }
-    if (r < M) {
-        const uint16_t *sc = (const uint16_t *)(rec + *(const uint32_t *)(rec + WARP_HDR_CORR_OFF));
-        const int soff = kind == 0 ? 0 : kind == 1 ? M : 2 * N;
-        y[(size_t)jb.yi[ts] * M + r] = __fmul_rn(acc, f16_keep(sc[soff + r]));
-    }
+    if (r < M) y[(size_t)jb.yi[ts] * M + r] = __fmul_rn(acc, f16_keep(jb.scale[r]));
     }
 }
 
@@ -803,7 +877,8 @@ __global__ __launch_bounds__(1024) void k_plan_chunk(const int *__restrict__ idx
                                                      int *__restrict__ counts, int *__restrict__ offsets,
                                                      int *__restrict__ pair_tok, int *__restrict__ pair_exp,
                                                      float *__restrict__ pair_w, warp_job *__restrict__ jobs,
-                                                     int max_jobs, int *__restrict__ njobs, int *__restrict__ missing) {
+                                                     int max_jobs, int *__restrict__ njobs, int *__restrict__ missing,
+                                                     int inter) {
     __shared__ int s_tiles_total;
     const int P = T * K;
     for (int e = threadIdx.x; e < E; e += blockDim.x) counts[e] = 0;
@@ -847,9 +922,9 @@ __global__ __launch_bounds__(1024) void k_plan_chunk(const int *__restrict__ idx
             const int base = offsets[e] + i * WARP_TPJ, n = min(WARP_TPJ, c - i * WARP_TPJ);
             for (int kind = 0; kind < 3; kind++) {
                 warp_job jb;
-                jb.rec = table[e];
-                jb.kind = kind;
+                job_ptrs(jb, table[e], kind, inter);
                 jb.n = n;
+                jb.rsv = 0;
                 for (int s = 0; s < WARP_TPJ; s++) {
                     const int slot = base + (s < n ? s : 0);
                     jb.xi[s] = kind == 2 ? slot : pair_tok[slot];
@@ -863,10 +938,10 @@ __global__ __launch_bounds__(1024) void k_plan_chunk(const int *__restrict__ idx
 
 extern "C" int wk_plan_chunk(const int *idx, const float *w, int T, int K, int E, const uint8_t *const *table,
                              int *counts, int *offsets, int *pair_tok, int *pair_exp, float *pair_w, warp_job *jobs,
-                             int max_jobs, int *njobs, int *missing, void *stream) {
+                             int max_jobs, int *njobs, int *missing, int inter, void *stream) {
     if (T <= 0 || K <= 0 || E <= 0 || max_jobs <= 0) return -1;
     hipLaunchKernelGGL(k_plan_chunk, dim3(1), dim3(1024), 0, (hipStream_t)stream, idx, w, T, K, E, table, counts,
-                       offsets, pair_tok, pair_exp, pair_w, jobs, max_jobs, njobs, missing);
+                       offsets, pair_tok, pair_exp, pair_w, jobs, max_jobs, njobs, missing, inter);
     CHECK_LAUNCH();
     return 0;
 }

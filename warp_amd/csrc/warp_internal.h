@@ -38,12 +38,14 @@ extern "C" {
 #define WARP_MAX_K 64         /* top-k bound (the reference's cfg_sane)  */
 
 /* One matvec job: one matrix (kind) of one expert record against up to
- * WARP_TPJ input vectors. xi[t] indexes the split inputs, yi[t] the output
- * rows block ([y_index][M]). */
+ * WARP_TPJ input vectors. idx/scale point at that matrix's index block and
+ * row scales inside the record; xi[t] indexes the split inputs, yi[t] the
+ * output rows block ([y_index][M]). The list a job sits in gives its kind. */
 typedef struct {
-    const uint8_t *rec;
-    int kind;                 /* 0 gate, 1 up, 2 down                    */
+    const uint8_t *idx;
+    const uint16_t *scale;
     int n;                    /* token slots in use, 1..WARP_TPJ         */
+    int rsv;
     int xi[WARP_TPJ];
     int yi[WARP_TPJ];
 } warp_job;
@@ -80,7 +82,7 @@ int wk_mvq(const int8_t *W, const uint16_t *ws, size_t rowbytes, int group, int 
 int wk_route(const float *logits, const float *bias, int E, int K, int T, int act,
              int renorm, float routed_scale, int *idx, float *w,
              const uint8_t *const *table, warp_job *jobs, int *njobs, int *missing,
-             void *stream);
+             int inter, void *stream);
 
 /* The MFMA decode-then-dot matvec over a job list, one launch per group of
  * kinds: kind_lo..kind_lo+nkinds-1. jobs[k] / njobs[k] are the lists of
@@ -132,7 +134,7 @@ int wk_act(const float *g, const float *u, int P, int I, int act_situ, float bet
 int wk_plan_chunk(const int *idx, const float *w, int T, int K, int E,
                   const uint8_t *const *table, int *counts, int *offsets,
                   int *pair_tok, int *pair_exp, float *pair_w, warp_job *jobs,
-                  int max_jobs, int *njobs, int *missing, void *stream);
+                  int max_jobs, int *njobs, int *missing, int inter, void *stream);
 /* out [T][H] = per token, sum over its pairs in ascending expert id of
  * w * y[pair], then + add0 [T][H] when given. */
 int wk_combine_chunk(const float *y, const int *offsets, const int *pair_tok,
