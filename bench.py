@@ -93,6 +93,7 @@ def setup(layers, resident, seed=1234):
 def run_gpu(args):
     from warp_amd.device import Buf, Event
     ctx, rec_bytes = setup(args.layers, args.resident)
+    ctx.set_matvec_path(args.matvec_path)
     n_in = max(args.steps, args.warmup, 1)
     X = Buf.of(np.random.default_rng(7).standard_normal((n_in, H), dtype=np.float32))
     bufs = [Buf.empty(H), Buf.empty(H)]
@@ -182,6 +183,8 @@ def main():
     ap.add_argument("--resident", type=int, default=64, help="expert records per layer kept in HBM")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--matvec-path", choices=["auto", "mfma"], default="auto",
+                    help="expert matvec kernel: auto = the LUT kernel, mfma = decode-then-dot on the matrix cores")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="before timing, one device-to-device copy of this many MiB (a known-size "
                          "kernel for scaling the profiler's traffic counters)")

@@ -236,6 +236,14 @@ int warp_hip_put_expert_dev(warp_hip_ctx *c, int layer, int expert, const uint8_
  * scales ((2*inter + hidden) fp16, gate then up then down). */
 int warp_hip_put_expert_synth(warp_hip_ctx *c, int layer, int expert, uint64_t seed,
                               const uint16_t *scales);
+/* Expert matvec kernels for single-token decode (no counterpart in the
+ * reference, which has one CPU path). AUTO (the default) runs the LUT
+ * kernel -- the reference's LUT algorithm, fp32 tables in LDS -- for the
+ * float-LUT formats when hidden and inter are multiples of 16; MFMA forces
+ * the decode-then-dot matrix-core kernel that prefill always uses. Applies
+ * to warp_hip_moe_decode* and warp_hip_vq_matvec. */
+enum { WARP_HIP_PATH_AUTO = 0, WARP_HIP_PATH_MFMA = 1 };
+int warp_hip_set_matvec_path(warp_hip_ctx *c, int path);
 /* Per-launch timing with HIP events on the compute stream: when on, every
  * warp_hip_moe_decode brackets its launches of class 0 (gate/up expert
  * matvec), 1 (down expert matvec) and 2 (router logits). get returns the

@@ -1,0 +1,76 @@
+"""The LUT expert matvec at shapes that exercise its work split: row groups
+that span jobs (gate/up share one input), per-job groups (down), odd and
+partial 64-row blocks, splits of a single 2-position chunk, and the
+decode-then-dot path on the same inputs for comparison.
+
+Bar: selection bit-exact, outputs max|d|/max|ref| <= 1e-4 against the oracle.
+The table entries themselves are the reference's fused chain bit for bit, so
+the only difference from the oracle is the order of the fp32 sum over
+positions (splits, then position parity); the logged errors are ~1e-7.
+"""
+import numpy as np
+import pytest
+
+import container as ct
+from gpu_util import dev, empty, host, log, open_ctx, rel_err
+from oracle import pyoracle as po
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+
+SHAPES = [
+    # partial last row block (96 = 64 + 32) and odd row-block counts
+    dict(hidden=160, inter=96, experts=8, top_k=3),
+    # gate/up: 8 jobs x 32 row blocks = 2 row groups spanning jobs; 1 chunk per split
+    dict(hidden=1024, inter=2048, experts=12, top_k=8),
+]
+
+
+@pytest.mark.parametrize("fmt", ["VQ12", "VQ3R", "VQ2R"])
+@pytest.mark.parametrize("shape", range(len(SHAPES)))
+def test_lut_decode_and_matvec(fmt, shape):
+    import warp_amd
+    spec = ct.Spec(layers=1, fmt=fmt, seed=100 + shape, **SHAPES[shape])
+    model = ct.build(spec)
+    ctx = open_ctx(model)
+    try:
+        warp_amd.load_container_model(ctx, model)
+        log(f"[{fmt} {SHAPES[shape]}] loaded")
+        lv = po.LayerView(model, 0)
+        rng = np.random.default_rng(17)
+        worst = {"auto": 0.0, "mfma": 0.0}
+        for t in range(3):
+            x = rng.normal(size=spec.hidden).astype(np.float32)
+            ro, ri, rw, _ = lv.moe_layer(x)
+            for path in ("auto", "mfma"):
+                ctx.set_matvec_path(path)
+                out = empty(spec.hidden)
+                idx, w = ctx.moe_decode(0, dev(x), out, want_route=True)
+                assert np.array_equal(idx, ri), (path, idx, ri)
+                e = rel_err(host(out), ro)
+                worst[path] = max(worst[path], e)
+                assert e <= TOL, (path, t, e)
+        log(f"[{fmt} {SHAPES[shape]}] moe_decode worst rel err lut {worst['auto']:.2e} "
+            f"mfma {worst['mfma']:.2e}")
+
+        ctx.set_matvec_path("auto")
+        S = ct.FMT_STAGES[fmt]
+        bT = po.books_T(model.books_raw)
+        for e in (0, spec.experts - 1):
+            rec = ctx.resident(0, e)
+            r = np.frombuffer(model.layers[0].records[e], np.uint8)
+            hdr = np.frombuffer(model.layers[0].records[e][:48], np.uint32)
+            for kind in range(3):
+                M, N = (spec.inter, spec.hidden) if kind < 2 else (spec.hidden, spec.inter)
+                x = rng.normal(size=N).astype(np.float32)
+                y = empty(M)
+                ctx.vq_matvec(0, kind, rec, dev(x), y)
+                off, corr = int(hdr[5 + kind]), int(hdr[8])
+                soff = [0, spec.inter, 2 * spec.inter][kind]
+                scale = r[corr + 2 * soff: corr + 2 * (soff + M)].view(np.uint16).copy()
+                yr = po.vq_matvec(fmt, r[off:].copy(), scale, x, bT, kind * S, M, N)
+                err = rel_err(host(y), yr)
+                assert err <= TOL, (e, kind, err)
+        log(f"[{fmt} {SHAPES[shape]}] vq_matvec (lut) within bar")
+    finally:
+        ctx.close()

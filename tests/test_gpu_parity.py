@@ -60,9 +60,11 @@ def test_decode_weights_bitexact(loaded):
     log(f"[{fmt}] decoded weights bit-exact")
 
 
-def test_vq_matvec(loaded):
+@pytest.mark.parametrize("path", ["auto", "mfma"])
+def test_vq_matvec(loaded, path):
     fmt, model, ctx = loaded
     spec = model.spec
+    ctx.set_matvec_path(path)
     S = {"VQ3R": 3, "VQ2R": 2, "VQ4P": 4, "VQ12": 2}[fmt]
     bT = po.books_T(model.books_raw)
     rng = np.random.default_rng(3)
@@ -85,7 +87,8 @@ def test_vq_matvec(loaded):
                     assert np.array_equal(yg, yr), (L, e, kind, rel_err(yg, yr))
                 else:
                     assert rel_err(yg, yr) <= TOL, (L, e, kind, rel_err(yg, yr))
-    log(f"[{fmt}] vq_matvec within bar")
+    ctx.set_matvec_path("auto")
+    log(f"[{fmt}] vq_matvec ({path}) within bar")
 
 
 def test_router_strict_and_route(loaded):
@@ -116,9 +119,11 @@ def test_router_strict_and_route(loaded):
     log(f"[{fmt}] strict router bit-exact, selection and weights bit-exact")
 
 
-def test_moe_decode(loaded):
+@pytest.mark.parametrize("path", ["auto", "mfma"])
+def test_moe_decode(loaded, path):
     fmt, model, ctx = loaded
     spec = model.spec
+    ctx.set_matvec_path(path)
     rng = np.random.default_rng(5)
     worst = 0.0
     for L in range(spec.layers):
@@ -132,7 +137,8 @@ def test_moe_decode(loaded):
             e = rel_err(host(out), ro)
             worst = max(worst, e)
             assert e <= TOL, (L, t, e)
-    log(f"[{fmt}] moe_decode worst rel err {worst:.2e}")
+    ctx.set_matvec_path("auto")
+    log(f"[{fmt}] moe_decode ({path}) worst rel err {worst:.2e}")
 
 
 def test_moe_decode_host_matches_device(loaded):

@@ -212,6 +212,7 @@ void warp_hip_table_stats(uint64_t *device_calls, uint64_t *fallback_calls)
 
 typedef struct {
     uint16_t *books;            /* [3][S][E][8] fp16, flushed              */
+    int books_x31;              /* some book value has exponent 31         */
     int cb_base, has_books;
     float *router;              /* [E][H] or NULL                          */
     int8_t *rq; uint16_t *rs;   /* quantised router                        */
@@ -263,6 +264,9 @@ struct warp_hip_ctx {
     int sh_cap;
     int8_t *lut8, *lut8d;
     float *lscale, *lscaled;
+    float *part;                /* LUT matvec partial sums                 */
+    size_t part_cap;            /* floats                                  */
+    int n_cu, lut_ok, mv_path;
     int *counts, *offsets, *pair_tok, *pair_exp;
     float *pair_w;
     float *xin, *xout;
@@ -371,6 +375,19 @@ static int ctx_alloc(warp_hip_ctx *c)
     DMALLOC(c, c->la_logits, (size_t)E * 4);
     DMALLOC(c, c->la_idx, (size_t)WARP_MAX_K * 4);
     DMALLOC(c, c->la_w, (size_t)WARP_MAX_K * 4);
+    if (c->lut_ok) {
+        /* decode: gate+up over K jobs sharing x, then down per job */
+        int gr, sp;
+        size_t need = 0;
+        if (!wk_lut_plan(I, H, K, 2, 1, c->n_cu, (size_t)-1, &gr, &sp))
+            need = (size_t)2 * sp * K * (((size_t)I + 63) / 64) * 64;
+        if (!wk_lut_plan(H, I, K, 1, 0, c->n_cu, (size_t)-1, &gr, &sp)) {
+            const size_t d = (size_t)sp * K * (((size_t)H + 63) / 64) * 64;
+            if (d > need) need = d;
+        }
+        c->part_cap = need;
+        DMALLOC(c, c->part, need * sizeof(float));
+    }
     if (c->P6) {
         DMALLOC(c, c->lut8, (size_t)T * 2 * nvH * 256);
         DMALLOC(c, c->lscale, (size_t)T * 2 * nblkH * 4);
@@ -466,6 +483,11 @@ int warp_hip_open(const warp_hip_cfg *cfg, warp_hip_ctx **out)
             rc = WARP_HIP_E_DEVICE;
             goto fail;
         }
+    if (!HIPOK(hipDeviceGetAttribute(&c->n_cu, hipDeviceAttributeMultiprocessorCount, g->device)) || c->n_cu < 1)
+        c->n_cu = 256;
+    /* the LUT matvec serves decode for the float-LUT formats; it walks the
+     * positions two at a time */
+    c->lut_ok = !c->P6 && g->hidden % 16 == 0 && g->inter % 16 == 0;
     c->L = (layer_t *)calloc((size_t)g->n_layers, sizeof(layer_t));
     if (!c->L) { rc = WARP_HIP_E_NOMEM; goto fail; }
     if ((rc = ctx_alloc(c)) != 0) goto fail;
@@ -496,7 +518,7 @@ void warp_hip_close(warp_hip_ctx *c)
     void *d[] = { c->logits, c->idx, c->w, c->jobs, c->njobs, c->missing, c->xs, c->xscale, c->yg, c->yu,
                   c->yd, c->xsh, c->xscaleh, c->hbuf, c->shg, c->shu, c->shh, c->sho, c->lut8, c->lut8d,
                   c->lscale, c->lscaled, c->counts, c->offsets, c->pair_tok, c->pair_exp, c->pair_w,
-                  c->xin, c->xout, c->la_logits, c->la_idx, c->la_w, c->table_dev, c->pool };
+                  c->xin, c->xout, c->la_logits, c->la_idx, c->la_w, c->table_dev, c->pool, c->part };
     for (size_t i = 0; i < sizeof d / sizeof d[0]; i++) hfree(d[i]);
     hhfree(c->h_idx); hhfree(c->h_w); hhfree(c->h_la_idx); hhfree(c->h_missing); hhfree(c->staging);
     free(c->key_slot); free(c->slot_key); free(c->hits); free(c->last); free(c->pin);
@@ -568,6 +590,11 @@ int warp_hip_set_codebooks(warp_hip_ctx *c, int layer, int cb_base, const uint16
      * kernels rebias them as the reference does. */
     for (size_t i = 0; i < n; i++) tmp[i] = ((books[i] >> 10) & 0x1f) ? books[i] : (uint16_t)(books[i] & 0x8000);
     rc = upload(c, (void **)&c->L[layer].books, tmp, n * sizeof(uint16_t));
+    /* the reference reads exponent 31 as a finite power of two; the LUT
+     * kernel then needs its exact (slower) conversion */
+    c->L[layer].books_x31 = 0;
+    for (size_t i = 0; i < n; i++)
+        if (((tmp[i] >> 10) & 0x1f) == 0x1f) { c->L[layer].books_x31 = 1; break; }
     free(tmp);
     if (rc) return rc;
     c->L[layer].cb_base = cb_base;
@@ -980,6 +1007,13 @@ static int timing_end(warp_hip_ctx *c)
     return 0;
 }
 
+int warp_hip_set_matvec_path(warp_hip_ctx *c, int path)
+{
+    if (!c || (path != WARP_HIP_PATH_AUTO && path != WARP_HIP_PATH_MFMA)) return WARP_HIP_E_ARG;
+    c->mv_path = path;
+    return 0;
+}
+
 int warp_hip_set_timing(warp_hip_ctx *c, int on)
 {
     if (!c) return WARP_HIP_E_ARG;
@@ -1079,9 +1113,12 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
     if (!L->has_books || (!L->router && !L->rq))
         return set_err(c, WARP_HIP_E_ARG, layer, -1, "layer %d has no codebooks or router", layer);
     const uint8_t *const *table = c->table_dev + (size_t)layer * E;
+    const int use_lut = c->lut_ok && c->mv_path == WARP_HIP_PATH_AUTO && L->books;
 
     /* inputs for the gate/up matvecs, then the router */
-    if (c->P6) {
+    if (use_lut) {
+        /* the table kernel reads x in f32 */
+    } else if (c->P6) {
         const size_t nvH = (size_t)H / 8, nblkH = (nvH + WARP_LUT_BLK - 1) / WARP_LUT_BLK;
         KRN(c, wk_lut_p6(x_dev, 1, H, books_kind(c, L, 0), c->lut8, c->lscale, c->st));
         KRN(c, wk_lut_p6(x_dev, 1, H, books_kind(c, L, 1), c->lut8 + nvH * 256, c->lscale + nblkH, c->st));
@@ -1125,7 +1162,20 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
 
     /* gate and up, activation, down */
     float *yk[3] = { c->yg, c->yu, c->yd };
-    if (c->P6) {
+    int sp_d = 0;
+    if (use_lut) {
+        int sp_gu = 0;
+        if ((rc = timing_begin(c, 0))) return rc;
+        KRN(c, wk_vq_lut(g->fmt, c->jobs, c->njobs, K, 0, 2, L->books, L->books_x31, x_dev, 1, c->part, c->part_cap, I, H,
+                         c->n_cu, &sp_gu, c->st));
+        if ((rc = timing_end(c))) return rc;
+        KRN(c, wk_act_lut(c->jobs, c->njobs, K, c->part, sp_gu, I, g->act_situ, g->situ_beta, g->situ_linear_beta,
+                          c->hbuf, c->st));
+        if ((rc = timing_begin(c, 1))) return rc;
+        KRN(c, wk_vq_lut(g->fmt, c->jobs, c->njobs, K, 2, 1, L->books, L->books_x31, c->hbuf, 0, c->part, c->part_cap, H, I,
+                         c->n_cu, &sp_d, c->st));
+        if ((rc = timing_end(c))) return rc;
+    } else if (c->P6) {
         const size_t nvH = (size_t)H / 8, nblkH = (nvH + WARP_LUT_BLK - 1) / WARP_LUT_BLK;
         KRN(c, wk_apply_p6(c->jobs, c->njobs, K, 0, c->lut8, c->lscale, c->yg, I, H, c->st));
         KRN(c, wk_apply_p6(c->jobs, c->njobs, K, 1, c->lut8 + nvH * 256, c->lscale + nblkH, c->yu, I, H, c->st));
@@ -1143,7 +1193,11 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
         if ((rc = timing_end(c))) return rc;
     }
     if (L->sq[0] && (rc = shared_ffn(c, L, x_dev, 1))) return rc;
-    KRN(c, wk_combine(c->yd, c->w, K, H, L->sq[0] ? c->sho : NULL, resid_dev, c->missing, out_dev, c->st));
+    if (use_lut)
+        KRN(c, wk_combine_lut(c->jobs + 2 * (size_t)K, c->part, sp_d, K, c->w, K, H, L->sq[0] ? c->sho : NULL,
+                              resid_dev, c->missing, out_dev, c->st));
+    else
+        KRN(c, wk_combine(c->yd, c->w, K, H, L->sq[0] ? c->sho : NULL, resid_dev, c->missing, out_dev, c->st));
     DEV(c, hipEventRecord(c->ev_after, c->st));
 
     if ((rc = lookahead_issue(c, layer, n_la))) return rc;
@@ -1301,6 +1355,12 @@ int warp_hip_vq_matvec(warp_hip_ctx *c, int layer, int kind, const uint8_t *rec_
         float *ls = kind == 2 ? c->lscaled : c->lscale;
         KRN(c, wk_lut_p6(x_dev, 1, N, books_kind(c, L, kind), lut, ls, c->st));
         KRN(c, wk_apply_p6(c->jobs, c->njobs, 1, kind, lut, ls, y_dev, M, N, c->st));
+    } else if (c->lut_ok && c->mv_path == WARP_HIP_PATH_AUTO && L->books) {
+        float *yk[3] = { y_dev, y_dev, y_dev };
+        int sp = 0;
+        KRN(c, wk_vq_lut(c->cfg.fmt, c->jobs, c->njobs, 1, kind, 1, L->books, L->books_x31, x_dev, 1, c->part, c->part_cap, M, N,
+                         c->n_cu, &sp, c->st));
+        KRN(c, wk_lut_reduce(c->jobs, c->njobs, 1, kind, 1, c->part, sp, M, yk, c->st));
     } else {
         float *yk[3] = { y_dev, y_dev, y_dev };
         uint16_t *xs = kind == 2 ? c->xsh : c->xs;

@@ -450,15 +450,27 @@ struct VqArgs {
     int M, N;
 };
 
-#define VQ_NW 16   // waves per block
-#define VQ_D 4     // code words in flight per wave
+// waves per block (NW) and code words in flight per wave (D) are template
+// parameters of the kernel below
 
 // Block = 16 waves, grid.y = kind. A unit is (job, 64-row block); WPU waves
 // share one unit, each over a contiguous range of 4-position groups, and
 // their partial sums meet in LDS (fixed order, so results are deterministic).
-// Code words and B operands run VQ_D groups ahead of their use.
-template <int FMT, int TPJ, int WPU>
-__global__ __launch_bounds__(1024) void k_vq_mfma(VqArgs a) {
+// Code words and B operands run VQ_D groups ahead of their use. With DB the
+// codebook gathers of the next group are issued before the current group's
+// MFMAs, so each wave keeps two groups of LDS reads in flight.
+template <int FMT, int SB>
+__device__ __forceinline__ void gather_group(const unsigned char *lds, const Word<SB> &wd, half8 (&a)[4][FmtT<FMT>::S]) {
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const unsigned sl = wd.slot(t);
+#pragma unroll
+        for (int s = 0; s < FmtT<FMT>::S; s++) a[t][s] = *(const half8 *)(lds + cb_off<FMT>(sl, s));
+    }
+}
+
+template <int FMT, int TPJ, int WPU, int DB, int VQ_NW, int VQ_D>
+__global__ __launch_bounds__(VQ_NW * 64) void k_vq_mfma(VqArgs a) {
     typedef FmtT<FMT> F;
     constexpr int UPW = VQ_NW / WPU;
     extern __shared__ __attribute__((aligned(16))) unsigned char lds_vq[];
@@ -505,25 +517,50 @@ __global__ __launch_bounds__(1024) void k_vq_mfma(VqArgs a) {
                     if (bvalid) bb[k] = *(const half8 *)(xrow + (size_t)(pg0 + k) * 64);
                 }
             }
-            for (int pgb = pg0; pgb < pg1; pgb += VQ_D) {
+            if (DB) {
+                // A operands double-buffered across groups
+                half8 av[2][4][F::S];
+                gather_group<FMT, F::SB>(lds_vq, buf[0], av[0]);
+                for (int pgb = pg0; pgb < pg1; pgb += VQ_D) {
 #pragma unroll
-                for (int k = 0; k < VQ_D; k++) {
-                    const int pg = pgb + k;
-                    if (pg < pg1) {
-                        const Word<F::SB> wd = buf[k];
-                        const half8 b = bb[k];
-                        if (pg + VQ_D < pg1) {
-                            buf[k].load(cp + (size_t)(pg + VQ_D) * 256 * F::SB);
-                            if (bvalid) bb[k] = *(const half8 *)(xrow + (size_t)(pg + VQ_D) * 64);
-                        }
-#pragma unroll
-                        for (int t = 0; t < 4; t++) {
-                            const unsigned sl = wd.slot(t);
-#pragma unroll
-                            for (int s = 0; s < F::S; s++) {
-                                const half8 av = *(const half8 *)(lds_vq + cb_off<FMT>(sl, s));
-                                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b, acc[t], 0, 0, 0);
+                    for (int k = 0; k < VQ_D; k++) {
+                        const int pg = pgb + k;
+                        if (pg < pg1) {
+                            const half8 b = bb[k];
+                            const int cur = k & 1;
+                            // the next group's gathers go out before this group's MFMAs
+                            if (pg + 1 < pg1) gather_group<FMT, F::SB>(lds_vq, buf[(k + 1) % VQ_D], av[cur ^ 1]);
+                            if (pg + VQ_D < pg1) {
+                                buf[k].load(cp + (size_t)(pg + VQ_D) * 256 * F::SB);
+                                if (bvalid) bb[k] = *(const half8 *)(xrow + (size_t)(pg + VQ_D) * 64);
                             }
+#pragma unroll
+                            for (int t = 0; t < 4; t++)
+#pragma unroll
+                                for (int s = 0; s < F::S; s++)
+                                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[cur][t][s], b, acc[t], 0, 0, 0);
+                        }
+                    }
+                }
+            } else {
+                for (int pgb = pg0; pgb < pg1; pgb += VQ_D) {
+#pragma unroll
+                    for (int k = 0; k < VQ_D; k++) {
+                        const int pg = pgb + k;
+                        if (pg < pg1) {
+                            const Word<F::SB> wd = buf[k];
+                            const half8 b = bb[k];
+                            if (pg + VQ_D < pg1) {
+                                buf[k].load(cp + (size_t)(pg + VQ_D) * 256 * F::SB);
+                                if (bvalid) bb[k] = *(const half8 *)(xrow + (size_t)(pg + VQ_D) * 64);
+                            }
+                            half8 av[4][F::S];
+                            gather_group<FMT, F::SB>(lds_vq, wd, av);
+#pragma unroll
+                            for (int t = 0; t < 4; t++)
+#pragma unroll
+                                for (int s = 0; s < F::S; s++)
+                                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[t][s], b, acc[t], 0, 0, 0);
                         }
                     }
                 }
@@ -555,50 +592,66 @@ __global__ __launch_bounds__(1024) void k_vq_mfma(VqArgs a) {
     }
 }
 
-template <int FMT, int TPJ, int WPU>
+template <int FMT, int TPJ, int WPU, int DB, int NW, int D>
 static int launch_vq(const VqArgs &a, int nkinds, int max_units, void *stream) {
     typedef FmtT<FMT> F;
-    constexpr int UPW = VQ_NW / WPU;
-    const size_t lds = (size_t)F::S * F::E * 16 + (size_t)VQ_NW * TPJ * 64 * 4;
+    constexpr int UPW = NW / WPU;
+    const size_t lds = (size_t)F::S * F::E * 16 + (size_t)NW * TPJ * 64 * 4;
     if (lds > 163840) return -2;
     static bool attr = false;
     if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_vq_mfma<FMT, TPJ, WPU>,
+        hipError_t e = hipFuncSetAttribute((const void *)k_vq_mfma<FMT, TPJ, WPU, DB, NW, D>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return -(int)e - 1000;
         attr = true;
     }
     int grid = (max_units + UPW - 1) / UPW;
-    if (grid > 256) grid = 256;
+    const int cap = FMT == WARP_FMT_VQ12 ? 256 : 512;
+    if (grid > cap) grid = cap;
     if (grid < 1) grid = 1;
-    hipLaunchKernelGGL((k_vq_mfma<FMT, TPJ, WPU>), dim3(grid, nkinds), dim3(1024), lds, (hipStream_t)stream, a);
+    hipLaunchKernelGGL((k_vq_mfma<FMT, TPJ, WPU, DB, NW, D>), dim3(grid, nkinds), dim3(NW * 64), lds,
+                       (hipStream_t)stream, a);
     CHECK_LAUNCH();
     return 0;
 }
 
-// Waves per unit: enough position groups per wave (>= 16) to amortise the
-// unit's start-up, at most 16. WARP_VQ_WPU overrides it (tuning).
-static int choose_wpu(int npg) {
-    static int forced = -1;
-    if (forced < 0) {
-        const char *e = getenv("WARP_VQ_WPU");
-        forced = e ? atoi(e) : 0;
-    }
-    if (forced == 1 || forced == 2 || forced == 4 || forced == 8 || forced == 16) return forced;
-    int w = 16;
+// Waves per unit: up to 4 waves share a unit (four units per 16-wave block,
+// which keeps the 64-row units of one launch spread over every CU), fewer
+// when a wave would get under 16 position groups. WARP_VQ_WPU overrides it.
+static int env_int(const char *name, int dflt) {
+    const char *e = getenv(name);
+    return e ? atoi(e) : dflt;
+}
+
+static int choose_wpu(int npg, int nw) {
+    const int forced = env_int("WARP_VQ_WPU", 0);
+    if ((forced == 1 || forced == 2 || forced == 4 || forced == 8 || forced == 16) && forced <= nw) return forced;
+    int w = nw < 4 ? nw : 4;
     while (w > 1 && npg / w < 16) w >>= 1;
     return w;
 }
 
+template <int FMT, int TPJ, int NW, int DB, int D>
+static int launch_vq_s(const VqArgs &a, int nkinds, int max_units, int npg, void *stream) {
+    switch (choose_wpu(npg, NW)) {
+    case 16: return launch_vq<FMT, TPJ, (NW >= 16 ? 16 : NW), DB, NW, D>(a, nkinds, max_units, stream);
+    case 8: return launch_vq<FMT, TPJ, 8, DB, NW, D>(a, nkinds, max_units, stream);
+    case 4: return launch_vq<FMT, TPJ, 4, DB, NW, D>(a, nkinds, max_units, stream);
+    case 2: return launch_vq<FMT, TPJ, 2, DB, NW, D>(a, nkinds, max_units, stream);
+    }
+    return launch_vq<FMT, TPJ, 1, DB, NW, D>(a, nkinds, max_units, stream);
+}
+
+// Kernel shape: 16 waves per block with the next group's codebook gathers
+// issued before the current group's MFMAs and 2 code words in flight (the
+// fastest measured on gfx950 for the K3 shapes); WARP_VQ_SHAPE=0 selects
+// single-buffered gathers with 4 code words in flight.
 template <int FMT, int TPJ>
 static int launch_vq_w(const VqArgs &a, int nkinds, int max_units, int npg, void *stream) {
-    switch (choose_wpu(npg)) {
-    case 16: return launch_vq<FMT, TPJ, 16>(a, nkinds, max_units, stream);
-    case 8: return launch_vq<FMT, TPJ, 8>(a, nkinds, max_units, stream);
-    case 4: return launch_vq<FMT, TPJ, 4>(a, nkinds, max_units, stream);
-    case 2: return launch_vq<FMT, TPJ, 2>(a, nkinds, max_units, stream);
-    }
-    return launch_vq<FMT, TPJ, 1>(a, nkinds, max_units, stream);
+    static int shape = -1;
+    if (shape < 0) shape = env_int("WARP_VQ_SHAPE", 1);
+    if (shape == 0) return launch_vq_s<FMT, TPJ, 16, 0, 4>(a, nkinds, max_units, npg, stream);
+    return launch_vq_s<FMT, TPJ, 16, 1, 2>(a, nkinds, max_units, npg, stream);
 }
 
 template <int FMT>
@@ -631,6 +684,373 @@ extern "C" int wk_vq_matvec(int fmt, const warp_job *jobs, const int *njobs, int
     case WARP_FMT_VQ12: return launch_vq_t<WARP_FMT_VQ12>(a, nkinds, max_units, npg, tokens_per_job, stream);
     }
     return -1;
+}
+
+// ---- the LUT expert matvec (decode) ---------------------------------------------------
+//
+// The reference's own algorithm (src/model.c:1843-2024), laid out for LDS:
+// for every vector position p the table LUT[s][c] = dot(codebook_s[c], x[8p..8p+8])
+// is built with the fused, d-ascending chain of the reference's AVX-512 build
+// (so every entry is bit-identical to the reference's), and each row sums
+// LUT[0][code0] + LUT[1][code1] (+ LUT[2][code2]) over its positions. A random
+// 4-byte LDS read costs about what a random 16-byte codebook gather does, and
+// replaces a gather plus 16 multiply-adds, so the table wins whenever it is
+// amortised over enough rows.
+//
+// Block = 16 waves, one per CU. A block owns a row group (64 pairs of 64-row
+// blocks = 8192 rows, round-robin over the waves; across the jobs of a list
+// when they share one input, within one job otherwise) and a split of the
+// positions, which it walks 2 positions at a time: the table of the next 2
+// positions (2 x S x E floats) is built into one LDS buffer while the rows are
+// summed from the other. The codebook of the block's kind sits in registers
+// (fp32, 8 entries per lane for 2 x 4096). A lane sums 4 rows of one row block
+// at one position parity; the two parities are added at the end and the block
+// writes one partial sum per row and split. The splits are added in order by
+// the consumer (k_lut_reduce, k_act_lut, k_combine_lut), so results are
+// deterministic.
+
+constexpr int LUT_NW = 16;                 // waves per block
+constexpr int LUT_PPW = 4;                 // row-block pairs per wave
+constexpr int LUT_PAIRS = LUT_NW * LUT_PPW;
+constexpr int LUT_RBG = 2 * LUT_PAIRS;     // row blocks per row group
+constexpr int LUT_XCH = 256;               // chunks of x a split stages in LDS (16 KiB)
+
+struct LutArgs {
+    const warp_job *jobs;
+    const int *njobs;
+    int max_jobs, kind_lo;
+    const uint16_t *books;     // [3][S][E][8] fp16, subnormals flushed
+    const float *x;            // inputs [*][N]; a job reads x + xi[0] * N
+    float *part;               // [nkinds][splits][max_jobs][nrb * 64]
+    int M, N, splits, shared_x;
+};
+
+template <int FMT>
+__device__ __forceinline__ unsigned lut_code(unsigned slot, int s) {
+    if (FMT == WARP_FMT_VQ12) return s == 0 ? (slot & 0xFFFu) : (slot >> 12);
+    return (slot >> (8 * s)) & 0xFFu;
+}
+
+// fp16 codebook element -> f32 as the reference converts it. X31 = false:
+// the hardware conversion (exact for every finite fp16; the flushed books
+// hold no subnormals). X31 = true: the reference's rebiasing, which also
+// maps exponent 31 to 2^16..2^17 instead of inf/NaN -- used only for layers
+// whose codebooks hold such values.
+template <bool X31>
+__device__ __forceinline__ float cb_f32(uint32_t packed, int hi) {
+    const uint16_t h = (uint16_t)(hi ? packed >> 16 : packed & 0xFFFFu);
+    if (X31) return f16_flushed(h);
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+
+template <int FMT, bool X31>
+__global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
+    typedef FmtT<FMT> F;
+    constexpr int SE = F::S * F::E;                        // table entries per position
+    constexpr int EPL = (SE + LUT_NW * 64 - 1) / (LUT_NW * 64);
+    constexpr int BUF = 2 * SE;                            // floats per buffer
+    extern __shared__ __attribute__((aligned(16))) float lut[];   // [2][2][S][E], then x of the split
+    const int kind = a.kind_lo + blockIdx.y;
+    const int nj = a.njobs[kind];
+    const warp_job *jobs = a.jobs + (size_t)kind * a.max_jobs;
+    const int nv = a.N >> 3, nrb = (a.M + 63) >> 6, nc = nv >> 1;
+    const int grp = blockIdx.x / a.splits, split = blockIdx.x % a.splits;
+    int fb0, fb_end, xj;
+    if (a.shared_x) {
+        fb0 = grp * LUT_RBG;
+        fb_end = nj * nrb;
+        xj = 0;
+    } else {
+        const int gpj = (nrb + LUT_RBG - 1) / LUT_RBG;
+        xj = grp / gpj;
+        fb0 = xj * nrb + (grp % gpj) * LUT_RBG;
+        fb_end = xj < nj ? (xj + 1) * nrb : 0;
+    }
+    const int c0 = split * nc / a.splits, c1 = (split + 1) * nc / a.splits;
+    if (fb0 >= fb_end || c0 >= c1) return;                 // uniform per block
+    const float *xin = a.x + (size_t)jobs[xj].xi[0] * a.N;
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int pl = (lane >> 4) & 1, rbsel = lane >> 5, quad = lane & 15;
+    // Pairs past the group's rows read row block 0 of the block's first job
+    // (in bounds) and are never written: the loop below has no per-pair
+    // branches, so the code-word loads of the next chunk stay in flight
+    // across the whole chunk and the LDS reads of all pairs overlap.
+    const uint8_t *cp[LUT_PPW];
+    const int jfirst = fb0 / nrb;
+#pragma unroll
+    for (int q = 0; q < LUT_PPW; q++) {
+        const int fb = fb0 + 2 * (q * LUT_NW + wave) + rbsel;
+        const bool ok = fb < fb_end;
+        const int j = ok ? fb / nrb : jfirst, rb = ok ? fb % nrb : 0;
+        cp[q] = jobs[j].idx + ((size_t)rb * nv + pl) * 64 * F::SB + (size_t)quad * 4 * F::SB;
+    }
+
+    // this lane's codebook entries (fp16 pairs), e = tid + 1024 i over [stage][entry]
+    uint4 cb[EPL];
+    const uint4 *bk = (const uint4 *)(a.books + (size_t)kind * SE * 8);
+#pragma unroll
+    for (int i = 0; i < EPL; i++) {
+        const int e = threadIdx.x + i * LUT_NW * 64;
+        cb[i] = e < SE ? bk[e] : make_uint4(0u, 0u, 0u, 0u);
+    }
+
+    // x of this split's positions -> LDS once; the builds read it back as
+    // wave-uniform values (SGPRs), so no vector-memory wait sits in the loop
+    float *xst = lut + 2 * BUF;
+    for (int i = threadIdx.x; i < (c1 - c0) * 16; i += LUT_NW * 64) xst[i] = xin[(size_t)c0 * 16 + i];
+
+    // table entries e = tid + 1024 i of positions 2c, 2c+1 (inputs xv) into buffer b
+    auto build_entry = [&](const float (&xv)[16], int b, int i) {
+        const int e = threadIdx.x + i * LUT_NW * 64;
+        if (e < SE) {
+            float *dst = lut + b * BUF;
+            const uint32_t w4[4] = {cb[i].x, cb[i].y, cb[i].z, cb[i].w};
+#pragma unroll
+            for (int pp = 0; pp < 2; pp++) {
+                float t = 0.0f;
+#pragma unroll
+                for (int d = 0; d < 8; d++) t = __builtin_fmaf(xv[pp * 8 + d], cb_f32<X31>(w4[d >> 1], d & 1), t);
+                dst[pp * SE + e] = t;
+            }
+        }
+    };
+    auto load_x = [&](float (&xv)[16], int c) {
+        const float *xc = xst + (c - c0) * 16;
+#pragma unroll
+        for (int k = 0; k < 16; k++) xv[k] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(xc[k])));
+    };
+
+    Word<F::SB> wd[LUT_PPW];
+#pragma unroll
+    for (int q = 0; q < LUT_PPW; q++) wd[q].load(cp[q] + (size_t)(2 * c0) * 64 * F::SB);
+    float acc[LUT_PPW][4];
+#pragma unroll
+    for (int q = 0; q < LUT_PPW; q++)
+#pragma unroll
+        for (int t = 0; t < 4; t++) acc[q][t] = 0.0f;
+
+    float xv[16];
+    __syncthreads();
+    load_x(xv, c0);
+#pragma unroll
+    for (int i = 0; i < EPL; i++) build_entry(xv, 0, i);
+    load_x(xv, c0 + 1 < c1 ? c0 + 1 : c0);
+    __syncthreads();
+    for (int c = c0; c < c1; c++) {
+        const int b = (c - c0) & 1;
+        const bool more = c + 1 < c1;              // uniform
+        const int cn = more ? c + 1 : c;
+        const float *L = lut + b * BUF + pl * SE;
+        // an empty asm makes the fp16 codebook words look new each chunk, so
+        // their conversions stay fused into v_fma_mix instead of being
+        // hoisted out of the loop as 64 live f32 values
+#pragma unroll
+        for (int i = 0; i < EPL; i++) asm volatile("" : "+v"(cb[i].x), "+v"(cb[i].y), "+v"(cb[i].z), "+v"(cb[i].w));
+        // Each pair step also builds a share of the next chunk's table, so
+        // every wave interleaves table FMAs with its lookups.
+#pragma unroll
+        for (int q = 0; q < LUT_PPW; q++) {
+            if (more) {
+#pragma unroll
+                for (int i = q; i < EPL; i += LUT_PPW) build_entry(xv, b ^ 1, i);
+            }
+            const Word<F::SB> w = wd[q];
+            wd[q].load(cp[q] + (size_t)(2 * cn) * 64 * F::SB);
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const unsigned sl = w.slot(t);
+                float v = L[lut_code<FMT>(sl, 0)];
+#pragma unroll
+                for (int s = 1; s < F::S; s++) v += L[s * F::E + lut_code<FMT>(sl, s)];
+                acc[q][t] += v;
+            }
+        }
+        if (more) load_x(xv, c + 2 < c1 ? c + 2 : c + 1);
+        __syncthreads();
+    }
+
+    // even + odd positions, one partial per row of this split
+    float *po = a.part + ((size_t)blockIdx.y * a.splits + split) * a.max_jobs * nrb * 64;
+#pragma unroll
+    for (int q = 0; q < LUT_PPW; q++) {
+        float v[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) v[t] = acc[q][t] + __shfl_xor(acc[q][t], 16);
+        const int fb = fb0 + 2 * (q * LUT_NW + wave) + rbsel;
+        if (pl == 0 && fb < fb_end) *(float4 *)(po + fb * 64 + 4 * quad) = make_float4(v[0], v[1], v[2], v[3]);
+    }
+}
+
+extern "C" int wk_lut_plan(int M, int N, int max_jobs, int nkinds, int shared_x, int target_blocks,
+                           size_t cap_floats, int *groups_out, int *splits_out) {
+    if (M <= 0 || N <= 0 || (N % 16) || max_jobs <= 0 || nkinds < 1 || nkinds > 3) return -1;
+    const long nrb = (M + 63) / 64, nc = N / 16;
+    const long groups = shared_x ? ((long)max_jobs * nrb + LUT_RBG - 1) / LUT_RBG
+                                 : (long)max_jobs * ((nrb + LUT_RBG - 1) / LUT_RBG);
+    const long gt = groups * nkinds;
+    long splits = target_blocks > gt ? target_blocks / gt : 1;
+    if (splits > nc) splits = nc;
+    if (splits < (nc + LUT_XCH - 1) / LUT_XCH) splits = (nc + LUT_XCH - 1) / LUT_XCH;   // x stash
+    while (splits > (nc + LUT_XCH - 1) / LUT_XCH && (size_t)nkinds * splits * max_jobs * nrb * 64 > cap_floats)
+        splits--;
+    if ((size_t)nkinds * splits * max_jobs * nrb * 64 > cap_floats) return -1;
+    if (groups * splits > 0x7fffffffL) return -1;
+    if (groups_out) *groups_out = (int)groups;
+    if (splits_out) *splits_out = (int)splits;
+    return 0;
+}
+
+template <int FMT, bool X31>
+static int launch_lut(const LutArgs &a, int groups, int nkinds, void *stream) {
+    typedef FmtT<FMT> F;
+    const size_t lds = ((size_t)2 * 2 * F::S * F::E + LUT_XCH * 16) * sizeof(float);
+    if (lds > 163840) return -2;
+    static bool attr = false;
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute((const void *)k_vq_lut<FMT, X31>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return -(int)e - 1000;
+        attr = true;
+    }
+    hipLaunchKernelGGL((k_vq_lut<FMT, X31>), dim3(groups * a.splits, nkinds), dim3(LUT_NW * 64), lds,
+                       (hipStream_t)stream, a);
+    CHECK_LAUNCH();
+    return 0;
+}
+
+template <int FMT>
+static int launch_lut_x(const LutArgs &a, int groups, int nkinds, int x31, void *stream) {
+    return x31 ? launch_lut<FMT, true>(a, groups, nkinds, stream) : launch_lut<FMT, false>(a, groups, nkinds, stream);
+}
+
+extern "C" int wk_vq_lut(int fmt, const warp_job *jobs, const int *njobs, int max_jobs, int kind_lo, int nkinds,
+                         const uint16_t *books, int books_x31, const float *x, int shared_x, float *part,
+                         size_t cap_floats, int M, int N, int target_blocks, int *splits_out, void *stream) {
+    if (kind_lo < 0 || kind_lo + nkinds > 3 || !books || !part) return -1;
+    int groups, splits;
+    if (wk_lut_plan(M, N, max_jobs, nkinds, shared_x, target_blocks, cap_floats, &groups, &splits)) return -1;
+    LutArgs a;
+    a.jobs = jobs;
+    a.njobs = njobs;
+    a.max_jobs = max_jobs;
+    a.kind_lo = kind_lo;
+    a.books = books;
+    a.x = x;
+    a.part = part;
+    a.M = M;
+    a.N = N;
+    a.splits = splits;
+    a.shared_x = shared_x;
+    if (splits_out) *splits_out = splits;
+    switch (fmt) {
+    case WARP_FMT_VQ3R: return launch_lut_x<WARP_FMT_VQ3R>(a, groups, nkinds, books_x31, stream);
+    case WARP_FMT_VQ2R: return launch_lut_x<WARP_FMT_VQ2R>(a, groups, nkinds, books_x31, stream);
+    case WARP_FMT_VQ12: return launch_lut_x<WARP_FMT_VQ12>(a, groups, nkinds, books_x31, stream);
+    }
+    return -1;
+}
+
+// Sum of a row's partials over the splits, in split order.
+__device__ __forceinline__ float lut_rowsum(const float *p, int splits, size_t stride) {
+    float v = 0.0f;
+    int s = 0;
+    for (; s + 4 <= splits; s += 4) {
+        const float a0 = p[(size_t)s * stride], a1 = p[(size_t)(s + 1) * stride];
+        const float a2 = p[(size_t)(s + 2) * stride], a3 = p[(size_t)(s + 3) * stride];
+        v += a0;
+        v += a1;
+        v += a2;
+        v += a3;
+    }
+    for (; s < splits; s++) v += p[(size_t)s * stride];
+    return v;
+}
+
+// y_kind[yi][r] = (sum of the partials) * row scale, for every job of each kind.
+__global__ __launch_bounds__(256) void k_lut_reduce(const warp_job *__restrict__ jobs, const int *__restrict__ njobs,
+                                                    int max_jobs, int kind_lo, const float *__restrict__ part,
+                                                    int splits, int M, float *y0, float *y1, float *y2) {
+    const int kk = blockIdx.z, kind = kind_lo + kk, j = blockIdx.y, r = blockIdx.x * 256 + threadIdx.x;
+    if (j >= njobs[kind] || r >= M) return;
+    const size_t nrows = (size_t)((M + 63) >> 6) * 64, stride = (size_t)max_jobs * nrows;
+    const warp_job &jb = jobs[(size_t)kind * max_jobs + j];
+    const float v = lut_rowsum(part + (size_t)kk * splits * stride + (size_t)j * nrows + r, splits, stride);
+    float *y = kind == 0 ? y0 : kind == 1 ? y1 : y2;
+    y[(size_t)jb.yi[0] * M + r] = v * f16_keep(jb.scale[r]);
+}
+
+extern "C" int wk_lut_reduce(const warp_job *jobs, const int *njobs, int max_jobs, int kind_lo, int nkinds,
+                             const float *part, int splits, int M, float *const *y, void *stream) {
+    if (M <= 0 || max_jobs <= 0 || splits <= 0 || kind_lo < 0 || nkinds < 1 || kind_lo + nkinds > 3) return -1;
+    hipLaunchKernelGGL(k_lut_reduce, dim3((M + 255) / 256, max_jobs, nkinds), dim3(256), 0, (hipStream_t)stream, jobs,
+                       njobs, max_jobs, kind_lo, part, splits, M, y[0], y[1], y[2]);
+    CHECK_LAUNCH();
+    return 0;
+}
+
+// Decode: gate and up partials (kinds 0 and 1 of one k_vq_lut launch) ->
+// h[yi][r] = act(gate, up), in f32 (the input of the down table).
+__global__ __launch_bounds__(256) void k_act_lut(const warp_job *__restrict__ jobs, const int *__restrict__ njobs,
+                                                 int max_jobs, const float *__restrict__ part, int splits, int I,
+                                                 int situ, float beta, float lbeta, float *__restrict__ h) {
+    const int j = blockIdx.y, r = blockIdx.x * 256 + threadIdx.x;
+    if (j >= njobs[0] || r >= I) return;
+    const size_t nrows = (size_t)((I + 63) >> 6) * 64, stride = (size_t)max_jobs * nrows;
+    const warp_job &jg = jobs[j], &ju = jobs[(size_t)max_jobs + j];
+    const float g = lut_rowsum(part + (size_t)j * nrows + r, splits, stride) * f16_keep(jg.scale[r]);
+    const float u = lut_rowsum(part + (size_t)splits * stride + (size_t)j * nrows + r, splits, stride) *
+                    f16_keep(ju.scale[r]);
+    h[(size_t)jg.yi[0] * I + r] = act_pair(g, u, situ, beta, lbeta);
+}
+
+extern "C" int wk_act_lut(const warp_job *jobs, const int *njobs, int max_jobs, const float *part, int splits, int I,
+                          int act_situ, float beta, float lbeta, float *h, void *stream) {
+    if (I <= 0 || max_jobs <= 0 || splits <= 0) return -1;
+    hipLaunchKernelGGL(k_act_lut, dim3((I + 255) / 256, max_jobs), dim3(256), 0, (hipStream_t)stream, jobs, njobs,
+                       max_jobs, part, splits, I, act_situ, beta, lbeta, h);
+    CHECK_LAUNCH();
+    return 0;
+}
+
+// Decode: down partials -> out[r] = sum_j w[j] * y_j[r] in selection order
+// (unfused, as k_combine), + add0 + add1. One block per 64 rows: the K
+// expert outputs of those rows are reduced in parallel into LDS, then one
+// thread per row combines them in order.
+__global__ __launch_bounds__(256) void k_combine_lut(const warp_job *__restrict__ jobs2, const float *__restrict__ part,
+                                                     int splits, int max_jobs, const float *__restrict__ w, int K,
+                                                     int H, const float *add0, const float *add1,
+                                                     const int *missing, float *__restrict__ out) {
+    __shared__ float yd[WARP_MAX_K][64];
+    const int r0 = blockIdx.x * 64, row = threadIdx.x & 63, jq = threadIdx.x >> 6;
+    const bool miss = missing && *missing;
+    const size_t nrows = (size_t)((H + 63) >> 6) * 64, stride = (size_t)max_jobs * nrows;
+    if (!miss && r0 + row < H)
+        for (int j = jq; j < K; j += 4)
+            yd[j][row] = lut_rowsum(part + (size_t)j * nrows + r0 + row, splits, stride) *
+                         f16_keep(jobs2[j].scale[r0 + row]);
+    __syncthreads();
+    if (jq != 0 || r0 + row >= H) return;
+    const int i = r0 + row;
+    if (miss) {                         // a selected expert was not computed
+        out[i] = __builtin_nanf("");
+        return;
+    }
+    float s = 0.0f;
+    for (int j = 0; j < K; j++) s = __fadd_rn(s, __fmul_rn(w[j], yd[j][row]));
+    if (add0) s = __fadd_rn(s, add0[i]);
+    if (add1) s = __fadd_rn(s, add1[i]);
+    out[i] = s;
+}
+
+extern "C" int wk_combine_lut(const warp_job *jobs2, const float *part, int splits, int max_jobs, const float *w,
+                              int K, int H, const float *add0, const float *add1, const int *missing, float *out,
+                              void *stream) {
+    if (K <= 0 || K > WARP_MAX_K || H <= 0 || splits <= 0 || K > max_jobs) return -1;
+    hipLaunchKernelGGL(k_combine_lut, dim3((H + 63) / 64), dim3(256), 0, (hipStream_t)stream, jobs2, part, splits,
+                       max_jobs, w, K, H, add0, add1, missing, out);
+    CHECK_LAUNCH();
+    return 0;
 }
 
 // ---- decoded weights ------------------------------------------------------------------

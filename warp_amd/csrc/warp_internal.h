@@ -94,6 +94,32 @@ int wk_vq_matvec(int fmt, const warp_job *jobs, const int *njobs, int max_jobs,
                  const float *xscale, float *const *y, int M, int N, int tokens_per_job,
                  void *stream);
 
+/* The LUT matvec (decode, one input per job): for each kind
+ * kind_lo..kind_lo+nkinds-1, every job's rows against the f32 input
+ * x + xi[0] * N, as per-split partial sums part[kind - kind_lo][split]
+ * [job][nrb * 64]. books: the layer's fp16 codebooks (flushed);
+ * books_x31 = 1 when they hold exponent-31 values, which the reference
+ * converts to finite floats (a slower exact conversion). shared_x = 1 when all
+ * jobs of a list read the same input (row groups then span jobs).
+ * cap_floats bounds part; target_blocks is the CU count. *splits_out gets
+ * the split count the consumers must be given. N % 16 == 0. */
+int wk_lut_plan(int M, int N, int max_jobs, int nkinds, int shared_x, int target_blocks,
+                size_t cap_floats, int *groups_out, int *splits_out);
+int wk_vq_lut(int fmt, const warp_job *jobs, const int *njobs, int max_jobs, int kind_lo,
+              int nkinds, const uint16_t *books, int books_x31, const float *x, int shared_x, float *part,
+              size_t cap_floats, int M, int N, int target_blocks, int *splits_out, void *stream);
+/* y[k][yi][r] = (sum over splits) * row scale, for the kinds of one LUT launch. */
+int wk_lut_reduce(const warp_job *jobs, const int *njobs, int max_jobs, int kind_lo, int nkinds,
+                  const float *part, int splits, int M, float *const *y, void *stream);
+/* Decode: gate/up partials (one launch over kinds 0 and 1) -> h [yi][I] = act(g, u). */
+int wk_act_lut(const warp_job *jobs, const int *njobs, int max_jobs, const float *part, int splits,
+               int I, int act_situ, float beta, float lbeta, float *h, void *stream);
+/* Decode: down partials -> out [H] = sum_j w[j] * y_j in j order, + add0 + add1;
+ * NaN everywhere when *missing is set. jobs2: the down job list. */
+int wk_combine_lut(const warp_job *jobs2, const float *part, int splits, int max_jobs,
+                   const float *w, int K, int H, const float *add0, const float *add1,
+                   const int *missing, float *out, void *stream);
+
 /* Decoded weights of one matrix, bit for bit the reference's closed form
  * (stage sum in fp32 from stage 0, then times the subnormal-keeping fp16
  * row scale). books: fp16 [stages][entries][8] of this kind. W [M][N]. */

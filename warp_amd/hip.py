@@ -85,6 +85,7 @@ SIGNATURES = {
     "warp_hip_resident": (C.c_void_p, [C.c_void_p, C.c_int, C.c_int]),
     "warp_hip_put_expert_dev": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p]),
     "warp_hip_put_expert_synth": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_uint64, C.c_void_p]),
+    "warp_hip_set_matvec_path": (C.c_int, [C.c_void_p, C.c_int]),
     "warp_hip_set_timing": (C.c_int, [C.c_void_p, C.c_int]),
     "warp_hip_get_timing": (C.c_int, [C.c_void_p, C.POINTER(C.c_double), C.POINTER(C.c_uint64)]),
     "warp_hip_sync": (C.c_int, [C.c_void_p]),
@@ -268,6 +269,11 @@ class Context:
 
     def put_expert_synth(self, layer, expert, seed, scales_u16):
         self._check(lib().warp_hip_put_expert_synth(self.h, layer, expert, seed, _addr(scales_u16)))
+
+    def set_matvec_path(self, path):
+        """"auto" (LUT kernel for decode where it applies) or "mfma"."""
+        code = {"auto": 0, "mfma": 1}[path]
+        self._check(lib().warp_hip_set_matvec_path(self.h, code))
 
     def set_timing(self, on):
         self._check(lib().warp_hip_set_timing(self.h, int(on)))
