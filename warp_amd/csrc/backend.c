@@ -242,7 +242,7 @@ struct warp_hip_ctx {
     uint32_t *hits;
     uint64_t *last, clock;
     unsigned rng;
-    const uint8_t **table_dev;
+    warp_slot *table_dev;       /* [layer][expert] residency and offsets  */
     uint8_t *staging;           /* pinned, N_STAGE records                 */
     int stage_next, stage_used[N_STAGE];
     warp_hip_fetch_fn fetch;
@@ -411,8 +411,8 @@ static int ctx_alloc(warp_hip_ctx *c)
         return set_err(c, WARP_HIP_E_NOMEM, -1, -1, "host allocation failed");
     for (size_t i = 0; i < nkeys; i++) c->key_slot[i] = -1;
     for (int i = 0; i < c->n_slots; i++) c->slot_key[i] = -1;
-    DMALLOC(c, c->table_dev, nkeys * sizeof(void *));
-    DEV(c, hipMemset(c->table_dev, 0, nkeys * sizeof(void *)));
+    DMALLOC(c, c->table_dev, nkeys * sizeof(warp_slot));
+    DEV(c, hipMemset(c->table_dev, 0, nkeys * sizeof(warp_slot)));
     if (c->n_slots > 0) DMALLOC(c, c->pool, (size_t)c->n_slots * g->rec_bytes);
     DEV(c, hipHostMalloc((void **)&c->staging, (size_t)N_STAGE * g->rec_bytes, 0));
     return 0;
@@ -750,7 +750,8 @@ static int claim_slot(warp_hip_ctx *c, int layer, int expert)
         c->key_slot[old] = -1;
         c->L[old / E].resident--;
         c->stats.evictions++;
-        if (wk_set_ptr(c->table_dev + old, NULL, c->cp))
+        static const uint32_t none[4] = { 0, 0, 0, 0 };
+        if (wk_set_slot(c->table_dev + old, NULL, none, c->cp))
             return set_err(c, WARP_HIP_E_DEVICE, layer, expert, "table update");
     }
     c->slot_key[s] = key;
@@ -761,10 +762,13 @@ static int claim_slot(warp_hip_ctx *c, int layer, int expert)
     return s;
 }
 
-static int publish_slot(warp_hip_ctx *c, int layer, int expert, int s)
+/* hdr: a host copy of the record's (checked) header */
+static int publish_slot(warp_hip_ctx *c, int layer, int expert, int s, const uint8_t *hdr)
 {
     const int key = layer * c->cfg.n_experts + expert;
-    if (wk_set_ptr(c->table_dev + key, c->pool + (size_t)s * c->cfg.rec_bytes, c->cp))
+    uint32_t off[4];
+    memcpy(off, hdr + WARP_HDR_GATE_OFF, sizeof off);
+    if (wk_set_slot(c->table_dev + key, c->pool + (size_t)s * c->cfg.rec_bytes, off, c->cp))
         return set_err(c, WARP_HIP_E_DEVICE, layer, expert, "table update");
     DEV(c, hipEventRecord(c->ev_copy, c->cp));
     c->copy_pending = 1;
@@ -787,7 +791,7 @@ int warp_hip_put_expert(warp_hip_ctx *c, int layer, int expert, const uint8_t *r
     DEV(c, hipStreamWaitEvent(c->cp, c->ev_before, 0));
     DEV(c, hipMemcpyAsync(c->pool + (size_t)s * c->cfg.rec_bytes, rec, c->cfg.rec_bytes, hipMemcpyHostToDevice, c->cp));
     DEV(c, hipStreamSynchronize(c->cp));
-    return publish_slot(c, layer, expert, s);
+    return publish_slot(c, layer, expert, s, rec);
 }
 
 int warp_hip_put_expert_dev(warp_hip_ctx *c, int layer, int expert, const uint8_t *rec_dev)
@@ -817,7 +821,7 @@ int warp_hip_put_expert_dev(warp_hip_ctx *c, int layer, int expert, const uint8_
         c->L[layer].resident--;
         return rc;
     }
-    return publish_slot(c, layer, expert, s);
+    return publish_slot(c, layer, expert, s, hdr);
 }
 
 int warp_hip_put_expert_synth(warp_hip_ctx *c, int layer, int expert, uint64_t seed, const uint16_t *scales)
@@ -855,7 +859,7 @@ int warp_hip_put_expert_synth(warp_hip_ctx *c, int layer, int expert, uint64_t s
     DEV(c, hipMemcpyAsync(slot, hdr, sizeof hdr, hipMemcpyHostToDevice, c->cp));
     DEV(c, hipMemcpyAsync(slot + off[3], scales, 2 * (2 * (size_t)g->inter + g->hidden), hipMemcpyHostToDevice, c->cp));
     DEV(c, hipStreamSynchronize(c->cp));
-    return publish_slot(c, layer, expert, s);
+    return publish_slot(c, layer, expert, s, hdr);
 }
 
 const uint8_t *warp_hip_resident(warp_hip_ctx *c, int layer, int expert)
@@ -906,7 +910,7 @@ static int fill_from_fetch(warp_hip_ctx *c, int layer, int expert, hipEvent_t af
     DEV(c, hipEventRecord(c->ev_stage[i], c->cp));
     c->stage_used[i] = 1;
     c->stats.bytes_read += c->cfg.rec_bytes;
-    return publish_slot(c, layer, expert, s);
+    return publish_slot(c, layer, expert, s, dst);
 }
 
 static int prefetch_after(warp_hip_ctx *c, int layer, const int *ids, int n, hipEvent_t after)
@@ -1112,7 +1116,7 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
     const int E = g->n_experts, K = g->top_k, H = g->hidden, I = g->inter;
     if (!L->has_books || (!L->router && !L->rq))
         return set_err(c, WARP_HIP_E_ARG, layer, -1, "layer %d has no codebooks or router", layer);
-    const uint8_t *const *table = c->table_dev + (size_t)layer * E;
+    const warp_slot *table = c->table_dev + (size_t)layer * E;
     const int use_lut = c->lut_ok && c->mv_path == WARP_HIP_PATH_AUTO && L->books;
 
     /* inputs for the gate/up matvecs, then the router */
@@ -1234,7 +1238,7 @@ int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *ou
     if (T < 1 || T > g->max_tokens) return set_err(c, WARP_HIP_E_ARG, layer, -1, "T = %d, max_tokens = %d", T, g->max_tokens);
     if (!L->has_books || (!L->router && !L->rq))
         return set_err(c, WARP_HIP_E_ARG, layer, -1, "layer %d has no codebooks or router", layer);
-    const uint8_t *const *table = c->table_dev + (size_t)layer * E;
+    const warp_slot *table = c->table_dev + (size_t)layer * E;
     const int P = T * K;
 
     KRN(c, logits_of(c, L, X_dev, T, c->logits, c->st));

@@ -264,13 +264,13 @@ extern "C" int wk_mvq(const int8_t *W, const uint16_t *ws, size_t rowbytes, int 
 
 // ---- jobs -----------------------------------------------------------------------------
 
-// Pointers of one matrix inside a record (header fields of waste_expert_hdr,
-// src/waste_format.h:98-130). Row scales are gate [I], up [I], down [H].
-__device__ __forceinline__ void job_ptrs(warp_job &jb, const uint8_t *rec, int kind, int inter) {
-    const uint32_t *h = (const uint32_t *)rec;
-    jb.idx = rec + h[WARP_HDR_GATE_OFF / 4 + kind];
+// Pointers of one matrix inside a record, from the header offsets the table
+// holds (waste_expert_hdr, src/waste_format.h:98-130). Row scales are gate
+// [I], up [I], down [H].
+__device__ __forceinline__ void job_ptrs(warp_job &jb, const warp_slot &sl, int kind, int inter) {
+    jb.idx = sl.rec + sl.off[kind];
     const int soff = kind == 0 ? 0 : kind == 1 ? inter : 2 * inter;
-    jb.scale = (const uint16_t *)(rec + h[WARP_HDR_CORR_OFF / 4]) + soff;
+    jb.scale = (const uint16_t *)(sl.rec + sl.off[3]) + soff;
 }
 
 // ---- routing -----------------------------------------------------------------------
@@ -282,7 +282,7 @@ __device__ __forceinline__ void job_ptrs(warp_job &jb, const uint8_t *rec, int k
 __global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits, const float *__restrict__ bias,
                                                int E, int K, int act, int renorm, float routed_scale,
                                                int *__restrict__ idx, float *__restrict__ w,
-                                               const uint8_t *const *__restrict__ table, warp_job *__restrict__ jobs,
+                                               const warp_slot *__restrict__ table, warp_job *__restrict__ jobs,
                                                int *__restrict__ njobs, int *__restrict__ missing, int inter) {
     extern __shared__ float lds_route[];
     float *score = lds_route;             // [E]
@@ -352,13 +352,133 @@ __global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits,
         __syncthreads();
         int miss = 0;
         for (int j = tid; j < K; j += 256) {
-            const uint8_t *rec = table[sel[j]];
-            miss |= rec == nullptr;
+            const warp_slot sl = table[sel[j]];
+            miss |= sl.rec == nullptr;
             for (int kind = 0; kind < 3; kind++) {
                 warp_job jb;
                 jb.idx = nullptr;
                 jb.scale = nullptr;
-                if (rec) job_ptrs(jb, rec, kind, inter);
+                if (sl.rec) job_ptrs(jb, sl, kind, inter);
+                jb.n = 1;
+                jb.rsv = 0;
+                for (int s = 0; s < WARP_TPJ; s++) { jb.xi[s] = 0; jb.yi[s] = 0; }
+                jb.xi[0] = kind == 2 ? j : 0;
+                jb.yi[0] = j;
+                jobs[kind * K + j] = jb;
+            }
+        }
+        miss = __syncthreads_or(miss);
+        if (tid == 0) {
+            for (int kind = 0; kind < 3; kind++) njobs[kind] = miss ? 0 : K;
+            if (miss) *missing = 1;
+        }
+    }
+}
+
+// Decode routing (one token). The logits, the bias and this layer's expert
+// table go to LDS in one pass of independent loads; one wave then takes the
+// K picks by repeated arg-max -- larger biased score first, the lower id on
+// equal scores, never a value at or below -1e30: the reference's scan
+// (src/model.c:2727-2739) -- each lane keeping the best of its own ids and
+// rescanning them only when that best is taken. The job lists are then
+// written from the table in LDS, with no dependent reads of HBM.
+__global__ __launch_bounds__(256) void k_route1(const float *__restrict__ logits, const float *__restrict__ bias,
+                                                int E, int K, int act, int renorm, float routed_scale,
+                                                int *__restrict__ idx, float *__restrict__ w,
+                                                const warp_slot *__restrict__ table, int table_lds,
+                                                warp_job *__restrict__ jobs, int *__restrict__ njobs,
+                                                int *__restrict__ missing, int inter) {
+    extern __shared__ __attribute__((aligned(16))) float lds_r1[];
+    float *score = lds_r1;                                     // [E]
+    float *biased = lds_r1 + E;                                // [E]
+    warp_slot *slots = (warp_slot *)(lds_r1 + 2 * ((E + 1) & ~1));   // [E] when table_lds
+    __shared__ int sel[WARP_MAX_K];
+    __shared__ float wsel[WARP_MAX_K];
+    __shared__ float red[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int e = tid; e < E; e += 256) {
+        score[e] = logits[e];
+        biased[e] = bias ? bias[e] : 0.0f;
+    }
+    if (table && table_lds)
+        for (int e = tid; e < E; e += 256) slots[e] = table[e];
+    if (tid < WARP_MAX_K) { sel[tid] = 0; wsel[tid] = 0.0f; }
+    __syncthreads();
+    if (act == 1) {
+        float mx = -INFINITY;
+        for (int e = tid; e < E; e += 256) mx = fmaxf(mx, score[e]);
+        mx = wave_max(mx);
+        if (lane == 0) red[wave] = mx;
+        __syncthreads();
+        mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        for (int e = tid; e < E; e += 256) score[e] = exp_cr(__fsub_rn(score[e], mx));
+        __syncthreads();
+        if (tid == 0) {
+            float s = 0.0f;                   // sequential, as the reference sums
+            for (int e = 0; e < E; e++) s = __fadd_rn(s, score[e]);
+            red[0] = s;
+        }
+        __syncthreads();
+        const float s = red[0];
+        for (int e = tid; e < E; e += 256) score[e] = __fdiv_rn(score[e], s);
+    } else {
+        for (int e = tid; e < E; e += 256) score[e] = __fdiv_rn(1.0f, __fadd_rn(1.0f, exp_cr(-score[e])));
+    }
+    for (int e = tid; e < E; e += 256) biased[e] = __fadd_rn(score[e], biased[e]);
+    __syncthreads();
+    if (wave == 0) {
+        float bv = -1e30f;
+        int be = 0x7fffffff;
+        for (int e = lane; e < E; e += 64) {
+            const float v = biased[e];
+            if (v > bv) { bv = v; be = e; }
+        }
+        for (int j = 0; j < K; j++) {
+            float v = bv;
+            int e = be;
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+                const float ov = __shfl_xor(v, o);
+                const int oe = __shfl_xor(e, o);
+                if (ov > v || (ov == v && oe < e)) { v = ov; e = oe; }
+            }
+            if (e == 0x7fffffff) break;       // nothing above -1e30 is left (uniform)
+            if (lane == 0) { sel[j] = e; wsel[j] = score[e]; }
+            if ((e & 63) == lane) {           // the owner of the pick rescans its ids
+                biased[e] = -INFINITY;
+                bv = -1e30f;
+                be = 0x7fffffff;
+                for (int q = lane; q < E; q += 64) {
+                    const float x = biased[q];
+                    if (x > bv) { bv = x; be = q; }
+                }
+            }
+        }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        if (renorm && K > 1) {
+            float s = 0.0f;
+            for (int j = 0; j < K; j++) s = __fadd_rn(s, wsel[j]);
+            const float d = __fadd_rn(s, 1e-20f);
+            for (int j = 0; j < K; j++) wsel[j] = __fdiv_rn(wsel[j], d);
+        }
+        for (int j = 0; j < K; j++) {
+            wsel[j] = __fmul_rn(wsel[j], routed_scale);
+            idx[j] = sel[j];
+            w[j] = wsel[j];
+        }
+    }
+    if (table) {
+        int miss = 0;
+        for (int j = tid; j < K; j += 256) {
+            const warp_slot sl = table_lds ? slots[sel[j]] : table[sel[j]];
+            miss |= sl.rec == nullptr;
+            for (int kind = 0; kind < 3; kind++) {
+                warp_job jb;
+                jb.idx = nullptr;
+                jb.scale = nullptr;
+                if (sl.rec) job_ptrs(jb, sl, kind, inter);
                 jb.n = 1;
                 jb.rsv = 0;
                 for (int s = 0; s < WARP_TPJ; s++) { jb.xi[s] = 0; jb.yi[s] = 0; }
@@ -376,10 +496,19 @@ __global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits,
 }
 
 extern "C" int wk_route(const float *logits, const float *bias, int E, int K, int T, int act, int renorm,
-                        float routed_scale, int *idx, float *w, const uint8_t *const *table, warp_job *jobs,
+                        float routed_scale, int *idx, float *w, const warp_slot *table, warp_job *jobs,
                         int *njobs, int *missing, int inter, void *stream) {
     if (E <= 0 || K <= 0 || K > WARP_MAX_K || K > E || T <= 0 || E > 8192) return -1;
     if (table && T != 1) return -1;
+    if (T == 1) {
+        // the table is staged in LDS up to 2048 experts (48 KiB)
+        const int tl = table && E <= 2048;
+        const size_t lds = (size_t)2 * ((E + 1) & ~1) * sizeof(float) + (tl ? (size_t)E * sizeof(warp_slot) : 0);
+        hipLaunchKernelGGL(k_route1, dim3(1), dim3(256), lds, (hipStream_t)stream, logits, bias, E, K, act, renorm,
+                           routed_scale, idx, w, table, tl, jobs, njobs, missing, inter);
+        CHECK_LAUNCH();
+        return 0;
+    }
     hipLaunchKernelGGL(k_route, dim3(T), dim3(256), (size_t)E * 2 * sizeof(float), (hipStream_t)stream, logits,
                        bias, E, K, act, renorm, routed_scale, idx, w, table, jobs, njobs, missing, inter);
     CHECK_LAUNCH();
@@ -690,24 +819,36 @@ extern "C" int wk_vq_matvec(int fmt, const warp_job *jobs, const int *njobs, int
 //
 // The reference's own algorithm (src/model.c:1843-2024), laid out for LDS:
 // for every vector position p the table LUT[s][c] = dot(codebook_s[c], x[8p..8p+8])
-// is built with the fused, d-ascending chain of the reference's AVX-512 build
-// (so every entry is bit-identical to the reference's), and each row sums
-// LUT[0][code0] + LUT[1][code1] (+ LUT[2][code2]) over its positions. A random
-// 4-byte LDS read costs about what a random 16-byte codebook gather does, and
-// replaces a gather plus 16 multiply-adds, so the table wins whenever it is
-// amortised over enough rows.
+// is built, and each row sums LUT[0][code0] + LUT[1][code1] (+ LUT[2][code2])
+// over its positions, in that order per position as the reference does. A
+// random 4-byte LDS read costs about what a random 16-byte codebook gather
+// does and replaces a gather plus 16 multiply-adds, so the table wins
+// whenever it is amortised over enough rows.
 //
 // Block = 16 waves, one per CU. A block owns a row group (64 pairs of 64-row
 // blocks = 8192 rows, round-robin over the waves; across the jobs of a list
 // when they share one input, within one job otherwise) and a split of the
 // positions, which it walks 2 positions at a time: the table of the next 2
 // positions (2 x S x E floats) is built into one LDS buffer while the rows are
-// summed from the other. The codebook of the block's kind sits in registers
-// (fp32, 8 entries per lane for 2 x 4096). A lane sums 4 rows of one row block
-// at one position parity; the two parities are added at the end and the block
-// writes one partial sum per row and split. The splits are added in order by
-// the consumer (k_lut_reduce, k_act_lut, k_combine_lut), so results are
-// deterministic.
+// summed from the other, each pair step of a wave doing a share of the build.
+// A lane sums 4 rows of one row block at one position parity; the two
+// parities are added at the end and the block writes one partial sum per row
+// and split. The splits are added in order by the consumer (k_lut_reduce,
+// k_act_lut, k_combine_lut), so results are deterministic.
+//
+// Table build. The codebook of the block's kind sits in registers (fp16, one
+// 64-entry group per 64 lanes, 8 groups per wave for 2 x 4096). The build runs
+// on the matrix cores: in v_mfma_f32_4x4x4_16b_f16 each lane's entry is one
+// column of B (block = 4 lanes = 4 codes), and A holds the split's x scaled
+// by 2^ks and split into fp16 hi and lo halves (x*2^ks = hi + lo to ~22
+// bits), with the two positions as rows and (dims, hi/lo) as K: four MFMAs
+// give sum_d cb[d] * (hi[d] + lo[d]), exact products summed in fp32, and
+// every lane ends with both positions of its own entry, which it stores as
+// one 8-byte pair (a wave writes 512 contiguous bytes, no bank conflicts).
+// The row sums carry the factor 2^ks, removed exactly at the end. Layers whose
+// codebooks hold exponent-31 values (finite in the reference, inf for the
+// matrix cores) take the X31 variant: the reference's fused d-ascending chain
+// on the vector ALUs from f32 x, bit-identical to its table entries.
 
 constexpr int LUT_NW = 16;                 // waves per block
 constexpr int LUT_PPW = 4;                 // row-block pairs per wave
@@ -731,25 +872,21 @@ __device__ __forceinline__ unsigned lut_code(unsigned slot, int s) {
     return (slot >> (8 * s)) & 0xFFu;
 }
 
-// fp16 codebook element -> f32 as the reference converts it. X31 = false:
-// the hardware conversion (exact for every finite fp16; the flushed books
-// hold no subnormals). X31 = true: the reference's rebiasing, which also
-// maps exponent 31 to 2^16..2^17 instead of inf/NaN -- used only for layers
-// whose codebooks hold such values.
-template <bool X31>
-__device__ __forceinline__ float cb_f32(uint32_t packed, int hi) {
-    const uint16_t h = (uint16_t)(hi ? packed >> 16 : packed & 0xFFFFu);
-    if (X31) return f16_flushed(h);
-    return (float)__builtin_bit_cast(_Float16, h);
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ half4 half4_of(uint32_t lo, uint32_t hi) {
+    return __builtin_bit_cast(half4, make_uint2(lo, hi));
 }
 
 template <int FMT, bool X31>
 __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
     typedef FmtT<FMT> F;
     constexpr int SE = F::S * F::E;                        // table entries per position
-    constexpr int EPL = (SE + LUT_NW * 64 - 1) / (LUT_NW * 64);
+    constexpr int NG = SE / 64;                            // 64-entry groups
+    constexpr int GPW = (NG + LUT_NW - 1) / LUT_NW;        // groups per wave
     constexpr int BUF = 2 * SE;                            // floats per buffer
-    extern __shared__ __attribute__((aligned(16))) float lut[];   // [2][2][S][E], then x of the split
+    static_assert(SE % 64 == 0, "table groups");
+    extern __shared__ __attribute__((aligned(16))) float lut[];   // [2][S][E][2], then x of the split
     const int kind = a.kind_lo + blockIdx.y;
     const int nj = a.njobs[kind];
     const warp_job *jobs = a.jobs + (size_t)kind * a.max_jobs;
@@ -786,39 +923,87 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
         cp[q] = jobs[j].idx + ((size_t)rb * nv + pl) * 64 * F::SB + (size_t)quad * 4 * F::SB;
     }
 
-    // this lane's codebook entries (fp16 pairs), e = tid + 1024 i over [stage][entry]
-    uint4 cb[EPL];
+    // codebook: group G = wave * GPW + g holds entries 64 G .. 64 G + 63 over
+    // [stage][entry], entry 64 G + lane in this lane
+    uint4 cb[GPW];
     const uint4 *bk = (const uint4 *)(a.books + (size_t)kind * SE * 8);
 #pragma unroll
-    for (int i = 0; i < EPL; i++) {
-        const int e = threadIdx.x + i * LUT_NW * 64;
-        cb[i] = e < SE ? bk[e] : make_uint4(0u, 0u, 0u, 0u);
+    for (int g = 0; g < GPW; g++) {
+        const int G = wave * GPW + g;
+        cb[g] = G < NG ? bk[G * 64 + lane] : make_uint4(0u, 0u, 0u, 0u);
     }
 
-    // x of this split's positions -> LDS once; the builds read it back as
-    // wave-uniform values (SGPRs), so no vector-memory wait sits in the loop
-    float *xst = lut + 2 * BUF;
-    for (int i = threadIdx.x; i < (c1 - c0) * 16; i += LUT_NW * 64) xst[i] = xin[(size_t)c0 * 16 + i];
+    // x of this split -> LDS: f32 [chunk][16] (X31) or the scaled fp16
+    // halves [chunk][position 2][hi, lo][8]
+    const int nx = (c1 - c0) * 16;
+    const float *xg = xin + (size_t)c0 * 16;
+    int ks = 0;
+    if constexpr (X31) {
+        float *xst = lut + 2 * BUF;
+        for (int i = threadIdx.x; i < nx; i += LUT_NW * 64) xst[i] = xg[i];
+    } else {
+        float m = 0.0f;
+        for (int i = threadIdx.x; i < nx; i += LUT_NW * 64) m = fmaxf(m, fabsf(xg[i]));
+        ks = split_exp(block_absmax(m));
+        _Float16 *xh = (_Float16 *)(lut + 2 * BUF);
+        for (int i = threadIdx.x; i < nx; i += LUT_NW * 64) {
+            const int o = (i >> 4) * 32 + ((i >> 3) & 1) * 16 + (i & 7);
+            split_store(xg[i], ks, &xh[o], &xh[o + 8]);
+        }
+    }
 
-    // table entries e = tid + 1024 i of positions 2c, 2c+1 (inputs xv) into buffer b
-    auto build_entry = [&](const float (&xv)[16], int b, int i) {
-        const int e = threadIdx.x + i * LUT_NW * 64;
-        if (e < SE) {
-            float *dst = lut + b * BUF;
-            const uint32_t w4[4] = {cb[i].x, cb[i].y, cb[i].z, cb[i].w};
+    // A operands (x) of chunk c: row i = lane % 4 is position i (i < 2) or
+    // zero; K runs over (hi dims 0-3, hi 4-7, lo 0-3, lo 4-7)
+    auto load_b = [&](half4 (&B)[4], int c) {
+        const int j = lane & 3;
+        const _Float16 *xh = (const _Float16 *)(lut + 2 * BUF) + (c - c0) * 32 + (j & 1) * 16;
 #pragma unroll
-            for (int pp = 0; pp < 2; pp++) {
-                float t = 0.0f;
+        for (int m = 0; m < 4; m++) {
+            const half4 v = *(const half4 *)(xh + (m >> 1) * 8 + (m & 1) * 4);
+            B[m] = j < 2 ? v : half4{0, 0, 0, 0};
+        }
+    };
+    // this wave's groups g = q, q + PPW, ... of the table into buffer b: x
+    // is A (rows = the 2 positions), this lane's entry the B column, so a
+    // lane gets both positions of its own entry and writes them as a pair
+    auto build_mfma = [&](const half4 (&X)[4], int b, int q) {
 #pragma unroll
-                for (int d = 0; d < 8; d++) t = __builtin_fmaf(xv[pp * 8 + d], cb_f32<X31>(w4[d >> 1], d & 1), t);
-                dst[pp * SE + e] = t;
+        for (int g = q; g < GPW; g += LUT_PPW) {
+            const int G = wave * GPW + g;
+            if (G < NG) {                                  // uniform per wave
+                const half4 clo = half4_of(cb[g].x, cb[g].y), chi = half4_of(cb[g].z, cb[g].w);
+                f4 d = {0.f, 0.f, 0.f, 0.f};
+                d = __builtin_amdgcn_mfma_f32_4x4x4f16(X[0], clo, d, 0, 0, 0);
+                d = __builtin_amdgcn_mfma_f32_4x4x4f16(X[1], chi, d, 0, 0, 0);
+                d = __builtin_amdgcn_mfma_f32_4x4x4f16(X[2], clo, d, 0, 0, 0);
+                d = __builtin_amdgcn_mfma_f32_4x4x4f16(X[3], chi, d, 0, 0, 0);
+                *(float2 *)(lut + b * BUF + (G * 64 + lane) * 2) = make_float2(d[0], d[1]);
             }
         }
     };
     auto load_x = [&](float (&xv)[16], int c) {
-        const float *xc = xst + (c - c0) * 16;
+        const float *xc = lut + 2 * BUF + (c - c0) * 16;
 #pragma unroll
         for (int k = 0; k < 16; k++) xv[k] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(xc[k])));
+    };
+    auto build_valu = [&](const float (&xv)[16], int b, int q) {
+#pragma unroll
+        for (int g = q; g < GPW; g += LUT_PPW) {
+            const int G = wave * GPW + g;
+            if (G < NG) {
+                const uint32_t w4[4] = {cb[g].x, cb[g].y, cb[g].z, cb[g].w};
+                float t[2];
+#pragma unroll
+                for (int pp = 0; pp < 2; pp++) {
+                    t[pp] = 0.0f;
+#pragma unroll
+                    for (int d = 0; d < 8; d++)
+                        t[pp] = __builtin_fmaf(xv[pp * 8 + d], f16_flushed((uint16_t)(w4[d >> 1] >> (16 * (d & 1)))),
+                                               t[pp]);
+                }
+                *(float2 *)(lut + b * BUF + (G * 64 + lane) * 2) = make_float2(t[0], t[1]);
+            }
+        }
     };
 
     Word<F::SB> wd[LUT_PPW];
@@ -830,53 +1015,59 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
 #pragma unroll
         for (int t = 0; t < 4; t++) acc[q][t] = 0.0f;
 
+    half4 B[4];
     float xv[16];
     __syncthreads();
-    load_x(xv, c0);
+    if constexpr (X31) {
+        load_x(xv, c0);
 #pragma unroll
-    for (int i = 0; i < EPL; i++) build_entry(xv, 0, i);
-    load_x(xv, c0 + 1 < c1 ? c0 + 1 : c0);
+        for (int q = 0; q < LUT_PPW; q++) build_valu(xv, 0, q);
+        load_x(xv, c0 + 1 < c1 ? c0 + 1 : c0);
+    } else {
+        load_b(B, c0);
+#pragma unroll
+        for (int q = 0; q < LUT_PPW; q++) build_mfma(B, 0, q);
+    }
     __syncthreads();
     for (int c = c0; c < c1; c++) {
         const int b = (c - c0) & 1;
         const bool more = c + 1 < c1;              // uniform
         const int cn = more ? c + 1 : c;
-        const float *L = lut + b * BUF + pl * SE;
-        // an empty asm makes the fp16 codebook words look new each chunk, so
-        // their conversions stay fused into v_fma_mix instead of being
-        // hoisted out of the loop as 64 live f32 values
-#pragma unroll
-        for (int i = 0; i < EPL; i++) asm volatile("" : "+v"(cb[i].x), "+v"(cb[i].y), "+v"(cb[i].z), "+v"(cb[i].w));
-        // Each pair step also builds a share of the next chunk's table, so
-        // every wave interleaves table FMAs with its lookups.
+        const float *L = lut + b * BUF + pl;
+        if constexpr (!X31) {
+            if (more) load_b(B, c + 1);
+        }
+        // each pair step also builds a share of the next chunk's table
 #pragma unroll
         for (int q = 0; q < LUT_PPW; q++) {
             if (more) {
-#pragma unroll
-                for (int i = q; i < EPL; i += LUT_PPW) build_entry(xv, b ^ 1, i);
+                if constexpr (X31) build_valu(xv, b ^ 1, q);
+                else build_mfma(B, b ^ 1, q);
             }
             const Word<F::SB> w = wd[q];
             wd[q].load(cp[q] + (size_t)(2 * cn) * 64 * F::SB);
 #pragma unroll
             for (int t = 0; t < 4; t++) {
                 const unsigned sl = w.slot(t);
-                float v = L[lut_code<FMT>(sl, 0)];
+                float v = L[lut_code<FMT>(sl, 0) * 2];
 #pragma unroll
-                for (int s = 1; s < F::S; s++) v += L[s * F::E + lut_code<FMT>(sl, s)];
+                for (int s = 1; s < F::S; s++) v += L[(s * F::E + lut_code<FMT>(sl, s)) * 2];
                 acc[q][t] += v;
             }
         }
-        if (more) load_x(xv, c + 2 < c1 ? c + 2 : c + 1);
+        if constexpr (X31) {
+            if (more) load_x(xv, c + 2 < c1 ? c + 2 : c + 1);
+        }
         __syncthreads();
     }
 
-    // even + odd positions, one partial per row of this split
+    // even + odd positions, unscaled: one partial per row of this split
     float *po = a.part + ((size_t)blockIdx.y * a.splits + split) * a.max_jobs * nrb * 64;
 #pragma unroll
     for (int q = 0; q < LUT_PPW; q++) {
         float v[4];
 #pragma unroll
-        for (int t = 0; t < 4; t++) v[t] = acc[q][t] + __shfl_xor(acc[q][t], 16);
+        for (int t = 0; t < 4; t++) v[t] = ldexpf(acc[q][t] + __shfl_xor(acc[q][t], 16), -ks);
         const int fb = fb0 + 2 * (q * LUT_NW + wave) + rbsel;
         if (pl == 0 && fb < fb_end) *(float4 *)(po + fb * 64 + 4 * quad) = make_float4(v[0], v[1], v[2], v[3]);
     }
@@ -1293,7 +1484,7 @@ extern "C" int wk_apply_p6(const warp_job *jobs, const int *njobs, int max_jobs,
 // One block. Counts per expert, exclusive scan, then one thread per expert
 // places its pairs in token order and cuts them into jobs of WARP_TPJ.
 __global__ __launch_bounds__(1024) void k_plan_chunk(const int *__restrict__ idx, const float *__restrict__ w, int T,
-                                                     int K, int E, const uint8_t *const *__restrict__ table,
+                                                     int K, int E, const warp_slot *__restrict__ table,
                                                      int *__restrict__ counts, int *__restrict__ offsets,
                                                      int *__restrict__ pair_tok, int *__restrict__ pair_exp,
                                                      float *__restrict__ pair_w, warp_job *__restrict__ jobs,
@@ -1311,7 +1502,7 @@ __global__ __launch_bounds__(1024) void k_plan_chunk(const int *__restrict__ idx
             offsets[e] = run;
             run += counts[e];
             tiles += (counts[e] + WARP_TPJ - 1) / WARP_TPJ;
-            if (counts[e] && !table[e]) miss = 1;
+            if (counts[e] && !table[e].rec) miss = 1;
         }
         offsets[E] = run;
         s_tiles_total = tiles;
@@ -1356,7 +1547,7 @@ __global__ __launch_bounds__(1024) void k_plan_chunk(const int *__restrict__ idx
     }
 }
 
-extern "C" int wk_plan_chunk(const int *idx, const float *w, int T, int K, int E, const uint8_t *const *table,
+extern "C" int wk_plan_chunk(const int *idx, const float *w, int T, int K, int E, const warp_slot *table,
                              int *counts, int *offsets, int *pair_tok, int *pair_exp, float *pair_w, warp_job *jobs,
                              int max_jobs, int *njobs, int *missing, int inter, void *stream) {
     if (T <= 0 || K <= 0 || E <= 0 || max_jobs <= 0) return -1;
@@ -1432,10 +1623,19 @@ extern "C" int wk_fill_random(uint8_t *p, size_t n, uint64_t seed, void *stream)
     return 0;
 }
 
-__global__ void k_set_ptr(const uint8_t **dst, const uint8_t *val) { *dst = val; }
+__global__ void k_set_slot(warp_slot *dst, const uint8_t *rec, uint32_t o0, uint32_t o1, uint32_t o2, uint32_t o3) {
+    warp_slot v;
+    v.rec = rec;
+    v.off[0] = o0;
+    v.off[1] = o1;
+    v.off[2] = o2;
+    v.off[3] = o3;
+    *dst = v;
+}
 
-extern "C" int wk_set_ptr(const uint8_t **dst, const uint8_t *val, void *stream) {
-    hipLaunchKernelGGL(k_set_ptr, dim3(1), dim3(1), 0, (hipStream_t)stream, dst, val);
+extern "C" int wk_set_slot(warp_slot *dst, const uint8_t *rec, const uint32_t off[4], void *stream) {
+    hipLaunchKernelGGL(k_set_slot, dim3(1), dim3(1), 0, (hipStream_t)stream, dst, rec, off[0], off[1], off[2],
+                       off[3]);
     CHECK_LAUNCH();
     return 0;
 }

@@ -50,6 +50,16 @@ typedef struct {
     int yi[WARP_TPJ];
 } warp_job;
 
+/* One expert of the device-side expert table: where its record sits in the
+ * HBM cache (NULL when it is not resident) and the header's byte offsets of
+ * the gate, up and down index blocks and of the row scales, copied from the
+ * header when the record is placed, so that routing needs no dependent
+ * reads of the record itself. */
+typedef struct {
+    const uint8_t *rec;
+    uint32_t off[4];
+} warp_slot;
+
 /* Byte offsets of the header fields the kernels read (waste_expert_hdr). */
 #define WARP_HDR_GATE_OFF 20
 #define WARP_HDR_UP_OFF 24
@@ -81,7 +91,7 @@ int wk_mvq(const int8_t *W, const uint16_t *ws, size_t rowbytes, int group, int 
  * when a selected expert has no resident record. */
 int wk_route(const float *logits, const float *bias, int E, int K, int T, int act,
              int renorm, float routed_scale, int *idx, float *w,
-             const uint8_t *const *table, warp_job *jobs, int *njobs, int *missing,
+             const warp_slot *table, warp_job *jobs, int *njobs, int *missing,
              int inter, void *stream);
 
 /* The MFMA decode-then-dot matvec over a job list, one launch per group of
@@ -158,7 +168,7 @@ int wk_act(const float *g, const float *u, int P, int I, int act_situ, float bet
  * slot) written to jobs[kind*max_jobs ..], counts to njobs[3]. Pairs whose
  * expert has no resident record set *missing. */
 int wk_plan_chunk(const int *idx, const float *w, int T, int K, int E,
-                  const uint8_t *const *table, int *counts, int *offsets,
+                  const warp_slot *table, int *counts, int *offsets,
                   int *pair_tok, int *pair_exp, float *pair_w, warp_job *jobs,
                   int max_jobs, int *njobs, int *missing, int inter, void *stream);
 /* out [T][H] = per token, sum over its pairs in ascending expert id of
@@ -171,8 +181,9 @@ int wk_combine_chunk(const float *y, const int *offsets, const int *pair_tok,
  * hash of (seed, offset). */
 int wk_fill_random(uint8_t *p, size_t n, uint64_t seed, void *stream);
 
-/* *dst = val, ordered on `stream` (device table updates). */
-int wk_set_ptr(const uint8_t **dst, const uint8_t *val, void *stream);
+/* *dst = {rec, off}, ordered on `stream` (expert table updates); rec NULL
+ * marks the expert not resident. */
+int wk_set_slot(warp_slot *dst, const uint8_t *rec, const uint32_t off[4], void *stream);
 
 /* Device properties the host needs: returns the gfx name into buf. */
 int wk_device_arch(int device, char *buf, int n);
