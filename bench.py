@@ -37,6 +37,7 @@ sys.path.insert(0, HERE)
 sys.path.insert(0, os.path.join(HERE, "tests", "golden"))
 
 METRIC = "MoE-layer tokens/s + achieved HBM GB/s (% of peak), K3-scale RVQ, 1 MI355X"
+TRAFFIC_FILE = os.path.join(HERE, "profiles", "k_vq_lut_k3_decode_traffic.json")
 HBM_PEAK_GBS = 8000.0
 H, I, E, K = 7168, 2048, 384, 16
 S, EN = 2, 4096
@@ -118,8 +119,8 @@ def run_gpu(args):
     for s in range(args.warmup):
         step(s)
     ctx.sync()
-    ctx.set_timing(True)
     e0, e1 = Event(), Event()
+    # timed steps: nothing but the layers on the stream
     log(f"bench: timing {args.steps} steps of {args.layers} layers")
     t0 = time.perf_counter()
     e0.record(stream)
@@ -130,6 +131,13 @@ def run_gpu(args):
     ctx.sync()
     wall = time.perf_counter() - t0
     ms = e0.elapsed_ms(e1)
+    # the same steps again with HIP events around each expert-matvec and
+    # router launch, for the per-kernel durations
+    log("bench: per-launch timing pass")
+    ctx.set_timing(True)
+    for s in range(args.steps):
+        step(s)
+    ctx.sync()
     kms, kn = ctx.get_timing()
     ctx.set_timing(False)
     out = bufs[(args.layers - 1) & 1].numpy()
@@ -137,6 +145,20 @@ def run_gpu(args):
     st = ctx.cache_stats()
     ctx.close()
     return ms, wall, kms, kn, st
+
+
+def measured_traffic(kernel):
+    """HBM traffic per launch of the expert matvec from the committed counter
+    summary (L2-to-memory read requests by size, write requests), when it
+    was taken on this kernel; None otherwise."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if t.get("kernel") != kernel:
+        return None
+    return {k: t[k]["read_bytes"] + t[k]["write_bytes"] for k in ("gate_up", "down")} | {"source": t["source"]}
 
 
 def cpu_baseline(seconds):
@@ -206,6 +228,11 @@ def main():
     kern_bytes = kn[0] * b0 + kn[1] * b1
     achieved = kern_bytes / (kern_ms / 1e3) / 1e9
     layer_gbs = layer_bytes() * layer_tokens / (ms / 1e3) / 1e9
+    kernel = "k_vq_lut" if args.matvec_path == "auto" else "k_vq_mfma"
+    tr = measured_traffic(kernel)
+    traffic = None
+    if tr:
+        traffic = round((kn[0] * tr["gate_up"] + kn[1] * tr["down"]) / max(kn[0] + kn[1], 1))
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     rec = {
         "metric": METRIC,
@@ -218,7 +245,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp32 accumulate (fp16 codebooks x hi/lo fp16 activations on MFMA)",
+        "dtype": "fp32",
         "data": "synthetic (random codes, codebooks, scales and routers of the K3 shapes)",
         "config": {"workload": "K3-scale MoE decode layer, batch 1, 60-layer stack",
                    "hidden": H, "inter": I, "experts": E, "top_k": K, "layers": layers,
@@ -228,8 +255,12 @@ def main():
         "layer_hbm_frac": round(layer_gbs / HBM_PEAK_GBS, 4),
         "layer_bytes": layer_bytes(),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "k_vq_mfma (expert matvec, gate/up and down launches)",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_per_launch": None if tr is None else {"gate_up": tr["gate_up"], "down": tr["down"],
+                                                                    "source": tr["source"]},
+                     "kernel": kernel + " (expert matvec, gate/up and down launches)",
+                     "timing": "HIP events around each launch on the compute stream, in a second pass of the "
+                               "same steps",
                      "bytes_per_launch": {"gate_up": b0, "down": b1},
                      "avg_launch_us": {"gate_up": round(kms[0] / max(kn[0], 1) * 1e3, 2),
                                        "down": round(kms[1] / max(kn[1], 1) * 1e3, 2)},

@@ -375,6 +375,31 @@ __global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits,
     }
 }
 
+// Wave-wide max of a float and min of an int with DPP row operations: the
+// result is reduced into lane 63 and returned to every lane (uniform).
+template <int CTRL, int ROWS>
+__device__ __forceinline__ int dpp_src(int v) {
+    return __builtin_amdgcn_update_dpp(v, v, CTRL, ROWS, 0xf, false);
+}
+__device__ __forceinline__ float wave_max_u(float v) {
+    v = fmaxf(v, __int_as_float(dpp_src<0xB1, 0xf>(__float_as_int(v))));   // quad_perm 1,0,3,2
+    v = fmaxf(v, __int_as_float(dpp_src<0x4E, 0xf>(__float_as_int(v))));   // quad_perm 2,3,0,1
+    v = fmaxf(v, __int_as_float(dpp_src<0x141, 0xf>(__float_as_int(v))));  // row_half_mirror
+    v = fmaxf(v, __int_as_float(dpp_src<0x140, 0xf>(__float_as_int(v))));  // row_mirror
+    v = fmaxf(v, __int_as_float(dpp_src<0x142, 0xa>(__float_as_int(v))));  // row_bcast15
+    v = fmaxf(v, __int_as_float(dpp_src<0x143, 0xc>(__float_as_int(v))));  // row_bcast31
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+__device__ __forceinline__ int wave_min_u(int v) {
+    v = min(v, dpp_src<0xB1, 0xf>(v));
+    v = min(v, dpp_src<0x4E, 0xf>(v));
+    v = min(v, dpp_src<0x141, 0xf>(v));
+    v = min(v, dpp_src<0x140, 0xf>(v));
+    v = min(v, dpp_src<0x142, 0xa>(v));
+    v = min(v, dpp_src<0x143, 0xc>(v));
+    return __builtin_amdgcn_readlane(v, 63);
+}
+
 // Decode routing (one token). The logits, the bias and this layer's expert
 // table go to LDS in one pass of independent loads; one wave then takes the
 // K picks by repeated arg-max -- larger biased score first, the lower id on
@@ -427,31 +452,48 @@ __global__ __launch_bounds__(256) void k_route1(const float *__restrict__ logits
     for (int e = tid; e < E; e += 256) biased[e] = __fadd_rn(score[e], biased[e]);
     __syncthreads();
     if (wave == 0) {
-        float bv = -1e30f;
-        int be = 0x7fffffff;
-        for (int e = lane; e < E; e += 64) {
-            const float v = biased[e];
-            if (v > bv) { bv = v; be = e; }
-        }
-        for (int j = 0; j < K; j++) {
-            float v = bv;
-            int e = be;
+        // Lane l holds ids l, l + 64, ... (up to 8 in registers; larger E
+        // rescans LDS). A pick: the wave max of the lanes' bests, then the
+        // lowest id holding it; the owner lane drops it and rescans.
+        constexpr int VPL = 8;
+        const bool regs = E <= 64 * VPL;
+        float val[VPL];
 #pragma unroll
-            for (int o = 32; o > 0; o >>= 1) {
-                const float ov = __shfl_xor(v, o);
-                const int oe = __shfl_xor(e, o);
-                if (ov > v || (ov == v && oe < e)) { v = ov; e = oe; }
+        for (int m = 0; m < VPL; m++) {
+            const int e = lane + 64 * m;
+            val[m] = regs && e < E ? biased[e] : -INFINITY;
+        }
+        auto best_of = [&](float &bv, int &be) {
+            bv = -1e30f;
+            be = 0x7fffffff;
+            if (regs) {
+#pragma unroll
+                for (int m = 0; m < VPL; m++)
+                    if (val[m] > bv) { bv = val[m]; be = lane + 64 * m; }
+            } else {
+                for (int e = lane; e < E; e += 64) {
+                    const float v = biased[e];
+                    if (v > bv) { bv = v; be = e; }
+                }
             }
+        };
+        float bv;
+        int be;
+        best_of(bv, be);
+        for (int j = 0; j < K; j++) {
+            const float m = wave_max_u(bv);
+            const int e = wave_min_u(bv == m ? be : 0x7fffffff);
             if (e == 0x7fffffff) break;       // nothing above -1e30 is left (uniform)
             if (lane == 0) { sel[j] = e; wsel[j] = score[e]; }
-            if ((e & 63) == lane) {           // the owner of the pick rescans its ids
-                biased[e] = -INFINITY;
-                bv = -1e30f;
-                be = 0x7fffffff;
-                for (int q = lane; q < E; q += 64) {
-                    const float x = biased[q];
-                    if (x > bv) { bv = x; be = q; }
+            if ((e & 63) == lane) {           // the owner of the pick drops it and rescans
+                if (regs) {
+#pragma unroll
+                    for (int q = 0; q < VPL; q++)
+                        if (q == (e >> 6)) val[q] = -INFINITY;
+                } else {
+                    biased[e] = -INFINITY;
                 }
+                best_of(bv, be);
             }
         }
     }
@@ -878,7 +920,9 @@ __device__ __forceinline__ half4 half4_of(uint32_t lo, uint32_t hi) {
     return __builtin_bit_cast(half4, make_uint2(lo, hi));
 }
 
-template <int FMT, bool X31>
+// SHX = true: the jobs of the list share one input and a row group spans
+// them (gate and up); false: one input per job (down).
+template <int FMT, bool X31, bool SHX>
 __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
     typedef FmtT<FMT> F;
     constexpr int SE = F::S * F::E;                        // table entries per position
@@ -893,7 +937,7 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
     const int nv = a.N >> 3, nrb = (a.M + 63) >> 6, nc = nv >> 1;
     const int grp = blockIdx.x / a.splits, split = blockIdx.x % a.splits;
     int fb0, fb_end, xj;
-    if (a.shared_x) {
+    if (SHX) {
         fb0 = grp * LUT_RBG;
         fb_end = nj * nrb;
         xj = 0;
@@ -1092,19 +1136,19 @@ extern "C" int wk_lut_plan(int M, int N, int max_jobs, int nkinds, int shared_x,
     return 0;
 }
 
-template <int FMT, bool X31>
+template <int FMT, bool X31, bool SHX>
 static int launch_lut(const LutArgs &a, int groups, int nkinds, void *stream) {
     typedef FmtT<FMT> F;
     const size_t lds = ((size_t)2 * 2 * F::S * F::E + LUT_XCH * 16) * sizeof(float);
     if (lds > 163840) return -2;
     static bool attr = false;
     if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_vq_lut<FMT, X31>,
+        hipError_t e = hipFuncSetAttribute((const void *)k_vq_lut<FMT, X31, SHX>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return -(int)e - 1000;
         attr = true;
     }
-    hipLaunchKernelGGL((k_vq_lut<FMT, X31>), dim3(groups * a.splits, nkinds), dim3(LUT_NW * 64), lds,
+    hipLaunchKernelGGL((k_vq_lut<FMT, X31, SHX>), dim3(groups * a.splits, nkinds), dim3(LUT_NW * 64), lds,
                        (hipStream_t)stream, a);
     CHECK_LAUNCH();
     return 0;
@@ -1112,7 +1156,11 @@ static int launch_lut(const LutArgs &a, int groups, int nkinds, void *stream) {
 
 template <int FMT>
 static int launch_lut_x(const LutArgs &a, int groups, int nkinds, int x31, void *stream) {
-    return x31 ? launch_lut<FMT, true>(a, groups, nkinds, stream) : launch_lut<FMT, false>(a, groups, nkinds, stream);
+    if (a.shared_x)
+        return x31 ? launch_lut<FMT, true, true>(a, groups, nkinds, stream)
+                   : launch_lut<FMT, false, true>(a, groups, nkinds, stream);
+    return x31 ? launch_lut<FMT, true, false>(a, groups, nkinds, stream)
+               : launch_lut<FMT, false, false>(a, groups, nkinds, stream);
 }
 
 extern "C" int wk_vq_lut(int fmt, const warp_job *jobs, const int *njobs, int max_jobs, int kind_lo, int nkinds,
@@ -1142,19 +1190,21 @@ extern "C" int wk_vq_lut(int fmt, const warp_job *jobs, const int *njobs, int ma
     return -1;
 }
 
-// Sum of a row's partials over the splits, in split order.
+// Sum of a row's partials over the splits, in split order. Up to 32 splits
+// every load is issued before the first add (one memory latency per row).
 __device__ __forceinline__ float lut_rowsum(const float *p, int splits, size_t stride) {
-    float v = 0.0f;
-    int s = 0;
-    for (; s + 4 <= splits; s += 4) {
-        const float a0 = p[(size_t)s * stride], a1 = p[(size_t)(s + 1) * stride];
-        const float a2 = p[(size_t)(s + 2) * stride], a3 = p[(size_t)(s + 3) * stride];
-        v += a0;
-        v += a1;
-        v += a2;
-        v += a3;
+    if (splits <= 32) {
+        float a[32];
+#pragma unroll
+        for (int s = 0; s < 32; s++) a[s] = s < splits ? p[(size_t)s * stride] : 0.0f;
+        float v = 0.0f;
+#pragma unroll
+        for (int s = 0; s < 32; s++)
+            if (s < splits) v += a[s];
+        return v;
     }
-    for (; s < splits; s++) v += p[(size_t)s * stride];
+    float v = 0.0f;
+    for (int s = 0; s < splits; s++) v += p[(size_t)s * stride];
     return v;
 }
 
@@ -1180,44 +1230,68 @@ extern "C" int wk_lut_reduce(const warp_job *jobs, const int *njobs, int max_job
     return 0;
 }
 
+// Sum of a row's partials over splits q, q + 4, q + 8, ... (a quarter), in order.
+__device__ __forceinline__ float lut_quartersum(const float *p, int q, int splits, size_t stride) {
+    float a[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const int s = q + 4 * k;
+        a[k] = s < splits ? p[(size_t)s * stride] : 0.0f;
+    }
+    float v = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+        if (q + 4 * k < splits) v += a[k];
+    for (int s = q + 32; s < splits; s += 4) v += p[(size_t)s * stride];
+    return v;
+}
+
 // Decode: gate and up partials (kinds 0 and 1 of one k_vq_lut launch) ->
-// h[yi][r] = act(gate, up), in f32 (the input of the down table).
+// h[yi][r] = act(gate, up), in f32 (the input of the down table). One block
+// per (job, 64 rows): four threads per row sum a quarter of the splits each,
+// and the quarters are added in order.
 __global__ __launch_bounds__(256) void k_act_lut(const warp_job *__restrict__ jobs, const int *__restrict__ njobs,
                                                  int max_jobs, const float *__restrict__ part, int splits, int I,
                                                  int situ, float beta, float lbeta, float *__restrict__ h) {
-    const int j = blockIdx.y, r = blockIdx.x * 256 + threadIdx.x;
-    if (j >= njobs[0] || r >= I) return;
+    __shared__ float qs[2][4][64];
+    const int j = blockIdx.y, row = threadIdx.x & 63, q = threadIdx.x >> 6, r = blockIdx.x * 64 + row;
+    if (j >= njobs[0]) return;                       // uniform per block
     const size_t nrows = (size_t)((I + 63) >> 6) * 64, stride = (size_t)max_jobs * nrows;
+    if (r < I) {
+        qs[0][q][row] = lut_quartersum(part + (size_t)j * nrows + r, q, splits, stride);
+        qs[1][q][row] = lut_quartersum(part + (size_t)splits * stride + (size_t)j * nrows + r, q, splits, stride);
+    }
+    __syncthreads();
+    if (q != 0 || r >= I) return;
     const warp_job &jg = jobs[j], &ju = jobs[(size_t)max_jobs + j];
-    const float g = lut_rowsum(part + (size_t)j * nrows + r, splits, stride) * f16_keep(jg.scale[r]);
-    const float u = lut_rowsum(part + (size_t)splits * stride + (size_t)j * nrows + r, splits, stride) *
-                    f16_keep(ju.scale[r]);
+    const float g = (((qs[0][0][row] + qs[0][1][row]) + qs[0][2][row]) + qs[0][3][row]) * f16_keep(jg.scale[r]);
+    const float u = (((qs[1][0][row] + qs[1][1][row]) + qs[1][2][row]) + qs[1][3][row]) * f16_keep(ju.scale[r]);
     h[(size_t)jg.yi[0] * I + r] = act_pair(g, u, situ, beta, lbeta);
 }
 
 extern "C" int wk_act_lut(const warp_job *jobs, const int *njobs, int max_jobs, const float *part, int splits, int I,
                           int act_situ, float beta, float lbeta, float *h, void *stream) {
     if (I <= 0 || max_jobs <= 0 || splits <= 0) return -1;
-    hipLaunchKernelGGL(k_act_lut, dim3((I + 255) / 256, max_jobs), dim3(256), 0, (hipStream_t)stream, jobs, njobs,
+    hipLaunchKernelGGL(k_act_lut, dim3((I + 63) / 64, max_jobs), dim3(256), 0, (hipStream_t)stream, jobs, njobs,
                        max_jobs, part, splits, I, act_situ, beta, lbeta, h);
     CHECK_LAUNCH();
     return 0;
 }
 
 // Decode: down partials -> out[r] = sum_j w[j] * y_j[r] in selection order
-// (unfused, as k_combine), + add0 + add1. One block per 64 rows: the K
-// expert outputs of those rows are reduced in parallel into LDS, then one
-// thread per row combines them in order.
+// (unfused, as k_combine), + add0 + add1. One block per 16 rows: the K
+// expert outputs of those rows are reduced in parallel into LDS (one thread
+// per expert and row), then one thread per row combines them in order.
 __global__ __launch_bounds__(256) void k_combine_lut(const warp_job *__restrict__ jobs2, const float *__restrict__ part,
                                                      int splits, int max_jobs, const float *__restrict__ w, int K,
                                                      int H, const float *add0, const float *add1,
                                                      const int *missing, float *__restrict__ out) {
-    __shared__ float yd[WARP_MAX_K][64];
-    const int r0 = blockIdx.x * 64, row = threadIdx.x & 63, jq = threadIdx.x >> 6;
+    __shared__ float yd[WARP_MAX_K][16];
+    const int r0 = blockIdx.x * 16, row = threadIdx.x & 15, jq = threadIdx.x >> 4;
     const bool miss = missing && *missing;
     const size_t nrows = (size_t)((H + 63) >> 6) * 64, stride = (size_t)max_jobs * nrows;
     if (!miss && r0 + row < H)
-        for (int j = jq; j < K; j += 4)
+        for (int j = jq; j < K; j += 16)
             yd[j][row] = lut_rowsum(part + (size_t)j * nrows + r0 + row, splits, stride) *
                          f16_keep(jobs2[j].scale[r0 + row]);
     __syncthreads();
@@ -1238,7 +1312,7 @@ extern "C" int wk_combine_lut(const warp_job *jobs2, const float *part, int spli
                               int K, int H, const float *add0, const float *add1, const int *missing, float *out,
                               void *stream) {
     if (K <= 0 || K > WARP_MAX_K || H <= 0 || splits <= 0 || K > max_jobs) return -1;
-    hipLaunchKernelGGL(k_combine_lut, dim3((H + 63) / 64), dim3(256), 0, (hipStream_t)stream, jobs2, part, splits,
+    hipLaunchKernelGGL(k_combine_lut, dim3((H + 15) / 16), dim3(256), 0, (hipStream_t)stream, jobs2, part, splits,
                        max_jobs, w, K, H, add0, add1, missing, out);
     CHECK_LAUNCH();
     return 0;
