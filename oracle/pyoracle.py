@@ -103,8 +103,10 @@ class LayerView:
         lay = model.layers[L]
         self.keep = []
         self.booksT = books_T(model.books_raw)
-        self.recs = [np.frombuffer(r, dtype=np.uint8) for r in lay.records]
-        self.rec_ptrs = (C.c_void_p * len(self.recs))(*[r.ctypes.data for r in self.recs])
+        # experts without a record (not materialised) are NULL: the oracle reads
+        # only the records of the experts a token selects
+        self.recs = [None if r is None else np.frombuffer(r, dtype=np.uint8) for r in lay.records]
+        self.rec_ptrs = (C.c_void_p * len(self.recs))(*[None if r is None else r.ctypes.data for r in self.recs])
         st = OrLayer()
         st.fmt = FMT[spec.fmt]
         st.hidden, st.inter, st.n_experts, st.top_k = spec.hidden, spec.inter, spec.experts, spec.top_k

@@ -57,6 +57,7 @@ class Spec:
     routed_scale: float = 2.0
     shared_bits: int = 8         # 8, 4, or 0 for no shared expert
     shared_group: int = 32
+    shared_scale: tuple = (0.002, 0.02)   # per-group fp16 scale range of the shared expert
     n_shared: int = 1
     act: str = "silu"            # "silu" | "situ"
     situ_beta: float = 4.0
@@ -67,6 +68,7 @@ class Spec:
     seed: int = 0
     keep_codes: bool = True      # keep the per-matrix code arrays (small shapes)
     dup_rows: tuple = ()         # (a, b): router row b is a copy of row a (exact ties)
+    materialize: tuple = ()      # expert ids that get records; () = all (large shapes)
 
 
 def index_bytes(fmt: str, M: int, N: int) -> int:
@@ -98,7 +100,7 @@ def f16_bits(a: np.ndarray) -> np.ndarray:
     return np.asarray(a, dtype=np.float16).view(np.uint16)
 
 
-def quant_rows(rng, rows: int, N: int, bits: int, group: int):
+def quant_rows(rng, rows: int, N: int, bits: int, group: int, scale=(0.002, 0.02)):
     """Q8G/Q4G payload (rows padded to whole groups) and per-group fp16 scales."""
     ng = (N + group - 1) // group
     n = ng * group
@@ -111,7 +113,7 @@ def quant_rows(rng, rows: int, N: int, bits: int, group: int):
         lo, hi = v[:, 0::2] + 8, v[:, 1::2] + 8
         payload = (lo | (hi << 4)).astype(np.uint8)
         rowbytes = n // 2
-    scales = f16_bits(rng.uniform(0.002, 0.02, size=(rows, ng)))
+    scales = f16_bits(rng.uniform(scale[0], scale[1], size=(rows, ng)))
     return payload.reshape(rows, rowbytes), scales.reshape(rows, ng), rowbytes
 
 
@@ -167,9 +169,14 @@ def build(spec: Spec) -> Model:
         if spec.shared_bits:
             si = I * spec.n_shared
             for (M, N) in [(si, H), (si, H), (H, si)]:
-                shared.append(quant_rows(rng, M, N, spec.shared_bits, spec.shared_group))
+                shared.append(quant_rows(rng, M, N, spec.shared_bits, spec.shared_group, spec.shared_scale))
         lay = Layer(router=router, router_q=router_q, bias=bias, shared=shared)
         for e in range(spec.experts):
+            if spec.materialize and e not in spec.materialize:
+                lay.codes.append(None)
+                lay.scales.append(None)
+                lay.records.append(None)
+                continue
             body = bytearray()
             offs = []
             codes_e, scales_e = [], []
@@ -241,7 +248,8 @@ def digest(model: Model) -> str:
             h.update(q[0].tobytes())
             h.update(q[1].tobytes())
         for r in lay.records:
-            h.update(r)
+            if r is not None:
+                h.update(r)
     return h.hexdigest()
 
 

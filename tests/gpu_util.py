@@ -29,6 +29,28 @@ def host(b):
     return b.numpy()
 
 
+# Synthetic magnitudes for layer-level GPU tests: codebooks N(0, 0.3) (a
+# normalised codebook's spread; with U(0.01, 0.05) row scales the decoded
+# weights are ~1e-2) and shared-expert group scales of 1e-4..3e-4, so that
+# the routed experts and the shared expert both show in a layer's output.
+BALANCED = dict(book_std=0.3, shared_scale=(1e-4, 3e-4))
+
+
+def routed_share(model, layer, x):
+    """max|routed part| / max|layer output| for one token, from the oracle:
+    the same layer with its shared expert taken out. A layer test is only
+    sensitive to the routed path when this is not tiny."""
+    import copy
+    m = copy.copy(model)
+    m.layers = list(model.layers)
+    lay = copy.copy(model.layers[layer])
+    lay.shared = []
+    m.layers[layer] = lay
+    full = po.LayerView(model, layer).moe_layer(x)[0]
+    routed = po.LayerView(m, layer).moe_layer(x)[0]
+    return float(np.max(np.abs(routed)) / max(np.max(np.abs(full)), 1e-30))
+
+
 def rel_err(got, ref):
     """max|got - ref| / max|ref|, the tolerance metric the parity bar uses."""
     got = np.asarray(got, np.float64)

@@ -4,23 +4,25 @@ partial 64-row blocks, splits of a single 2-position chunk, and the
 decode-then-dot path on the same inputs for comparison.
 
 Bar: selection bit-exact, outputs max|d|/max|ref| <= 1e-4 against the oracle.
-The table entries themselves are the reference's fused chain bit for bit, so
-the only difference from the oracle is the order of the fp32 sum over
-positions (splits, then position parity); the logged errors are ~1e-7.
+The tables are built on the matrix cores from x split into fp16 halves
+(exact products, ~22 bits of x) and the rows are summed in a different order
+from the oracle's (splits, then position parity); the logged errors are
+~1e-7. The synthetic magnitudes keep the routed experts visible next to the
+shared expert (checked on the oracle).
 """
 import numpy as np
 import pytest
 
 import container as ct
-from gpu_util import dev, empty, host, log, open_ctx, rel_err
+from gpu_util import BALANCED, dev, empty, host, log, open_ctx, rel_err, routed_share
 from oracle import pyoracle as po
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-4
 
 SHAPES = [
-    # partial last row block (96 = 64 + 32) and odd row-block counts
-    dict(hidden=160, inter=96, experts=8, top_k=3),
+    # partial last row block (96 = 64 + 32) and odd row-block counts; no shared expert
+    dict(hidden=160, inter=96, experts=8, top_k=3, shared_bits=0),
     # gate/up: 8 jobs x 32 row blocks = 2 row groups spanning jobs; 1 chunk per split
     dict(hidden=1024, inter=2048, experts=12, top_k=8),
 ]
@@ -30,7 +32,7 @@ SHAPES = [
 @pytest.mark.parametrize("shape", range(len(SHAPES)))
 def test_lut_decode_and_matvec(fmt, shape):
     import warp_amd
-    spec = ct.Spec(layers=1, fmt=fmt, seed=100 + shape, **SHAPES[shape])
+    spec = ct.Spec(layers=1, fmt=fmt, seed=100 + shape, **SHAPES[shape], **BALANCED)
     model = ct.build(spec)
     ctx = open_ctx(model)
     try:
@@ -42,6 +44,8 @@ def test_lut_decode_and_matvec(fmt, shape):
         for t in range(3):
             x = rng.normal(size=spec.hidden).astype(np.float32)
             ro, ri, rw, _ = lv.moe_layer(x)
+            if t == 0 and spec.shared_bits:
+                assert routed_share(model, 0, x) > 0.05
             for path in ("auto", "mfma"):
                 ctx.set_matvec_path(path)
                 out = empty(spec.hidden)

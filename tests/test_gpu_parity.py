@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 import container as ct
-from gpu_util import dev, empty, host, log, open_ctx, rel_err
+from gpu_util import BALANCED, dev, empty, host, log, open_ctx, rel_err, routed_share
 from oracle import pyoracle as po
 
 pytestmark = pytest.mark.gpu
@@ -19,7 +19,7 @@ FMTS = ["VQ3R", "VQ2R", "VQ4P", "VQ12"]
 
 
 def small_spec(fmt, **kw):
-    base = dict(hidden=128, inter=64, experts=8, top_k=2, layers=2, fmt=fmt, seed=7)
+    base = dict(hidden=128, inter=64, experts=8, top_k=2, layers=2, fmt=fmt, seed=7, **BALANCED)
     base.update(kw)
     return ct.Spec(**base)
 
@@ -130,6 +130,9 @@ def test_moe_decode(loaded, path):
         lv = po.LayerView(model, L)
         for t in range(6):
             x = rng.normal(size=spec.hidden).astype(np.float32)
+            if t == 0:
+                share = routed_share(model, L, x)
+                assert share > 0.05, f"the routed experts are {share:.1e} of the output: test not sensitive"
             out = empty(spec.hidden)
             idx, w = ctx.moe_decode(L, dev(x), out, want_route=True)
             ro, ri, rw, _ = lv.moe_layer(x)

@@ -375,29 +375,31 @@ __global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits,
     }
 }
 
-// Wave-wide max of a float and min of an int with DPP row operations: the
-// result is reduced into lane 63 and returned to every lane (uniform).
+// Wave-wide max / min of an int with DPP row operations: reduced into lane
+// 63 and returned to every lane (uniform).
 template <int CTRL, int ROWS>
 __device__ __forceinline__ int dpp_src(int v) {
     return __builtin_amdgcn_update_dpp(v, v, CTRL, ROWS, 0xf, false);
 }
-__device__ __forceinline__ float wave_max_u(float v) {
-    v = fmaxf(v, __int_as_float(dpp_src<0xB1, 0xf>(__float_as_int(v))));   // quad_perm 1,0,3,2
-    v = fmaxf(v, __int_as_float(dpp_src<0x4E, 0xf>(__float_as_int(v))));   // quad_perm 2,3,0,1
-    v = fmaxf(v, __int_as_float(dpp_src<0x141, 0xf>(__float_as_int(v))));  // row_half_mirror
-    v = fmaxf(v, __int_as_float(dpp_src<0x140, 0xf>(__float_as_int(v))));  // row_mirror
-    v = fmaxf(v, __int_as_float(dpp_src<0x142, 0xa>(__float_as_int(v))));  // row_bcast15
-    v = fmaxf(v, __int_as_float(dpp_src<0x143, 0xc>(__float_as_int(v))));  // row_bcast31
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
-__device__ __forceinline__ int wave_min_u(int v) {
-    v = min(v, dpp_src<0xB1, 0xf>(v));
-    v = min(v, dpp_src<0x4E, 0xf>(v));
-    v = min(v, dpp_src<0x141, 0xf>(v));
-    v = min(v, dpp_src<0x140, 0xf>(v));
-    v = min(v, dpp_src<0x142, 0xa>(v));
-    v = min(v, dpp_src<0x143, 0xc>(v));
+template <bool MAX>
+__device__ __forceinline__ int wave_reduce_i(int v) {
+    auto op = [](int a, int b) { return MAX ? max(a, b) : min(a, b); };
+    v = op(v, dpp_src<0xB1, 0xf>(v));    // quad_perm 1,0,3,2
+    v = op(v, dpp_src<0x4E, 0xf>(v));    // quad_perm 2,3,0,1
+    v = op(v, dpp_src<0x141, 0xf>(v));   // row_half_mirror
+    v = op(v, dpp_src<0x140, 0xf>(v));   // row_mirror
+    v = op(v, dpp_src<0x142, 0xa>(v));   // row_bcast15
+    v = op(v, dpp_src<0x143, 0xc>(v));   // row_bcast31
     return __builtin_amdgcn_readlane(v, 63);
+}
+
+// Order-preserving int key of a biased score: larger score, larger key.
+// -0 counts as +0 (the reference compares floats), and values the
+// reference's scan can never pick (at or below -1e30, NaN) get INT_MIN.
+__device__ __forceinline__ int route_key(float v) {
+    if (!(v > -1e30f)) return INT_MIN;
+    const int b = __float_as_int(v + 0.0f);
+    return b ^ ((b >> 31) & 0x7fffffff);
 }
 
 // Decode routing (one token). The logits, the bias and this layer's expert
@@ -407,6 +409,7 @@ __device__ __forceinline__ int wave_min_u(int v) {
 // (src/model.c:2727-2739) -- each lane keeping the best of its own ids and
 // rescanning them only when that best is taken. The job lists are then
 // written from the table in LDS, with no dependent reads of HBM.
+template <bool REGS>
 __global__ __launch_bounds__(256) void k_route1(const float *__restrict__ logits, const float *__restrict__ bias,
                                                 int E, int K, int act, int renorm, float routed_scale,
                                                 int *__restrict__ idx, float *__restrict__ w,
@@ -452,82 +455,91 @@ __global__ __launch_bounds__(256) void k_route1(const float *__restrict__ logits
     for (int e = tid; e < E; e += 256) biased[e] = __fadd_rn(score[e], biased[e]);
     __syncthreads();
     if (wave == 0) {
-        // Lane l holds ids l, l + 64, ... (up to 8 in registers; larger E
-        // rescans LDS). A pick: the wave max of the lanes' bests, then the
-        // lowest id holding it; the owner lane drops it and rescans.
-        constexpr int VPL = 8;
-        const bool regs = E <= 64 * VPL;
-        float val[VPL];
+        // Lane l holds the keys of ids l, l + 64, ... (REGS: all in registers,
+        // E <= 512; else rescans LDS). A pick: the wave max key; the lowest id
+        // holding it (one ballot when it is unique, else a min over ids); the
+        // owner lane drops it and rescans, the other lanes keep their best
+        // (selects, no branches). Pick j stays in lane j.
+        constexpr int VPL = REGS ? 8 : 1;
+        int key[VPL];
 #pragma unroll
         for (int m = 0; m < VPL; m++) {
             const int e = lane + 64 * m;
-            val[m] = regs && e < E ? biased[e] : -INFINITY;
+            key[m] = REGS && e < E ? route_key(biased[e]) : INT_MIN;
         }
-        auto best_of = [&](float &bv, int &be) {
-            bv = -1e30f;
-            be = 0x7fffffff;
-            if (regs) {
+        auto best_of = [&](int &bk, int &bid) {
+            bk = INT_MIN;
+            bid = 0x7fffffff;
+            if (REGS) {
 #pragma unroll
-                for (int m = 0; m < VPL; m++)
-                    if (val[m] > bv) { bv = val[m]; be = lane + 64 * m; }
+                for (int m = 0; m < VPL; m++) {
+                    const bool b = key[m] > bk;
+                    bk = b ? key[m] : bk;
+                    bid = b ? lane + 64 * m : bid;
+                }
             } else {
                 for (int e = lane; e < E; e += 64) {
-                    const float v = biased[e];
-                    if (v > bv) { bv = v; be = e; }
+                    const int k = route_key(biased[e]);
+                    if (k > bk) { bk = k; bid = e; }
                 }
             }
         };
-        float bv;
-        int be;
-        best_of(bv, be);
+        int bk, bid;
+        best_of(bk, bid);
+        int mine = 0, npick = 0;
         for (int j = 0; j < K; j++) {
-            const float m = wave_max_u(bv);
-            const int e = wave_min_u(bv == m ? be : 0x7fffffff);
-            if (e == 0x7fffffff) break;       // nothing above -1e30 is left (uniform)
-            if (lane == 0) { sel[j] = e; wsel[j] = score[e]; }
-            if ((e & 63) == lane) {           // the owner of the pick drops it and rescans
-                if (regs) {
+            const int m = wave_reduce_i<true>(bk);
+            if (m == INT_MIN) break;          // nothing pickable is left (uniform)
+            const unsigned long long hit = __ballot(bk == m);
+            int e;
+            if (__popcll(hit) == 1) e = __builtin_amdgcn_readlane(bid, __ffsll((long long)hit) - 1);
+            else e = wave_reduce_i<false>(bk == m ? bid : 0x7fffffff);
+            mine = lane == j ? e : mine;
+            npick = j + 1;
+            const bool own = (e & 63) == lane;
+            if (REGS) {
 #pragma unroll
-                    for (int q = 0; q < VPL; q++)
-                        if (q == (e >> 6)) val[q] = -INFINITY;
-                } else {
-                    biased[e] = -INFINITY;
-                }
-                best_of(bv, be);
+                for (int q = 0; q < VPL; q++) key[q] = own && q == (e >> 6) ? INT_MIN : key[q];
+                int nk, ni;
+                best_of(nk, ni);
+                bk = own ? nk : bk;
+                bid = own ? ni : bid;
+            } else if (own) {
+                biased[e] = -INFINITY;
+                best_of(bk, bid);
             }
+        }
+        // weights: the sum in pick order (one lane, as the reference), the
+        // divisions and the scale in parallel
+        float wv = lane < npick ? score[mine] : 0.0f;
+        float ssum = 0.0f;
+        for (int j = 0; j < K; j++) ssum = __fadd_rn(ssum, __shfl(wv, j));
+        if (renorm && K > 1) wv = __fdiv_rn(wv, __fadd_rn(ssum, 1e-20f));
+        wv = __fmul_rn(wv, routed_scale);
+        if (lane < K) {
+            sel[lane] = lane < npick ? mine : 0;
+            wsel[lane] = wv;
+            idx[lane] = lane < npick ? mine : 0;
+            w[lane] = wv;
         }
     }
     __syncthreads();
-    if (tid == 0) {
-        if (renorm && K > 1) {
-            float s = 0.0f;
-            for (int j = 0; j < K; j++) s = __fadd_rn(s, wsel[j]);
-            const float d = __fadd_rn(s, 1e-20f);
-            for (int j = 0; j < K; j++) wsel[j] = __fdiv_rn(wsel[j], d);
-        }
-        for (int j = 0; j < K; j++) {
-            wsel[j] = __fmul_rn(wsel[j], routed_scale);
-            idx[j] = sel[j];
-            w[j] = wsel[j];
-        }
-    }
     if (table) {
         int miss = 0;
-        for (int j = tid; j < K; j += 256) {
+        for (int t = tid; t < 3 * K; t += 256) {          // one thread per (kind, pick)
+            const int kind = t / K, j = t - kind * K;
             const warp_slot sl = table_lds ? slots[sel[j]] : table[sel[j]];
             miss |= sl.rec == nullptr;
-            for (int kind = 0; kind < 3; kind++) {
-                warp_job jb;
-                jb.idx = nullptr;
-                jb.scale = nullptr;
-                if (sl.rec) job_ptrs(jb, sl, kind, inter);
-                jb.n = 1;
-                jb.rsv = 0;
-                for (int s = 0; s < WARP_TPJ; s++) { jb.xi[s] = 0; jb.yi[s] = 0; }
-                jb.xi[0] = kind == 2 ? j : 0;
-                jb.yi[0] = j;
-                jobs[kind * K + j] = jb;
-            }
+            warp_job jb;
+            jb.idx = nullptr;
+            jb.scale = nullptr;
+            if (sl.rec) job_ptrs(jb, sl, kind, inter);
+            jb.n = 1;
+            jb.rsv = 0;
+            for (int s = 0; s < WARP_TPJ; s++) { jb.xi[s] = 0; jb.yi[s] = 0; }
+            jb.xi[0] = kind == 2 ? j : 0;
+            jb.yi[0] = j;
+            jobs[kind * K + j] = jb;
         }
         miss = __syncthreads_or(miss);
         if (tid == 0) {
@@ -546,8 +558,12 @@ extern "C" int wk_route(const float *logits, const float *bias, int E, int K, in
         // the table is staged in LDS up to 2048 experts (48 KiB)
         const int tl = table && E <= 2048;
         const size_t lds = (size_t)2 * ((E + 1) & ~1) * sizeof(float) + (tl ? (size_t)E * sizeof(warp_slot) : 0);
-        hipLaunchKernelGGL(k_route1, dim3(1), dim3(256), lds, (hipStream_t)stream, logits, bias, E, K, act, renorm,
-                           routed_scale, idx, w, table, tl, jobs, njobs, missing, inter);
+        if (E <= 512)
+            hipLaunchKernelGGL(k_route1<true>, dim3(1), dim3(256), lds, (hipStream_t)stream, logits, bias, E, K, act,
+                               renorm, routed_scale, idx, w, table, tl, jobs, njobs, missing, inter);
+        else
+            hipLaunchKernelGGL(k_route1<false>, dim3(1), dim3(256), lds, (hipStream_t)stream, logits, bias, E, K, act,
+                               renorm, routed_scale, idx, w, table, tl, jobs, njobs, missing, inter);
         CHECK_LAUNCH();
         return 0;
     }

@@ -20,6 +20,7 @@ FMT = {"VQ3R": VQ3R, "VQ2R": VQ2R, "VQ4P": VQ4P, "VQ12": VQ12}
 ROUTE_SIGMOID, ROUTE_SOFTMAX = 0, 1
 ERRORS = {-1: "E_ARG", -2: "E_DEVICE", -3: "E_NOMEM", -4: "E_READ", -5: "E_HEADER",
           -6: "E_CRC", -7: "E_NOSLOT", -8: "E_MISSING"}
+E_ARG, E_DEVICE, E_NOMEM, E_READ, E_HEADER, E_CRC, E_NOSLOT, E_MISSING = range(-1, -9, -1)
 
 _lib = None
 
@@ -310,4 +311,5 @@ def load_container_model(ctx: Context, model, layers=None):
                            [np.ascontiguousarray(s[0]) for s in lay.shared],
                            [np.ascontiguousarray(s[1]) for s in lay.shared], [s[2] for s in lay.shared])
         for e, rec in enumerate(lay.records):
-            ctx.put_expert(L, e, np.frombuffer(rec, np.uint8))
+            if rec is not None:                  # experts without a record stay out of the cache
+                ctx.put_expert(L, e, np.frombuffer(rec, np.uint8))
