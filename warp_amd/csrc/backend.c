@@ -381,10 +381,8 @@ static int ctx_alloc(warp_hip_ctx *c)
         size_t need = 0;
         if (!wk_lut_plan(I, H, K, 2, 1, c->n_cu, (size_t)-1, &gr, &sp))
             need = (size_t)2 * sp * K * (((size_t)I + 63) / 64) * 64;
-        if (!wk_lut_plan(H, I, K, 1, 0, c->n_cu, (size_t)-1, &gr, &sp)) {
-            const size_t d = (size_t)sp * K * (((size_t)H + 63) / 64) * 64;
-            if (d > need) need = d;
-        }
+        if (!wk_lut_plan(H, I, K, 1, 0, c->n_cu, (size_t)-1, &gr, &sp))
+            need += (size_t)sp * K * (((size_t)H + 63) / 64) * 64;   /* down partials after the gate/up ones */
         c->part_cap = need;
         DMALLOC(c, c->part, need * sizeof(float));
     }
@@ -1134,7 +1132,6 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
     if ((rc = timing_end(c))) return rc;
     const int n_la = lookahead_launch(c, layer, x_dev);
     if (n_la < 0) return n_la;
-
     if (L->resident == E) {
         /* everything resident: route and build the jobs on the device, no
          * host round trip */
@@ -1167,17 +1164,21 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
     /* gate and up, activation, down */
     float *yk[3] = { c->yg, c->yu, c->yd };
     int sp_d = 0;
+    size_t d_off = 0;
     if (use_lut) {
         int sp_gu = 0;
         if ((rc = timing_begin(c, 0))) return rc;
         KRN(c, wk_vq_lut(g->fmt, c->jobs, c->njobs, K, 0, 2, L->books, L->books_x31, x_dev, 1, c->part, c->part_cap, I, H,
-                         c->n_cu, &sp_gu, c->st));
+                         c->n_cu, NULL, 0, 0, 0.0f, 0.0f, &sp_gu, c->st));
         if ((rc = timing_end(c))) return rc;
-        KRN(c, wk_act_lut(c->jobs, c->njobs, K, c->part, sp_gu, I, g->act_situ, g->situ_beta, g->situ_linear_beta,
-                          c->hbuf, c->st));
+        /* the down launch makes its inputs from the gate/up partials (SwiGLU
+         * in its prologue); its partials go after the gate/up ones */
+        const size_t gu_floats = (size_t)2 * sp_gu * K * (((size_t)I + 63) / 64) * 64;
         if ((rc = timing_begin(c, 1))) return rc;
-        KRN(c, wk_vq_lut(g->fmt, c->jobs, c->njobs, K, 2, 1, L->books, L->books_x31, c->hbuf, 0, c->part, c->part_cap, H, I,
-                         c->n_cu, &sp_d, c->st));
+        KRN(c, wk_vq_lut(g->fmt, c->jobs, c->njobs, K, 2, 1, L->books, L->books_x31, NULL, 0, c->part + gu_floats,
+                         c->part_cap - gu_floats, H, I, c->n_cu, c->part, sp_gu, g->act_situ, g->situ_beta,
+                         g->situ_linear_beta, &sp_d, c->st));
+        d_off = gu_floats;
         if ((rc = timing_end(c))) return rc;
     } else if (c->P6) {
         const size_t nvH = (size_t)H / 8, nblkH = (nvH + WARP_LUT_BLK - 1) / WARP_LUT_BLK;
@@ -1198,8 +1199,8 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
     }
     if (L->sq[0] && (rc = shared_ffn(c, L, x_dev, 1))) return rc;
     if (use_lut)
-        KRN(c, wk_combine_lut(c->jobs + 2 * (size_t)K, c->part, sp_d, K, c->w, K, H, L->sq[0] ? c->sho : NULL,
-                              resid_dev, c->missing, out_dev, c->st));
+        KRN(c, wk_combine_lut(c->jobs + 2 * (size_t)K, c->part + d_off, sp_d, K, c->w, K, H,
+                              L->sq[0] ? c->sho : NULL, resid_dev, c->missing, out_dev, c->st));
     else
         KRN(c, wk_combine(c->yd, c->w, K, H, L->sq[0] ? c->sho : NULL, resid_dev, c->missing, out_dev, c->st));
     DEV(c, hipEventRecord(c->ev_after, c->st));
@@ -1363,7 +1364,7 @@ int warp_hip_vq_matvec(warp_hip_ctx *c, int layer, int kind, const uint8_t *rec_
         float *yk[3] = { y_dev, y_dev, y_dev };
         int sp = 0;
         KRN(c, wk_vq_lut(c->cfg.fmt, c->jobs, c->njobs, 1, kind, 1, L->books, L->books_x31, x_dev, 1, c->part, c->part_cap, M, N,
-                         c->n_cu, &sp, c->st));
+                         c->n_cu, NULL, 0, 0, 0.0f, 0.0f, &sp, c->st));
         KRN(c, wk_lut_reduce(c->jobs, c->njobs, 1, kind, 1, c->part, sp, M, yk, c->st));
     } else {
         float *yk[3] = { y_dev, y_dev, y_dev };

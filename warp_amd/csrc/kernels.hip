@@ -150,10 +150,10 @@ extern "C" int wk_split(const float *x, int T, int N, uint16_t *xs, float *xscal
 
 // One 256-thread block per (token, row): eight float4 loads in flight per
 // thread, lane partials, then a fixed-order block sum (deterministic).
-__global__ __launch_bounds__(256) void k_router_fast(const float *__restrict__ W, const float *__restrict__ x,
-                                                     int E, int H, int T, float *__restrict__ logits) {
+// One logit row per 256-thread block (row = t * E + e), returned in thread 0.
+__device__ __forceinline__ float router_row_fast(const float *__restrict__ W, const float *__restrict__ x, int E,
+                                                 int H, int row) {
     __shared__ float part[4];
-    const int row = blockIdx.x;
     const int t = row / E, e = row % E;
     const float *w = W + (size_t)e * H, *xt = x + (size_t)t * H;
     float acc = 0.0f;
@@ -186,7 +186,13 @@ __global__ __launch_bounds__(256) void k_router_fast(const float *__restrict__ W
     acc = wave_sum(acc);
     if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
     __syncthreads();
-    if (threadIdx.x == 0) logits[row] = (part[0] + part[1]) + (part[2] + part[3]);
+    return (part[0] + part[1]) + (part[2] + part[3]);
+}
+
+__global__ __launch_bounds__(256) void k_router_fast(const float *__restrict__ W, const float *__restrict__ x,
+                                                     int E, int H, int T, float *__restrict__ logits) {
+    const float v = router_row_fast(W, x, E, H, blockIdx.x);
+    if (threadIdx.x == 0) logits[blockIdx.x] = v;
 }
 
 // The reference's dotf on x86 (src/model.c:155-160): one sequential, unfused
@@ -410,12 +416,12 @@ __device__ __forceinline__ int route_key(float v) {
 // rescanning them only when that best is taken. The job lists are then
 // written from the table in LDS, with no dependent reads of HBM.
 template <bool REGS>
-__global__ __launch_bounds__(256) void k_route1(const float *__restrict__ logits, const float *__restrict__ bias,
-                                                int E, int K, int act, int renorm, float routed_scale,
-                                                int *__restrict__ idx, float *__restrict__ w,
-                                                const warp_slot *__restrict__ table, int table_lds,
-                                                warp_job *__restrict__ jobs, int *__restrict__ njobs,
-                                                int *__restrict__ missing, int inter) {
+__device__ __forceinline__ void route1_block(const float *__restrict__ logits, const float *__restrict__ bias,
+                                             int E, int K, int act, int renorm, float routed_scale,
+                                             int *__restrict__ idx, float *__restrict__ w,
+                                             const warp_slot *__restrict__ table, int table_lds,
+                                             warp_job *__restrict__ jobs, int *__restrict__ njobs,
+                                             int *__restrict__ missing, int inter) {
     extern __shared__ __attribute__((aligned(16))) float lds_r1[];
     float *score = lds_r1;                                     // [E]
     float *biased = lds_r1 + E;                                // [E]
@@ -547,6 +553,17 @@ __global__ __launch_bounds__(256) void k_route1(const float *__restrict__ logits
             if (miss) *missing = 1;
         }
     }
+}
+
+template <bool REGS>
+__global__ __launch_bounds__(256) void k_route1(const float *__restrict__ logits, const float *__restrict__ bias,
+                                                int E, int K, int act, int renorm, float routed_scale,
+                                                int *__restrict__ idx, float *__restrict__ w,
+                                                const warp_slot *__restrict__ table, int table_lds,
+                                                warp_job *__restrict__ jobs, int *__restrict__ njobs,
+                                                int *__restrict__ missing, int inter) {
+    route1_block<REGS>(logits, bias, E, K, act, renorm, routed_scale, idx, w, table, table_lds, jobs, njobs,
+                       missing, inter);
 }
 
 extern "C" int wk_route(const float *logits, const float *bias, int E, int K, int T, int act, int renorm,
@@ -892,7 +909,7 @@ extern "C" int wk_vq_matvec(int fmt, const warp_job *jobs, const int *njobs, int
 // A lane sums 4 rows of one row block at one position parity; the two
 // parities are added at the end and the block writes one partial sum per row
 // and split. The splits are added in order by the consumer (k_lut_reduce,
-// k_act_lut, k_combine_lut), so results are deterministic.
+// the down launch's prologue, k_combine_lut), so results are deterministic.
 //
 // Table build. The codebook of the block's kind sits in registers (fp16, one
 // 64-entry group per 64 lanes, 8 groups per wave for 2 x 4096). The build runs
@@ -922,7 +939,31 @@ struct LutArgs {
     const float *x;            // inputs [*][N]; a job reads x + xi[0] * N
     float *part;               // [nkinds][splits][max_jobs][nrb * 64]
     int M, N, splits, shared_x;
+    // when set (down, one input per job): the input of job j is not read
+    // from x but made here, h[r] = act(gate[r], up[r]) from the gate/up
+    // partial sums (kinds 0 and 1 of the previous launch, act_splits each)
+    const float *act_part;
+    int act_splits, act_situ;
+    float act_beta, act_lbeta;
 };
+
+// Sum of a row's partials over the splits, in split order. Up to 32 splits
+// every load is issued before the first add (one memory latency per row).
+__device__ __forceinline__ float lut_rowsum(const float *p, int splits, size_t stride) {
+    if (splits <= 32) {
+        float a[32];
+#pragma unroll
+        for (int s = 0; s < 32; s++) a[s] = s < splits ? p[(size_t)s * stride] : 0.0f;
+        float v = 0.0f;
+#pragma unroll
+        for (int s = 0; s < 32; s++)
+            if (s < splits) v += a[s];
+        return v;
+    }
+    float v = 0.0f;
+    for (int s = 0; s < splits; s++) v += p[(size_t)s * stride];
+    return v;
+}
 
 template <int FMT>
 __device__ __forceinline__ unsigned lut_code(unsigned slot, int s) {
@@ -993,22 +1034,57 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
         cb[g] = G < NG ? bk[G * 64 + lane] : make_uint4(0u, 0u, 0u, 0u);
     }
 
-    // x of this split -> LDS: f32 [chunk][16] (X31) or the scaled fp16
-    // halves [chunk][position 2][hi, lo][8]
+    // x of this split (at most LUT_XCH x 16 values, 4 per thread) into
+    // registers: read from the input, or made from the gate/up partials
     const int nx = (c1 - c0) * 16;
     const float *xg = xin + (size_t)c0 * 16;
+    float xr[LUT_XCH * 16 / (LUT_NW * 64)];
+    if (!SHX && a.act_part) {
+        const size_t arows = (size_t)((a.N + 63) >> 6) * 64, astride = (size_t)a.max_jobs * arows;
+        const warp_job &jg = a.jobs[xj], &ju = a.jobs[(size_t)a.max_jobs + xj];
+        const float *pg = a.act_part + (size_t)xj * arows + (size_t)c0 * 16;
+        const float *pu = pg + (size_t)a.act_splits * astride;
+        const uint16_t *sg = jg.scale + (size_t)c0 * 16, *su = ju.scale + (size_t)c0 * 16;
+#pragma unroll
+        for (int k = 0; k < LUT_XCH * 16 / (LUT_NW * 64); k++) {
+            const int i = threadIdx.x + k * LUT_NW * 64;
+            xr[k] = 0.0f;
+            if (i < nx) {
+                const float g = lut_rowsum(pg + i, a.act_splits, astride) * f16_keep(sg[i]);
+                const float u = lut_rowsum(pu + i, a.act_splits, astride) * f16_keep(su[i]);
+                xr[k] = act_pair(g, u, a.act_situ, a.act_beta, a.act_lbeta);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < LUT_XCH * 16 / (LUT_NW * 64); k++) {
+            const int i = threadIdx.x + k * LUT_NW * 64;
+            xr[k] = i < nx ? xg[i] : 0.0f;
+        }
+    }
+    // -> LDS: f32 [chunk][16] (X31) or the scaled fp16 halves
+    // [chunk][position 2][hi, lo][8]
     int ks = 0;
     if constexpr (X31) {
         float *xst = lut + 2 * BUF;
-        for (int i = threadIdx.x; i < nx; i += LUT_NW * 64) xst[i] = xg[i];
+#pragma unroll
+        for (int k = 0; k < LUT_XCH * 16 / (LUT_NW * 64); k++) {
+            const int i = threadIdx.x + k * LUT_NW * 64;
+            if (i < nx) xst[i] = xr[k];
+        }
     } else {
         float m = 0.0f;
-        for (int i = threadIdx.x; i < nx; i += LUT_NW * 64) m = fmaxf(m, fabsf(xg[i]));
+#pragma unroll
+        for (int k = 0; k < LUT_XCH * 16 / (LUT_NW * 64); k++) m = fmaxf(m, fabsf(xr[k]));
         ks = split_exp(block_absmax(m));
         _Float16 *xh = (_Float16 *)(lut + 2 * BUF);
-        for (int i = threadIdx.x; i < nx; i += LUT_NW * 64) {
-            const int o = (i >> 4) * 32 + ((i >> 3) & 1) * 16 + (i & 7);
-            split_store(xg[i], ks, &xh[o], &xh[o + 8]);
+#pragma unroll
+        for (int k = 0; k < LUT_XCH * 16 / (LUT_NW * 64); k++) {
+            const int i = threadIdx.x + k * LUT_NW * 64;
+            if (i < nx) {
+                const int o = (i >> 4) * 32 + ((i >> 3) & 1) * 16 + (i & 7);
+                split_store(xr[k], ks, &xh[o], &xh[o + 8]);
+            }
         }
     }
 
@@ -1181,8 +1257,11 @@ static int launch_lut_x(const LutArgs &a, int groups, int nkinds, int x31, void 
 
 extern "C" int wk_vq_lut(int fmt, const warp_job *jobs, const int *njobs, int max_jobs, int kind_lo, int nkinds,
                          const uint16_t *books, int books_x31, const float *x, int shared_x, float *part,
-                         size_t cap_floats, int M, int N, int target_blocks, int *splits_out, void *stream) {
+                         size_t cap_floats, int M, int N, int target_blocks, const float *act_part,
+                         int act_splits, int act_situ, float act_beta, float act_lbeta, int *splits_out,
+                         void *stream) {
     if (kind_lo < 0 || kind_lo + nkinds > 3 || !books || !part) return -1;
+    if (act_part && (shared_x || kind_lo != 2 || nkinds != 1 || act_splits <= 0)) return -1;
     int groups, splits;
     if (wk_lut_plan(M, N, max_jobs, nkinds, shared_x, target_blocks, cap_floats, &groups, &splits)) return -1;
     LutArgs a;
@@ -1197,6 +1276,11 @@ extern "C" int wk_vq_lut(int fmt, const warp_job *jobs, const int *njobs, int ma
     a.N = N;
     a.splits = splits;
     a.shared_x = shared_x;
+    a.act_part = act_part;
+    a.act_splits = act_splits;
+    a.act_situ = act_situ;
+    a.act_beta = act_beta;
+    a.act_lbeta = act_lbeta;
     if (splits_out) *splits_out = splits;
     switch (fmt) {
     case WARP_FMT_VQ3R: return launch_lut_x<WARP_FMT_VQ3R>(a, groups, nkinds, books_x31, stream);
@@ -1206,23 +1290,6 @@ extern "C" int wk_vq_lut(int fmt, const warp_job *jobs, const int *njobs, int ma
     return -1;
 }
 
-// Sum of a row's partials over the splits, in split order. Up to 32 splits
-// every load is issued before the first add (one memory latency per row).
-__device__ __forceinline__ float lut_rowsum(const float *p, int splits, size_t stride) {
-    if (splits <= 32) {
-        float a[32];
-#pragma unroll
-        for (int s = 0; s < 32; s++) a[s] = s < splits ? p[(size_t)s * stride] : 0.0f;
-        float v = 0.0f;
-#pragma unroll
-        for (int s = 0; s < 32; s++)
-            if (s < splits) v += a[s];
-        return v;
-    }
-    float v = 0.0f;
-    for (int s = 0; s < splits; s++) v += p[(size_t)s * stride];
-    return v;
-}
 
 // y_kind[yi][r] = (sum of the partials) * row scale, for every job of each kind.
 __global__ __launch_bounds__(256) void k_lut_reduce(const warp_job *__restrict__ jobs, const int *__restrict__ njobs,
@@ -1242,54 +1309,6 @@ extern "C" int wk_lut_reduce(const warp_job *jobs, const int *njobs, int max_job
     if (M <= 0 || max_jobs <= 0 || splits <= 0 || kind_lo < 0 || nkinds < 1 || kind_lo + nkinds > 3) return -1;
     hipLaunchKernelGGL(k_lut_reduce, dim3((M + 255) / 256, max_jobs, nkinds), dim3(256), 0, (hipStream_t)stream, jobs,
                        njobs, max_jobs, kind_lo, part, splits, M, y[0], y[1], y[2]);
-    CHECK_LAUNCH();
-    return 0;
-}
-
-// Sum of a row's partials over splits q, q + 4, q + 8, ... (a quarter), in order.
-__device__ __forceinline__ float lut_quartersum(const float *p, int q, int splits, size_t stride) {
-    float a[8];
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-        const int s = q + 4 * k;
-        a[k] = s < splits ? p[(size_t)s * stride] : 0.0f;
-    }
-    float v = 0.0f;
-#pragma unroll
-    for (int k = 0; k < 8; k++)
-        if (q + 4 * k < splits) v += a[k];
-    for (int s = q + 32; s < splits; s += 4) v += p[(size_t)s * stride];
-    return v;
-}
-
-// Decode: gate and up partials (kinds 0 and 1 of one k_vq_lut launch) ->
-// h[yi][r] = act(gate, up), in f32 (the input of the down table). One block
-// per (job, 64 rows): four threads per row sum a quarter of the splits each,
-// and the quarters are added in order.
-__global__ __launch_bounds__(256) void k_act_lut(const warp_job *__restrict__ jobs, const int *__restrict__ njobs,
-                                                 int max_jobs, const float *__restrict__ part, int splits, int I,
-                                                 int situ, float beta, float lbeta, float *__restrict__ h) {
-    __shared__ float qs[2][4][64];
-    const int j = blockIdx.y, row = threadIdx.x & 63, q = threadIdx.x >> 6, r = blockIdx.x * 64 + row;
-    if (j >= njobs[0]) return;                       // uniform per block
-    const size_t nrows = (size_t)((I + 63) >> 6) * 64, stride = (size_t)max_jobs * nrows;
-    if (r < I) {
-        qs[0][q][row] = lut_quartersum(part + (size_t)j * nrows + r, q, splits, stride);
-        qs[1][q][row] = lut_quartersum(part + (size_t)splits * stride + (size_t)j * nrows + r, q, splits, stride);
-    }
-    __syncthreads();
-    if (q != 0 || r >= I) return;
-    const warp_job &jg = jobs[j], &ju = jobs[(size_t)max_jobs + j];
-    const float g = (((qs[0][0][row] + qs[0][1][row]) + qs[0][2][row]) + qs[0][3][row]) * f16_keep(jg.scale[r]);
-    const float u = (((qs[1][0][row] + qs[1][1][row]) + qs[1][2][row]) + qs[1][3][row]) * f16_keep(ju.scale[r]);
-    h[(size_t)jg.yi[0] * I + r] = act_pair(g, u, situ, beta, lbeta);
-}
-
-extern "C" int wk_act_lut(const warp_job *jobs, const int *njobs, int max_jobs, const float *part, int splits, int I,
-                          int act_situ, float beta, float lbeta, float *h, void *stream) {
-    if (I <= 0 || max_jobs <= 0 || splits <= 0) return -1;
-    hipLaunchKernelGGL(k_act_lut, dim3((I + 63) / 64, max_jobs), dim3(256), 0, (hipStream_t)stream, jobs, njobs,
-                       max_jobs, part, splits, I, act_situ, beta, lbeta, h);
     CHECK_LAUNCH();
     return 0;
 }

@@ -117,13 +117,15 @@ int wk_lut_plan(int M, int N, int max_jobs, int nkinds, int shared_x, int target
                 size_t cap_floats, int *groups_out, int *splits_out);
 int wk_vq_lut(int fmt, const warp_job *jobs, const int *njobs, int max_jobs, int kind_lo,
               int nkinds, const uint16_t *books, int books_x31, const float *x, int shared_x, float *part,
-              size_t cap_floats, int M, int N, int target_blocks, int *splits_out, void *stream);
+              size_t cap_floats, int M, int N, int target_blocks, const float *act_part,
+              int act_splits, int act_situ, float act_beta, float act_lbeta, int *splits_out,
+              void *stream);
+/* (act_part: the down launch makes each job's input itself, h = act(gate,
+ * up) from the gate/up partial sums -- kinds 0 and 1 of the previous launch
+ * with act_splits splits -- instead of reading x; NULL otherwise.) */
 /* y[k][yi][r] = (sum over splits) * row scale, for the kinds of one LUT launch. */
 int wk_lut_reduce(const warp_job *jobs, const int *njobs, int max_jobs, int kind_lo, int nkinds,
                   const float *part, int splits, int M, float *const *y, void *stream);
-/* Decode: gate/up partials (one launch over kinds 0 and 1) -> h [yi][I] = act(g, u). */
-int wk_act_lut(const warp_job *jobs, const int *njobs, int max_jobs, const float *part, int splits,
-               int I, int act_situ, float beta, float lbeta, float *h, void *stream);
 /* Decode: down partials -> out [H] = sum_j w[j] * y_j in j order, + add0 + add1;
  * NaN everywhere when *missing is set. jobs2: the down job list. */
 int wk_combine_lut(const warp_job *jobs2, const float *part, int splits, int max_jobs,
