@@ -32,6 +32,12 @@ def cases(rng):
     out.append((lg, b))
     # all equal: the lowest ids in order
     out.append((np.full(E, 0.3), np.zeros(E)))
+    # distinct values except for one value shared by the 9th..15th largest,
+    # so the cut at K falls inside a run of ties and only its lowest ids go
+    lg = rng.normal(size=E)
+    order = np.argsort(-lg, kind="stable")
+    lg[order[8:15]] = lg[order[8]]
+    out.append((lg, None))
     return [(np.asarray(l, np.float32), None if b is None else np.asarray(b, np.float32)) for l, b in out]
 
 

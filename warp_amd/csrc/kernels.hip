@@ -462,57 +462,114 @@ __device__ __forceinline__ void route1_block(const float *__restrict__ logits, c
     __syncthreads();
     if (wave == 0) {
         // Lane l holds the keys of ids l, l + 64, ... (REGS: all in registers,
-        // E <= 512; else rescans LDS). A pick: the wave max key; the lowest id
-        // holding it (one ballot when it is unique, else a min over ids); the
-        // owner lane drops it and rescans, the other lanes keep their best
-        // (selects, no branches). Pick j stays in lane j.
+        // E <= 512; else rescans LDS). The picks of the reference's loop (max
+        // each time, strict >, lowest id on ties) are the K largest of
+        // (key, -id), in that order.
         constexpr int VPL = REGS ? 8 : 1;
-        int key[VPL];
-#pragma unroll
-        for (int m = 0; m < VPL; m++) {
-            const int e = lane + 64 * m;
-            key[m] = REGS && e < E ? route_key(biased[e]) : INT_MIN;
-        }
-        auto best_of = [&](int &bk, int &bid) {
-            bk = INT_MIN;
-            bid = 0x7fffffff;
-            if (REGS) {
-#pragma unroll
-                for (int m = 0; m < VPL; m++) {
-                    const bool b = key[m] > bk;
-                    bk = b ? key[m] : bk;
-                    bid = b ? lane + 64 * m : bid;
-                }
-            } else {
-                for (int e = lane; e < E; e += 64) {
-                    const int k = route_key(biased[e]);
-                    if (k > bk) { bk = k; bid = e; }
-                }
-            }
-        };
-        int bk, bid;
-        best_of(bk, bid);
         int mine = 0, npick = 0;
-        for (int j = 0; j < K; j++) {
-            const int m = wave_reduce_i<true>(bk);
-            if (m == INT_MIN) break;          // nothing pickable is left (uniform)
-            const unsigned long long hit = __ballot(bk == m);
-            int e;
-            if (__popcll(hit) == 1) e = __builtin_amdgcn_readlane(bid, __ffsll((long long)hit) - 1);
-            else e = wave_reduce_i<false>(bk == m ? bid : 0x7fffffff);
-            mine = lane == j ? e : mine;
-            npick = j + 1;
-            const bool own = (e & 63) == lane;
-            if (REGS) {
+        bool done = false;
+        if (REGS) {
+            // Order-preserving unsigned keys, 0 for the unpickable. The K-th
+            // largest lane maximum t0 bounds the K-th largest key from below
+            // (the maxima are K elements of the set), so the picks are among
+            // the keys >= max(t0, 1). When those survivors fit one per lane
+            // (the usual case), each ranks itself among them by the packed
+            // (key, ~id); otherwise the pick loop below runs.
+            __shared__ unsigned long long ck[64];
+            __shared__ int ord[64];
+            unsigned u[VPL], mx = 0;
 #pragma unroll
-                for (int q = 0; q < VPL; q++) key[q] = own && q == (e >> 6) ? INT_MIN : key[q];
-                int nk, ni;
-                best_of(nk, ni);
-                bk = own ? nk : bk;
-                bid = own ? ni : bid;
-            } else if (own) {
-                biased[e] = -INFINITY;
-                best_of(bk, bid);
+            for (int m = 0; m < VPL; m++) {
+                const int e = lane + 64 * m;
+                u[m] = e < E ? (unsigned)route_key(biased[e]) ^ 0x80000000u : 0u;
+                mx = u[m] > mx ? u[m] : mx;
+            }
+            unsigned t0 = 0;
+#pragma unroll
+            for (int bit = 31; bit >= 0; bit--) {
+                const unsigned cand = t0 | (1u << bit);
+                if (__popcll(__ballot(mx >= cand)) >= K) t0 = cand;
+            }
+            const unsigned lo = t0 ? t0 : 1u;
+            const unsigned long long below = (1ull << lane) - 1ull;
+            int n = 0;
+#pragma unroll
+            for (int m = 0; m < VPL; m++) {
+                const bool sv = u[m] >= lo;
+                const unsigned long long bm = __ballot(sv);
+                const int p = n + __popcll(bm & below);
+                if (sv && p < 64) ck[p] = ((unsigned long long)u[m] << 32) | (unsigned)~(lane + 64 * m);
+                n += __popcll(bm);
+            }
+            if (n <= 64) {                                 // uniform
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                if (lane < n) {
+                    const unsigned long long me = ck[lane];
+                    int r = 0;
+                    for (int i = 0; i < n; i++) r += ck[i] > me;
+                    if (r < K) ord[r] = (int)~(unsigned)me;
+                }
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                npick = n < K ? n : K;
+                mine = lane < npick ? ord[lane] : 0;
+                done = true;
+            }
+        }
+        if (!done) {
+            // A pick: the wave max key; the lowest id holding it (one ballot
+            // when it is unique, else a min over ids); the owner lane drops it
+            // and rescans, the other lanes keep their best (selects, no
+            // branches). Pick j stays in lane j.
+            int key[VPL];
+#pragma unroll
+            for (int m = 0; m < VPL; m++) {
+                const int e = lane + 64 * m;
+                key[m] = REGS && e < E ? route_key(biased[e]) : INT_MIN;
+            }
+            auto best_of = [&](int &bk, int &bid) {
+                bk = INT_MIN;
+                bid = 0x7fffffff;
+                if (REGS) {
+#pragma unroll
+                    for (int m = 0; m < VPL; m++) {
+                        const bool b = key[m] > bk;
+                        bk = b ? key[m] : bk;
+                        bid = b ? lane + 64 * m : bid;
+                    }
+                } else {
+                    for (int e = lane; e < E; e += 64) {
+                        const int k = route_key(biased[e]);
+                        if (k > bk) { bk = k; bid = e; }
+                    }
+                }
+            };
+            int bk, bid;
+            best_of(bk, bid);
+            for (int j = 0; j < K; j++) {
+                const int m = wave_reduce_i<true>(bk);
+                if (m == INT_MIN) break;          // nothing pickable is left (uniform)
+                const unsigned long long hit = __ballot(bk == m);
+                int e;
+                if (__popcll(hit) == 1) e = __builtin_amdgcn_readlane(bid, __ffsll((long long)hit) - 1);
+                else e = wave_reduce_i<false>(bk == m ? bid : 0x7fffffff);
+                mine = lane == j ? e : mine;
+                npick = j + 1;
+                const bool own = (e & 63) == lane;
+                if (REGS) {
+#pragma unroll
+                    for (int q = 0; q < VPL; q++) key[q] = own && q == (e >> 6) ? INT_MIN : key[q];
+                    int nk, ni;
+                    best_of(nk, ni);
+                    bk = own ? nk : bk;
+                    bid = own ? ni : bid;
+                } else if (own) {
+                    biased[e] = -INFINITY;
+                    best_of(bk, bid);
+                }
             }
         }
         // weights: the sum in pick order (one lane, as the reference), the
@@ -605,6 +662,10 @@ template <> struct Word<3> {
         const unsigned *q = (const unsigned *)p;
         w = u3v{__builtin_nontemporal_load(q), __builtin_nontemporal_load(q + 1), __builtin_nontemporal_load(q + 2)};
     }
+    __device__ __forceinline__ void load_keep(const uint8_t *p) {
+        const unsigned *q = (const unsigned *)p;
+        w = u3v{q[0], q[1], q[2]};
+    }
     // 24-bit slot of row t (0..3)
     __device__ __forceinline__ unsigned slot(int t) const {
         switch (t) {
@@ -620,6 +681,10 @@ template <> struct Word<2> {
     __device__ __forceinline__ void load(const uint8_t *p) {
         const unsigned *q = (const unsigned *)p;
         w = u2v{__builtin_nontemporal_load(q), __builtin_nontemporal_load(q + 1)};
+    }
+    __device__ __forceinline__ void load_keep(const uint8_t *p) {
+        const unsigned *q = (const unsigned *)p;
+        w = u2v{q[0], q[1]};
     }
     __device__ __forceinline__ unsigned slot(int t) const {
         switch (t) {
@@ -1144,7 +1209,7 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
 
     Word<F::SB> wd[LUT_PPW];
 #pragma unroll
-    for (int q = 0; q < LUT_PPW; q++) wd[q].load(cp[q] + (size_t)(2 * c0) * 64 * F::SB);
+    for (int q = 0; q < LUT_PPW; q++) wd[q].load_keep(cp[q] + (size_t)(2 * c0) * 64 * F::SB);
     float acc[LUT_PPW][4];
 #pragma unroll
     for (int q = 0; q < LUT_PPW; q++)
@@ -1181,7 +1246,7 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
                 else build_mfma(B, b ^ 1, q);
             }
             const Word<F::SB> w = wd[q];
-            wd[q].load(cp[q] + (size_t)(2 * cn) * 64 * F::SB);
+            wd[q].load_keep(cp[q] + (size_t)(2 * cn) * 64 * F::SB);
 #pragma unroll
             for (int t = 0; t < 4; t++) {
                 const unsigned sl = w.slot(t);
