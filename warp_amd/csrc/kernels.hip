@@ -148,9 +148,10 @@ extern "C" int wk_split(const float *x, int T, int N, uint16_t *xs, float *xscal
 
 // ---- router logits --------------------------------------------------------------
 
-// One 256-thread block per (token, row): eight float4 loads in flight per
-// thread, lane partials, then a fixed-order block sum (deterministic).
-// One logit row per 256-thread block (row = t * E + e), returned in thread 0.
+// One 256-thread block per (token, row): up to eight float4 loads of W and x
+// in flight per thread (all issued before the first multiply-add), lane
+// partials in ascending index order, then a fixed-order block sum
+// (deterministic). Returned in thread 0.
 __device__ __forceinline__ float router_row_fast(const float *__restrict__ W, const float *__restrict__ x, int E,
                                                  int H, int row) {
     __shared__ float part[4];
@@ -160,25 +161,23 @@ __device__ __forceinline__ float router_row_fast(const float *__restrict__ W, co
     if ((H & 3) == 0) {
         const float4 *w4 = (const float4 *)w, *x4 = (const float4 *)xt;
         const int n4 = H >> 2;
-        int i = threadIdx.x;
-        for (; i + 7 * 256 < n4; i += 8 * 256) {
+        for (int i0 = threadIdx.x; i0 < n4; i0 += 8 * 256) {
             float4 a[8], b[8];
 #pragma unroll
-            for (int k = 0; k < 8; k++) { a[k] = w4[i + k * 256]; b[k] = x4[i + k * 256]; }
+            for (int k = 0; k < 8; k++) {
+                const int i = min(i0 + k * 256, n4 - 1);
+                a[k] = w4[i];
+                b[k] = x4[i];
+            }
 #pragma unroll
             for (int k = 0; k < 8; k++) {
-                acc = __builtin_fmaf(a[k].x, b[k].x, acc);
-                acc = __builtin_fmaf(a[k].y, b[k].y, acc);
-                acc = __builtin_fmaf(a[k].z, b[k].z, acc);
-                acc = __builtin_fmaf(a[k].w, b[k].w, acc);
+                if (i0 + k * 256 < n4) {
+                    acc = __builtin_fmaf(a[k].x, b[k].x, acc);
+                    acc = __builtin_fmaf(a[k].y, b[k].y, acc);
+                    acc = __builtin_fmaf(a[k].z, b[k].z, acc);
+                    acc = __builtin_fmaf(a[k].w, b[k].w, acc);
+                }
             }
-        }
-        for (; i < n4; i += 256) {
-            const float4 a = w4[i], b = x4[i];
-            acc = __builtin_fmaf(a.x, b.x, acc);
-            acc = __builtin_fmaf(a.y, b.y, acc);
-            acc = __builtin_fmaf(a.z, b.z, acc);
-            acc = __builtin_fmaf(a.w, b.w, acc);
         }
     } else {
         for (int i = threadIdx.x; i < H; i += 256) acc = __builtin_fmaf(w[i], xt[i], acc);
@@ -654,6 +653,10 @@ template <> struct FmtT<WARP_FMT_VQ3R> { static constexpr int S = 3, E = 256, SB
 template <> struct FmtT<WARP_FMT_VQ2R> { static constexpr int S = 2, E = 256, SB = 2; };
 template <> struct FmtT<WARP_FMT_VQ12> { static constexpr int S = 2, E = 4096, SB = 3; };
 
+// Device memory seen as global (not generic) memory, so that loads through
+// pointers read from job lists are global loads.
+typedef const __attribute__((address_space(1))) unsigned gu32;
+
 // Code word of 4 consecutive rows at one position, as loaded by a lane.
 template <int SB> struct Word;
 template <> struct Word<3> {
@@ -663,7 +666,7 @@ template <> struct Word<3> {
         w = u3v{__builtin_nontemporal_load(q), __builtin_nontemporal_load(q + 1), __builtin_nontemporal_load(q + 2)};
     }
     __device__ __forceinline__ void load_keep(const uint8_t *p) {
-        const unsigned *q = (const unsigned *)p;
+        const gu32 *q = (const gu32 *)p;
         w = u3v{q[0], q[1], q[2]};
     }
     // 24-bit slot of row t (0..3)
@@ -683,7 +686,7 @@ template <> struct Word<2> {
         w = u2v{__builtin_nontemporal_load(q), __builtin_nontemporal_load(q + 1)};
     }
     __device__ __forceinline__ void load_keep(const uint8_t *p) {
-        const unsigned *q = (const unsigned *)p;
+        const gu32 *q = (const gu32 *)p;
         w = u2v{q[0], q[1]};
     }
     __device__ __forceinline__ unsigned slot(int t) const {
@@ -995,6 +998,7 @@ constexpr int LUT_PPW = 4;                 // row-block pairs per wave
 constexpr int LUT_PAIRS = LUT_NW * LUT_PPW;
 constexpr int LUT_RBG = 2 * LUT_PAIRS;     // row blocks per row group
 constexpr int LUT_XCH = 256;               // chunks of x a split stages in LDS (16 KiB)
+constexpr int ACT_LD = 8;                  // staged partial-sum loads per thread (down prologue)
 
 struct LutArgs {
     const warp_job *jobs;
@@ -1030,6 +1034,34 @@ __device__ __forceinline__ float lut_rowsum(const float *p, int splits, size_t s
     return v;
 }
 
+// The same sum for at most MAXS splits: MAXS loads issued unconditionally
+// (indices past the last split repeat it), then the adds in split order.
+template <int MAXS>
+__device__ __forceinline__ float lut_rowsum_n(const float *p, int splits, size_t stride) {
+    float a[MAXS];
+#pragma unroll
+    for (int s = 0; s < MAXS; s++) a[s] = p[(size_t)min(s, splits - 1) * stride];
+    float v = 0.0f;
+#pragma unroll
+    for (int s = 0; s < MAXS; s++)
+        if (s < splits) v += a[s];
+    return v;
+}
+
+// The same sum with at most 8 loads in flight (few registers).
+__device__ __forceinline__ float lut_rowsum8(const float *p, int splits, size_t stride) {
+    float v = 0.0f;
+    for (int s0 = 0; s0 < splits; s0 += 8) {
+        float a8[8];
+#pragma unroll
+        for (int s = 0; s < 8; s++) a8[s] = p[(size_t)min(s0 + s, splits - 1) * stride];
+#pragma unroll
+        for (int s = 0; s < 8; s++)
+            if (s0 + s < splits) v += a8[s];
+    }
+    return v;
+}
+
 template <int FMT>
 __device__ __forceinline__ unsigned lut_code(unsigned slot, int s) {
     if (FMT == WARP_FMT_VQ12) return s == 0 ? (slot & 0xFFFu) : (slot >> 12);
@@ -1043,8 +1075,9 @@ __device__ __forceinline__ half4 half4_of(uint32_t lo, uint32_t hi) {
 }
 
 // SHX = true: the jobs of the list share one input and a row group spans
-// them (gate and up); false: one input per job (down).
-template <int FMT, bool X31, bool SHX>
+// them (gate and up); false: one input per job (down). ACT (with SHX false):
+// the inputs are made from the gate/up partial sums (a.act_part).
+template <int FMT, bool X31, bool SHX, bool ACT>
 __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
     typedef FmtT<FMT> F;
     constexpr int SE = F::S * F::E;                        // table entries per position
@@ -1054,43 +1087,96 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
     static_assert(SE % 64 == 0, "table groups");
     extern __shared__ __attribute__((aligned(16))) float lut[];   // [2][S][E][2], then x of the split
     const int kind = a.kind_lo + blockIdx.y;
-    const int nj = a.njobs[kind];
     const warp_job *jobs = a.jobs + (size_t)kind * a.max_jobs;
     const int nv = a.N >> 3, nrb = (a.M + 63) >> 6, nc = nv >> 1;
     const int grp = blockIdx.x / a.splits, split = blockIdx.x % a.splits;
-    int fb0, fb_end, xj;
+    const int c0 = split * nc / a.splits, c1 = (split + 1) * nc / a.splits;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int pl = (lane >> 4) & 1, rbsel = lane >> 5, quad = lane & 15;
+    int fb0, xj;
     if (SHX) {
         fb0 = grp * LUT_RBG;
-        fb_end = nj * nrb;
         xj = 0;
     } else {
         const int gpj = (nrb + LUT_RBG - 1) / LUT_RBG;
         xj = grp / gpj;
         fb0 = xj * nrb + (grp % gpj) * LUT_RBG;
-        fb_end = xj < nj ? (xj + 1) * nrb : 0;
     }
-    const int c0 = split * nc / a.splits, c1 = (split + 1) * nc / a.splits;
-    if (fb0 >= fb_end || c0 >= c1) return;                 // uniform per block
-    const float *xin = a.x + (size_t)jobs[xj].xi[0] * a.N;
+    constexpr bool act = ACT && !SHX;
+    const int nx = (c1 - c0) * 16;                         // inputs of this split
+    constexpr int XPT = LUT_XCH * 16 / (LUT_NW * 64);      // inputs per thread, at most
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int pl = (lane >> 4) & 1, rbsel = lane >> 5, quad = lane & 15;
-    // Pairs past the group's rows read row block 0 of the block's first job
-    // (in bounds) and are never written: the loop below has no per-pair
-    // branches, so the code-word loads of the next chunk stay in flight
-    // across the whole chunk and the LDS reads of all pairs overlap.
-    const uint8_t *cp[LUT_PPW];
-    const int jfirst = fb0 / nrb;
+    // The prologue issues its loads in the order their data is needed and
+    // waits for no load it does not use (loads complete in issue order).
+    // 1. The job list, written by the routing launch: the record of every
+    //    pair (the job of a pair follows from the block's position; the job
+    //    count, read alongside, only decides which pairs are real), the
+    //    input index and, for the down launch, the gate/up row scales.
+    const uint8_t *jrec[LUT_PPW];
 #pragma unroll
     for (int q = 0; q < LUT_PPW; q++) {
         const int fb = fb0 + 2 * (q * LUT_NW + wave) + rbsel;
-        const bool ok = fb < fb_end;
-        const int j = ok ? fb / nrb : jfirst, rb = ok ? fb % nrb : 0;
-        cp[q] = jobs[j].idx + ((size_t)rb * nv + pl) * 64 * F::SB + (size_t)quad * 4 * F::SB;
+        jrec[q] = jobs[min(fb / nrb, a.max_jobs - 1)].idx;
     }
+    const uint8_t *jrec0 = jobs[fb0 / nrb].idx;
+    const int xi = act ? 0 : jobs[xj].xi[0];
+    gu32 *sg = act ? (gu32 *)a.jobs[xj].scale : nullptr;
+    gu32 *su = act ? (gu32 *)a.jobs[(size_t)a.max_jobs + xj].scale : nullptr;
+    const int nj = a.njobs[kind];
 
-    // codebook: group G = wave * GPW + g holds entries 64 G .. 64 G + 63 over
-    // [stage][entry], entry 64 G + lane in this lane
+    // 2. Down launch: the gate/up partial sums of this split's inputs, rows
+    //    [kind 0, 1][split s] of nx values, spread over the block (one load
+    //    per thread per row-chunk; indices past the end are clamped and their
+    //    values dropped), to be staged in the table buffers.
+    const size_t arows = (size_t)((a.N + 63) >> 6) * 64, astride = (size_t)a.max_jobs * arows;
+    const int atot = act ? 2 * a.act_splits * nx : 0;
+    const bool astage = act && atot <= ACT_LD * LUT_NW * 64 && atot <= 2 * BUF;   // uniform
+    float av[ACT_LD];
+    if (astage) {
+        const float *pa = a.act_part + (size_t)xj * arows + (size_t)c0 * 16;
+        const int drow = (LUT_NW * 64) / nx, dv = (LUT_NW * 64) % nx, rmax = 2 * a.act_splits - 1;
+        int row = threadIdx.x / nx, v = threadIdx.x % nx;
+#pragma unroll
+        for (int k = 0; k < ACT_LD; k++) {
+            av[k] = pa[(size_t)min(row, rmax) * astride + v];
+            row += drow;
+            v += dv;
+            if (v >= nx) { v -= nx; row++; }
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    const int fb_end = SHX ? nj * nrb : (xj < nj ? (xj + 1) * nrb : 0);
+    if (fb0 >= fb_end || c0 >= c1) return;                 // uniform per block
+
+    // 3. The input: read, or (down launch) the gate/up row scales to make it
+    //    with, as the 4-byte words that hold them (the scale arrays of a
+    //    record are 4-byte aligned and a split starts at an even input).
+    //    Only jobs below the count are dereferenced.
+    float xr[XPT];
+    unsigned gs[XPT], us[XPT];
+    if constexpr (act) {
+#pragma unroll
+        for (int k = 0; k < XPT; k++) {
+            const int i = min((int)threadIdx.x + k * LUT_NW * 64, nx - 1) + c0 * 16;
+            gs[k] = sg[i >> 1];
+            us[k] = su[i >> 1];
+        }
+    } else {
+        const float *xg = a.x + (size_t)xi * a.N + (size_t)c0 * 16;
+#pragma unroll
+        for (int k = 0; k < XPT; k++) {
+            const int i = threadIdx.x + k * LUT_NW * 64;
+            const float v = xg[min(i, nx - 1)];
+            xr[k] = i < nx ? v : 0.0f;
+        }
+    }
+    // 4. The codebook of this kind (group G = wave * GPW + g holds entries
+    //    64 G .. 64 G + 63 over [stage][entry], entry 64 G + lane in this
+    //    lane), 128 KiB per block for 2 x 4096 entries, which the first
+    //    table build needs, then the code words of the first chunk, which
+    //    the loop needs.
+    __builtin_amdgcn_sched_barrier(0);
     uint4 cb[GPW];
     const uint4 *bk = (const uint4 *)(a.books + (size_t)kind * SE * 8);
 #pragma unroll
@@ -1098,33 +1184,66 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
         const int G = wave * GPW + g;
         cb[g] = G < NG ? bk[G * 64 + lane] : make_uint4(0u, 0u, 0u, 0u);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    // Pairs past the group's rows read row block 0 of the block's first job
+    // (in bounds) and are never written: the loop below has no per-pair
+    // branches, so the code-word loads of the next chunk stay in flight
+    // across the whole chunk and the LDS reads of all pairs overlap.
+    const uint8_t *cp[LUT_PPW];
+#pragma unroll
+    for (int q = 0; q < LUT_PPW; q++) {
+        const int fb = fb0 + 2 * (q * LUT_NW + wave) + rbsel;
+        const bool ok = fb < fb_end;
+        const int rb = fb - (fb / nrb) * nrb;
+        const size_t off = (size_t)(ok ? rb : 0) * nv * 64 * F::SB;
+        cp[q] = (ok ? jrec[q] : jrec0) + off + (size_t)pl * 64 * F::SB + (size_t)quad * 4 * F::SB;
+    }
+    Word<F::SB> wd[LUT_PPW];
+#pragma unroll
+    for (int q = 0; q < LUT_PPW; q++) wd[q].load_keep(cp[q] + (size_t)(2 * c0) * 64 * F::SB);
+    __builtin_amdgcn_sched_barrier(0);
 
-    // x of this split (at most LUT_XCH x 16 values, 4 per thread) into
-    // registers: read from the input, or made from the gate/up partials
-    const int nx = (c1 - c0) * 16;
-    const float *xg = xin + (size_t)c0 * 16;
-    float xr[LUT_XCH * 16 / (LUT_NW * 64)];
-    if (!SHX && a.act_part) {
-        const size_t arows = (size_t)((a.N + 63) >> 6) * 64, astride = (size_t)a.max_jobs * arows;
-        const warp_job &jg = a.jobs[xj], &ju = a.jobs[(size_t)a.max_jobs + xj];
-        const float *pg = a.act_part + (size_t)xj * arows + (size_t)c0 * 16;
-        const float *pu = pg + (size_t)a.act_splits * astride;
-        const uint16_t *sg = jg.scale + (size_t)c0 * 16, *su = ju.scale + (size_t)c0 * 16;
+    // 5. Down launch: h = act(gate, up) from the partial sums, added over the
+    //    splits in split order (through the staging area when it fits).
+    if constexpr (act) {
+        if (astage) {
+            const int drow = (LUT_NW * 64) / nx, dv = (LUT_NW * 64) % nx;
+            int row = threadIdx.x / nx, v = threadIdx.x % nx;
 #pragma unroll
-        for (int k = 0; k < LUT_XCH * 16 / (LUT_NW * 64); k++) {
-            const int i = threadIdx.x + k * LUT_NW * 64;
-            xr[k] = 0.0f;
-            if (i < nx) {
-                const float g = lut_rowsum(pg + i, a.act_splits, astride) * f16_keep(sg[i]);
-                const float u = lut_rowsum(pu + i, a.act_splits, astride) * f16_keep(su[i]);
-                xr[k] = act_pair(g, u, a.act_situ, a.act_beta, a.act_lbeta);
+            for (int k = 0; k < ACT_LD; k++) {
+                if (row * nx + v < atot) lut[row * nx + v] = av[k];
+                row += drow;
+                v += dv;
+                if (v >= nx) { v -= nx; row++; }
             }
-        }
-    } else {
+            __syncthreads();
 #pragma unroll
-        for (int k = 0; k < LUT_XCH * 16 / (LUT_NW * 64); k++) {
-            const int i = threadIdx.x + k * LUT_NW * 64;
-            xr[k] = i < nx ? xg[i] : 0.0f;
+            for (int k = 0; k < XPT; k++) {
+                const int i = threadIdx.x + k * LUT_NW * 64;
+                xr[k] = 0.0f;
+                if (i < nx) {
+                    float g = 0.0f, u = 0.0f;
+                    for (int s2 = 0; s2 < a.act_splits; s2++) g += lut[s2 * nx + i];
+                    for (int s2 = 0; s2 < a.act_splits; s2++) u += lut[(a.act_splits + s2) * nx + i];
+                    const int sh = 16 * (i & 1);
+                    xr[k] = act_pair(g * f16_keep((uint16_t)(gs[k] >> sh)), u * f16_keep((uint16_t)(us[k] >> sh)),
+                                     a.act_situ, a.act_beta, a.act_lbeta);
+                }
+            }
+        } else {
+            const float *pg = a.act_part + (size_t)xj * arows + (size_t)c0 * 16;
+            const float *pu = pg + (size_t)a.act_splits * astride;
+#pragma unroll
+            for (int k = 0; k < XPT; k++) {
+                const int i = threadIdx.x + k * LUT_NW * 64;
+                xr[k] = 0.0f;
+                if (i < nx) {
+                    const int sh = 16 * (i & 1);
+                    const float g = lut_rowsum8(pg + i, a.act_splits, astride) * f16_keep((uint16_t)(gs[k] >> sh));
+                    const float u = lut_rowsum8(pu + i, a.act_splits, astride) * f16_keep((uint16_t)(us[k] >> sh));
+                    xr[k] = act_pair(g, u, a.act_situ, a.act_beta, a.act_lbeta);
+                }
+            }
         }
     }
     // -> LDS: f32 [chunk][16] (X31) or the scaled fp16 halves
@@ -1133,18 +1252,18 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
     if constexpr (X31) {
         float *xst = lut + 2 * BUF;
 #pragma unroll
-        for (int k = 0; k < LUT_XCH * 16 / (LUT_NW * 64); k++) {
+        for (int k = 0; k < XPT; k++) {
             const int i = threadIdx.x + k * LUT_NW * 64;
             if (i < nx) xst[i] = xr[k];
         }
     } else {
         float m = 0.0f;
 #pragma unroll
-        for (int k = 0; k < LUT_XCH * 16 / (LUT_NW * 64); k++) m = fmaxf(m, fabsf(xr[k]));
+        for (int k = 0; k < XPT; k++) m = fmaxf(m, fabsf(xr[k]));
         ks = split_exp(block_absmax(m));
         _Float16 *xh = (_Float16 *)(lut + 2 * BUF);
 #pragma unroll
-        for (int k = 0; k < LUT_XCH * 16 / (LUT_NW * 64); k++) {
+        for (int k = 0; k < XPT; k++) {
             const int i = threadIdx.x + k * LUT_NW * 64;
             if (i < nx) {
                 const int o = (i >> 4) * 32 + ((i >> 3) & 1) * 16 + (i & 7);
@@ -1207,9 +1326,6 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
         }
     };
 
-    Word<F::SB> wd[LUT_PPW];
-#pragma unroll
-    for (int q = 0; q < LUT_PPW; q++) wd[q].load_keep(cp[q] + (size_t)(2 * c0) * 64 * F::SB);
     float acc[LUT_PPW][4];
 #pragma unroll
     for (int q = 0; q < LUT_PPW; q++)
@@ -1293,19 +1409,19 @@ extern "C" int wk_lut_plan(int M, int N, int max_jobs, int nkinds, int shared_x,
     return 0;
 }
 
-template <int FMT, bool X31, bool SHX>
+template <int FMT, bool X31, bool SHX, bool ACT>
 static int launch_lut(const LutArgs &a, int groups, int nkinds, void *stream) {
     typedef FmtT<FMT> F;
     const size_t lds = ((size_t)2 * 2 * F::S * F::E + LUT_XCH * 16) * sizeof(float);
     if (lds > 163840) return -2;
     static bool attr = false;
     if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_vq_lut<FMT, X31, SHX>,
+        hipError_t e = hipFuncSetAttribute((const void *)k_vq_lut<FMT, X31, SHX, ACT>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return -(int)e - 1000;
         attr = true;
     }
-    hipLaunchKernelGGL((k_vq_lut<FMT, X31, SHX>), dim3(groups * a.splits, nkinds), dim3(LUT_NW * 64), lds,
+    hipLaunchKernelGGL((k_vq_lut<FMT, X31, SHX, ACT>), dim3(groups * a.splits, nkinds), dim3(LUT_NW * 64), lds,
                        (hipStream_t)stream, a);
     CHECK_LAUNCH();
     return 0;
@@ -1314,10 +1430,13 @@ static int launch_lut(const LutArgs &a, int groups, int nkinds, void *stream) {
 template <int FMT>
 static int launch_lut_x(const LutArgs &a, int groups, int nkinds, int x31, void *stream) {
     if (a.shared_x)
-        return x31 ? launch_lut<FMT, true, true>(a, groups, nkinds, stream)
-                   : launch_lut<FMT, false, true>(a, groups, nkinds, stream);
-    return x31 ? launch_lut<FMT, true, false>(a, groups, nkinds, stream)
-               : launch_lut<FMT, false, false>(a, groups, nkinds, stream);
+        return x31 ? launch_lut<FMT, true, true, false>(a, groups, nkinds, stream)
+                   : launch_lut<FMT, false, true, false>(a, groups, nkinds, stream);
+    if (a.act_part)
+        return x31 ? launch_lut<FMT, true, false, true>(a, groups, nkinds, stream)
+                   : launch_lut<FMT, false, false, true>(a, groups, nkinds, stream);
+    return x31 ? launch_lut<FMT, true, false, false>(a, groups, nkinds, stream)
+               : launch_lut<FMT, false, false, false>(a, groups, nkinds, stream);
 }
 
 extern "C" int wk_vq_lut(int fmt, const warp_job *jobs, const int *njobs, int max_jobs, int kind_lo, int nkinds,
@@ -1381,30 +1500,47 @@ extern "C" int wk_lut_reduce(const warp_job *jobs, const int *njobs, int max_job
 // Decode: down partials -> out[r] = sum_j w[j] * y_j[r] in selection order
 // (unfused, as k_combine), + add0 + add1. One block per 16 rows: the K
 // expert outputs of those rows are reduced in parallel into LDS (one thread
-// per expert and row), then one thread per row combines them in order.
+// per expert and row), then one thread per row combines them in order. Every
+// load that does not depend on another is issued first (the partial sums,
+// the weights, the addends); only the row scale waits for its job entry.
 __global__ __launch_bounds__(256) void k_combine_lut(const warp_job *__restrict__ jobs2, const float *__restrict__ part,
                                                      int splits, int max_jobs, const float *__restrict__ w, int K,
                                                      int H, const float *add0, const float *add1,
                                                      const int *missing, float *__restrict__ out) {
     __shared__ float yd[WARP_MAX_K][16];
+    __shared__ float wl[WARP_MAX_K];
     const int r0 = blockIdx.x * 16, row = threadIdx.x & 15, jq = threadIdx.x >> 4;
-    const bool miss = missing && *missing;
+    const int i = min(r0 + row, H - 1);
     const size_t nrows = (size_t)((H + 63) >> 6) * 64, stride = (size_t)max_jobs * nrows;
-    if (!miss && r0 + row < H)
-        for (int j = jq; j < K; j += 16)
-            yd[j][row] = lut_rowsum(part + (size_t)j * nrows + r0 + row, splits, stride) *
-                         f16_keep(jobs2[j].scale[r0 + row]);
+    // (volatile: read here, not after the barrier where it is used)
+    const bool miss = missing && *(volatile const int *)missing;
+    const float wv = threadIdx.x < K ? w[threadIdx.x] : 0.0f;
+    const float a0 = jq == 0 && add0 ? add0[i] : 0.0f;
+    const float a1 = jq == 0 && add1 ? add1[i] : 0.0f;
+    // expert j's output at row i: its partial sums, then times the row scale
+    // (the scale arrays of a record are 4-byte aligned: the word holding row
+    // i's scale; a missing expert has no scale pointer)
+    auto expert_row = [&](int j, float v) {
+        gu32 *sc = (gu32 *)jobs2[j].scale;
+        const unsigned sw = sc ? sc[i >> 1] : 0u;
+        yd[j][row] = v * f16_keep((uint16_t)(sw >> (16 * (i & 1))));
+    };
+    if (K <= 16 && splits <= 16) {                         // one expert per thread
+        if (jq < K) expert_row(jq, lut_rowsum_n<16>(part + (size_t)jq * nrows + i, splits, stride));
+    } else {
+        for (int j = jq; j < K; j += 16) expert_row(j, lut_rowsum8(part + (size_t)j * nrows + i, splits, stride));
+    }
+    if (threadIdx.x < K) wl[threadIdx.x] = wv;
     __syncthreads();
     if (jq != 0 || r0 + row >= H) return;
-    const int i = r0 + row;
     if (miss) {                         // a selected expert was not computed
         out[i] = __builtin_nanf("");
         return;
     }
     float s = 0.0f;
-    for (int j = 0; j < K; j++) s = __fadd_rn(s, __fmul_rn(w[j], yd[j][row]));
-    if (add0) s = __fadd_rn(s, add0[i]);
-    if (add1) s = __fadd_rn(s, add1[i]);
+    for (int j = 0; j < K; j++) s = __fadd_rn(s, __fmul_rn(wl[j], yd[j][row]));
+    if (add0) s = __fadd_rn(s, a0);
+    if (add1) s = __fadd_rn(s, a1);
     out[i] = s;
 }
 
