@@ -1132,12 +1132,16 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
     if ((rc = timing_end(c))) return rc;
     const int n_la = lookahead_launch(c, layer, x_dev);
     if (n_la < 0) return n_la;
+    /* where the device routes with the expert table, the table kernel's
+     * gate/up launch does the routing itself (one launch less) */
+    const int fuse_route = use_lut && (L->resident == E || !c->fetch) && wk_lut_route_ok(g->fmt, E, K, 1, 0, 2);
     if (L->resident == E) {
         /* everything resident: route and build the jobs on the device, no
          * host round trip */
         KRN(c, wait_copies(c));
-        KRN(c, wk_route(c->logits, L->bias, E, K, 1, g->router_act, g->renorm, g->routed_scale, c->idx, c->w, table,
-                        c->jobs, c->njobs, c->missing, I, c->st));
+        if (!fuse_route)
+            KRN(c, wk_route(c->logits, L->bias, E, K, 1, g->router_act, g->renorm, g->routed_scale, c->idx, c->w,
+                            table, c->jobs, c->njobs, c->missing, I, c->st));
         c->stats.hits += (uint64_t)K;
         if (c->pin_layer == layer) c->pin_layer = -1;
     } else if (!c->fetch) {
@@ -1145,8 +1149,9 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
          * not resident (sticky), the combine poisons this layer's output with
          * NaN, and the next synchronising call reports E_MISSING */
         KRN(c, wait_copies(c));
-        KRN(c, wk_route(c->logits, L->bias, E, K, 1, g->router_act, g->renorm, g->routed_scale, c->idx, c->w, table,
-                        c->jobs, c->njobs, c->missing, I, c->st));
+        if (!fuse_route)
+            KRN(c, wk_route(c->logits, L->bias, E, K, 1, g->router_act, g->renorm, g->routed_scale, c->idx, c->w,
+                            table, c->jobs, c->njobs, c->missing, I, c->st));
         c->missing_pending = 1;
         if (c->pin_layer == layer) c->pin_layer = -1;
     } else {
@@ -1167,9 +1172,11 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
     size_t d_off = 0;
     if (use_lut) {
         int sp_gu = 0;
+        const warp_route_args ra = { c->logits, L->bias, table, E, g->router_act, g->renorm, I, g->routed_scale,
+                                     c->idx, c->w, c->jobs, c->njobs, c->missing };
         if ((rc = timing_begin(c, 0))) return rc;
         KRN(c, wk_vq_lut(g->fmt, c->jobs, c->njobs, K, 0, 2, L->books, L->books_x31, x_dev, 1, c->part, c->part_cap, I, H,
-                         c->n_cu, NULL, 0, 0, 0.0f, 0.0f, &sp_gu, c->st));
+                         c->n_cu, NULL, 0, 0, 0.0f, 0.0f, fuse_route ? &ra : NULL, &sp_gu, c->st));
         if ((rc = timing_end(c))) return rc;
         /* the down launch makes its inputs from the gate/up partials (SwiGLU
          * in its prologue); its partials go after the gate/up ones */
@@ -1177,7 +1184,7 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
         if ((rc = timing_begin(c, 1))) return rc;
         KRN(c, wk_vq_lut(g->fmt, c->jobs, c->njobs, K, 2, 1, L->books, L->books_x31, NULL, 0, c->part + gu_floats,
                          c->part_cap - gu_floats, H, I, c->n_cu, c->part, sp_gu, g->act_situ, g->situ_beta,
-                         g->situ_linear_beta, &sp_d, c->st));
+                         g->situ_linear_beta, NULL, &sp_d, c->st));
         d_off = gu_floats;
         if ((rc = timing_end(c))) return rc;
     } else if (c->P6) {
@@ -1364,7 +1371,7 @@ int warp_hip_vq_matvec(warp_hip_ctx *c, int layer, int kind, const uint8_t *rec_
         float *yk[3] = { y_dev, y_dev, y_dev };
         int sp = 0;
         KRN(c, wk_vq_lut(c->cfg.fmt, c->jobs, c->njobs, 1, kind, 1, L->books, L->books_x31, x_dev, 1, c->part, c->part_cap, M, N,
-                         c->n_cu, NULL, 0, 0, 0.0f, 0.0f, &sp, c->st));
+                         c->n_cu, NULL, 0, 0, 0.0f, 0.0f, NULL, &sp, c->st));
         KRN(c, wk_lut_reduce(c->jobs, c->njobs, 1, kind, 1, c->part, sp, M, yk, c->st));
     } else {
         float *yk[3] = { y_dev, y_dev, y_dev };

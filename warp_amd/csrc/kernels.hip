@@ -414,37 +414,29 @@ __device__ __forceinline__ int route_key(float v) {
 // (src/model.c:2727-2739) -- each lane keeping the best of its own ids and
 // rescanning them only when that best is taken. The job lists are then
 // written from the table in LDS, with no dependent reads of HBM.
-template <bool REGS>
-__device__ __forceinline__ void route1_block(const float *__restrict__ logits, const float *__restrict__ bias,
-                                             int E, int K, int act, int renorm, float routed_scale,
-                                             int *__restrict__ idx, float *__restrict__ w,
-                                             const warp_slot *__restrict__ table, int table_lds,
-                                             warp_job *__restrict__ jobs, int *__restrict__ njobs,
-                                             int *__restrict__ missing, int inter) {
-    extern __shared__ __attribute__((aligned(16))) float lds_r1[];
-    float *score = lds_r1;                                     // [E]
-    float *biased = lds_r1 + E;                                // [E]
-    warp_slot *slots = (warp_slot *)(lds_r1 + 2 * ((E + 1) & ~1));   // [E] when table_lds
-    __shared__ int sel[WARP_MAX_K];
-    __shared__ float wsel[WARP_MAX_K];
-    __shared__ float red[4];
+// Scores, selection and weights of one token's routing (src/model.c:2723-
+// 2745) by a block of NT threads, from the logits and biases already in LDS
+// (score[E], biased[E]; both overwritten). On return (all threads past a
+// barrier) sel[0..K) holds the picks in order and wsel[0..K) their weights,
+// 0 past the picks found; returns the number of picks (< K only when fewer
+// than K experts are pickable).
+template <bool REGS, int NT>
+__device__ __forceinline__ int route_pick_lds(int E, int K, int act, int renorm, float routed_scale, float *score,
+                                              float *biased, int *sel, float *wsel) {
+    __shared__ float red[NT / 64];
+    __shared__ int np_s;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    for (int e = tid; e < E; e += 256) {
-        score[e] = logits[e];
-        biased[e] = bias ? bias[e] : 0.0f;
-    }
-    if (table && table_lds)
-        for (int e = tid; e < E; e += 256) slots[e] = table[e];
     if (tid < WARP_MAX_K) { sel[tid] = 0; wsel[tid] = 0.0f; }
     __syncthreads();
     if (act == 1) {
         float mx = -INFINITY;
-        for (int e = tid; e < E; e += 256) mx = fmaxf(mx, score[e]);
+        for (int e = tid; e < E; e += NT) mx = fmaxf(mx, score[e]);
         mx = wave_max(mx);
         if (lane == 0) red[wave] = mx;
         __syncthreads();
-        mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-        for (int e = tid; e < E; e += 256) score[e] = exp_cr(__fsub_rn(score[e], mx));
+        mx = red[0];
+        for (int i = 1; i < NT / 64; i++) mx = fmaxf(mx, red[i]);
+        for (int e = tid; e < E; e += NT) score[e] = exp_cr(__fsub_rn(score[e], mx));
         __syncthreads();
         if (tid == 0) {
             float s = 0.0f;                   // sequential, as the reference sums
@@ -453,11 +445,11 @@ __device__ __forceinline__ void route1_block(const float *__restrict__ logits, c
         }
         __syncthreads();
         const float s = red[0];
-        for (int e = tid; e < E; e += 256) score[e] = __fdiv_rn(score[e], s);
+        for (int e = tid; e < E; e += NT) score[e] = __fdiv_rn(score[e], s);
     } else {
-        for (int e = tid; e < E; e += 256) score[e] = __fdiv_rn(1.0f, __fadd_rn(1.0f, exp_cr(-score[e])));
+        for (int e = tid; e < E; e += NT) score[e] = __fdiv_rn(1.0f, __fadd_rn(1.0f, exp_cr(-score[e])));
     }
-    for (int e = tid; e < E; e += 256) biased[e] = __fadd_rn(score[e], biased[e]);
+    for (int e = tid; e < E; e += NT) biased[e] = __fadd_rn(score[e], biased[e]);
     __syncthreads();
     if (wave == 0) {
         // Lane l holds the keys of ids l, l + 64, ... (REGS: all in registers,
@@ -477,10 +469,13 @@ __device__ __forceinline__ void route1_block(const float *__restrict__ logits, c
             __shared__ unsigned long long ck[64];
             __shared__ int ord[64];
             unsigned u[VPL], mx = 0;
+            float bk[VPL];
+#pragma unroll
+            for (int m = 0; m < VPL; m++) bk[m] = biased[min(lane + 64 * m, E - 1)];   // all reads in flight
 #pragma unroll
             for (int m = 0; m < VPL; m++) {
                 const int e = lane + 64 * m;
-                u[m] = e < E ? (unsigned)route_key(biased[e]) ^ 0x80000000u : 0u;
+                u[m] = e < E ? (unsigned)route_key(bk[m]) ^ 0x80000000u : 0u;
                 mx = u[m] > mx ? u[m] : mx;
             }
             unsigned t0 = 0;
@@ -504,12 +499,18 @@ __device__ __forceinline__ void route1_block(const float *__restrict__ logits, c
                 __builtin_amdgcn_wave_barrier();
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-                if (lane < n) {
-                    const unsigned long long me = ck[lane];
-                    int r = 0;
-                    for (int i = 0; i < n; i++) r += ck[i] > me;
-                    if (r < K) ord[r] = (int)~(unsigned)me;
+                // each survivor's rank: the others' keys by readlane (no
+                // LDS round trip per candidate)
+                const unsigned long long me = lane < n ? ck[lane] : 0ull;
+                const unsigned mlo = (unsigned)me, mhi = (unsigned)(me >> 32);
+                int r = 0;
+                for (int i = 0; i < n; i++) {
+                    const unsigned long long o =
+                        ((unsigned long long)(unsigned)__builtin_amdgcn_readlane((int)mhi, i) << 32) |
+                        (unsigned)__builtin_amdgcn_readlane((int)mlo, i);
+                    r += o > me;
                 }
+                if (lane < n && r < K) ord[r] = (int)~(unsigned)me;
                 __builtin_amdgcn_wave_barrier();
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -575,40 +576,79 @@ __device__ __forceinline__ void route1_block(const float *__restrict__ logits, c
         // divisions and the scale in parallel
         float wv = lane < npick ? score[mine] : 0.0f;
         float ssum = 0.0f;
-        for (int j = 0; j < K; j++) ssum = __fadd_rn(ssum, __shfl(wv, j));
+        for (int j = 0; j < K; j++)
+            ssum = __fadd_rn(ssum, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wv), j)));
         if (renorm && K > 1) wv = __fdiv_rn(wv, __fadd_rn(ssum, 1e-20f));
         wv = __fmul_rn(wv, routed_scale);
         if (lane < K) {
             sel[lane] = lane < npick ? mine : 0;
             wsel[lane] = wv;
-            idx[lane] = lane < npick ? mine : 0;
-            w[lane] = wv;
         }
+        if (lane == 0) np_s = npick;
     }
     __syncthreads();
-    if (table) {
-        int miss = 0;
-        for (int t = tid; t < 3 * K; t += 256) {          // one thread per (kind, pick)
-            const int kind = t / K, j = t - kind * K;
-            const warp_slot sl = table_lds ? slots[sel[j]] : table[sel[j]];
-            miss |= sl.rec == nullptr;
-            warp_job jb;
-            jb.idx = nullptr;
-            jb.scale = nullptr;
-            if (sl.rec) job_ptrs(jb, sl, kind, inter);
-            jb.n = 1;
-            jb.rsv = 0;
-            for (int s = 0; s < WARP_TPJ; s++) { jb.xi[s] = 0; jb.yi[s] = 0; }
-            jb.xi[0] = kind == 2 ? j : 0;
-            jb.yi[0] = j;
-            jobs[kind * K + j] = jb;
-        }
-        miss = __syncthreads_or(miss);
-        if (tid == 0) {
-            for (int kind = 0; kind < 3; kind++) njobs[kind] = miss ? 0 : K;
-            if (miss) *missing = 1;
-        }
+    return np_s;
+}
+
+// The decode job lists from the picks, by a block of NT threads: jobs[0..K)
+// gate, [K..2K) up, [2K..3K) down, njobs[3] = {K, K, K}, or {0, 0, 0} and
+// *missing = 1 when a picked expert has no record. slots: the layer's expert
+// table (in LDS or global memory).
+template <int NT>
+__device__ __forceinline__ void route_jobs(const int *sel, int K, const warp_slot *slots, warp_job *__restrict__ jobs,
+                                           int *__restrict__ njobs, int *__restrict__ missing, int inter) {
+    const int tid = threadIdx.x;
+    int miss = 0;
+    for (int t = tid; t < 3 * K; t += NT) {          // one thread per (kind, pick)
+        const int kind = t / K, j = t - kind * K;
+        const warp_slot sl = slots[sel[j]];
+        miss |= sl.rec == nullptr;
+        warp_job jb;
+        jb.idx = nullptr;
+        jb.scale = nullptr;
+        if (sl.rec) job_ptrs(jb, sl, kind, inter);
+        jb.n = 1;
+        jb.rsv = 0;
+        for (int s = 0; s < WARP_TPJ; s++) { jb.xi[s] = 0; jb.yi[s] = 0; }
+        jb.xi[0] = kind == 2 ? j : 0;
+        jb.yi[0] = j;
+        jobs[kind * K + j] = jb;
     }
+    miss = __syncthreads_or(miss);
+    if (tid == 0) {
+        for (int kind = 0; kind < 3; kind++) njobs[kind] = miss ? 0 : K;
+        if (miss) *missing = 1;
+    }
+}
+
+// One token's routing by a 256-thread block (logits, biases and the expert
+// table staged in LDS), idx/w, and the job lists when a table is given.
+template <bool REGS>
+__device__ __forceinline__ void route1_block(const float *__restrict__ logits, const float *__restrict__ bias,
+                                             int E, int K, int act, int renorm, float routed_scale,
+                                             int *__restrict__ idx, float *__restrict__ w,
+                                             const warp_slot *__restrict__ table, int table_lds,
+                                             warp_job *__restrict__ jobs, int *__restrict__ njobs,
+                                             int *__restrict__ missing, int inter) {
+    extern __shared__ __attribute__((aligned(16))) float lds_r1[];
+    float *score = lds_r1;                                     // [E]
+    float *biased = lds_r1 + E;                                // [E]
+    warp_slot *slots = (warp_slot *)(lds_r1 + 2 * ((E + 1) & ~1));   // [E] when table_lds
+    __shared__ int sel[WARP_MAX_K];
+    __shared__ float wsel[WARP_MAX_K];
+    const int tid = threadIdx.x;
+    for (int e = tid; e < E; e += 256) {
+        score[e] = logits[e];
+        biased[e] = bias ? bias[e] : 0.0f;
+    }
+    if (table && table_lds)
+        for (int e = tid; e < E; e += 256) slots[e] = table[e];
+    route_pick_lds<REGS, 256>(E, K, act, renorm, routed_scale, score, biased, sel, wsel);
+    if (tid < K) {
+        idx[tid] = sel[tid];
+        w[tid] = wsel[tid];
+    }
+    if (table) route_jobs<256>(sel, K, table_lds ? slots : table, jobs, njobs, missing, inter);
 }
 
 template <bool REGS>
@@ -1014,6 +1054,11 @@ struct LutArgs {
     const float *act_part;
     int act_splits, act_situ;
     float act_beta, act_lbeta;
+    // routing in the prologue (gate and up of a decode step): every block
+    // picks the experts from the logits itself (the same picks everywhere);
+    // block 0 writes idx, w, the job lists of all three kinds (into jobs),
+    // njobs and the missing flag for the launches that follow
+    warp_route_args r;
 };
 
 // Sum of a row's partials over the splits, in split order. Up to 32 splits
@@ -1076,8 +1121,9 @@ __device__ __forceinline__ half4 half4_of(uint32_t lo, uint32_t hi) {
 
 // SHX = true: the jobs of the list share one input and a row group spans
 // them (gate and up); false: one input per job (down). ACT (with SHX false):
-// the inputs are made from the gate/up partial sums (a.act_part).
-template <int FMT, bool X31, bool SHX, bool ACT>
+// the inputs are made from the gate/up partial sums (a.act_part). RT (with
+// SHX): the jobs are picked in the prologue from the router logits (a.r).
+template <int FMT, bool X31, bool SHX, bool ACT, bool RT>
 __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
     typedef FmtT<FMT> F;
     constexpr int SE = F::S * F::E;                        // table entries per position
@@ -1108,21 +1154,98 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
 
     // The prologue issues its loads in the order their data is needed and
     // waits for no load it does not use (loads complete in issue order).
-    // 1. The job list, written by the routing launch: the record of every
-    //    pair (the job of a pair follows from the block's position; the job
-    //    count, read alongside, only decides which pairs are real), the
-    //    input index and, for the down launch, the gate/up row scales.
+    constexpr bool rt = RT && SHX;
     const uint8_t *jrec[LUT_PPW];
+    const uint8_t *jrec0;
+    int xi, nj;
+    gu32 *sg = nullptr, *su = nullptr;
+    float xr[XPT];
+    // The codebook of this kind: group G = wave * GPW + g holds entries
+    // 64 G .. 64 G + 63 over [stage][entry], entry 64 G + lane in this lane
+    // (128 KiB per block for 2 x 4096 entries).
+    uint4 cb[GPW];
+    auto load_cb = [&]() {
+        const uint4 *bk = (const uint4 *)(a.books + (size_t)kind * SE * 8);
 #pragma unroll
-    for (int q = 0; q < LUT_PPW; q++) {
-        const int fb = fb0 + 2 * (q * LUT_NW + wave) + rbsel;
-        jrec[q] = jobs[min(fb / nrb, a.max_jobs - 1)].idx;
+        for (int g = 0; g < GPW; g++) {
+            const int G = wave * GPW + g;
+            cb[g] = G < NG ? bk[G * 64 + lane] : make_uint4(0u, 0u, 0u, 0u);
+        }
+    };
+    if constexpr (rt) {
+        // 1. The routing inputs (one expert per thread: E <= the block
+        //    size), then the token's input and the codebook; the routing
+        //    inputs staged in the table buffers, which are not built yet; the
+        //    picks; then the record of every pair straight from the staged
+        //    expert table.
+        const int E = a.r.E, E2 = (E + 1) & ~1, K = a.max_jobs, e = threadIdx.x;
+        float *score = lut, *biased = lut + E2;
+        warp_slot *slots = (warp_slot *)(lut + 2 * E2);
+        __shared__ int r_sel[WARP_MAX_K];
+        __shared__ float r_wsel[WARP_MAX_K];
+        float lg = 0.0f, bs = 0.0f;
+        warp_slot sl{};
+        if (e < E) {
+            lg = a.r.logits[e];
+            bs = a.r.bias ? a.r.bias[e] : 0.0f;
+            sl = a.r.table[e];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        const float *xg = a.x + (size_t)c0 * 16;
+#pragma unroll
+        for (int k = 0; k < XPT; k++) {
+            const int i = threadIdx.x + k * LUT_NW * 64;
+            const float v = xg[min(i, nx - 1)];
+            xr[k] = i < nx ? v : 0.0f;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        load_cb();                                         // streams in while the picks are made
+        __builtin_amdgcn_sched_barrier(0);
+        if (e < E) {
+            score[e] = lg;
+            biased[e] = bs;
+            slots[e] = sl;
+        }
+        route_pick_lds<true, LUT_NW * 64>(E, K, a.r.act, a.r.renorm, a.r.routed_scale, score, biased, r_sel, r_wsel);
+        bool miss = false;                                 // a pick without a record (the same in every block)
+        for (int j = 0; j < K; j++) miss |= slots[r_sel[j]].rec == nullptr;
+        if (blockIdx.x == 0 && blockIdx.y == 0) {          // uniform per block
+            if (threadIdx.x < K) {
+                a.r.idx[threadIdx.x] = r_sel[threadIdx.x];
+                a.r.w[threadIdx.x] = r_wsel[threadIdx.x];
+            }
+            route_jobs<LUT_NW * 64>(r_sel, K, slots, a.r.jobs, a.r.njobs, a.r.missing, a.r.inter);
+        }
+#pragma unroll
+        for (int q = 0; q < LUT_PPW; q++) {
+            const int fb = fb0 + 2 * (q * LUT_NW + wave) + rbsel;
+            const warp_slot &sl = slots[r_sel[min(fb / nrb, K - 1)]];
+            jrec[q] = sl.rec + sl.off[kind];
+        }
+        const warp_slot &s0 = slots[r_sel[min(fb0 / nrb, K - 1)]];
+        jrec0 = s0.rec + s0.off[kind];
+        xi = 0;
+        nj = miss ? 0 : K;
+        __syncthreads();                                   // the staging area is reused below
+    } else {
+        // 1. The job list, written by the routing launch: the record of every
+        //    pair (the job of a pair follows from the block's position; the
+        //    job count, read alongside, only decides which pairs are real),
+        //    the input index and, for the down launch, the gate/up row
+        //    scales.
+#pragma unroll
+        for (int q = 0; q < LUT_PPW; q++) {
+            const int fb = fb0 + 2 * (q * LUT_NW + wave) + rbsel;
+            jrec[q] = jobs[min(fb / nrb, a.max_jobs - 1)].idx;
+        }
+        jrec0 = jobs[fb0 / nrb].idx;
+        xi = act ? 0 : jobs[xj].xi[0];
+        if constexpr (act) {
+            sg = (gu32 *)a.jobs[xj].scale;
+            su = (gu32 *)a.jobs[(size_t)a.max_jobs + xj].scale;
+        }
+        nj = a.njobs[kind];
     }
-    const uint8_t *jrec0 = jobs[fb0 / nrb].idx;
-    const int xi = act ? 0 : jobs[xj].xi[0];
-    gu32 *sg = act ? (gu32 *)a.jobs[xj].scale : nullptr;
-    gu32 *su = act ? (gu32 *)a.jobs[(size_t)a.max_jobs + xj].scale : nullptr;
-    const int nj = a.njobs[kind];
 
     // 2. Down launch: the gate/up partial sums of this split's inputs, rows
     //    [kind 0, 1][split s] of nx values, spread over the block (one load
@@ -1153,7 +1276,6 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
     //    with, as the 4-byte words that hold them (the scale arrays of a
     //    record are 4-byte aligned and a split starts at an even input).
     //    Only jobs below the count are dereferenced.
-    float xr[XPT];
     unsigned gs[XPT], us[XPT];
     if constexpr (act) {
 #pragma unroll
@@ -1162,7 +1284,7 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
             gs[k] = sg[i >> 1];
             us[k] = su[i >> 1];
         }
-    } else {
+    } else if constexpr (!rt) {
         const float *xg = a.x + (size_t)xi * a.N + (size_t)c0 * 16;
 #pragma unroll
         for (int k = 0; k < XPT; k++) {
@@ -1171,19 +1293,11 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
             xr[k] = i < nx ? v : 0.0f;
         }
     }
-    // 4. The codebook of this kind (group G = wave * GPW + g holds entries
-    //    64 G .. 64 G + 63 over [stage][entry], entry 64 G + lane in this
-    //    lane), 128 KiB per block for 2 x 4096 entries, which the first
-    //    table build needs, then the code words of the first chunk, which
-    //    the loop needs.
+    // 4. The codebook (unless loaded with the routing inputs), which the
+    //    first table build needs, then the code words of the first chunk,
+    //    which the loop needs.
     __builtin_amdgcn_sched_barrier(0);
-    uint4 cb[GPW];
-    const uint4 *bk = (const uint4 *)(a.books + (size_t)kind * SE * 8);
-#pragma unroll
-    for (int g = 0; g < GPW; g++) {
-        const int G = wave * GPW + g;
-        cb[g] = G < NG ? bk[G * 64 + lane] : make_uint4(0u, 0u, 0u, 0u);
-    }
+    if constexpr (!rt) load_cb();
     __builtin_amdgcn_sched_barrier(0);
     // Pairs past the group's rows read row block 0 of the block's first job
     // (in bounds) and are never written: the loop below has no per-pair
@@ -1222,9 +1336,24 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
                 const int i = threadIdx.x + k * LUT_NW * 64;
                 xr[k] = 0.0f;
                 if (i < nx) {
+                    // the splits in order, 16 LDS reads in flight at a time
+                    const int S = a.act_splits;
                     float g = 0.0f, u = 0.0f;
-                    for (int s2 = 0; s2 < a.act_splits; s2++) g += lut[s2 * nx + i];
-                    for (int s2 = 0; s2 < a.act_splits; s2++) u += lut[(a.act_splits + s2) * nx + i];
+                    for (int s0 = 0; s0 < S; s0 += 16) {
+                        float ga[16], ua[16];
+#pragma unroll
+                        for (int t = 0; t < 16; t++) {
+                            const int s2 = min(s0 + t, S - 1);
+                            ga[t] = lut[s2 * nx + i];
+                            ua[t] = lut[(S + s2) * nx + i];
+                        }
+#pragma unroll
+                        for (int t = 0; t < 16; t++)
+                            if (s0 + t < S) {
+                                g += ga[t];
+                                u += ua[t];
+                            }
+                    }
                     const int sh = 16 * (i & 1);
                     xr[k] = act_pair(g * f16_keep((uint16_t)(gs[k] >> sh)), u * f16_keep((uint16_t)(us[k] >> sh)),
                                      a.act_situ, a.act_beta, a.act_lbeta);
@@ -1409,43 +1538,63 @@ extern "C" int wk_lut_plan(int M, int N, int max_jobs, int nkinds, int shared_x,
     return 0;
 }
 
-template <int FMT, bool X31, bool SHX, bool ACT>
+template <int FMT, bool X31, bool SHX, bool ACT, bool RT>
 static int launch_lut(const LutArgs &a, int groups, int nkinds, void *stream) {
     typedef FmtT<FMT> F;
     const size_t lds = ((size_t)2 * 2 * F::S * F::E + LUT_XCH * 16) * sizeof(float);
     if (lds > 163840) return -2;
     static bool attr = false;
     if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_vq_lut<FMT, X31, SHX, ACT>,
+        hipError_t e = hipFuncSetAttribute((const void *)k_vq_lut<FMT, X31, SHX, ACT, RT>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return -(int)e - 1000;
         attr = true;
     }
-    hipLaunchKernelGGL((k_vq_lut<FMT, X31, SHX, ACT>), dim3(groups * a.splits, nkinds), dim3(LUT_NW * 64), lds,
+    hipLaunchKernelGGL((k_vq_lut<FMT, X31, SHX, ACT, RT>), dim3(groups * a.splits, nkinds), dim3(LUT_NW * 64), lds,
                        (hipStream_t)stream, a);
     CHECK_LAUNCH();
     return 0;
 }
 
+extern "C" int wk_lut_route_ok(int fmt, int E, int K, int shared_x, int kind_lo, int nkinds) {
+    int se;
+    switch (fmt) {
+    case WARP_FMT_VQ3R: se = FmtT<WARP_FMT_VQ3R>::S * FmtT<WARP_FMT_VQ3R>::E; break;
+    case WARP_FMT_VQ2R: se = FmtT<WARP_FMT_VQ2R>::S * FmtT<WARP_FMT_VQ2R>::E; break;
+    case WARP_FMT_VQ12: se = FmtT<WARP_FMT_VQ12>::S * FmtT<WARP_FMT_VQ12>::E; break;
+    default: return 0;
+    }
+    // one expert per thread; logits, biases and the expert table staged in
+    // the table buffers and the input stash
+    const size_t stage = (size_t)2 * ((E + 1) & ~1) * sizeof(float) + (size_t)E * sizeof(warp_slot);
+    const size_t room = ((size_t)4 * se + LUT_XCH * 16) * sizeof(float);
+    return shared_x && kind_lo == 0 && nkinds == 2 && E > 0 && E <= LUT_NW * 64 && E <= 512 && K > 0 &&
+           K <= WARP_MAX_K && K <= E && stage <= room;
+}
+
 template <int FMT>
 static int launch_lut_x(const LutArgs &a, int groups, int nkinds, int x31, void *stream) {
+    if (a.shared_x && a.r.table)
+        return x31 ? launch_lut<FMT, true, true, false, true>(a, groups, nkinds, stream)
+                   : launch_lut<FMT, false, true, false, true>(a, groups, nkinds, stream);
     if (a.shared_x)
-        return x31 ? launch_lut<FMT, true, true, false>(a, groups, nkinds, stream)
-                   : launch_lut<FMT, false, true, false>(a, groups, nkinds, stream);
+        return x31 ? launch_lut<FMT, true, true, false, false>(a, groups, nkinds, stream)
+                   : launch_lut<FMT, false, true, false, false>(a, groups, nkinds, stream);
     if (a.act_part)
-        return x31 ? launch_lut<FMT, true, false, true>(a, groups, nkinds, stream)
-                   : launch_lut<FMT, false, false, true>(a, groups, nkinds, stream);
-    return x31 ? launch_lut<FMT, true, false, false>(a, groups, nkinds, stream)
-               : launch_lut<FMT, false, false, false>(a, groups, nkinds, stream);
+        return x31 ? launch_lut<FMT, true, false, true, false>(a, groups, nkinds, stream)
+                   : launch_lut<FMT, false, false, true, false>(a, groups, nkinds, stream);
+    return x31 ? launch_lut<FMT, true, false, false, false>(a, groups, nkinds, stream)
+               : launch_lut<FMT, false, false, false, false>(a, groups, nkinds, stream);
 }
 
 extern "C" int wk_vq_lut(int fmt, const warp_job *jobs, const int *njobs, int max_jobs, int kind_lo, int nkinds,
                          const uint16_t *books, int books_x31, const float *x, int shared_x, float *part,
                          size_t cap_floats, int M, int N, int target_blocks, const float *act_part,
-                         int act_splits, int act_situ, float act_beta, float act_lbeta, int *splits_out,
-                         void *stream) {
+                         int act_splits, int act_situ, float act_beta, float act_lbeta,
+                         const warp_route_args *route, int *splits_out, void *stream) {
     if (kind_lo < 0 || kind_lo + nkinds > 3 || !books || !part) return -1;
     if (act_part && (shared_x || kind_lo != 2 || nkinds != 1 || act_splits <= 0)) return -1;
+    if (route && !wk_lut_route_ok(fmt, route->E, max_jobs, shared_x, kind_lo, nkinds)) return -1;
     int groups, splits;
     if (wk_lut_plan(M, N, max_jobs, nkinds, shared_x, target_blocks, cap_floats, &groups, &splits)) return -1;
     LutArgs a;
@@ -1465,6 +1614,7 @@ extern "C" int wk_vq_lut(int fmt, const warp_job *jobs, const int *njobs, int ma
     a.act_situ = act_situ;
     a.act_beta = act_beta;
     a.act_lbeta = act_lbeta;
+    a.r = route ? *route : warp_route_args{};
     if (splits_out) *splits_out = splits;
     switch (fmt) {
     case WARP_FMT_VQ3R: return launch_lut_x<WARP_FMT_VQ3R>(a, groups, nkinds, books_x31, stream);

@@ -115,14 +115,31 @@ int wk_vq_matvec(int fmt, const warp_job *jobs, const int *njobs, int max_jobs,
  * the split count the consumers must be given. N % 16 == 0. */
 int wk_lut_plan(int M, int N, int max_jobs, int nkinds, int shared_x, int target_blocks,
                 size_t cap_floats, int *groups_out, int *splits_out);
+/* Routing done inside the gate/up launch of a decode step (see wk_vq_lut):
+ * the arguments of wk_route with a table, for one token. */
+typedef struct {
+    const float *logits, *bias;
+    const warp_slot *table;
+    int E, act, renorm, inter;
+    float routed_scale;
+    int *idx;
+    float *w;
+    warp_job *jobs;           /* written: the lists of all three kinds */
+    int *njobs, *missing;
+} warp_route_args;
 int wk_vq_lut(int fmt, const warp_job *jobs, const int *njobs, int max_jobs, int kind_lo,
               int nkinds, const uint16_t *books, int books_x31, const float *x, int shared_x, float *part,
               size_t cap_floats, int M, int N, int target_blocks, const float *act_part,
-              int act_splits, int act_situ, float act_beta, float act_lbeta, int *splits_out,
-              void *stream);
+              int act_splits, int act_situ, float act_beta, float act_lbeta,
+              const warp_route_args *route, int *splits_out, void *stream);
 /* (act_part: the down launch makes each job's input itself, h = act(gate,
  * up) from the gate/up partial sums -- kinds 0 and 1 of the previous launch
- * with act_splits splits -- instead of reading x; NULL otherwise.) */
+ * with act_splits splits -- instead of reading x; NULL otherwise.
+ * route: the gate/up launch (kinds 0 and 1, shared input x) also routes the
+ * token, K = max_jobs picks, as wk_route would with the table, instead of
+ * reading jobs/njobs; route->jobs/njobs/idx/w/missing get what wk_route
+ * writes. Only where wk_lut_route_ok says so; NULL otherwise.) */
+int wk_lut_route_ok(int fmt, int E, int K, int shared_x, int kind_lo, int nkinds);
 /* y[k][yi][r] = (sum over splits) * row scale, for the kinds of one LUT launch. */
 int wk_lut_reduce(const warp_job *jobs, const int *njobs, int max_jobs, int kind_lo, int nkinds,
                   const float *part, int splits, int M, float *const *y, void *stream);
