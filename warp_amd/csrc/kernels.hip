@@ -599,20 +599,22 @@ __device__ __forceinline__ void route_jobs(const int *sel, int K, const warp_slo
                                            int *__restrict__ njobs, int *__restrict__ missing, int inter) {
     const int tid = threadIdx.x;
     int miss = 0;
-    for (int t = tid; t < 3 * K; t += NT) {          // one thread per (kind, pick)
+    for (int t = tid; t < 3 * K; t += NT) {          // one thread per (kind, pick), field by field
         const int kind = t / K, j = t - kind * K;
-        const warp_slot sl = slots[sel[j]];
-        miss |= sl.rec == nullptr;
-        warp_job jb;
-        jb.idx = nullptr;
-        jb.scale = nullptr;
-        if (sl.rec) job_ptrs(jb, sl, kind, inter);
-        jb.n = 1;
-        jb.rsv = 0;
-        for (int s = 0; s < WARP_TPJ; s++) { jb.xi[s] = 0; jb.yi[s] = 0; }
-        jb.xi[0] = kind == 2 ? j : 0;
-        jb.yi[0] = j;
-        jobs[kind * K + j] = jb;
+        const warp_slot &sl = slots[sel[j]];
+        const uint8_t *rec = sl.rec;
+        miss |= rec == nullptr;
+        warp_job *jo = jobs + kind * K + j;
+        const int soff = kind == 0 ? 0 : kind == 1 ? inter : 2 * inter;
+        jo->idx = rec ? rec + sl.off[kind] : nullptr;
+        jo->scale = rec ? (const uint16_t *)(rec + sl.off[3]) + soff : nullptr;
+        jo->n = 1;
+        jo->rsv = 0;
+#pragma unroll
+        for (int s = 0; s < WARP_TPJ; s++) {
+            jo->xi[s] = s == 0 && kind == 2 ? j : 0;
+            jo->yi[s] = s == 0 ? j : 0;
+        }
     }
     miss = __syncthreads_or(miss);
     if (tid == 0) {
@@ -1183,12 +1185,16 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
         warp_slot *slots = (warp_slot *)(lut + 2 * E2);
         __shared__ int r_sel[WARP_MAX_K];
         __shared__ float r_wsel[WARP_MAX_K];
+        // (the slot by fields: an aggregate copy would go through scratch)
         float lg = 0.0f, bs = 0.0f;
-        warp_slot sl{};
+        const uint8_t *srec = nullptr;
+        uint2 so01 = make_uint2(0u, 0u), so23 = make_uint2(0u, 0u);
         if (e < E) {
             lg = a.r.logits[e];
             bs = a.r.bias ? a.r.bias[e] : 0.0f;
-            sl = a.r.table[e];
+            srec = a.r.table[e].rec;
+            so01 = *(const uint2 *)&a.r.table[e].off[0];
+            so23 = *(const uint2 *)&a.r.table[e].off[2];
         }
         __builtin_amdgcn_sched_barrier(0);
         const float *xg = a.x + (size_t)c0 * 16;
@@ -1204,7 +1210,9 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
         if (e < E) {
             score[e] = lg;
             biased[e] = bs;
-            slots[e] = sl;
+            slots[e].rec = srec;
+            *(uint2 *)&slots[e].off[0] = so01;
+            *(uint2 *)&slots[e].off[2] = so23;
         }
         route_pick_lds<true, LUT_NW * 64>(E, K, a.r.act, a.r.renorm, a.r.routed_scale, score, biased, r_sel, r_wsel);
         bool miss = false;                                 // a pick without a record (the same in every block)
