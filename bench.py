@@ -26,6 +26,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import shutil
 import sys
 import tempfile
 import time
@@ -187,6 +188,7 @@ def cpu_baseline(seconds):
         n += 1
     dt = time.perf_counter() - t0
     ref.close()
+    shutil.rmtree(tmp, ignore_errors=True)
     return {"value": n / dt, "unit": "MoE-layer tokens/s", "cores": threads, "kind": "reference",
             "sample": f"{n} decode tokens through one K3-shape layer (H {H}, I {I}, top-16 of 16 "
                       f"routed experts) in the reference's VQ3R format (3x256, 3.00 bits/weight, the "
@@ -196,9 +198,183 @@ def cpu_baseline(seconds):
                       f"of the bytes) that the GPU workload does not have"}
 
 
+# ---- Kimi-Linear-shape prefill (a second workload, not the headline line) ----------------
+
+KH, KI, KE, KK, KIS = 2304, 1024, 256, 8, 1024      # hidden, inter, experts, top-k, shared inter
+
+
+def kimi_rec_layout():
+    gate = (KI // 64) * (KH // 8) * 64 * 3
+    down = (KH // 64) * (KI // 8) * 64 * 3
+    scales = 2 * (2 * KI + KH)
+    raw = 48 + 2 * gate + down + scales
+    return gate, down, scales, (raw + 4095) // 4096 * 4096
+
+
+def zipf_bias(router, X, s=1.1, seed=5, iters=80):
+    """A per-expert bias (the e_score_correction_bias the reference's selection
+    adds, src/model.c:2723-2745) under which the tokens-per-expert counts of
+    top-8 softmax routing of X follow Zipf(s) over a random ranking of the
+    experts (counts capped at one pick per token and expert): fitted on the
+    host by raising each expert's bias by the log ratio of its target count
+    to its count."""
+    T = X.shape[0]
+    logits = X.astype(np.float64) @ router.astype(np.float64).T
+    logits -= logits.max(1, keepdims=True)
+    sc = np.exp(logits)
+    sc /= sc.sum(1, keepdims=True)
+    z = (np.arange(KE) + 1.0) ** -s
+    target = z / z.sum() * T * KK
+    for _ in range(20):                      # cap at T, spread the excess over the rest
+        over = target > T
+        if not over.any():
+            break
+        excess = (target[over] - T).sum()
+        target[over] = T
+        target[~over] += excess * target[~over] / target[~over].sum()
+    want = target[np.random.default_rng(seed).permutation(KE)]      # expert e's target count
+    step = float(np.std(sc))
+    b = np.zeros(KE)
+    for _ in range(iters):
+        pick = np.argpartition(-(sc + b), KK, axis=1)[:, :KK]
+        cnt = np.bincount(pick.ravel(), minlength=KE)
+        b += 0.5 * step * (np.log(want + 0.5) - np.log(cnt + 0.5))
+    return b.astype(np.float32)
+
+
+def run_prefill(args):
+    import warp_amd
+    import container as ct
+    from warp_amd.hip import ROUTE_SOFTMAX
+    from warp_amd.device import Buf, Event
+    T, layers = args.tokens, args.layers
+    gate, down, scales_b, rec_bytes = kimi_rec_layout()
+    ctx = warp_amd.Context(hidden=KH, inter=KI, n_experts=KE, top_k=KK, n_layers=layers, fmt="VQ12",
+                           renorm=True, routed_scale=1.0, router_act=ROUTE_SOFTMAX, max_tokens=T,
+                           rec_bytes=rec_bytes, cache_bytes=layers * KE * rec_bytes)
+    rng = np.random.Generator(np.random.PCG64(4321))
+    X = rng.standard_normal((T, KH), dtype=np.float32)
+    shared_bytes = 0
+    t0 = time.time()
+    for L in range(layers):
+        books = rng.normal(0.0, 0.02, size=(3 * S, EN, 8)).astype(np.float16).view(np.uint16)
+        ctx.set_codebooks(L, L * 3 * S, books)
+        router = rng.standard_normal((KE, KH), dtype=np.float32) * np.float32(0.02)
+        ctx.set_router(L, router, zipf_bias(router, X, seed=5 + L))
+        for e in range(KE):
+            sc = rng.uniform(0.01, 0.05, size=2 * KI + KH).astype(np.float16).view(np.uint16)
+            ctx.put_expert_synth(L, e, int(rng.integers(1 << 62)), sc)
+        sh = [ct.quant_rows(rng, M, N, 8, 32, (1e-4, 3e-4)) for M, N in ((KIS, KH), (KIS, KH), (KH, KIS))]
+        ctx.set_shared(L, 8, 32, KIS, [np.ascontiguousarray(q[0]) for q in sh],
+                       [np.ascontiguousarray(q[1]) for q in sh], [q[2] for q in sh])
+        shared_bytes = sum(q[0].nbytes + q[1].nbytes for q in sh)
+    ctx.sync()
+    log(f"bench: {layers} Kimi-Linear layers set up ({time.time() - t0:.1f}s)")
+    Xd = Buf.of(X)
+    outs = [Buf.empty((T, KH)) for _ in range(layers)]
+    # the routing of the timed input: distinct experts and pairs per layer
+    distinct = []
+    for L in range(layers):
+        route, _ = ctx.moe_chunk(L, Xd.ptr, outs[L].ptr, T, want_route=True)
+        distinct.append(len(np.unique(route)))
+    counts = np.sort(np.bincount(route.ravel(), minlength=KE))[::-1]
+
+    def step():
+        for L in range(layers):
+            ctx.moe_chunk(L, Xd.ptr, outs[L].ptr, T)
+
+    for _ in range(args.warmup):
+        step()
+    ctx.sync()
+    e0, e1 = Event(), Event()
+    stream = ctx.stream
+    log(f"bench: timing {args.steps} prefill steps of {T} tokens x {layers} layers")
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(stream)
+    e1.synchronize()
+    ctx.sync()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_ms(e1)
+    for L in range(layers):
+        assert np.isfinite(outs[L].numpy()).all(), "non-finite prefill output"
+    ctx.close()
+    pair_bytes = 2 * gate + down + scales_b
+    per_layer = (np.mean(distinct) * pair_bytes + shared_bytes + KE * KH * 4 + 3 * S * EN * 8 * 2 + KE * 4
+                 + 2 * T * KH * 4)
+    flops = 2 * 3 * KH * KI * T * KK + 2 * 3 * KH * KIS * T
+    sec = ms / 1e3
+    n_lt = args.steps * layers
+    gbs = per_layer * n_lt / sec / 1e9
+    tfs = flops * n_lt / sec / 1e12
+    return {
+        "metric": "MoE-layer prefill tokens/s, Kimi-Linear shape, 1 MI355X",
+        "value": round(T * n_lt / sec, 1),
+        "unit": "MoE-layer tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms / args.steps, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
+        "data": "synthetic (random codes, codebooks, scales, shared expert and routers of the Kimi-Linear shapes; "
+                "a per-expert bias that skews tokens per expert towards Zipf(1.1))",
+        "config": {"workload": f"Kimi-Linear-shape MoE layer, prefill of {T} tokens, {layers}-layer stack",
+                   "hidden": KH, "inter": KI, "experts": KE, "top_k": KK, "routing": "softmax + bias",
+                   "shared_expert": "Q8G group 32, intermediate 1024", "tokens": T, "layers": layers,
+                   "format": "RVQ 2x4096 12-bit codes (3.00 b/w)", "parallelism": "single GPU"},
+        "per_layer": {"distinct_experts": round(float(np.mean(distinct)), 1), "pairs": T * KK,
+                      "tokens_on_busiest_5": counts[:5].tolist(), "algorithmic_bytes": int(per_layer),
+                      "useful_flops": int(flops)},
+        "hbm": {"achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)},
+        "mfma": {"achieved": round(tfs, 2), "peak": 2500.0, "unit": "TFLOP/s",
+                 "frac": round(tfs / 2500.0, 5),
+                 "note": "useful FLOPs (2 x 3 x H x I per pair, plus the shared expert); the expert matvecs run "
+                         "fp16 hi/lo halves of x on the matrix cores, twice the useful MFMA work"},
+        "wall_s": round(wall, 3),
+        "cpu_baseline": None if args.no_cpu else cpu_baseline_prefill(args.cpu_seconds, T),
+    }
+
+
+def cpu_baseline_prefill(seconds, T):
+    """The reference's moe_chunk on the VQ3R twin of one Kimi-Linear layer."""
+    from oracle import pyoracle as po
+    import container as ct
+    if not os.path.exists(po.REF_LIB):
+        return None
+    spec = ct.Spec(hidden=KH, inter=KI, experts=KE, top_k=KK, layers=1, fmt="VQ3R", renorm=True,
+                   routed_scale=1.0, shared_bits=8, shared_group=32, subnormals=False, keep_codes=False, seed=98)
+    log("bench: writing the VQ3R twin container for the prefill CPU baseline")
+    model = ct.build(spec)
+    tmp = tempfile.mkdtemp(prefix="warp_kimi_twin_")
+    ct.write(model, tmp)
+    del model
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+    ref = po.Ref(tmp, cache_bytes=KE * 2_700_000 + (64 << 20), n_threads=threads)
+    threads = ref.threads()
+    rng = np.random.default_rng(3)
+    chunk = 64
+    for _ in range(8):                                 # fills the reference's cache
+        ref.moe_chunk(0, rng.standard_normal((chunk, KH), dtype=np.float32), KK, KH)
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        ref.moe_chunk(0, rng.standard_normal((chunk, KH), dtype=np.float32), KK, KH)
+        n += chunk
+    dt = time.perf_counter() - t0
+    ref.close()
+    shutil.rmtree(tmp, ignore_errors=True)
+    return {"value": n / dt, "unit": "MoE-layer tokens/s", "cores": threads, "kind": "reference",
+            "sample": f"{n} prefill tokens in chunks of {chunk} through one Kimi-Linear-shape layer (H {KH}, "
+                      f"I {KI}, top-8 of 256 experts, Q8G shared expert) in the reference's VQ3R format (3x256, "
+                      f"3.00 bits/weight), its own moe_chunk over {threads} threads, {dt:.1f}s, records "
+                      f"cache-resident; the reference routes with sigmoid scores (softmax is not in it)"}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--workload", choices=["k3-decode", "kimi-prefill"], default="k3-decode",
+                    help="k3-decode (the headline line) or kimi-prefill (a 512-token Kimi-Linear-shape prefill)")
+    ap.add_argument("--tokens", type=int, default=512, help="kimi-prefill: tokens per step")
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--layers", type=int, default=60)
@@ -216,6 +392,11 @@ def main():
               "(the path is single-GPU; multi-GPU sharding is described in DESIGN.md)", file=sys.stderr)
         sys.exit(2)
 
+    if args.workload == "kimi-prefill":
+        if args.layers == 60:
+            args.layers = 4
+        print(json.dumps(run_prefill(args)))
+        return
     ms, wall, kms, kn, st = run_gpu(args)
     steps, layers = args.steps, args.layers
     layer_tokens = steps * layers

@@ -261,6 +261,8 @@ struct warp_hip_ctx {
     uint16_t *xsh;
     float *xscaleh, *hbuf;
     float *shg, *shu, *shh, *sho;
+    uint16_t *shxs;               /* the shared expert's h split for the matrix cores */
+    float *shxscale;
     int sh_cap;
     int8_t *lut8, *lut8d;
     float *lscale, *lscaled;
@@ -268,6 +270,7 @@ struct warp_hip_ctx {
     size_t part_cap;            /* floats                                  */
     int n_cu, lut_ok, mv_path;
     int *counts, *offsets, *pair_tok, *pair_exp;
+    int *tok_slots;               /* per token, its pair slots in ascending expert id */
     float *pair_w;
     float *xin, *xout;
     float *la_logits;
@@ -372,6 +375,7 @@ static int ctx_alloc(warp_hip_ctx *c)
     DMALLOC(c, c->pair_tok, P * 4);
     DMALLOC(c, c->pair_exp, P * 4);
     DMALLOC(c, c->pair_w, P * 4);
+    DMALLOC(c, c->tok_slots, P * 4);
     DMALLOC(c, c->la_logits, (size_t)E * 4);
     DMALLOC(c, c->la_idx, (size_t)WARP_MAX_K * 4);
     DMALLOC(c, c->la_w, (size_t)WARP_MAX_K * 4);
@@ -515,8 +519,9 @@ void warp_hip_close(warp_hip_ctx *c)
     free(c->L);
     void *d[] = { c->logits, c->idx, c->w, c->jobs, c->njobs, c->missing, c->xs, c->xscale, c->yg, c->yu,
                   c->yd, c->xsh, c->xscaleh, c->hbuf, c->shg, c->shu, c->shh, c->sho, c->lut8, c->lut8d,
-                  c->lscale, c->lscaled, c->counts, c->offsets, c->pair_tok, c->pair_exp, c->pair_w,
-                  c->xin, c->xout, c->la_logits, c->la_idx, c->la_w, c->table_dev, c->pool, c->part };
+                  c->lscale, c->lscaled, c->counts, c->offsets, c->pair_tok, c->pair_exp, c->pair_w, c->tok_slots,
+                  c->xin, c->xout, c->la_logits, c->la_idx, c->la_w, c->table_dev, c->pool, c->part,
+                  c->shxs, c->shxscale };
     for (size_t i = 0; i < sizeof d / sizeof d[0]; i++) hfree(d[i]);
     hhfree(c->h_idx); hhfree(c->h_w); hhfree(c->h_la_idx); hhfree(c->h_missing); hhfree(c->staging);
     free(c->key_slot); free(c->slot_key); free(c->hits); free(c->last); free(c->pin);
@@ -660,13 +665,17 @@ int warp_hip_set_shared(warp_hip_ctx *c, int layer, int bits, int group, int int
     int max_is = 0;
     for (int l = 0; l < c->cfg.n_layers; l++) if (c->L[l].s_inter > max_is) max_is = c->L[l].s_inter;
     if (max_is > c->sh_cap) {
-        hfree(c->shg); hfree(c->shu); hfree(c->shh);
+        hfree(c->shg); hfree(c->shu); hfree(c->shh); hfree(c->shxs); hfree(c->shxscale);
         c->shg = c->shu = c->shh = NULL;
+        c->shxs = NULL;
+        c->shxscale = NULL;
         c->sh_cap = 0;
         const size_t bytes = (size_t)c->cfg.max_tokens * max_is * 4;
         DMALLOC(c, c->shg, bytes);
         DMALLOC(c, c->shu, bytes);
         DMALLOC(c, c->shh, bytes);
+        DMALLOC(c, c->shxs, bytes);
+        DMALLOC(c, c->shxscale, (size_t)c->cfg.max_tokens * 4);
         c->sh_cap = max_is;
     }
     return 0;
@@ -1064,6 +1073,19 @@ static int shared_ffn(warp_hip_ctx *c, const layer_t *L, const float *x, int T)
 {
     const warp_hip_cfg *g = &c->cfg;
     const int H = g->hidden, Is = L->s_inter;
+    /* a batch: on the matrix cores, x and h split into fp16 halves */
+    if (T >= 8 && L->s_bits != 3 && L->s_group % 32 == 0 && H % L->s_group == 0 && Is % L->s_group == 0) {
+        KRN(c, wk_split(x, T, H, c->xs, c->xscale, c->st));
+        KRN(c, wk_mvq_mfma(L->sq[0], L->ss[0], L->s_rowbytes[0], L->s_group, L->s_bits, c->xs, c->xscale, Is, H, T,
+                           c->shg, c->st));
+        KRN(c, wk_mvq_mfma(L->sq[1], L->ss[1], L->s_rowbytes[1], L->s_group, L->s_bits, c->xs, c->xscale, Is, H, T,
+                           c->shu, c->st));
+        KRN(c, wk_act_split(c->shg, c->shu, T, Is, g->act_situ, g->situ_beta, g->situ_linear_beta, c->shxs,
+                            c->shxscale, NULL, c->st));
+        KRN(c, wk_mvq_mfma(L->sq[2], L->ss[2], L->s_rowbytes[2], L->s_group, L->s_bits, c->shxs, c->shxscale, H, Is,
+                           T, c->sho, c->st));
+        return 0;
+    }
     KRN(c, wk_mvq(L->sq[0], L->ss[0], L->s_rowbytes[0], L->s_group, L->s_bits, x, Is, H, T, c->shg, c->st));
     KRN(c, wk_mvq(L->sq[1], L->ss[1], L->s_rowbytes[1], L->s_group, L->s_bits, x, Is, H, T, c->shu, c->st));
     KRN(c, wk_act(c->shg, c->shu, T, Is, g->act_situ, g->situ_beta, g->situ_linear_beta, c->shh, c->st));
@@ -1272,7 +1294,7 @@ int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *ou
     KRN(c, wait_copies(c));
     DEV(c, hipMemsetAsync(c->missing, 0, sizeof(int), c->st));
     KRN(c, wk_plan_chunk(c->idx, c->w, T, K, E, table, c->counts, c->offsets, c->pair_tok, c->pair_exp, c->pair_w,
-                         c->jobs, c->max_jobs, c->njobs, c->missing, I, c->st));
+                         c->tok_slots, c->jobs, c->max_jobs, c->njobs, c->missing, I, c->st));
     DEV(c, hipEventRecord(c->ev_before, c->st));
     float *yk[3] = { c->yg, c->yu, c->yd };
     if (c->P6) {
@@ -1297,7 +1319,7 @@ int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *ou
                             WARP_TPJ, c->st));
     }
     if (L->sq[0] && (rc = shared_ffn(c, L, X_dev, T))) return rc;
-    KRN(c, wk_combine_chunk(c->yd, c->offsets, c->pair_tok, c->pair_w, T, K, E, H, L->sq[0] ? c->sho : NULL, out_dev,
+    KRN(c, wk_combine_chunk(c->yd, c->tok_slots, c->pair_w, T, K, H, L->sq[0] ? c->sho : NULL, out_dev,
                             c->st));
     DEV(c, hipMemcpyAsync(c->h_missing, c->missing, sizeof(int), hipMemcpyDeviceToHost, c->st));
     if (route) DEV(c, hipMemcpyAsync(c->h_idx, c->idx, (size_t)P * sizeof(int), hipMemcpyDeviceToHost, c->st));

@@ -267,6 +267,118 @@ extern "C" int wk_mvq(const int8_t *W, const uint16_t *ws, size_t rowbytes, int 
     return 0;
 }
 
+// Batches of tokens on the matrix cores (the shared expert of a chunk):
+// y[t][o] = sum over groups g of scale[o][g] * sum_{i in g} W[o][i] x[t][i],
+// as mvq_rows_f32 (src/simd_avx512.c:20-88) per token. v_mfma_f32_16x16x32_f16
+// takes 16 rows of 32 weights as A (int8 or 4-bit values, exact in fp16) and
+// the fp16 hi/lo halves of x for 8 tokens as B (token t's hi in column 2t, lo
+// in 2t + 1; xs from wk_split), so every product is exact and the sums are
+// fp32; a group's sums are scaled by its fp16 scale in fp32, and at the end
+// the two halves are added and the token's power of two removed. A wave
+// computes 32 rows x 16 tokens (2 x 2 tiles) and loads the next 32-column
+// slice while it multiplies the current one; a block of 4 waves covers 64
+// rows x 32 tokens. N and the group are multiples of 32.
+typedef _Float16 half8v __attribute__((ext_vector_type(8)));
+
+template <int BITS>
+__device__ __forceinline__ half8v q8_of(const int8_t *row, int k) {
+    half8v h;
+    if (BITS == 8) {
+        const uint2 w = *(const uint2 *)(row + k);
+#pragma unroll
+        for (int i = 0; i < 8; i++) h[i] = (_Float16)(int)(int8_t)(((i < 4 ? w.x : w.y) >> (8 * (i & 3))) & 0xFF);
+    } else {
+        const unsigned w = *(const unsigned *)((const uint8_t *)row + (k >> 1));
+#pragma unroll
+        for (int i = 0; i < 8; i++) h[i] = (_Float16)((int)((w >> (4 * i)) & 0xF) - 8);
+    }
+    return h;
+}
+
+template <int BITS>
+__global__ __launch_bounds__(256) void k_mvq_mfma(const int8_t *__restrict__ W, const uint16_t *__restrict__ ws,
+                                                  size_t rowbytes, int group, const _Float16 *__restrict__ xs,
+                                                  const float *__restrict__ xscale, int M, int N, int T,
+                                                  float *__restrict__ y) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int o0 = blockIdx.x * 64 + (wave & 1) * 32, t0 = blockIdx.y * 32 + (wave >> 1) * 16;
+    const int m = lane & 15, kb = lane >> 4, nv = N >> 3, ng = N / group;
+    const int8_t *wr[2];
+    const _Float16 *xr[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) wr[i] = W + (size_t)min(o0 + i * 16 + m, M - 1) * rowbytes;
+#pragma unroll
+    for (int j = 0; j < 2; j++) xr[j] = xs + (size_t)min(t0 + j * 8 + (m >> 1), T - 1) * nv * 16 + (m & 1) * 8;
+    auto load = [&](half8v (&a)[2], half8v (&b)[2], int k0) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) a[i] = q8_of<BITS>(wr[i], k0 + kb * 8);
+#pragma unroll
+        for (int j = 0; j < 2; j++) b[j] = *(const half8v *)(xr[j] + (size_t)((k0 >> 3) + kb) * 16);
+    };
+    f4 acc[2][2], part[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = part[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+    half8v a[2], b[2], an[2], bn[2];
+    load(an, bn, 0);
+    int g = 0, gend = group;
+    for (int k0 = 0; k0 < N; k0 += 32) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) { a[i] = an[i]; b[i] = bn[i]; }
+        if (k0 + 32 < N) load(an, bn, k0 + 32);            // uniform
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) part[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], part[i][j], 0, 0, 0);
+        if (k0 + 32 == gend) {                             // uniform: the group is complete
+            // lane (kb, m) holds rows 4 kb + r of each 16-row tile
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float sc = f16_keep(ws[(size_t)min(o0 + i * 16 + 4 * kb + r, M - 1) * ng + g]);
+#pragma unroll
+                    for (int j = 0; j < 2; j++) {
+                        acc[i][j][r] = __builtin_fmaf(sc, part[i][j][r], acc[i][j][r]);
+                        part[i][j][r] = 0.0f;
+                    }
+                }
+            g++;
+            gend += group;
+        }
+    }
+    // column m holds token m / 2, half m % 2: add the halves, remove 2^k
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float v = acc[i][j][r] + __shfl_xor(acc[i][j][r], 1);
+                const int t = t0 + j * 8 + (m >> 1), o = o0 + i * 16 + 4 * kb + r;
+                if ((m & 1) == 0 && t < T && o < M) y[(size_t)t * M + o] = v * xscale[t];
+            }
+}
+
+extern "C" int wk_mvq_mfma(const int8_t *W, const uint16_t *ws, size_t rowbytes, int group, int bits,
+                           const uint16_t *xs, const float *xscale, int M, int N, int T, float *y, void *stream) {
+    if (M <= 0 || N <= 0 || T <= 0 || (N % 32) || group <= 0 || (group % 32) || (N % group)) return -1;
+    if (bits == 8 && (rowbytes % 8)) return -1;
+    if (bits == 4 && (rowbytes % 4)) return -1;
+    const dim3 grid((M + 63) / 64, (T + 31) / 32);
+    if (bits == 8)
+        hipLaunchKernelGGL(k_mvq_mfma<8>, grid, dim3(256), 0, (hipStream_t)stream, W, ws, rowbytes, group,
+                           (const _Float16 *)xs, xscale, M, N, T, y);
+    else if (bits == 4)
+        hipLaunchKernelGGL(k_mvq_mfma<4>, grid, dim3(256), 0, (hipStream_t)stream, W, ws, rowbytes, group,
+                           (const _Float16 *)xs, xscale, M, N, T, y);
+    else
+        return -1;
+    CHECK_LAUNCH();
+    return 0;
+}
+
 // ---- jobs -----------------------------------------------------------------------------
 
 // Pointers of one matrix inside a record, from the header offsets the table
@@ -1951,105 +2063,157 @@ extern "C" int wk_apply_p6(const warp_job *jobs, const int *njobs, int max_jobs,
 
 // One block. Counts per expert, exclusive scan, then one thread per expert
 // places its pairs in token order and cuts them into jobs of WARP_TPJ.
+// A pair (t, k) is computed when it is token t's first pick of its expert
+// and its weight is not 0 (moe_chunk takes the first pick's weight and
+// skips 0, src/model.c:3631-3636); the others get slot -1.
+__device__ __forceinline__ bool pair_valid(const int *pid, const float *w, int t, int k, int K) {
+    const int e = pid[t * K + k];
+    for (int k2 = 0; k2 < k; k2++)
+        if (pid[t * K + k2] == e) return false;
+    return w[t * K + k] != 0.0f;
+}
+
+// One block. The picks are staged in LDS; each expert gets a bitmap of the
+// tokens that pick it (in LDS when it fits, else the pairs are found by a
+// scan per expert); a pair's place in its expert's list is the number of
+// earlier tokens in that bitmap, its slot in its token's list the number
+// of the token's computed picks with a lower expert id.
 __global__ __launch_bounds__(1024) void k_plan_chunk(const int *__restrict__ idx, const float *__restrict__ w, int T,
                                                      int K, int E, const warp_slot *__restrict__ table,
                                                      int *__restrict__ counts, int *__restrict__ offsets,
                                                      int *__restrict__ pair_tok, int *__restrict__ pair_exp,
-                                                     float *__restrict__ pair_w, warp_job *__restrict__ jobs,
-                                                     int max_jobs, int *__restrict__ njobs, int *__restrict__ missing,
-                                                     int inter) {
-    __shared__ int s_tiles_total;
-    const int P = T * K;
-    for (int e = threadIdx.x; e < E; e += blockDim.x) counts[e] = 0;
+                                                     float *__restrict__ pair_w, int *__restrict__ tok_slots,
+                                                     warp_job *__restrict__ jobs, int max_jobs,
+                                                     int *__restrict__ njobs, int *__restrict__ missing, int inter,
+                                                     int bitmaps) {
+    extern __shared__ int lds_plan[];
+    const int P = T * K, NW = (T + 31) >> 5;
+    int *pid = lds_plan;                            // [P]
+    int *cnt = pid + P;                             // [E]
+    int *off = cnt + E;                             // [E]
+    int *tile0 = off + E;                           // [E]
+    unsigned *bm = (unsigned *)(tile0 + E);         // [E][NW] when bitmaps
+    for (int q = threadIdx.x; q < P; q += blockDim.x) pid[q] = idx[q];
+    for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[e] = 0;
+    if (bitmaps)
+        for (int i = threadIdx.x; i < E * NW; i += blockDim.x) bm[i] = 0u;
     __syncthreads();
-    for (int q = threadIdx.x; q < P; q += blockDim.x) atomicAdd(&counts[idx[q]], 1);
+    for (int q = threadIdx.x; q < P; q += blockDim.x) {
+        const int t = q / K, k = q - t * K;
+        if (pair_valid(pid, w, t, k, K)) {
+            atomicAdd(&cnt[pid[q]], 1);
+            if (bitmaps) atomicOr(&bm[pid[q] * NW + (t >> 5)], 1u << (t & 31));
+        }
+    }
     __syncthreads();
     if (threadIdx.x == 0) {
         int run = 0, tiles = 0, miss = 0;
         for (int e = 0; e < E; e++) {
+            off[e] = run;
             offsets[e] = run;
-            run += counts[e];
-            tiles += (counts[e] + WARP_TPJ - 1) / WARP_TPJ;
-            if (counts[e] && !table[e].rec) miss = 1;
+            counts[e] = cnt[e];
+            tile0[e] = tiles;
+            run += cnt[e];
+            tiles += (cnt[e] + WARP_TPJ - 1) / WARP_TPJ;
+            if (cnt[e] && !table[e].rec) miss = 1;
         }
         offsets[E] = run;
-        s_tiles_total = tiles;
         if (miss) *missing = 1;
         const int nj = (miss || tiles > max_jobs) ? 0 : tiles;
         njobs[0] = njobs[1] = njobs[2] = nj;
         if (tiles > max_jobs) *missing = 2;
     }
     __syncthreads();
+    // every token's K slots: its computed pairs in ascending expert id, then -1
+    for (int q = threadIdx.x; q < P; q += blockDim.x) {
+        const int t = q / K, k = q - t * K, e = pid[q];
+        const bool v = pair_valid(pid, w, t, k, K);
+        int r = 0, nv = 0, ninv = 0;
+        for (int k2 = 0; k2 < K; k2++) {
+            const bool v2 = pair_valid(pid, w, t, k2, K);
+            nv += v2;
+            r += v2 && pid[t * K + k2] < e;
+            ninv += !v2 && k2 < k;
+        }
+        if (!v) {
+            tok_slots[q - k + nv + ninv] = -1;
+            continue;
+        }
+        int pos = off[e];
+        if (bitmaps) {
+            const unsigned *row = bm + e * NW;
+            for (int i = 0; i < (t >> 5); i++) pos += __popc(row[i]);
+            pos += __popc(row[t >> 5] & ((1u << (t & 31)) - 1u));
+        } else {
+            for (int t2 = 0; t2 < t; t2++)
+                for (int k2 = 0; k2 < K; k2++)
+                    if (pid[t2 * K + k2] == e && pair_valid(pid, w, t2, k2, K)) pos++;
+        }
+        pair_tok[pos] = t;
+        pair_exp[pos] = e;
+        pair_w[pos] = w[q];
+        tok_slots[q - k + r] = pos;
+    }
+    __syncthreads();
     if (njobs[0] == 0) return;
-    // job index of expert e's first tile = number of tiles of experts < e
     for (int e = threadIdx.x; e < E; e += blockDim.x) {
-        const int c = counts[e];
-        if (!c) continue;
-        int tile0 = 0;
-        for (int e2 = 0; e2 < e; e2++) tile0 += (counts[e2] + WARP_TPJ - 1) / WARP_TPJ;
-        int pos = offsets[e];
-        for (int t = 0; t < T; t++)
-            for (int k = 0; k < K; k++)
-                if (idx[t * K + k] == e) {
-                    pair_tok[pos] = t;
-                    pair_exp[pos] = e;
-                    pair_w[pos] = w[t * K + k];
-                    pos++;
-                }
+        const int c = cnt[e];
         const int ntile = (c + WARP_TPJ - 1) / WARP_TPJ;
         for (int i = 0; i < ntile; i++) {
-            const int base = offsets[e] + i * WARP_TPJ, n = min(WARP_TPJ, c - i * WARP_TPJ);
+            const int base = off[e] + i * WARP_TPJ, n = min(WARP_TPJ, c - i * WARP_TPJ);
             for (int kind = 0; kind < 3; kind++) {
-                warp_job jb;
-                job_ptrs(jb, table[e], kind, inter);
-                jb.n = n;
-                jb.rsv = 0;
+                warp_job *jo = jobs + (size_t)kind * max_jobs + tile0[e] + i;
+                const int soff = kind == 0 ? 0 : kind == 1 ? inter : 2 * inter;
+                jo->idx = table[e].rec + table[e].off[kind];
+                jo->scale = (const uint16_t *)(table[e].rec + table[e].off[3]) + soff;
+                jo->n = n;
+                jo->rsv = 0;
                 for (int s = 0; s < WARP_TPJ; s++) {
                     const int slot = base + (s < n ? s : 0);
-                    jb.xi[s] = kind == 2 ? slot : pair_tok[slot];
-                    jb.yi[s] = slot;
+                    jo->xi[s] = kind == 2 ? slot : pair_tok[slot];
+                    jo->yi[s] = slot;
                 }
-                jobs[(size_t)kind * max_jobs + tile0 + i] = jb;
             }
         }
     }
 }
 
 extern "C" int wk_plan_chunk(const int *idx, const float *w, int T, int K, int E, const warp_slot *table,
-                             int *counts, int *offsets, int *pair_tok, int *pair_exp, float *pair_w, warp_job *jobs,
-                             int max_jobs, int *njobs, int *missing, int inter, void *stream) {
+                             int *counts, int *offsets, int *pair_tok, int *pair_exp, float *pair_w, int *tok_slots,
+                             warp_job *jobs, int max_jobs, int *njobs, int *missing, int inter, void *stream) {
     if (T <= 0 || K <= 0 || E <= 0 || max_jobs <= 0) return -1;
-    hipLaunchKernelGGL(k_plan_chunk, dim3(1), dim3(1024), 0, (hipStream_t)stream, idx, w, T, K, E, table, counts,
-                       offsets, pair_tok, pair_exp, pair_w, jobs, max_jobs, njobs, missing, inter);
+    // the picks and the per-expert tables in LDS; the token bitmaps too when they fit
+    const size_t base = ((size_t)T * K + 3 * (size_t)E) * sizeof(int);
+    const size_t bms = (size_t)E * ((T + 31) / 32) * sizeof(unsigned);
+    if (base > 65536) return -1;
+    const int bitmaps = base + bms <= 98304;
+    static bool attr = false;
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute((const void *)k_plan_chunk, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           98304);
+        if (e != hipSuccess) return -(int)e - 1000;
+        attr = true;
+    }
+    hipLaunchKernelGGL(k_plan_chunk, dim3(1), dim3(1024), base + (bitmaps ? bms : 0), (hipStream_t)stream, idx, w, T,
+                       K, E, table, counts, offsets, pair_tok, pair_exp, pair_w, tok_slots, jobs, max_jobs, njobs,
+                       missing, inter, bitmaps);
     CHECK_LAUNCH();
     return 0;
 }
 
 // Per token: the pairs of that token in ascending expert id, each weighted
 // and added in that order (moe_chunk's loop order, src/model.c:3601-3656).
-__global__ __launch_bounds__(256) void k_combine_chunk(const float *__restrict__ y, const int *__restrict__ offsets,
-                                                       const int *__restrict__ pair_tok,
-                                                       const float *__restrict__ pair_w, int T, int K, int E, int H,
+__global__ __launch_bounds__(256) void k_combine_chunk(const float *__restrict__ y, const int *__restrict__ tok_slots,
+                                                       const float *__restrict__ pair_w, int T, int K, int H,
                                                        const float *__restrict__ add0, float *__restrict__ out) {
-    __shared__ int slots[WARP_MAX_K];
-    __shared__ int nsl;
     const int t = blockIdx.y;
-    if (threadIdx.x == 0) {
-        int n = 0;
-        for (int e = 0; e < E && n < K; e++)
-            for (int p = offsets[e]; p < offsets[e + 1]; p++)
-                if (pair_tok[p] == t) {
-                    slots[n++] = p;
-                    break;
-                }
-        nsl = n;
-    }
-    __syncthreads();
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= H) return;
+    const int *sl = tok_slots + (size_t)t * K;
     float s = 0.0f;
-    for (int q = 0; q < nsl; q++) {
-        const int p = slots[q];
+    for (int q = 0; q < K; q++) {
+        const int p = sl[q];
+        if (p < 0) break;                       // the token's computed pairs come first
         const float wj = pair_w[p];
         if (wj == 0.0f) continue;
         s = __fadd_rn(s, __fmul_rn(wj, y[(size_t)p * H + i]));
@@ -2058,11 +2222,11 @@ __global__ __launch_bounds__(256) void k_combine_chunk(const float *__restrict__
     out[(size_t)t * H + i] = s;
 }
 
-extern "C" int wk_combine_chunk(const float *y, const int *offsets, const int *pair_tok, const float *pair_w, int T,
-                                int K, int E, int H, const float *add0, float *out, void *stream) {
-    if (T <= 0 || K <= 0 || K > WARP_MAX_K || E <= 0 || H <= 0) return -1;
-    hipLaunchKernelGGL(k_combine_chunk, dim3((H + 255) / 256, T), dim3(256), 0, (hipStream_t)stream, y, offsets,
-                       pair_tok, pair_w, T, K, E, H, add0, out);
+extern "C" int wk_combine_chunk(const float *y, const int *tok_slots, const float *pair_w, int T, int K, int H,
+                                const float *add0, float *out, void *stream) {
+    if (T <= 0 || K <= 0 || K > WARP_MAX_K || H <= 0) return -1;
+    hipLaunchKernelGGL(k_combine_chunk, dim3((H + 255) / 256, T), dim3(256), 0, (hipStream_t)stream, y, tok_slots,
+                       pair_w, T, K, H, add0, out);
     CHECK_LAUNCH();
     return 0;
 }

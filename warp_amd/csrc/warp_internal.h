@@ -73,6 +73,13 @@ typedef struct {
 /* x [T][N] f32 -> xs [T][N/8][2][8] fp16, xscale [T]. */
 int wk_split(const float *x, int T, int N, uint16_t *xs, float *xscale, void *stream);
 
+/* Batched quantised rows on the matrix cores (Q8G and Q4G with groups of a
+ * multiple of 32, N a multiple of the group): y [T][M] = dequant(W) . x, x
+ * given split as [T][N/8][2][8] fp16 with xscale [T] (wk_split). Returns -1
+ * for shapes it does not take (the caller uses wk_mvq). */
+int wk_mvq_mfma(const int8_t *W, const uint16_t *ws, size_t rowbytes, int group, int bits,
+                const uint16_t *xs, const float *xscale, int M, int N, int T, float *y, void *stream);
+
 /* Router logits [T][E] = W [E][H] . x [T][H]. strict = 1 reproduces the
  * reference's sequential, unfused fp32 sum (dotf on x86); 0 is a parallel
  * fixed-order tree. */
@@ -182,19 +189,19 @@ int wk_act(const float *g, const float *u, int P, int I, int act_situ, float bet
 
 /* Prefill: token-to-expert grouping on the GPU. From route idx/w [T][K]:
  * counts per expert, exclusive scan, pairs sorted by (expert, token) into
- * pair_tok/pair_exp/pair_w [T*K]; gate/up jobs (tiles of WARP_TPJ tokens of
+ * pair_tok/pair_exp/pair_w [T*K], and tok_slots [T][K]: each token's pair
+ * slots in ascending expert id; gate/up jobs (tiles of WARP_TPJ tokens of
  * one expert; xi = token, yi = pair slot) and down jobs (xi = yi = pair
  * slot) written to jobs[kind*max_jobs ..], counts to njobs[3]. Pairs whose
  * expert has no resident record set *missing. */
 int wk_plan_chunk(const int *idx, const float *w, int T, int K, int E,
-                  const warp_slot *table, int *counts, int *offsets,
-                  int *pair_tok, int *pair_exp, float *pair_w, warp_job *jobs,
+                  const warp_slot *table, int *counts, int *offsets, int *pair_tok,
+                  int *pair_exp, float *pair_w, int *tok_slots, warp_job *jobs,
                   int max_jobs, int *njobs, int *missing, int inter, void *stream);
-/* out [T][H] = per token, sum over its pairs in ascending expert id of
- * w * y[pair], then + add0 [T][H] when given. */
-int wk_combine_chunk(const float *y, const int *offsets, const int *pair_tok,
-                     const float *pair_w, int T, int K, int E, int H, const float *add0,
-                     float *out, void *stream);
+/* out [T][H] = per token, sum over its pairs in ascending expert id (tok_slots)
+ * of w * y[pair], then + add0 [T][H] when given. */
+int wk_combine_chunk(const float *y, const int *tok_slots, const float *pair_w, int T, int K, int H,
+                     const float *add0, float *out, void *stream);
 
 /* Synthetic device data for benchmarks: fill n bytes with a counter-based
  * hash of (seed, offset). */
