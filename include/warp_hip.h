@@ -127,6 +127,13 @@ typedef struct warp_hip_ctx warp_hip_ctx;
  * reference's waste_fetch_fn (src/ecache.h:35-38), e.g. bank_fetch. */
 typedef int (*warp_hip_fetch_fn)(void *user, int layer, int expert, uint8_t *dst);
 
+/* Returns where record (layer, expert) already sits in pinned host memory
+ * (from warp_hip_host_alloc), or NULL when it cannot. The miss copies it to
+ * HBM from there, without a staging copy: the ecache's host slots as the DMA
+ * source (src/ecache.c:347-349). It must stay unchanged until the next
+ * synchronising call. No counterpart in the reference's interface. */
+typedef const uint8_t *(*warp_hip_fetch_host_fn)(void *user, int layer, int expert);
+
 typedef struct {
     uint64_t hits, misses, bytes_read, evictions;
     uint64_t prefetched, spec_issued;      /* as waste_ecache (src/ecache.h:69-71) */
@@ -170,6 +177,13 @@ int warp_hip_set_shared(warp_hip_ctx *c, int layer, int bits, int group, int int
  * record_check does, src/model.c:1698-1745, plus the offsets the kernels
  * rely on). fetch is how misses are filled. */
 int warp_hip_set_fetch(warp_hip_ctx *c, warp_hip_fetch_fn fetch, void *user);
+/* Misses read in place from pinned host records instead (replaces a
+ * fetch function set before, and is replaced by one set after). */
+int warp_hip_set_fetch_host(warp_hip_ctx *c, warp_hip_fetch_host_fn fetch, void *user);
+/* Pinned host memory the device copies from directly (hipHostMalloc), for
+ * records kept on the host; NULL on failure. */
+void *warp_hip_host_alloc(warp_hip_ctx *c, size_t bytes);
+void warp_hip_host_free(warp_hip_ctx *c, void *p);
 int warp_hip_put_expert(warp_hip_ctx *c, int layer, int expert, const uint8_t *rec);
 /* Replaces waste_ecache_prefetch (src/ecache.h:160-164): speculative fills on
  * the copy stream; not counted as misses. */

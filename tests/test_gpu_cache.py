@@ -34,9 +34,12 @@ def resident_ctx(model, **kw):
     return ctx
 
 
-def fetching_ctx(model, slots, lookahead=0, verify=False, records=None):
+def fetching_ctx(model, slots, lookahead=0, verify=False, records=None, mode="copy"):
     """Codebooks, routers and shared experts uploaded, no records: every
-    record comes through the fetch callback into a cache of `slots`."""
+    record comes through the fetch callback into a cache of `slots`. mode
+    "copy": the callback copies the record into the library's staging
+    buffer; "host": the records sit in pinned host memory and the callback
+    returns where, so the miss copies from there."""
     import warp_amd
     ctx = open_ctx(model, max_tokens=32, cache_slots=slots, lookahead=lookahead, verify=verify)
     S = ct.FMT_STAGES[model.spec.fmt]
@@ -52,7 +55,17 @@ def fetching_ctx(model, slots, lookahead=0, verify=False, records=None):
                            [np.ascontiguousarray(q[1]) for q in lay.shared], [q[2] for q in lay.shared])
     recs = records if records is not None else {(L, e): r for L in range(model.spec.layers)
                                                 for e, r in enumerate(model.layers[L].records)}
-    ctx.set_fetch(lambda L, e: recs.get((L, e)))
+    if mode == "copy":
+        ctx.set_fetch(lambda L, e: recs.get((L, e)))
+        return ctx
+    keys = sorted(recs)
+    pool = ctx.host_alloc(len(keys) * model.rec_bytes)
+    where = {}
+    for i, k in enumerate(keys):
+        pool[i * model.rec_bytes:(i + 1) * model.rec_bytes] = np.frombuffer(recs[k], np.uint8)
+        where[k] = pool.ctypes.data + i * model.rec_bytes
+    ctx._host_pool = pool
+    ctx.set_fetch_host(lambda L, e: where.get((L, e)))
     return ctx
 
 
@@ -70,8 +83,9 @@ def run_stack(ctx, X):
     return np.array(outs), np.array(routes)
 
 
+@pytest.mark.parametrize("mode", ["copy", "host"])
 @pytest.mark.parametrize("lookahead", [0, 3])
-def test_decode_cache_equals_resident(model, lookahead):
+def test_decode_cache_equals_resident(model, lookahead, mode):
     X = np.random.default_rng(5).normal(size=(12, SPEC["hidden"])).astype(np.float32)
     ref_ctx = resident_ctx(model)
     try:
@@ -79,12 +93,14 @@ def test_decode_cache_equals_resident(model, lookahead):
     finally:
         ref_ctx.close()
     slots = 10                                   # 3 layers x 32 experts do not fit
-    ctx = fetching_ctx(model, slots, lookahead=lookahead)
+    ctx = fetching_ctx(model, slots, lookahead=lookahead, mode=mode)
     try:
         out, route = run_stack(ctx, X)
         st = ctx.cache_stats()
     finally:
-        ctx.close()
+        ctx.close()                              # drains the copy stream before the pool goes
+        if mode == "host":
+            ctx.host_free(ctx._host_pool)
     assert np.array_equal(route, ref_route)
     assert np.array_equal(out.view(np.uint32), ref_out.view(np.uint32)), "cache path changed the result"
     K, sel = SPEC["top_k"], len(route) * SPEC["top_k"]
@@ -93,11 +109,12 @@ def test_decode_cache_equals_resident(model, lookahead):
     assert st["bytes_read"] == (st["misses"] + st["prefetched"]) * model.rec_bytes or \
         st["bytes_read"] >= st["misses"] * model.rec_bytes, st
     assert st["evictions"] > 0 and st["resident"] <= slots, st
-    log(f"decode, lookahead {lookahead}: bit-identical to resident over {len(X)} tokens x "
+    log(f"decode, lookahead {lookahead}, {mode} fetch: bit-identical to resident over {len(X)} tokens x "
         f"{SPEC['layers']} layers; {st}")
 
 
-def test_chunk_cache_equals_resident(model):
+@pytest.mark.parametrize("mode", ["copy", "host"])
+def test_chunk_cache_equals_resident(model, mode):
     T = 23                                       # a ragged batch
     X = np.random.default_rng(8).normal(size=(T, SPEC["hidden"])).astype(np.float32)
     ref_ctx = resident_ctx(model)
@@ -105,17 +122,19 @@ def test_chunk_cache_equals_resident(model):
         ref = [ref_ctx.moe_chunk_host(L, X) for L in range(SPEC["layers"])]
     finally:
         ref_ctx.close()
-    ctx = fetching_ctx(model, slots=SPEC["experts"])   # one layer's worth: misses and evictions
+    ctx = fetching_ctx(model, slots=SPEC["experts"], mode=mode)   # one layer's worth: misses and evictions
     try:
         got = [ctx.moe_chunk_host(L, X) for L in range(SPEC["layers"])]
         st = ctx.cache_stats()
     finally:
-        ctx.close()
+        ctx.close()                              # drains the copy stream before the pool goes
+        if mode == "host":
+            ctx.host_free(ctx._host_pool)
     for L in range(SPEC["layers"]):
         assert np.array_equal(got[L][1], ref[L][1])
         assert np.array_equal(got[L][0].view(np.uint32), ref[L][0].view(np.uint32)), L
     assert st["misses"] > 0 and st["evictions"] > 0, st
-    log(f"chunk of {T}: bit-identical to resident over {SPEC['layers']} layers; {st}")
+    log(f"chunk of {T}, {mode} fetch: bit-identical to resident over {SPEC['layers']} layers; {st}")
 
 
 def test_corrupt_record_is_refused(model):

@@ -247,6 +247,8 @@ struct warp_hip_ctx {
     int stage_next, stage_used[N_STAGE];
     warp_hip_fetch_fn fetch;
     void *fetch_user;
+    warp_hip_fetch_host_fn fetch_host;  /* records read in place from pinned host memory */
+    void *fetch_host_user;
     warp_hip_cache_stats stats;
     int *pin, n_pin, pin_layer;     /* experts of the layer in flight      */
     /* device scratch */
@@ -881,8 +883,37 @@ int warp_hip_set_fetch(warp_hip_ctx *c, warp_hip_fetch_fn fetch, void *user)
     if (!c) return WARP_HIP_E_ARG;
     c->fetch = fetch;
     c->fetch_user = user;
+    if (fetch) c->fetch_host = NULL;
     return 0;
 }
+
+int warp_hip_set_fetch_host(warp_hip_ctx *c, warp_hip_fetch_host_fn fetch, void *user)
+{
+    if (!c) return WARP_HIP_E_ARG;
+    c->fetch_host = fetch;
+    c->fetch_host_user = user;
+    if (fetch) c->fetch = NULL;
+    return 0;
+}
+
+void *warp_hip_host_alloc(warp_hip_ctx *c, size_t bytes)
+{
+    void *p = NULL;
+    if (!c || !bytes) return NULL;
+    if (hipSetDevice(c->cfg.device) != hipSuccess || hipHostMalloc(&p, bytes, 0) != hipSuccess) {
+        set_err(c, WARP_HIP_E_NOMEM, -1, -1, "pinned host allocation of %zu bytes", bytes);
+        return NULL;
+    }
+    return p;
+}
+
+void warp_hip_host_free(warp_hip_ctx *c, void *p)
+{
+    (void)c;
+    if (p) (void)hipHostFree(p);
+}
+
+static int can_fetch(const warp_hip_ctx *c) { return c->fetch != NULL || c->fetch_host != NULL; }
 
 void warp_hip_get_cache_stats(const warp_hip_ctx *c, warp_hip_cache_stats *st)
 {
@@ -900,8 +931,23 @@ void warp_hip_get_cache_stats(const warp_hip_ctx *c, warp_hip_cache_stats *st)
  * read the victim), or NULL. */
 static int fill_from_fetch(warp_hip_ctx *c, int layer, int expert, hipEvent_t after)
 {
-    if (!c->fetch)
+    if (!can_fetch(c))
         return set_err(c, WARP_HIP_E_MISSING, layer, expert, "expert not resident and no fetch function");
+    if (c->fetch_host) {
+        /* the record is copied from where the caller keeps it (pinned host
+         * memory from warp_hip_host_alloc), no staging copy */
+        const uint8_t *src = c->fetch_host(c->fetch_host_user, layer, expert);
+        if (!src) return set_err(c, WARP_HIP_E_READ, layer, expert, "fetch failed");
+        int rc = check_record(c, src, layer, expert);
+        if (rc) return rc;
+        const int s = claim_slot(c, layer, expert);
+        if (s < 0) return s;
+        if (after) DEV(c, hipStreamWaitEvent(c->cp, after, 0));
+        DEV(c, hipMemcpyAsync(c->pool + (size_t)s * c->cfg.rec_bytes, src, c->cfg.rec_bytes, hipMemcpyHostToDevice,
+                              c->cp));
+        c->stats.bytes_read += c->cfg.rec_bytes;
+        return publish_slot(c, layer, expert, s, src);
+    }
     const int i = c->stage_next;
     c->stage_next = (c->stage_next + 1) % N_STAGE;
     if (c->stage_used[i]) DEV(c, hipEventSynchronize(c->ev_stage[i]));
@@ -1101,7 +1147,7 @@ static int shared_ffn(warp_hip_ctx *c, const layer_t *L, const float *x, int T)
 static int lookahead_launch(warp_hip_ctx *c, int layer, const float *x_dev)
 {
     const warp_hip_cfg *g = &c->cfg;
-    if (!g->lookahead || !c->fetch || layer + 1 >= g->n_layers) return 0;
+    if (!g->lookahead || !can_fetch(c) || layer + 1 >= g->n_layers) return 0;
     const layer_t *N = &c->L[layer + 1];
     if (!N->router && !N->rq) return 0;
     if (N->resident == g->n_experts) return 0;
@@ -1156,7 +1202,7 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
     if (n_la < 0) return n_la;
     /* where the device routes with the expert table, the table kernel's
      * gate/up launch does the routing itself (one launch less) */
-    const int fuse_route = use_lut && (L->resident == E || !c->fetch) && wk_lut_route_ok(g->fmt, E, K, 1, 0, 2);
+    const int fuse_route = use_lut && (L->resident == E || !can_fetch(c)) && wk_lut_route_ok(g->fmt, E, K, 1, 0, 2);
     if (L->resident == E) {
         /* everything resident: route and build the jobs on the device, no
          * host round trip */
@@ -1166,7 +1212,7 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
                             table, c->jobs, c->njobs, c->missing, I, c->st));
         c->stats.hits += (uint64_t)K;
         if (c->pin_layer == layer) c->pin_layer = -1;
-    } else if (!c->fetch) {
+    } else if (!can_fetch(c)) {
         /* nothing to fetch with: the device flags a selected expert that is
          * not resident (sticky), the combine poisons this layer's output with
          * NaN, and the next synchronising call reports E_MISSING */
@@ -1274,7 +1320,7 @@ int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *ou
     KRN(c, logits_of(c, L, X_dev, T, c->logits, c->st));
     KRN(c, wk_route(c->logits, L->bias, E, K, T, g->router_act, g->renorm, g->routed_scale, c->idx, c->w, NULL, NULL,
                     NULL, NULL, 0, c->st));
-    if (L->resident != E && c->fetch) {
+    if (L->resident != E && can_fetch(c)) {
         DEV(c, hipMemcpyAsync(c->h_idx, c->idx, (size_t)P * sizeof(int), hipMemcpyDeviceToHost, c->st));
         DEV(c, hipStreamSynchronize(c->st));
         /* each distinct record once, ascending (src/model.c:3595-3603) */

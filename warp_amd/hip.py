@@ -49,6 +49,7 @@ class CacheStats(C.Structure):
 
 
 FETCH_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_int, C.c_int, C.POINTER(C.c_uint8))
+FETCH_HOST_FN = C.CFUNCTYPE(C.c_void_p, C.c_void_p, C.c_int, C.c_int)
 
 # name -> (restype, argtypes); also the list of symbols the header declares
 SIGNATURES = {
@@ -66,6 +67,9 @@ SIGNATURES = {
     "warp_hip_set_shared": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p * 3,
                                       C.c_void_p * 3, C.c_size_t * 3]),
     "warp_hip_set_fetch": (C.c_int, [C.c_void_p, FETCH_FN, C.c_void_p]),
+    "warp_hip_set_fetch_host": (C.c_int, [C.c_void_p, FETCH_HOST_FN, C.c_void_p]),
+    "warp_hip_host_alloc": (C.c_void_p, [C.c_void_p, C.c_size_t]),
+    "warp_hip_host_free": (None, [C.c_void_p, C.c_void_p]),
     "warp_hip_put_expert": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p]),
     "warp_hip_prefetch": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_int]),
     "warp_hip_get_cache_stats": (None, [C.c_void_p, C.POINTER(CacheStats)]),
@@ -198,6 +202,31 @@ class Context:
                 return -1
         self._fetch_cb = FETCH_FN(cb)
         self._check(lib().warp_hip_set_fetch(self.h, self._fetch_cb, None))
+
+    def set_fetch_host(self, fn):
+        """fn(layer, expert) -> address (int) of the record in pinned host
+        memory from host_alloc, or 0/None when it cannot; the miss copies it
+        to HBM from there."""
+        def cb(_user, layer, expert):
+            try:
+                return fn(layer, expert) or None
+            except Exception:
+                return None
+        self._fetch_host_cb = FETCH_HOST_FN(cb)
+        self._check(lib().warp_hip_set_fetch_host(self.h, self._fetch_host_cb, None))
+
+    def host_alloc(self, nbytes):
+        """Pinned host memory as a uint8 numpy array (freed with host_free)."""
+        import numpy as np
+        p = lib().warp_hip_host_alloc(self.h, nbytes)
+        if not p:
+            self._check(E_NOMEM)
+        return np.ctypeslib.as_array((C.c_uint8 * nbytes).from_address(p))
+
+    def host_free(self, arr):
+        """Free host_alloc memory: after every copy from it has finished
+        (a synchronising call, or close)."""
+        lib().warp_hip_host_free(self.h, arr.ctypes.data)
 
     def prefetch(self, layer, ids):
         import numpy as np
