@@ -116,8 +116,9 @@ typedef struct {
     size_t cache_bytes;    /* HBM budget for expert records                    */
     int verify;            /* crc32 every record entering the cache
                             * (WASTE_VERIFY, src/model.c:1742-1744)            */
-    int lookahead;         /* experts of layer L+1 to prefetch from layer L's
-                            * input (WASTE_LOOKAHEAD, src/model.c:2680-2711)   */
+    int lookahead;         /* experts of layer L+1 to prefetch per token from
+                            * layer L's input (WASTE_LOOKAHEAD,
+                            * src/model.c:2680-2711)                           */
     int device;            /* HIP device ordinal                               */
 } warp_hip_cfg;
 
@@ -204,10 +205,12 @@ int warp_hip_moe_decode_host(warp_hip_ctx *c, int layer, const float *x, float *
 /* Replaces moe_chunk (src/model.c:3512-3693) for T <= max_tokens tokens:
  * per-token routing, pairs grouped by expert on the GPU, matrix-core
  * matvecs over tiles of up to 8 tokens per expert, per-token combine in
- * ascending expert id, shared expert. route/rw (host, may be NULL) get
- * [T][K]. */
-int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *out_dev, int T,
-                       int *route, float *rw);
+ * ascending expert id, shared expert. resid_dev ([T][H], may be NULL) is
+ * added to out. route/rw (host, may be NULL) get [T][K]. With lookahead,
+ * the next layer's experts predicted for each token are fetched while this
+ * layer computes (the reference has no lookahead on this path). */
+int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *out_dev,
+                       const float *resid_dev, int T, int *route, float *rw);
 int warp_hip_moe_chunk_host(warp_hip_ctx *c, int layer, const float *X, float *out, int T,
                             int *route, float *rw);
 

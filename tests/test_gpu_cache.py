@@ -137,6 +137,76 @@ def test_chunk_cache_equals_resident(model, mode):
     log(f"chunk of {T}, {mode} fetch: bit-identical to resident over {SPEC['layers']} layers; {st}")
 
 
+def run_chunk_stack(ctx, batches):
+    """Each batch through every layer on the device, h <- h + moe(h) (the
+    residual added by the chunk's combine)."""
+    outs, routes = [], []
+    for X in batches:
+        h = dev(X)
+        for L in range(SPEC["layers"]):
+            o = empty((len(X), SPEC["hidden"]))
+            r, _ = ctx.moe_chunk(L, h, o, len(X), want_route=True, resid_dev=h)
+            routes.append(r)
+            h = o
+        outs.append(host(h))
+    return outs, routes
+
+
+@pytest.mark.parametrize("mode", ["copy", "host"])
+@pytest.mark.parametrize("lookahead", [0, 4])
+def test_chunk_stack_cache_equals_resident(model, lookahead, mode):
+    """Ragged batches of 9 tokens through the 3-layer stack, twice: about
+    two thirds of a layer's experts are picked per batch, so a cache of one
+    layer's worth both misses and has room for the lookahead's guesses,
+    which the batch's own fills must not evict."""
+    rng = np.random.default_rng(12)
+    batches = [rng.normal(size=(9, SPEC["hidden"])).astype(np.float32) for _ in range(2)]
+    ref_ctx = resident_ctx(model)
+    try:
+        ref_out, ref_route = run_chunk_stack(ref_ctx, batches)
+    finally:
+        ref_ctx.close()
+    ctx = fetching_ctx(model, slots=SPEC["experts"], lookahead=lookahead, mode=mode)
+    try:
+        out, route = run_chunk_stack(ctx, batches)
+        st = ctx.cache_stats()
+    finally:
+        ctx.close()
+        if mode == "host":
+            ctx.host_free(ctx._host_pool)
+    for a, b in zip(route, ref_route):
+        assert np.array_equal(a, b)
+    for a, b in zip(out, ref_out):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), "cache path changed the result"
+    distinct = sum(len(np.unique(r)) for r in route)
+    assert st["hits"] + st["misses"] == distinct, st      # each distinct record of a layer once
+    assert st["bytes_read"] == (st["misses"] + st["spec_issued"]) * model.rec_bytes, st
+    if lookahead:
+        assert st["spec_issued"] > 0, st
+    else:
+        assert st["spec_issued"] == 0, st
+    log(f"chunk stack, lookahead {lookahead}, {mode} fetch: bit-identical to resident; {st}")
+
+
+def test_chunk_residual_is_added_last():
+    """out(resid) = fl(out(no resid) + resid), bit for bit: the residual
+    is the last addition, as decode's."""
+    m = ct.build(ct.Spec(**{**SPEC, "layers": 1}))
+    ctx = resident_ctx(m)
+    try:
+        X = np.random.default_rng(4).normal(size=(11, SPEC["hidden"])).astype(np.float32)
+        R = np.random.default_rng(6).normal(size=(11, SPEC["hidden"])).astype(np.float32)
+        xd, rd = dev(X), dev(R)
+        o0, o1 = empty((11, SPEC["hidden"])), empty((11, SPEC["hidden"]))
+        ctx.moe_chunk(0, xd, o0, 11)
+        ctx.moe_chunk(0, xd, o1, 11, resid_dev=rd)
+        want = (host(o0) + R).astype(np.float32)
+        assert np.array_equal(host(o1).view(np.uint32), want.view(np.uint32))
+        log("chunk residual: out(resid) == out + resid bit for bit over 11 tokens")
+    finally:
+        ctx.close()
+
+
 def test_corrupt_record_is_refused(model):
     import warp_amd
     recs = {(L, e): bytearray(r) for L in range(model.spec.layers) for e, r in enumerate(model.layers[L].records)}

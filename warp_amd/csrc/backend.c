@@ -224,6 +224,7 @@ typedef struct {
 } layer_t;
 
 #define N_STAGE 32
+#define N_TQ 4                  /* pinned lists of table updates in flight */
 #define WARP_TIMING_N 2048
 #define WARP_TIMING_CLS 4
 
@@ -245,12 +246,26 @@ struct warp_hip_ctx {
     warp_slot *table_dev;       /* [layer][expert] residency and offsets  */
     uint8_t *staging;           /* pinned, N_STAGE records                 */
     int stage_next, stage_used[N_STAGE];
+    /* Expert-table updates of a batch of fills, applied by one launch on
+     * the copy stream after the batch's copies (each key once, the last
+     * value): the copies are not interleaved with kernels. */
+    warp_slot_upd *tq_host[N_TQ];   /* pinned                             */
+    warp_slot_upd *tq_dev;
+    hipEvent_t ev_tq[N_TQ];
+    int tq_used[N_TQ], tq_cur, tq_n, tq_cap;
+    int *tq_pos;                    /* [layer][expert]: index in the list, or -1 */
     warp_hip_fetch_fn fetch;
     void *fetch_user;
     warp_hip_fetch_host_fn fetch_host;  /* records read in place from pinned host memory */
     void *fetch_host_user;
     warp_hip_cache_stats stats;
-    int *pin, n_pin, pin_layer;     /* experts of the layer in flight      */
+    /* Holds keep records from eviction: `hold` is the selection of the
+     * layer in flight, `spec_hold` what the last lookahead brought in or
+     * found resident. A key is held when its pin_gen equals either; 0 is
+     * no hold. */
+    uint32_t *pin_gen;              /* [layer][expert]                     */
+    uint32_t hold, spec_hold, hold_next;
+    int pin_layer;                  /* the layer `hold` belongs to, or -1  */
     /* device scratch */
     float *logits;
     int *idx;
@@ -278,6 +293,8 @@ struct warp_hip_ctx {
     float *la_logits;
     int *la_idx;
     float *la_w;
+    int la_T;                     /* tokens of the lookahead in flight      */
+    int *la_votes, *la_order;     /* [E] host: per expert, tokens predicting it; ids in prefetch order */
     /* pinned host */
     int *h_idx, *h_la_idx, *h_missing;
     float *h_w;
@@ -378,9 +395,9 @@ static int ctx_alloc(warp_hip_ctx *c)
     DMALLOC(c, c->pair_exp, P * 4);
     DMALLOC(c, c->pair_w, P * 4);
     DMALLOC(c, c->tok_slots, P * 4);
-    DMALLOC(c, c->la_logits, (size_t)E * 4);
-    DMALLOC(c, c->la_idx, (size_t)WARP_MAX_K * 4);
-    DMALLOC(c, c->la_w, (size_t)WARP_MAX_K * 4);
+    DMALLOC(c, c->la_logits, (size_t)T * E * 4);
+    DMALLOC(c, c->la_idx, (size_t)T * WARP_MAX_K * 4);
+    DMALLOC(c, c->la_w, (size_t)T * WARP_MAX_K * 4);
     if (c->lut_ok) {
         /* decode: gate+up over K jobs sharing x, then down per job */
         int gr, sp;
@@ -401,7 +418,7 @@ static int ctx_alloc(warp_hip_ctx *c)
     DEV(c, hipMemset(c->missing, 0, sizeof(int)));
     DEV(c, hipHostMalloc((void **)&c->h_idx, P * 4, 0));
     DEV(c, hipHostMalloc((void **)&c->h_w, P * 4, 0));
-    DEV(c, hipHostMalloc((void **)&c->h_la_idx, WARP_MAX_K * 4, 0));
+    DEV(c, hipHostMalloc((void **)&c->h_la_idx, (size_t)T * WARP_MAX_K * 4, 0));
     DEV(c, hipHostMalloc((void **)&c->h_missing, 4 * sizeof(int), 0));
     /* expert cache */
     c->n_slots = g->rec_bytes ? (int)(g->cache_bytes / g->rec_bytes) : 0;
@@ -409,9 +426,11 @@ static int ctx_alloc(warp_hip_ctx *c)
     c->key_slot = (int *)malloc(nkeys * sizeof(int));
     c->slot_key = (int *)malloc(((size_t)c->n_slots + 1) * sizeof(int));
     c->hits = (uint32_t *)calloc((size_t)c->n_slots + 1, sizeof(uint32_t));
-    c->pin = (int *)calloc((size_t)E + 1, sizeof(int));
+    c->pin_gen = (uint32_t *)calloc(nkeys, sizeof(uint32_t));
+    c->la_votes = (int *)calloc((size_t)E, sizeof(int));
+    c->la_order = (int *)calloc((size_t)E, sizeof(int));
     c->last = (uint64_t *)calloc((size_t)c->n_slots + 1, sizeof(uint64_t));
-    if (!c->key_slot || !c->slot_key || !c->hits || !c->last || !c->pin)
+    if (!c->key_slot || !c->slot_key || !c->hits || !c->last || !c->pin_gen || !c->la_votes || !c->la_order)
         return set_err(c, WARP_HIP_E_NOMEM, -1, -1, "host allocation failed");
     for (size_t i = 0; i < nkeys; i++) c->key_slot[i] = -1;
     for (int i = 0; i < c->n_slots; i++) c->slot_key[i] = -1;
@@ -419,6 +438,14 @@ static int ctx_alloc(warp_hip_ctx *c)
     DEV(c, hipMemset(c->table_dev, 0, nkeys * sizeof(warp_slot)));
     if (c->n_slots > 0) DMALLOC(c, c->pool, (size_t)c->n_slots * g->rec_bytes);
     DEV(c, hipHostMalloc((void **)&c->staging, (size_t)N_STAGE * g->rec_bytes, 0));
+    /* a batch touches each expert of one layer at most twice over (the
+     * records it places and the ones they evict) */
+    c->tq_cap = 2 * E + 2;
+    for (int i = 0; i < N_TQ; i++) DEV(c, hipHostMalloc((void **)&c->tq_host[i], (size_t)c->tq_cap * sizeof(warp_slot_upd), 0));
+    DMALLOC(c, c->tq_dev, (size_t)c->tq_cap * sizeof(warp_slot_upd));
+    c->tq_pos = (int *)malloc(nkeys * sizeof(int));
+    if (!c->tq_pos) return set_err(c, WARP_HIP_E_NOMEM, -1, -1, "host allocation failed");
+    for (size_t i = 0; i < nkeys; i++) c->tq_pos[i] = -1;
     return 0;
 }
 
@@ -487,6 +514,11 @@ int warp_hip_open(const warp_hip_cfg *cfg, warp_hip_ctx **out)
             rc = WARP_HIP_E_DEVICE;
             goto fail;
         }
+    for (int i = 0; i < N_TQ; i++)
+        if (!HIPOK(hipEventCreateWithFlags(&c->ev_tq[i], hipEventDisableTiming))) {
+            rc = WARP_HIP_E_DEVICE;
+            goto fail;
+        }
     if (!HIPOK(hipDeviceGetAttribute(&c->n_cu, hipDeviceAttributeMultiprocessorCount, g->device)) || c->n_cu < 1)
         c->n_cu = 256;
     /* the LUT matvec serves decode for the float-LUT formats; it walks the
@@ -523,15 +555,19 @@ void warp_hip_close(warp_hip_ctx *c)
                   c->yd, c->xsh, c->xscaleh, c->hbuf, c->shg, c->shu, c->shh, c->sho, c->lut8, c->lut8d,
                   c->lscale, c->lscaled, c->counts, c->offsets, c->pair_tok, c->pair_exp, c->pair_w, c->tok_slots,
                   c->xin, c->xout, c->la_logits, c->la_idx, c->la_w, c->table_dev, c->pool, c->part,
-                  c->shxs, c->shxscale };
+                  c->shxs, c->shxscale, c->tq_dev };
     for (size_t i = 0; i < sizeof d / sizeof d[0]; i++) hfree(d[i]);
     hhfree(c->h_idx); hhfree(c->h_w); hhfree(c->h_la_idx); hhfree(c->h_missing); hhfree(c->staging);
-    free(c->key_slot); free(c->slot_key); free(c->hits); free(c->last); free(c->pin);
+    for (int i = 0; i < N_TQ; i++) hhfree(c->tq_host[i]);
+    free(c->tq_pos);
+    free(c->key_slot); free(c->slot_key); free(c->hits); free(c->last); free(c->pin_gen);
+    free(c->la_votes); free(c->la_order);
     if (c->tev) {
         for (int i = 0; i < 2 * WARP_TIMING_N; i++) if (c->tev[i]) (void)hipEventDestroy(c->tev[i]);
         free(c->tev);
     }
     for (int i = 0; i < N_STAGE; i++) if (c->ev_stage[i]) (void)hipEventDestroy(c->ev_stage[i]);
+    for (int i = 0; i < N_TQ; i++) if (c->ev_tq[i]) (void)hipEventDestroy(c->ev_tq[i]);
     if (c->ev_copy) (void)hipEventDestroy(c->ev_copy);
     if (c->ev_before) (void)hipEventDestroy(c->ev_before);
     if (c->ev_after) (void)hipEventDestroy(c->ev_after);
@@ -722,32 +758,82 @@ static int check_record(warp_hip_ctx *c, const uint8_t *rec, int layer, int expe
 
 static int is_pinned(const warp_hip_ctx *c, int key)
 {
-    const int E = c->cfg.n_experts;
-    if (c->pin_layer < 0 || key / E != c->pin_layer) return 0;
-    for (int i = 0; i < c->n_pin; i++) if (c->pin[i] == key % E) return 1;
-    return 0;
+    const uint32_t h = c->pin_gen[key];
+    return h != 0 && (h == c->hold || h == c->spec_hold);
+}
+
+static uint32_t new_hold(warp_hip_ctx *c)
+{
+    if (++c->hold_next == 0) ++c->hold_next;
+    return c->hold_next;
 }
 
 /* A slot to fill: a never-used one, else the least-frequent (then least
- * recent) of 16 sampled slots, skipping the layer in flight
+ * recent) of 16 sampled slots that no hold keeps, else the first such slot
  * (the LFRU sampled victim of src/ecache.c:432-460). */
 static int pick_victim(warp_hip_ctx *c)
 {
     if (c->next_free < c->n_slots) return c->next_free++;
     int best = -1;
-    for (int tries = 0; tries < 64 && best < 0; tries++)
-        for (int k = 0; k < 16; k++) {
-            c->rng = c->rng * 1664525u + 1013904223u;
-            const int s = (int)((c->rng >> 8) % (unsigned)c->n_slots);
-            if (c->slot_key[s] >= 0 && is_pinned(c, c->slot_key[s])) continue;
-            if (best < 0 || c->hits[s] < c->hits[best] || (c->hits[s] == c->hits[best] && c->last[s] < c->last[best]))
-                best = s;
-        }
+    for (int k = 0; k < 16; k++) {
+        c->rng = c->rng * 1664525u + 1013904223u;
+        const int s = (int)((c->rng >> 8) % (unsigned)c->n_slots);
+        if (c->slot_key[s] >= 0 && is_pinned(c, c->slot_key[s])) continue;
+        if (best < 0 || c->hits[s] < c->hits[best] || (c->hits[s] == c->hits[best] && c->last[s] < c->last[best]))
+            best = s;
+    }
+    if (best < 0)
+        for (int s = 0; s < c->n_slots; s++)
+            if (c->slot_key[s] < 0 || !is_pinned(c, c->slot_key[s])) { best = s; break; }
     return best;
 }
 
+/* Apply the queued table updates after everything queued on the copy
+ * stream so far (the batch's copies). Kernels that read the table wait for
+ * ev_copy (wait_copies). */
+static int flush_table(warp_hip_ctx *c)
+{
+    if (!c->tq_n) return 0;
+    const int i = c->tq_cur, n = c->tq_n;
+    warp_slot_upd *u = c->tq_host[i];
+    for (int q = 0; q < n; q++) c->tq_pos[u[q].key] = -1;
+    c->tq_n = 0;
+    c->tq_cur = (i + 1) % N_TQ;
+    DEV(c, hipMemcpyAsync(c->tq_dev, u, (size_t)n * sizeof *u, hipMemcpyHostToDevice, c->cp));
+    DEV(c, hipEventRecord(c->ev_tq[i], c->cp));
+    c->tq_used[i] = 1;
+    if (wk_set_slots(c->table_dev, c->tq_dev, n, c->cp))
+        return set_err(c, WARP_HIP_E_DEVICE, -1, -1, "table update");
+    DEV(c, hipEventRecord(c->ev_copy, c->cp));
+    c->copy_pending = 1;
+    return 0;
+}
+
+/* Queue table[key] = {rec, off} for the batch's update launch. */
+static int queue_slot(warp_hip_ctx *c, int key, const uint8_t *rec, const uint32_t off[4])
+{
+    int rc;
+    if (c->tq_n == c->tq_cap && (rc = flush_table(c)) != 0) return rc;
+    if (c->tq_n == 0 && c->tq_used[c->tq_cur]) {
+        DEV(c, hipEventSynchronize(c->ev_tq[c->tq_cur]));   /* its previous list has been copied */
+        c->tq_used[c->tq_cur] = 0;
+    }
+    warp_slot_upd *u = c->tq_host[c->tq_cur];
+    int i = c->tq_pos[key];
+    if (i < 0) {
+        i = c->tq_n++;
+        c->tq_pos[key] = i;
+        u[i].key = key;
+        u[i].pad = 0;
+    }
+    u[i].v.rec = rec;
+    memcpy(u[i].v.off, off, sizeof u[i].v.off);
+    return 0;
+}
+
 /* Assign (layer, expert) a slot, evicting if needed. Returns the slot or a
- * negative code. The caller fills it. */
+ * negative code. The caller fills it; the eviction reaches the device
+ * table with the batch's updates. */
 static int claim_slot(warp_hip_ctx *c, int layer, int expert)
 {
     const int E = c->cfg.n_experts, key = layer * E + expert;
@@ -760,28 +846,24 @@ static int claim_slot(warp_hip_ctx *c, int layer, int expert)
         c->L[old / E].resident--;
         c->stats.evictions++;
         static const uint32_t none[4] = { 0, 0, 0, 0 };
-        if (wk_set_slot(c->table_dev + old, NULL, none, c->cp))
-            return set_err(c, WARP_HIP_E_DEVICE, layer, expert, "table update");
+        int rc = queue_slot(c, old, NULL, none);
+        if (rc) return rc;
     }
     c->slot_key[s] = key;
     c->key_slot[key] = s;
-    c->hits[s] = 0;
+    c->hits[s] = 1;                 /* a claim counts as a use (src/ecache.c:489,508) */
     c->last[s] = ++c->clock;
     c->L[layer].resident++;
     return s;
 }
 
-/* hdr: a host copy of the record's (checked) header */
+/* hdr: a host copy of the record's (checked) header. The entry reaches the
+ * device with the batch's flush_table. */
 static int publish_slot(warp_hip_ctx *c, int layer, int expert, int s, const uint8_t *hdr)
 {
-    const int key = layer * c->cfg.n_experts + expert;
     uint32_t off[4];
     memcpy(off, hdr + WARP_HDR_GATE_OFF, sizeof off);
-    if (wk_set_slot(c->table_dev + key, c->pool + (size_t)s * c->cfg.rec_bytes, off, c->cp))
-        return set_err(c, WARP_HIP_E_DEVICE, layer, expert, "table update");
-    DEV(c, hipEventRecord(c->ev_copy, c->cp));
-    c->copy_pending = 1;
-    return 0;
+    return queue_slot(c, layer * c->cfg.n_experts + expert, c->pool + (size_t)s * c->cfg.rec_bytes, off);
 }
 
 int warp_hip_put_expert(warp_hip_ctx *c, int layer, int expert, const uint8_t *rec)
@@ -792,15 +874,17 @@ int warp_hip_put_expert(warp_hip_ctx *c, int layer, int expert, const uint8_t *r
         return set_err(c, WARP_HIP_E_ARG, layer, expert, "expert id");
     if ((rc = check_record(c, rec, layer, expert))) return rc;
     const int key = layer * c->cfg.n_experts + expert;
-    int s = c->key_slot[key];
-    if (s < 0 && (s = claim_slot(c, layer, expert)) < 0) return s;
-    /* the overwrite waits for everything already queued on the compute
-     * stream, which may still read the slot's previous record */
+    /* the eviction's table update and the overwrite wait for everything
+     * already queued on the compute stream, which may still read the
+     * slot's previous record */
     DEV(c, hipEventRecord(c->ev_before, c->st));
     DEV(c, hipStreamWaitEvent(c->cp, c->ev_before, 0));
+    int s = c->key_slot[key];
+    if (s < 0 && (s = claim_slot(c, layer, expert)) < 0) return s;
     DEV(c, hipMemcpyAsync(c->pool + (size_t)s * c->cfg.rec_bytes, rec, c->cfg.rec_bytes, hipMemcpyHostToDevice, c->cp));
     DEV(c, hipStreamSynchronize(c->cp));
-    return publish_slot(c, layer, expert, s, rec);
+    if ((rc = publish_slot(c, layer, expert, s, rec))) return rc;
+    return flush_table(c);
 }
 
 int warp_hip_put_expert_dev(warp_hip_ctx *c, int layer, int expert, const uint8_t *rec_dev)
@@ -810,10 +894,10 @@ int warp_hip_put_expert_dev(warp_hip_ctx *c, int layer, int expert, const uint8_
     if (expert < 0 || expert >= c->cfg.n_experts || !rec_dev)
         return set_err(c, WARP_HIP_E_ARG, layer, expert, "expert id");
     const int key = layer * c->cfg.n_experts + expert;
-    int s = c->key_slot[key];
-    if (s < 0 && (s = claim_slot(c, layer, expert)) < 0) return s;
     DEV(c, hipEventRecord(c->ev_before, c->st));
     DEV(c, hipStreamWaitEvent(c->cp, c->ev_before, 0));
+    int s = c->key_slot[key];
+    if (s < 0 && (s = claim_slot(c, layer, expert)) < 0) return s;
     DEV(c, hipMemcpyAsync(c->pool + (size_t)s * c->cfg.rec_bytes, rec_dev, c->cfg.rec_bytes,
                           hipMemcpyDeviceToDevice, c->cp));
     /* the header is checked on a host copy of its first bytes */
@@ -828,9 +912,11 @@ int warp_hip_put_expert_dev(warp_hip_ctx *c, int layer, int expert, const uint8_
         c->key_slot[key] = -1;
         c->slot_key[s] = -1;
         c->L[layer].resident--;
+        (void)flush_table(c);          /* the eviction, if any */
         return rc;
     }
-    return publish_slot(c, layer, expert, s, hdr);
+    if ((rc = publish_slot(c, layer, expert, s, hdr))) return rc;
+    return flush_table(c);
 }
 
 int warp_hip_put_expert_synth(warp_hip_ctx *c, int layer, int expert, uint64_t seed, const uint16_t *scales)
@@ -859,16 +945,17 @@ int warp_hip_put_expert_synth(warp_hip_ctx *c, int layer, int expert, uint64_t s
     memcpy(hdr + 20, off, 16);
     if ((rc = check_record(c, hdr, layer, expert))) return rc;
     const int key = layer * g->n_experts + expert;
+    DEV(c, hipEventRecord(c->ev_before, c->st));
+    DEV(c, hipStreamWaitEvent(c->cp, c->ev_before, 0));
     int s = c->key_slot[key];
     if (s < 0 && (s = claim_slot(c, layer, expert)) < 0) return s;
     uint8_t *slot = c->pool + (size_t)s * g->rec_bytes;
-    DEV(c, hipEventRecord(c->ev_before, c->st));
-    DEV(c, hipStreamWaitEvent(c->cp, c->ev_before, 0));
     KRN(c, wk_fill_random(slot, g->rec_bytes, seed, c->cp));
     DEV(c, hipMemcpyAsync(slot, hdr, sizeof hdr, hipMemcpyHostToDevice, c->cp));
     DEV(c, hipMemcpyAsync(slot + off[3], scales, 2 * (2 * (size_t)g->inter + g->hidden), hipMemcpyHostToDevice, c->cp));
     DEV(c, hipStreamSynchronize(c->cp));
-    return publish_slot(c, layer, expert, s, hdr);
+    if ((rc = publish_slot(c, layer, expert, s, hdr))) return rc;
+    return flush_table(c);
 }
 
 const uint8_t *warp_hip_resident(warp_hip_ctx *c, int layer, int expert)
@@ -926,10 +1013,11 @@ void warp_hip_get_cache_stats(const warp_hip_ctx *c, warp_hip_cache_stats *st)
 }
 
 /* Fetch (layer, expert) through the caller's fetch function into a pinned
- * staging buffer, check it, and copy it into a slot on the copy stream.
- * `after` is an event the copy must wait for (the compute that may still
- * read the victim), or NULL. */
-static int fill_from_fetch(warp_hip_ctx *c, int layer, int expert, hipEvent_t after)
+ * staging buffer (or find it in the caller's pinned memory), check it, and
+ * copy it into a slot on the copy stream. The caller orders the copy stream
+ * after the compute that may still read the victim, and ends the batch
+ * with flush_table. */
+static int fill_from_fetch(warp_hip_ctx *c, int layer, int expert)
 {
     if (!can_fetch(c))
         return set_err(c, WARP_HIP_E_MISSING, layer, expert, "expert not resident and no fetch function");
@@ -942,7 +1030,6 @@ static int fill_from_fetch(warp_hip_ctx *c, int layer, int expert, hipEvent_t af
         if (rc) return rc;
         const int s = claim_slot(c, layer, expert);
         if (s < 0) return s;
-        if (after) DEV(c, hipStreamWaitEvent(c->cp, after, 0));
         DEV(c, hipMemcpyAsync(c->pool + (size_t)s * c->cfg.rec_bytes, src, c->cfg.rec_bytes, hipMemcpyHostToDevice,
                               c->cp));
         c->stats.bytes_read += c->cfg.rec_bytes;
@@ -958,7 +1045,6 @@ static int fill_from_fetch(warp_hip_ctx *c, int layer, int expert, hipEvent_t af
     if (rc) return rc;
     const int s = claim_slot(c, layer, expert);
     if (s < 0) return s;
-    if (after) DEV(c, hipStreamWaitEvent(c->cp, after, 0));
     DEV(c, hipMemcpyAsync(c->pool + (size_t)s * c->cfg.rec_bytes, dst, c->cfg.rec_bytes, hipMemcpyHostToDevice, c->cp));
     DEV(c, hipEventRecord(c->ev_stage[i], c->cp));
     c->stage_used[i] = 1;
@@ -966,20 +1052,34 @@ static int fill_from_fetch(warp_hip_ctx *c, int layer, int expert, hipEvent_t af
     return publish_slot(c, layer, expert, s, dst);
 }
 
-static int prefetch_after(warp_hip_ctx *c, int layer, const int *ids, int n, hipEvent_t after)
+/* Speculative fills of `ids` in order, until the cache has no slot left
+ * that no hold keeps. With `hold`, every id is kept under spec_hold: the
+ * resident ones first, so that no fill of this batch evicts another record
+ * the batch asks for. */
+static int prefetch_after(warp_hip_ctx *c, int layer, const int *ids, int n, hipEvent_t after, int hold)
 {
-    int rc;
+    const int E = c->cfg.n_experts;
+    int rc = 0;
+    if (n <= 0) return 0;
+    if (hold)
+        for (int i = 0; i < n; i++)
+            if (ids[i] >= 0 && ids[i] < E && c->key_slot[layer * E + ids[i]] >= 0)
+                c->pin_gen[layer * E + ids[i]] = c->spec_hold;
+    /* every eviction and copy of the batch waits for `after` */
+    if (after) DEV(c, hipStreamWaitEvent(c->cp, after, 0));
     for (int i = 0; i < n; i++) {
-        if (ids[i] < 0 || ids[i] >= c->cfg.n_experts) continue;
-        if (c->key_slot[layer * c->cfg.n_experts + ids[i]] >= 0) continue;
+        if (ids[i] < 0 || ids[i] >= E) continue;
+        if (c->key_slot[layer * E + ids[i]] >= 0) continue;
         /* a guess: not a miss, and never allowed to stall on a full cache */
-        if ((rc = fill_from_fetch(c, layer, ids[i], after)) != 0) {
-            if (rc == WARP_HIP_E_NOSLOT) return 0;
-            return rc;
+        if ((rc = fill_from_fetch(c, layer, ids[i])) != 0) {
+            if (rc == WARP_HIP_E_NOSLOT) rc = 0;
+            break;
         }
+        if (hold) c->pin_gen[layer * E + ids[i]] = c->spec_hold;
         c->stats.spec_issued++;
     }
-    return 0;
+    const int f = flush_table(c);
+    return rc ? rc : f;
 }
 
 int warp_hip_prefetch(warp_hip_ctx *c, int layer, const int *ids, int n)
@@ -988,7 +1088,7 @@ int warp_hip_prefetch(warp_hip_ctx *c, int layer, const int *ids, int n)
     if (rc) return rc;
     /* everything queued so far may still read the slots it would evict */
     DEV(c, hipEventRecord(c->ev_after, c->st));
-    return prefetch_after(c, layer, ids, n, c->ev_after);
+    return prefetch_after(c, layer, ids, n, c->ev_after, 0);
 }
 
 /* Demand residency for `n` experts of `layer`, all pinned against eviction
@@ -997,12 +1097,14 @@ int warp_hip_prefetch(warp_hip_ctx *c, int layer, const int *ids, int n)
 static int ensure_selected(warp_hip_ctx *c, int layer, const int *ids, int n)
 {
     const int E = c->cfg.n_experts;
-    c->pin_layer = layer;
-    c->n_pin = 0;
-    for (int j = 0; j < n; j++) {
+    for (int j = 0; j < n; j++)
         if (ids[j] < 0 || ids[j] >= E) return set_err(c, WARP_HIP_E_ARG, layer, ids[j], "expert id from the router");
-        c->pin[c->n_pin++] = ids[j];
-    }
+    /* this selection is held until the next one; the lookahead's guesses
+     * are now either in it or wrong */
+    c->pin_layer = layer;
+    c->hold = new_hold(c);
+    c->spec_hold = 0;
+    for (int j = 0; j < n; j++) c->pin_gen[layer * E + ids[j]] = c->hold;
     for (int j = 0; j < n; j++) {
         const int e = ids[j];
         const int s = c->key_slot[layer * E + e];
@@ -1013,10 +1115,23 @@ static int ensure_selected(warp_hip_ctx *c, int layer, const int *ids, int n)
             continue;
         }
         c->stats.misses++;
-        int rc = fill_from_fetch(c, layer, e, NULL);
-        if (rc) return rc;
+        int rc = fill_from_fetch(c, layer, e);
+        if (rc) {
+            (void)flush_table(c);      /* what was placed before the failure */
+            return rc;
+        }
     }
-    return 0;
+    return flush_table(c);
+}
+
+/* A layer that selects without the host (all resident, or nothing to
+ * fetch with) ends its own earlier hold. */
+static void release_hold(warp_hip_ctx *c, int layer)
+{
+    if (c->pin_layer == layer) {
+        c->pin_layer = -1;
+        c->hold = 0;
+    }
 }
 
 static int wait_copies(warp_hip_ctx *c)
@@ -1144,7 +1259,10 @@ static int shared_ffn(warp_hip_ctx *c, const layer_t *L, const float *x, int T)
  * router runs on its own stream from the start of the layer; the fills are
  * issued after this layer's expert kernels are queued and may not evict
  * this layer's experts. */
-static int lookahead_launch(warp_hip_ctx *c, int layer, const float *x_dev)
+/* The next layer's router on this layer's input, each of T tokens' top n
+ * by sigmoid + bias (predict_next_moe, src/model.c:2680-2711), on the
+ * lookahead stream while this layer computes. */
+static int lookahead_launch(warp_hip_ctx *c, int layer, const float *x_dev, int T)
 {
     const warp_hip_cfg *g = &c->cfg;
     if (!g->lookahead || !can_fetch(c) || layer + 1 >= g->n_layers) return 0;
@@ -1154,22 +1272,44 @@ static int lookahead_launch(warp_hip_ctx *c, int layer, const float *x_dev)
     const int n = g->lookahead < g->n_experts ? (g->lookahead < WARP_MAX_K ? g->lookahead : WARP_MAX_K) : g->n_experts;
     DEV(c, hipEventRecord(c->ev_x, c->st));
     DEV(c, hipStreamWaitEvent(c->la, c->ev_x, 0));
-    KRN(c, logits_of(c, N, x_dev, 1, c->la_logits, c->la));
-    KRN(c, wk_route(c->la_logits, N->bias, g->n_experts, n, 1, WARP_HIP_ROUTE_SIGMOID, 0, 1.0f, c->la_idx, c->la_w,
+    KRN(c, logits_of(c, N, x_dev, T, c->la_logits, c->la));
+    KRN(c, wk_route(c->la_logits, N->bias, g->n_experts, n, T, WARP_HIP_ROUTE_SIGMOID, 0, 1.0f, c->la_idx, c->la_w,
                     NULL, NULL, NULL, NULL, 0, c->la));
-    DEV(c, hipMemcpyAsync(c->h_la_idx, c->la_idx, (size_t)n * sizeof(int), hipMemcpyDeviceToHost, c->la));
+    DEV(c, hipMemcpyAsync(c->h_la_idx, c->la_idx, (size_t)T * n * sizeof(int), hipMemcpyDeviceToHost, c->la));
     DEV(c, hipEventRecord(c->ev_la, c->la));
+    c->la_T = T;
     return n;
 }
 
-/* When this layer's selection is pinned (it went through the host), the
- * fills need only wait for the work queued before this layer's expert
- * kernels, and so overlap them; otherwise they wait for the whole layer. */
+/* The guesses are fetched once this layer's own work is queued (as
+ * src/model.c:2922-2931 issues them last) and held until the next layer
+ * selects. One token's go in rank order; a batch's are each expert once,
+ * the most-predicted first, ties by id. When this layer's selection is held
+ * (it went through the host), the fills need only wait for the work queued
+ * before this layer's expert kernels, and so overlap them; otherwise they
+ * wait for the whole layer. */
 static int lookahead_issue(warp_hip_ctx *c, int layer, int n)
 {
     if (n <= 0) return 0;
     DEV(c, hipEventSynchronize(c->ev_la));
-    return prefetch_after(c, layer + 1, c->h_la_idx, n, c->pin_layer == layer ? c->ev_before : c->ev_after);
+    const int E = c->cfg.n_experts, T = c->la_T;
+    const int *ids = c->h_la_idx;
+    int m = n;
+    if (T > 1) {
+        int top = 0;
+        memset(c->la_votes, 0, (size_t)E * sizeof(int));
+        for (int q = 0; q < T * n; q++) {
+            const int e = c->h_la_idx[q];
+            if (e >= 0 && e < E && ++c->la_votes[e] > top) top = c->la_votes[e];
+        }
+        m = 0;
+        for (int v = top; v >= 1; v--)
+            for (int e = 0; e < E; e++)
+                if (c->la_votes[e] == v) c->la_order[m++] = e;
+        ids = c->la_order;
+    }
+    c->spec_hold = new_hold(c);
+    return prefetch_after(c, layer + 1, ids, m, c->pin_layer == layer ? c->ev_before : c->ev_after, 1);
 }
 
 int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *out_dev, const float *resid_dev,
@@ -1198,7 +1338,7 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
     if ((rc = timing_begin(c, 2))) return rc;
     KRN(c, logits_of(c, L, x_dev, 1, c->logits, c->st));
     if ((rc = timing_end(c))) return rc;
-    const int n_la = lookahead_launch(c, layer, x_dev);
+    const int n_la = lookahead_launch(c, layer, x_dev, 1);
     if (n_la < 0) return n_la;
     /* where the device routes with the expert table, the table kernel's
      * gate/up launch does the routing itself (one launch less) */
@@ -1211,7 +1351,7 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
             KRN(c, wk_route(c->logits, L->bias, E, K, 1, g->router_act, g->renorm, g->routed_scale, c->idx, c->w,
                             table, c->jobs, c->njobs, c->missing, I, c->st));
         c->stats.hits += (uint64_t)K;
-        if (c->pin_layer == layer) c->pin_layer = -1;
+        release_hold(c, layer);
     } else if (!can_fetch(c)) {
         /* nothing to fetch with: the device flags a selected expert that is
          * not resident (sticky), the combine poisons this layer's output with
@@ -1221,7 +1361,7 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
             KRN(c, wk_route(c->logits, L->bias, E, K, 1, g->router_act, g->renorm, g->routed_scale, c->idx, c->w,
                             table, c->jobs, c->njobs, c->missing, I, c->st));
         c->missing_pending = 1;
-        if (c->pin_layer == layer) c->pin_layer = -1;
+        release_hold(c, layer);
     } else {
         KRN(c, wk_route(c->logits, L->bias, E, K, 1, g->router_act, g->renorm, g->routed_scale, c->idx, c->w, NULL,
                         NULL, NULL, NULL, 0, c->st));
@@ -1304,7 +1444,8 @@ int warp_hip_moe_decode_host(warp_hip_ctx *c, int layer, const float *x, float *
     return take_missing(c);
 }
 
-int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *out_dev, int T, int *route, float *rw)
+int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *out_dev, const float *resid_dev, int T,
+                       int *route, float *rw)
 {
     int rc = check_layer(c, layer);
     if (rc) return rc;
@@ -1320,6 +1461,8 @@ int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *ou
     KRN(c, logits_of(c, L, X_dev, T, c->logits, c->st));
     KRN(c, wk_route(c->logits, L->bias, E, K, T, g->router_act, g->renorm, g->routed_scale, c->idx, c->w, NULL, NULL,
                     NULL, NULL, 0, c->st));
+    const int n_la = lookahead_launch(c, layer, X_dev, T);
+    if (n_la < 0) return n_la;
     if (L->resident != E && can_fetch(c)) {
         DEV(c, hipMemcpyAsync(c->h_idx, c->idx, (size_t)P * sizeof(int), hipMemcpyDeviceToHost, c->st));
         DEV(c, hipStreamSynchronize(c->st));
@@ -1336,6 +1479,8 @@ int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *ou
         free(ids);
         free(used);
         if (rc) return rc;
+    } else {
+        release_hold(c, layer);
     }
     KRN(c, wait_copies(c));
     DEV(c, hipMemsetAsync(c->missing, 0, sizeof(int), c->st));
@@ -1365,8 +1510,10 @@ int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *ou
                             WARP_TPJ, c->st));
     }
     if (L->sq[0] && (rc = shared_ffn(c, L, X_dev, T))) return rc;
-    KRN(c, wk_combine_chunk(c->yd, c->tok_slots, c->pair_w, T, K, H, L->sq[0] ? c->sho : NULL, out_dev,
+    KRN(c, wk_combine_chunk(c->yd, c->tok_slots, c->pair_w, T, K, H, L->sq[0] ? c->sho : NULL, resid_dev, out_dev,
                             c->st));
+    DEV(c, hipEventRecord(c->ev_after, c->st));
+    if ((rc = lookahead_issue(c, layer, n_la))) return rc;
     DEV(c, hipMemcpyAsync(c->h_missing, c->missing, sizeof(int), hipMemcpyDeviceToHost, c->st));
     if (route) DEV(c, hipMemcpyAsync(c->h_idx, c->idx, (size_t)P * sizeof(int), hipMemcpyDeviceToHost, c->st));
     if (rw) DEV(c, hipMemcpyAsync(c->h_w, c->w, (size_t)P * sizeof(float), hipMemcpyDeviceToHost, c->st));
@@ -1385,7 +1532,7 @@ int warp_hip_moe_chunk_host(warp_hip_ctx *c, int layer, const float *X, float *o
     if (T < 1 || T > c->cfg.max_tokens) return set_err(c, WARP_HIP_E_ARG, layer, -1, "T out of range");
     const size_t bytes = (size_t)T * c->cfg.hidden * 4;
     DEV(c, hipMemcpyAsync(c->xin, X, bytes, hipMemcpyHostToDevice, c->st));
-    int rc = warp_hip_moe_chunk(c, layer, c->xin, c->xout, T, route, rw);
+    int rc = warp_hip_moe_chunk(c, layer, c->xin, c->xout, NULL, T, route, rw);
     if (rc) return rc;
     DEV(c, hipMemcpyAsync(out, c->xout, bytes, hipMemcpyDeviceToHost, c->st));
     DEV(c, hipStreamSynchronize(c->st));

@@ -2202,10 +2202,12 @@ extern "C" int wk_plan_chunk(const int *idx, const float *w, int T, int K, int E
 }
 
 // Per token: the pairs of that token in ascending expert id, each weighted
-// and added in that order (moe_chunk's loop order, src/model.c:3601-3656).
+// and added in that order (moe_chunk's loop order, src/model.c:3601-3656),
+// then + add0 (the shared expert) + add1 (the caller's residual).
 __global__ __launch_bounds__(256) void k_combine_chunk(const float *__restrict__ y, const int *__restrict__ tok_slots,
                                                        const float *__restrict__ pair_w, int T, int K, int H,
-                                                       const float *__restrict__ add0, float *__restrict__ out) {
+                                                       const float *__restrict__ add0, const float *__restrict__ add1,
+                                                       float *__restrict__ out) {
     const int t = blockIdx.y;
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= H) return;
@@ -2219,14 +2221,15 @@ __global__ __launch_bounds__(256) void k_combine_chunk(const float *__restrict__
         s = __fadd_rn(s, __fmul_rn(wj, y[(size_t)p * H + i]));
     }
     if (add0) s = __fadd_rn(s, add0[(size_t)t * H + i]);
+    if (add1) s = __fadd_rn(s, add1[(size_t)t * H + i]);
     out[(size_t)t * H + i] = s;
 }
 
 extern "C" int wk_combine_chunk(const float *y, const int *tok_slots, const float *pair_w, int T, int K, int H,
-                                const float *add0, float *out, void *stream) {
+                                const float *add0, const float *add1, float *out, void *stream) {
     if (T <= 0 || K <= 0 || K > WARP_MAX_K || H <= 0) return -1;
     hipLaunchKernelGGL(k_combine_chunk, dim3((H + 255) / 256, T), dim3(256), 0, (hipStream_t)stream, y, tok_slots,
-                       pair_w, T, K, H, add0, out);
+                       pair_w, T, K, H, add0, add1, out);
     CHECK_LAUNCH();
     return 0;
 }
@@ -2255,19 +2258,15 @@ extern "C" int wk_fill_random(uint8_t *p, size_t n, uint64_t seed, void *stream)
     return 0;
 }
 
-__global__ void k_set_slot(warp_slot *dst, const uint8_t *rec, uint32_t o0, uint32_t o1, uint32_t o2, uint32_t o3) {
-    warp_slot v;
-    v.rec = rec;
-    v.off[0] = o0;
-    v.off[1] = o1;
-    v.off[2] = o2;
-    v.off[3] = o3;
-    *dst = v;
+__global__ __launch_bounds__(256) void k_set_slots(warp_slot *__restrict__ table, const warp_slot_upd *__restrict__ u,
+                                                   int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) table[u[i].key] = u[i].v;
 }
 
-extern "C" int wk_set_slot(warp_slot *dst, const uint8_t *rec, const uint32_t off[4], void *stream) {
-    hipLaunchKernelGGL(k_set_slot, dim3(1), dim3(1), 0, (hipStream_t)stream, dst, rec, off[0], off[1], off[2],
-                       off[3]);
+extern "C" int wk_set_slots(warp_slot *table, const warp_slot_upd *u, int n, void *stream) {
+    if (n <= 0) return 0;
+    hipLaunchKernelGGL(k_set_slots, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, table, u, n);
     CHECK_LAUNCH();
     return 0;
 }

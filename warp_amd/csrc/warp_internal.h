@@ -201,7 +201,7 @@ int wk_plan_chunk(const int *idx, const float *w, int T, int K, int E,
 /* out [T][H] = per token, sum over its pairs in ascending expert id (tok_slots)
  * of w * y[pair], then + add0 [T][H] when given. */
 int wk_combine_chunk(const float *y, const int *tok_slots, const float *pair_w, int T, int K, int H,
-                     const float *add0, float *out, void *stream);
+                     const float *add0, const float *add1, float *out, void *stream);
 
 /* Synthetic device data for benchmarks: fill n bytes with a counter-based
  * hash of (seed, offset). */
@@ -209,7 +209,13 @@ int wk_fill_random(uint8_t *p, size_t n, uint64_t seed, void *stream);
 
 /* *dst = {rec, off}, ordered on `stream` (expert table updates); rec NULL
  * marks the expert not resident. */
-int wk_set_slot(warp_slot *dst, const uint8_t *rec, const uint32_t off[4], void *stream);
+/* A batch of expert-table updates, each key at most once: table[key] = v. */
+typedef struct {
+    warp_slot v;
+    int key;
+    int pad;
+} warp_slot_upd;
+int wk_set_slots(warp_slot *table, const warp_slot_upd *u, int n, void *stream);
 
 /* Device properties the host needs: returns the gfx name into buf. */
 int wk_device_arch(int device, char *buf, int n);

@@ -76,8 +76,8 @@ SIGNATURES = {
     "warp_hip_moe_decode": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                       C.c_void_p]),
     "warp_hip_moe_decode_host": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]),
-    "warp_hip_moe_chunk": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p,
-                                     C.c_void_p]),
+    "warp_hip_moe_chunk": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int,
+                                     C.c_void_p, C.c_void_p]),
     "warp_hip_moe_chunk_host": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p,
                                           C.c_void_p]),
     "warp_hip_vq_matvec": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]),
@@ -260,13 +260,13 @@ class Context:
                                                    routed.ctypes.data))
         return out, routed
 
-    def moe_chunk(self, layer, X_dev, out_dev, T, want_route=False):
+    def moe_chunk(self, layer, X_dev, out_dev, T, want_route=False, resid_dev=None):
         import numpy as np
         K = self.cfg.top_k
         route = np.empty((T, K), np.int32) if want_route else None
         rw = np.empty((T, K), np.float32) if want_route else None
-        self._check(lib().warp_hip_moe_chunk(self.h, layer, _addr(X_dev), _addr(out_dev), T, _addr(route),
-                                             _addr(rw)))
+        self._check(lib().warp_hip_moe_chunk(self.h, layer, _addr(X_dev), _addr(out_dev), _addr(resid_dev), T,
+                                             _addr(route), _addr(rw)))
         return (route, rw) if want_route else None
 
     def moe_chunk_host(self, layer, X):
