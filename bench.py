@@ -551,7 +551,7 @@ def main():
                     help="tokens per step: kimi-prefill (default 512), k3-miss (default 32)")
     ap.add_argument("--cache-frac", type=float, default=0.69,
                     help="k3-miss: HBM cache slots as a fraction of the stack's records")
-    ap.add_argument("--lookahead", type=int, default=8,
+    ap.add_argument("--lookahead", type=int, default=4,
                     help="k3-miss: experts of layer L+1 predicted per token from layer L's input")
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
