@@ -25,6 +25,8 @@ Other workloads (--workload), each printing its own JSON line:
   kimi-prefill  512 tokens through a Kimi-Linear-shape MoE layer stack
                 (hidden 2304, 256 experts of intermediate 1024, top-8
                 softmax, Zipf(1.1)-skewed expert loads, 8-bit shared expert)
+  kimi-decode   one decode token through 26 Kimi-Linear-shape layers (all
+                256 expert records of each resident, Q8G shared expert)
   k3-miss       32 decode tokens (one per sequence) through 4 K3 layers,
                 an HBM cache of 0.69 of the stack's records, misses copied
                 from pinned host memory on the copy stream; passes without
@@ -253,7 +255,6 @@ def zipf_bias(router, X, s=1.1, seed=5, iters=80):
 
 def run_prefill(args):
     import warp_amd
-    import container as ct
     from warp_amd.hip import ROUTE_SOFTMAX
     from warp_amd.device import Buf, Event
     T, layers = args.tokens, args.layers
@@ -263,22 +264,7 @@ def run_prefill(args):
                            rec_bytes=rec_bytes, cache_bytes=layers * KE * rec_bytes)
     rng = np.random.Generator(np.random.PCG64(4321))
     X = rng.standard_normal((T, KH), dtype=np.float32)
-    shared_bytes = 0
-    t0 = time.time()
-    for L in range(layers):
-        books = rng.normal(0.0, 0.02, size=(3 * S, EN, 8)).astype(np.float16).view(np.uint16)
-        ctx.set_codebooks(L, L * 3 * S, books)
-        router = rng.standard_normal((KE, KH), dtype=np.float32) * np.float32(0.02)
-        ctx.set_router(L, router, zipf_bias(router, X, seed=5 + L))
-        for e in range(KE):
-            sc = rng.uniform(0.01, 0.05, size=2 * KI + KH).astype(np.float16).view(np.uint16)
-            ctx.put_expert_synth(L, e, int(rng.integers(1 << 62)), sc)
-        sh = [ct.quant_rows(rng, M, N, 8, 32, (1e-4, 3e-4)) for M, N in ((KIS, KH), (KIS, KH), (KH, KIS))]
-        ctx.set_shared(L, 8, 32, KIS, [np.ascontiguousarray(q[0]) for q in sh],
-                       [np.ascontiguousarray(q[1]) for q in sh], [q[2] for q in sh])
-        shared_bytes = sum(q[0].nbytes + q[1].nbytes for q in sh)
-    ctx.sync()
-    log(f"bench: {layers} Kimi-Linear layers set up ({time.time() - t0:.1f}s)")
+    shared_bytes = kimi_layers(ctx, layers, rng, lambda L, router: zipf_bias(router, X, seed=5 + L))
     Xd = Buf.of(X)
     outs = [Buf.empty((T, KH)) for _ in range(layers)]
     # the routing of the timed input: distinct experts and pairs per layer
@@ -342,6 +328,147 @@ def run_prefill(args):
         "wall_s": round(wall, 3),
         "cpu_baseline": None if args.no_cpu else cpu_baseline_prefill(args.cpu_seconds, T),
     }
+
+
+def kimi_layers(ctx, layers, rng, bias_of):
+    """Codebooks, router (+ bias_of(L, router)), all 256 expert records and
+    the Q8G g32 shared expert of each Kimi-Linear-shape layer; returns the
+    shared expert's bytes per layer."""
+    import container as ct
+    shared_bytes = 0
+    t0 = time.time()
+    for L in range(layers):
+        books = rng.normal(0.0, 0.02, size=(3 * S, EN, 8)).astype(np.float16).view(np.uint16)
+        ctx.set_codebooks(L, L * 3 * S, books)
+        router = rng.standard_normal((KE, KH), dtype=np.float32) * np.float32(0.02)
+        ctx.set_router(L, router, bias_of(L, router))
+        for e in range(KE):
+            sc = rng.uniform(0.01, 0.05, size=2 * KI + KH).astype(np.float16).view(np.uint16)
+            ctx.put_expert_synth(L, e, int(rng.integers(1 << 62)), sc)
+        sh = [ct.quant_rows(rng, M, N, 8, 32, (1e-4, 3e-4)) for M, N in ((KIS, KH), (KIS, KH), (KH, KIS))]
+        ctx.set_shared(L, 8, 32, KIS, [np.ascontiguousarray(q[0]) for q in sh],
+                       [np.ascontiguousarray(q[1]) for q in sh], [q[2] for q in sh])
+        shared_bytes = sum(q[0].nbytes + q[1].nbytes for q in sh)
+        if L % 8 == 7:
+            log(f"bench: {L + 1}/{layers} Kimi-Linear layers set up ({time.time() - t0:.1f}s)")
+    ctx.sync()
+    return shared_bytes
+
+
+def run_kimi_decode(args):
+    """One step = one decode token through a stack of Kimi-Linear-shape MoE
+    layers (every expert record resident), h <- h + moe(h)."""
+    import warp_amd
+    from warp_amd.hip import ROUTE_SOFTMAX
+    from warp_amd.device import Buf, Event
+    layers = args.layers
+    gate, down, scales_b, rec_bytes = kimi_rec_layout()
+    ctx = warp_amd.Context(hidden=KH, inter=KI, n_experts=KE, top_k=KK, n_layers=layers, fmt="VQ12",
+                           renorm=True, routed_scale=1.0, router_act=ROUTE_SOFTMAX, max_tokens=1,
+                           rec_bytes=rec_bytes, cache_bytes=layers * KE * rec_bytes)
+    rng = np.random.Generator(np.random.PCG64(8642))
+    shared_bytes = kimi_layers(ctx, layers, rng, lambda L, router: None)
+    ctx.set_matvec_path(args.matvec_path)
+    n_in = max(args.steps, args.warmup, 1)
+    X = Buf.of(rng.standard_normal((n_in, KH), dtype=np.float32))
+    bufs = [Buf.empty(KH), Buf.empty(KH)]
+
+    def step(s):
+        x = X.ptr + (s % n_in) * KH * 4
+        for L in range(layers):
+            out = bufs[L & 1]
+            ctx.moe_decode(L, x, out, resid_dev=x)
+            x = out.ptr
+
+    for s in range(args.warmup):
+        step(s)
+    ctx.sync()
+    e0, e1 = Event(), Event()
+    log(f"bench: timing {args.steps} decode steps of {layers} Kimi-Linear layers")
+    t0 = time.perf_counter()
+    e0.record(ctx.stream)
+    for s in range(args.steps):
+        step(s)
+    e1.record(ctx.stream)
+    e1.synchronize()
+    ctx.sync()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_ms(e1)
+    ctx.set_timing(True)
+    for s in range(args.steps):
+        step(s)
+    ctx.sync()
+    kms, kn = ctx.get_timing()
+    ctx.set_timing(False)
+    assert np.isfinite(bufs[(layers - 1) & 1].numpy()).all(), "non-finite hidden state after the stack"
+    ctx.close()
+    n_lt = args.steps * layers
+    b0 = KK * (2 * gate + 2 * 2 * KI)
+    b1 = KK * (down + 2 * KH)
+    kern_ms = kms[0] + kms[1]
+    achieved = (kn[0] * b0 + kn[1] * b1) / (kern_ms / 1e3) / 1e9
+    per_layer = (KK * (2 * gate + down + scales_b) + shared_bytes + KE * KH * 4 + 3 * S * EN * 8 * 2 + KE * 4
+                 + 2 * KH * 4)
+    layer_gbs = per_layer * n_lt / (ms / 1e3) / 1e9
+    kernel = "k_vq_lut" if args.matvec_path == "auto" else "k_vq_mfma"
+    return {
+        "metric": "MoE-layer decode tokens/s, Kimi-Linear shape, 1 MI355X",
+        "value": round(n_lt / (ms / 1e3), 2),
+        "unit": "MoE-layer tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms / args.steps, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
+        "data": "synthetic (random codes, codebooks, scales, shared expert and routers of the Kimi-Linear shapes)",
+        "config": {"workload": f"Kimi-Linear-shape MoE layer, decode batch 1, {layers}-layer stack",
+                   "hidden": KH, "inter": KI, "experts": KE, "top_k": KK, "routing": "softmax",
+                   "shared_expert": "Q8G group 32, intermediate 1024", "layers": layers,
+                   "format": "RVQ 2x4096 12-bit codes (3.00 b/w)", "parallelism": "single GPU"},
+        "layer_bytes": int(per_layer),
+        "layer_hbm_gbs": round(layer_gbs, 1),
+        "layer_hbm_frac": round(layer_gbs / HBM_PEAK_GBS, 4),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": kernel + " (expert matvec, gate/up and down launches)",
+                     "bytes_per_launch": {"gate_up": b0, "down": b1},
+                     "avg_launch_us": {"gate_up": round(kms[0] / max(kn[0], 1) * 1e3, 2),
+                                       "down": round(kms[1] / max(kn[1], 1) * 1e3, 2)},
+                     "router_avg_us": round(kms[2] / max(kn[2], 1) * 1e3, 2)},
+        "wall_s": round(wall, 3),
+        "cpu_baseline": None if args.no_cpu else cpu_baseline_kimi_decode(args.cpu_seconds),
+    }
+
+
+def cpu_baseline_kimi_decode(seconds):
+    """The reference's moe_layer on the VQ3R twin of one Kimi-Linear layer."""
+    from oracle import pyoracle as po
+    import container as ct
+    if not os.path.exists(po.REF_LIB):
+        return None
+    spec = ct.Spec(hidden=KH, inter=KI, experts=KE, top_k=KK, layers=1, fmt="VQ3R", renorm=True,
+                   routed_scale=1.0, shared_bits=8, shared_group=32, subnormals=False, keep_codes=False, seed=97)
+    log("bench: writing the VQ3R twin container for the decode CPU baseline")
+    model = ct.build(spec)
+    tmp = tempfile.mkdtemp(prefix="warp_kimi_twin_")
+    ct.write(model, tmp)
+    del model
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+    ref = po.Ref(tmp, cache_bytes=KE * 2_700_000 + (64 << 20), n_threads=threads)
+    threads = ref.threads()
+    rng = np.random.default_rng(3)
+    for _ in range(64):                                # fills the reference's cache
+        ref.moe_layer(0, rng.standard_normal(KH, dtype=np.float32), KE, KK, KH)
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        ref.moe_layer(0, rng.standard_normal(KH, dtype=np.float32), KE, KK, KH)
+        n += 1
+    dt = time.perf_counter() - t0
+    ref.close()
+    shutil.rmtree(tmp, ignore_errors=True)
+    return {"value": n / dt, "unit": "MoE-layer tokens/s", "cores": threads, "kind": "reference",
+            "sample": f"{n} decode tokens through one Kimi-Linear-shape layer (H {KH}, I {KI}, top-8 of 256 "
+                      f"experts, Q8G shared expert) in the reference's VQ3R format (3x256, 3.00 bits/weight), its "
+                      f"own moe_layer over {threads} threads, {dt:.1f}s, records cache-resident; the reference "
+                      f"routes with sigmoid scores (softmax is not in it)"}
 
 
 def cpu_baseline_prefill(seconds, T):
@@ -544,9 +671,11 @@ def run_miss(args):
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--workload", choices=["k3-decode", "kimi-prefill", "k3-miss"], default="k3-decode",
+    ap.add_argument("--workload", choices=["k3-decode", "kimi-prefill", "k3-miss", "kimi-decode"],
+                    default="k3-decode",
                     help="k3-decode (the headline line), kimi-prefill (a 512-token Kimi-Linear-shape prefill) "
-                         "or k3-miss (a 32-token K3 decode batch with half its expert records streamed from host)")
+                         ", k3-miss (a 32-token K3 decode batch with half its expert records streamed from host) "
+                         "or kimi-decode (Kimi-Linear-shape decode, batch 1, with its shared expert)")
     ap.add_argument("--tokens", type=int, default=None,
                     help="tokens per step: kimi-prefill (default 512), k3-miss (default 32)")
     ap.add_argument("--cache-frac", type=float, default=0.69,
@@ -556,7 +685,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--layers", type=int, default=None,
-                    help="layers in the stack: k3-decode 60, kimi-prefill 4, k3-miss 4")
+                    help="layers in the stack: k3-decode 60, kimi-prefill 4, k3-miss 4, kimi-decode 26")
     ap.add_argument("--resident", type=int, default=64, help="expert records per layer kept in HBM")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -575,6 +704,10 @@ def main():
         args.layers = args.layers or 4
         args.tokens = args.tokens or 512
         print(json.dumps(run_prefill(args)))
+        return
+    if args.workload == "kimi-decode":
+        args.layers = args.layers or 26
+        print(json.dumps(run_kimi_decode(args)))
         return
     if args.workload == "k3-miss":
         args.layers = args.layers or 4

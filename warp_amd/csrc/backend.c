@@ -1230,6 +1230,28 @@ static int logits_of(warp_hip_ctx *c, const layer_t *L, const float *x, int T, f
     return -1;
 }
 
+/* The layer's shared expert as the fused decode kernels take it: an fp32
+ * router with the fast (tree) sum, the hidden state in shh. */
+static int shared_args(const warp_hip_ctx *c, const layer_t *L, warp_shared_args *sa)
+{
+    const warp_hip_cfg *g = &c->cfg;
+    memset(sa, 0, sizeof *sa);
+    if (!L->sq[0] || !L->router || g->router_strict || !c->shh) return 0;
+    for (int k = 0; k < 3; k++) {
+        sa->q[k] = L->sq[k];
+        sa->s[k] = L->ss[k];
+        sa->rowbytes[k] = L->s_rowbytes[k];
+    }
+    sa->bits = L->s_bits;
+    sa->group = L->s_group;
+    sa->inter = L->s_inter;
+    sa->situ = g->act_situ;
+    sa->beta = g->situ_beta;
+    sa->lbeta = g->situ_linear_beta;
+    sa->h = c->shh;
+    return 1;
+}
+
 static int shared_ffn(warp_hip_ctx *c, const layer_t *L, const float *x, int T)
 {
     const warp_hip_cfg *g = &c->cfg;
@@ -1254,11 +1276,6 @@ static int shared_ffn(warp_hip_ctx *c, const layer_t *L, const float *x, int T)
     return 0;
 }
 
-/* Lookahead (src/model.c:2680-2711, 2923-2931): layer L+1's router on layer
- * L's input, top-n by biased sigmoid score, issued as speculative fills. The
- * router runs on its own stream from the start of the layer; the fills are
- * issued after this layer's expert kernels are queued and may not evict
- * this layer's experts. */
 /* The next layer's router on this layer's input, each of T tokens' top n
  * by sigmoid + bias (predict_next_moe, src/model.c:2680-2711), on the
  * lookahead stream while this layer computes. */
@@ -1335,8 +1352,13 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
     } else {
         KRN(c, wk_split(x_dev, 1, H, c->xs, c->xscale, c->st));
     }
+    /* with the table kernel, a Q8G/Q4G shared expert runs inside the router
+     * launch (gate, up, act) and the combine (down) */
+    warp_shared_args sa;
+    const int fuse_shared = use_lut && shared_args(c, L, &sa) && wk_shared_fast_ok(H, &sa);
     if ((rc = timing_begin(c, 2))) return rc;
-    KRN(c, logits_of(c, L, x_dev, 1, c->logits, c->st));
+    if (fuse_shared) KRN(c, wk_router_shared(L->router, x_dev, E, H, c->logits, &sa, c->st));
+    else KRN(c, logits_of(c, L, x_dev, 1, c->logits, c->st));
     if ((rc = timing_end(c))) return rc;
     const int n_la = lookahead_launch(c, layer, x_dev, 1);
     if (n_la < 0) return n_la;
@@ -1412,10 +1434,11 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
         KRN(c, wk_vq_matvec(g->fmt, c->jobs, c->njobs, K, 2, 1, L->books, c->xsh, c->xscaleh, yk, H, I, 1, c->st));
         if ((rc = timing_end(c))) return rc;
     }
-    if (L->sq[0] && (rc = shared_ffn(c, L, x_dev, 1))) return rc;
+    if (L->sq[0] && !fuse_shared && (rc = shared_ffn(c, L, x_dev, 1))) return rc;
     if (use_lut)
         KRN(c, wk_combine_lut(c->jobs + 2 * (size_t)K, c->part + d_off, sp_d, K, c->w, K, H,
-                              L->sq[0] ? c->sho : NULL, resid_dev, c->missing, out_dev, c->st));
+                              L->sq[0] && !fuse_shared ? c->sho : NULL, resid_dev, c->missing,
+                              fuse_shared ? &sa : NULL, out_dev, c->st));
     else
         KRN(c, wk_combine(c->yd, c->w, K, H, L->sq[0] ? c->sho : NULL, resid_dev, c->missing, out_dev, c->st));
     DEV(c, hipEventRecord(c->ev_after, c->st));

@@ -267,6 +267,104 @@ extern "C" int wk_mvq(const int8_t *W, const uint16_t *ws, size_t rowbytes, int 
     return 0;
 }
 
+// ---- decode: the shared expert inside the router and combine launches ---------------------
+
+// One wave's dot of a quantised row (Q8G: 16 weights per 16-byte chunk, Q4G:
+// 32) with x in LDS. Lane l takes chunks l, l + 64, ...: load() issues every
+// chunk and its group scale (clamped to the row, so no load is
+// conditional), dot() multiplies each chunk, scales its sum by the group's
+// fp16 scale and sums the lanes. The group is a multiple of a chunk's
+// weights, so a chunk never straddles two groups.
+template <int BITS, int MAXC>
+struct QRow {
+    static constexpr int WPC = BITS == 8 ? 16 : 32;
+    uint4 w[MAXC];
+    uint16_t s[MAXC];
+    __device__ __forceinline__ void load(const int8_t *row, const uint16_t *sc, int g, int nc) {
+        const int lane = threadIdx.x & 63;
+#pragma unroll
+        for (int k = 0; k < MAXC; k++) {
+            const int c = min(lane + 64 * k, nc - 1);
+            w[k] = *(const uint4 *)(row + (size_t)c * 16);
+            s[k] = sc[c * WPC / g];
+        }
+    }
+    __device__ __forceinline__ float dot(const float *xl, int nc) const {
+        const int lane = threadIdx.x & 63;
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < MAXC; k++) {
+            if (lane + 64 * k < nc) {
+                const float *xv = xl + (lane + 64 * k) * WPC;
+                const unsigned u[4] = { w[k].x, w[k].y, w[k].z, w[k].w };
+                float p = 0.0f;
+                if constexpr (BITS == 8) {
+#pragma unroll
+                    for (int i = 0; i < 16; i++)
+                        p = __builtin_fmaf((float)(int)(int8_t)(u[i >> 2] >> (8 * (i & 3))), xv[i], p);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 32; i++)
+                        p = __builtin_fmaf((float)((int)((u[i >> 3] >> (4 * (i & 7))) & 0xF) - 8), xv[i], p);
+                }
+                acc = __builtin_fmaf(f16_keep(s[k]), p, acc);
+            }
+        }
+        return wave_sum(acc);
+    }
+};
+
+constexpr int SH_MAXC = 8;       // chunks per lane: rows up to 8192 (Q8G) or 16384 (Q4G) weights
+
+extern "C" int wk_shared_fast_ok(int H, const warp_shared_args *sa) {
+    if (!sa || (sa->bits != 8 && sa->bits != 4) || H <= 0 || sa->inter <= 0 || (H & 3) || (sa->inter & 3))
+        return 0;
+    const int wpc = sa->bits == 8 ? 16 : 32;
+    if (sa->group <= 0 || sa->group % wpc || H % sa->group || sa->inter % sa->group) return 0;
+    if (H / wpc > 64 * SH_MAXC || sa->inter / wpc > 64 * SH_MAXC) return 0;
+    for (int k = 0; k < 3; k++)
+        if (!sa->q[k] || !sa->s[k] || (sa->rowbytes[k] & 15) || ((uintptr_t)sa->q[k] & 15)) return 0;
+    return 1;
+}
+
+// Blocks [0, E): one router row each, as k_router_fast. Blocks past E: four
+// rows of the shared expert's gate and up each (one wave per row), every
+// weight load issued before x is staged in LDS, then h = act(gate, up).
+template <int BITS>
+__global__ __launch_bounds__(256) void k_router_shared(const float *__restrict__ W, const float *__restrict__ x, int E,
+                                                       int H, float *__restrict__ logits, warp_shared_args sa) {
+    if ((int)blockIdx.x < E) {
+        const float v = router_row_fast(W, x, E, H, blockIdx.x);
+        if (threadIdx.x == 0) logits[blockIdx.x] = v;
+        return;
+    }
+    extern __shared__ float xl[];
+    using Q = QRow<BITS, SH_MAXC>;
+    const int r = ((int)blockIdx.x - E) * 4 + (int)(threadIdx.x >> 6), rr = min(r, sa.inter - 1);
+    const int nc = H / Q::WPC, ng = H / sa.group;
+    Q qg, qu;
+    qg.load(sa.q[0] + (size_t)rr * sa.rowbytes[0], sa.s[0] + (size_t)rr * ng, sa.group, nc);
+    qu.load(sa.q[1] + (size_t)rr * sa.rowbytes[1], sa.s[1] + (size_t)rr * ng, sa.group, nc);
+    for (int i = threadIdx.x; i < H / 4; i += 256) ((float4 *)xl)[i] = ((const float4 *)x)[i];
+    __syncthreads();
+    const float gv = qg.dot(xl, nc), uv = qu.dot(xl, nc);
+    if (r < sa.inter && (threadIdx.x & 63) == 0) sa.h[r] = act_pair(gv, uv, sa.situ, sa.beta, sa.lbeta);
+}
+
+extern "C" int wk_router_shared(const float *W, const float *x, int E, int H, float *logits, const warp_shared_args *sa,
+                                void *stream) {
+    if (E <= 0 || !wk_shared_fast_ok(H, sa)) return -1;
+    const dim3 grid(E + (sa->inter + 3) / 4);
+    const size_t lds = (size_t)H * sizeof(float);
+    if (lds > 64 * 1024) return -1;
+    if (sa->bits == 8)
+        hipLaunchKernelGGL(k_router_shared<8>, grid, dim3(256), lds, (hipStream_t)stream, W, x, E, H, logits, *sa);
+    else
+        hipLaunchKernelGGL(k_router_shared<4>, grid, dim3(256), lds, (hipStream_t)stream, W, x, E, H, logits, *sa);
+    CHECK_LAUNCH();
+    return 0;
+}
+
 // Batches of tokens on the matrix cores (the shared expert of a chunk):
 // y[t][o] = sum over groups g of scale[o][g] * sum_{i in g} W[o][i] x[t][i],
 // as mvq_rows_f32 (src/simd_avx512.c:20-88) per token. v_mfma_f32_16x16x32_f16
@@ -1773,14 +1871,32 @@ extern "C" int wk_lut_reduce(const warp_job *jobs, const int *njobs, int max_job
 // per expert and row), then one thread per row combines them in order. Every
 // load that does not depend on another is issued first (the partial sums,
 // the weights, the addends); only the row scale waits for its job entry.
+// SHB (8 or 4): add0 is the shared expert's down rows of this block against
+// sa.h, one wave per 4 rows, their weights loaded first.
+template <int SHB>
 __global__ __launch_bounds__(256) void k_combine_lut(const warp_job *__restrict__ jobs2, const float *__restrict__ part,
                                                      int splits, int max_jobs, const float *__restrict__ w, int K,
                                                      int H, const float *add0, const float *add1,
-                                                     const int *missing, float *__restrict__ out) {
+                                                     const int *missing, warp_shared_args sa,
+                                                     float *__restrict__ out) {
     __shared__ float yd[WARP_MAX_K][16];
     __shared__ float wl[WARP_MAX_K];
+    __shared__ float shd[16];
+    extern __shared__ float hl[];
     const int r0 = blockIdx.x * 16, row = threadIdx.x & 15, jq = threadIdx.x >> 4;
     const int i = min(r0 + row, H - 1);
+    using Q = QRow<SHB ? SHB : 8, 4>;
+    Q qd[4];
+    const int snc = SHB ? sa.inter / Q::WPC : 0;
+    if constexpr (SHB != 0) {
+        const int sng = sa.inter / sa.group;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int rr = min(r0 + (int)(threadIdx.x >> 6) * 4 + k, H - 1);
+            qd[k].load(sa.q[2] + (size_t)rr * sa.rowbytes[2], sa.s[2] + (size_t)rr * sng, sa.group, snc);
+        }
+        for (int q = threadIdx.x; q < sa.inter / 4; q += 256) ((float4 *)hl)[q] = ((const float4 *)sa.h)[q];
+    }
     const size_t nrows = (size_t)((H + 63) >> 6) * 64, stride = (size_t)max_jobs * nrows;
     // (volatile: read here, not after the barrier where it is used)
     const bool miss = missing && *(volatile const int *)missing;
@@ -1802,6 +1918,14 @@ __global__ __launch_bounds__(256) void k_combine_lut(const warp_job *__restrict_
     }
     if (threadIdx.x < K) wl[threadIdx.x] = wv;
     __syncthreads();
+    if constexpr (SHB != 0) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float v = qd[k].dot(hl, snc);
+            if ((threadIdx.x & 63) == 0) shd[(threadIdx.x >> 6) * 4 + k] = v;
+        }
+        __syncthreads();
+    }
     if (jq != 0 || r0 + row >= H) return;
     if (miss) {                         // a selected expert was not computed
         out[i] = __builtin_nanf("");
@@ -1809,17 +1933,35 @@ __global__ __launch_bounds__(256) void k_combine_lut(const warp_job *__restrict_
     }
     float s = 0.0f;
     for (int j = 0; j < K; j++) s = __fadd_rn(s, __fmul_rn(wl[j], yd[j][row]));
-    if (add0) s = __fadd_rn(s, a0);
+    if (SHB) s = __fadd_rn(s, shd[row]);
+    else if (add0) s = __fadd_rn(s, a0);
     if (add1) s = __fadd_rn(s, a1);
     out[i] = s;
 }
 
 extern "C" int wk_combine_lut(const warp_job *jobs2, const float *part, int splits, int max_jobs, const float *w,
-                              int K, int H, const float *add0, const float *add1, const int *missing, float *out,
-                              void *stream) {
+                              int K, int H, const float *add0, const float *add1, const int *missing,
+                              const warp_shared_args *sa, float *out, void *stream) {
     if (K <= 0 || K > WARP_MAX_K || H <= 0 || splits <= 0 || K > max_jobs) return -1;
-    hipLaunchKernelGGL(k_combine_lut, dim3((H + 15) / 16), dim3(256), 0, (hipStream_t)stream, jobs2, part, splits,
-                       max_jobs, w, K, H, add0, add1, missing, out);
+    const dim3 grid((H + 15) / 16);
+    if (sa) {
+        /* the shared down rows: H rows of sa->inter weights */
+        warp_shared_args d = *sa;
+        if (!wk_shared_fast_ok(H, sa) || add0 || d.inter / (d.bits == 8 ? 16 : 32) > 64 * 4 ||
+            (size_t)d.inter * sizeof(float) > 64 * 1024)
+            return -1;
+        const size_t lds = (size_t)d.inter * sizeof(float);
+        if (d.bits == 8)
+            hipLaunchKernelGGL(k_combine_lut<8>, grid, dim3(256), lds, (hipStream_t)stream, jobs2, part, splits,
+                               max_jobs, w, K, H, add0, add1, missing, d, out);
+        else
+            hipLaunchKernelGGL(k_combine_lut<4>, grid, dim3(256), lds, (hipStream_t)stream, jobs2, part, splits,
+                               max_jobs, w, K, H, add0, add1, missing, d, out);
+    } else {
+        const warp_shared_args none = {};
+        hipLaunchKernelGGL(k_combine_lut<0>, grid, dim3(256), 0, (hipStream_t)stream, jobs2, part, splits, max_jobs,
+                           w, K, H, add0, add1, missing, none, out);
+    }
     CHECK_LAUNCH();
     return 0;
 }

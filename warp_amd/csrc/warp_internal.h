@@ -91,6 +91,25 @@ int wk_router_logits(const float *W, const float *x, int E, int H, int T, int st
 int wk_mvq(const int8_t *W, const uint16_t *ws, size_t rowbytes, int group, int bits,
            const float *x, int M, int N, int T, float *y, void *stream);
 
+/* A layer's shared expert for one decode token, folded into the router and
+ * combine launches: h = act(gate . x, up . x), then down . h. */
+typedef struct {
+    const int8_t *q[3];         /* gate, up, down rows (Q8G or Q4G)    */
+    const uint16_t *s[3];       /* their fp16 group scales, [rows][N/group] */
+    size_t rowbytes[3];
+    int bits, group, inter;
+    int situ;
+    float beta, lbeta;
+    float *h;                   /* [inter]                             */
+} warp_shared_args;
+/* Whether the fused kernels take this shape: bits 8 or 4, 16-byte rows,
+ * a group a multiple of one 16-byte chunk's weights, rows short enough. */
+int wk_shared_fast_ok(int H, const warp_shared_args *sa);
+/* Router logits [E] of one token (the fast fixed-order tree) and, in the
+ * same launch, the shared expert's h. */
+int wk_router_shared(const float *W, const float *x, int E, int H, float *logits, const warp_shared_args *sa,
+                     void *stream);
+
 /* Routing for T tokens: scores, top-k by score + bias (strict >, lowest
  * index wins), weights, renorm, scale. When `table` is not NULL (decode,
  * T == 1) it also writes the decode job lists: jobs[0..K) gate, [K..2K) up,
@@ -151,10 +170,11 @@ int wk_lut_route_ok(int fmt, int E, int K, int shared_x, int kind_lo, int nkinds
 int wk_lut_reduce(const warp_job *jobs, const int *njobs, int max_jobs, int kind_lo, int nkinds,
                   const float *part, int splits, int M, float *const *y, void *stream);
 /* Decode: down partials -> out [H] = sum_j w[j] * y_j in j order, + add0 + add1;
- * NaN everywhere when *missing is set. jobs2: the down job list. */
+ * NaN everywhere when *missing is set. jobs2: the down job list. With `sa`
+ * (add0 NULL), add0 is the shared expert's down . sa->h, computed here. */
 int wk_combine_lut(const warp_job *jobs2, const float *part, int splits, int max_jobs,
                    const float *w, int K, int H, const float *add0, const float *add1,
-                   const int *missing, float *out, void *stream);
+                   const int *missing, const warp_shared_args *sa, float *out, void *stream);
 
 /* Decoded weights of one matrix, bit for bit the reference's closed form
  * (stage sum in fp32 from stage 0, then times the subnormal-keeping fp16
