@@ -166,3 +166,40 @@ def test_moe_chunk(loaded):
         e = rel_err(out, ro)
         assert e <= TOL, (L, e)
         log(f"[{fmt}] moe_chunk L{L} rel err {e:.2e}")
+
+
+def test_router_batch_on_matrix_cores():
+    """Batches of 16 tokens or more take the fp32 matrix-core router. Its
+    logits are within the fp32 summation bound of a float64 product
+    (|d| <= H * 2^-24 * sum|w x|); a token's logits do not depend on its
+    place in the batch or on the batch size (bit for bit); and they select
+    the same experts as the one-token router, whose sum runs in another
+    order. Token and expert counts are not multiples of the 32 x 32 block."""
+    import warp_amd
+    spec = ct.Spec(hidden=256, inter=64, experts=40, top_k=4, layers=1, fmt="VQ3R", seed=17, **BALANCED)
+    model = ct.build(spec)
+    ctx = open_ctx(model, max_tokens=64)
+    try:
+        warp_amd.load_container_model(ctx, model)
+        rng = np.random.default_rng(19)
+        X = rng.normal(size=(45, spec.hidden)).astype(np.float32)
+        W = model.layers[0].router
+        lg = empty((45, spec.experts))
+        ctx.router_logits(0, dev(X), 45, lg)
+        got = host(lg)
+        ref = X.astype(np.float64) @ W.astype(np.float64).T
+        bound = spec.hidden * 2.0 ** -24 * (np.abs(X).astype(np.float64) @ np.abs(W).astype(np.float64).T)
+        assert np.all(np.abs(got - ref) <= bound), float(np.max(np.abs(got - ref) / bound))
+        perm = rng.permutation(45)[:17]
+        lg2 = empty((17, spec.experts))
+        ctx.router_logits(0, dev(np.ascontiguousarray(X[perm])), 17, lg2)
+        assert np.array_equal(host(lg2).view(np.uint32), got[perm].view(np.uint32)), "batch place changed a logit"
+        out = empty((45, spec.hidden))
+        route, _ = ctx.moe_chunk(0, dev(X), out, 45, want_route=True)
+        for t in range(0, 45, 4):
+            o = empty(spec.hidden)
+            idx, _ = ctx.moe_decode(0, dev(X[t]), o, want_route=True)
+            assert np.array_equal(idx, route[t]), t
+        log(f"batch router: within the fp32 bound of float64, batch-place invariant, decode picks agree")
+    finally:
+        ctx.close()

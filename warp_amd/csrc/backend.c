@@ -288,6 +288,7 @@ struct warp_hip_ctx {
     int n_cu, lut_ok, mv_path;
     int *counts, *offsets, *pair_tok, *pair_exp;
     int *tok_slots;               /* per token, its pair slots in ascending expert id */
+    int *runs;                    /* prefill: runs of one expert's jobs (first << 3 | count) */
     float *pair_w;
     float *xin, *xout;
     float *la_logits;
@@ -395,6 +396,7 @@ static int ctx_alloc(warp_hip_ctx *c)
     DMALLOC(c, c->pair_exp, P * 4);
     DMALLOC(c, c->pair_w, P * 4);
     DMALLOC(c, c->tok_slots, P * 4);
+    DMALLOC(c, c->runs, (size_t)c->max_jobs * 4);
     DMALLOC(c, c->la_logits, (size_t)T * E * 4);
     DMALLOC(c, c->la_idx, (size_t)T * WARP_MAX_K * 4);
     DMALLOC(c, c->la_w, (size_t)T * WARP_MAX_K * 4);
@@ -553,7 +555,7 @@ void warp_hip_close(warp_hip_ctx *c)
     free(c->L);
     void *d[] = { c->logits, c->idx, c->w, c->jobs, c->njobs, c->missing, c->xs, c->xscale, c->yg, c->yu,
                   c->yd, c->xsh, c->xscaleh, c->hbuf, c->shg, c->shu, c->shh, c->sho, c->lut8, c->lut8d,
-                  c->lscale, c->lscaled, c->counts, c->offsets, c->pair_tok, c->pair_exp, c->pair_w, c->tok_slots,
+                  c->lscale, c->lscaled, c->counts, c->offsets, c->pair_tok, c->pair_exp, c->pair_w, c->tok_slots, c->runs,
                   c->xin, c->xout, c->la_logits, c->la_idx, c->la_w, c->table_dev, c->pool, c->part,
                   c->shxs, c->shxscale, c->tq_dev };
     for (size_t i = 0; i < sizeof d / sizeof d[0]; i++) hfree(d[i]);
@@ -1508,7 +1510,7 @@ int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *ou
     KRN(c, wait_copies(c));
     DEV(c, hipMemsetAsync(c->missing, 0, sizeof(int), c->st));
     KRN(c, wk_plan_chunk(c->idx, c->w, T, K, E, table, c->counts, c->offsets, c->pair_tok, c->pair_exp, c->pair_w,
-                         c->tok_slots, c->jobs, c->max_jobs, c->njobs, c->missing, I, c->st));
+                         c->tok_slots, c->jobs, c->max_jobs, c->njobs, c->runs, c->missing, I, c->st));
     DEV(c, hipEventRecord(c->ev_before, c->st));
     float *yk[3] = { c->yg, c->yu, c->yd };
     if (c->P6) {
@@ -1524,13 +1526,14 @@ int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *ou
         KRN(c, wk_lut_p6(c->hbuf, P, I, books_kind(c, L, 2), c->lut8d, c->lscaled, c->st));
         KRN(c, wk_apply_p6(c->jobs, c->njobs, c->max_jobs, 2, c->lut8d, c->lscaled, c->yd, H, I, c->st));
     } else {
+        /* by runs: each expert's records decoded once per WARP_RUN_J jobs */
         KRN(c, wk_split(X_dev, T, H, c->xs, c->xscale, c->st));
-        KRN(c, wk_vq_matvec(g->fmt, c->jobs, c->njobs, c->max_jobs, 0, 2, L->books, c->xs, c->xscale, yk, I, H,
-                            WARP_TPJ, c->st));
+        KRN(c, wk_vq_runs(g->fmt, c->jobs, c->njobs, c->max_jobs, c->runs, 0, 2, L->books, c->xs, c->xscale, yk, I,
+                          H, c->st));
         KRN(c, wk_act_split(c->yg, c->yu, P, I, g->act_situ, g->situ_beta, g->situ_linear_beta, c->xsh, c->xscaleh,
                             NULL, c->st));
-        KRN(c, wk_vq_matvec(g->fmt, c->jobs, c->njobs, c->max_jobs, 2, 1, L->books, c->xsh, c->xscaleh, yk, H, I,
-                            WARP_TPJ, c->st));
+        KRN(c, wk_vq_runs(g->fmt, c->jobs, c->njobs, c->max_jobs, c->runs, 2, 1, L->books, c->xsh, c->xscaleh, yk, H,
+                          I, c->st));
     }
     if (L->sq[0] && (rc = shared_ffn(c, L, X_dev, T))) return rc;
     KRN(c, wk_combine_chunk(c->yd, c->tok_slots, c->pair_w, T, K, H, L->sq[0] ? c->sho : NULL, resid_dev, out_dev,

@@ -194,6 +194,55 @@ __global__ __launch_bounds__(256) void k_router_fast(const float *__restrict__ W
     if (threadIdx.x == 0) logits[blockIdx.x] = v;
 }
 
+// A batch of tokens on the matrix cores: logits[t][e] = X[t] . W[e] with
+// v_mfma_f32_16x16x4_f32 (fp32 products, fp32 sums). A block of 4 waves owns
+// 32 tokens x 32 experts, one 16 x 16 tile per wave, over all of H. Per 16
+// columns of H a lane loads one float4 of its token row and one of its
+// expert row (columns 4j..4j+3 of the 16, j = lane / 16) and feeds their
+// components to 4 MFMA steps: step s sums column 4j + s, the same column on
+// both sides. Each output is a fixed sequence of MFMA steps whatever the
+// token's place in the batch. Loads run 7 chunks of 16 columns ahead of
+// the multiplies. H is a multiple of 16.
+__global__ __launch_bounds__(256) void k_router_mfma(const float *__restrict__ W, const float *__restrict__ x, int E,
+                                                     int H, int T, float *__restrict__ logits) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int t0 = blockIdx.x * 32 + (wave & 1) * 16, e0 = blockIdx.y * 32 + (wave >> 1) * 16;
+    const int r = lane & 15, j = lane >> 4;
+    const float4 *xa = (const float4 *)(x + (size_t)min(t0 + r, T - 1) * H) + j;
+    const float4 *wb = (const float4 *)(W + (size_t)min(e0 + r, E - 1) * H) + j;
+    const int nc = H >> 4;
+    constexpr int RING = 8;                                 // 16-column chunks in flight: RING - 1 ahead
+    f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    float4 a[RING], b[RING];
+#pragma unroll
+    for (int u = 0; u < RING - 1; u++) {
+        const int c = min(u, nc - 1);
+        a[u] = xa[(size_t)c * 4];
+        b[u] = wb[(size_t)c * 4];
+    }
+    for (int c0 = 0; c0 < nc; c0 += RING) {
+#pragma unroll
+        for (int u = 0; u < RING; u++) {
+            const int c = c0 + u;
+            if (c < nc) {                                   // uniform
+                const int cl = min(c + RING - 1, nc - 1);
+                a[(u + RING - 1) % RING] = xa[(size_t)cl * 4];
+                b[(u + RING - 1) % RING] = wb[(size_t)cl * 4];
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].x, b[u].x, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].y, b[u].y, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].z, b[u].z, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].w, b[u].w, acc, 0, 0, 0);
+            }
+        }
+    }
+    // lane (r, j) holds rows 4j..4j+3 (tokens) of column r (expert)
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int t = t0 + 4 * j + q, e = e0 + r;
+        if (t < T && e < E) logits[(size_t)t * E + e] = acc[q];
+    }
+}
+
 // The reference's dotf on x86 (src/model.c:155-160): one sequential, unfused
 // sum per row, bit for bit.
 __global__ __launch_bounds__(64) void k_router_strict(const float *__restrict__ W, const float *__restrict__ x,
@@ -214,6 +263,9 @@ extern "C" int wk_router_logits(const float *W, const float *x, int E, int H, in
     if (strict)
         hipLaunchKernelGGL(k_router_strict, dim3((rows + 63) / 64), dim3(64), 0, (hipStream_t)stream, W, x, E, H,
                            T, logits);
+    else if (T >= WARP_ROUTER_MFMA_T && (H & 15) == 0)
+        hipLaunchKernelGGL(k_router_mfma, dim3((T + 31) / 32, (E + 31) / 32), dim3(256), 0, (hipStream_t)stream, W, x,
+                           E, H, T, logits);
     else
         hipLaunchKernelGGL(k_router_fast, dim3(rows), dim3(256), 0, (hipStream_t)stream, W, x, E, H, T, logits);
     CHECK_LAUNCH();
@@ -372,10 +424,12 @@ extern "C" int wk_router_shared(const float *W, const float *x, int E, int H, fl
 // the fp16 hi/lo halves of x for 8 tokens as B (token t's hi in column 2t, lo
 // in 2t + 1; xs from wk_split), so every product is exact and the sums are
 // fp32; a group's sums are scaled by its fp16 scale in fp32, and at the end
-// the two halves are added and the token's power of two removed. A wave
-// computes 32 rows x 16 tokens (2 x 2 tiles) and loads the next 32-column
-// slice while it multiplies the current one; a block of 4 waves covers 64
-// rows x 32 tokens. N and the group are multiples of 32.
+// the two halves are added and the token's power of two removed. A block
+// of 4 waves covers 32 rows x 32 tokens (2 x 4 tiles, 8 MFMAs per 32
+// columns), each wave over a quarter of the groups with its loads three
+// 32-column slices ahead; the quarters are added in LDS in wave order, and
+// the rows' group scales are staged in LDS once. N and the group are
+// multiples of 32.
 typedef _Float16 half8v __attribute__((ext_vector_type(8)));
 
 template <int BITS>
@@ -398,65 +452,91 @@ __global__ __launch_bounds__(256) void k_mvq_mfma(const int8_t *__restrict__ W, 
                                                   size_t rowbytes, int group, const _Float16 *__restrict__ xs,
                                                   const float *__restrict__ xscale, int M, int N, int T,
                                                   float *__restrict__ y) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char lds_mvq[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int o0 = blockIdx.x * 64 + (wave & 1) * 32, t0 = blockIdx.y * 32 + (wave >> 1) * 16;
+    const int o0 = blockIdx.x * 32, t0 = blockIdx.y * 32;
     const int m = lane & 15, kb = lane >> 4, nv = N >> 3, ng = N / group;
+    float *red = (float *)lds_mvq;                          // [4 waves][32 rows][32 tokens]
+    uint16_t *sc_lds = (uint16_t *)(red + 4 * 32 * 32);     // [32 rows][ng] group scales of the block
+    // the wave's columns: a quarter of the groups
+    const int g_lo = wave * ng / 4, g_hi = (wave + 1) * ng / 4;
+    const int k_lo = g_lo * group, k_hi = g_hi * group;
     const int8_t *wr[2];
-    const _Float16 *xr[2];
+    const _Float16 *xr[4];
 #pragma unroll
     for (int i = 0; i < 2; i++) wr[i] = W + (size_t)min(o0 + i * 16 + m, M - 1) * rowbytes;
 #pragma unroll
-    for (int j = 0; j < 2; j++) xr[j] = xs + (size_t)min(t0 + j * 8 + (m >> 1), T - 1) * nv * 16 + (m & 1) * 8;
-    auto load = [&](half8v (&a)[2], half8v (&b)[2], int k0) {
+    for (int j = 0; j < 4; j++) xr[j] = xs + (size_t)min(t0 + j * 8 + (m >> 1), T - 1) * nv * 16 + (m & 1) * 8;
+    auto load = [&](half8v (&a)[2], half8v (&b)[4], int k0) {
 #pragma unroll
         for (int i = 0; i < 2; i++) a[i] = q8_of<BITS>(wr[i], k0 + kb * 8);
 #pragma unroll
-        for (int j = 0; j < 2; j++) b[j] = *(const half8v *)(xr[j] + (size_t)((k0 >> 3) + kb) * 16);
+        for (int j = 0; j < 4; j++) b[j] = *(const half8v *)(xr[j] + (size_t)((k0 >> 3) + kb) * 16);
     };
-    f4 acc[2][2], part[2][2];
+    constexpr int RING = 4;                                 // slices in flight: RING - 1 ahead
+    half8v A[RING][2], B[RING][4];
+#pragma unroll
+    for (int u = 0; u < RING - 1; u++)
+        if (k_lo + 32 * u < k_hi) load(A[u], B[u], k_lo + 32 * u);
+    for (int q = threadIdx.x; q < 32 * ng; q += 256) sc_lds[q] = ws[(size_t)min(o0 + q / ng, M - 1) * ng + q % ng];
+    __syncthreads();
+    const uint16_t *scw = sc_lds + (size_t)(4 * kb) * ng;
+    f4 acc[2][4], part[2][4];
 #pragma unroll
     for (int i = 0; i < 2; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) acc[i][j] = part[i][j] = f4{0.f, 0.f, 0.f, 0.f};
-    half8v a[2], b[2], an[2], bn[2];
-    load(an, bn, 0);
-    int g = 0, gend = group;
-    for (int k0 = 0; k0 < N; k0 += 32) {
+        for (int j = 0; j < 4; j++) acc[i][j] = part[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+    int g = g_lo, gend = k_lo + group;
+    for (int kc = k_lo; kc < k_hi; kc += 32 * RING) {
 #pragma unroll
-        for (int i = 0; i < 2; i++) { a[i] = an[i]; b[i] = bn[i]; }
-        if (k0 + 32 < N) load(an, bn, k0 + 32);            // uniform
+        for (int u = 0; u < RING; u++) {
+            const int k0 = kc + 32 * u;
+            if (k0 < k_hi) {                                // uniform
+                if (k0 + 32 * (RING - 1) < k_hi)
+                    load(A[(u + RING - 1) % RING], B[(u + RING - 1) % RING], k0 + 32 * (RING - 1));
 #pragma unroll
-        for (int i = 0; i < 2; i++)
+                for (int i = 0; i < 2; i++)
 #pragma unroll
-            for (int j = 0; j < 2; j++) part[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], part[i][j], 0, 0, 0);
-        if (k0 + 32 == gend) {                             // uniform: the group is complete
-            // lane (kb, m) holds rows 4 kb + r of each 16-row tile
+                    for (int j = 0; j < 4; j++)
+                        part[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[u][i], B[u][j], part[i][j], 0, 0, 0);
+                if (k0 + 32 == gend) {                      // uniform: the group is complete
+                    // lane (kb, m) holds rows 4 kb + r of each 16-row tile
 #pragma unroll
-            for (int i = 0; i < 2; i++)
+                    for (int i = 0; i < 2; i++)
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const float sc = f16_keep(ws[(size_t)min(o0 + i * 16 + 4 * kb + r, M - 1) * ng + g]);
+                        for (int r = 0; r < 4; r++) {
+                            const float sc = f16_keep(scw[(size_t)(i * 16 + r) * ng + g]);
 #pragma unroll
-                    for (int j = 0; j < 2; j++) {
-                        acc[i][j][r] = __builtin_fmaf(sc, part[i][j][r], acc[i][j][r]);
-                        part[i][j][r] = 0.0f;
-                    }
+                            for (int j = 0; j < 4; j++) {
+                                acc[i][j][r] = __builtin_fmaf(sc, part[i][j][r], acc[i][j][r]);
+                                part[i][j][r] = 0.0f;
+                            }
+                        }
+                    g++;
+                    gend += group;
                 }
-            g++;
-            gend += group;
+            }
         }
     }
-    // column m holds token m / 2, half m % 2: add the halves, remove 2^k
+    // column m holds token m / 2, half m % 2: add the halves; the quarters
+    // meet in LDS and are added in wave order, then 2^k is removed
 #pragma unroll
     for (int i = 0; i < 2; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+        for (int j = 0; j < 4; j++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const float v = acc[i][j][r] + __shfl_xor(acc[i][j][r], 1);
-                const int t = t0 + j * 8 + (m >> 1), o = o0 + i * 16 + 4 * kb + r;
-                if ((m & 1) == 0 && t < T && o < M) y[(size_t)t * M + o] = v * xscale[t];
+                if ((m & 1) == 0) red[(wave * 32 + i * 16 + 4 * kb + r) * 32 + j * 8 + (m >> 1)] = v;
             }
+    __syncthreads();
+    for (int q = threadIdx.x; q < 32 * 32; q += 256) {
+        const int o = o0 + (q >> 5), t = t0 + (q & 31);
+        if (o < M && t < T) {
+            const float v = ((red[q] + red[1024 + q]) + red[2048 + q]) + red[3072 + q];
+            y[(size_t)t * M + o] = v * xscale[t];
+        }
+    }
 }
 
 extern "C" int wk_mvq_mfma(const int8_t *W, const uint16_t *ws, size_t rowbytes, int group, int bits,
@@ -464,12 +544,14 @@ extern "C" int wk_mvq_mfma(const int8_t *W, const uint16_t *ws, size_t rowbytes,
     if (M <= 0 || N <= 0 || T <= 0 || (N % 32) || group <= 0 || (group % 32) || (N % group)) return -1;
     if (bits == 8 && (rowbytes % 8)) return -1;
     if (bits == 4 && (rowbytes % 4)) return -1;
-    const dim3 grid((M + 63) / 64, (T + 31) / 32);
+    const dim3 grid((M + 31) / 32, (T + 31) / 32);
+    const size_t lds = (size_t)4 * 32 * 32 * sizeof(float) + (size_t)32 * (N / group) * sizeof(uint16_t);
+    if (lds > 64 * 1024) return -1;
     if (bits == 8)
-        hipLaunchKernelGGL(k_mvq_mfma<8>, grid, dim3(256), 0, (hipStream_t)stream, W, ws, rowbytes, group,
+        hipLaunchKernelGGL(k_mvq_mfma<8>, grid, dim3(256), lds, (hipStream_t)stream, W, ws, rowbytes, group,
                            (const _Float16 *)xs, xscale, M, N, T, y);
     else if (bits == 4)
-        hipLaunchKernelGGL(k_mvq_mfma<4>, grid, dim3(256), 0, (hipStream_t)stream, W, ws, rowbytes, group,
+        hipLaunchKernelGGL(k_mvq_mfma<4>, grid, dim3(256), lds, (hipStream_t)stream, W, ws, rowbytes, group,
                            (const _Float16 *)xs, xscale, M, N, T, y);
     else
         return -1;
@@ -1182,6 +1264,160 @@ template <int FMT>
 static int launch_vq_t(const VqArgs &a, int nkinds, int max_units, int npg, int tpj, void *stream) {
     if (tpj == 1) return launch_vq_w<FMT, 1>(a, nkinds, max_units, npg, stream);
     return launch_vq_w<FMT, WARP_TPJ>(a, nkinds, max_units, npg, stream);
+}
+
+// Prefill by runs: one wave per (run, 64-row block), a run being up to
+// WARP_RUN_J consecutive jobs of one expert (up to 32 of its tokens, from
+// the grouping's run list; njobs[3] runs). The wave gathers the expert's
+// codebook vectors (the A operands) once per position group and multiplies
+// them with the B operands of every job of the run, so a busy expert's
+// records are decoded once per 32 tokens instead of once per 8; only the
+// run's own jobs are multiplied. No split over positions: the wave walks
+// all of a unit's positions, the next group's gathers issued before the
+// current group's MFMAs, then writes its rows (8 waves per block, so each
+// holds 4 x 4 accumulator tiles). Code words stream from HBM WD groups
+// ahead (8 waves per CU need that many bytes in flight); the B operands
+// come from L2, BD groups ahead.
+template <int FMT, int WD>
+__global__ __launch_bounds__(512) void k_vq_mfma_run(VqArgs a, const int *__restrict__ runs) {
+    typedef FmtT<FMT> F;
+    constexpr int RJ = WARP_RUN_J;
+    extern __shared__ __attribute__((aligned(16))) unsigned char lds_vq[];
+    const int kind = a.kind_lo + blockIdx.y;
+    const warp_job *jobs = a.jobs + (size_t)kind * a.max_jobs;
+    const int M = a.M, N = a.N, nv = N >> 3, npg = nv >> 2, nrb = (M + 63) >> 6;
+    const int units = a.njobs[3] * nrb;
+    if ((int)(blockIdx.x * 8) >= units) return;   // uniform per block
+    {
+        const uint4 *src = (const uint4 *)(a.books + (size_t)kind * F::S * F::E * 8);
+        uint4 *dst = (uint4 *)lds_vq;
+        for (int i = threadIdx.x; i < F::S * F::E; i += blockDim.x) dst[i] = src[i];
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, jc = lane & 15, ts = jc >> 1, hl = jc & 1;
+    for (int u = blockIdx.x * 8 + wave; u < units; u += gridDim.x * 8) {
+        const int rv = __builtin_amdgcn_readfirstlane(runs[u / nrb]);   // uniform: u is
+        const int j0 = rv >> 3, nt = rv & 7, rb = u % nrb;
+        const uint8_t *cp = jobs[j0].idx + ((size_t)rb * nv) * 64 * F::SB + (size_t)lane * 4 * F::SB;
+        // B operands of every job of the run; a slot past a job's tokens
+        // points at one of its tokens (the grouping fills every slot), so
+        // every load is unconditional: its column of the product is not
+        // written out. Loads without branches keep the wait counts exact.
+        const _Float16 *xrow[RJ];
+#pragma unroll
+        for (int q = 0; q < RJ; q++)
+            xrow[q] = a.xs + (size_t)jobs[j0 + min(q, nt - 1)].xi[ts] * nv * 16 + hl * 8 + (size_t)g * 16;
+        f4 acc[RJ][4];
+#pragma unroll
+        for (int q = 0; q < RJ; q++)
+#pragma unroll
+            for (int t = 0; t < 4; t++) acc[q][t] = f4{0.f, 0.f, 0.f, 0.f};
+        constexpr int BD = 2;
+        Word<F::SB> buf[WD];
+        half8 bb[BD][RJ];
+#pragma unroll
+        for (int k = 0; k < WD; k++) buf[k].load_keep(cp + (size_t)min(k, npg - 1) * 256 * F::SB);
+#pragma unroll
+        for (int k = 0; k < BD; k++)
+#pragma unroll
+            for (int q = 0; q < RJ; q++) bb[k][q] = *(const half8 *)(xrow[q] + (size_t)min(k, npg - 1) * 64);
+        half8 av[2][4][F::S];
+        gather_group<FMT, F::SB>(lds_vq, buf[0], av[0]);
+        // one position group: the next group's gathers, the loads WD (code
+        // words) and BD (B) groups ahead, clamped to the last group, then
+        // this group's MFMAs
+        auto step = [&](int k, int pg) {
+            const int cur = k & 1;                            // = pg & 1: WD is even
+            half8 b[RJ];
+#pragma unroll
+            for (int q = 0; q < RJ; q++) b[q] = bb[k % BD][q];
+            gather_group<FMT, F::SB>(lds_vq, buf[(k + 1) % WD], av[cur ^ 1]);
+            buf[k].load_keep(cp + (size_t)min(pg + WD, npg - 1) * 256 * F::SB);
+#pragma unroll
+            for (int q = 0; q < RJ; q++) bb[k % BD][q] = *(const half8 *)(xrow[q] + (size_t)min(pg + BD, npg - 1) * 64);
+#pragma unroll
+            for (int q = 0; q < RJ; q++)
+                if (q < nt)                                   // uniform
+#pragma unroll
+                    for (int t = 0; t < 4; t++)
+#pragma unroll
+                        for (int s = 0; s < F::S; s++)
+                            acc[q][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[cur][t][s], b[q], acc[q][t], 0, 0, 0);
+        };
+        const int npg_full = npg - npg % WD;
+        for (int pgb = 0; pgb < npg_full; pgb += WD) {
+#pragma unroll
+            for (int k = 0; k < WD; k++) step(k, pgb + k);
+        }
+#pragma unroll
+        for (int k = 0; k < WD; k++)
+            if (npg_full + k < npg) step(k, npg_full + k);    // uniform
+        // lane (g, jc) holds C[4g + r][jc] of row tile t: block row 16g + 4r + t,
+        // token slot jc / 2 of the job, half jc % 2
+#pragma unroll
+        for (int q = 0; q < RJ; q++) {
+            if (q >= nt) break;                               // uniform
+            const warp_job &jq = jobs[j0 + q];
+            const bool tv = hl == 0 && ts < jq.n;
+            const float xsc = tv ? a.xscale[jq.xi[ts]] : 0.0f;
+            const int yrow = tv ? jq.yi[ts] : 0;
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float v = acc[q][t][r] + __shfl_xor(acc[q][t][r], 1);
+                    const int row = rb * 64 + 16 * g + 4 * r + t;
+                    if (tv && row < M) a.y[kind][(size_t)yrow * M + row] = (v * xsc) * f16_keep(jq.scale[row]);
+                }
+        }
+    }
+}
+
+template <int FMT>
+static int launch_vq_run(const VqArgs &a, const int *runs, int nkinds, int max_units, void *stream) {
+    typedef FmtT<FMT> F;
+    constexpr int WD = F::S == 3 ? 2 : 8;                   // three stages leave room for fewer words
+    const size_t lds = (size_t)F::S * F::E * 16;
+    static bool attr = false;
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute((const void *)k_vq_mfma_run<FMT, WD>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return -(int)e - 1000;
+        attr = true;
+    }
+    int grid = (max_units + 7) / 8;
+    const int cap = FMT == WARP_FMT_VQ12 ? 256 : 1024;
+    if (grid > cap) grid = cap;
+    if (grid < 1) grid = 1;
+    hipLaunchKernelGGL((k_vq_mfma_run<FMT, WD>), dim3(grid, nkinds), dim3(512), lds, (hipStream_t)stream, a, runs);
+    CHECK_LAUNCH();
+    return 0;
+}
+
+extern "C" int wk_vq_runs(int fmt, const warp_job *jobs, const int *njobs, int max_jobs, const int *runs,
+                          int kind_lo, int nkinds, const uint16_t *books, const uint16_t *xs, const float *xscale,
+                          float *const *y, int M, int N, void *stream) {
+    if (M <= 0 || N <= 0 || (N % 32) || max_jobs <= 0 || !runs || kind_lo < 0 || nkinds < 1 || kind_lo + nkinds > 3)
+        return -1;
+    VqArgs a;
+    a.jobs = jobs;
+    a.njobs = njobs;
+    a.max_jobs = max_jobs;
+    a.kind_lo = kind_lo;
+    a.books = books;
+    a.xs = (const _Float16 *)xs;
+    a.xscale = xscale;
+    for (int k = 0; k < 3; k++) a.y[k] = y[k];
+    a.M = M;
+    a.N = N;
+    const int max_units = max_jobs * ((M + 63) / 64);
+    switch (fmt) {
+    case WARP_FMT_VQ3R: return launch_vq_run<WARP_FMT_VQ3R>(a, runs, nkinds, max_units, stream);
+    case WARP_FMT_VQ2R: return launch_vq_run<WARP_FMT_VQ2R>(a, runs, nkinds, max_units, stream);
+    case WARP_FMT_VQ12: return launch_vq_run<WARP_FMT_VQ12>(a, runs, nkinds, max_units, stream);
+    }
+    return -1;
 }
 
 extern "C" int wk_vq_matvec(int fmt, const warp_job *jobs, const int *njobs, int max_jobs, int kind_lo,
@@ -2215,6 +2451,30 @@ __device__ __forceinline__ bool pair_valid(const int *pid, const float *w, int t
     return w[t * K + k] != 0.0f;
 }
 
+// Exclusive prefix sum of v over the block (blockDim a multiple of 64, at
+// most 1024 threads); *total gets the block's sum. tmp: 16 ints of LDS.
+// Every thread of the block calls it.
+__device__ __forceinline__ int block_scan_excl(int v, int *tmp, int &total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    int x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o);
+        if (lane >= o) x += y;
+    }
+    if (lane == 63) tmp[wave] = x;
+    __syncthreads();
+    int base = 0, tot = 0;
+    for (int w = 0; w < nw; w++) {
+        const int t = tmp[w];
+        base += w < wave ? t : 0;
+        tot += t;
+    }
+    __syncthreads();
+    total = tot;
+    return base + x - v;
+}
+
 // One block. The picks are staged in LDS; each expert gets a bitmap of the
 // tokens that pick it (in LDS when it fits, else the pairs are found by a
 // scan per expert); a pair's place in its expert's list is the number of
@@ -2226,15 +2486,17 @@ __global__ __launch_bounds__(1024) void k_plan_chunk(const int *__restrict__ idx
                                                      int *__restrict__ pair_tok, int *__restrict__ pair_exp,
                                                      float *__restrict__ pair_w, int *__restrict__ tok_slots,
                                                      warp_job *__restrict__ jobs, int max_jobs,
-                                                     int *__restrict__ njobs, int *__restrict__ missing, int inter,
-                                                     int bitmaps) {
+                                                     int *__restrict__ njobs, int *__restrict__ runs,
+                                                     int *__restrict__ missing, int inter, int bitmaps) {
     extern __shared__ int lds_plan[];
     const int P = T * K, NW = (T + 31) >> 5;
     int *pid = lds_plan;                            // [P]
     int *cnt = pid + P;                             // [E]
     int *off = cnt + E;                             // [E]
     int *tile0 = off + E;                           // [E]
-    unsigned *bm = (unsigned *)(tile0 + E);         // [E][NW] when bitmaps
+    int *run0 = tile0 + E;                          // [E] place of the expert's first full run
+    int *runr = run0 + E;                           // [E] place of its last, partial run
+    unsigned *bm = (unsigned *)(runr + E);          // [E][NW] when bitmaps
     for (int q = threadIdx.x; q < P; q += blockDim.x) pid[q] = idx[q];
     for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[e] = 0;
     if (bitmaps)
@@ -2248,21 +2510,59 @@ __global__ __launch_bounds__(1024) void k_plan_chunk(const int *__restrict__ idx
         }
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        int run = 0, tiles = 0, miss = 0;
-        for (int e = 0; e < E; e++) {
-            off[e] = run;
-            offsets[e] = run;
-            counts[e] = cnt[e];
-            tile0[e] = tiles;
-            run += cnt[e];
-            tiles += (cnt[e] + WARP_TPJ - 1) / WARP_TPJ;
-            if (cnt[e] && !table[e].rec) miss = 1;
+    // per expert, in parallel: pair offset, first job, and the places of
+    // its runs -- heaviest first: every full run of WARP_RUN_J jobs, then the
+    // partial runs by their job count down to 1 (the launch hands units to
+    // waves round-robin, so the long ones start first)
+    __shared__ int sc_tmp[16];
+    __shared__ int miss_s;
+    if (threadIdx.x == 0) miss_s = 0;
+    int carry[2 + WARP_RUN_J] = {0, 0, 0, 0, 0, 0};   // pairs, jobs, full runs, partial runs by size
+    for (int e0 = 0; e0 < E; e0 += blockDim.x) {
+        const int e = e0 + threadIdx.x;
+        const int c = e < E ? cnt[e] : 0, nt = (c + WARP_TPJ - 1) / WARP_TPJ, r = nt % WARP_RUN_J;
+        int tot;
+        const int pc = block_scan_excl(c, sc_tmp, tot) + carry[0];
+        const int tc = tot;
+        const int pt = block_scan_excl(nt, sc_tmp, tot) + carry[1];
+        carry[1] += tot;
+        const int pf = block_scan_excl(nt / WARP_RUN_J, sc_tmp, tot) + carry[2];
+        carry[2] += tot;
+        int pr = 0;
+#pragma unroll
+        for (int q = 1; q < WARP_RUN_J; q++) {
+            const int x = block_scan_excl(r == q ? 1 : 0, sc_tmp, tot);
+            if (r == q) pr = x + carry[2 + q];
+            carry[2 + q] += tot;
         }
-        offsets[E] = run;
-        if (miss) *missing = 1;
-        const int nj = (miss || tiles > max_jobs) ? 0 : tiles;
+        if (e < E) {
+            off[e] = offsets[e] = pc;
+            counts[e] = c;
+            tile0[e] = pt;
+            run0[e] = pf;
+            runr[e] = r ? pr : -1;            // rank among the partial runs of its size, placed below
+            if (c && !table[e].rec) miss_s = 1;
+        }
+        carry[0] += tc;
+    }
+    __syncthreads();
+    // partial runs after the full ones, by size: WARP_RUN_J - 1 first
+    int base[WARP_RUN_J];
+    base[WARP_RUN_J - 1] = carry[2];
+    for (int q = WARP_RUN_J - 1; q > 1; q--) base[q - 1] = base[q] + carry[2 + q];
+    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+        const int r = ((cnt[e] + WARP_TPJ - 1) / WARP_TPJ) % WARP_RUN_J;
+#pragma unroll
+        for (int q = 1; q < WARP_RUN_J; q++)
+            if (r == q) runr[e] += base[q];
+    }
+    const int tiles = carry[1], nrun = base[1] + carry[3];
+    if (threadIdx.x == 0) {
+        offsets[E] = carry[0];
+        if (miss_s) *missing = 1;
+        const int nj = (miss_s || tiles > max_jobs) ? 0 : tiles;
         njobs[0] = njobs[1] = njobs[2] = nj;
+        njobs[3] = nj ? nrun : 0;
         if (tiles > max_jobs) *missing = 2;
     }
     __syncthreads();
@@ -2297,24 +2597,37 @@ __global__ __launch_bounds__(1024) void k_plan_chunk(const int *__restrict__ idx
         tok_slots[q - k + r] = pos;
     }
     __syncthreads();
-    if (njobs[0] == 0) return;
+    if (miss_s || tiles > max_jobs) return;          // uniform
+    // the runs, one thread per expert (a few entries each)
     for (int e = threadIdx.x; e < E; e += blockDim.x) {
-        const int c = cnt[e];
-        const int ntile = (c + WARP_TPJ - 1) / WARP_TPJ;
-        for (int i = 0; i < ntile; i++) {
-            const int base = off[e] + i * WARP_TPJ, n = min(WARP_TPJ, c - i * WARP_TPJ);
-            for (int kind = 0; kind < 3; kind++) {
-                warp_job *jo = jobs + (size_t)kind * max_jobs + tile0[e] + i;
-                const int soff = kind == 0 ? 0 : kind == 1 ? inter : 2 * inter;
-                jo->idx = table[e].rec + table[e].off[kind];
-                jo->scale = (const uint16_t *)(table[e].rec + table[e].off[3]) + soff;
-                jo->n = n;
-                jo->rsv = 0;
-                for (int s = 0; s < WARP_TPJ; s++) {
-                    const int slot = base + (s < n ? s : 0);
-                    jo->xi[s] = kind == 2 ? slot : pair_tok[slot];
-                    jo->yi[s] = slot;
-                }
+        const int ntile = (cnt[e] + WARP_TPJ - 1) / WARP_TPJ;
+        for (int i = 0; i + WARP_RUN_J <= ntile; i += WARP_RUN_J)
+            runs[run0[e] + i / WARP_RUN_J] = ((tile0[e] + i) << 3) | WARP_RUN_J;
+        if (ntile % WARP_RUN_J)
+            runs[runr[e]] = ((tile0[e] + ntile / WARP_RUN_J * WARP_RUN_J) << 3) | (ntile % WARP_RUN_J);
+    }
+    // the jobs, one thread per job: its expert is the last one whose first
+    // job is not after it (experts without jobs share the next one's first)
+    for (int j = threadIdx.x; j < tiles; j += blockDim.x) {
+        int lo = 0, hi = E - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (tile0[mid] <= j) lo = mid;
+            else hi = mid - 1;
+        }
+        const int e = lo, i = j - tile0[e], c = cnt[e];
+        const int base = off[e] + i * WARP_TPJ, n = min(WARP_TPJ, c - i * WARP_TPJ);
+        for (int kind = 0; kind < 3; kind++) {
+            warp_job *jo = jobs + (size_t)kind * max_jobs + j;
+            const int soff = kind == 0 ? 0 : kind == 1 ? inter : 2 * inter;
+            jo->idx = table[e].rec + table[e].off[kind];
+            jo->scale = (const uint16_t *)(table[e].rec + table[e].off[3]) + soff;
+            jo->n = n;
+            jo->rsv = 0;
+            for (int s = 0; s < WARP_TPJ; s++) {
+                const int slot = base + (s < n ? s : 0);
+                jo->xi[s] = kind == 2 ? slot : pair_tok[slot];
+                jo->yi[s] = slot;
             }
         }
     }
@@ -2322,10 +2635,11 @@ __global__ __launch_bounds__(1024) void k_plan_chunk(const int *__restrict__ idx
 
 extern "C" int wk_plan_chunk(const int *idx, const float *w, int T, int K, int E, const warp_slot *table,
                              int *counts, int *offsets, int *pair_tok, int *pair_exp, float *pair_w, int *tok_slots,
-                             warp_job *jobs, int max_jobs, int *njobs, int *missing, int inter, void *stream) {
-    if (T <= 0 || K <= 0 || E <= 0 || max_jobs <= 0) return -1;
+                             warp_job *jobs, int max_jobs, int *njobs, int *runs, int *missing, int inter,
+                             void *stream) {
+    if (T <= 0 || K <= 0 || E <= 0 || max_jobs <= 0 || !runs) return -1;
     // the picks and the per-expert tables in LDS; the token bitmaps too when they fit
-    const size_t base = ((size_t)T * K + 3 * (size_t)E) * sizeof(int);
+    const size_t base = ((size_t)T * K + 5 * (size_t)E) * sizeof(int);
     const size_t bms = (size_t)E * ((T + 31) / 32) * sizeof(unsigned);
     if (base > 65536) return -1;
     const int bitmaps = base + bms <= 98304;
@@ -2338,7 +2652,7 @@ extern "C" int wk_plan_chunk(const int *idx, const float *w, int T, int K, int E
     }
     hipLaunchKernelGGL(k_plan_chunk, dim3(1), dim3(1024), base + (bitmaps ? bms : 0), (hipStream_t)stream, idx, w, T,
                        K, E, table, counts, offsets, pair_tok, pair_exp, pair_w, tok_slots, jobs, max_jobs, njobs,
-                       missing, inter, bitmaps);
+                       runs, missing, inter, bitmaps);
     CHECK_LAUNCH();
     return 0;
 }

@@ -35,6 +35,7 @@ extern "C" {
 #define WARP_TILE 64          /* index_block of the container format     */
 #define WARP_LUT_BLK 32       /* positions per int8 LUT scale (VQ4P)     */
 #define WARP_TPJ 8            /* token slots per matvec job              */
+#define WARP_RUN_J 4          /* jobs of one expert per prefill run      */
 #define WARP_MAX_K 64         /* top-k bound (the reference's cfg_sane)  */
 
 /* One matvec job: one matrix (kind) of one expert record against up to
@@ -82,7 +83,9 @@ int wk_mvq_mfma(const int8_t *W, const uint16_t *ws, size_t rowbytes, int group,
 
 /* Router logits [T][E] = W [E][H] . x [T][H]. strict = 1 reproduces the
  * reference's sequential, unfused fp32 sum (dotf on x86); 0 is a parallel
- * fixed-order tree. */
+ * fixed-order tree, or for batches of WARP_ROUTER_MFMA_T tokens or more
+ * (H a multiple of 16) a fixed order of fp32 matrix-core steps. */
+#define WARP_ROUTER_MFMA_T 16
 int wk_router_logits(const float *W, const float *x, int E, int H, int T, int strict,
                      float *logits, void *stream);
 
@@ -129,6 +132,12 @@ int wk_vq_matvec(int fmt, const warp_job *jobs, const int *njobs, int max_jobs,
                  int kind_lo, int nkinds, const uint16_t *books, const uint16_t *xs,
                  const float *xscale, float *const *y, int M, int N, int tokens_per_job,
                  void *stream);
+/* The same for prefill by runs: runs[0..njobs[3]) = (first job << 3) | jobs,
+ * up to WARP_RUN_J consecutive jobs of one expert (wk_plan_chunk writes
+ * them); each run's records are decoded once for all its jobs. */
+int wk_vq_runs(int fmt, const warp_job *jobs, const int *njobs, int max_jobs, const int *runs,
+               int kind_lo, int nkinds, const uint16_t *books, const uint16_t *xs, const float *xscale,
+               float *const *y, int M, int N, void *stream);
 
 /* The LUT matvec (decode, one input per job): for each kind
  * kind_lo..kind_lo+nkinds-1, every job's rows against the f32 input
@@ -212,12 +221,13 @@ int wk_act(const float *g, const float *u, int P, int I, int act_situ, float bet
  * pair_tok/pair_exp/pair_w [T*K], and tok_slots [T][K]: each token's pair
  * slots in ascending expert id; gate/up jobs (tiles of WARP_TPJ tokens of
  * one expert; xi = token, yi = pair slot) and down jobs (xi = yi = pair
- * slot) written to jobs[kind*max_jobs ..], counts to njobs[3]. Pairs whose
- * expert has no resident record set *missing. */
+ * slot) written to jobs[kind*max_jobs ..], counts to njobs[0..3); the runs
+ * of up to WARP_RUN_J jobs of one expert to runs, their count to njobs[3].
+ * Pairs whose expert has no resident record set *missing. */
 int wk_plan_chunk(const int *idx, const float *w, int T, int K, int E,
                   const warp_slot *table, int *counts, int *offsets, int *pair_tok,
                   int *pair_exp, float *pair_w, int *tok_slots, warp_job *jobs,
-                  int max_jobs, int *njobs, int *missing, int inter, void *stream);
+                  int max_jobs, int *njobs, int *runs, int *missing, int inter, void *stream);
 /* out [T][H] = per token, sum over its pairs in ascending expert id (tok_slots)
  * of w * y[pair], then + add0 [T][H] when given. */
 int wk_combine_chunk(const float *y, const int *tok_slots, const float *pair_w, int T, int K, int H,
