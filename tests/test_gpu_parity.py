@@ -174,7 +174,7 @@ def test_router_batch_on_matrix_cores():
     (|d| <= H * 2^-24 * sum|w x|); a token's logits do not depend on its
     place in the batch or on the batch size (bit for bit); and they select
     the same experts as the one-token router, whose sum runs in another
-    order. Token and expert counts are not multiples of the 32 x 32 block."""
+    order. Token and expert counts are not multiples of the 16 x 16 block."""
     import warp_amd
     spec = ct.Spec(hidden=256, inter=64, experts=40, top_k=4, layers=1, fmt="VQ3R", seed=17, **BALANCED)
     model = ct.build(spec)

@@ -196,35 +196,36 @@ __global__ __launch_bounds__(256) void k_router_fast(const float *__restrict__ W
 
 // A batch of tokens on the matrix cores: logits[t][e] = X[t] . W[e] with
 // v_mfma_f32_16x16x4_f32 (fp32 products, fp32 sums). A block of 4 waves owns
-// 32 tokens x 32 experts, one 16 x 16 tile per wave, over all of H. Per 16
-// columns of H a lane loads one float4 of its token row and one of its
+// 16 tokens x 16 experts; wave w sums the w-th quarter of H's 16-column
+// chunks. Per chunk a lane loads one float4 of its token row and one of its
 // expert row (columns 4j..4j+3 of the 16, j = lane / 16) and feeds their
 // components to 4 MFMA steps: step s sums column 4j + s, the same column on
-// both sides. Each output is a fixed sequence of MFMA steps whatever the
-// token's place in the batch. Loads run 7 chunks of 16 columns ahead of
-// the multiplies. H is a multiple of 16.
+// both sides. The quarters meet in LDS and are added in wave order, so each
+// logit is a fixed sequence of sums whatever the token's place in the
+// batch. Loads run 7 chunks ahead of the multiplies. H is a multiple of 16.
 __global__ __launch_bounds__(256) void k_router_mfma(const float *__restrict__ W, const float *__restrict__ x, int E,
                                                      int H, int T, float *__restrict__ logits) {
+    __shared__ float red[4][16][16];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int t0 = blockIdx.x * 32 + (wave & 1) * 16, e0 = blockIdx.y * 32 + (wave >> 1) * 16;
+    const int t0 = blockIdx.x * 16, e0 = blockIdx.y * 16;
     const int r = lane & 15, j = lane >> 4;
     const float4 *xa = (const float4 *)(x + (size_t)min(t0 + r, T - 1) * H) + j;
     const float4 *wb = (const float4 *)(W + (size_t)min(e0 + r, E - 1) * H) + j;
-    const int nc = H >> 4;
+    const int nc = H >> 4, c_lo = wave * nc / 4, c_hi = (wave + 1) * nc / 4;
     constexpr int RING = 8;                                 // 16-column chunks in flight: RING - 1 ahead
     f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     float4 a[RING], b[RING];
 #pragma unroll
     for (int u = 0; u < RING - 1; u++) {
-        const int c = min(u, nc - 1);
+        const int c = min(c_lo + u, nc - 1);
         a[u] = xa[(size_t)c * 4];
         b[u] = wb[(size_t)c * 4];
     }
-    for (int c0 = 0; c0 < nc; c0 += RING) {
+    for (int c0 = c_lo; c0 < c_hi; c0 += RING) {
 #pragma unroll
         for (int u = 0; u < RING; u++) {
             const int c = c0 + u;
-            if (c < nc) {                                   // uniform
+            if (c < c_hi) {                                 // uniform
                 const int cl = min(c + RING - 1, nc - 1);
                 a[(u + RING - 1) % RING] = xa[(size_t)cl * 4];
                 b[(u + RING - 1) % RING] = wb[(size_t)cl * 4];
@@ -237,10 +238,10 @@ __global__ __launch_bounds__(256) void k_router_mfma(const float *__restrict__ W
     }
     // lane (r, j) holds rows 4j..4j+3 (tokens) of column r (expert)
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-        const int t = t0 + 4 * j + q, e = e0 + r;
-        if (t < T && e < E) logits[(size_t)t * E + e] = acc[q];
-    }
+    for (int q = 0; q < 4; q++) red[wave][4 * j + q][r] = acc[q];
+    __syncthreads();
+    const int tt = threadIdx.x >> 4, ee = threadIdx.x & 15, t = t0 + tt, e = e0 + ee;
+    if (t < T && e < E) logits[(size_t)t * E + e] = ((red[0][tt][ee] + red[1][tt][ee]) + red[2][tt][ee]) + red[3][tt][ee];
 }
 
 // The reference's dotf on x86 (src/model.c:155-160): one sequential, unfused
@@ -264,7 +265,7 @@ extern "C" int wk_router_logits(const float *W, const float *x, int E, int H, in
         hipLaunchKernelGGL(k_router_strict, dim3((rows + 63) / 64), dim3(64), 0, (hipStream_t)stream, W, x, E, H,
                            T, logits);
     else if (T >= WARP_ROUTER_MFMA_T && (H & 15) == 0)
-        hipLaunchKernelGGL(k_router_mfma, dim3((T + 31) / 32, (E + 31) / 32), dim3(256), 0, (hipStream_t)stream, W, x,
+        hipLaunchKernelGGL(k_router_mfma, dim3((T + 15) / 16, (E + 15) / 16), dim3(256), 0, (hipStream_t)stream, W, x,
                            E, H, T, logits);
     else
         hipLaunchKernelGGL(k_router_fast, dim3(rows), dim3(256), 0, (hipStream_t)stream, W, x, E, H, T, logits);
@@ -1336,13 +1337,14 @@ __global__ __launch_bounds__(512) void k_vq_mfma_run(VqArgs a, const int *__rest
             buf[k].load_keep(cp + (size_t)min(pg + WD, npg - 1) * 256 * F::SB);
 #pragma unroll
             for (int q = 0; q < RJ; q++) bb[k % BD][q] = *(const half8 *)(xrow[q] + (size_t)min(pg + BD, npg - 1) * 64);
+            // stage-major: the 4 row tiles' chains interleave, no MFMA waits on the previous one
 #pragma unroll
             for (int q = 0; q < RJ; q++)
                 if (q < nt)                                   // uniform
 #pragma unroll
-                    for (int t = 0; t < 4; t++)
+                    for (int s = 0; s < F::S; s++)
 #pragma unroll
-                        for (int s = 0; s < F::S; s++)
+                        for (int t = 0; t < 4; t++)
                             acc[q][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[cur][t][s], b[q], acc[q][t], 0, 0, 0);
         };
         const int npg_full = npg - npg % WD;
