@@ -13,7 +13,9 @@ Workload (one "step" = one decode token through the whole stack):
 
 Reported:
   value        MoE-layer tokens/s (tokens x layers / wall time of the
-               timed steps, HIP events on the compute stream)
+               timed steps, HIP events on the compute stream); one step's
+               launches are captured as a HIP graph and replayed per token
+               (--no-graph: launched from the host)
   roofline     the expert matvec kernel: algorithmic bytes (codes + row
                scales of the 16 selected experts) / its launch time from HIP
                events bracketing each launch, against 8 TB/s
@@ -131,13 +133,37 @@ def run_gpu(args):
     for s in range(args.warmup):
         step(s)
     ctx.sync()
+    timed = step
+    graph = None
+    if args.graph:
+        # one step captured as a HIP graph (its 4 x layers launches), replayed
+        # per token after the token's input is copied into its input buffer
+        from warp_amd.device import D2D, Graph, copy_async
+        stage = Buf.empty(H)
+
+        def body():
+            x = stage.ptr
+            for L in range(args.layers):
+                out = bufs[L & 1]
+                ctx.moe_decode(L, x, out, resid_dev=x)
+                x = out.ptr
+
+        graph = Graph(stream, body)
+
+        def timed(s):
+            copy_async(stage.ptr, X.ptr + (s % n_in) * H * 4, H * 4, D2D, stream)
+            graph.launch()
+
+        for s in range(args.warmup):
+            timed(s)
+        ctx.sync()
     e0, e1 = Event(), Event()
     # timed steps: nothing but the layers on the stream
-    log(f"bench: timing {args.steps} steps of {args.layers} layers")
+    log(f"bench: timing {args.steps} steps of {args.layers} layers" + (" (graph replays)" if graph else ""))
     t0 = time.perf_counter()
     e0.record(stream)
     for s in range(args.steps):
-        step(s)
+        timed(s)
     e1.record(stream)
     e1.synchronize()
     ctx.sync()
@@ -155,6 +181,8 @@ def run_gpu(args):
     out = bufs[(args.layers - 1) & 1].numpy()
     assert np.isfinite(out).all(), "non-finite hidden state after the stack"
     st = ctx.cache_stats()
+    if graph is not None:
+        graph.free()
     ctx.close()
     return ms, wall, kms, kn, st
 
@@ -689,6 +717,8 @@ def main():
     ap.add_argument("--resident", type=int, default=64, help="expert records per layer kept in HBM")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-graph", dest="graph", action="store_false",
+                    help="k3-decode: launch every kernel from the host instead of replaying one captured step")
     ap.add_argument("--matvec-path", choices=["auto", "mfma"], default="auto",
                     help="expert matvec kernel: auto = the LUT kernel, mfma = decode-then-dot on the matrix cores")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
@@ -746,6 +776,7 @@ def main():
         "vs_baseline": None,
         "dtype": "fp32",
         "data": "synthetic (random codes, codebooks, scales and routers of the K3 shapes)",
+        "launch": "one step captured as a HIP graph and replayed per token" if args.graph else "host launches",
         "config": {"workload": "K3-scale MoE decode layer, batch 1, 60-layer stack",
                    "hidden": H, "inter": I, "experts": E, "top_k": K, "layers": layers,
                    "format": "RVQ 2x4096 12-bit codes (3.00 b/w)", "resident_per_layer": args.resident,

@@ -1508,7 +1508,6 @@ int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *ou
         release_hold(c, layer);
     }
     KRN(c, wait_copies(c));
-    DEV(c, hipMemsetAsync(c->missing, 0, sizeof(int), c->st));
     KRN(c, wk_plan_chunk(c->idx, c->w, T, K, E, table, c->counts, c->offsets, c->pair_tok, c->pair_exp, c->pair_w,
                          c->tok_slots, c->jobs, c->max_jobs, c->njobs, c->runs, c->missing, I, c->st));
     DEV(c, hipEventRecord(c->ev_before, c->st));

@@ -2561,11 +2561,10 @@ __global__ __launch_bounds__(1024) void k_plan_chunk(const int *__restrict__ idx
     const int tiles = carry[1], nrun = base[1] + carry[3];
     if (threadIdx.x == 0) {
         offsets[E] = carry[0];
-        if (miss_s) *missing = 1;
         const int nj = (miss_s || tiles > max_jobs) ? 0 : tiles;
         njobs[0] = njobs[1] = njobs[2] = nj;
         njobs[3] = nj ? nrun : 0;
-        if (tiles > max_jobs) *missing = 2;
+        *missing = tiles > max_jobs ? 2 : miss_s ? 1 : 0;   // written every call: no clearing needed
     }
     __syncthreads();
     // every token's K slots: its computed pairs in ascending expert id, then -1

@@ -223,7 +223,8 @@ int wk_act(const float *g, const float *u, int P, int I, int act_situ, float bet
  * one expert; xi = token, yi = pair slot) and down jobs (xi = yi = pair
  * slot) written to jobs[kind*max_jobs ..], counts to njobs[0..3); the runs
  * of up to WARP_RUN_J jobs of one expert to runs, their count to njobs[3].
- * Pairs whose expert has no resident record set *missing. */
+ * *missing is written every call: 1 when a pair's expert has no resident
+ * record, 2 when the jobs exceed max_jobs, else 0. */
 int wk_plan_chunk(const int *idx, const float *w, int T, int K, int E,
                   const warp_slot *table, int *counts, int *offsets, int *pair_tok,
                   int *pair_exp, float *pair_w, int *tok_slots, warp_job *jobs,

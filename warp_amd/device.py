@@ -31,6 +31,10 @@ def rt():
             ("hipEventElapsedTime", i, [C.POINTER(C.c_float), vp, vp]),
             ("hipGetErrorString", C.c_char_p, [i]), ("hipGetDeviceCount", i, [C.POINTER(i)]),
             ("hipMemGetInfo", i, [C.POINTER(sz), C.POINTER(sz)]),
+            ("hipMemcpyAsync", i, [vp, vp, sz, i, vp]),
+            ("hipStreamBeginCapture", i, [vp, i]), ("hipStreamEndCapture", i, [vp, C.POINTER(vp)]),
+            ("hipGraphInstantiate", i, [C.POINTER(vp), vp, vp, vp, sz]), ("hipGraphLaunch", i, [vp, vp]),
+            ("hipGraphExecDestroy", i, [vp]), ("hipGraphDestroy", i, [vp]),
         ]:
             fn = getattr(R, name)
             fn.restype, fn.argtypes = res, args
@@ -103,6 +107,46 @@ class Buf:
         if self.ptr:
             rt().hipFree(self.ptr)
             self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def copy_async(dst: int, src: int, nbytes: int, kind: int, stream):
+    check(rt().hipMemcpyAsync(dst, src, nbytes, kind, stream), "hipMemcpyAsync")
+
+
+class Graph:
+    """Work issued on one stream by `fn()` captured into a HIP graph
+    (relaxed capture mode) and replayed with launch(). The captured calls
+    must issue only kernels, event records and copies between device
+    buffers on that stream: nothing that waits on the host."""
+
+    def __init__(self, stream, fn):
+        self.stream = stream
+        self.graph = C.c_void_p()
+        self.exec = C.c_void_p()
+        check(rt().hipStreamBeginCapture(stream, 2), "hipStreamBeginCapture")
+        try:
+            fn()
+        finally:
+            rc = rt().hipStreamEndCapture(stream, C.byref(self.graph))
+        check(rc, "hipStreamEndCapture")
+        check(rt().hipGraphInstantiate(C.byref(self.exec), self.graph, None, None, 0), "hipGraphInstantiate")
+
+    def launch(self):
+        check(rt().hipGraphLaunch(self.exec, self.stream), "hipGraphLaunch")
+
+    def free(self):
+        if self.exec:
+            rt().hipGraphExecDestroy(self.exec)
+            self.exec = C.c_void_p()
+        if self.graph:
+            rt().hipGraphDestroy(self.graph)
+            self.graph = C.c_void_p()
 
     def __del__(self):
         try:
