@@ -411,12 +411,33 @@ def run_kimi_decode(args):
     for s in range(args.warmup):
         step(s)
     ctx.sync()
+    timed, graph = step, None
+    if args.graph:
+        from warp_amd.device import D2D, Graph, copy_async
+        stage = Buf.empty(KH)
+
+        def body():
+            x = stage.ptr
+            for L in range(layers):
+                out = bufs[L & 1]
+                ctx.moe_decode(L, x, out, resid_dev=x)
+                x = out.ptr
+
+        graph = Graph(ctx.stream, body)
+
+        def timed(s):
+            copy_async(stage.ptr, X.ptr + (s % n_in) * KH * 4, KH * 4, D2D, ctx.stream)
+            graph.launch()
+
+        for s in range(args.warmup):
+            timed(s)
+        ctx.sync()
     e0, e1 = Event(), Event()
     log(f"bench: timing {args.steps} decode steps of {layers} Kimi-Linear layers")
     t0 = time.perf_counter()
     e0.record(ctx.stream)
     for s in range(args.steps):
-        step(s)
+        timed(s)
     e1.record(ctx.stream)
     e1.synchronize()
     ctx.sync()
@@ -429,6 +450,8 @@ def run_kimi_decode(args):
     kms, kn = ctx.get_timing()
     ctx.set_timing(False)
     assert np.isfinite(bufs[(layers - 1) & 1].numpy()).all(), "non-finite hidden state after the stack"
+    if graph is not None:
+        graph.free()
     ctx.close()
     n_lt = args.steps * layers
     b0 = KK * (2 * gate + 2 * 2 * KI)
@@ -447,6 +470,7 @@ def run_kimi_decode(args):
         "ms_per_step": round(ms / args.steps, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
         "data": "synthetic (random codes, codebooks, scales, shared expert and routers of the Kimi-Linear shapes)",
+        "launch": "one step captured as a HIP graph and replayed per token" if args.graph else "host launches",
         "config": {"workload": f"Kimi-Linear-shape MoE layer, decode batch 1, {layers}-layer stack",
                    "hidden": KH, "inter": KI, "experts": KE, "top_k": KK, "routing": "softmax",
                    "shared_expert": "Q8G group 32, intermediate 1024", "layers": layers,
@@ -718,7 +742,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", dest="graph", action="store_false",
-                    help="k3-decode: launch every kernel from the host instead of replaying one captured step")
+                    help="k3-decode, kimi-decode: launch every kernel from the host instead of replaying one "
+                         "captured step")
     ap.add_argument("--matvec-path", choices=["auto", "mfma"], default="auto",
                     help="expert matvec kernel: auto = the LUT kernel, mfma = decode-then-dot on the matrix cores")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
