@@ -203,3 +203,30 @@ def test_router_batch_on_matrix_cores():
         log(f"batch router: within the fp32 bound of float64, batch-place invariant, decode picks agree")
     finally:
         ctx.close()
+
+
+@pytest.mark.parametrize("T", [1, 16, 48])
+def test_moe_chunk_sizes(T):
+    """A chunk of one token, of exactly the batch router's threshold, and of
+    the context's max_tokens (48): routes bit-exact and outputs within the
+    bar against the oracle's moe_chunk, a layer with a Q8G shared expert in
+    the 12-bit format; one token past max_tokens is refused."""
+    import warp_amd
+    spec = ct.Spec(hidden=256, inter=128, experts=24, top_k=4, layers=1, fmt="VQ12", seed=43, **BALANCED)
+    model = ct.build(spec)
+    ctx = open_ctx(model, max_tokens=48)
+    try:
+        warp_amd.load_container_model(ctx, model)
+        X = np.random.default_rng(47 + T).normal(size=(T, spec.hidden)).astype(np.float32)
+        out, route, rw = ctx.moe_chunk_host(0, X)
+        ro, rr, rrw = po.LayerView(model, 0).moe_chunk(X)
+        assert np.array_equal(route, rr)
+        e = rel_err(out, ro)
+        assert e <= TOL, e
+        if T == 48:
+            with pytest.raises(warp_amd.WarpHipError) as ei:
+                ctx.moe_chunk_host(0, np.zeros((49, spec.hidden), np.float32))
+            assert ei.value.code == warp_amd.E_ARG, ei.value
+        log(f"moe_chunk T={T}: routes bit-exact, rel err {e:.2e}")
+    finally:
+        ctx.close()
