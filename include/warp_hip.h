@@ -271,6 +271,31 @@ int warp_hip_get_timing(warp_hip_ctx *c, double ms[4], uint64_t launches[4]);
 /* Blocks until the context's streams are idle. */
 int warp_hip_sync(warp_hip_ctx *c);
 
+/* ---- the encoder (conversion time; no context) ----------------------------
+ * Replaces waste_vq_encode (src/vq.c:96-103), same arguments, dim 8: X
+ * [n][8], books [stages][entries][8] (entries <= 256), out [n][stages]; per
+ * stage the nearest entry under squared L2 with unfused fp32 arithmetic in
+ * dimension order, the first minimum winning, the residual feeding the next
+ * stage; bit-identical codes. nthreads is ignored. Host buffers; returns 0
+ * or a negative WARP_HIP_E_* code. */
+int warp_hip_vq_encode(const float *X, int n, const float *books, int stages, int entries, int dim,
+                       uint8_t *out, int nthreads);
+/* The same with 16-bit codes and up to 4096 entries (the 12-bit format's
+ * codebooks); no counterpart in the reference, whose codes are 8-bit. */
+int warp_hip_vq_encode16(const float *X, long n, const float *books, int stages, int entries, int dim,
+                         uint16_t *out);
+/* The same on device buffers (16-byte aligned) on `stream` (a hipStream_t,
+ * NULL for the null stream), for callers that keep the matrix in HBM;
+ * resid_dev [n][8] is scratch for stages > 1. */
+int warp_hip_vq_encode_dev(const float *X_dev, long n, const float *books_dev, int stages, int entries,
+                           float *resid_dev, uint16_t *codes_dev, void *stream);
+/* Replaces waste_vq_lloyd (src/vq.c:109-136), same arguments, dim 8: one
+ * iteration (assign, then each non-empty cluster's centroid = the mean of
+ * its members summed in double in index order, bit-identical to the
+ * reference); returns the number of non-empty clusters, or a negative
+ * WARP_HIP_E_* code. entries <= 4096. */
+int warp_hip_vq_lloyd(const float *X, int n, float *C, int entries, int dim, int nthreads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -2691,6 +2691,195 @@ extern "C" int wk_combine_chunk(const float *y, const int *tok_slots, const floa
     return 0;
 }
 
+// ---- the encoder (conversion) ------------------------------------------------------------------
+//
+// waste_vq_encode (src/vq.c:50-103) for 8-dim vectors: per stage the entry
+// nearest the current vector under squared L2, d = sum over j ascending of
+// (v[j] - e[j])^2 with every multiply and add rounded on its own (the
+// reference's vq.c is built without FMA), the first minimum winning
+// (strict <), then the exact residual v - e feeds the next stage. One launch
+// per stage: the stage's codebook (entries x 8 fp32, up to 128 KiB) in LDS,
+// one thread per vector scanning every entry (all lanes read the same entry
+// at once: LDS broadcasts). The residual is kept in `cur`.
+constexpr int ENC_NT = 256;
+
+__global__ __launch_bounds__(ENC_NT) void k_vq_encode_stage(const float *__restrict__ X, float *__restrict__ cur,
+                                                            const float *__restrict__ book, int entries, long n,
+                                                            int stage, int stages, uint16_t *__restrict__ codes) {
+    extern __shared__ float4 cb4[];                  // [entries][2] float4
+    for (int i = threadIdx.x; i < entries * 2; i += ENC_NT) cb4[i] = ((const float4 *)book)[i];
+    __syncthreads();
+    const long i = (long)blockIdx.x * ENC_NT + threadIdx.x;
+    if (i >= n) return;
+    const float4 *src = (const float4 *)((stage == 0 ? X : cur) + i * 8);
+    const float4 v0 = src[0], v1 = src[1];
+    const float v[8] = { v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w };
+    int best = 0;
+    float bestd = INFINITY;
+    for (int c = 0; c < entries; c++) {
+        const float4 e0 = cb4[2 * c], e1 = cb4[2 * c + 1];
+        const float e[8] = { e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w };
+        float d = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float t = __fsub_rn(v[j], e[j]);
+            d = __fadd_rn(d, __fmul_rn(t, t));
+        }
+        if (d < bestd) {
+            bestd = d;
+            best = c;
+        }
+    }
+    codes[i * stages + stage] = (uint16_t)best;
+    if (stage + 1 < stages) {
+        const float4 b0 = cb4[2 * best], b1 = cb4[2 * best + 1];
+        float4 *dst = (float4 *)(cur + i * 8);
+        dst[0] = make_float4(__fsub_rn(v[0], b0.x), __fsub_rn(v[1], b0.y), __fsub_rn(v[2], b0.z), __fsub_rn(v[3], b0.w));
+        dst[1] = make_float4(__fsub_rn(v[4], b1.x), __fsub_rn(v[5], b1.y), __fsub_rn(v[6], b1.z), __fsub_rn(v[7], b1.w));
+    }
+}
+
+extern "C" int wk_vq_encode(const float *X, long n, const float *books, int stages, int entries, float *cur,
+                            uint16_t *codes, void *stream) {
+    if (n <= 0 || stages < 1 || entries < 1 || entries > 4096) return -1;
+    if (((uintptr_t)X | (uintptr_t)books | (uintptr_t)cur) & 15) return -1;
+    const size_t lds = (size_t)entries * 8 * sizeof(float);
+    static bool attr = false;
+    if (!attr) {
+        if (hipFuncSetAttribute((const void *)k_vq_encode_stage, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                4096 * 8 * (int)sizeof(float)) != hipSuccess)
+            return -2;
+        attr = true;
+    }
+    const unsigned grid = (unsigned)((n + ENC_NT - 1) / ENC_NT);
+    for (int s = 0; s < stages; s++) {
+        hipLaunchKernelGGL(k_vq_encode_stage, dim3(grid), dim3(ENC_NT), lds, (hipStream_t)stream, X, cur,
+                           books + (size_t)s * entries * 8, entries, n, s, stages, codes);
+        CHECK_LAUNCH();
+    }
+    return 0;
+}
+
+// One Lloyd iteration (waste_vq_lloyd, src/vq.c:109-136) after the
+// assignment: per cluster, the mean of its members, summed in double in
+// ascending member index as the reference does, so the new centroids are
+// bit-identical to it. A stable counting sort by cluster gives each
+// cluster its members in index order: counts per chunk of ENC_CH vectors,
+// per-cluster offsets (cluster-major, chunk-minor), then one wave per chunk
+// places its members in order.
+constexpr int ENC_CH = 4096;
+
+__global__ __launch_bounds__(256) void k_lloyd_count(const uint16_t *__restrict__ asg, long n, int entries,
+                                                     int *__restrict__ counts) {
+    extern __shared__ int hist[];
+    for (int c = threadIdx.x; c < entries; c += 256) hist[c] = 0;
+    __syncthreads();
+    const long i0 = (long)blockIdx.x * ENC_CH;
+    for (int k = threadIdx.x; k < ENC_CH && i0 + k < n; k += 256) atomicAdd(&hist[asg[i0 + k]], 1);
+    __syncthreads();
+    for (int c = threadIdx.x; c < entries; c += 256) counts[(size_t)blockIdx.x * entries + c] = hist[c];
+}
+
+// per cluster: running offsets over the chunks (in place) and its total
+__global__ __launch_bounds__(256) void k_lloyd_offsets(int *__restrict__ counts, int nchunk, int entries,
+                                                       int *__restrict__ total) {
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= entries) return;
+    int run = 0;
+    for (int b = 0; b < nchunk; b++) {
+        const int v = counts[(size_t)b * entries + c];
+        counts[(size_t)b * entries + c] = run;
+        run += v;
+    }
+    total[c] = run;
+}
+
+// exclusive scan of the totals (one block) and the number of live clusters
+__global__ __launch_bounds__(1024) void k_lloyd_scan(const int *__restrict__ total, int entries, int *__restrict__ base,
+                                                     int *__restrict__ live) {
+    __shared__ int tmp[16];
+    int carry = 0, nlive = 0;
+    for (int c0 = 0; c0 < entries; c0 += 1024) {
+        const int c = c0 + threadIdx.x;
+        const int v = c < entries ? total[c] : 0;
+        int tot;
+        const int ex = block_scan_excl(v, tmp, tot);
+        if (c < entries) base[c] = carry + ex;
+        carry += tot;
+        int lv;
+        (void)block_scan_excl(v > 0 ? 1 : 0, tmp, lv);
+        nlive += lv;
+    }
+    if (threadIdx.x == 0) *live = nlive;
+}
+
+// one wave per chunk, its vectors in index order, 64 at a time: a lane's
+// place among the equal clusters of its step is the number of earlier lanes
+// with its cluster; the chunk's running count per cluster is in LDS
+__global__ __launch_bounds__(64) void k_lloyd_scatter(const uint16_t *__restrict__ asg, long n, int entries,
+                                                      const int *__restrict__ rel, const int *__restrict__ base,
+                                                      int *__restrict__ sorted) {
+    extern __shared__ int ctr[];
+    const int lane = threadIdx.x;
+    for (int c = lane; c < entries; c += 64) ctr[c] = 0;
+    __syncthreads();
+    const long i0 = (long)blockIdx.x * ENC_CH;
+    const unsigned long long below = (1ull << lane) - 1ull;
+    for (int k0 = 0; k0 < ENC_CH && i0 + k0 < n; k0 += 64) {
+        const long i = i0 + k0 + lane;
+        const bool ok = i < n;
+        const int c = ok ? (int)asg[i] : -1;
+        unsigned long long peers = 0;
+        for (int j = 0; j < 64; j++)
+            if (__builtin_amdgcn_readlane(c, j) == c) peers |= 1ull << j;
+        const int rank = __popcll(peers & below), cnt = __popcll(peers);
+        const int seen = ok ? ctr[c] : 0;
+        __syncthreads();
+        if (ok) {
+            sorted[base[c] + rel[(size_t)blockIdx.x * entries + c] + seen + rank] = (int)i;
+            if (rank == 0) ctr[c] = seen + cnt;
+        }
+        __syncthreads();
+    }
+}
+
+// one thread per (cluster, dim): its members' values in index order, in double
+__global__ __launch_bounds__(256) void k_lloyd_mean(const float *__restrict__ X, const int *__restrict__ sorted,
+                                                    const int *__restrict__ base, const int *__restrict__ total,
+                                                    int entries, int dim, float *__restrict__ C) {
+    const int q = blockIdx.x * 256 + threadIdx.x;
+    if (q >= entries * dim) return;
+    const int c = q / dim, d = q - c * dim, n = total[c];
+    if (!n) return;                                   // an empty cluster keeps its centroid
+    const int *m = sorted + base[c];
+    double s = 0.0;
+    for (int k = 0; k < n; k++) s = __dadd_rn(s, (double)X[(size_t)m[k] * dim + d]);
+    C[q] = (float)__ddiv_rn(s, (double)n);
+}
+
+extern "C" int wk_vq_lloyd(const float *X, long n, float *C, int entries, int dim, uint16_t *asg, int *counts,
+                           int *total, int *base, int *sorted, int *live, void *stream) {
+    if (n <= 0 || entries < 1 || entries > 4096 || dim != 8) return -1;
+    int rc = wk_vq_encode(X, n, C, 1, entries, nullptr, asg, stream);
+    if (rc) return rc;
+    const int nchunk = (int)((n + ENC_CH - 1) / ENC_CH);
+    const size_t lds = (size_t)entries * sizeof(int);
+    hipLaunchKernelGGL(k_lloyd_count, dim3(nchunk), dim3(256), lds, (hipStream_t)stream, asg, n, entries, counts);
+    CHECK_LAUNCH();
+    hipLaunchKernelGGL(k_lloyd_offsets, dim3((entries + 255) / 256), dim3(256), 0, (hipStream_t)stream, counts,
+                       nchunk, entries, total);
+    CHECK_LAUNCH();
+    hipLaunchKernelGGL(k_lloyd_scan, dim3(1), dim3(1024), 0, (hipStream_t)stream, total, entries, base, live);
+    CHECK_LAUNCH();
+    hipLaunchKernelGGL(k_lloyd_scatter, dim3(nchunk), dim3(64), lds, (hipStream_t)stream, asg, n, entries, counts, base,
+                       sorted);
+    CHECK_LAUNCH();
+    hipLaunchKernelGGL(k_lloyd_mean, dim3((entries * dim + 255) / 256), dim3(256), 0, (hipStream_t)stream, X, sorted,
+                       base, total, entries, dim, C);
+    CHECK_LAUNCH();
+    return 0;
+}
+
 // ---- synthetic data ---------------------------------------------------------------------------
 
 __device__ __forceinline__ uint64_t splitmix(uint64_t z) {

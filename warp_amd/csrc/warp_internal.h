@@ -94,6 +94,18 @@ int wk_router_logits(const float *W, const float *x, int E, int H, int T, int st
 int wk_mvq(const int8_t *W, const uint16_t *ws, size_t rowbytes, int group, int bits,
            const float *x, int M, int N, int T, float *y, void *stream);
 
+/* The encoder (waste_vq_encode for 8-dim vectors): one launch per stage; codes
+ * [n][stages] 16-bit; cur [n][8] holds the residual between stages (unused
+ * for one stage). X, books and cur 16-byte aligned; entries <= 4096. */
+int wk_vq_encode(const float *X, long n, const float *books, int stages, int entries, float *cur,
+                 uint16_t *codes, void *stream);
+/* One Lloyd iteration (waste_vq_lloyd) on device buffers: assignment into asg,
+ * the new centroids into C (empty clusters keep theirs), the number of
+ * non-empty clusters into *live. Scratch: counts [ceil(n/4096)][entries],
+ * total, base [entries], sorted [n]. dim 8. */
+int wk_vq_lloyd(const float *X, long n, float *C, int entries, int dim, uint16_t *asg, int *counts, int *total,
+                int *base, int *sorted, int *live, void *stream);
+
 /* A layer's shared expert for one decode token, folded into the router and
  * combine launches: h = act(gate . x, up . x), then down . h. */
 typedef struct {

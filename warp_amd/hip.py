@@ -94,6 +94,12 @@ SIGNATURES = {
     "warp_hip_set_timing": (C.c_int, [C.c_void_p, C.c_int]),
     "warp_hip_get_timing": (C.c_int, [C.c_void_p, C.POINTER(C.c_double), C.POINTER(C.c_uint64)]),
     "warp_hip_sync": (C.c_int, [C.c_void_p]),
+    "warp_hip_vq_encode": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p,
+                                     C.c_int]),
+    "warp_hip_vq_encode16": (C.c_int, [C.c_void_p, C.c_long, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p]),
+    "warp_hip_vq_encode_dev": (C.c_int, [C.c_void_p, C.c_long, C.c_void_p, C.c_int, C.c_int, C.c_void_p,
+                                         C.c_void_p, C.c_void_p]),
+    "warp_hip_vq_lloyd": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_int]),
 }
 
 
@@ -316,6 +322,40 @@ class Context:
 
     def fill_random(self, dev, nbytes, seed):
         self._check(lib().warp_hip_fill_random(self.h, _addr(dev), nbytes, seed))
+
+
+def _check_rc(rc, what):
+    if rc < 0:
+        raise WarpHipError(rc, what)
+    return rc
+
+
+def vq_encode(X, books):
+    """waste_vq_encode on the device: X [n][8] f32, books [stages][entries][8]
+    f32 -> codes [n][stages] (uint8 for up to 256 entries, else uint16)."""
+    import numpy as np
+    X = np.ascontiguousarray(X, np.float32)
+    books = np.ascontiguousarray(books, np.float32)
+    n, (S, E, D) = X.shape[0], books.shape
+    if E <= 256:
+        out = np.empty((n, S), np.uint8)
+        _check_rc(lib().warp_hip_vq_encode(X.ctypes.data, n, books.ctypes.data, S, E, D, out.ctypes.data, 0),
+                  "vq_encode")
+    else:
+        out = np.empty((n, S), np.uint16)
+        _check_rc(lib().warp_hip_vq_encode16(X.ctypes.data, n, books.ctypes.data, S, E, D, out.ctypes.data),
+                  "vq_encode16")
+    return out
+
+
+def vq_lloyd(X, C):
+    """One waste_vq_lloyd iteration on the device; C [entries][8] is updated
+    in place. Returns the number of non-empty clusters."""
+    import numpy as np
+    X = np.ascontiguousarray(X, np.float32)
+    assert C.dtype == np.float32 and C.flags.c_contiguous
+    return _check_rc(lib().warp_hip_vq_lloyd(X.ctypes.data, X.shape[0], C.ctypes.data, C.shape[0], C.shape[1], 0),
+                     "vq_lloyd")
 
 
 def load_container_model(ctx: Context, model, layers=None):
