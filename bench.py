@@ -29,6 +29,8 @@ Other workloads (--workload), each printing its own JSON line:
                 softmax, Zipf(1.1)-skewed expert loads, 8-bit shared expert)
   kimi-decode   one decode token through 26 Kimi-Linear-shape layers (all
                 256 expert records of each resident, Q8G shared expert)
+  vq-encode     the encoder (waste_vq_encode) on one K3 gate matrix, 2 x 4096
+                and 3 x 256 codebooks
   k3-miss       32 decode tokens (one per sequence) through 4 K3 layers,
                 an HBM cache of 0.69 of the stack's records, misses copied
                 from pinned host memory on the copy stream; passes without
@@ -720,14 +722,103 @@ def run_miss(args):
     }
 
 
+VALU_PEAK_OPS = 78.6e12   # fp32 vector operations/s: the 157.3 TFLOP/s vector peak counts an FMA as 2
+
+
+def run_vq_encode(args):
+    """The encoder (waste_vq_encode) on one K3 gate matrix: 2048 x 7168
+    weights = 1,835,008 vectors of 8, N(0, 1), on device buffers; the
+    3 x 256 codebooks of the reference's own format and the 2 x 4096 of the
+    12-bit format. A step encodes the whole matrix."""
+    import warp_amd.hip as wh
+    from warp_amd.device import Buf, Event, check, rt
+    n = I * H // 8
+    rng = np.random.Generator(np.random.PCG64(97))
+    X = Buf.of(rng.standard_normal((n, 8), dtype=np.float32))
+    resid = Buf.empty((n, 8))
+    codes = Buf.empty((n, 3), np.uint16)
+    res = {}
+    for S_, E_ in ((3, 256), (2, 4096)):
+        books = Buf.of(rng.standard_normal((S_, E_, 8), dtype=np.float32))
+
+        def step():
+            rc = wh.lib().warp_hip_vq_encode_dev(X.ptr, n, books.ptr, S_, E_, resid.ptr, codes.ptr, None)
+            if rc:
+                raise wh.WarpHipError(rc, "vq_encode_dev")
+        for _ in range(args.warmup):
+            step()
+        check(rt().hipDeviceSynchronize(), "sync")
+        e0, e1 = Event(), Event()
+        e0.record(None)
+        for _ in range(args.steps):
+            step()
+        e1.record(None)
+        e1.synchronize()
+        ms = e0.elapsed_ms(e1) / args.steps
+        ops = n * S_ * E_ * 25.0                     # per entry: 8 subtract, 8 multiply, 8 add, 1 compare
+        res[f"{S_}x{E_}"] = {"ms_per_matrix": round(ms, 3), "vectors_per_s": round(n / (ms / 1e3), 1),
+                             "valu_ops_per_s": ops / (ms / 1e3), "valu_frac": round(ops / (ms / 1e3) / VALU_PEAK_OPS, 4)}
+        log(f"bench: vq-encode {S_}x{E_}: {ms:.3f} ms per matrix")
+        books.free()
+    main = res["3x256"]                               # the reference's format, beside its CPU encoder
+    cpu = None if args.no_cpu else cpu_baseline_encode(args.cpu_seconds)
+    return {
+        "metric": "VQ-encoded vectors/s (waste_vq_encode, 8-dim vectors), 1 MI355X",
+        "value": main["vectors_per_s"],
+        "unit": "vectors/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": main["ms_per_matrix"],
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
+        "data": "synthetic (N(0,1) vectors and codebooks)",
+        "config": {"workload": "encode one K3 gate matrix (2048 x 7168 weights, 1,835,008 vectors of 8) with "
+                               "3 x 256 codebooks (the reference's format); 2 x 4096 (16-bit codes) beside it",
+                   "vectors": n, "parallelism": "single GPU"},
+        "passes": {k: {kk: (round(vv, 1) if isinstance(vv, float) and kk != "valu_frac" else vv)
+                       for kk, vv in v.items()} for k, v in res.items()},
+        "roofline": {"bound": "valu", "achieved": round(main["valu_ops_per_s"] / 1e12, 2),
+                     "peak": round(VALU_PEAK_OPS / 1e12, 2), "unit": "T fp32 vector ops/s",
+                     "frac": main["valu_frac"], "traffic": None,
+                     "kernel": "k_vq_encode_stage (a scan of every codebook entry per vector and stage)"},
+        "cpu_baseline": cpu,
+    }
+
+
+def cpu_baseline_encode(seconds):
+    """The reference's waste_vq_encode (oracle/_ref) on the 3 x 256 case."""
+    import ctypes
+    from oracle import pyoracle as po
+    if not os.path.exists(po.REF_LIB):
+        return None
+    L = ctypes.CDLL(po.REF_LIB)
+    L.waste_vq_encode.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                  ctypes.c_int, ctypes.c_void_p, ctypes.c_int]
+    L.waste_vq_encode.restype = None
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+    rng = np.random.default_rng(98)
+    m = 1 << 16
+    X = rng.standard_normal((m, 8), dtype=np.float32)
+    books = rng.standard_normal((3, 256, 8), dtype=np.float32)
+    out = np.empty((m, 3), np.uint8)
+    L.waste_vq_encode(X.ctypes.data, m, books.ctypes.data, 3, 256, 8, out.ctypes.data, threads)
+    k, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        L.waste_vq_encode(X.ctypes.data, m, books.ctypes.data, 3, 256, 8, out.ctypes.data, threads)
+        k += 1
+    dt = time.perf_counter() - t0
+    return {"value": k * m / dt, "unit": "vectors/s", "cores": threads, "kind": "reference",
+            "sample": f"{k} calls of waste_vq_encode on {m} vectors with 3 x 256 codebooks (the reference's "
+                      f"8-bit codes; it has no 4096-entry encoder) over {threads} threads, {dt:.1f}s"}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--workload", choices=["k3-decode", "kimi-prefill", "k3-miss", "kimi-decode"],
+    ap.add_argument("--workload", choices=["k3-decode", "kimi-prefill", "k3-miss", "kimi-decode", "vq-encode"],
                     default="k3-decode",
                     help="k3-decode (the headline line), kimi-prefill (a 512-token Kimi-Linear-shape prefill) "
                          ", k3-miss (a 32-token K3 decode batch with half its expert records streamed from host) "
-                         "or kimi-decode (Kimi-Linear-shape decode, batch 1, with its shared expert)")
+                         ", kimi-decode (Kimi-Linear-shape decode, batch 1, with its shared expert) "
+                         "or vq-encode (the encoder on one K3 matrix)")
     ap.add_argument("--tokens", type=int, default=None,
                     help="tokens per step: kimi-prefill (default 512), k3-miss (default 32)")
     ap.add_argument("--cache-frac", type=float, default=0.69,
@@ -759,6 +850,9 @@ def main():
         args.layers = args.layers or 4
         args.tokens = args.tokens or 512
         print(json.dumps(run_prefill(args)))
+        return
+    if args.workload == "vq-encode":
+        print(json.dumps(run_vq_encode(args)))
         return
     if args.workload == "kimi-decode":
         args.layers = args.layers or 26

@@ -2700,8 +2700,10 @@ extern "C" int wk_combine_chunk(const float *y, const int *tok_slots, const floa
 // (strict <), then the exact residual v - e feeds the next stage. One launch
 // per stage: the stage's codebook (entries x 8 fp32, up to 128 KiB) in LDS,
 // one thread per vector scanning every entry (all lanes read the same entry
-// at once: LDS broadcasts). The residual is kept in `cur`.
-constexpr int ENC_NT = 256;
+// at once: LDS broadcasts). The residual is kept in `cur`. Blocks of 1024
+// threads, so that a 4096-entry codebook (128 KiB, one block per CU) still
+// leaves 4 waves per SIMD.
+constexpr int ENC_NT = 1024;
 
 __global__ __launch_bounds__(ENC_NT) void k_vq_encode_stage(const float *__restrict__ X, float *__restrict__ cur,
                                                             const float *__restrict__ book, int entries, long n,
