@@ -712,10 +712,11 @@ __device__ __forceinline__ int route_key(float v) {
 // (score[E], biased[E]; both overwritten). On return (all threads past a
 // barrier) sel[0..K) holds the picks in order and wsel[0..K) their weights,
 // 0 past the picks found; returns the number of picks (< K only when fewer
-// than K experts are pickable).
+// than K experts are pickable). want_w (uniform) false: the weights are not
+// computed and wsel is left at 0 (a block that only needs the picks).
 template <bool REGS, int NT>
 __device__ __forceinline__ int route_pick_lds(int E, int K, int act, int renorm, float routed_scale, float *score,
-                                              float *biased, int *sel, float *wsel) {
+                                              float *biased, int *sel, float *wsel, bool want_w = true) {
     __shared__ float red[NT / 64];
     __shared__ int np_s;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -867,15 +868,15 @@ __device__ __forceinline__ int route_pick_lds(int E, int K, int act, int renorm,
         }
         // weights: the sum in pick order (one lane, as the reference), the
         // divisions and the scale in parallel
-        float wv = lane < npick ? score[mine] : 0.0f;
-        float ssum = 0.0f;
-        for (int j = 0; j < K; j++)
-            ssum = __fadd_rn(ssum, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wv), j)));
-        if (renorm && K > 1) wv = __fdiv_rn(wv, __fadd_rn(ssum, 1e-20f));
-        wv = __fmul_rn(wv, routed_scale);
-        if (lane < K) {
-            sel[lane] = lane < npick ? mine : 0;
-            wsel[lane] = wv;
+        if (lane < K) sel[lane] = lane < npick ? mine : 0;
+        if (want_w) {
+            float wv = lane < npick ? score[mine] : 0.0f;
+            float ssum = 0.0f;
+            for (int j = 0; j < K; j++)
+                ssum = __fadd_rn(ssum, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wv), j)));
+            if (renorm && K > 1) wv = __fdiv_rn(wv, __fadd_rn(ssum, 1e-20f));
+            wv = __fmul_rn(wv, routed_scale);
+            if (lane < K) wsel[lane] = wv;
         }
         if (lane == 0) np_s = npick;
     }
@@ -1004,6 +1005,7 @@ template <> struct Word<3> {
         const gu32 *q = (const gu32 *)p;
         w = u3v{q[0], q[1], q[2]};
     }
+    __device__ __forceinline__ void mask(unsigned m) { w = u3v{w.x & m, w.y & m, w.z & m}; }
     // 24-bit slot of row t (0..3)
     __device__ __forceinline__ unsigned slot(int t) const {
         switch (t) {
@@ -1024,6 +1026,7 @@ template <> struct Word<2> {
         const gu32 *q = (const gu32 *)p;
         w = u2v{q[0], q[1]};
     }
+    __device__ __forceinline__ void mask(unsigned m) { w = u2v{w.x & m, w.y & m}; }
     __device__ __forceinline__ unsigned slot(int t) const {
         switch (t) {
         case 0: return w.x & 0xFFFFu;
@@ -1610,15 +1613,18 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
     int xi, nj;
     gu32 *sg = nullptr, *su = nullptr;
     float xr[XPT];
-    // The codebook of this kind: group G = wave * GPW + g holds entries
+    // The codebook of this kind: group G = vw * GPW + g holds entries
     // 64 G .. 64 G + 63 over [stage][entry], entry 64 G + lane in this lane
-    // (128 KiB per block for 2 x 4096 entries).
+    // (128 KiB per block for 2 x 4096 entries). vw rotates the waves' groups
+    // by block, so that the blocks of a launch, which all load the same
+    // codebook at once, start on different lines.
+    const int vw = (wave + (int)blockIdx.x) & (LUT_NW - 1);
     uint4 cb[GPW];
     auto load_cb = [&]() {
         const uint4 *bk = (const uint4 *)(a.books + (size_t)kind * SE * 8);
 #pragma unroll
         for (int g = 0; g < GPW; g++) {
-            const int G = wave * GPW + g;
+            const int G = vw * GPW + g;
             cb[g] = G < NG ? bk[G * 64 + lane] : make_uint4(0u, 0u, 0u, 0u);
         }
     };
@@ -1662,10 +1668,13 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
             *(uint2 *)&slots[e].off[0] = so01;
             *(uint2 *)&slots[e].off[2] = so23;
         }
-        route_pick_lds<true, LUT_NW * 64>(E, K, a.r.act, a.r.renorm, a.r.routed_scale, score, biased, r_sel, r_wsel);
+        // only the block that publishes the routing needs the weights
+        const bool pub = blockIdx.x == 0 && blockIdx.y == 0;
+        route_pick_lds<true, LUT_NW * 64>(E, K, a.r.act, a.r.renorm, a.r.routed_scale, score, biased, r_sel, r_wsel,
+                                          pub);
         bool miss = false;                                 // a pick without a record (the same in every block)
         for (int j = 0; j < K; j++) miss |= slots[r_sel[j]].rec == nullptr;
-        if (blockIdx.x == 0 && blockIdx.y == 0) {          // uniform per block
+        if (pub) {                                         // uniform per block
             if (threadIdx.x < K) {
                 a.r.idx[threadIdx.x] = r_sel[threadIdx.x];
                 a.r.w[threadIdx.x] = r_wsel[threadIdx.x];
@@ -1756,9 +1765,10 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
     if constexpr (!rt) load_cb();
     __builtin_amdgcn_sched_barrier(0);
     // Pairs past the group's rows read row block 0 of the block's first job
-    // (in bounds) and are never written: the loop below has no per-pair
-    // branches, so the code-word loads of the next chunk stay in flight
-    // across the whole chunk and the LDS reads of all pairs overlap.
+    // (in bounds), look up entry 0 only and are never written: the loop
+    // below has no per-pair branches, so the code-word loads of the next
+    // chunk stay in flight across the whole chunk and the LDS reads of all
+    // pairs overlap.
     const uint8_t *cp[LUT_PPW];
 #pragma unroll
     for (int q = 0; q < LUT_PPW; q++) {
@@ -1787,28 +1797,58 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
                 if (v >= nx) { v -= nx; row++; }
             }
             __syncthreads();
+            // P threads per input (uniform): thread (p, i) adds splits
+            // [p S / P, (p + 1) S / P) of input i in split order into LDS
+            // after the staged rows, then the P parts are added in part order
+            const int S = a.act_splits;
+            int P = (LUT_NW * 64) / nx;
+            P = P > 8 ? 8 : P;
+            while (P > 1 && atot + 2 * P * nx > 2 * BUF) P--;
+            float *ps = lut + atot;                        // [gate, up][P][nx]
+            if (P > 1) {
+                const int i = (int)threadIdx.x % nx, p = (int)threadIdx.x / nx;
+                if (p < P) {
+                    const int s1 = (p + 1) * S / P;
+                    float g = 0.0f, u = 0.0f;
+                    for (int s2 = p * S / P; s2 < s1; s2++) {
+                        g += lut[s2 * nx + i];
+                        u += lut[(S + s2) * nx + i];
+                    }
+                    ps[p * nx + i] = g;
+                    ps[(P + p) * nx + i] = u;
+                }
+                __syncthreads();
+            }
 #pragma unroll
             for (int k = 0; k < XPT; k++) {
                 const int i = threadIdx.x + k * LUT_NW * 64;
                 xr[k] = 0.0f;
                 if (i < nx) {
-                    // the splits in order, 16 LDS reads in flight at a time
-                    const int S = a.act_splits;
                     float g = 0.0f, u = 0.0f;
-                    for (int s0 = 0; s0 < S; s0 += 16) {
-                        float ga[16], ua[16];
-#pragma unroll
-                        for (int t = 0; t < 16; t++) {
-                            const int s2 = min(s0 + t, S - 1);
-                            ga[t] = lut[s2 * nx + i];
-                            ua[t] = lut[(S + s2) * nx + i];
+                    if (P > 1) {
+                        g = ps[i];
+                        u = ps[P * nx + i];
+                        for (int p = 1; p < P; p++) {
+                            g += ps[p * nx + i];
+                            u += ps[(P + p) * nx + i];
                         }
+                    } else {
+                        // the splits in order, 16 LDS reads in flight at a time
+                        for (int s0 = 0; s0 < S; s0 += 16) {
+                            float ga[16], ua[16];
 #pragma unroll
-                        for (int t = 0; t < 16; t++)
-                            if (s0 + t < S) {
-                                g += ga[t];
-                                u += ua[t];
+                            for (int t = 0; t < 16; t++) {
+                                const int s2 = min(s0 + t, S - 1);
+                                ga[t] = lut[s2 * nx + i];
+                                ua[t] = lut[(S + s2) * nx + i];
                             }
+#pragma unroll
+                            for (int t = 0; t < 16; t++)
+                                if (s0 + t < S) {
+                                    g += ga[t];
+                                    u += ua[t];
+                                }
+                        }
                     }
                     const int sh = 16 * (i & 1);
                     xr[k] = act_pair(g * f16_keep((uint16_t)(gs[k] >> sh)), u * f16_keep((uint16_t)(us[k] >> sh)),
@@ -1874,7 +1914,7 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
     auto build_mfma = [&](const half4 (&X)[4], int b, int q) {
 #pragma unroll
         for (int g = q; g < GPW; g += LUT_PPW) {
-            const int G = wave * GPW + g;
+            const int G = vw * GPW + g;
             if (G < NG) {                                  // uniform per wave
                 const half4 clo = half4_of(cb[g].x, cb[g].y), chi = half4_of(cb[g].z, cb[g].w);
                 f4 d = {0.f, 0.f, 0.f, 0.f};
@@ -1894,7 +1934,7 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
     auto build_valu = [&](const float (&xv)[16], int b, int q) {
 #pragma unroll
         for (int g = q; g < GPW; g += LUT_PPW) {
-            const int G = wave * GPW + g;
+            const int G = vw * GPW + g;
             if (G < NG) {
                 const uint32_t w4[4] = {cb[g].x, cb[g].y, cb[g].z, cb[g].w};
                 float t[2];
@@ -1919,6 +1959,7 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
 
     half4 B[4];
     float xv[16];
+    const int fb_lim = fb_end - fb0;                       // pairs at or past it are not real
     __syncthreads();
     if constexpr (X31) {
         load_x(xv, c0);
@@ -1946,7 +1987,10 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
                 if constexpr (X31) build_valu(xv, b ^ 1, q);
                 else build_mfma(B, b ^ 1, q);
             }
-            const Word<F::SB> w = wd[q];
+            // a pair past the group's rows looks up entry 0 of each table
+            // (one address per position: a broadcast, no bank conflicts)
+            Word<F::SB> w = wd[q];
+            w.mask(rbsel < fb_lim - 2 * (q * LUT_NW + wave) ? ~0u : 0u);
             wd[q].load_keep(cp[q] + (size_t)(2 * cn) * 64 * F::SB);
 #pragma unroll
             for (int t = 0; t < 4; t++) {
