@@ -230,3 +230,30 @@ def test_moe_chunk_sizes(T):
         log(f"moe_chunk T={T}: routes bit-exact, rel err {e:.2e}")
     finally:
         ctx.close()
+
+
+@pytest.mark.parametrize("bits,group,hidden,inter", [(8, 32, 160, 96), (4, 128, 256, 128), (8, 64, 192, 320)])
+def test_moe_chunk_shared_on_matrix_cores(bits, group, hidden, inter):
+    """The chunk's shared expert on the matrix cores (gate and up in one
+    launch, 64-row x 64-token tiles, weights staged 128 columns at a time):
+    Q8G and Q4G, groups of 32, 64 and 128, shapes that fill neither a tile
+    (96, 128, 160, 192, 256 and 320 rows; 40 tokens) nor always a slab (96,
+    160, 192 and 320 columns). The shared expert's scales are the default
+    0.002-0.02, so it dominates the output and its error is what the bar
+    sees. Routes bit-exact, output within the bar against the oracle."""
+    import warp_amd
+    spec = ct.Spec(hidden=hidden, inter=inter, experts=8, top_k=2, layers=1, fmt="VQ12", seed=53 + bits + group,
+                   shared_bits=bits, shared_group=group, book_std=0.3)
+    model = ct.build(spec)
+    ctx = open_ctx(model, max_tokens=48)
+    try:
+        warp_amd.load_container_model(ctx, model)
+        X = np.random.default_rng(59).normal(size=(40, hidden)).astype(np.float32)
+        out, route, _ = ctx.moe_chunk_host(0, X)
+        ro, rr, _ = po.LayerView(model, 0).moe_chunk(X)
+        assert np.array_equal(route, rr)
+        e = rel_err(out, ro)
+        assert e <= TOL, e
+        log(f"shared expert Q{bits}G group {group}, {inter}x{hidden}: rel err {e:.2e}")
+    finally:
+        ctx.close()

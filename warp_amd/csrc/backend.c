@@ -220,6 +220,7 @@ typedef struct {
     float *bias;                /* [E] or NULL                             */
     int8_t *sq[3]; uint16_t *ss[3];
     size_t s_rowbytes[3]; int s_bits, s_group, s_inter;
+    int s_small;    /* every shared scale finite and below 256 in magnitude */
     int resident;               /* records of this layer in the cache      */
 } layer_t;
 
@@ -692,12 +693,17 @@ int warp_hip_set_shared(warp_hip_ctx *c, int layer, int bits, int group, int int
     layer_t *L = &c->L[layer];
     const int H = c->cfg.hidden, Is = inter_shared;
     const int rows[3] = { Is, Is, H }, cols[3] = { H, H, Is };
+    int small = 1;
     for (int k = 0; k < 3; k++) {
         const int ng = (cols[k] + group - 1) / group;
         if ((rc = upload(c, (void **)&L->sq[k], q[k], (size_t)rows[k] * rowbytes[k]))) return rc;
         if ((rc = upload(c, (void **)&L->ss[k], scales[k], (size_t)rows[k] * ng * 2))) return rc;
         L->s_rowbytes[k] = rowbytes[k];
+        /* fp16 magnitude below 256 = 2^8: biased exponent below 23 */
+        for (size_t i = 0; i < (size_t)rows[k] * ng; i++)
+            small &= (scales[k][i] & 0x7fffu) < 0x5c00u;
     }
+    L->s_small = small;
     L->s_bits = bits;
     L->s_group = group;
     L->s_inter = Is;
@@ -1259,16 +1265,22 @@ static int shared_ffn(warp_hip_ctx *c, const layer_t *L, const float *x, int T)
     const warp_hip_cfg *g = &c->cfg;
     const int H = g->hidden, Is = L->s_inter;
     /* a batch: on the matrix cores, x and h split into fp16 halves */
-    if (T >= 8 && L->s_bits != 3 && L->s_group % 32 == 0 && H % L->s_group == 0 && Is % L->s_group == 0) {
+    if (T >= 8 && L->s_bits != 3 && L->s_small && L->s_group % 32 == 0 && H % L->s_group == 0 &&
+        Is % L->s_group == 0) {
+        const int8_t *wq[2] = {L->sq[0], L->sq[1]};
+        const uint16_t *wsc[2] = {L->ss[0], L->ss[1]};
+        float *gu[2] = {c->shg, c->shu};
         KRN(c, wk_split(x, T, H, c->xs, c->xscale, c->st));
-        KRN(c, wk_mvq_mfma(L->sq[0], L->ss[0], L->s_rowbytes[0], L->s_group, L->s_bits, c->xs, c->xscale, Is, H, T,
-                           c->shg, c->st));
-        KRN(c, wk_mvq_mfma(L->sq[1], L->ss[1], L->s_rowbytes[1], L->s_group, L->s_bits, c->xs, c->xscale, Is, H, T,
-                           c->shu, c->st));
+        /* gate and up in one launch: they share x */
+        KRN(c, wk_mvq_gemm(2, wq, wsc, L->s_rowbytes, L->s_group, L->s_bits, c->xs, c->xscale, Is, H, T, gu,
+                           c->st));
         KRN(c, wk_act_split(c->shg, c->shu, T, Is, g->act_situ, g->situ_beta, g->situ_linear_beta, c->shxs,
                             c->shxscale, NULL, c->st));
-        KRN(c, wk_mvq_mfma(L->sq[2], L->ss[2], L->s_rowbytes[2], L->s_group, L->s_bits, c->shxs, c->shxscale, H, Is,
-                           T, c->sho, c->st));
+        const int8_t *dq = L->sq[2];
+        const uint16_t *dsc = L->ss[2];
+        float *dy = c->sho;
+        KRN(c, wk_mvq_gemm(1, &dq, &dsc, &L->s_rowbytes[2], L->s_group, L->s_bits, c->shxs, c->shxscale, H, Is, T,
+                           &dy, c->st));
         return 0;
     }
     KRN(c, wk_mvq(L->sq[0], L->ss[0], L->s_rowbytes[0], L->s_group, L->s_bits, x, Is, H, T, c->shg, c->st));

@@ -19,6 +19,8 @@
 #include <stdint.h>
 #include <stdlib.h>
 
+#include <type_traits>
+
 #include "warp_internal.h"
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
@@ -425,137 +427,222 @@ extern "C" int wk_router_shared(const float *W, const float *x, int E, int H, fl
 // the fp16 hi/lo halves of x for 8 tokens as B (token t's hi in column 2t, lo
 // in 2t + 1; xs from wk_split), so every product is exact and the sums are
 // fp32; a group's sums are scaled by its fp16 scale in fp32, and at the end
-// the two halves are added and the token's power of two removed. A block
-// of 4 waves covers 32 rows x 32 tokens (2 x 4 tiles, 8 MFMAs per 32
-// columns), each wave over a quarter of the groups with its loads three
-// 32-column slices ahead; the quarters are added in LDS in wave order, and
-// the rows' group scales are staged in LDS once. N and the group are
-// multiples of 32.
-typedef _Float16 half8v __attribute__((ext_vector_type(8)));
+// the two halves are added and the token's power of two removed.
+//
+// One launch takes one or two matrices of the same shape that share x
+// (blockIdx.z: the shared expert's gate and up). The group scale is folded
+// into A: q * s is exact in f32 (8 + 11 significant bits) and splits exactly
+// into fp16 hi + lo (|s| < 256, so |q s| stays below the fp16 range; the
+// caller checks), so acc += A_hi . B + A_lo . B sums the same exact products
+// q s x with no per-group scaling step: the accumulators stay in the matrix
+// cores' registers. Block = 4 waves, tile 64 rows x 64 tokens: wave w takes
+// tokens 16w .. 16w + 15 (two 16-column tiles) against all 64 rows (four
+// 16-row tiles), 16 MFMAs per 32 columns. The block stages 128 columns of
+// its rows at a time in LDS as the hi and lo fp16 planes, converted once
+// for the 4 waves (rows padded by 16 bytes, so the 16 rows a wave reads at
+// one column land in distinct banks), double-buffered, with the raw weights
+// of the next 2 slabs in flight in registers. Each wave's x loads run 8
+// steps of 32 columns (2 slabs) ahead. The loop has no data-dependent
+// branches, so every wait is for the load it needs: the slab count is
+// rounded up to even and columns past N are staged as zeros (their x loads
+// repeat the last step).
+constexpr int MQ_MB = 64, MQ_TB = 64, MQ_KS = 128;
+constexpr int MQ_LDA = MQ_KS + 8;                // fp16 per staged row
+constexpr int MQ_PLANE = MQ_MB * MQ_LDA;         // fp16 per (buffer, hi/lo) plane
+
+struct MvqMat {
+    const int8_t *W;
+    const uint16_t *ws;
+    size_t rowbytes;
+    float *y;
+};
 
 template <int BITS>
-__device__ __forceinline__ half8v q8_of(const int8_t *row, int k) {
-    half8v h;
-    if (BITS == 8) {
-        const uint2 w = *(const uint2 *)(row + k);
-#pragma unroll
-        for (int i = 0; i < 8; i++) h[i] = (_Float16)(int)(int8_t)(((i < 4 ? w.x : w.y) >> (8 * (i & 3))) & 0xFF);
-    } else {
-        const unsigned w = *(const unsigned *)((const uint8_t *)row + (k >> 1));
-#pragma unroll
-        for (int i = 0; i < 8; i++) h[i] = (_Float16)((int)((w >> (4 * i)) & 0xF) - 8);
-    }
-    return h;
-}
-
-template <int BITS>
-__global__ __launch_bounds__(256) void k_mvq_mfma(const int8_t *__restrict__ W, const uint16_t *__restrict__ ws,
-                                                  size_t rowbytes, int group, const _Float16 *__restrict__ xs,
-                                                  const float *__restrict__ xscale, int M, int N, int T,
-                                                  float *__restrict__ y) {
-    extern __shared__ __attribute__((aligned(16))) unsigned char lds_mvq[];
+__global__ __launch_bounds__(256) void k_mvq_gemm(MvqMat m0, MvqMat m1, int group, const half8 *__restrict__ xs,
+                                                  const float *__restrict__ xscale, int M, int N, int T) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char lds_mq[];
+    _Float16 *As = (_Float16 *)lds_mq;           // [2 buffers][hi, lo][MB][LDA]
+    const MvqMat mt = blockIdx.z ? m1 : m0;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int o0 = blockIdx.x * 32, t0 = blockIdx.y * 32;
-    const int m = lane & 15, kb = lane >> 4, nv = N >> 3, ng = N / group;
-    float *red = (float *)lds_mvq;                          // [4 waves][32 rows][32 tokens]
-    uint16_t *sc_lds = (uint16_t *)(red + 4 * 32 * 32);     // [32 rows][ng] group scales of the block
-    // the wave's columns: a quarter of the groups
-    const int g_lo = wave * ng / 4, g_hi = (wave + 1) * ng / 4;
-    const int k_lo = g_lo * group, k_hi = g_hi * group;
-    const int8_t *wr[2];
-    const _Float16 *xr[4];
+    const int r0 = blockIdx.x * MQ_MB, t0 = blockIdx.y * MQ_TB;
+    const int m = lane & 15, kb = lane >> 4, nv = N >> 3, ng = N / group, nks = N >> 5;
+    const int nslab = ((N + MQ_KS - 1) / MQ_KS + 1) & ~1;
+
+    // staging: thread (row sr, part sp) takes 32 columns of a slab, which lie
+    // in one group (slabs and parts start at multiples of 32, groups are
+    // multiples of 32)
+    const int sr = threadIdx.x >> 2, sp = threadIdx.x & 3;
+    const size_t grow = (size_t)min(r0 + sr, M - 1);
+    const uint8_t *wrow = (const uint8_t *)mt.W + grow * mt.rowbytes;
+    const uint16_t *srow = mt.ws + grow * ng;
+    constexpr int WB = BITS == 8 ? 8 : 4;        // bytes per load, 4 loads = 32 values
+    constexpr int DA = 2;                        // slabs of raw weights in flight
+    unsigned raw_r[DA][4][2];
+    uint16_t sraw_r[DA];
+    auto load_raw = [&](unsigned (&raw)[4][2], uint16_t &sraw, int sl) {
+        const int k = min(sl * MQ_KS + 32 * sp, N - 32);   // past N: any valid columns, staged as zeros
+        const uint8_t *p = wrow + (size_t)k * BITS / 8;
 #pragma unroll
-    for (int i = 0; i < 2; i++) wr[i] = W + (size_t)min(o0 + i * 16 + m, M - 1) * rowbytes;
-#pragma unroll
-    for (int j = 0; j < 4; j++) xr[j] = xs + (size_t)min(t0 + j * 8 + (m >> 1), T - 1) * nv * 16 + (m & 1) * 8;
-    auto load = [&](half8v (&a)[2], half8v (&b)[4], int k0) {
-#pragma unroll
-        for (int i = 0; i < 2; i++) a[i] = q8_of<BITS>(wr[i], k0 + kb * 8);
-#pragma unroll
-        for (int j = 0; j < 4; j++) b[j] = *(const half8v *)(xr[j] + (size_t)((k0 >> 3) + kb) * 16);
+        for (int q = 0; q < 4; q++) {
+            if (BITS == 8) {
+                const uint2 v = *(const uint2 *)(p + q * WB);
+                raw[q][0] = v.x;
+                raw[q][1] = v.y;
+            } else {
+                raw[q][0] = *(const unsigned *)(p + q * WB);
+                raw[q][1] = 0u;
+            }
+        }
+        sraw = srow[k / group];                            // (tested at the store: no wait here)
     };
-    constexpr int RING = 4;                                 // slices in flight: RING - 1 ahead
-    half8v A[RING][2], B[RING][4];
+    auto store_raw = [&](const unsigned (&raw)[4][2], uint16_t sraw, int buf, int sl) {
+        _Float16 *dh = As + (size_t)(2 * buf) * MQ_PLANE + sr * MQ_LDA + 32 * sp;
+        const float sc = sl * MQ_KS + 32 * sp < N ? f16_keep(sraw) : 0.0f;   // past N: zeros
 #pragma unroll
-    for (int u = 0; u < RING - 1; u++)
-        if (k_lo + 32 * u < k_hi) load(A[u], B[u], k_lo + 32 * u);
-    for (int q = threadIdx.x; q < 32 * ng; q += 256) sc_lds[q] = ws[(size_t)min(o0 + q / ng, M - 1) * ng + q % ng];
+        for (int q = 0; q < 4; q++) {
+            half8 h, l;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int v = BITS == 8 ? (int)(int8_t)((raw[q][i >> 2] >> (8 * (i & 3))) & 0xFFu)
+                                        : (int)((raw[q][0] >> (4 * i)) & 0xFu) - 8;
+                const float qs = __fmul_rn((float)v, sc);       // exact
+                h[i] = (_Float16)qs;
+                l[i] = (_Float16)__fsub_rn(qs, (float)h[i]);    // exact
+            }
+            *(half8 *)(dh + 8 * q) = h;
+            *(half8 *)(dh + MQ_PLANE + 8 * q) = l;
+        }
+    };
+
+    // x of this wave's two column tiles: token 8 j + m / 2, half m % 2
+    const half8 *xr[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+        xr[j] = xs + (size_t)min(t0 + 16 * wave + 8 * j + (m >> 1), T - 1) * nv * 2 + (m & 1);
+    constexpr int RB = 4 * DA;                   // x steps in flight
+    half8 bq[RB][2];
+    auto load_b = [&](half8 (&b)[2], int ks) {
+        const int p = min(ks, nks - 1) * 4 + kb;
+#pragma unroll
+        for (int j = 0; j < 2; j++) b[j] = xr[j][(size_t)p * 2];
+    };
+
+#pragma unroll
+    for (int d = 0; d < DA; d++) load_raw(raw_r[d], sraw_r[d], d);
+#pragma unroll
+    for (int u = 0; u < RB; u++) load_b(bq[u], u);
+    store_raw(raw_r[0], sraw_r[0], 0, 0);
+    load_raw(raw_r[0], sraw_r[0], DA);                     // the slot refilled with slab DA
     __syncthreads();
-    const uint16_t *scw = sc_lds + (size_t)(4 * kb) * ng;
-    f4 acc[2][4], part[2][4];
+
+    f4 acc[4][2];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = part[i][j] = f4{0.f, 0.f, 0.f, 0.f};
-    int g = g_lo, gend = k_lo + group;
-    for (int kc = k_lo; kc < k_hi; kc += 32 * RING) {
+        for (int j = 0; j < 2; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+    // slab sl (d = sl % DA): its 4 steps from LDS buffer d with x from ring
+    // slots 4 d .. 4 d + 3; then slab sl + 1's raw weights (ring slot
+    // 1 - d) go to the other buffer, which nobody reads until the barrier,
+    // and that slot is refilled with slab sl + 1 + DA
+    auto slab = [&](int sl, auto dc) {
+        constexpr int d = decltype(dc)::value;
+        const _Float16 *a_base = As + (size_t)(2 * d) * MQ_PLANE + m * MQ_LDA + 8 * kb;
 #pragma unroll
-        for (int u = 0; u < RING; u++) {
-            const int k0 = kc + 32 * u;
-            if (k0 < k_hi) {                                // uniform
-                if (k0 + 32 * (RING - 1) < k_hi)
-                    load(A[(u + RING - 1) % RING], B[(u + RING - 1) % RING], k0 + 32 * (RING - 1));
+        for (int u = 0; u < 4; u++) {
+            const int ks = sl * 4 + u;
+            half8 ah[4], al[4];
 #pragma unroll
-                for (int i = 0; i < 2; i++)
+            for (int i = 0; i < 4; i++) {
+                ah[i] = *(const half8 *)(a_base + 16 * i * MQ_LDA + 32 * u);
+                al[i] = *(const half8 *)(a_base + MQ_PLANE + 16 * i * MQ_LDA + 32 * u);
+            }
+            half8 b[2] = {bq[4 * d + u][0], bq[4 * d + u][1]};
+            load_b(bq[4 * d + u], ks + RB);
 #pragma unroll
-                    for (int j = 0; j < 4; j++)
-                        part[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[u][i], B[u][j], part[i][j], 0, 0, 0);
-                if (k0 + 32 == gend) {                      // uniform: the group is complete
-                    // lane (kb, m) holds rows 4 kb + r of each 16-row tile
+            for (int i = 0; i < 4; i++)
 #pragma unroll
-                    for (int i = 0; i < 2; i++)
+                for (int j = 0; j < 2; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], b[j], acc[i][j], 0, 0, 0);
 #pragma unroll
-                        for (int r = 0; r < 4; r++) {
-                            const float sc = f16_keep(scw[(size_t)(i * 16 + r) * ng + g]);
+            for (int i = 0; i < 4; i++)
 #pragma unroll
-                            for (int j = 0; j < 4; j++) {
-                                acc[i][j][r] = __builtin_fmaf(sc, part[i][j][r], acc[i][j][r]);
-                                part[i][j][r] = 0.0f;
-                            }
-                        }
-                    g++;
-                    gend += group;
+                for (int j = 0; j < 2; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], b[j], acc[i][j], 0, 0, 0);
+        }
+        constexpr int dn = (d + 1) % DA;
+        store_raw(raw_r[dn], sraw_r[dn], dn, sl + 1);
+        load_raw(raw_r[dn], sraw_r[dn], sl + 1 + DA);
+        __syncthreads();
+    };
+    static_assert(DA == 2, "the slab loop below is unrolled by DA");
+    for (int sl = 0; sl < nslab; sl += DA) {
+        slab(sl, std::integral_constant<int, 0>{});
+        slab(sl + 1, std::integral_constant<int, 1>{});
+    }
+    // lane (kb, m) holds rows 4 kb + r of each 16-row tile; column m holds
+    // token m / 2, half m % 2: add the halves, remove 2^k
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int t = t0 + 16 * wave + 8 * j + (m >> 1);
+        const float xsc = xscale[min(t, T - 1)];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            f4 v;
+#pragma unroll
+            for (int r = 0; r < 4; r++) v[r] = (acc[i][j][r] + __shfl_xor(acc[i][j][r], 1)) * xsc;
+            const int row = r0 + 16 * i + 4 * kb;
+            if ((m & 1) == 0 && t < T) {
+                float *yo = mt.y + (size_t)t * M + row;
+                if (row + 3 < M && (M & 3) == 0) {
+                    *(f4 *)yo = v;
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        if (row + r < M) yo[r] = v[r];
                 }
             }
         }
     }
-    // column m holds token m / 2, half m % 2: add the halves; the quarters
-    // meet in LDS and are added in wave order, then 2^k is removed
-#pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const float v = acc[i][j][r] + __shfl_xor(acc[i][j][r], 1);
-                if ((m & 1) == 0) red[(wave * 32 + i * 16 + 4 * kb + r) * 32 + j * 8 + (m >> 1)] = v;
-            }
-    __syncthreads();
-    for (int q = threadIdx.x; q < 32 * 32; q += 256) {
-        const int o = o0 + (q >> 5), t = t0 + (q & 31);
-        if (o < M && t < T) {
-            const float v = ((red[q] + red[1024 + q]) + red[2048 + q]) + red[3072 + q];
-            y[(size_t)t * M + o] = v * xscale[t];
-        }
-    }
 }
 
-extern "C" int wk_mvq_mfma(const int8_t *W, const uint16_t *ws, size_t rowbytes, int group, int bits,
-                           const uint16_t *xs, const float *xscale, int M, int N, int T, float *y, void *stream) {
-    if (M <= 0 || N <= 0 || T <= 0 || (N % 32) || group <= 0 || (group % 32) || (N % group)) return -1;
-    if (bits == 8 && (rowbytes % 8)) return -1;
-    if (bits == 4 && (rowbytes % 4)) return -1;
-    const dim3 grid((M + 31) / 32, (T + 31) / 32);
-    const size_t lds = (size_t)4 * 32 * 32 * sizeof(float) + (size_t)32 * (N / group) * sizeof(uint16_t);
-    if (lds > 64 * 1024) return -1;
-    if (bits == 8)
-        hipLaunchKernelGGL(k_mvq_mfma<8>, grid, dim3(256), lds, (hipStream_t)stream, W, ws, rowbytes, group,
-                           (const _Float16 *)xs, xscale, M, N, T, y);
-    else if (bits == 4)
-        hipLaunchKernelGGL(k_mvq_mfma<4>, grid, dim3(256), lds, (hipStream_t)stream, W, ws, rowbytes, group,
-                           (const _Float16 *)xs, xscale, M, N, T, y);
-    else
+extern "C" int wk_mvq_gemm(int nmat, const int8_t *const *W, const uint16_t *const *ws, const size_t *rowbytes,
+                           int group, int bits, const uint16_t *xs, const float *xscale, int M, int N, int T,
+                           float *const *y, void *stream) {
+    if (nmat < 1 || nmat > 2 || M <= 0 || N < 32 || T <= 0 || (N % 32) || group <= 0 || (group % 32) ||
+        (N % group))
         return -1;
+    for (int k = 0; k < nmat; k++) {
+        if (!W[k] || !ws[k] || !y[k]) return -1;
+        if (bits == 8 && (rowbytes[k] % 8 || rowbytes[k] < (size_t)N)) return -1;
+        if (bits == 4 && (rowbytes[k] % 4 || rowbytes[k] < (size_t)N / 2)) return -1;
+    }
+    const size_t lds = (size_t)4 * MQ_PLANE * sizeof(_Float16);
+    const MvqMat a = {W[0], ws[0], rowbytes[0], y[0]};
+    const MvqMat b = nmat > 1 ? MvqMat{W[1], ws[1], rowbytes[1], y[1]} : a;
+    const dim3 grid((M + MQ_MB - 1) / MQ_MB, (T + MQ_TB - 1) / MQ_TB, nmat);
+    if (bits == 8) {
+        static bool attr = false;
+        if (!attr) {
+            hipError_t e = hipFuncSetAttribute((const void *)k_mvq_gemm<8>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               160 * 1024);
+            if (e != hipSuccess) return -(int)e - 1000;
+            attr = true;
+        }
+        hipLaunchKernelGGL(k_mvq_gemm<8>, grid, dim3(256), lds, (hipStream_t)stream, a, b, group,
+                           (const half8 *)xs, xscale, M, N, T);
+    } else if (bits == 4) {
+        static bool attr = false;
+        if (!attr) {
+            hipError_t e = hipFuncSetAttribute((const void *)k_mvq_gemm<4>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               160 * 1024);
+            if (e != hipSuccess) return -(int)e - 1000;
+            attr = true;
+        }
+        hipLaunchKernelGGL(k_mvq_gemm<4>, grid, dim3(256), lds, (hipStream_t)stream, a, b, group,
+                           (const half8 *)xs, xscale, M, N, T);
+    } else {
+        return -1;
+    }
     CHECK_LAUNCH();
     return 0;
 }

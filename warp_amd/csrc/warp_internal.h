@@ -75,11 +75,14 @@ typedef struct {
 int wk_split(const float *x, int T, int N, uint16_t *xs, float *xscale, void *stream);
 
 /* Batched quantised rows on the matrix cores (Q8G and Q4G with groups of a
- * multiple of 32, N a multiple of the group): y [T][M] = dequant(W) . x, x
- * given split as [T][N/8][2][8] fp16 with xscale [T] (wk_split). Returns -1
- * for shapes it does not take (the caller uses wk_mvq). */
-int wk_mvq_mfma(const int8_t *W, const uint16_t *ws, size_t rowbytes, int group, int bits,
-                const uint16_t *xs, const float *xscale, int M, int N, int T, float *y, void *stream);
+ * multiple of 32, N a multiple of the group, every scale finite and below
+ * 256 in magnitude, which the caller checks): y_k [T][M] = dequant(W_k) . x
+ * for nmat (1 or 2) matrices of one shape sharing x, x given split as
+ * [T][N/8][2][8] fp16 with xscale [T] (wk_split). Returns -1 for shapes it
+ * does not take (the caller uses wk_mvq). */
+int wk_mvq_gemm(int nmat, const int8_t *const *W, const uint16_t *const *ws, const size_t *rowbytes, int group,
+                int bits, const uint16_t *xs, const float *xscale, int M, int N, int T, float *const *y,
+                void *stream);
 
 /* Router logits [T][E] = W [E][H] . x [T][H]. strict = 1 reproduces the
  * reference's sequential, unfused fp32 sum (dotf on x86); 0 is a parallel
