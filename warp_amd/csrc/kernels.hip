@@ -2577,12 +2577,6 @@ extern "C" int wk_apply_p6(const warp_job *jobs, const int *njobs, int max_jobs,
 // A pair (t, k) is computed when it is token t's first pick of its expert
 // and its weight is not 0 (moe_chunk takes the first pick's weight and
 // skips 0, src/model.c:3631-3636); the others get slot -1.
-__device__ __forceinline__ bool pair_valid(const int *pid, const float *w, int t, int k, int K) {
-    const int e = pid[t * K + k];
-    for (int k2 = 0; k2 < k; k2++)
-        if (pid[t * K + k2] == e) return false;
-    return w[t * K + k] != 0.0f;
-}
 
 // Exclusive prefix sum of v over the block (blockDim a multiple of 64, at
 // most 1024 threads); *total gets the block's sum. tmp: 16 ints of LDS.
@@ -2601,6 +2595,30 @@ __device__ __forceinline__ int block_scan_excl(int v, int *tmp, int &total) {
     for (int w = 0; w < nw; w++) {
         const int t = tmp[w];
         base += w < wave ? t : 0;
+        tot += t;
+    }
+    __syncthreads();
+    total = tot;
+    return base + x - v;
+}
+
+// The same for a 64-bit value (three 21-bit counters packed in one: one
+// scan instead of three). tmp: 16 64-bit words of LDS.
+__device__ __forceinline__ unsigned long long block_scan_excl64(unsigned long long v, unsigned long long *tmp,
+                                                                unsigned long long &total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    unsigned long long x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const unsigned lo = __shfl_up((unsigned)x, o), hi = __shfl_up((unsigned)(x >> 32), o);
+        if (lane >= o) x += ((unsigned long long)hi << 32) | lo;
+    }
+    if (lane == 63) tmp[wave] = x;
+    __syncthreads();
+    unsigned long long base = 0, tot = 0;
+    for (int w = 0; w < nw; w++) {
+        const unsigned long long t = tmp[w];
+        base += w < wave ? t : 0ull;
         tot += t;
     }
     __syncthreads();
@@ -2630,43 +2648,84 @@ __global__ __launch_bounds__(1024) void k_plan_chunk(const int *__restrict__ idx
     int *run0 = tile0 + E;                          // [E] place of the expert's first full run
     int *runr = run0 + E;                           // [E] place of its last, partial run
     unsigned *bm = (unsigned *)(runr + E);          // [E][NW] when bitmaps
-    for (int q = threadIdx.x; q < P; q += blockDim.x) pid[q] = idx[q];
+    unsigned char *pv = (unsigned char *)(bm + (bitmaps ? E * NW : 0));   // [P] pair computed
+    // Up to PPT pairs per thread: their picks and weights loaded at once
+    // (clamped, so no load waits on another) and the weights kept in
+    // registers for the pair loops below; larger batches loop.
+    constexpr int PPT = 8;
+    const bool regs = P <= PPT * 1024;              // uniform (blockDim 1024)
+    float wr[PPT];
+    if (regs) {
+        int ir[PPT];
+#pragma unroll
+        for (int i = 0; i < PPT; i++) {
+            const int q = min((int)threadIdx.x + i * 1024, P - 1);
+            ir[i] = idx[q];
+            wr[i] = w[q];
+        }
+#pragma unroll
+        for (int i = 0; i < PPT; i++)
+            if ((int)threadIdx.x + i * 1024 < P) pid[threadIdx.x + i * 1024] = ir[i];
+    } else {
+        for (int q = threadIdx.x; q < P; q += blockDim.x) pid[q] = idx[q];
+    }
     for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[e] = 0;
     if (bitmaps)
         for (int i = threadIdx.x; i < E * NW; i += blockDim.x) bm[i] = 0u;
     __syncthreads();
-    for (int q = threadIdx.x; q < P; q += blockDim.x) {
-        const int t = q / K, k = q - t * K;
-        if (pair_valid(pid, w, t, k, K)) {
-            atomicAdd(&cnt[pid[q]], 1);
-            if (bitmaps) atomicOr(&bm[pid[q] * NW + (t >> 5)], 1u << (t & 31));
+    // each pair's test once (no earlier pick of the token has its expert,
+    // and its weight is not 0), kept in LDS for the loops below
+    auto count_pair = [&](int q, float wq) {
+        const int t = q / K, k = q - t * K, e = pid[q];
+        bool v = wq != 0.0f;
+        for (int k2 = 0; k2 < k; k2++) v &= pid[t * K + k2] != e;
+        pv[q] = v;
+        if (v) {
+            atomicAdd(&cnt[e], 1);
+            if (bitmaps) atomicOr(&bm[e * NW + (t >> 5)], 1u << (t & 31));
         }
+    };
+    if (regs) {
+#pragma unroll
+        for (int i = 0; i < PPT; i++)
+            if ((int)threadIdx.x + i * 1024 < P) count_pair(threadIdx.x + i * 1024, wr[i]);
+    } else {
+        for (int q = threadIdx.x; q < P; q += blockDim.x) count_pair(q, w[q]);
     }
     __syncthreads();
     // per expert, in parallel: pair offset, first job, and the places of
     // its runs -- heaviest first: every full run of WARP_RUN_J jobs, then the
     // partial runs by their job count down to 1 (the launch hands units to
     // waves round-robin, so the long ones start first)
-    __shared__ int sc_tmp[16];
+    __shared__ unsigned long long sc_tmp[16];
     __shared__ int miss_s;
     if (threadIdx.x == 0) miss_s = 0;
     int carry[2 + WARP_RUN_J] = {0, 0, 0, 0, 0, 0};   // pairs, jobs, full runs, partial runs by size
+    static_assert(WARP_RUN_J == 4, "three partial-run sizes packed in one scan");
+    constexpr unsigned long long F = (1ull << 21) - 1ull;   // 21-bit fields: every sum is below P, E < 2^21
     for (int e0 = 0; e0 < E; e0 += blockDim.x) {
         const int e = e0 + threadIdx.x;
         const int c = e < E ? cnt[e] : 0, nt = (c + WARP_TPJ - 1) / WARP_TPJ, r = nt % WARP_RUN_J;
-        int tot;
-        const int pc = block_scan_excl(c, sc_tmp, tot) + carry[0];
-        const int tc = tot;
-        const int pt = block_scan_excl(nt, sc_tmp, tot) + carry[1];
-        carry[1] += tot;
-        const int pf = block_scan_excl(nt / WARP_RUN_J, sc_tmp, tot) + carry[2];
-        carry[2] += tot;
+        // pairs, jobs and full runs in one scan; the partial runs of 1, 2
+        // and 3 jobs in another
+        unsigned long long t0, t1;
+        const unsigned long long s0 =
+            block_scan_excl64((unsigned long long)c | ((unsigned long long)nt << 21) |
+                                  ((unsigned long long)(nt / WARP_RUN_J) << 42), sc_tmp, t0);
+        const unsigned long long s1 =
+            block_scan_excl64((unsigned long long)(r == 1) | ((unsigned long long)(r == 2) << 21) |
+                                  ((unsigned long long)(r == 3) << 42), sc_tmp, t1);
+        const int pc = (int)(s0 & F) + carry[0];
+        const int tc = (int)(t0 & F);
+        const int pt = (int)((s0 >> 21) & F) + carry[1];
+        carry[1] += (int)((t0 >> 21) & F);
+        const int pf = (int)(s0 >> 42) + carry[2];
+        carry[2] += (int)(t0 >> 42);
         int pr = 0;
 #pragma unroll
         for (int q = 1; q < WARP_RUN_J; q++) {
-            const int x = block_scan_excl(r == q ? 1 : 0, sc_tmp, tot);
-            if (r == q) pr = x + carry[2 + q];
-            carry[2 + q] += tot;
+            if (r == q) pr = (int)((s1 >> (21 * (q - 1))) & F) + carry[2 + q];
+            carry[2 + q] += (int)((t1 >> (21 * (q - 1))) & F);
         }
         if (e < E) {
             off[e] = offsets[e] = pc;
@@ -2699,19 +2758,19 @@ __global__ __launch_bounds__(1024) void k_plan_chunk(const int *__restrict__ idx
     }
     __syncthreads();
     // every token's K slots: its computed pairs in ascending expert id, then -1
-    for (int q = threadIdx.x; q < P; q += blockDim.x) {
+    auto place_pair = [&](int q, float wq) {
         const int t = q / K, k = q - t * K, e = pid[q];
-        const bool v = pair_valid(pid, w, t, k, K);
+        const bool v = pv[q];
         int r = 0, nv = 0, ninv = 0;
         for (int k2 = 0; k2 < K; k2++) {
-            const bool v2 = pair_valid(pid, w, t, k2, K);
+            const bool v2 = pv[t * K + k2];
             nv += v2;
             r += v2 && pid[t * K + k2] < e;
             ninv += !v2 && k2 < k;
         }
         if (!v) {
             tok_slots[q - k + nv + ninv] = -1;
-            continue;
+            return;
         }
         int pos = off[e];
         if (bitmaps) {
@@ -2721,12 +2780,19 @@ __global__ __launch_bounds__(1024) void k_plan_chunk(const int *__restrict__ idx
         } else {
             for (int t2 = 0; t2 < t; t2++)
                 for (int k2 = 0; k2 < K; k2++)
-                    if (pid[t2 * K + k2] == e && pair_valid(pid, w, t2, k2, K)) pos++;
+                    if (pid[t2 * K + k2] == e && pv[t2 * K + k2]) pos++;
         }
         pair_tok[pos] = t;
         pair_exp[pos] = e;
-        pair_w[pos] = w[q];
+        pair_w[pos] = wq;
         tok_slots[q - k + r] = pos;
+    };
+    if (regs) {
+#pragma unroll
+        for (int i = 0; i < PPT; i++)
+            if ((int)threadIdx.x + i * 1024 < P) place_pair(threadIdx.x + i * 1024, wr[i]);
+    } else {
+        for (int q = threadIdx.x; q < P; q += blockDim.x) place_pair(q, w[q]);
     }
     __syncthreads();
     if (miss_s || tiles > max_jobs) return;          // uniform
@@ -2749,16 +2815,25 @@ __global__ __launch_bounds__(1024) void k_plan_chunk(const int *__restrict__ idx
         }
         const int e = lo, i = j - tile0[e], c = cnt[e];
         const int base = off[e] + i * WARP_TPJ, n = min(WARP_TPJ, c - i * WARP_TPJ);
+        // the record and the job's tokens, each read once, all loads in flight
+        const uint8_t *rec = table[e].rec;
+        const uint2 o01 = *(const uint2 *)&table[e].off[0], o23 = *(const uint2 *)&table[e].off[2];
+        const uint4 offs = make_uint4(o01.x, o01.y, o23.x, o23.y);
+        int tk[WARP_TPJ];
+#pragma unroll
+        for (int s = 0; s < WARP_TPJ; s++) tk[s] = pair_tok[base + (s < n ? s : 0)];
+#pragma unroll
         for (int kind = 0; kind < 3; kind++) {
             warp_job *jo = jobs + (size_t)kind * max_jobs + j;
             const int soff = kind == 0 ? 0 : kind == 1 ? inter : 2 * inter;
-            jo->idx = table[e].rec + table[e].off[kind];
-            jo->scale = (const uint16_t *)(table[e].rec + table[e].off[3]) + soff;
+            jo->idx = rec + (kind == 0 ? offs.x : kind == 1 ? offs.y : offs.z);
+            jo->scale = (const uint16_t *)(rec + offs.w) + soff;
             jo->n = n;
             jo->rsv = 0;
+#pragma unroll
             for (int s = 0; s < WARP_TPJ; s++) {
                 const int slot = base + (s < n ? s : 0);
-                jo->xi[s] = kind == 2 ? slot : pair_tok[slot];
+                jo->xi[s] = kind == 2 ? slot : tk[s];
                 jo->yi[s] = slot;
             }
         }
@@ -2770,8 +2845,9 @@ extern "C" int wk_plan_chunk(const int *idx, const float *w, int T, int K, int E
                              warp_job *jobs, int max_jobs, int *njobs, int *runs, int *missing, int inter,
                              void *stream) {
     if (T <= 0 || K <= 0 || E <= 0 || max_jobs <= 0 || !runs) return -1;
-    // the picks and the per-expert tables in LDS; the token bitmaps too when they fit
-    const size_t base = ((size_t)T * K + 5 * (size_t)E) * sizeof(int);
+    // the picks, the per-expert tables and a flag per pair in LDS; the token
+    // bitmaps too when they fit
+    const size_t base = ((size_t)T * K + 5 * (size_t)E) * sizeof(int) + (size_t)T * K;
     const size_t bms = (size_t)E * ((T + 31) / 32) * sizeof(unsigned);
     if (base > 65536) return -1;
     const int bitmaps = base + bms <= 98304;
