@@ -660,6 +660,22 @@ __device__ __forceinline__ void job_ptrs(warp_job &jb, const warp_slot &sl, int 
 
 // ---- routing -----------------------------------------------------------------------
 
+// fl(...fl(fl(0 + v[0]) + v[1]) ... + v[n-1]), one thread: the values of 64
+// steps are read at once, so the adds wait for one LDS round trip per 64.
+__device__ __forceinline__ float seq_sum_lds(const float *v, int n) {
+    float s = 0.0f;
+    int e = 0;
+    for (; e + 64 <= n; e += 64) {
+        float b[64];
+#pragma unroll
+        for (int i = 0; i < 64; i++) b[i] = v[e + i];
+#pragma unroll
+        for (int i = 0; i < 64; i++) s = __fadd_rn(s, b[i]);
+    }
+    for (; e < n; e++) s = __fadd_rn(s, v[e]);
+    return s;
+}
+
 // One 256-thread block per token: the logits are read in one pass and
 // scored into LDS, then every candidate ranks itself against all others in
 // the reference's order (larger biased score first, on equal scores the
@@ -689,11 +705,7 @@ __global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits,
         mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
         for (int e = tid; e < E; e += 256) score[e] = exp_cr(__fsub_rn(score[e], mx));
         __syncthreads();
-        if (tid == 0) {
-            float s = 0.0f;                   // sequential, as the reference sums
-            for (int e = 0; e < E; e++) s = __fadd_rn(s, score[e]);
-            red[0] = s;
-        }
+        if (tid == 0) red[0] = seq_sum_lds(score, E);   // sequential, as the reference sums
         __syncthreads();
         const float s = red[0];
         for (int e = tid; e < E; e += 256) score[e] = __fdiv_rn(score[e], s);
@@ -819,11 +831,7 @@ __device__ __forceinline__ int route_pick_lds(int E, int K, int act, int renorm,
         for (int i = 1; i < NT / 64; i++) mx = fmaxf(mx, red[i]);
         for (int e = tid; e < E; e += NT) score[e] = exp_cr(__fsub_rn(score[e], mx));
         __syncthreads();
-        if (tid == 0) {
-            float s = 0.0f;                   // sequential, as the reference sums
-            for (int e = 0; e < E; e++) s = __fadd_rn(s, score[e]);
-            red[0] = s;
-        }
+        if (tid == 0) red[0] = seq_sum_lds(score, E);   // sequential, as the reference sums
         __syncthreads();
         const float s = red[0];
         for (int e = tid; e < E; e += NT) score[e] = __fdiv_rn(score[e], s);
