@@ -141,8 +141,103 @@ __global__ __launch_bounds__(1024) void k_split(const float *__restrict__ x, int
     if (threadIdx.x == 0) xscale[t] = ldexpf(1.0f, -e);
 }
 
+// One wave per row (1 or 4 rows per block) for rows of up to 64 * NP positions of
+// 8 values: the row's values stay in registers (two float4 loads per
+// position, all issued first), its max |v| is a wave reduction, and each
+// position's hi and lo halves leave as one 16-byte store each. ACT: the row
+// is act(g, u) of two inputs (the SwiGLU of a batch), optionally also
+// written to h_out. Same values as the block-per-row kernels, bit for bit
+// (the same exponent from the same maximum).
+template <int NP, bool ACT>
+__global__ __launch_bounds__(256) void k_split_w(const float *__restrict__ g, const float *__restrict__ u, int P, int N,
+                                                 int situ, float beta, float lbeta, half8 *__restrict__ xs,
+                                                 float *__restrict__ xscale, float *__restrict__ h_out) {
+    const int lane = threadIdx.x & 63, p = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (p >= P) return;                                    // uniform per wave
+    const int nv = N >> 3;
+    const float4 *gp = (const float4 *)(g + (size_t)p * N), *up = ACT ? (const float4 *)(u + (size_t)p * N) : nullptr;
+    float4 gv[NP][2], uv[NP][2];
+#pragma unroll
+    for (int j = 0; j < NP; j++) {
+        const int pos = min(lane + 64 * j, nv - 1);
+        gv[j][0] = gp[2 * pos];
+        gv[j][1] = gp[2 * pos + 1];
+        if (ACT) {
+            uv[j][0] = up[2 * pos];
+            uv[j][1] = up[2 * pos + 1];
+        }
+    }
+    float h[NP][8];
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NP; j++) {
+        const float gx[8] = {gv[j][0].x, gv[j][0].y, gv[j][0].z, gv[j][0].w, gv[j][1].x, gv[j][1].y, gv[j][1].z, gv[j][1].w};
+        const float ux[8] = {uv[j][0].x, uv[j][0].y, uv[j][0].z, uv[j][0].w, uv[j][1].x, uv[j][1].y, uv[j][1].z, uv[j][1].w};
+        const bool in = lane + 64 * j < nv;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            h[j][e] = ACT ? act_pair(gx[e], ux[e], situ, beta, lbeta) : gx[e];
+            if (in) m = fmaxf(m, fabsf(h[j][e]));
+        }
+    }
+    m = wave_max(m);
+    const int k = split_exp(m);
+    half8 *o = xs + (size_t)p * nv * 2;
+#pragma unroll
+    for (int j = 0; j < NP; j++) {
+        const int pos = lane + 64 * j;
+        if (pos < nv) {
+            half8 hi, lo;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float v = ldexpf(h[j][e], k);
+                hi[e] = (_Float16)v;
+                lo[e] = (_Float16)(v - (float)hi[e]);
+            }
+            o[2 * pos] = hi;
+            o[2 * pos + 1] = lo;
+            if (ACT && h_out) {
+                float4 *ho = (float4 *)(h_out + (size_t)p * N) + 2 * pos;
+                ho[0] = make_float4(h[j][0], h[j][1], h[j][2], h[j][3]);
+                ho[1] = make_float4(h[j][4], h[j][5], h[j][6], h[j][7]);
+            }
+        }
+    }
+    if (lane == 0) xscale[p] = ldexpf(1.0f, -k);
+}
+
+template <bool ACT>
+static int launch_split_w(const float *g, const float *u, int P, int N, int situ, float beta, float lbeta,
+                          uint16_t *xs, float *xscale, float *h_out, void *stream) {
+    const int np = (N / 8 + 63) / 64;
+    const int rpb = P >= 2048 ? 4 : 1;                    // rows per block: small batches spread over more CUs
+    const dim3 grid((P + rpb - 1) / rpb);
+#define SPLIT_W(n)                                                                                                  \
+    case n:                                                                                                         \
+        hipLaunchKernelGGL((k_split_w<n, ACT>), grid, dim3(64 * rpb), 0, (hipStream_t)stream, g, u, P, N, situ,    \
+                           beta, lbeta, (half8 *)xs, xscale, h_out);                                                \
+        break;
+    switch (np) {
+        SPLIT_W(1)
+        SPLIT_W(2)
+        SPLIT_W(3)
+        SPLIT_W(4)
+        SPLIT_W(5)
+        SPLIT_W(6)
+        SPLIT_W(7)
+        SPLIT_W(8)
+    default: return -1;
+    }
+#undef SPLIT_W
+    CHECK_LAUNCH();
+    return 0;
+}
+
 extern "C" int wk_split(const float *x, int T, int N, uint16_t *xs, float *xscale, void *stream) {
     if (T <= 0 || N <= 0 || (N & 7)) return -1;
+    // rows of up to 4096 values (and 16-byte aligned) one wave each
+    if (N <= 4096 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)xs & 15) == 0)
+        return launch_split_w<false>(x, nullptr, T, N, 0, 0.0f, 0.0f, xs, xscale, nullptr, stream);
     hipLaunchKernelGGL(k_split, dim3(T), dim3(1024), 0, (hipStream_t)stream, x, N, (_Float16 *)xs, xscale);
     CHECK_LAUNCH();
     return 0;
@@ -2441,6 +2536,8 @@ __global__ __launch_bounds__(1024) void k_act_split(const float *__restrict__ g,
 extern "C" int wk_act_split(const float *g, const float *u, int P, int I, int act_situ, float beta, float lbeta,
                             uint16_t *xs, float *xscale, float *h_out, void *stream) {
     if (P <= 0 || I <= 0 || (I & 7) || I > 16384) return -1;
+    if (I <= 4096 && (((uintptr_t)g | (uintptr_t)u | (uintptr_t)xs | (uintptr_t)h_out) & 15) == 0)
+        return launch_split_w<true>(g, u, P, I, act_situ, beta, lbeta, xs, xscale, h_out, stream);
     hipLaunchKernelGGL(k_act_split, dim3(P), dim3(1024), (size_t)I * sizeof(float), (hipStream_t)stream, g, u, I,
                        act_situ, beta, lbeta, (_Float16 *)xs, xscale, h_out);
     CHECK_LAUNCH();
@@ -2876,32 +2973,60 @@ extern "C" int wk_plan_chunk(const int *idx, const float *w, int T, int K, int E
 // Per token: the pairs of that token in ascending expert id, each weighted
 // and added in that order (moe_chunk's loop order, src/model.c:3601-3656),
 // then + add0 (the shared expert) + add1 (the caller's residual).
+// V consecutive outputs per thread (float4 when H allows). The token's
+// slots, their weights and their rows are read 8 pairs at a time, each kind
+// in one batch (clamped to pair 0, so no load waits on another), then added
+// in slot order; slots past the computed pairs are -1.
+template <int V>
 __global__ __launch_bounds__(256) void k_combine_chunk(const float *__restrict__ y, const int *__restrict__ tok_slots,
                                                        const float *__restrict__ pair_w, int T, int K, int H,
                                                        const float *__restrict__ add0, const float *__restrict__ add1,
                                                        float *__restrict__ out) {
+    typedef float vec __attribute__((ext_vector_type(V)));
     const int t = blockIdx.y;
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    const int i = (blockIdx.x * blockDim.x + threadIdx.x) * V;
     if (i >= H) return;
     const int *sl = tok_slots + (size_t)t * K;
-    float s = 0.0f;
-    for (int q = 0; q < K; q++) {
-        const int p = sl[q];
-        if (p < 0) break;                       // the token's computed pairs come first
-        const float wj = pair_w[p];
-        if (wj == 0.0f) continue;
-        s = __fadd_rn(s, __fmul_rn(wj, y[(size_t)p * H + i]));
+    vec s = {};
+    for (int q0 = 0; q0 < K; q0 += 8) {
+        int pv[8];
+        float wv[8];
+        vec yv[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) pv[j] = q0 + j < K ? sl[q0 + j] : -1;
+#pragma unroll
+        for (int j = 0; j < 8; j++) wv[j] = pair_w[max(pv[j], 0)];
+#pragma unroll
+        for (int j = 0; j < 8; j++) yv[j] = *(const vec *)(y + (size_t)max(pv[j], 0) * H + i);
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (pv[j] >= 0 && wv[j] != 0.0f)
+#pragma unroll
+                for (int c = 0; c < V; c++) s[c] = __fadd_rn(s[c], __fmul_rn(wv[j], yv[j][c]));
+        if (pv[7] < 0) break;                  // uniform: the token's computed pairs come first
     }
-    if (add0) s = __fadd_rn(s, add0[(size_t)t * H + i]);
-    if (add1) s = __fadd_rn(s, add1[(size_t)t * H + i]);
-    out[(size_t)t * H + i] = s;
+    if (add0) {
+        const vec a = *(const vec *)(add0 + (size_t)t * H + i);
+#pragma unroll
+        for (int c = 0; c < V; c++) s[c] = __fadd_rn(s[c], a[c]);
+    }
+    if (add1) {
+        const vec a = *(const vec *)(add1 + (size_t)t * H + i);
+#pragma unroll
+        for (int c = 0; c < V; c++) s[c] = __fadd_rn(s[c], a[c]);
+    }
+    *(vec *)(out + (size_t)t * H + i) = s;
 }
 
 extern "C" int wk_combine_chunk(const float *y, const int *tok_slots, const float *pair_w, int T, int K, int H,
                                 const float *add0, const float *add1, float *out, void *stream) {
     if (T <= 0 || K <= 0 || K > WARP_MAX_K || H <= 0) return -1;
-    hipLaunchKernelGGL(k_combine_chunk, dim3((H + 255) / 256, T), dim3(256), 0, (hipStream_t)stream, y, tok_slots,
-                       pair_w, T, K, H, add0, add1, out);
+    if (H % 4 == 0 && (((uintptr_t)y | (uintptr_t)add0 | (uintptr_t)add1 | (uintptr_t)out) & 15) == 0)
+        hipLaunchKernelGGL(k_combine_chunk<4>, dim3((H / 4 + 255) / 256, T), dim3(256), 0, (hipStream_t)stream, y,
+                           tok_slots, pair_w, T, K, H, add0, add1, out);
+    else
+        hipLaunchKernelGGL(k_combine_chunk<1>, dim3((H + 255) / 256, T), dim3(256), 0, (hipStream_t)stream, y,
+                           tok_slots, pair_w, T, K, H, add0, add1, out);
     CHECK_LAUNCH();
     return 0;
 }
