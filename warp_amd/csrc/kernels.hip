@@ -480,7 +480,9 @@ extern "C" int wk_shared_fast_ok(int H, const warp_shared_args *sa) {
 // Blocks [0, E): one router row each, as k_router_fast. Blocks past E: four
 // rows of the shared expert's gate and up each (one wave per row), every
 // weight load issued before x is staged in LDS, then h = act(gate, up).
-template <int BITS>
+// MC: 16-byte chunks per lane, the fewest that cover a row (no load of a
+// chunk past the row's end).
+template <int BITS, int MC>
 __global__ __launch_bounds__(256) void k_router_shared(const float *__restrict__ W, const float *__restrict__ x, int E,
                                                        int H, float *__restrict__ logits, warp_shared_args sa) {
     if ((int)blockIdx.x < E) {
@@ -489,7 +491,7 @@ __global__ __launch_bounds__(256) void k_router_shared(const float *__restrict__
         return;
     }
     extern __shared__ float xl[];
-    using Q = QRow<BITS, SH_MAXC>;
+    using Q = QRow<BITS, MC>;
     const int r = ((int)blockIdx.x - E) * 4 + (int)(threadIdx.x >> 6), rr = min(r, sa.inter - 1);
     const int nc = H / Q::WPC, ng = H / sa.group;
     Q qg, qu;
@@ -507,10 +509,23 @@ extern "C" int wk_router_shared(const float *W, const float *x, int E, int H, fl
     const dim3 grid(E + (sa->inter + 3) / 4);
     const size_t lds = (size_t)H * sizeof(float);
     if (lds > 64 * 1024) return -1;
-    if (sa->bits == 8)
-        hipLaunchKernelGGL(k_router_shared<8>, grid, dim3(256), lds, (hipStream_t)stream, W, x, E, H, logits, *sa);
-    else
-        hipLaunchKernelGGL(k_router_shared<4>, grid, dim3(256), lds, (hipStream_t)stream, W, x, E, H, logits, *sa);
+    const int mc = (H / (sa->bits == 8 ? 16 : 32) + 63) / 64;     // <= SH_MAXC (wk_shared_fast_ok)
+#define RS(b, n)                                                                                                   \
+    hipLaunchKernelGGL((k_router_shared<b, n>), grid, dim3(256), lds, (hipStream_t)stream, W, x, E, H, logits, *sa)
+    if (sa->bits == 8) {
+        if (mc <= 1) RS(8, 1);
+        else if (mc <= 2) RS(8, 2);
+        else if (mc <= 3) RS(8, 3);
+        else if (mc <= 4) RS(8, 4);
+        else RS(8, SH_MAXC);
+    } else {
+        if (mc <= 1) RS(4, 1);
+        else if (mc <= 2) RS(4, 2);
+        else if (mc <= 3) RS(4, 3);
+        else if (mc <= 4) RS(4, 4);
+        else RS(4, SH_MAXC);
+    }
+#undef RS
     CHECK_LAUNCH();
     return 0;
 }
@@ -2345,7 +2360,7 @@ extern "C" int wk_lut_reduce(const warp_job *jobs, const int *njobs, int max_job
 // the weights, the addends); only the row scale waits for its job entry.
 // SHB (8 or 4): add0 is the shared expert's down rows of this block against
 // sa.h, one wave per 4 rows, their weights loaded first.
-template <int SHB>
+template <int SHB, int MC>
 __global__ __launch_bounds__(256) void k_combine_lut(const warp_job *__restrict__ jobs2, const float *__restrict__ part,
                                                      int splits, int max_jobs, const float *__restrict__ w, int K,
                                                      int H, const float *add0, const float *add1,
@@ -2357,7 +2372,7 @@ __global__ __launch_bounds__(256) void k_combine_lut(const warp_job *__restrict_
     extern __shared__ float hl[];
     const int r0 = blockIdx.x * 16, row = threadIdx.x & 15, jq = threadIdx.x >> 4;
     const int i = min(r0 + row, H - 1);
-    using Q = QRow<SHB ? SHB : 8, 4>;
+    using Q = QRow<SHB ? SHB : 8, MC>;
     Q qd[4];
     const int snc = SHB ? sa.inter / Q::WPC : 0;
     if constexpr (SHB != 0) {
@@ -2423,16 +2438,25 @@ extern "C" int wk_combine_lut(const warp_job *jobs2, const float *part, int spli
             (size_t)d.inter * sizeof(float) > 64 * 1024)
             return -1;
         const size_t lds = (size_t)d.inter * sizeof(float);
-        if (d.bits == 8)
-            hipLaunchKernelGGL(k_combine_lut<8>, grid, dim3(256), lds, (hipStream_t)stream, jobs2, part, splits,
-                               max_jobs, w, K, H, add0, add1, missing, d, out);
-        else
-            hipLaunchKernelGGL(k_combine_lut<4>, grid, dim3(256), lds, (hipStream_t)stream, jobs2, part, splits,
-                               max_jobs, w, K, H, add0, add1, missing, d, out);
+        /* chunks per lane: the fewest that cover a shared down row */
+        const int mc = (d.inter / (d.bits == 8 ? 16 : 32) + 63) / 64;
+#define CL(b, n)                                                                                                   \
+    hipLaunchKernelGGL((k_combine_lut<b, n>), grid, dim3(256), lds, (hipStream_t)stream, jobs2, part, splits,       \
+                       max_jobs, w, K, H, add0, add1, missing, d, out)
+        if (d.bits == 8) {
+            if (mc <= 1) CL(8, 1);
+            else if (mc <= 2) CL(8, 2);
+            else CL(8, 4);
+        } else {
+            if (mc <= 1) CL(4, 1);
+            else if (mc <= 2) CL(4, 2);
+            else CL(4, 4);
+        }
+#undef CL
     } else {
         const warp_shared_args none = {};
-        hipLaunchKernelGGL(k_combine_lut<0>, grid, dim3(256), 0, (hipStream_t)stream, jobs2, part, splits, max_jobs,
-                           w, K, H, add0, add1, missing, none, out);
+        hipLaunchKernelGGL((k_combine_lut<0, 1>), grid, dim3(256), 0, (hipStream_t)stream, jobs2, part, splits,
+                           max_jobs, w, K, H, add0, add1, missing, none, out);
     }
     CHECK_LAUNCH();
     return 0;
