@@ -786,104 +786,6 @@ __device__ __forceinline__ float seq_sum_lds(const float *v, int n) {
     return s;
 }
 
-// One 256-thread block per token: the logits are read in one pass and
-// scored into LDS, then every candidate ranks itself against all others in
-// the reference's order (larger biased score first, on equal scores the
-// lower id: it scans ids upwards with strict >, src/model.c:2729-2742).
-__global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits, const float *__restrict__ bias,
-                                               int E, int K, int act, int renorm, float routed_scale,
-                                               int *__restrict__ idx, float *__restrict__ w,
-                                               const warp_slot *__restrict__ table, warp_job *__restrict__ jobs,
-                                               int *__restrict__ njobs, int *__restrict__ missing, int inter) {
-    extern __shared__ float lds_route[];
-    float *score = lds_route;             // [E]
-    float *biased = lds_route + E;        // [E], -inf once taken
-    __shared__ int sel[WARP_MAX_K];
-    __shared__ float wsel[WARP_MAX_K];
-    __shared__ float red[4];
-    const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (tid < WARP_MAX_K) { sel[tid] = 0; wsel[tid] = 0.0f; }
-    const float *lt = logits + (size_t)t * E;
-    for (int e = tid; e < E; e += 256) score[e] = lt[e];
-    __syncthreads();
-    if (act == 1) {
-        float mx = -INFINITY;
-        for (int e = tid; e < E; e += 256) mx = fmaxf(mx, score[e]);
-        mx = wave_max(mx);
-        if (lane == 0) red[wave] = mx;
-        __syncthreads();
-        mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-        for (int e = tid; e < E; e += 256) score[e] = exp_cr(__fsub_rn(score[e], mx));
-        __syncthreads();
-        if (tid == 0) red[0] = seq_sum_lds(score, E);   // sequential, as the reference sums
-        __syncthreads();
-        const float s = red[0];
-        for (int e = tid; e < E; e += 256) score[e] = __fdiv_rn(score[e], s);
-    } else {
-        for (int e = tid; e < E; e += 256) score[e] = __fdiv_rn(1.0f, __fadd_rn(1.0f, exp_cr(-score[e])));
-    }
-    __syncthreads();
-    for (int e = tid; e < E; e += 256) biased[e] = __fadd_rn(score[e], bias ? bias[e] : 0.0f);
-    __syncthreads();
-    // Rank selection: candidate e takes place r = #{e' beating e}, where e'
-    // beats e if its biased score is larger, or equal with a lower id. The
-    // first K places are the K picks of the reference's repeated strict-max
-    // scan, in its order. Values at or below -1e30 are never picked there.
-    for (int e = tid; e < E; e += 256) {
-        const float v = biased[e];
-        int r = 0;
-        for (int q = 0; q < E; q++) {
-            const float o = biased[q];
-            r += (o > v) || (o == v && q < e);
-        }
-        if (r < K && v > -1e30f) {
-            sel[r] = e;
-            wsel[r] = score[e];
-        }
-    }
-    __syncthreads();
-    if (tid == 0) {
-        if (renorm && K > 1) {
-            float s = 0.0f;
-            for (int j = 0; j < K; j++) s = __fadd_rn(s, wsel[j]);
-            const float d = __fadd_rn(s, 1e-20f);
-            for (int j = 0; j < K; j++) wsel[j] = __fdiv_rn(wsel[j], d);
-        }
-        for (int j = 0; j < K; j++) {
-            wsel[j] = __fmul_rn(wsel[j], routed_scale);
-            idx[(size_t)t * K + j] = sel[j];
-            w[(size_t)t * K + j] = wsel[j];
-        }
-    }
-    if (table) {
-        __syncthreads();
-        int miss = 0;
-        for (int j = tid; j < K; j += 256) {
-            const warp_slot sl = table[sel[j]];
-            miss |= sl.rec == nullptr;
-            for (int kind = 0; kind < 3; kind++) {
-                warp_job jb;
-                jb.idx = nullptr;
-                jb.scale = nullptr;
-                if (sl.rec) job_ptrs(jb, sl, kind, inter);
-                jb.n = 1;
-                jb.rsv = 0;
-                for (int s = 0; s < WARP_TPJ; s++) { jb.xi[s] = 0; jb.yi[s] = 0; }
-                jb.xi[0] = kind == 2 ? j : 0;
-                jb.yi[0] = j;
-                jobs[kind * K + j] = jb;
-            }
-        }
-        miss = __syncthreads_or(miss);
-        if (tid == 0) {
-            for (int kind = 0; kind < 3; kind++) njobs[kind] = miss ? 0 : K;
-            if (miss) *missing = 1;
-        }
-    }
-}
-
-// Wave-wide max / min of an int with DPP row operations: reduced into lane
-// 63 and returned to every lane (uniform).
 template <int CTRL, int ROWS>
 __device__ __forceinline__ int dpp_src(int v) {
     return __builtin_amdgcn_update_dpp(v, v, CTRL, ROWS, 0xf, false);
@@ -1152,6 +1054,7 @@ __device__ __forceinline__ void route1_block(const float *__restrict__ logits, c
     if (table) route_jobs<256>(sel, K, table_lds ? slots : table, jobs, njobs, missing, inter);
 }
 
+// One block per token (blockIdx.x); the job lists only for a single token.
 template <bool REGS>
 __global__ __launch_bounds__(256) void k_route1(const float *__restrict__ logits, const float *__restrict__ bias,
                                                 int E, int K, int act, int renorm, float routed_scale,
@@ -1159,8 +1062,9 @@ __global__ __launch_bounds__(256) void k_route1(const float *__restrict__ logits
                                                 const warp_slot *__restrict__ table, int table_lds,
                                                 warp_job *__restrict__ jobs, int *__restrict__ njobs,
                                                 int *__restrict__ missing, int inter) {
-    route1_block<REGS>(logits, bias, E, K, act, renorm, routed_scale, idx, w, table, table_lds, jobs, njobs,
-                       missing, inter);
+    const size_t t = blockIdx.x;
+    route1_block<REGS>(logits + t * E, bias, E, K, act, renorm, routed_scale, idx + t * K, w + t * K, table,
+                       table_lds, jobs, njobs, missing, inter);
 }
 
 extern "C" int wk_route(const float *logits, const float *bias, int E, int K, int T, int act, int renorm,
@@ -1168,21 +1072,15 @@ extern "C" int wk_route(const float *logits, const float *bias, int E, int K, in
                         int *njobs, int *missing, int inter, void *stream) {
     if (E <= 0 || K <= 0 || K > WARP_MAX_K || K > E || T <= 0 || E > 8192) return -1;
     if (table && T != 1) return -1;
-    if (T == 1) {
-        // the table is staged in LDS up to 2048 experts (48 KiB)
-        const int tl = table && E <= 2048;
-        const size_t lds = (size_t)2 * ((E + 1) & ~1) * sizeof(float) + (tl ? (size_t)E * sizeof(warp_slot) : 0);
-        if (E <= 512)
-            hipLaunchKernelGGL(k_route1<true>, dim3(1), dim3(256), lds, (hipStream_t)stream, logits, bias, E, K, act,
-                               renorm, routed_scale, idx, w, table, tl, jobs, njobs, missing, inter);
-        else
-            hipLaunchKernelGGL(k_route1<false>, dim3(1), dim3(256), lds, (hipStream_t)stream, logits, bias, E, K, act,
-                               renorm, routed_scale, idx, w, table, tl, jobs, njobs, missing, inter);
-        CHECK_LAUNCH();
-        return 0;
-    }
-    hipLaunchKernelGGL(k_route, dim3(T), dim3(256), (size_t)E * 2 * sizeof(float), (hipStream_t)stream, logits,
-                       bias, E, K, act, renorm, routed_scale, idx, w, table, jobs, njobs, missing, inter);
+    // one block per token; the table is staged in LDS up to 2048 experts (48 KiB)
+    const int tl = table && E <= 2048;
+    const size_t lds = (size_t)2 * ((E + 1) & ~1) * sizeof(float) + (tl ? (size_t)E * sizeof(warp_slot) : 0);
+    if (E <= 512)
+        hipLaunchKernelGGL(k_route1<true>, dim3(T), dim3(256), lds, (hipStream_t)stream, logits, bias, E, K, act,
+                           renorm, routed_scale, idx, w, table, tl, jobs, njobs, missing, inter);
+    else
+        hipLaunchKernelGGL(k_route1<false>, dim3(T), dim3(256), lds, (hipStream_t)stream, logits, bias, E, K, act,
+                           renorm, routed_scale, idx, w, table, tl, jobs, njobs, missing, inter);
     CHECK_LAUNCH();
     return 0;
 }
@@ -2400,6 +2298,8 @@ __global__ __launch_bounds__(256) void k_combine_lut(const warp_job *__restrict_
     };
     if (K <= 16 && splits <= 16) {                         // one expert per thread
         if (jq < K) expert_row(jq, lut_rowsum_n<16>(part + (size_t)jq * nrows + i, splits, stride));
+    } else if (K <= 16 && splits <= 32) {                  // the same, 32 loads in flight
+        if (jq < K) expert_row(jq, lut_rowsum_n<32>(part + (size_t)jq * nrows + i, splits, stride));
     } else {
         for (int j = jq; j < K; j += 16) expert_row(j, lut_rowsum8(part + (size_t)j * nrows + i, splits, stride));
     }
