@@ -169,7 +169,10 @@ int warp_hip_set_router(warp_hip_ctx *c, int layer, const float *w, const float 
 int warp_hip_set_router_q(warp_hip_ctx *c, int layer, int bits, int group, const int8_t *q,
                           const uint16_t *scales, size_t rowbytes, const float *bias);
 /* Shared expert (block_sparse_moe.shared_experts.{gate,up,down}_proj), quantised
- * trunk rows; inter_shared = moe_inter * n_shared. q/scales/rowbytes: gate, up, down. */
+ * trunk rows; inter_shared = moe_inter * n_shared. q/scales/rowbytes: gate, up, down.
+ * Batches of 8 tokens or more run it on the matrix cores when every scale is finite
+ * and below 256 in magnitude (checked here, on the host copies); otherwise, and for
+ * Q3G, on the vector units. Both meet the same bar. */
 int warp_hip_set_shared(warp_hip_ctx *c, int layer, int bits, int group, int inter_shared,
                         const int8_t *const q[3], const uint16_t *const scales[3],
                         const size_t rowbytes[3]);

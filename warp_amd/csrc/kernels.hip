@@ -156,7 +156,7 @@ __global__ __launch_bounds__(256) void k_split_w(const float *__restrict__ g, co
     if (p >= P) return;                                    // uniform per wave
     const int nv = N >> 3;
     const float4 *gp = (const float4 *)(g + (size_t)p * N), *up = ACT ? (const float4 *)(u + (size_t)p * N) : nullptr;
-    float4 gv[NP][2], uv[NP][2];
+    float4 gv[NP][2], uv[NP][2] = {};
 #pragma unroll
     for (int j = 0; j < NP; j++) {
         const int pos = min(lane + 64 * j, nv - 1);
