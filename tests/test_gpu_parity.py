@@ -257,3 +257,24 @@ def test_moe_chunk_shared_on_matrix_cores(bits, group, hidden, inter):
         log(f"shared expert Q{bits}G group {group}, {inter}x{hidden}: rel err {e:.2e}")
     finally:
         ctx.close()
+
+
+def test_moe_chunk_many_pairs():
+    """600 tokens x top-16 of 64 experts: 9,600 pairs, more than the grouping
+    keeps in registers (8 per thread of its 1,024), so its looping path
+    runs; routes bit-exact and outputs within the bar against the oracle."""
+    import warp_amd
+    spec = ct.Spec(hidden=64, inter=32, experts=64, top_k=16, layers=1, fmt="VQ12", seed=61, **BALANCED)
+    model = ct.build(spec)
+    ctx = open_ctx(model, max_tokens=600)
+    try:
+        warp_amd.load_container_model(ctx, model)
+        X = np.random.default_rng(67).normal(size=(600, spec.hidden)).astype(np.float32)
+        out, route, _ = ctx.moe_chunk_host(0, X)
+        ro, rr, _ = po.LayerView(model, 0).moe_chunk(X)
+        assert np.array_equal(route, rr)
+        e = rel_err(out, ro)
+        assert e <= TOL, e
+        log(f"moe_chunk of 600 tokens x top-16 of 64: routes bit-exact, rel err {e:.2e}")
+    finally:
+        ctx.close()
