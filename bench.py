@@ -842,8 +842,9 @@ def main():
                          "kernel for scaling the profiler's traffic counters)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported by this build "
-              "(the path is single-GPU; multi-GPU sharding is described in DESIGN.md)", file=sys.stderr)
+        print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported: the path runs on a "
+              "single GPU (experts would shard across GPUs by owner, with an all-to-all of token groups "
+              "for prefill; not built)", file=sys.stderr)
         sys.exit(2)
 
     if args.workload == "kimi-prefill":
