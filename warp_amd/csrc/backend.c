@@ -374,7 +374,8 @@ static int ctx_alloc(warp_hip_ctx *c)
     if (c->max_jobs < K) c->max_jobs = K;
     const size_t nvH = (size_t)H / 8, nvI = (size_t)I / 8;
     const size_t nblkH = (nvH + WARP_LUT_BLK - 1) / WARP_LUT_BLK, nblkI = (nvI + WARP_LUT_BLK - 1) / WARP_LUT_BLK;
-    DMALLOC(c, c->logits, (size_t)T * E * 4);
+    /* at least two rows: one token's scores and biased scores (wk_router_scored) */
+    DMALLOC(c, c->logits, (size_t)(T > 2 ? T : 2) * E * 4);
     DMALLOC(c, c->idx, P * 4);
     DMALLOC(c, c->w, P * 4);
     DMALLOC(c, c->jobs, (size_t)3 * c->max_jobs * sizeof(warp_job));
@@ -1370,15 +1371,20 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
      * launch (gate, up, act) and the combine (down) */
     warp_shared_args sa;
     const int fuse_shared = use_lut && shared_args(c, L, &sa) && wk_shared_fast_ok(H, &sa);
+    /* where the device routes with the expert table, the table kernel's
+     * gate/up launch does the routing itself (one launch less) */
+    const int fuse_route = use_lut && (L->resident == E || !can_fetch(c)) && wk_lut_route_ok(g->fmt, E, K, 1, 0, 2);
+    /* then, for sigmoid scores from an fp32 router, the router launch also
+     * scores (one pass less in the routing prologue) */
+    const int scored = fuse_route && !fuse_shared && L->router && !g->router_strict &&
+                       g->router_act == WARP_HIP_ROUTE_SIGMOID;
     if ((rc = timing_begin(c, 2))) return rc;
     if (fuse_shared) KRN(c, wk_router_shared(L->router, x_dev, E, H, c->logits, &sa, c->st));
+    else if (scored) KRN(c, wk_router_scored(L->router, x_dev, E, H, L->bias, c->logits, c->st));
     else KRN(c, logits_of(c, L, x_dev, 1, c->logits, c->st));
     if ((rc = timing_end(c))) return rc;
     const int n_la = lookahead_launch(c, layer, x_dev, 1);
     if (n_la < 0) return n_la;
-    /* where the device routes with the expert table, the table kernel's
-     * gate/up launch does the routing itself (one launch less) */
-    const int fuse_route = use_lut && (L->resident == E || !can_fetch(c)) && wk_lut_route_ok(g->fmt, E, K, 1, 0, 2);
     if (L->resident == E) {
         /* everything resident: route and build the jobs on the device, no
          * host round trip */
@@ -1417,7 +1423,7 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
     if (use_lut) {
         int sp_gu = 0;
         const warp_route_args ra = { c->logits, L->bias, table, E, g->router_act, g->renorm, I, g->routed_scale,
-                                     c->idx, c->w, c->jobs, c->njobs, c->missing };
+                                     c->idx, c->w, c->jobs, c->njobs, c->missing, scored };
         if ((rc = timing_begin(c, 0))) return rc;
         KRN(c, wk_vq_lut(g->fmt, c->jobs, c->njobs, K, 0, 2, L->books, L->books_x31, x_dev, 1, c->part, c->part_cap, I, H,
                          c->n_cu, NULL, 0, 0, 0.0f, 0.0f, fuse_route ? &ra : NULL, &sp_gu, c->st));

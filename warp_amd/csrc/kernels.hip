@@ -291,6 +291,28 @@ __global__ __launch_bounds__(256) void k_router_fast(const float *__restrict__ W
     if (threadIdx.x == 0) logits[blockIdx.x] = v;
 }
 
+// One token: row e's logit, then its sigmoid score and biased score with the
+// same operations as the routing's scoring pass (route_pick_lds).
+__global__ __launch_bounds__(256) void k_router_scored(const float *__restrict__ W, const float *__restrict__ x,
+                                                       int E, int H, const float *__restrict__ bias,
+                                                       float *__restrict__ out) {
+    const int e = blockIdx.x;
+    const float v = router_row_fast(W, x, E, H, e);
+    if (threadIdx.x == 0) {
+        const float sc = __fdiv_rn(1.0f, __fadd_rn(1.0f, exp_cr(-v)));
+        out[e] = sc;
+        out[E + e] = __fadd_rn(sc, bias ? bias[e] : 0.0f);
+    }
+}
+
+extern "C" int wk_router_scored(const float *W, const float *x, int E, int H, const float *bias, float *out,
+                                void *stream) {
+    if (E <= 0 || H <= 0) return -1;
+    hipLaunchKernelGGL(k_router_scored, dim3(E), dim3(256), 0, (hipStream_t)stream, W, x, E, H, bias, out);
+    CHECK_LAUNCH();
+    return 0;
+}
+
 // A batch of tokens on the matrix cores: logits[t][e] = X[t] . W[e] with
 // v_mfma_f32_16x16x4_f32 (fp32 products, fp32 sums). A block of 4 waves owns
 // 16 tokens x 16 experts; wave w sums the w-th quarter of H's 16-column
@@ -825,33 +847,38 @@ __device__ __forceinline__ int route_key(float v) {
 // 0 past the picks found; returns the number of picks (< K only when fewer
 // than K experts are pickable). want_w (uniform) false: the weights are not
 // computed and wsel is left at 0 (a block that only needs the picks).
+// scored (uniform): score and biased already hold the sigmoid scores and the
+// biased scores (k_router_scored), so the scoring pass is skipped.
 template <bool REGS, int NT>
 __device__ __forceinline__ int route_pick_lds(int E, int K, int act, int renorm, float routed_scale, float *score,
-                                              float *biased, int *sel, float *wsel, bool want_w = true) {
+                                              float *biased, int *sel, float *wsel, bool want_w = true,
+                                              bool scored = false) {
     __shared__ float red[NT / 64];
     __shared__ int np_s;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     if (tid < WARP_MAX_K) { sel[tid] = 0; wsel[tid] = 0.0f; }
     __syncthreads();
-    if (act == 1) {
-        float mx = -INFINITY;
-        for (int e = tid; e < E; e += NT) mx = fmaxf(mx, score[e]);
-        mx = wave_max(mx);
-        if (lane == 0) red[wave] = mx;
+    if (!scored) {
+        if (act == 1) {
+            float mx = -INFINITY;
+            for (int e = tid; e < E; e += NT) mx = fmaxf(mx, score[e]);
+            mx = wave_max(mx);
+            if (lane == 0) red[wave] = mx;
+            __syncthreads();
+            mx = red[0];
+            for (int i = 1; i < NT / 64; i++) mx = fmaxf(mx, red[i]);
+            for (int e = tid; e < E; e += NT) score[e] = exp_cr(__fsub_rn(score[e], mx));
+            __syncthreads();
+            if (tid == 0) red[0] = seq_sum_lds(score, E);   // sequential, as the reference sums
+            __syncthreads();
+            const float s = red[0];
+            for (int e = tid; e < E; e += NT) score[e] = __fdiv_rn(score[e], s);
+        } else {
+            for (int e = tid; e < E; e += NT) score[e] = __fdiv_rn(1.0f, __fadd_rn(1.0f, exp_cr(-score[e])));
+        }
+        for (int e = tid; e < E; e += NT) biased[e] = __fadd_rn(score[e], biased[e]);
         __syncthreads();
-        mx = red[0];
-        for (int i = 1; i < NT / 64; i++) mx = fmaxf(mx, red[i]);
-        for (int e = tid; e < E; e += NT) score[e] = exp_cr(__fsub_rn(score[e], mx));
-        __syncthreads();
-        if (tid == 0) red[0] = seq_sum_lds(score, E);   // sequential, as the reference sums
-        __syncthreads();
-        const float s = red[0];
-        for (int e = tid; e < E; e += NT) score[e] = __fdiv_rn(score[e], s);
-    } else {
-        for (int e = tid; e < E; e += NT) score[e] = __fdiv_rn(1.0f, __fadd_rn(1.0f, exp_cr(-score[e])));
     }
-    for (int e = tid; e < E; e += NT) biased[e] = __fadd_rn(score[e], biased[e]);
-    __syncthreads();
     if (wave == 0) {
         // Lane l holds the keys of ids l, l + 64, ... (REGS: all in registers,
         // E <= 512; else rescans LDS). The picks of the reference's loop (max
@@ -1748,7 +1775,7 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
         uint2 so01 = make_uint2(0u, 0u), so23 = make_uint2(0u, 0u);
         if (e < E) {
             lg = a.r.logits[e];
-            bs = a.r.bias ? a.r.bias[e] : 0.0f;
+            bs = a.r.scored ? a.r.logits[E + e] : a.r.bias ? a.r.bias[e] : 0.0f;
             srec = a.r.table[e].rec;
             so01 = *(const uint2 *)&a.r.table[e].off[0];
             so23 = *(const uint2 *)&a.r.table[e].off[2];
@@ -1774,7 +1801,7 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
         // only the block that publishes the routing needs the weights
         const bool pub = blockIdx.x == 0 && blockIdx.y == 0;
         route_pick_lds<true, LUT_NW * 64>(E, K, a.r.act, a.r.renorm, a.r.routed_scale, score, biased, r_sel, r_wsel,
-                                          pub);
+                                          pub, a.r.scored != 0);
         bool miss = false;                                 // a pick without a record (the same in every block)
         for (int j = 0; j < K; j++) miss |= slots[r_sel[j]].rec == nullptr;
         if (pub) {                                         // uniform per block

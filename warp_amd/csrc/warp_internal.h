@@ -91,6 +91,10 @@ int wk_mvq_gemm(int nmat, const int8_t *const *W, const uint16_t *const *ws, con
 #define WARP_ROUTER_MFMA_T 16
 int wk_router_logits(const float *W, const float *x, int E, int H, int T, int strict,
                      float *logits, void *stream);
+/* One token's router rows with the fast sum, then its sigmoid scores
+ * out[0..E) and biased scores out[E..2E) (score + bias, bias may be NULL), as
+ * the routing computes them: the input of warp_route_args with scored = 1. */
+int wk_router_scored(const float *W, const float *x, int E, int H, const float *bias, float *out, void *stream);
 
 /* Quantised router / dense trunk rows (Q8G, Q4G, Q3G with the reference's
  * packing): y [T][M] = dequant(W) [M][N] . x [T][N]. */
@@ -166,7 +170,9 @@ int wk_vq_runs(int fmt, const warp_job *jobs, const int *njobs, int max_jobs, co
 int wk_lut_plan(int M, int N, int max_jobs, int nkinds, int shared_x, int target_blocks,
                 size_t cap_floats, int *groups_out, int *splits_out);
 /* Routing done inside the gate/up launch of a decode step (see wk_vq_lut):
- * the arguments of wk_route with a table, for one token. */
+ * the arguments of wk_route with a table, for one token. scored = 1: logits
+ * holds the sigmoid scores [E] and the biased scores [E] (wk_router_scored),
+ * not the logits. */
 typedef struct {
     const float *logits, *bias;
     const warp_slot *table;
@@ -176,6 +182,7 @@ typedef struct {
     float *w;
     warp_job *jobs;           /* written: the lists of all three kinds */
     int *njobs, *missing;
+    int scored;
 } warp_route_args;
 int wk_vq_lut(int fmt, const warp_job *jobs, const int *njobs, int max_jobs, int kind_lo,
               int nkinds, const uint16_t *books, int books_x31, const float *x, int shared_x, float *part,
