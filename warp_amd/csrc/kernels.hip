@@ -2704,7 +2704,8 @@ __global__ __launch_bounds__(1024) void k_plan_chunk(const int *__restrict__ idx
     int *run0 = tile0 + E;                          // [E] place of the expert's first full run
     int *runr = run0 + E;                           // [E] place of its last, partial run
     unsigned *bm = (unsigned *)(runr + E);          // [E][NW] when bitmaps
-    unsigned char *pv = (unsigned char *)(bm + (bitmaps ? E * NW : 0));   // [P] pair computed
+    int *ptok = (int *)(bm + (bitmaps ? E * NW : 0));                     // [P] pair_tok, kept on chip
+    unsigned char *pv = (unsigned char *)(ptok + P);                     // [P] pair computed
     // Up to PPT pairs per thread: their picks and weights loaded at once
     // (clamped, so no load waits on another) and the weights kept in
     // registers for the pair loops below; larger batches loop.
@@ -2839,6 +2840,7 @@ __global__ __launch_bounds__(1024) void k_plan_chunk(const int *__restrict__ idx
                     if (pid[t2 * K + k2] == e && pv[t2 * K + k2]) pos++;
         }
         pair_tok[pos] = t;
+        ptok[pos] = t;
         pair_exp[pos] = e;
         pair_w[pos] = wq;
         tok_slots[q - k + r] = pos;
@@ -2877,7 +2879,7 @@ __global__ __launch_bounds__(1024) void k_plan_chunk(const int *__restrict__ idx
         const uint4 offs = make_uint4(o01.x, o01.y, o23.x, o23.y);
         int tk[WARP_TPJ];
 #pragma unroll
-        for (int s = 0; s < WARP_TPJ; s++) tk[s] = pair_tok[base + (s < n ? s : 0)];
+        for (int s = 0; s < WARP_TPJ; s++) tk[s] = ptok[base + (s < n ? s : 0)];
 #pragma unroll
         for (int kind = 0; kind < 3; kind++) {
             warp_job *jo = jobs + (size_t)kind * max_jobs + j;
@@ -2901,16 +2903,18 @@ extern "C" int wk_plan_chunk(const int *idx, const float *w, int T, int K, int E
                              warp_job *jobs, int max_jobs, int *njobs, int *runs, int *missing, int inter,
                              void *stream) {
     if (T <= 0 || K <= 0 || E <= 0 || max_jobs <= 0 || !runs) return -1;
-    // the picks, the per-expert tables and a flag per pair in LDS; the token
-    // bitmaps too when they fit
-    const size_t base = ((size_t)T * K + 5 * (size_t)E) * sizeof(int) + (size_t)T * K;
+    // the picks, the per-expert tables, each pair's token and a flag per pair
+    // in LDS; the token bitmaps too when they fit
+    const size_t base = ((size_t)2 * T * K + 5 * (size_t)E) * sizeof(int) + (size_t)T * K;
     const size_t bms = (size_t)E * ((T + 31) / 32) * sizeof(unsigned);
-    if (base > 65536) return -1;
-    const int bitmaps = base + bms <= 98304;
+    // dynamic LDS up to 152 KiB: the kernel's static shared memory takes the rest of the 160
+    constexpr size_t LDS_MAX = 152 * 1024;
+    if (base > LDS_MAX) return -1;
+    const int bitmaps = base + bms <= LDS_MAX;
     static bool attr = false;
     if (!attr) {
         hipError_t e = hipFuncSetAttribute((const void *)k_plan_chunk, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           98304);
+                                           (int)LDS_MAX);
         if (e != hipSuccess) return -(int)e - 1000;
         attr = true;
     }
