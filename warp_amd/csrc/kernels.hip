@@ -249,6 +249,7 @@ extern "C" int wk_split(const float *x, int T, int N, uint16_t *xs, float *xscal
 // in flight per thread (all issued before the first multiply-add), lane
 // partials in ascending index order, then a fixed-order block sum
 // (deterministic). Returned in thread 0.
+template <int UNR = 8>
 __device__ __forceinline__ float router_row_fast(const float *__restrict__ W, const float *__restrict__ x, int E,
                                                  int H, int row) {
     __shared__ float part[4];
@@ -258,16 +259,16 @@ __device__ __forceinline__ float router_row_fast(const float *__restrict__ W, co
     if ((H & 3) == 0) {
         const float4 *w4 = (const float4 *)w, *x4 = (const float4 *)xt;
         const int n4 = H >> 2;
-        for (int i0 = threadIdx.x; i0 < n4; i0 += 8 * 256) {
-            float4 a[8], b[8];
+        for (int i0 = threadIdx.x; i0 < n4; i0 += UNR * 256) {
+            float4 a[UNR], b[UNR];
 #pragma unroll
-            for (int k = 0; k < 8; k++) {
+            for (int k = 0; k < UNR; k++) {
                 const int i = min(i0 + k * 256, n4 - 1);
                 a[k] = w4[i];
                 b[k] = x4[i];
             }
 #pragma unroll
-            for (int k = 0; k < 8; k++) {
+            for (int k = 0; k < UNR; k++) {
                 if (i0 + k * 256 < n4) {
                     acc = __builtin_fmaf(a[k].x, b[k].x, acc);
                     acc = __builtin_fmaf(a[k].y, b[k].y, acc);
@@ -508,7 +509,9 @@ template <int BITS, int MC>
 __global__ __launch_bounds__(256) void k_router_shared(const float *__restrict__ W, const float *__restrict__ x, int E,
                                                        int H, float *__restrict__ logits, warp_shared_args sa) {
     if ((int)blockIdx.x < E) {
-        const float v = router_row_fast(W, x, E, H, blockIdx.x);
+        // as many float4 steps per thread as a row has (the same sums in the same order)
+        constexpr int UNR = BITS == 8 ? MC : (2 * MC < 8 ? 2 * MC : 8);
+        const float v = router_row_fast<UNR>(W, x, E, H, blockIdx.x);
         if (threadIdx.x == 0) logits[blockIdx.x] = v;
         return;
     }
