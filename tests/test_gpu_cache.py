@@ -222,3 +222,39 @@ def test_corrupt_record_is_refused(model):
         log(f"corrupt record refused: {ei.value}")
     finally:
         ctx.close()
+
+
+@pytest.mark.parametrize("mode", ["copy", "host"])
+@pytest.mark.parametrize("lookahead", [0, 4])
+def test_chunk_with_more_experts_than_slots(model, lookahead, mode):
+    """A chunk naming more distinct experts than the cache has slots (23
+    tokens x top-4 of 32: about 30 distinct records per layer, 8 slots): the
+    chunk runs in windows of distinct experts that fit, as the reference's
+    moe_chunk streams its experts through any cache size
+    (src/model.c:3595-3606). Bit-identical to all-resident; each distinct
+    record asked for once per layer."""
+    T = 23
+    X = np.random.default_rng(18).normal(size=(T, SPEC["hidden"])).astype(np.float32)
+    ref_ctx = resident_ctx(model)
+    try:
+        ref = [ref_ctx.moe_chunk_host(L, X) for L in range(SPEC["layers"])]
+    finally:
+        ref_ctx.close()
+    ctx = fetching_ctx(model, slots=8, lookahead=lookahead, mode=mode)
+    try:
+        got = [ctx.moe_chunk_host(L, X) for L in range(SPEC["layers"])]
+        st = ctx.cache_stats()
+    finally:
+        ctx.close()
+        if mode == "host":
+            ctx.host_free(ctx._host_pool)
+    distinct = 0
+    for L in range(SPEC["layers"]):
+        assert np.array_equal(got[L][1], ref[L][1])
+        assert np.array_equal(got[L][0].view(np.uint32), ref[L][0].view(np.uint32)), L
+        distinct += len(np.unique(ref[L][1]))
+    assert distinct > 3 * 8, distinct
+    assert st["hits"] + st["misses"] == distinct, st
+    assert st["resident"] <= 8, st
+    log(f"chunk of {T} over {distinct} distinct records with 8 slots, lookahead {lookahead}, {mode} fetch: "
+        f"bit-identical to resident; {st}")

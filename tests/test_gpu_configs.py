@@ -10,6 +10,13 @@ codes, U(0.01, 0.05) row scales).
   (token order does not change any token's result, bit for bit; each token
   equals its own single-token decode within the bar).
 
+The Kimi-Linear cases run with both routings: the reference's sigmoid and
+the softmax the configurations name (an extension the reference does not
+have; the oracle's softmax is pinned against float64 in
+test_oracle_math.py). Decode covers the table kernel, whose gate/up launch
+routes the token itself, and the decode-then-dot kernel after the routing
+launch; prefill routes each token in its own block.
+
 Only the experts routing can select get records (the rest are never read);
 their bias is lifted so that selection stays among them, as in the
 benchmark. The K3-scale miss path is covered at reduced size by
@@ -72,14 +79,18 @@ def test_config1_single_expert(fmt):
         ctx.close()
 
 
-def test_config2_kimi_layer():
+ACTS = {"sigmoid": 0, "softmax": 1}
+
+
+@pytest.mark.parametrize("act", sorted(ACTS))
+def test_config2_kimi_layer(act):
     import warp_amd
     ids = np.arange(3, 256, 8)[:24]                 # 24 experts spread over the id range
     model = lifted(dict(KIMI, fmt="VQ12", seed=2), ids, np.full(len(ids), 1.0))
-    ctx = open_ctx(model, cache_slots=len(ids))
+    ctx = open_ctx(model, cache_slots=len(ids), router_act=ACTS[act])
     try:
         warp_amd.load_container_model(ctx, model)
-        lv = po.LayerView(model, 0)
+        lv = po.LayerView(model, 0, router_act=ACTS[act])
         rng = np.random.default_rng(3)
         worst = 0.0
         for t in range(4):
@@ -99,44 +110,52 @@ def test_config2_kimi_layer():
                 worst = max(worst, e)
                 assert e <= TOL, (t, path, e)
         ctx.set_matvec_path("auto")
-        log(f"config 2: Kimi-Linear layer (E 256, top-8, Q8G g32 shared) worst rel err {worst:.2e}; routed "
+        log(f"config 2 ({act}): Kimi-Linear layer (E 256, top-8, Q8G g32 shared) worst rel err {worst:.2e}; routed "
             f"share of the output {share:.2f}; LUT vs MFMA decode max|d| {np.abs(outs['auto'] - outs['mfma']).max():.2e}")
     finally:
         ctx.close()
 
 
-def zipf_model(fmt, seed, n=48, s=1.1):
+def zipf_model(fmt, seed, n=48, s=1.1, act="sigmoid"):
     """n experts with records, biases falling with rank so that token counts
-    per expert follow a Zipf-like skew under the reference's own selection."""
+    per expert follow a Zipf-like skew under the reference's own selection
+    rule (softmax scores spread about 20x less than sigmoid ones at these
+    logits, so their bias steps are smaller by as much)."""
     ids = np.random.default_rng(seed).permutation(256)[:n]
-    lift = 1.0 + 0.06 * (np.arange(n, dtype=np.float64) + 1.0) ** -s
+    step = 0.06 if act == "sigmoid" else 0.003
+    lift = 1.0 + step * (np.arange(n, dtype=np.float64) + 1.0) ** -s
     return lifted(dict(KIMI, fmt=fmt, seed=seed), ids, lift), ids
 
 
-def test_config3_prefill_64_against_oracle():
+@pytest.mark.parametrize("act", sorted(ACTS))
+def test_config3_prefill_64_against_oracle(act):
     import warp_amd
-    model, _ = zipf_model("VQ12", 4)
-    ctx = open_ctx(model, max_tokens=64, cache_slots=48)
+    model, _ = zipf_model("VQ12", 4, act=act)
+    ctx = open_ctx(model, max_tokens=64, cache_slots=48, router_act=ACTS[act])
     try:
         warp_amd.load_container_model(ctx, model)
         X = np.random.default_rng(5).normal(size=(64, KIMI["hidden"])).astype(np.float32)
         assert routed_share(model, 0, X[0]) > 0.05
         out, route, rw = ctx.moe_chunk_host(0, X)
-        ro, rr, rrw = po.LayerView(model, 0).moe_chunk(X)
+        ro, rr, rrw = po.LayerView(model, 0, router_act=ACTS[act]).moe_chunk(X)
         assert np.array_equal(route, rr)
+        assert np.allclose(rw, rrw, rtol=1e-5, atol=0), float(np.max(np.abs(rw - rrw) / np.abs(rrw)))
         e = rel_err(out, ro)
         assert e <= TOL, e
         counts = np.bincount(route.ravel(), minlength=256)
-        log(f"config 3, 64 tokens: rel err {e:.2e}; tokens on the 5 busiest experts {sorted(counts)[-5:]}")
+        assert len(np.unique(route)) > 8, "selection did not spread over the lifted experts"
+        log(f"config 3 ({act}), 64 tokens: rel err {e:.2e}; tokens on the 5 busiest experts {sorted(counts)[-5:]}; "
+            f"{len(np.unique(route))} distinct experts")
     finally:
         ctx.close()
 
 
-def test_config3_prefill_512_properties():
+@pytest.mark.parametrize("act", sorted(ACTS))
+def test_config3_prefill_512_properties(act):
     import warp_amd
-    model, _ = zipf_model("VQ12", 6)
+    model, _ = zipf_model("VQ12", 6, act=act)
     T = 512
-    ctx = open_ctx(model, max_tokens=T, cache_slots=48)
+    ctx = open_ctx(model, max_tokens=T, cache_slots=48, router_act=ACTS[act])
     try:
         warp_amd.load_container_model(ctx, model)
         X = np.random.default_rng(7).normal(size=(T, KIMI["hidden"])).astype(np.float32)
@@ -154,7 +173,7 @@ def test_config3_prefill_512_properties():
             worst = max(worst, e)
             assert e <= TOL, (t, e)
         counts = np.bincount(route.ravel(), minlength=256)
-        log(f"config 3, 512 tokens: order-invariant bit for bit; decode vs chunk worst {worst:.2e}; "
+        log(f"config 3 ({act}), 512 tokens: order-invariant bit for bit; decode vs chunk worst {worst:.2e}; "
             f"pairs on the 5 busiest experts {sorted(counts)[-5:]} of {T * 8}")
     finally:
         ctx.close()

@@ -131,3 +131,47 @@ def test_route_rules():
     # softmax extension: same order for monotone scores, weights are probabilities
     idx, w, sc = po.route(logits, None, 2, 1, 0, 1.0)
     assert list(idx) == [1, 2] and abs(sc.sum() - 1.0) < 1e-6
+
+
+@pytest.mark.parametrize("E,K,renorm,scale,spread", [(256, 8, 0, 1.0, 3.0), (256, 8, 1, 2.5, 1.0),
+                                                     (384, 16, 1, 1.0, 0.05), (64, 4, 0, 0.7, 8.0)])
+def test_softmax_route_against_float64(E, K, renorm, scale, spread):
+    """The softmax routing extension against a float64 softmax computed here
+    (exp of the max-subtracted logits over their sum): each score within the
+    rounding of one exp, an E-term sequential fp32 sum and one division; the
+    picks are the top K of score + bias (bias selects, the weights stay
+    unbiased); the weights renormalised when asked and scaled. A base-2 exp,
+    a temperature, exp of the biased logits, biased weights or a missing
+    renormalisation each miss these bounds by orders of magnitude."""
+    rng = np.random.default_rng(E + K + renorm)
+    logits = (rng.standard_normal(E) * spread).astype(np.float32)
+    bias = (rng.standard_normal(E) * 0.02).astype(np.float32)
+    idx, w, sc = po.route(logits, bias, K, 1, renorm, scale)
+    l64 = logits.astype(np.float64)
+    p = np.exp(l64 - l64.max())
+    p /= p.sum()
+    tol = (E + 4) * 2.0 ** -24
+    assert np.all(np.abs(sc - p) <= tol * p + 2.0 ** -149), float(np.max(np.abs(sc - p) / p))
+    order = sorted(range(E), key=lambda e: (-(p[e] + float(bias[e])), e))[:K]
+    assert list(idx) == order
+    wr = p[order]
+    if renorm:
+        wr = wr / wr.sum()
+    wr = wr * scale
+    assert np.allclose(w, wr, rtol=tol + 2.0 ** -22, atol=0), float(np.max(np.abs(w - wr) / wr))
+
+
+def test_sigmoid_route_against_float64():
+    """The reference's sigmoid scores (src/model.c:2723-2725) against float64:
+    within 2 ulp of 1/(1+exp(-x)); picks the top K of score + bias."""
+    rng = np.random.default_rng(5)
+    E, K = 384, 16
+    logits = (rng.standard_normal(E) * 2).astype(np.float32)
+    bias = (rng.standard_normal(E) * 0.05).astype(np.float32)
+    idx, w, sc = po.route(logits, bias, K, 0, 1, 2.5)
+    p = 1.0 / (1.0 + np.exp(-logits.astype(np.float64)))
+    assert np.all(np.abs(sc - p) <= 4 * 2.0 ** -24 * p)
+    order = sorted(range(E), key=lambda e: (-(p[e] + float(bias[e])), e))[:K]
+    assert list(idx) == order
+    wr = p[order] / p[order].sum() * 2.5
+    assert np.allclose(w, wr, rtol=(K + 4) * 2.0 ** -24, atol=0)

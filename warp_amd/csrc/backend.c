@@ -902,6 +902,16 @@ int warp_hip_put_expert_dev(warp_hip_ctx *c, int layer, int expert, const uint8_
     if (rc) return rc;
     if (expert < 0 || expert >= c->cfg.n_experts || !rec_dev)
         return set_err(c, WARP_HIP_E_ARG, layer, expert, "expert id");
+    /* the header is checked on a host copy of its first bytes before any
+     * slot is touched: a refused record leaves the cache as it was (a
+     * record already resident for the key stays resident) */
+    uint8_t hdr[WARP_HDR_BYTES];
+    DEV(c, hipMemcpy(hdr, rec_dev, sizeof hdr, hipMemcpyDeviceToHost));
+    const int v = c->cfg.verify;
+    c->cfg.verify = 0;                 /* the payload is not on the host */
+    rc = check_record(c, hdr, layer, expert);
+    c->cfg.verify = v;
+    if (rc) return rc;
     const int key = layer * c->cfg.n_experts + expert;
     DEV(c, hipEventRecord(c->ev_before, c->st));
     DEV(c, hipStreamWaitEvent(c->cp, c->ev_before, 0));
@@ -909,21 +919,7 @@ int warp_hip_put_expert_dev(warp_hip_ctx *c, int layer, int expert, const uint8_
     if (s < 0 && (s = claim_slot(c, layer, expert)) < 0) return s;
     DEV(c, hipMemcpyAsync(c->pool + (size_t)s * c->cfg.rec_bytes, rec_dev, c->cfg.rec_bytes,
                           hipMemcpyDeviceToDevice, c->cp));
-    /* the header is checked on a host copy of its first bytes */
-    uint8_t hdr[WARP_HDR_BYTES];
-    DEV(c, hipMemcpyAsync(hdr, rec_dev, sizeof hdr, hipMemcpyDeviceToHost, c->cp));
     DEV(c, hipStreamSynchronize(c->cp));
-    const int v = c->cfg.verify;
-    c->cfg.verify = 0;                 /* the payload is not on the host */
-    rc = check_record(c, hdr, layer, expert);
-    c->cfg.verify = v;
-    if (rc) {
-        c->key_slot[key] = -1;
-        c->slot_key[s] = -1;
-        c->L[layer].resident--;
-        (void)flush_table(c);          /* the eviction, if any */
-        return rc;
-    }
     if ((rc = publish_slot(c, layer, expert, s, hdr))) return rc;
     return flush_table(c);
 }
@@ -1487,6 +1483,48 @@ int warp_hip_moe_decode_host(warp_hip_ctx *c, int layer, const float *x, float *
     return take_missing(c);
 }
 
+/* The routed experts of a chunk whose experts e_lo..e_hi (in the windowed
+ * case, the window's) are resident and held: grouping, then the matvecs of
+ * their pairs into the pair rows of yd. */
+static int chunk_experts(warp_hip_ctx *c, int layer, const float *X_dev, int T, int e_lo, int e_hi, int first)
+{
+    const warp_hip_cfg *g = &c->cfg;
+    const layer_t *L = &c->L[layer];
+    const int E = g->n_experts, K = g->top_k, H = g->hidden, I = g->inter, P = T * K;
+    const warp_slot *table = c->table_dev + (size_t)layer * E;
+    KRN(c, wait_copies(c));
+    KRN(c, wk_plan_chunk(c->idx, c->w, T, K, E, table, c->counts, c->offsets, c->pair_tok, c->pair_exp, c->pair_w,
+                         c->tok_slots, c->jobs, c->max_jobs, c->njobs, c->runs, c->missing, I, e_lo, e_hi, !first,
+                         c->st));
+    DEV(c, hipEventRecord(c->ev_before, c->st));
+    float *yk[3] = { c->yg, c->yu, c->yd };
+    if (c->P6) {
+        const size_t nvH = (size_t)H / 8, nblkH = (nvH + WARP_LUT_BLK - 1) / WARP_LUT_BLK;
+        if (first) {
+            /* per token: gate LUT at [t][0], up LUT at [t][1] */
+            KRN(c, wk_lut_p6(X_dev, T, H, books_kind(c, L, 0), c->lut8, c->lscale, c->st));
+            KRN(c, wk_lut_p6(X_dev, T, H, books_kind(c, L, 1), c->lut8 + (size_t)T * nvH * 256,
+                             c->lscale + (size_t)T * nblkH, c->st));
+        }
+        KRN(c, wk_apply_p6(c->jobs, c->njobs, c->max_jobs, 0, c->lut8, c->lscale, c->yg, I, H, c->st));
+        KRN(c, wk_apply_p6(c->jobs, c->njobs, c->max_jobs, 1, c->lut8 + (size_t)T * nvH * 256,
+                           c->lscale + (size_t)T * nblkH, c->yu, I, H, c->st));
+        KRN(c, wk_act(c->yg, c->yu, P, I, g->act_situ, g->situ_beta, g->situ_linear_beta, c->hbuf, c->st));
+        KRN(c, wk_lut_p6(c->hbuf, P, I, books_kind(c, L, 2), c->lut8d, c->lscaled, c->st));
+        KRN(c, wk_apply_p6(c->jobs, c->njobs, c->max_jobs, 2, c->lut8d, c->lscaled, c->yd, H, I, c->st));
+    } else {
+        /* by runs: each expert's records decoded once per WARP_RUN_J jobs */
+        if (first) KRN(c, wk_split(X_dev, T, H, c->xs, c->xscale, c->st));
+        KRN(c, wk_vq_runs(g->fmt, c->jobs, c->njobs, c->max_jobs, c->runs, 0, 2, L->books, c->xs, c->xscale, yk, I,
+                          H, c->st));
+        KRN(c, wk_act_split(c->yg, c->yu, P, I, g->act_situ, g->situ_beta, g->situ_linear_beta, c->xsh, c->xscaleh,
+                            NULL, c->st));
+        KRN(c, wk_vq_runs(g->fmt, c->jobs, c->njobs, c->max_jobs, c->runs, 2, 1, L->books, c->xsh, c->xscaleh, yk, H,
+                          I, c->st));
+    }
+    return 0;
+}
+
 int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *out_dev, const float *resid_dev, int T,
                        int *route, float *rw)
 {
@@ -1494,11 +1532,10 @@ int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *ou
     if (rc) return rc;
     const warp_hip_cfg *g = &c->cfg;
     const layer_t *L = &c->L[layer];
-    const int E = g->n_experts, K = g->top_k, H = g->hidden, I = g->inter;
+    const int E = g->n_experts, K = g->top_k, H = g->hidden;
     if (T < 1 || T > g->max_tokens) return set_err(c, WARP_HIP_E_ARG, layer, -1, "T = %d, max_tokens = %d", T, g->max_tokens);
     if (!L->has_books || (!L->router && !L->rq))
         return set_err(c, WARP_HIP_E_ARG, layer, -1, "layer %d has no codebooks or router", layer);
-    const warp_slot *table = c->table_dev + (size_t)layer * E;
     const int P = T * K;
 
     KRN(c, logits_of(c, L, X_dev, T, c->logits, c->st));
@@ -1518,39 +1555,35 @@ int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *ou
             if (c->h_idx[q] >= 0 && c->h_idx[q] < E) used[c->h_idx[q]] = 1;
         int n = 0;
         for (int e = 0; e < E; e++) if (used[e]) ids[n++] = e;
-        rc = ensure_selected(c, layer, ids, n);
-        free(ids);
         free(used);
+        if (n == 0) {
+            rc = chunk_experts(c, layer, X_dev, T, 0, E - 1, 1);
+        } else {
+            /* Windows of distinct experts that the cache holds at once, in
+             * ascending id: the reference streams a chunk's experts through
+             * its cache the same way, whatever the cache size
+             * (src/model.c:3595-3606). Each window is held while its
+             * matvecs run; the next window's fills wait for them. Pairs are
+             * independent, so the windows fill disjoint pair rows and the
+             * combine below sees what one window would give, bit for bit. */
+            const int win = c->n_slots < n ? c->n_slots : n;
+            if (win < 1) rc = set_err(c, WARP_HIP_E_NOSLOT, layer, ids[0], "no cache slots");
+            for (int a = 0; rc == 0 && a < n; a += win) {
+                const int b = a + win < n ? a + win : n;
+                if (a > 0) {
+                    hipError_t e = hipEventRecord(c->ev_before, c->st);
+                    if (e == hipSuccess) e = hipStreamWaitEvent(c->cp, c->ev_before, 0);
+                    if (e != hipSuccess) { rc = dev_err(c, "window order", e); break; }
+                }
+                if ((rc = ensure_selected(c, layer, ids + a, b - a)) != 0) break;
+                rc = chunk_experts(c, layer, X_dev, T, ids[a], ids[b - 1], a == 0);
+            }
+        }
+        free(ids);
         if (rc) return rc;
     } else {
         release_hold(c, layer);
-    }
-    KRN(c, wait_copies(c));
-    KRN(c, wk_plan_chunk(c->idx, c->w, T, K, E, table, c->counts, c->offsets, c->pair_tok, c->pair_exp, c->pair_w,
-                         c->tok_slots, c->jobs, c->max_jobs, c->njobs, c->runs, c->missing, I, c->st));
-    DEV(c, hipEventRecord(c->ev_before, c->st));
-    float *yk[3] = { c->yg, c->yu, c->yd };
-    if (c->P6) {
-        const size_t nvH = (size_t)H / 8, nblkH = (nvH + WARP_LUT_BLK - 1) / WARP_LUT_BLK;
-        /* per token: gate LUT at [t][0], up LUT at [t][1] */
-        KRN(c, wk_lut_p6(X_dev, T, H, books_kind(c, L, 0), c->lut8, c->lscale, c->st));
-        KRN(c, wk_lut_p6(X_dev, T, H, books_kind(c, L, 1), c->lut8 + (size_t)T * nvH * 256, c->lscale + (size_t)T * nblkH,
-                         c->st));
-        KRN(c, wk_apply_p6(c->jobs, c->njobs, c->max_jobs, 0, c->lut8, c->lscale, c->yg, I, H, c->st));
-        KRN(c, wk_apply_p6(c->jobs, c->njobs, c->max_jobs, 1, c->lut8 + (size_t)T * nvH * 256,
-                           c->lscale + (size_t)T * nblkH, c->yu, I, H, c->st));
-        KRN(c, wk_act(c->yg, c->yu, P, I, g->act_situ, g->situ_beta, g->situ_linear_beta, c->hbuf, c->st));
-        KRN(c, wk_lut_p6(c->hbuf, P, I, books_kind(c, L, 2), c->lut8d, c->lscaled, c->st));
-        KRN(c, wk_apply_p6(c->jobs, c->njobs, c->max_jobs, 2, c->lut8d, c->lscaled, c->yd, H, I, c->st));
-    } else {
-        /* by runs: each expert's records decoded once per WARP_RUN_J jobs */
-        KRN(c, wk_split(X_dev, T, H, c->xs, c->xscale, c->st));
-        KRN(c, wk_vq_runs(g->fmt, c->jobs, c->njobs, c->max_jobs, c->runs, 0, 2, L->books, c->xs, c->xscale, yk, I,
-                          H, c->st));
-        KRN(c, wk_act_split(c->yg, c->yu, P, I, g->act_situ, g->situ_beta, g->situ_linear_beta, c->xsh, c->xscaleh,
-                            NULL, c->st));
-        KRN(c, wk_vq_runs(g->fmt, c->jobs, c->njobs, c->max_jobs, c->runs, 2, 1, L->books, c->xsh, c->xscaleh, yk, H,
-                          I, c->st));
+        if ((rc = chunk_experts(c, layer, X_dev, T, 0, E - 1, 1))) return rc;
     }
     if (L->sq[0] && (rc = shared_ffn(c, L, X_dev, T))) return rc;
     KRN(c, wk_combine_chunk(c->yd, c->tok_slots, c->pair_w, T, K, H, L->sq[0] ? c->sho : NULL, resid_dev, out_dev,

@@ -2700,7 +2700,8 @@ __global__ __launch_bounds__(1024) void k_plan_chunk(const int *__restrict__ idx
                                                      float *__restrict__ pair_w, int *__restrict__ tok_slots,
                                                      warp_job *__restrict__ jobs, int max_jobs,
                                                      int *__restrict__ njobs, int *__restrict__ runs,
-                                                     int *__restrict__ missing, int inter, int bitmaps) {
+                                                     int *__restrict__ missing, int inter, int bitmaps,
+                                                     int e_lo, int e_hi, int or_missing) {
     extern __shared__ int lds_plan[];
     const int P = T * K, NW = (T + 31) >> 5;
     int *pid = lds_plan;                            // [P]
@@ -2768,7 +2769,9 @@ __global__ __launch_bounds__(1024) void k_plan_chunk(const int *__restrict__ idx
     constexpr unsigned long long F = (1ull << 21) - 1ull;   // 21-bit fields: every sum is below P, E < 2^21
     for (int e0 = 0; e0 < E; e0 += blockDim.x) {
         const int e = e0 + threadIdx.x;
-        const int c = e < E ? cnt[e] : 0, nt = (c + WARP_TPJ - 1) / WARP_TPJ, r = nt % WARP_RUN_J;
+        // every pair gets its place; jobs and runs only the window's experts
+        const int c = e < E ? cnt[e] : 0, cw = e >= e_lo && e <= e_hi ? c : 0;
+        const int nt = (cw + WARP_TPJ - 1) / WARP_TPJ, r = nt % WARP_RUN_J;
         // pairs, jobs and full runs in one scan; the partial runs of 1, 2
         // and 3 jobs in another
         unsigned long long t0, t1;
@@ -2796,7 +2799,7 @@ __global__ __launch_bounds__(1024) void k_plan_chunk(const int *__restrict__ idx
             tile0[e] = pt;
             run0[e] = pf;
             runr[e] = r ? pr : -1;            // rank among the partial runs of its size, placed below
-            if (c && !table[e].rec) miss_s = 1;
+            if (cw && !table[e].rec) miss_s = 1;
         }
         carry[0] += tc;
     }
@@ -2806,7 +2809,8 @@ __global__ __launch_bounds__(1024) void k_plan_chunk(const int *__restrict__ idx
     base[WARP_RUN_J - 1] = carry[2];
     for (int q = WARP_RUN_J - 1; q > 1; q--) base[q - 1] = base[q] + carry[2 + q];
     for (int e = threadIdx.x; e < E; e += blockDim.x) {
-        const int r = ((cnt[e] + WARP_TPJ - 1) / WARP_TPJ) % WARP_RUN_J;
+        const int cw = e >= e_lo && e <= e_hi ? cnt[e] : 0;
+        const int r = ((cw + WARP_TPJ - 1) / WARP_TPJ) % WARP_RUN_J;
 #pragma unroll
         for (int q = 1; q < WARP_RUN_J; q++)
             if (r == q) runr[e] += base[q];
@@ -2817,7 +2821,10 @@ __global__ __launch_bounds__(1024) void k_plan_chunk(const int *__restrict__ idx
         const int nj = (miss_s || tiles > max_jobs) ? 0 : tiles;
         njobs[0] = njobs[1] = njobs[2] = nj;
         njobs[3] = nj ? nrun : 0;
-        *missing = tiles > max_jobs ? 2 : miss_s ? 1 : 0;   // written every call: no clearing needed
+        // written every call (no clearing needed), except that a later window
+        // of one chunk only adds its own failure
+        const int m = tiles > max_jobs ? 2 : miss_s ? 1 : 0;
+        if (!or_missing || m) *missing = m;
     }
     __syncthreads();
     // every token's K slots: its computed pairs in ascending expert id, then -1
@@ -2862,7 +2869,7 @@ __global__ __launch_bounds__(1024) void k_plan_chunk(const int *__restrict__ idx
     if (miss_s || tiles > max_jobs) return;          // uniform
     // the runs, one thread per expert (a few entries each)
     for (int e = threadIdx.x; e < E; e += blockDim.x) {
-        const int ntile = (cnt[e] + WARP_TPJ - 1) / WARP_TPJ;
+        const int ntile = e >= e_lo && e <= e_hi ? (cnt[e] + WARP_TPJ - 1) / WARP_TPJ : 0;
         for (int i = 0; i + WARP_RUN_J <= ntile; i += WARP_RUN_J)
             runs[run0[e] + i / WARP_RUN_J] = ((tile0[e] + i) << 3) | WARP_RUN_J;
         if (ntile % WARP_RUN_J)
@@ -2907,8 +2914,8 @@ __global__ __launch_bounds__(1024) void k_plan_chunk(const int *__restrict__ idx
 extern "C" int wk_plan_chunk(const int *idx, const float *w, int T, int K, int E, const warp_slot *table,
                              int *counts, int *offsets, int *pair_tok, int *pair_exp, float *pair_w, int *tok_slots,
                              warp_job *jobs, int max_jobs, int *njobs, int *runs, int *missing, int inter,
-                             void *stream) {
-    if (T <= 0 || K <= 0 || E <= 0 || max_jobs <= 0 || !runs) return -1;
+                             int e_lo, int e_hi, int or_missing, void *stream) {
+    if (T <= 0 || K <= 0 || E <= 0 || max_jobs <= 0 || !runs || e_lo < 0 || e_hi >= E || e_lo > e_hi) return -1;
     // the picks, the per-expert tables, each pair's token and a flag per pair
     // in LDS; the token bitmaps too when they fit
     const size_t base = ((size_t)2 * T * K + 5 * (size_t)E) * sizeof(int) + (size_t)T * K;
@@ -2926,7 +2933,7 @@ extern "C" int wk_plan_chunk(const int *idx, const float *w, int T, int K, int E
     }
     hipLaunchKernelGGL(k_plan_chunk, dim3(1), dim3(1024), base + (bitmaps ? bms : 0), (hipStream_t)stream, idx, w, T,
                        K, E, table, counts, offsets, pair_tok, pair_exp, pair_w, tok_slots, jobs, max_jobs, njobs,
-                       runs, missing, inter, bitmaps);
+                       runs, missing, inter, bitmaps, e_lo, e_hi, or_missing);
     CHECK_LAUNCH();
     return 0;
 }

@@ -246,11 +246,16 @@ int wk_act(const float *g, const float *u, int P, int I, int act_situ, float bet
  * slot) written to jobs[kind*max_jobs ..], counts to njobs[0..3); the runs
  * of up to WARP_RUN_J jobs of one expert to runs, their count to njobs[3].
  * *missing is written every call: 1 when a pair's expert has no resident
- * record, 2 when the jobs exceed max_jobs, else 0. */
+ * record, 2 when the jobs exceed max_jobs, else 0 (with or_missing, only a
+ * nonzero value is written). Jobs and runs are made for the experts
+ * e_lo..e_hi only (a window of a chunk whose experts do not fit the cache
+ * at once); every pair gets its place and slot either way, so the windows
+ * of one chunk fill disjoint pair rows of one layout. */
 int wk_plan_chunk(const int *idx, const float *w, int T, int K, int E,
                   const warp_slot *table, int *counts, int *offsets, int *pair_tok,
                   int *pair_exp, float *pair_w, int *tok_slots, warp_job *jobs,
-                  int max_jobs, int *njobs, int *runs, int *missing, int inter, void *stream);
+                  int max_jobs, int *njobs, int *runs, int *missing, int inter,
+                  int e_lo, int e_hi, int or_missing, void *stream);
 /* out [T][H] = per token, sum over its pairs in ascending expert id (tok_slots)
  * of w * y[pair], then + add0 [T][H] when given. */
 int wk_combine_chunk(const float *y, const int *tok_slots, const float *pair_w, int T, int K, int H,

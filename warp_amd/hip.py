@@ -196,13 +196,17 @@ class Context:
         self._check(lib().warp_hip_put_expert_dev(self.h, layer, expert, _addr(rec_dev)))
 
     def set_fetch(self, fn):
-        """fn(layer, expert) -> bytes of one record, or None on failure."""
+        """fn(layer, expert) -> bytes of one record, or None on failure. A
+        record of any length other than rec_bytes is a failed fetch (the
+        staging slot holds exactly one record)."""
+        rec_bytes = self.cfg.rec_bytes
+
         def cb(_user, layer, expert, dst):
             try:
                 data = fn(layer, expert)
-                if data is None:
+                if data is None or len(data) != rec_bytes:
                     return -1
-                C.memmove(dst, data, len(data))
+                C.memmove(dst, data, rec_bytes)
                 return 0
             except Exception:
                 return -1
