@@ -19,11 +19,21 @@ Reported:
   roofline     the expert matvec kernel: algorithmic bytes (codes + row
                scales of the 16 selected experts) / its launch time from HIP
                events bracketing each launch, against 8 TB/s
-  cpu_baseline the reference's own CPU path (oracle/_ref, all host cores)
-               on the VQ3R twin of one K3 layer (3 x 256 entries, the same
-               3.00 bits per weight), 16 routed experts per token
+  cpu_baseline the reference's own CPU path (oracle/_ref) on the VQ3R twin
+               of a K3 layer (3 x 256 entries, the same 3.00 bits per
+               weight), 16 of 64 experts routed per token (1.06 GB of
+               records rotating through DRAM), over the host CPUs this
+               process may use (at most 16, one GPU's share of the box),
+               with a one-thread row beside it
 
-Other workloads (--workload), each printing its own JSON line:
+The default run also measures the other four configurations, each in a
+child process of its own (the same code as --workload), and carries their
+lines in "workloads": single-expert, kimi-decode, kimi-prefill, k3-miss.
+
+Workloads (--workload), each printing its own JSON line:
+  single-expert one expert's SwiGLU FFN on one token (hidden 2304,
+                intermediate 1024), rotating over 128 resident records
+                (341 MB, beyond the 256 MB MALL)
   kimi-prefill  512 tokens through a Kimi-Linear-shape MoE layer stack
                 (hidden 2304, 256 experts of intermediate 1024, top-8
                 softmax, Zipf(1.1)-skewed expert loads, 8-bit shared expert)
@@ -189,54 +199,246 @@ def run_gpu(args):
     return ms, wall, kms, kn, st
 
 
+def kernels_sha256():
+    import hashlib
+    with open(os.path.join(HERE, "warp_amd", "csrc", "kernels.hip"), "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()
+
+
 def measured_traffic(kernel):
     """HBM traffic per launch of the expert matvec from the committed counter
     summary (L2-to-memory read requests by size, write requests), when it
-    was taken on this kernel; None otherwise."""
+    was taken on this kernel from this very kernels.hip (its sha256 is
+    recorded with the counters); None otherwise, with the reason."""
     try:
         with open(TRAFFIC_FILE) as f:
             t = json.load(f)
     except (OSError, ValueError):
-        return None
+        return None, "no counter summary"
     if t.get("kernel") != kernel:
+        return None, f"counters were taken on {t.get('kernel')}"
+    if t.get("kernels_sha256") != kernels_sha256():
+        return None, "counters were taken on another build of kernels.hip"
+    return ({k: t[k]["read_bytes"] + t[k]["write_bytes"] for k in ("gate_up", "down")} | {"source": t["source"]},
+            None)
+
+
+def cpu_threads():
+    """Host CPUs for the reference's pool: those this process may run on, at
+    most 16 (one GPU's share of the GPU box's cores), or WARP_BENCH_CPU_THREADS."""
+    env = int(os.environ.get("WARP_BENCH_CPU_THREADS", "0"))
+    if env > 0:
+        return env
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def twin_dir(args, name, spec):
+    """The container of a VQ3R twin, written once per bench run into the
+    run's twin directory (shared by the child processes), or into a fresh
+    temporary directory."""
+    import container as ct
+    root = args.twin_dir or tempfile.mkdtemp(prefix="warp_twin_")
+    d = os.path.join(root, name)
+    if os.path.exists(os.path.join(d, "manifest.json")):
+        return d, False
+    log(f"bench: writing the VQ3R twin container {name} for the CPU baseline")
+    model = ct.build(spec)
+    tmp = d + ".tmp"
+    shutil.rmtree(tmp, ignore_errors=True)
+    os.makedirs(tmp)
+    ct.write(model, tmp)
+    del model
+    os.replace(tmp, d)
+    return d, not args.twin_dir
+
+
+def ref_rows(d, cache_bytes, warm, one, units, seconds, describe):
+    """The reference (oracle/_ref) on container d over cpu_threads() and over
+    one thread (half the time): warm(ref) fills its cache, one(ref, i) is
+    call i of the timed loop, each worth `units`. Returns the cpu_baseline
+    object."""
+    from oracle import pyoracle as po
+    rows = []
+    for threads, secs in ((cpu_threads(), seconds), (1, seconds / 2)):
+        ref = po.Ref(d, cache_bytes=cache_bytes, n_threads=threads)
+        used, isa = ref.threads(), ref.backend()
+        warm(ref)
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < secs:
+            one(ref, n)
+            n += 1
+        dt = time.perf_counter() - t0
+        ref.close(reset_pool=True)
+        rows.append((n * units / dt, n, dt, used, isa))
+    (v, n, dt, used, isa), (v1, n1, dt1, _, _) = rows
+    return {"value": v, "unit": describe["unit"], "cores": used, "kind": "reference", "isa": isa,
+            "sample": describe["sample"].format(n=n * units, threads=used, secs=dt, isa=isa),
+            "one_thread": {"value": v1, "cores": 1,
+                           "sample": describe["sample"].format(n=n1 * units, threads=1, secs=dt1, isa=isa)}}
+
+
+def k3_twin_spec():
+    import container as ct
+    # 64 experts of the K3 shape (1.06 GB of records), top-16 by a random
+    # router; the reference's loader requires a shared expert: Q4G g128
+    return ct.Spec(hidden=H, inter=I, experts=64, top_k=K, layers=1, fmt="VQ3R", bias=False, renorm=True,
+                   routed_scale=1.0, shared_bits=4, shared_group=128, subnormals=False, keep_codes=False, seed=99)
+
+
+def cpu_baseline(args, seconds):
+    """The reference's moe_layer on the VQ3R twin of a K3 layer."""
+    from oracle import pyoracle as po
+    if not os.path.exists(po.REF_LIB):
         return None
-    return {k: t[k]["read_bytes"] + t[k]["write_bytes"] for k in ("gate_up", "down")} | {"source": t["source"]}
+    d, own = twin_dir(args, "k3_vq3r_64", k3_twin_spec())
+    rng = np.random.default_rng(3)
+    xs = rng.standard_normal((64, H), dtype=np.float32)
+
+    def warm(ref):
+        for t in range(24):                        # the first tokens fill the reference's cache
+            ref.moe_layer(0, xs[t % 64], 64, K, H)
+
+    def one(ref, i):
+        ref.moe_layer(0, xs[i % 64], 64, K, H)
+    res = ref_rows(d, 64 * 17_000_000 + (64 << 20), warm, one, 1, seconds, {
+        "unit": "MoE-layer tokens/s",
+        "sample": "{n} decode tokens through a K3-shape layer (H 7168, I 2048, top-16 of 64 experts, 1.06 GB of "
+                  "records rotating through DRAM) in the reference's VQ3R format (3x256, 3.00 bits/weight, the "
+                  "twin of the 2x4096 format it cannot load), its own moe_layer ({isa} LUT build + gather apply) "
+                  "over {threads} threads, {secs:.1f}s; its loader requires a shared expert, so each token also "
+                  "runs a Q4G shared expert (about 8% of the bytes) that the GPU workload does not have"})
+    if own:
+        shutil.rmtree(os.path.dirname(d), ignore_errors=True)
+    return res
 
 
-def cpu_baseline(seconds):
-    """The reference's CPU path on the VQ3R twin of one K3 layer."""
+# ---- config 1: one expert's FFN, decode ----------------------------------------------------
+
+N_SINGLE = 128        # resident records the single-expert workload rotates over (341 MB)
+
+
+def run_single_expert(args):
+    """One step = one graph replay of N_SINGLE consecutive single-expert FFNs
+    (one per resident record, one token each)."""
+    import warp_amd
+    from warp_amd.device import Buf, Event, Graph
+    gate, down, scales_b, rec_bytes = kimi_rec_layout()
+    ctx = warp_amd.Context(hidden=KH, inter=KI, n_experts=N_SINGLE, top_k=1, n_layers=1, fmt="VQ12", renorm=False,
+                           routed_scale=1.0, max_tokens=1, rec_bytes=rec_bytes, cache_bytes=N_SINGLE * rec_bytes)
+    rng = np.random.Generator(np.random.PCG64(1357))
+    ctx.set_codebooks(0, 0, rng.normal(0.0, 0.02, size=(3 * S, EN, 8)).astype(np.float16).view(np.uint16))
+    for e in range(N_SINGLE):
+        sc = rng.uniform(0.01, 0.05, size=2 * KI + KH).astype(np.float16).view(np.uint16)
+        ctx.put_expert_synth(0, e, int(rng.integers(1 << 62)), sc)
+    ctx.set_matvec_path(args.matvec_path)
+    X = Buf.of(rng.standard_normal((N_SINGLE, KH), dtype=np.float32))
+    Y = Buf.empty((N_SINGLE, KH))
+
+    def body():
+        for e in range(N_SINGLE):
+            ctx.expert_ffn(0, e, X.ptr + e * KH * 4, Y.ptr + e * KH * 4)
+
+    for _ in range(args.warmup):
+        body()
+    ctx.sync()
+    graph = Graph(ctx.stream, body) if args.graph else None
+    run = graph.launch if graph else body
+    for _ in range(args.warmup):
+        run()
+    ctx.sync()
+    e0, e1 = Event(), Event()
+    log(f"bench: timing {args.steps} passes over {N_SINGLE} single-expert FFNs")
+    t0 = time.perf_counter()
+    e0.record(ctx.stream)
+    for _ in range(args.steps):
+        run()
+    e1.record(ctx.stream)
+    e1.synchronize()
+    ctx.sync()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_ms(e1)
+    ctx.set_timing(True)
+    body()
+    body()
+    ctx.sync()
+    kms, kn = ctx.get_timing()
+    ctx.set_timing(False)
+    assert np.isfinite(Y.numpy()).all(), "non-finite expert output"
+    if graph is not None:
+        graph.free()
+    ctx.close()
+    n_ffn = args.steps * N_SINGLE
+    us_ffn = ms * 1e3 / n_ffn
+    pair = 2 * gate + down + scales_b
+    b0 = 2 * gate + 2 * 2 * KI
+    b1 = down + 2 * KH
+    achieved = (kn[0] * b0 + kn[1] * b1) / ((kms[0] + kms[1]) / 1e3) / 1e9 if kn[0] and kn[1] else None
+    ffn_gbs = pair / (us_ffn * 1e-6) / 1e9
+    kernel = "k_vq_lut" if args.matvec_path == "auto" else "k_vq_mfma"
+    return {
+        "metric": "single-expert SwiGLU FFN decode tokens/s (one expert per token), 1 MI355X",
+        "value": round(n_ffn / (ms / 1e3), 1),
+        "unit": "expert-FFN tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms / args.steps, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
+        "data": "synthetic (random codes, codebooks and scales of the Kimi-Linear expert shape)",
+        "launch": (f"{N_SINGLE} FFNs captured as one HIP graph and replayed per step" if graph
+                   else "host launches"),
+        "config": {"workload": f"single routed expert SwiGLU FFN, decode batch 1, rotating over {N_SINGLE} resident "
+                               f"records ({N_SINGLE * pair / 1e6:.0f} MB)",
+                   "hidden": KH, "inter": KI, "records": N_SINGLE, "format": "RVQ 2x4096 12-bit codes (3.00 b/w)",
+                   "parallelism": "single GPU"},
+        "us_per_ffn": round(us_ffn, 3),
+        "ffn_bytes": pair,
+        "ffn_hbm_gbs": round(ffn_gbs, 1),
+        "ffn_hbm_frac": round(ffn_gbs / HBM_PEAK_GBS, 4),
+        "roofline": {"bound": "hbm", "achieved": None if achieved is None else round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": None if achieved is None else round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": kernel + " (expert matvec, gate/up and down launches)",
+                     "bytes_per_launch": {"gate_up": b0, "down": b1},
+                     "avg_launch_us": {"gate_up": round(kms[0] / max(kn[0], 1) * 1e3, 2),
+                                       "down": round(kms[1] / max(kn[1], 1) * 1e3, 2)}},
+        "published_reference_gpu": {"value_gbs": 405.3, "what": "one expert matrix [1024x2304] VQ3R (2.4 MB), "
+                                    "kernel only, on an RTX 5060 Ti (third party), docs/LEARNED.md:2910"},
+        "wall_s": round(wall, 3),
+        "cpu_baseline": None if args.no_cpu else cpu_baseline_single(args, args.cpu_seconds),
+    }
+
+
+def cpu_baseline_single(args, seconds):
+    """The reference's per-expert FFN (gate and up tables and applies, SiLU,
+    down matvec, as moe_layer runs each routed expert) on the VQ3R twin,
+    rotating over 400 records (1.07 GB)."""
     from oracle import pyoracle as po
     import container as ct
     if not os.path.exists(po.REF_LIB):
         return None
-    spec = ct.Spec(hidden=H, inter=I, experts=K, top_k=K, layers=1, fmt="VQ3R", bias=False,
-                   renorm=True, routed_scale=1.0, shared_bits=4, shared_group=128, subnormals=False,
-                   keep_codes=False, seed=99)
-    log("bench: writing the VQ3R twin container for the CPU baseline")
-    model = ct.build(spec)
-    tmp = tempfile.mkdtemp(prefix="warp_k3_twin_")
-    ct.write(model, tmp)
-    del model
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
-    ref = po.Ref(tmp, cache_bytes=2 * K * 17_000_000, n_threads=threads)
-    threads = ref.threads()
-    rng = np.random.default_rng(3)
-    x = rng.standard_normal(H, dtype=np.float32)
-    ref.moe_layer(0, x, K, K, H)                   # first token fills the reference's cache
-    n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        ref.moe_layer(0, rng.standard_normal(H, dtype=np.float32), K, K, H)
-        n += 1
-    dt = time.perf_counter() - t0
-    ref.close()
-    shutil.rmtree(tmp, ignore_errors=True)
-    return {"value": n / dt, "unit": "MoE-layer tokens/s", "cores": threads, "kind": "reference",
-            "sample": f"{n} decode tokens through one K3-shape layer (H {H}, I {I}, top-16 of 16 "
-                      f"routed experts) in the reference's VQ3R format (3x256, 3.00 bits/weight, the "
-                      f"twin of the 2x4096 format it cannot load), its own LUT build + gather apply "
-                      f"over {threads} threads, {dt:.1f}s, records cache-resident; the reference loader "
-                      f"requires a shared expert, so each token also runs a Q4G shared expert (about 8% "
-                      f"of the bytes) that the GPU workload does not have"}
+    n_rec = 400
+    spec = ct.Spec(hidden=KH, inter=KI, experts=n_rec, top_k=1, layers=1, fmt="VQ3R", renorm=False,
+                   routed_scale=1.0, shared_bits=8, shared_group=32, subnormals=False, keep_codes=False, seed=95)
+    d, own = twin_dir(args, "kimi_vq3r_400", spec)
+    x = np.random.default_rng(3).standard_normal(KH, dtype=np.float32)
+
+    def warm(ref):
+        for e in range(n_rec):
+            ref.expert_ffn(0, e, x, KH)
+
+    def one(ref, i):
+        ref.expert_ffn(0, i % n_rec, x, KH)
+    res = ref_rows(d, n_rec * 2_700_000 + (64 << 20), warm, one, 1, seconds, {
+        "unit": "expert-FFN tokens/s",
+        "sample": "{n} single-expert FFNs (H 2304, I 1024) rotating over 400 records (1.07 GB) in the reference's "
+                  "VQ3R format (3x256, 3.00 bits/weight), its own per-expert path of moe_layer ({isa} LUT builds, "
+                  "gather applies, SiLU, down matvec) over {threads} threads, {secs:.1f}s"})
+    if own:
+        shutil.rmtree(os.path.dirname(d), ignore_errors=True)
+    return res
 
 
 # ---- Kimi-Linear-shape prefill (a second workload, not the headline line) ----------------
@@ -356,7 +558,7 @@ def run_prefill(args):
                  "note": "useful FLOPs (2 x 3 x H x I per pair, plus the shared expert); the expert matvecs run "
                          "fp16 hi/lo halves of x on the matrix cores, twice the useful MFMA work"},
         "wall_s": round(wall, 3),
-        "cpu_baseline": None if args.no_cpu else cpu_baseline_prefill(args.cpu_seconds, T),
+        "cpu_baseline": None if args.no_cpu else cpu_baseline_prefill(args, args.cpu_seconds, T),
     }
 
 
@@ -488,75 +690,103 @@ def run_kimi_decode(args):
                                        "down": round(kms[1] / max(kn[1], 1) * 1e3, 2)},
                      "router_avg_us": round(kms[2] / max(kn[2], 1) * 1e3, 2)},
         "wall_s": round(wall, 3),
-        "cpu_baseline": None if args.no_cpu else cpu_baseline_kimi_decode(args.cpu_seconds),
+        "cpu_baseline": None if args.no_cpu else cpu_baseline_kimi_decode(args, args.cpu_seconds),
     }
 
 
-def cpu_baseline_kimi_decode(seconds):
-    """The reference's moe_layer on the VQ3R twin of one Kimi-Linear layer."""
-    from oracle import pyoracle as po
+def kimi_twin(args):
+    """The VQ3R twin of two Kimi-Linear-shape layers (2 x 256 records, 1.37 GB
+    rotating through DRAM), with a Q8G g32 shared expert."""
     import container as ct
-    if not os.path.exists(po.REF_LIB):
-        return None
-    spec = ct.Spec(hidden=KH, inter=KI, experts=KE, top_k=KK, layers=1, fmt="VQ3R", renorm=True,
-                   routed_scale=1.0, shared_bits=8, shared_group=32, subnormals=False, keep_codes=False, seed=97)
-    log("bench: writing the VQ3R twin container for the decode CPU baseline")
-    model = ct.build(spec)
-    tmp = tempfile.mkdtemp(prefix="warp_kimi_twin_")
-    ct.write(model, tmp)
-    del model
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
-    ref = po.Ref(tmp, cache_bytes=KE * 2_700_000 + (64 << 20), n_threads=threads)
-    threads = ref.threads()
-    rng = np.random.default_rng(3)
-    for _ in range(64):                                # fills the reference's cache
-        ref.moe_layer(0, rng.standard_normal(KH, dtype=np.float32), KE, KK, KH)
-    n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        ref.moe_layer(0, rng.standard_normal(KH, dtype=np.float32), KE, KK, KH)
-        n += 1
-    dt = time.perf_counter() - t0
-    ref.close()
-    shutil.rmtree(tmp, ignore_errors=True)
-    return {"value": n / dt, "unit": "MoE-layer tokens/s", "cores": threads, "kind": "reference",
-            "sample": f"{n} decode tokens through one Kimi-Linear-shape layer (H {KH}, I {KI}, top-8 of 256 "
-                      f"experts, Q8G shared expert) in the reference's VQ3R format (3x256, 3.00 bits/weight), its "
-                      f"own moe_layer over {threads} threads, {dt:.1f}s, records cache-resident; the reference "
-                      f"routes with sigmoid scores (softmax is not in it)"}
+    spec = ct.Spec(hidden=KH, inter=KI, experts=KE, top_k=KK, layers=2, fmt="VQ3R", renorm=True, routed_scale=1.0,
+                   shared_bits=8, shared_group=32, subnormals=False, keep_codes=False, seed=97)
+    return twin_dir(args, "kimi_vq3r_2x256", spec)
 
 
-def cpu_baseline_prefill(seconds, T):
-    """The reference's moe_chunk on the VQ3R twin of one Kimi-Linear layer."""
+KIMI_CACHE = 2 * KE * 2_700_000 + (64 << 20)
+
+
+def cpu_baseline_kimi_decode(args, seconds):
+    """The reference's moe_layer on the VQ3R twin of two Kimi-Linear layers,
+    alternating layers token by token."""
     from oracle import pyoracle as po
-    import container as ct
     if not os.path.exists(po.REF_LIB):
         return None
-    spec = ct.Spec(hidden=KH, inter=KI, experts=KE, top_k=KK, layers=1, fmt="VQ3R", renorm=True,
-                   routed_scale=1.0, shared_bits=8, shared_group=32, subnormals=False, keep_codes=False, seed=98)
-    log("bench: writing the VQ3R twin container for the prefill CPU baseline")
-    model = ct.build(spec)
-    tmp = tempfile.mkdtemp(prefix="warp_kimi_twin_")
-    ct.write(model, tmp)
-    del model
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
-    ref = po.Ref(tmp, cache_bytes=KE * 2_700_000 + (64 << 20), n_threads=threads)
-    threads = ref.threads()
-    rng = np.random.default_rng(3)
+    d, own = kimi_twin(args)
+    xs = np.random.default_rng(3).standard_normal((64, KH), dtype=np.float32)
+
+    def warm(ref):
+        for t in range(128):                       # fills the reference's cache
+            ref.moe_layer(t & 1, xs[t % 64], KE, KK, KH)
+
+    def one(ref, i):
+        ref.moe_layer(i & 1, xs[i % 64], KE, KK, KH)
+    res = ref_rows(d, KIMI_CACHE, warm, one, 1, seconds, {
+        "unit": "MoE-layer tokens/s",
+        "sample": "{n} decode tokens through two Kimi-Linear-shape layers in turn (H 2304, I 1024, top-8 of 256 "
+                  "experts, Q8G shared expert; 1.37 GB of records) in the reference's VQ3R format (3x256, 3.00 "
+                  "bits/weight), its own moe_layer ({isa}) over {threads} threads, {secs:.1f}s; the reference "
+                  "routes with sigmoid scores (softmax is not in it)"})
+    if own:
+        shutil.rmtree(os.path.dirname(d), ignore_errors=True)
+    return res
+
+
+def cpu_baseline_prefill(args, seconds, T):
+    """The reference's moe_chunk on the VQ3R twin of two Kimi-Linear layers,
+    chunks of 64 tokens (its prefill chunk, src/model.h:285), alternating
+    layers."""
+    from oracle import pyoracle as po
+    if not os.path.exists(po.REF_LIB):
+        return None
+    d, own = kimi_twin(args)
     chunk = 64
-    for _ in range(8):                                 # fills the reference's cache
-        ref.moe_chunk(0, rng.standard_normal((chunk, KH), dtype=np.float32), KK, KH)
-    n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        ref.moe_chunk(0, rng.standard_normal((chunk, KH), dtype=np.float32), KK, KH)
-        n += chunk
-    dt = time.perf_counter() - t0
-    ref.close()
-    shutil.rmtree(tmp, ignore_errors=True)
-    return {"value": n / dt, "unit": "MoE-layer tokens/s", "cores": threads, "kind": "reference",
-            "sample": f"{n} prefill tokens in chunks of {chunk} through one Kimi-Linear-shape layer (H {KH}, "
-                      f"I {KI}, top-8 of 256 experts, Q8G shared expert) in the reference's VQ3R format (3x256, "
-                      f"3.00 bits/weight), its own moe_chunk over {threads} threads, {dt:.1f}s, records "
-                      f"cache-resident; the reference routes with sigmoid scores (softmax is not in it)"}
+    Xs = np.random.default_rng(3).standard_normal((8, chunk, KH), dtype=np.float32)
+
+    def warm(ref):
+        for t in range(8):
+            ref.moe_chunk(t & 1, Xs[t], KK, KH)
+
+    def one(ref, i):
+        ref.moe_chunk(i & 1, Xs[i % 8], KK, KH)
+    res = ref_rows(d, KIMI_CACHE, warm, one, chunk, seconds, {
+        "unit": "MoE-layer tokens/s",
+        "sample": "{n} prefill tokens in chunks of 64 through two Kimi-Linear-shape layers in turn (H 2304, I 1024, "
+                  "top-8 of 256 experts, Q8G shared expert) in the reference's VQ3R format (3x256, 3.00 "
+                  "bits/weight), its own moe_chunk ({isa}) over {threads} threads, {secs:.1f}s; the reference routes "
+                  "with sigmoid scores (softmax is not in it)"})
+    if own:
+        shutil.rmtree(os.path.dirname(d), ignore_errors=True)
+    return res
+
+
+def cpu_baseline_miss(args, seconds, T):
+    """The reference's moe_chunk on the VQ3R twin of a K3 layer (64 experts)
+    with its expert cache holding half of them: a T-token batch picks about
+    all 64, so about half of every chunk's distinct records miss and are
+    read from the container (page cache) by its bank_fetch
+    (src/model.c:1767-1795, src/ecache.c:596-669)."""
+    from oracle import pyoracle as po
+    if not os.path.exists(po.REF_LIB):
+        return None
+    d, own = twin_dir(args, "k3_vq3r_64", k3_twin_spec())
+    Xs = np.random.default_rng(4).standard_normal((4, T, H), dtype=np.float32)
+
+    def warm(ref):
+        ref.moe_chunk(0, Xs[0], K, H)
+
+    def one(ref, i):
+        ref.moe_chunk(0, Xs[i % 4], K, H)
+    res = ref_rows(d, 32 * 16_600_000, warm, one, T, seconds, {
+        "unit": "MoE-layer tokens/s",
+        "sample": "{n} decode tokens in batches of " + str(T) + " through a K3-shape layer (H 7168, I 2048, top-16 "
+                  "of 64 experts) in the reference's VQ3R format, its own moe_chunk ({isa}) over {threads} "
+                  "threads, {secs:.1f}s, with its expert cache at 32 records (half of the 64 the batch picks): "
+                  "misses read from the container through its bank_fetch, served by the host's page cache, so "
+                  "this prices the CPU path's compute plus a host memory copy, not a storage read"})
+    if own:
+        shutil.rmtree(os.path.dirname(d), ignore_errors=True)
+    return res
 
 
 MISS_METRIC = "MoE-layer tokens/s with half the selected expert records missing from HBM, K3-scale, 1 MI355X"
@@ -716,9 +946,7 @@ def run_miss(args):
                           "peak_source": "best of 3 synchronous 1 GiB copies from the pinned host tier"},
         "layer_ms_bounds": {"copy_at_peak": round(copy_ms, 3), "compute_resident": res["resident"]["ms_per_layer"],
                             "measured": la["ms_per_layer"]},
-        "cpu_baseline": None,
-        "cpu_baseline_note": "not measured for this workload: its cost is the host-to-device stream, "
-                             "which the reference's CPU path does not have",
+        "cpu_baseline": None if args.no_cpu else cpu_baseline_miss(args, args.cpu_seconds, T),
     }
 
 
@@ -793,7 +1021,7 @@ def cpu_baseline_encode(seconds):
     L.waste_vq_encode.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
                                   ctypes.c_int, ctypes.c_void_p, ctypes.c_int]
     L.waste_vq_encode.restype = None
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+    threads = cpu_threads()
     rng = np.random.default_rng(98)
     m = 1 << 16
     X = rng.standard_normal((m, 8), dtype=np.float32)
@@ -813,12 +1041,19 @@ def cpu_baseline_encode(seconds):
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--workload", choices=["k3-decode", "kimi-prefill", "k3-miss", "kimi-decode", "vq-encode"],
+    ap.add_argument("--workload", choices=["k3-decode", "single-expert", "kimi-prefill", "k3-miss", "kimi-decode",
+                                           "vq-encode"],
                     default="k3-decode",
-                    help="k3-decode (the headline line), kimi-prefill (a 512-token Kimi-Linear-shape prefill) "
-                         ", k3-miss (a 32-token K3 decode batch with half its expert records streamed from host) "
-                         ", kimi-decode (Kimi-Linear-shape decode, batch 1, with its shared expert) "
-                         "or vq-encode (the encoder on one K3 matrix)")
+                    help="k3-decode (the headline line), single-expert (one expert's FFN, decode), kimi-prefill "
+                         "(a 512-token Kimi-Linear-shape prefill), k3-miss (a 32-token K3 decode batch with half its "
+                         "expert records streamed from host), kimi-decode (Kimi-Linear-shape decode, batch 1, with "
+                         "its shared expert) or vq-encode (the encoder on one K3 matrix)")
+    ap.add_argument("--only", action="store_true",
+                    help="k3-decode: the headline line alone, without the other configurations' children")
+    ap.add_argument("--twin-dir", default=None,
+                    help="directory for the CPU baselines' twin containers (shared by the children of one run)")
+    ap.add_argument("--child-timeout", type=float, default=420.0,
+                    help="seconds allowed to each other configuration's child process")
     ap.add_argument("--tokens", type=int, default=None,
                     help="tokens per step: kimi-prefill (default 512), k3-miss (default 32)")
     ap.add_argument("--cache-frac", type=float, default=0.69,
@@ -830,7 +1065,8 @@ def main():
     ap.add_argument("--layers", type=int, default=None,
                     help="layers in the stack: k3-decode 60, kimi-prefill 4, k3-miss 4, kimi-decode 26")
     ap.add_argument("--resident", type=int, default=64, help="expert records per layer kept in HBM")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="seconds of the reference's CPU path per baseline (the one-thread row gets half)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", dest="graph", action="store_false",
                     help="k3-decode, kimi-decode: launch every kernel from the host instead of replaying one "
@@ -847,6 +1083,9 @@ def main():
               "for prefill; not built)", file=sys.stderr)
         sys.exit(2)
 
+    if args.workload == "single-expert":
+        print(json.dumps(run_single_expert(args)))
+        return
     if args.workload == "kimi-prefill":
         args.layers = args.layers or 4
         args.tokens = args.tokens or 512
@@ -865,6 +1104,16 @@ def main():
         print(json.dumps(run_miss(args)))
         return
     args.layers = args.layers or 60
+    workloads = {}
+    if not args.twin_dir:
+        # one directory of twin containers for the whole run, removed at exit
+        import atexit
+        args.twin_dir = tempfile.mkdtemp(prefix="warp_bench_twins_")
+        atexit.register(shutil.rmtree, args.twin_dir, True)
+    if not args.only:
+        # the other configurations first, each in a child process, before this
+        # process touches the GPU
+        workloads = run_children(args)
     ms, wall, kms, kn, st = run_gpu(args)
     steps, layers = args.steps, args.layers
     layer_tokens = steps * layers
@@ -878,11 +1127,11 @@ def main():
     achieved = kern_bytes / (kern_ms / 1e3) / 1e9
     layer_gbs = layer_bytes() * layer_tokens / (ms / 1e3) / 1e9
     kernel = "k_vq_lut" if args.matvec_path == "auto" else "k_vq_mfma"
-    tr = measured_traffic(kernel)
+    tr, tr_why = measured_traffic(kernel)
     traffic = None
     if tr:
         traffic = round((kn[0] * tr["gate_up"] + kn[1] * tr["down"]) / max(kn[0] + kn[1], 1))
-    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+    cpu = None if args.no_cpu else cpu_baseline(args, args.cpu_seconds)
     rec = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -906,8 +1155,8 @@ def main():
         "layer_bytes": layer_bytes(),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "traffic_per_launch": None if tr is None else {"gate_up": tr["gate_up"], "down": tr["down"],
-                                                                    "source": tr["source"]},
+                     "traffic_per_launch": ({"gate_up": tr["gate_up"], "down": tr["down"], "source": tr["source"]}
+                                            if tr else {"unmeasured": tr_why}),
                      "kernel": kernel + " (expert matvec, gate/up and down launches)",
                      "timing": "HIP events around each launch on the compute stream, in a second pass of the "
                                "same steps",
@@ -918,8 +1167,46 @@ def main():
         "cache": {"hits": st["hits"], "misses": st["misses"], "resident": st["resident"]},
         "wall_s": round(wall, 3),
         "cpu_baseline": cpu,
+        "workloads": workloads,
     }
     print(json.dumps(rec))
+
+
+CHILDREN = [("single_expert", "single-expert"), ("kimi_decode", "kimi-decode"), ("kimi_prefill", "kimi-prefill"),
+            ("k3_miss", "k3-miss")]
+
+
+def run_children(args):
+    """The other four configurations, each `bench.py --workload X` in a child
+    process (its own HIP context and memory), with this run's step counts
+    and CPU-baseline seconds; a child that fails is reported, not fatal."""
+    import subprocess
+    out = {}
+    for key, wl in CHILDREN:
+        cmd = [sys.executable, os.path.abspath(__file__), "--workload", wl, "--twin-dir", args.twin_dir,
+               "--cpu-seconds", str(args.cpu_seconds), "--matvec-path", args.matvec_path]
+        if wl == "k3-miss":
+            cmd += ["--steps", "3", "--warmup", "1"]
+        else:
+            cmd += ["--steps", str(args.steps), "--warmup", str(args.warmup)]
+        if args.no_cpu:
+            cmd.append("--no-cpu")
+        if not args.graph:
+            cmd.append("--no-graph")
+        log(f"bench: configuration {wl} in a child process")
+        t0 = time.perf_counter()
+        try:
+            r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=None, text=True, timeout=args.child_timeout)
+            lines = [l for l in r.stdout.splitlines() if l.startswith("{")]
+            if r.returncode == 0 and lines:
+                out[key] = json.loads(lines[-1])
+                out[key]["child_wall_s"] = round(time.perf_counter() - t0, 1)
+            else:
+                out[key] = {"error": f"exit status {r.returncode}", "stdout_tail": r.stdout[-400:]}
+        except subprocess.TimeoutExpired:
+            out[key] = {"error": f"did not finish in {args.child_timeout:.0f}s"}
+        log(f"bench: configuration {wl}: " + ("ok" if "error" not in out[key] else out[key]["error"]))
+    return out
 
 
 if __name__ == "__main__":

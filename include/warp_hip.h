@@ -205,6 +205,14 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
  * (src/model.c:3929-3934). `routed` (may be NULL) gets the K ids. */
 int warp_hip_moe_decode_host(warp_hip_ctx *c, int layer, const float *x, float *out, int *routed);
 
+/* Replaces the per-expert part of moe_layer (src/model.c:2886-2909): one
+ * resident expert's SwiGLU FFN on one token, out_dev [H] = W_down .
+ * (act(W_gate x) * (W_up x)), unweighted, in the reference's arithmetic
+ * (the gate and up tables of x, the gather apply, SiLU/SiTU, the down
+ * table of h). No routing, no shared expert. E_MISSING if the record is not
+ * resident. Queued on the compute stream; nothing waits. */
+int warp_hip_expert_ffn(warp_hip_ctx *c, int layer, int expert, const float *x_dev, float *out_dev);
+
 /* Replaces moe_chunk (src/model.c:3512-3693) for T <= max_tokens tokens:
  * per-token routing, pairs grouped by expert on the GPU, matrix-core
  * matvecs over tiles of up to 8 tokens per expert, per-token combine in

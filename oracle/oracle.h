@@ -202,6 +202,11 @@ void or_vq_encode(const float *X, int n, const float *books, int stages,
 /* zlib crc32 (src/crc32.c:176; record payload at src/model.c:1742-1744). */
 uint32_t or_crc32(const uint8_t *p, size_t n);
 
+/* expf_check.c: the device expf restatement against glibc's expf */
+uint64_t or_expf_mismatches(uint32_t lo, uint64_t n, int nthreads, uint32_t *first);
+void or_expf_array(const float *x, float *y, long n);
+void or_sigmoid_array(const float *x, float *y, long n);
+
 /* record_check (src/model.c:1698-1745). Returns 0 ok, 2 header, 3 crc.
  * index_bits 8, 6 or 12 (the last for the extension format). */
 int or_record_check(const uint8_t *rec, size_t rec_bytes, int layer, int expert,

@@ -57,6 +57,9 @@ def _declare(L):
         "or_expert_ffn": (None, [vp, vp, vp, vp, vp, vp, vp, vp, vp]),
         "or_vq_encode": (None, [vp, i, vp, i, i, i, vp]),
         "or_crc32": (C.c_uint32, [vp, sz]),
+        "or_expf_mismatches": (C.c_uint64, [C.c_uint32, C.c_uint64, i, vp]),
+        "or_expf_array": (None, [vp, vp, C.c_long]),
+        "or_sigmoid_array": (None, [vp, vp, C.c_long]),
         "or_record_check": (i, [vp, sz, i, i, i, i, i, vp, i]),
     }
     for name, (res, args) in sig.items():
@@ -218,16 +221,23 @@ class Ref:
         L.ref_build_lut.argtypes = [vp, i, i, vp, i, vp]
         L.ref_vq_matvec.restype = i
         L.ref_vq_matvec.argtypes = [vp, i, i, i, vp, vp]
+        L.ref_pool_reset.restype = None
+        L.ref_expert_ffn.restype = i
+        L.ref_expert_ffn.argtypes = [vp, i, i, vp, vp]
         L.ref_trunk_matvec.restype = i
         L.ref_trunk_matvec.argtypes = [vp, C.c_char_p, vp, vp, i, i]
         self.m = L.ref_open(container_dir.encode(), cache_bytes, n_threads)
         if not self.m:
             raise RuntimeError(f"reference refused {container_dir}")
 
-    def close(self):
+    def close(self, reset_pool=False):
+        """reset_pool: also end the reference's process-wide thread pool, so a
+        model opened next gets a pool of its own n_threads."""
         if self.m:
             self.L.ref_close(self.m)
             self.m = None
+        if reset_pool:
+            self.L.ref_pool_reset()
 
     def backend(self) -> str:
         return self.L.ref_backend().decode()
@@ -259,6 +269,12 @@ class Ref:
         x = np.ascontiguousarray(x, np.float32)
         y = np.empty(M, np.float32)
         assert self.L.ref_vq_matvec(self.m, L, expert, kind, _p(x), _p(y)) == 0
+        return y
+
+    def expert_ffn(self, L, expert, x, H):
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.empty(H, np.float32)
+        assert self.L.ref_expert_ffn(self.m, L, expert, _p(x), _p(y)) == 0
         return y
 
     def build_lut(self, L, kind, x, n_out):

@@ -106,3 +106,38 @@ int ref_trunk_matvec(void *p, const char *name, const float *x, float *y, int ou
     matvec_t(m, y, t, x, out, in);
     return 0;
 }
+
+/* One expert's FFN as moe_layer runs it for each routed expert
+ * (src/model.c:2886-2909): the gate and up tables of x, their gather
+ * applies, SiLU(gate) * up, then the down matvec; y [hidden], unweighted. */
+int ref_expert_ffn(void *p, int L, int expert, const float *x, float *y)
+{
+    waste_model *m = (waste_model *)p;
+    const uint8_t *rec = read_expert(m, L, expert);
+    if (!rec) return -1;
+    const waste_expert_hdr *h = (const waste_expert_hdr *)rec;
+    const uint16_t *sc = (const uint16_t *)(rec + h->chan_corr_off);
+    const int inter = m->cfg.moe_inter, hid = m->cfg.hidden;
+    const size_t lin = (size_t)(hid / m->vec_dim) * m->stages * m->cb_entries;
+    const size_t ldn = (size_t)(inter / m->vec_dim) * m->stages * m->cb_entries;
+    float *lg = (float *)malloc(lin * sizeof(float)), *lu = (float *)malloc(lin * sizeof(float));
+    float *ld = (float *)malloc(ldn * sizeof(float));
+    float *ga = (float *)malloc((size_t)inter * sizeof(float)), *ub = (float *)malloc((size_t)inter * sizeof(float));
+    if (!lg || !lu || !ld || !ga || !ub || m->index_bits == 6) {
+        free(lg); free(lu); free(ld); free(ga); free(ub);
+        return -1;
+    }
+    vq_build_lut(m, lg, h->codebook_id + 0 * m->stages, x, hid, m->stages, m->cb_entries, m->vec_dim, NULL, NULL);
+    vq_build_lut(m, lu, h->codebook_id + 1 * m->stages, x, hid, m->stages, m->cb_entries, m->vec_dim, NULL, NULL);
+    vq_apply(m, ga, rec + h->gate_off, sc, inter, hid, lg, NULL, NULL);
+    vq_apply(m, ub, rec + h->up_off, sc + inter, inter, hid, lu, NULL, NULL);
+    for (int i = 0; i < inter; i++) ga[i] = silu(ga[i]) * ub[i];
+    vq_matvec(m, y, rec + h->down_off, sc + 2 * inter, ga, hid, inter, h->codebook_id + 2 * m->stages, ld, NULL,
+              NULL);
+    free(lg); free(lu); free(ld); free(ga); free(ub);
+    return 0;
+}
+
+/* Ends the process-wide thread pool, so that the next ref_open sizes a new
+ * one (the pool is otherwise fixed by the first model opened). */
+void ref_pool_reset(void) { waste_pool_shutdown(); }

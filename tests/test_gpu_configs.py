@@ -73,8 +73,34 @@ def test_config1_single_expert(fmt):
                 ctx.vq_matvec(0, kind, rec, dev(x), y)
                 e = rel_err(host(y), yr)
                 assert e <= TOL, (kind, path, e)
+        # the whole expert FFN (warp_hip_expert_ffn): the oracle's gate and up
+        # matvecs, SiLU(gate) * up, the down matvec
+        S0 = [0, S, 2 * S]
+        mats = []
+        for kind in range(3):
+            M, N = (spec.inter, spec.hidden) if kind < 2 else (spec.hidden, spec.inter)
+            soff = [0, spec.inter, 2 * spec.inter][kind]
+            corr = int(hdr[8])
+            mats.append((r[int(hdr[5 + kind]):].copy(), r[corr + 2 * soff: corr + 2 * (soff + M)].view(np.uint16).copy(),
+                         M, N))
+        for t in range(3):
+            x = rng.normal(size=spec.hidden).astype(np.float32)
+            g = po.vq_matvec(fmt, mats[0][0], mats[0][1], x, bT, S0[0], spec.inter, spec.hidden)
+            u = po.vq_matvec(fmt, mats[1][0], mats[1][1], x, bT, S0[1], spec.inter, spec.hidden)
+            h = np.array([po.lib().or_silu(float(v)) for v in g], np.float32) * u
+            yr = po.vq_matvec(fmt, mats[2][0], mats[2][1], h.astype(np.float32), bT, S0[2], spec.hidden, spec.inter)
+            for path in ("auto", "mfma"):
+                ctx.set_matvec_path(path)
+                y = empty(spec.hidden)
+                ctx.expert_ffn(0, 1, dev(x), y)
+                ctx.sync()
+                e = rel_err(host(y), yr)
+                assert e <= TOL, (t, path, e)
+        with pytest.raises(warp_amd.WarpHipError) as ei:
+            ctx.expert_ffn(0, 2, dev(x), empty(spec.hidden))      # expert 2 of 2 does not exist
+        assert ei.value.code == warp_amd.E_ARG
         ctx.set_matvec_path("auto")
-        log(f"config 1 ({fmt}): gate, up, down of one expert within the bar on both kernels")
+        log(f"config 1 ({fmt}): gate, up, down and the whole expert FFN within the bar on both kernels")
     finally:
         ctx.close()
 

@@ -65,3 +65,48 @@ def test_route_ties(act):
         log(f"route act={act}: {len(cases(rng))} tie cases bit-exact on both kernels")
     finally:
         ctx.close()
+
+
+@pytest.mark.parametrize("act", [0, 1])
+def test_scores_bitexact_on_many_logits(act):
+    """Every expert picked (K = E = 64, no renormalisation, scale 1), so the
+    weights are the scores themselves: sigmoid 1/(1+expf(-l)) or softmax
+    expf(l - max)/sum. 4096 tokens through the batched kernel and 64 through
+    the one-token kernel, against the oracle (glibc's expf): selection and
+    weights bit-exact. The exp arguments span the range where the score
+    depends on every bit of expf, and the sample includes arguments on which
+    a correctly rounded exp differs from glibc's, so only an expf that
+    reproduces glibc's passes."""
+    import warp_amd
+    Ek, T = 64, 4096
+    ctx = warp_amd.Context(hidden=64, inter=32, n_experts=Ek, top_k=Ek, n_layers=1, fmt="VQ12", renorm=False,
+                           routed_scale=1.0, router_act=act, max_tokens=T, rec_bytes=8192, cache_bytes=8192)
+    try:
+        ctx.set_router(0, np.zeros((Ek, 64), np.float32), None)
+        rng = np.random.default_rng(71 + act)
+        if act == 0:
+            lg = -rng.uniform(-17.0, 88.0, (T, Ek)).astype(np.float32)
+            args = -lg
+        else:
+            lg = rng.uniform(-87.0, 0.0, (T, Ek)).astype(np.float32)
+            args = lg - lg.max(axis=1, keepdims=True)
+        gl = np.empty_like(args)
+        po.lib().or_expf_array(args.ctypes.data, gl.ctypes.data, args.size)
+        cr = np.exp(args.astype(np.float64)).astype(np.float32)
+        differ = int(np.count_nonzero(gl.view(np.uint32) != cr.view(np.uint32)))
+        assert differ > 0
+        idx, w = empty((T, Ek), np.int32), empty((T, Ek))
+        ctx.route(0, dev(lg), T, idx, w)
+        gi, gw = host(idx), host(w)
+        for t in range(T):
+            ri, rw, _ = po.route(lg[t], None, Ek, act, 0, 1.0)
+            assert np.array_equal(gi[t], ri), t
+            assert np.array_equal(gw[t].view(np.uint32), rw.view(np.uint32)), t
+        for t in range(64):
+            i1, w1 = empty(Ek, np.int32), empty(Ek)
+            ctx.route(0, dev(lg[t]), 1, i1, w1)
+            assert np.array_equal(host(i1), gi[t]) and np.array_equal(host(w1).view(np.uint32), gw[t].view(np.uint32))
+        log(f"route act={act}: {T * Ek} scores bit-exact with glibc's expf ({differ} arguments where a "
+            f"correctly rounded exp differs)")
+    finally:
+        ctx.close()

@@ -175,3 +175,22 @@ def test_sigmoid_route_against_float64():
     assert list(idx) == order
     wr = p[order] / p[order].sum() * 2.5
     assert np.allclose(w, wr, rtol=(K + 4) * 2.0 ** -24, atol=0)
+
+
+def test_device_expf_is_glibc_on_every_float():
+    """The kernels' expf (warp_amd/csrc/expf_glibc.h, compiled here as C)
+    against the host's glibc expf on all 2^32 inputs, bit for bit. The
+    reference scores its router logits and computes SiLU with glibc's expf
+    (src/model.c:2724, :501), which is not correctly rounded; a correctly
+    rounded exp, or the same algorithm without the fused range reduction,
+    differs from it on some inputs."""
+    import os
+    first = np.zeros(1, np.uint32)
+    n = po.lib().or_expf_mismatches(0, 1 << 32, max(1, min(os.cpu_count() or 1, 16)), first.ctypes.data)
+    assert n == 0, f"{n} inputs differ, first 0x{int(first[0]):08x}"
+    # the comparison is sensitive: a correctly rounded exp misses glibc on this sample
+    x = np.random.default_rng(0).uniform(-100, 80, 1 << 20).astype(np.float32)
+    gl = np.empty_like(x)
+    po.lib().or_expf_array(x.ctypes.data, gl.ctypes.data, len(x))
+    cr = np.exp(x.astype(np.float64)).astype(np.float32)
+    assert np.count_nonzero(cr.view(np.uint32) != gl.view(np.uint32)) > 0

@@ -1471,6 +1471,59 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
     return 0;
 }
 
+int warp_hip_expert_ffn(warp_hip_ctx *c, int layer, int expert, const float *x_dev, float *out_dev)
+{
+    int rc = check_layer(c, layer);
+    if (rc) return rc;
+    const warp_hip_cfg *g = &c->cfg;
+    const layer_t *L = &c->L[layer];
+    const int H = g->hidden, I = g->inter;
+    if (expert < 0 || expert >= g->n_experts || !x_dev || !out_dev)
+        return set_err(c, WARP_HIP_E_ARG, layer, expert, "expert_ffn arguments");
+    if (!L->has_books) return set_err(c, WARP_HIP_E_ARG, layer, -1, "layer %d has no codebooks", layer);
+    if (c->key_slot[layer * g->n_experts + expert] < 0)
+        return set_err(c, WARP_HIP_E_MISSING, layer, expert, "expert not resident");
+    /* the record's table entry may still be on its way (copy stream) */
+    KRN(c, wait_copies(c));
+    KRN(c, wk_expert_jobs(c->table_dev + (size_t)layer * g->n_experts + expert, I, c->jobs, c->njobs, c->w,
+                          c->missing, c->st));
+    c->missing_pending = 1;
+    if (c->lut_ok && c->mv_path == WARP_HIP_PATH_AUTO) {
+        int sp_gu = 0, sp_d = 0;
+        if ((rc = timing_begin(c, 0))) return rc;
+        KRN(c, wk_vq_lut(g->fmt, c->jobs, c->njobs, 1, 0, 2, L->books, L->books_x31, x_dev, 1, c->part, c->part_cap,
+                         I, H, c->n_cu, NULL, 0, 0, 0.0f, 0.0f, NULL, &sp_gu, c->st));
+        if ((rc = timing_end(c))) return rc;
+        const size_t gu_floats = (size_t)2 * sp_gu * (((size_t)I + 63) / 64) * 64;
+        if ((rc = timing_begin(c, 1))) return rc;
+        KRN(c, wk_vq_lut(g->fmt, c->jobs, c->njobs, 1, 2, 1, L->books, L->books_x31, NULL, 0, c->part + gu_floats,
+                         c->part_cap - gu_floats, H, I, c->n_cu, c->part, sp_gu, g->act_situ, g->situ_beta,
+                         g->situ_linear_beta, NULL, &sp_d, c->st));
+        if ((rc = timing_end(c))) return rc;
+        KRN(c, wk_combine_lut(c->jobs + 2, c->part + gu_floats, sp_d, 1, c->w, 1, H, NULL, NULL, c->missing, NULL,
+                              out_dev, c->st));
+        return 0;
+    }
+    float *yk[3] = { c->yg, c->yu, out_dev };
+    if (c->P6) {
+        const size_t nvH = (size_t)H / 8, nblkH = (nvH + WARP_LUT_BLK - 1) / WARP_LUT_BLK;
+        KRN(c, wk_lut_p6(x_dev, 1, H, books_kind(c, L, 0), c->lut8, c->lscale, c->st));
+        KRN(c, wk_lut_p6(x_dev, 1, H, books_kind(c, L, 1), c->lut8 + nvH * 256, c->lscale + nblkH, c->st));
+        KRN(c, wk_apply_p6(c->jobs, c->njobs, 1, 0, c->lut8, c->lscale, c->yg, I, H, c->st));
+        KRN(c, wk_apply_p6(c->jobs, c->njobs, 1, 1, c->lut8 + nvH * 256, c->lscale + nblkH, c->yu, I, H, c->st));
+        KRN(c, wk_act(c->yg, c->yu, 1, I, g->act_situ, g->situ_beta, g->situ_linear_beta, c->hbuf, c->st));
+        KRN(c, wk_lut_p6(c->hbuf, 1, I, books_kind(c, L, 2), c->lut8d, c->lscaled, c->st));
+        KRN(c, wk_apply_p6(c->jobs, c->njobs, 1, 2, c->lut8d, c->lscaled, out_dev, H, I, c->st));
+        return 0;
+    }
+    KRN(c, wk_split(x_dev, 1, H, c->xs, c->xscale, c->st));
+    KRN(c, wk_vq_matvec(g->fmt, c->jobs, c->njobs, 1, 0, 2, L->books, c->xs, c->xscale, yk, I, H, 1, c->st));
+    KRN(c, wk_act_split(c->yg, c->yu, 1, I, g->act_situ, g->situ_beta, g->situ_linear_beta, c->xsh, c->xscaleh, NULL,
+                        c->st));
+    KRN(c, wk_vq_matvec(g->fmt, c->jobs, c->njobs, 1, 2, 1, L->books, c->xsh, c->xscaleh, yk, H, I, 1, c->st));
+    return 0;
+}
+
 int warp_hip_moe_decode_host(warp_hip_ctx *c, int layer, const float *x, float *out, int *routed)
 {
     if (!c) return WARP_HIP_E_ARG;

@@ -55,19 +55,20 @@ __device__ __forceinline__ float f16_flushed(uint16_t h) {
     return __uint_as_float(e ? (sign | ((e + 112u) << 23) | (mn << 13)) : sign);
 }
 
-// expf rounded from a double-precision exp: the correctly rounded value in
-// all but a vanishing fraction of inputs.
-__device__ __forceinline__ float exp_cr(float x) { return (float)exp((double)x); }
+// glibc's expf bit for bit (the reference's scores and SiLU call it):
+// warp_expf, the table-and-cubic algorithm in double precision.
+#define WARP_EXPF_QUAL __device__ __forceinline__
+#include "expf_glibc.h"
 
 __device__ __forceinline__ float silu_ref(float v) {
     // src/model.c:501: v / (1 + expf(-v))
-    return __fdiv_rn(v, __fadd_rn(1.0f, exp_cr(-v)));
+    return __fdiv_rn(v, __fadd_rn(1.0f, warp_expf(-v)));
 }
 
 __device__ __forceinline__ float act_pair(float g, float u, int situ, float beta, float lbeta) {
     if (!situ) return __fmul_rn(silu_ref(g), u);
     // src/model.c:505-509
-    const float a = __fdiv_rn(__fmul_rn(beta, tanhf(__fdiv_rn(g, beta))), __fadd_rn(1.0f, exp_cr(-g)));
+    const float a = __fdiv_rn(__fmul_rn(beta, tanhf(__fdiv_rn(g, beta))), __fadd_rn(1.0f, warp_expf(-g)));
     return __fmul_rn(a, lbeta > 0.0f ? __fmul_rn(lbeta, tanhf(__fdiv_rn(u, lbeta))) : u);
 }
 
@@ -300,7 +301,7 @@ __global__ __launch_bounds__(256) void k_router_scored(const float *__restrict__
     const int e = blockIdx.x;
     const float v = router_row_fast(W, x, E, H, e);
     if (threadIdx.x == 0) {
-        const float sc = __fdiv_rn(1.0f, __fadd_rn(1.0f, exp_cr(-v)));
+        const float sc = __fdiv_rn(1.0f, __fadd_rn(1.0f, warp_expf(-v)));
         out[e] = sc;
         out[E + e] = __fadd_rn(sc, bias ? bias[e] : 0.0f);
     }
@@ -870,14 +871,14 @@ __device__ __forceinline__ int route_pick_lds(int E, int K, int act, int renorm,
             __syncthreads();
             mx = red[0];
             for (int i = 1; i < NT / 64; i++) mx = fmaxf(mx, red[i]);
-            for (int e = tid; e < E; e += NT) score[e] = exp_cr(__fsub_rn(score[e], mx));
+            for (int e = tid; e < E; e += NT) score[e] = warp_expf(__fsub_rn(score[e], mx));
             __syncthreads();
             if (tid == 0) red[0] = seq_sum_lds(score, E);   // sequential, as the reference sums
             __syncthreads();
             const float s = red[0];
             for (int e = tid; e < E; e += NT) score[e] = __fdiv_rn(score[e], s);
         } else {
-            for (int e = tid; e < E; e += NT) score[e] = __fdiv_rn(1.0f, __fadd_rn(1.0f, exp_cr(-score[e])));
+            for (int e = tid; e < E; e += NT) score[e] = __fdiv_rn(1.0f, __fadd_rn(1.0f, warp_expf(-score[e])));
         }
         for (int e = tid; e < E; e += NT) biased[e] = __fadd_rn(score[e], biased[e]);
         __syncthreads();
@@ -3223,6 +3224,39 @@ __global__ __launch_bounds__(256) void k_set_slots(warp_slot *__restrict__ table
 extern "C" int wk_set_slots(warp_slot *table, const warp_slot_upd *u, int n, void *stream) {
     if (n <= 0) return 0;
     hipLaunchKernelGGL(k_set_slots, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, table, u, n);
+    CHECK_LAUNCH();
+    return 0;
+}
+
+// One expert's three matvec jobs from its device table entry (one input,
+// one output row block each), its combine weight 1 and the job counts:
+// the single-expert FFN without routing.
+__global__ __launch_bounds__(64) void k_expert_jobs(const warp_slot *__restrict__ entry, int inter,
+                                                    warp_job *__restrict__ jobs, int *__restrict__ njobs,
+                                                    float *__restrict__ w, int *__restrict__ missing) {
+    const int kind = threadIdx.x;
+    const warp_slot s = *entry;
+    if (kind < 3) {
+        warp_job jb = {};
+        jb.idx = s.rec ? s.rec + s.off[kind] : nullptr;
+        jb.scale = s.rec ? (const uint16_t *)(s.rec + s.off[3]) + (kind == 0 ? 0 : kind == 1 ? inter : 2 * inter)
+                         : nullptr;
+        jb.n = 1;
+        jobs[kind] = jb;
+        njobs[kind] = s.rec ? 1 : 0;
+    }
+    if (kind == 3) {
+        w[0] = 1.0f;
+        njobs[3] = 0;
+        if (!s.rec) *missing = 1;     // sticky until reported
+    }
+}
+
+extern "C" int wk_expert_jobs(const warp_slot *entry, int inter, warp_job *jobs, int *njobs, float *w, int *missing,
+                              void *stream) {
+    if (!entry || !jobs || !njobs || !w || !missing || inter <= 0) return -1;
+    hipLaunchKernelGGL(k_expert_jobs, dim3(1), dim3(64), 0, (hipStream_t)stream, entry, inter, jobs, njobs, w,
+                       missing);
     CHECK_LAUNCH();
     return 0;
 }

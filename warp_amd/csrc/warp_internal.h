@@ -261,6 +261,12 @@ int wk_plan_chunk(const int *idx, const float *w, int T, int K, int E,
 int wk_combine_chunk(const float *y, const int *tok_slots, const float *pair_w, int T, int K, int H,
                      const float *add0, const float *add1, float *out, void *stream);
 
+/* The single-expert FFN's jobs from one device table entry: jobs[0..2] =
+ * gate, up, down (list stride 1, input 0, output 0), njobs = {1, 1, 1, 0},
+ * w[0] = 1; a missing record gives empty lists and sets *missing. */
+int wk_expert_jobs(const warp_slot *entry, int inter, warp_job *jobs, int *njobs, float *w, int *missing,
+                   void *stream);
+
 /* Synthetic device data for benchmarks: fill n bytes with a counter-based
  * hash of (seed, offset). */
 int wk_fill_random(uint8_t *p, size_t n, uint64_t seed, void *stream);

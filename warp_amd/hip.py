@@ -76,6 +76,7 @@ SIGNATURES = {
     "warp_hip_moe_decode": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                       C.c_void_p]),
     "warp_hip_moe_decode_host": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]),
+    "warp_hip_expert_ffn": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]),
     "warp_hip_moe_chunk": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int,
                                      C.c_void_p, C.c_void_p]),
     "warp_hip_moe_chunk_host": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p,
@@ -260,6 +261,10 @@ class Context:
         self._check(lib().warp_hip_moe_decode(self.h, layer, _addr(x_dev), _addr(out_dev), _addr(resid_dev),
                                               _addr(idx), _addr(w)))
         return (idx, w) if want_route else None
+
+    def expert_ffn(self, layer, expert, x_dev, out_dev):
+        """One resident expert's FFN on one token (no routing), queued."""
+        self._check(lib().warp_hip_expert_ffn(self.h, layer, expert, _addr(x_dev), _addr(out_dev)))
 
     def moe_decode_host(self, layer, x):
         import numpy as np
