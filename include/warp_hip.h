@@ -300,6 +300,19 @@ int warp_hip_vq_encode16(const float *X, long n, const float *books, int stages,
  * resid_dev [n][8] is scratch for stages > 1. */
 int warp_hip_vq_encode_dev(const float *X_dev, long n, const float *books_dev, int stages, int entries,
                            float *resid_dev, uint16_t *codes_dev, void *stream);
+/* The same as warp_hip_vq_encode_dev without the resid_dev workspace, and
+ * allocating nothing: no counterpart in the reference. For callers that
+ * cannot allocate device memory (code under HIP graph capture, serving
+ * loops, harnesses that forbid hipMalloc). The residuals between stages live
+ * in a fixed device array of WARP_HIP_NOALLOC_MAX_VECTORS x 8 floats (16 MiB)
+ * that each device keeps until the process ends; with stages > 1, n above
+ * that maximum is refused with WARP_HIP_E_ARG (encode a larger matrix in
+ * pieces). Every call on one device shares the array: calls that overlap on
+ * one device (on two streams at once) race. Codes bit-identical to
+ * warp_hip_vq_encode_dev's. */
+#define WARP_HIP_NOALLOC_MAX_VECTORS (1L << 19)
+int warp_hip_vq_encode_dev_noalloc(const float *X_dev, long n, const float *books_dev, int stages, int entries,
+                                   uint16_t *codes_dev, void *stream);
 /* Replaces waste_vq_lloyd (src/vq.c:109-136), same arguments, dim 8: one
  * iteration (assign, then each non-empty cluster's centroid = the mean of
  * its members summed in double in index order, bit-identical to the

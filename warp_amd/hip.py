@@ -101,6 +101,8 @@ SIGNATURES = {
     "warp_hip_vq_encode_dev": (C.c_int, [C.c_void_p, C.c_long, C.c_void_p, C.c_int, C.c_int, C.c_void_p,
                                          C.c_void_p, C.c_void_p]),
     "warp_hip_vq_lloyd": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_int]),
+    "warp_hip_vq_encode_dev_noalloc": (C.c_int, [C.c_void_p, C.c_long, C.c_void_p, C.c_int, C.c_int, C.c_void_p,
+                                                 C.c_void_p]),
 }
 
 
