@@ -115,7 +115,11 @@ typedef struct {
     size_t rec_bytes;      /* expert record stride, a 4 KiB multiple           */
     size_t cache_bytes;    /* HBM budget for expert records                    */
     int verify;            /* crc32 every record entering the cache
-                            * (WASTE_VERIFY, src/model.c:1742-1744)            */
+                            * (WASTE_VERIFY, src/model.c:1742-1744), on the
+                            * device after its copy; a refused record is
+                            * reported as E_CRC by the call that fetched it
+                            * (or, for a prefetch, by the next call that
+                            * waits) and leaves the cache                    */
     int lookahead;         /* experts of layer L+1 to prefetch per token from
                             * layer L's input (WASTE_LOOKAHEAD,
                             * src/model.c:2680-2711)                           */
@@ -251,6 +255,25 @@ int warp_hip_route(warp_hip_ctx *c, int layer, const float *logits_dev, int T, i
 int warp_hip_mvq(warp_hip_ctx *c, int bits, int group, const int8_t *q_dev,
                  const uint16_t *scales_dev, size_t rowbytes, const float *x_dev, int M, int N,
                  int T, float *y_dev);
+
+/* Replaces waste_crc32 (src/crc32.c:176) for n bytes of device memory: zlib's
+ * crc32, computed on the device (the payload checksum that cfg.verify takes
+ * of every record entering the cache runs the same kernels). n <= 16 GiB.
+ * Synchronous. */
+int warp_hip_crc32(warp_hip_ctx *c, const void *p_dev, size_t n, uint32_t *crc);
+
+/* Replaces waste_ecache_save_usage / waste_ecache_warm (src/ecache.c:730-816)
+ * for the HBM cache: save writes the usage file of the reference's format
+ * (waste_usage_hdr then one waste_usage_ent per resident record: layer,
+ * expert, hit count, last use; src/waste_format.h:173-187); warm reads one,
+ * sorts it by hits descending then (layer, expert), and fills the cache
+ * through the fetch function with the hottest records until it is full,
+ * seeding each slot's hit count from the file. Warming is best effort:
+ * entries naming experts the context does not have, records that fail to
+ * read or fail their checksum are skipped. Returns the records loaded or a
+ * negative code (no fetch function, unreadable file). */
+int warp_hip_save_usage(warp_hip_ctx *c, const char *path, uint64_t tokens);
+int warp_hip_warm(warp_hip_ctx *c, const char *path);
 
 /* Fill n bytes of device memory with deterministic noise (synthetic expert
  * data for benchmarks that cannot afford host generation). */

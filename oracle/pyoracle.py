@@ -222,6 +222,8 @@ class Ref:
         L.ref_vq_matvec.restype = i
         L.ref_vq_matvec.argtypes = [vp, i, i, i, vp, vp]
         L.ref_pool_reset.restype = None
+        L.ref_save_usage.restype = i
+        L.ref_save_usage.argtypes = [vp, C.c_char_p]
         L.ref_expert_ffn.restype = i
         L.ref_expert_ffn.argtypes = [vp, i, i, vp, vp]
         L.ref_trunk_matvec.restype = i
@@ -276,6 +278,9 @@ class Ref:
         y = np.empty(H, np.float32)
         assert self.L.ref_expert_ffn(self.m, L, expert, _p(x), _p(y)) == 0
         return y
+
+    def save_usage(self, path):
+        assert self.L.ref_save_usage(self.m, os.fsencode(path)) == 0
 
     def build_lut(self, L, kind, x, n_out):
         x = np.ascontiguousarray(x, np.float32)

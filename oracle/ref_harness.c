@@ -141,3 +141,7 @@ int ref_expert_ffn(void *p, int L, int expert, const float *x, float *y)
 /* Ends the process-wide thread pool, so that the next ref_open sizes a new
  * one (the pool is otherwise fixed by the first model opened). */
 void ref_pool_reset(void) { waste_pool_shutdown(); }
+
+/* The reference's usage file of its expert cache (waste_model_save_usage,
+ * src/model.c:2991-2995). */
+int ref_save_usage(void *p, const char *path) { return waste_model_save_usage((waste_model *)p, path); }

@@ -22,27 +22,6 @@
 
 /* ---- small utilities ----------------------------------------------------- */
 
-static uint32_t crc_table[256];
-static pthread_once_t crc_once = PTHREAD_ONCE_INIT;
-
-static void crc_init(void)
-{
-    for (uint32_t i = 0; i < 256; i++) {
-        uint32_t c = i;
-        for (int k = 0; k < 8; k++) c = (c >> 1) ^ (0xEDB88320u & (0u - (c & 1u)));
-        crc_table[i] = c;
-    }
-}
-
-/* zlib's crc32, as the record checksum is defined (src/waste_format.h:116-127) */
-static uint32_t crc32_buf(const uint8_t *p, size_t n)
-{
-    pthread_once(&crc_once, crc_init);
-    uint32_t c = 0xFFFFFFFFu;
-    for (size_t i = 0; i < n; i++) c = crc_table[(c ^ p[i]) & 0xFF] ^ (c >> 8);
-    return c ^ 0xFFFFFFFFu;
-}
-
 static int fmt_stages(int fmt)
 {
     switch (fmt) {
@@ -226,6 +205,7 @@ typedef struct {
 
 #define N_STAGE 32
 #define N_TQ 4                  /* pinned lists of table updates in flight */
+#define CRC_MAX_BYTES ((size_t)16 << 30)   /* longest buffer warp_hip_crc32 takes */
 #define WARP_TIMING_N 2048
 #define WARP_TIMING_CLS 4
 
@@ -260,6 +240,13 @@ struct warp_hip_ctx {
     warp_hip_fetch_host_fn fetch_host;  /* records read in place from pinned host memory */
     void *fetch_host_user;
     warp_hip_cache_stats stats;
+    /* device crc32 of records entering the cache (cfg.verify): per key the
+     * verdict of its last checked fill, and the keys the table refused */
+    uint32_t *crc_tmp;              /* block sums, then one output word    */
+    int8_t *crc_bad;                /* [layer][expert]                     */
+    warp_crc_err *crc_err, *h_crc_err;
+    uint32_t *h_word;               /* pinned: one result word             */
+    int crc_pending;                /* checked fills not yet read back     */
     /* Holds keep records from eviction: `hold` is the selection of the
      * layer in flight, `spec_hold` what the last lookahead brought in or
      * found resident. A key is held when its pin_gen equals either; 0 is
@@ -440,6 +427,13 @@ static int ctx_alloc(warp_hip_ctx *c)
     for (int i = 0; i < c->n_slots; i++) c->slot_key[i] = -1;
     DMALLOC(c, c->table_dev, nkeys * sizeof(warp_slot));
     DEV(c, hipMemset(c->table_dev, 0, nkeys * sizeof(warp_slot)));
+    DMALLOC(c, c->crc_tmp, (wk_crc32_tmp_words(CRC_MAX_BYTES) + 1) * sizeof(uint32_t));
+    DMALLOC(c, c->crc_bad, nkeys);
+    DEV(c, hipMemset(c->crc_bad, 0, nkeys));
+    DMALLOC(c, c->crc_err, sizeof(warp_crc_err));
+    DEV(c, hipMemset(c->crc_err, 0, sizeof(warp_crc_err)));
+    DEV(c, hipHostMalloc((void **)&c->h_crc_err, sizeof(warp_crc_err), 0));
+    DEV(c, hipHostMalloc((void **)&c->h_word, sizeof(uint32_t), 0));
     if (c->n_slots > 0) DMALLOC(c, c->pool, (size_t)c->n_slots * g->rec_bytes);
     DEV(c, hipHostMalloc((void **)&c->staging, (size_t)N_STAGE * g->rec_bytes, 0));
     /* a batch touches each expert of one layer at most twice over (the
@@ -559,9 +553,10 @@ void warp_hip_close(warp_hip_ctx *c)
                   c->yd, c->xsh, c->xscaleh, c->hbuf, c->shg, c->shu, c->shh, c->sho, c->lut8, c->lut8d,
                   c->lscale, c->lscaled, c->counts, c->offsets, c->pair_tok, c->pair_exp, c->pair_w, c->tok_slots, c->runs,
                   c->xin, c->xout, c->la_logits, c->la_idx, c->la_w, c->table_dev, c->pool, c->part,
-                  c->shxs, c->shxscale, c->tq_dev };
+                  c->shxs, c->shxscale, c->tq_dev, c->crc_tmp, c->crc_bad, c->crc_err };
     for (size_t i = 0; i < sizeof d / sizeof d[0]; i++) hfree(d[i]);
     hhfree(c->h_idx); hhfree(c->h_w); hhfree(c->h_la_idx); hhfree(c->h_missing); hhfree(c->staging);
+    hhfree(c->h_crc_err); hhfree(c->h_word);
     for (int i = 0; i < N_TQ; i++) hhfree(c->tq_host[i]);
     free(c->tq_pos);
     free(c->key_slot); free(c->slot_key); free(c->hits); free(c->last); free(c->pin_gen);
@@ -585,8 +580,12 @@ void warp_hip_close(warp_hip_ctx *c)
 
 /* Reads and clears the sticky missing-expert flag once the compute stream
  * is idle. */
+static int crc_report(warp_hip_ctx *c);
+
 static int take_missing(warp_hip_ctx *c)
 {
+    int rc = crc_report(c);
+    if (rc) return rc;
     if (!c->missing_pending) return 0;
     DEV(c, hipMemcpy(c->h_missing, c->missing, sizeof(int), hipMemcpyDeviceToHost));
     c->missing_pending = 0;
@@ -760,8 +759,7 @@ static int check_record(warp_hip_ctx *c, const uint8_t *rec, int layer, int expe
           (size_t)off[1] + c->gate_bytes <= off[2] && (size_t)off[2] + c->down_bytes <= off[3] &&
           (size_t)off[3] + scales <= g->rec_bytes))
         return set_err(c, WARP_HIP_E_HEADER, layer, expert, "record offsets do not fit the shape");
-    if (g->verify && crc32_buf(rec + WARP_HDR_BYTES, (size_t)off[3] + scales - WARP_HDR_BYTES) != crc)
-        return set_err(c, WARP_HIP_E_CRC, layer, expert, "record payload checksum");
+    (void)crc;                       /* the payload checksum is taken on the device (verify_slot) */
     return 0;
 }
 
@@ -811,15 +809,16 @@ static int flush_table(warp_hip_ctx *c)
     DEV(c, hipMemcpyAsync(c->tq_dev, u, (size_t)n * sizeof *u, hipMemcpyHostToDevice, c->cp));
     DEV(c, hipEventRecord(c->ev_tq[i], c->cp));
     c->tq_used[i] = 1;
-    if (wk_set_slots(c->table_dev, c->tq_dev, n, c->cp))
+    if (wk_set_slots(c->table_dev, c->tq_dev, n, c->crc_bad, c->crc_err, c->cp))
         return set_err(c, WARP_HIP_E_DEVICE, -1, -1, "table update");
     DEV(c, hipEventRecord(c->ev_copy, c->cp));
     c->copy_pending = 1;
     return 0;
 }
 
-/* Queue table[key] = {rec, off} for the batch's update launch. */
-static int queue_slot(warp_hip_ctx *c, int key, const uint8_t *rec, const uint32_t off[4])
+/* Queue table[key] = {rec, off} for the batch's update launch; checked: the
+ * record's device checksum decides whether the entry is taken. */
+static int queue_slot(warp_hip_ctx *c, int key, const uint8_t *rec, const uint32_t off[4], int checked)
 {
     int rc;
     if (c->tq_n == c->tq_cap && (rc = flush_table(c)) != 0) return rc;
@@ -833,8 +832,8 @@ static int queue_slot(warp_hip_ctx *c, int key, const uint8_t *rec, const uint32
         i = c->tq_n++;
         c->tq_pos[key] = i;
         u[i].key = key;
-        u[i].pad = 0;
     }
+    u[i].checked = checked;
     u[i].v.rec = rec;
     memcpy(u[i].v.off, off, sizeof u[i].v.off);
     return 0;
@@ -855,7 +854,7 @@ static int claim_slot(warp_hip_ctx *c, int layer, int expert)
         c->L[old / E].resident--;
         c->stats.evictions++;
         static const uint32_t none[4] = { 0, 0, 0, 0 };
-        int rc = queue_slot(c, old, NULL, none);
+        int rc = queue_slot(c, old, NULL, none, 0);
         if (rc) return rc;
     }
     c->slot_key[s] = key;
@@ -866,13 +865,57 @@ static int claim_slot(warp_hip_ctx *c, int layer, int expert)
     return s;
 }
 
-/* hdr: a host copy of the record's (checked) header. The entry reaches the
- * device with the batch's flush_table. */
+/* A slot's claim undone: the device refused its record. */
+static void unclaim(warp_hip_ctx *c, int key)
+{
+    const int s = c->key_slot[key];
+    if (s < 0) return;
+    c->key_slot[key] = -1;
+    c->slot_key[s] = -1;
+    c->hits[s] = 0;
+    c->L[key / c->cfg.n_experts].resident--;
+}
+
+/* hdr: a host copy of the record's (checked) header; the record is in slot
+ * s, or on its way there on the copy stream. With cfg.verify the payload's
+ * crc32 is taken on the device next (record_check's checksum,
+ * src/model.c:1742-1744), after the copy, and the batch's table update
+ * refuses a record whose checksum differs from its header's; the host
+ * learns of it at crc_report. The entry reaches the device with the batch's
+ * flush_table. */
 static int publish_slot(warp_hip_ctx *c, int layer, int expert, int s, const uint8_t *hdr)
 {
     uint32_t off[4];
     memcpy(off, hdr + WARP_HDR_GATE_OFF, sizeof off);
-    return queue_slot(c, layer * c->cfg.n_experts + expert, c->pool + (size_t)s * c->cfg.rec_bytes, off);
+    const int key = layer * c->cfg.n_experts + expert;
+    const uint8_t *slot = c->pool + (size_t)s * c->cfg.rec_bytes;
+    if (c->cfg.verify) {
+        const size_t scales = 2u * (2 * (size_t)c->cfg.inter + c->cfg.hidden);
+        KRN(c, wk_crc32(slot + WARP_HDR_BYTES, (size_t)off[3] + scales - WARP_HDR_BYTES, c->crc_tmp, NULL,
+                        (const uint32_t *)(slot + WARP_HDR_CRC_OFF), key, c->crc_bad, c->cp));
+        c->crc_pending = 1;
+    }
+    return queue_slot(c, key, slot, off, c->cfg.verify);
+}
+
+/* Waits for the copy stream and reports the records whose device checksum
+ * failed since the last report: their slots are freed and the call fails
+ * with E_CRC naming the first of them. */
+static int crc_report(warp_hip_ctx *c)
+{
+    if (!c->crc_pending) return 0;
+    DEV(c, hipMemcpyAsync(c->h_crc_err, c->crc_err, sizeof *c->h_crc_err, hipMemcpyDeviceToHost, c->cp));
+    DEV(c, hipStreamSynchronize(c->cp));
+    c->crc_pending = 0;
+    const int n = c->h_crc_err->n;
+    if (n == 0) return 0;
+    const int nk = n < WARP_CRC_ERR_KEYS ? n : WARP_CRC_ERR_KEYS;
+    for (int i = 0; i < nk; i++) unclaim(c, c->h_crc_err->keys[i]);
+    DEV(c, hipMemsetAsync(c->crc_err, 0, sizeof c->crc_err->n, c->cp));
+    DEV(c, hipStreamSynchronize(c->cp));
+    const int E = c->cfg.n_experts, k0 = c->h_crc_err->keys[0];
+    return set_err(c, WARP_HIP_E_CRC, k0 / E, k0 % E, "record payload checksum (%d record%s refused)", n,
+                   n > 1 ? "s" : "");
 }
 
 int warp_hip_put_expert(warp_hip_ctx *c, int layer, int expert, const uint8_t *rec)
@@ -892,8 +935,8 @@ int warp_hip_put_expert(warp_hip_ctx *c, int layer, int expert, const uint8_t *r
     if (s < 0 && (s = claim_slot(c, layer, expert)) < 0) return s;
     DEV(c, hipMemcpyAsync(c->pool + (size_t)s * c->cfg.rec_bytes, rec, c->cfg.rec_bytes, hipMemcpyHostToDevice, c->cp));
     DEV(c, hipStreamSynchronize(c->cp));
-    if ((rc = publish_slot(c, layer, expert, s, rec))) return rc;
-    return flush_table(c);
+    if ((rc = publish_slot(c, layer, expert, s, rec)) || (rc = flush_table(c))) return rc;
+    return crc_report(c);
 }
 
 int warp_hip_put_expert_dev(warp_hip_ctx *c, int layer, int expert, const uint8_t *rec_dev)
@@ -907,11 +950,7 @@ int warp_hip_put_expert_dev(warp_hip_ctx *c, int layer, int expert, const uint8_
      * record already resident for the key stays resident) */
     uint8_t hdr[WARP_HDR_BYTES];
     DEV(c, hipMemcpy(hdr, rec_dev, sizeof hdr, hipMemcpyDeviceToHost));
-    const int v = c->cfg.verify;
-    c->cfg.verify = 0;                 /* the payload is not on the host */
-    rc = check_record(c, hdr, layer, expert);
-    c->cfg.verify = v;
-    if (rc) return rc;
+    if ((rc = check_record(c, hdr, layer, expert))) return rc;
     const int key = layer * c->cfg.n_experts + expert;
     DEV(c, hipEventRecord(c->ev_before, c->st));
     DEV(c, hipStreamWaitEvent(c->cp, c->ev_before, 0));
@@ -920,8 +959,8 @@ int warp_hip_put_expert_dev(warp_hip_ctx *c, int layer, int expert, const uint8_
     DEV(c, hipMemcpyAsync(c->pool + (size_t)s * c->cfg.rec_bytes, rec_dev, c->cfg.rec_bytes,
                           hipMemcpyDeviceToDevice, c->cp));
     DEV(c, hipStreamSynchronize(c->cp));
-    if ((rc = publish_slot(c, layer, expert, s, hdr))) return rc;
-    return flush_table(c);
+    if ((rc = publish_slot(c, layer, expert, s, hdr)) || (rc = flush_table(c))) return rc;
+    return crc_report(c);
 }
 
 int warp_hip_put_expert_synth(warp_hip_ctx *c, int layer, int expert, uint64_t seed, const uint16_t *scales)
@@ -959,7 +998,8 @@ int warp_hip_put_expert_synth(warp_hip_ctx *c, int layer, int expert, uint64_t s
     DEV(c, hipMemcpyAsync(slot, hdr, sizeof hdr, hipMemcpyHostToDevice, c->cp));
     DEV(c, hipMemcpyAsync(slot + off[3], scales, 2 * (2 * (size_t)g->inter + g->hidden), hipMemcpyHostToDevice, c->cp));
     DEV(c, hipStreamSynchronize(c->cp));
-    if ((rc = publish_slot(c, layer, expert, s, hdr))) return rc;
+    /* a synthetic record carries no checksum: never verified */
+    if ((rc = queue_slot(c, key, slot, off, 0))) return rc;
     return flush_table(c);
 }
 
@@ -1126,7 +1166,10 @@ static int ensure_selected(warp_hip_ctx *c, int layer, const int *ids, int n)
             return rc;
         }
     }
-    return flush_table(c);
+    int rc = flush_table(c);
+    /* records the device checksum refused are reported before any kernel
+     * reads the table */
+    return rc ? rc : crc_report(c);
 }
 
 /* A layer that selects without the host (all resident, or nothing to
@@ -1783,4 +1826,125 @@ int warp_hip_fill_random(warp_hip_ctx *c, void *dev, size_t n, uint64_t seed)
     if (!c) return WARP_HIP_E_ARG;
     KRN(c, wk_fill_random((uint8_t *)dev, n, seed, c->st));
     return 0;
+}
+
+/* ---- checksums and the learned hotlist ------------------------------------------------------ */
+
+int warp_hip_crc32(warp_hip_ctx *c, const void *p_dev, size_t n, uint32_t *crc)
+{
+    if (!c || !crc || (n && !p_dev)) return c ? set_err(c, WARP_HIP_E_ARG, -1, -1, "crc32 arguments") : WARP_HIP_E_ARG;
+    if (n == 0) {
+        *crc = 0;                      /* zlib's crc32 of nothing */
+        return 0;
+    }
+    if (n > CRC_MAX_BYTES) return set_err(c, WARP_HIP_E_ARG, -1, -1, "crc32 of %zu bytes: at most %zu", n, CRC_MAX_BYTES);
+    /* on the copy stream, in order with the record checksums that share
+     * the scratch; the result goes after the block sums */
+    uint32_t *out = c->crc_tmp + wk_crc32_tmp_words(CRC_MAX_BYTES);
+    KRN(c, wk_crc32((const uint8_t *)p_dev, n, c->crc_tmp, out, NULL, -1, NULL, c->cp));
+    DEV(c, hipMemcpyAsync(c->h_word, out, sizeof(uint32_t), hipMemcpyDeviceToHost, c->cp));
+    DEV(c, hipStreamSynchronize(c->cp));
+    *crc = *c->h_word;
+    return 0;
+}
+
+/* waste_usage_hdr / waste_usage_ent (src/waste_format.h:173-187) */
+typedef struct {
+    uint32_t magic, version;
+    uint64_t total_tokens;
+} usage_hdr;
+typedef struct {
+    uint16_t layer, expert_id;
+    uint32_t hits, last_seen, next_layer_top;
+} usage_ent;
+#define USAGE_MAGIC 0x47535557u
+
+int warp_hip_save_usage(warp_hip_ctx *c, const char *path, uint64_t tokens)
+{
+    if (!c || !path) return WARP_HIP_E_ARG;
+    FILE *f = fopen(path, "wb");
+    if (!f) return set_err(c, WARP_HIP_E_READ, -1, -1, "cannot write %s", path);
+    const usage_hdr h = { USAGE_MAGIC, 1, tokens };
+    int ok = fwrite(&h, sizeof h, 1, f) == 1;
+    const int E = c->cfg.n_experts;
+    for (int s = 0; ok && s < c->n_slots; s++) {
+        const int key = c->slot_key[s];
+        if (key < 0) continue;
+        const usage_ent e = { (uint16_t)(key / E), (uint16_t)(key % E), c->hits[s], (uint32_t)c->last[s], 0 };
+        ok = fwrite(&e, sizeof e, 1, f) == 1;
+    }
+    ok &= fclose(f) == 0;
+    if (!ok) {
+        remove(path);
+        return set_err(c, WARP_HIP_E_READ, -1, -1, "writing %s failed", path);
+    }
+    return 0;
+}
+
+/* hits descending, then (layer, expert) ascending: the order
+ * src/ecache.c:749-760 warms in, the same for any sort */
+static int usage_cmp(const void *a, const void *b)
+{
+    const usage_ent *x = (const usage_ent *)a, *y = (const usage_ent *)b;
+    if (x->hits != y->hits) return x->hits > y->hits ? -1 : 1;
+    if (x->layer != y->layer) return x->layer < y->layer ? -1 : 1;
+    if (x->expert_id != y->expert_id) return x->expert_id < y->expert_id ? -1 : 1;
+    return 0;
+}
+
+int warp_hip_warm(warp_hip_ctx *c, const char *path)
+{
+    if (!c || !path) return WARP_HIP_E_ARG;
+    if (!can_fetch(c)) return set_err(c, WARP_HIP_E_ARG, -1, -1, "warming needs a fetch function");
+    FILE *f = fopen(path, "rb");
+    if (!f) return set_err(c, WARP_HIP_E_READ, -1, -1, "cannot read %s", path);
+    usage_hdr h;
+    long n = 0;
+    usage_ent *ent = NULL;
+    int bad = fread(&h, sizeof h, 1, f) != 1 || h.magic != USAGE_MAGIC;
+    if (!bad) {
+        const long start = ftell(f);
+        bad = fseek(f, 0, SEEK_END) != 0;
+        n = bad ? 0 : (ftell(f) - start) / (long)sizeof(usage_ent);
+        bad |= fseek(f, start, SEEK_SET) != 0;
+    }
+    if (!bad && n > 0) {
+        ent = (usage_ent *)malloc((size_t)n * sizeof *ent);
+        bad = !ent || fread(ent, sizeof *ent, (size_t)n, f) != (size_t)n;
+    }
+    fclose(f);
+    if (bad) {
+        free(ent);
+        return set_err(c, WARP_HIP_E_READ, -1, -1, "%s is not a usage file", path);
+    }
+    qsort(ent, (size_t)n, sizeof *ent, usage_cmp);
+    const int want = n < c->n_slots ? (int)n : c->n_slots;
+    const int E = c->cfg.n_experts;
+    int loaded = 0;
+    /* the fills overwrite nothing a kernel may still read */
+    DEV(c, hipEventRecord(c->ev_before, c->st));
+    DEV(c, hipStreamWaitEvent(c->cp, c->ev_before, 0));
+    for (int i = 0; i < want; i++) {
+        const int L = ent[i].layer, e = ent[i].expert_id;
+        /* ids from a file that travels beside a container: a stale entry
+         * is skipped, not an error (src/model.c:1770-1783, :2983-2988) */
+        if (L >= c->cfg.n_layers || e >= E || !c->L[L].has_books) continue;
+        if (c->key_slot[L * E + e] >= 0) continue;
+        const int rc = fill_from_fetch(c, L, e);
+        if (rc == WARP_HIP_E_NOSLOT) break;
+        if (rc) continue;
+        const int s = c->key_slot[L * E + e];
+        c->hits[s] = ent[i].hits;          /* the recorded frequency seeds the LFRU */
+        c->stats.prefetched++;
+        loaded++;
+    }
+    free(ent);
+    int rc = flush_table(c);
+    if (rc) return rc;
+    /* warming is best effort: records refused by their checksum are
+     * dropped, not reported */
+    if (c->cfg.verify && crc_report(c) == WARP_HIP_E_CRC) loaded -= c->h_crc_err->n;
+    c->err[0] = 0;
+    c->err_layer = c->err_expert = -1;
+    return loaded;
 }

@@ -3216,14 +3216,26 @@ extern "C" int wk_fill_random(uint8_t *p, size_t n, uint64_t seed, void *stream)
 }
 
 __global__ __launch_bounds__(256) void k_set_slots(warp_slot *__restrict__ table, const warp_slot_upd *__restrict__ u,
-                                                   int n) {
+                                                   int n, const int8_t *__restrict__ crc_bad,
+                                                   warp_crc_err *__restrict__ err) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) table[u[i].key] = u[i].v;
+    if (i >= n) return;
+    const int key = u[i].key;
+    warp_slot v = u[i].v;
+    if (u[i].checked && crc_bad && crc_bad[key]) {
+        v.rec = nullptr;                       // refused: the record stays out of the table
+        const int k = atomicAdd(&err->n, 1);
+        if (k < WARP_CRC_ERR_KEYS) err->keys[k] = key;
+    }
+    table[key] = v;
 }
 
-extern "C" int wk_set_slots(warp_slot *table, const warp_slot_upd *u, int n, void *stream) {
+extern "C" int wk_set_slots(warp_slot *table, const warp_slot_upd *u, int n, const int8_t *crc_bad, warp_crc_err *err,
+                            void *stream) {
     if (n <= 0) return 0;
-    hipLaunchKernelGGL(k_set_slots, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, table, u, n);
+    if (crc_bad && !err) return -1;
+    hipLaunchKernelGGL(k_set_slots, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, table, u, n, crc_bad,
+                       err);
     CHECK_LAUNCH();
     return 0;
 }

@@ -66,6 +66,7 @@ typedef struct {
 #define WARP_HDR_UP_OFF 24
 #define WARP_HDR_DOWN_OFF 28
 #define WARP_HDR_CORR_OFF 32
+#define WARP_HDR_CRC_OFF 36
 #define WARP_HDR_BYTES 48
 
 /* Every launcher returns 0 or a negative hipError_t-derived code, and
@@ -271,15 +272,30 @@ int wk_expert_jobs(const warp_slot *entry, int inter, warp_job *jobs, int *njobs
  * hash of (seed, offset). */
 int wk_fill_random(uint8_t *p, size_t n, uint64_t seed, void *stream);
 
-/* *dst = {rec, off}, ordered on `stream` (expert table updates); rec NULL
- * marks the expert not resident. */
-/* A batch of expert-table updates, each key at most once: table[key] = v. */
+/* A batch of expert-table updates, each key at most once: table[key] = v.
+ * checked = 1: the record was checksummed on the device (wk_crc32 with this
+ * key); if crc_bad[key] is set, the entry becomes NULL (not resident) and the
+ * key is appended to err (the first WARP_CRC_ERR_KEYS keys; n counts every
+ * failure). */
 typedef struct {
     warp_slot v;
     int key;
-    int pad;
+    int checked;
 } warp_slot_upd;
-int wk_set_slots(warp_slot *table, const warp_slot_upd *u, int n, void *stream);
+#define WARP_CRC_ERR_KEYS 255
+typedef struct {
+    int n;
+    int keys[WARP_CRC_ERR_KEYS];
+} warp_crc_err;
+int wk_set_slots(warp_slot *table, const warp_slot_upd *u, int n, const int8_t *crc_bad, warp_crc_err *err,
+                 void *stream);
+
+/* zlib's crc32 of p[0, n) in device memory (crc.hip). tmp holds
+ * wk_crc32_tmp_words(n) words. key < 0: the checksum to *out (device);
+ * key >= 0: bad[key] = (checksum != *expect), both in device memory. */
+size_t wk_crc32_tmp_words(size_t n);
+int wk_crc32(const uint8_t *p, size_t n, uint32_t *tmp, uint32_t *out, const uint32_t *expect, int key,
+             int8_t *bad, void *stream);
 
 /* Device properties the host needs: returns the gfx name into buf. */
 int wk_device_arch(int device, char *buf, int n);

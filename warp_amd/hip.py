@@ -88,6 +88,9 @@ SIGNATURES = {
     "warp_hip_mvq": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p,
                                C.c_int, C.c_int, C.c_int, C.c_void_p]),
     "warp_hip_fill_random": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_uint64]),
+    "warp_hip_crc32": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.POINTER(C.c_uint32)]),
+    "warp_hip_save_usage": (C.c_int, [C.c_void_p, C.c_char_p, C.c_uint64]),
+    "warp_hip_warm": (C.c_int, [C.c_void_p, C.c_char_p]),
     "warp_hip_resident": (C.c_void_p, [C.c_void_p, C.c_int, C.c_int]),
     "warp_hip_put_expert_dev": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p]),
     "warp_hip_put_expert_synth": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_uint64, C.c_void_p]),
@@ -330,6 +333,23 @@ class Context:
         n = (C.c_uint64 * 4)()
         self._check(lib().warp_hip_get_timing(self.h, ms, n))
         return list(ms), list(n)
+
+    def crc32(self, dev, nbytes):
+        """zlib's crc32 of nbytes of device memory, computed on the device."""
+        out = C.c_uint32()
+        self._check(lib().warp_hip_crc32(self.h, _addr(dev), nbytes, C.byref(out)))
+        return out.value
+
+    def save_usage(self, path, tokens=0):
+        self._check(lib().warp_hip_save_usage(self.h, os.fsencode(path), tokens))
+
+    def warm(self, path):
+        """Fill the cache with the hottest records of a usage file; returns
+        how many were loaded."""
+        n = lib().warp_hip_warm(self.h, os.fsencode(path))
+        if n < 0:
+            self._check(n)
+        return n
 
     def fill_random(self, dev, nbytes, seed):
         self._check(lib().warp_hip_fill_random(self.h, _addr(dev), nbytes, seed))
