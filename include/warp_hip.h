@@ -55,10 +55,14 @@ typedef struct {
  * waste_register_hip beside waste_register_metal, src/metal.m). Probes for a
  * gfx950 device and returns NULL (declines) without one; otherwise fills
  * mvq_rows_f32 (argument struct mvq_arg, src/simd.h:35-39, host pointers) and
- * sets on_device = 1, and returns "HIP gfx950". The slot keeps the table's
- * previous mvq_rows_f32 and calls it with the same arguments if a device call
- * fails, as the reference's accelerator contract requires (src/metal.m:177-181);
- * warp_hip_table_stats() reports how many calls ran where. */
+ * kda_step (src/waste_backend.h:69-72: waste_kda_step's arguments, host
+ * pointers; the state goes to the device and back on every call, and the
+ * results are bit-identical to src/kda.c:26-68), sets on_device = 1, and
+ * returns "HIP gfx950". Each slot keeps the table's previous function and
+ * calls it with the same arguments if a device call fails, as the
+ * reference's accelerator contract requires (src/metal.m:177-181);
+ * warp_hip_table_stats() and warp_hip_kda_stats() report how many calls ran
+ * where. */
 const char *waste_register_hip(waste_kernels *t);
 
 /* Replaces: src/waste_backend.h:112-114 for this backend. Drops the device
@@ -68,6 +72,17 @@ void waste_hip_release_host_buffers(void);
 
 /* Calls of the mvq_rows_f32 slot that ran on the device / fell back. */
 void warp_hip_table_stats(uint64_t *device_calls, uint64_t *fallback_calls);
+/* The same for the kda_step slot. */
+void warp_hip_kda_stats(uint64_t *device_calls, uint64_t *fallback_calls);
+
+/* Replaces waste_kda_forward (src/kda.c:70-82) for state and inputs already in
+ * device memory: T steps of the recurrence in one launch on `stream` (a
+ * hipStream_t, NULL for the null stream), the state S [H][K][V] updated in
+ * place and kept on chip between the steps; q, k, g_log [T][H][K], v, o
+ * [T][H][V], beta [T][H]. K <= 256, V <= 1024, K*V <= 38400. Bit-identical to
+ * T calls of waste_kda_step. */
+int warp_hip_kda_forward(int T, int H, int K, int V, const float *q_dev, const float *k_dev, const float *v_dev,
+                         const float *g_dev, const float *beta_dev, float *S_dev, float *o_dev, void *stream);
 
 /* ---- 2. MoE slots ---------------------------------------------------------- */
 

@@ -685,3 +685,44 @@ int or_record_check(const uint8_t *rec, size_t rec_bytes, int layer, int expert,
     if (or_crc32(rec + sizeof *h, payload) != h->crc32) return 3;
     return 0;
 }
+
+/* ---- Kimi Delta Attention step (src/kda.c:19-68) ---------------------------------- */
+
+static float kda_rnorm(const float *x, int n)
+{
+    float s = 0.0f;
+    for (int i = 0; i < n; i++) s += x[i] * x[i];
+    return 1.0f / sqrtf(s + 1e-12f);
+}
+
+void or_kda_step(int H, int K, int V, const float *q, const float *k, const float *v, const float *g_log,
+                 const float *beta, float *S, float *o)
+{
+    const float qscale = 1.0f / sqrtf((float)K);
+    float *u = (float *)malloc((size_t)V * sizeof(float));
+    if (!u) return;
+    for (int h = 0; h < H; h++) {
+        const float *qh = q + (size_t)h * K, *kh = k + (size_t)h * K, *gh = g_log + (size_t)h * K;
+        const float *vh = v + (size_t)h * V;
+        float *Sh = S + (size_t)h * K * V, *oh = o + (size_t)h * V;
+        const float qn = kda_rnorm(qh, K) * qscale, kn = kda_rnorm(kh, K);
+        for (int i = 0; i < V; i++) u[i] = 0.0f;
+        for (int r = 0; r < K; r++) {               /* decay, u = S^T k */
+            const float d = expf(gh[r]), kv = kh[r] * kn;
+            for (int i = 0; i < V; i++) {
+                Sh[(size_t)r * V + i] *= d;
+                u[i] += Sh[(size_t)r * V + i] * kv;
+            }
+        }
+        for (int i = 0; i < V; i++) u[i] = beta[h] * (vh[i] - u[i]);
+        for (int i = 0; i < V; i++) oh[i] = 0.0f;
+        for (int r = 0; r < K; r++) {               /* S += k d^T, o = S^T q */
+            const float kv = kh[r] * kn, qv = qh[r] * qn;
+            for (int i = 0; i < V; i++) {
+                Sh[(size_t)r * V + i] += u[i] * kv;
+                oh[i] += Sh[(size_t)r * V + i] * qv;
+            }
+        }
+    }
+    free(u);
+}

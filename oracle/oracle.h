@@ -202,6 +202,10 @@ void or_vq_encode(const float *X, int n, const float *books, int stages,
 /* zlib crc32 (src/crc32.c:176; record payload at src/model.c:1742-1744). */
 uint32_t or_crc32(const uint8_t *p, size_t n);
 
+/* Kimi Delta Attention step (src/kda.c:19-68): S [H][K][V] in place, o [H][V]. */
+void or_kda_step(int H, int K, int V, const float *q, const float *k, const float *v, const float *g_log,
+                 const float *beta, float *S, float *o);
+
 /* expf_check.c: the device expf restatement against glibc's expf */
 uint64_t or_expf_mismatches(uint32_t lo, uint64_t n, int nthreads, uint32_t *first);
 void or_expf_array(const float *x, float *y, long n);

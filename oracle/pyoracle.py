@@ -58,6 +58,7 @@ def _declare(L):
         "or_vq_encode": (None, [vp, i, vp, i, i, i, vp]),
         "or_crc32": (C.c_uint32, [vp, sz]),
         "or_expf_mismatches": (C.c_uint64, [C.c_uint32, C.c_uint64, i, vp]),
+        "or_kda_step": (None, [i, i, i, vp, vp, vp, vp, vp, vp, vp]),
         "or_expf_array": (None, [vp, vp, C.c_long]),
         "or_sigmoid_array": (None, [vp, vp, C.c_long]),
         "or_record_check": (i, [vp, sz, i, i, i, i, i, vp, i]),
@@ -287,3 +288,16 @@ class Ref:
         lut = np.empty(n_out, np.float32)
         self.L.ref_build_lut(self.m, L, kind, _p(x), x.shape[0], _p(lut))
         return lut
+
+
+def kda_forward(q, k, v, g, beta, S):
+    """T steps of or_kda_step: q, k, g [T][H][K], v [T][H][V], beta [T][H],
+    S [H][K][V] (not modified). Returns (S after, o [T][H][V])."""
+    T, H, K = q.shape
+    V = v.shape[2]
+    S = np.ascontiguousarray(S, np.float32).copy()
+    o = np.empty((T, H, V), np.float32)
+    for t in range(T):
+        a = [np.ascontiguousarray(z[t], np.float32) for z in (q, k, v, g, beta)]
+        lib().or_kda_step(H, K, V, *(_p(z) for z in a), _p(S), _p(o[t]))
+    return S, o

@@ -101,3 +101,17 @@ def test_ties_go_to_the_lowest_id():
             if a in idx:
                 seen += 1
     assert seen, "the tie case never reached the selection"
+
+
+def test_kda_step_bitexact_against_the_reference():
+    """The oracle's KDA step (or_kda_step) against the compiled reference's
+    waste_kda_step outputs in tests/golden/kda.npz (make_kda.py), over
+    several steps and shapes: state and outputs bit for bit."""
+    g = load("kda")
+    n = 0
+    while f"c{n}_q" in g:
+        S, o = po.kda_forward(g[f"c{n}_q"], g[f"c{n}_k"], g[f"c{n}_v"], g[f"c{n}_g"], g[f"c{n}_beta"], g[f"c{n}_S0"])
+        assert np.array_equal(bits(S), bits(g[f"c{n}_S"])), n
+        assert np.array_equal(bits(o), bits(g[f"c{n}_o"])), n
+        n += 1
+    assert n == 3

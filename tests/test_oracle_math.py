@@ -194,3 +194,26 @@ def test_device_expf_is_glibc_on_every_float():
     po.lib().or_expf_array(x.ctypes.data, gl.ctypes.data, len(x))
     cr = np.exp(x.astype(np.float64)).astype(np.float32)
     assert np.count_nonzero(cr.view(np.uint32) != gl.view(np.uint32)) > 0
+
+
+def test_kda_step_against_float64():
+    """The KDA recurrence in float64 (q, k L2-normalised, q by 1/sqrt(K);
+    S <- diag(exp g) S; d = beta (v - S^T k); S <- S + k d^T; o = S^T q)
+    against the oracle's fp32 step: a transposed state, a missing decay,
+    the update before the readout or an unnormalised key fail by far more
+    than fp32 rounding."""
+    rng = np.random.default_rng(21)
+    H, K, V = 3, 32, 48
+    q, k = rng.normal(size=(1, H, K)), rng.normal(size=(1, H, K))
+    v, g = rng.normal(size=(1, H, V)), -rng.uniform(0, 2, size=(1, H, K))
+    beta, S0 = rng.uniform(0, 1, size=(1, H)), rng.normal(size=(H, K, V)) * 0.1
+    f32 = lambda a: np.asarray(a, np.float32)
+    S, o = po.kda_forward(f32(q), f32(k), f32(v), f32(g), f32(beta), f32(S0))
+    for h in range(H):
+        qn = q[0, h] / np.sqrt((q[0, h] ** 2).sum() + 1e-12) / np.sqrt(K)
+        kn = k[0, h] / np.sqrt((k[0, h] ** 2).sum() + 1e-12)
+        Sh = np.exp(g[0, h])[:, None] * f32(S0[h]).astype(np.float64)
+        d = beta[0, h] * (v[0, h] - Sh.T @ kn)
+        Sh = Sh + np.outer(kn, d)
+        assert np.allclose(S[h], Sh, rtol=1e-5, atol=1e-6)
+        assert np.allclose(o[0, h], Sh.T @ qn, rtol=1e-4, atol=1e-5)

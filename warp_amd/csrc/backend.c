@@ -76,6 +76,12 @@ typedef struct {
 
 static pthread_mutex_t g_tab_mu = PTHREAD_MUTEX_INITIALIZER;
 static void (*g_prev_mvq)(int, int, void *);
+typedef void (*kda_fn)(int, int, int, const float *, const float *, const float *, const float *, const float *,
+                       float *, float *, float *);
+static kda_fn g_prev_kda;
+static float *g_kda_buf;
+static size_t g_kda_cap;
+static uint64_t g_kda_calls, g_kda_fallbacks;
 static mirror_t *g_mirrors;
 static int g_n_mirrors, g_cap_mirrors;
 static hipStream_t g_tab_stream;
@@ -151,6 +157,45 @@ static void hip_mvq_rows_f32(int b, int e, void *p)
     if (rc != 0 && g_prev_mvq) g_prev_mvq(b, e, p);
 }
 
+/* The kda_step slot (src/waste_backend.h:69-72): host pointers, so the
+ * inputs and the state go to the device and the state and output come back
+ * on every call; one block per head does the step (wk_kda). */
+static int kda_on_device(int H, int K, int V, const float *q, const float *k, const float *v, const float *g,
+                         const float *beta, float *S, float *o)
+{
+    if (!g_tab_stream && !HIPOK(hipStreamCreate(&g_tab_stream))) return -1;
+    const size_t hk = (size_t)H * K, hv = (size_t)H * V, ns = (size_t)H * K * V;
+    const size_t need = 3 * hk + 2 * hv + (size_t)H + ns;
+    if (g_kda_cap < need) {
+        if (g_kda_buf) (void)hipFree(g_kda_buf);
+        g_kda_buf = NULL;
+        g_kda_cap = 0;
+        if (!HIPOK(hipMalloc((void **)&g_kda_buf, need * sizeof(float)))) return -1;
+        g_kda_cap = need;
+    }
+    float *dq = g_kda_buf, *dk = dq + hk, *dg = dk + hk, *dv = dg + hk, *dob = dv + hv, *db = dob + hv, *dS = db + H;
+    const struct { float *d; const float *h; size_t n; } in[] = {
+        { dq, q, hk }, { dk, k, hk }, { dg, g, hk }, { dv, v, hv }, { db, beta, (size_t)H }, { dS, S, ns } };
+    for (size_t i = 0; i < sizeof in / sizeof in[0]; i++)
+        if (!HIPOK(hipMemcpyAsync(in[i].d, in[i].h, in[i].n * sizeof(float), hipMemcpyHostToDevice, g_tab_stream)))
+            return -1;
+    if (wk_kda(1, H, K, V, dq, dk, dv, dg, db, dS, dob, g_tab_stream)) return -1;
+    if (!HIPOK(hipMemcpyAsync(S, dS, ns * sizeof(float), hipMemcpyDeviceToHost, g_tab_stream)) ||
+        !HIPOK(hipMemcpyAsync(o, dob, hv * sizeof(float), hipMemcpyDeviceToHost, g_tab_stream)))
+        return -1;
+    return HIPOK(hipStreamSynchronize(g_tab_stream)) ? 0 : -1;
+}
+
+static void hip_kda_step(int H, int K, int V, const float *q, const float *k, const float *v, const float *g_log,
+                         const float *beta, float *S, float *o, float *scratch)
+{
+    pthread_mutex_lock(&g_tab_mu);
+    const int rc = kda_on_device(H, K, V, q, k, v, g_log, beta, S, o);
+    if (rc == 0) g_kda_calls++; else g_kda_fallbacks++;
+    pthread_mutex_unlock(&g_tab_mu);
+    if (rc != 0 && g_prev_kda) g_prev_kda(H, K, V, q, k, v, g_log, beta, S, o, scratch);
+}
+
 static int device_is_gfx950(int dev)
 {
     char arch[64];
@@ -165,8 +210,10 @@ const char *waste_register_hip(waste_kernels *t)
     if (!device_is_gfx950(0)) return NULL;
     pthread_mutex_lock(&g_tab_mu);
     if (t->mvq_rows_f32 != hip_mvq_rows_f32) g_prev_mvq = t->mvq_rows_f32;
+    if (t->kda_step != hip_kda_step) g_prev_kda = t->kda_step;
     pthread_mutex_unlock(&g_tab_mu);
     t->mvq_rows_f32 = hip_mvq_rows_f32;
+    t->kda_step = hip_kda_step;
     t->on_device = 1;
     return "HIP gfx950";
 }
@@ -185,6 +232,22 @@ void warp_hip_table_stats(uint64_t *device_calls, uint64_t *fallback_calls)
     if (device_calls) *device_calls = g_dev_calls;
     if (fallback_calls) *fallback_calls = g_fallback_calls;
     pthread_mutex_unlock(&g_tab_mu);
+}
+
+void warp_hip_kda_stats(uint64_t *device_calls, uint64_t *fallback_calls)
+{
+    pthread_mutex_lock(&g_tab_mu);
+    if (device_calls) *device_calls = g_kda_calls;
+    if (fallback_calls) *fallback_calls = g_kda_fallbacks;
+    pthread_mutex_unlock(&g_tab_mu);
+}
+
+int warp_hip_kda_forward(int T, int H, int K, int V, const float *q_dev, const float *k_dev, const float *v_dev,
+                         const float *g_dev, const float *beta_dev, float *S_dev, float *o_dev, void *stream)
+{
+    if (!q_dev || !k_dev || !v_dev || !g_dev || !beta_dev || !S_dev || !o_dev) return WARP_HIP_E_ARG;
+    const int rc = wk_kda(T, H, K, V, q_dev, k_dev, v_dev, g_dev, beta_dev, S_dev, o_dev, stream);
+    return rc == -1 ? WARP_HIP_E_ARG : rc ? WARP_HIP_E_DEVICE : 0;
 }
 
 /* ---- 2. the context ---------------------------------------------------------------- */

@@ -297,6 +297,13 @@ size_t wk_crc32_tmp_words(size_t n);
 int wk_crc32(const uint8_t *p, size_t n, uint32_t *tmp, uint32_t *out, const uint32_t *expect, int key,
              int8_t *bad, void *stream);
 
+/* T steps of the Kimi Delta Attention recurrence (kda.hip), one block per
+ * head, state S [H][K][V] in place: inputs of step t at q/k/g + t*H*K,
+ * v + t*H*V, beta + t*H, output o + t*H*V. K <= 256, V <= 1024, K*V*4 <=
+ * 150 KiB. */
+int wk_kda(int T, int H, int K, int V, const float *q, const float *k, const float *v, const float *g,
+           const float *beta, float *S, float *o, void *stream);
+
 /* Device properties the host needs: returns the gfx name into buf. */
 int wk_device_arch(int device, char *buf, int n);
 

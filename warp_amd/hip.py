@@ -56,6 +56,9 @@ SIGNATURES = {
     "waste_register_hip": (C.c_char_p, [C.c_void_p]),
     "waste_hip_release_host_buffers": (None, []),
     "warp_hip_table_stats": (None, [C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
+    "warp_hip_kda_stats": (None, [C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
+    "warp_hip_kda_forward": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p,
+                                       C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),
     "warp_hip_open": (C.c_int, [C.POINTER(Cfg), C.POINTER(C.c_void_p)]),
     "warp_hip_close": (None, [C.c_void_p]),
     "warp_hip_error": (C.c_char_p, [C.c_void_p, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
