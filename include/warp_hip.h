@@ -112,7 +112,7 @@ enum {
 enum { WARP_HIP_ROUTE_SIGMOID = 0, WARP_HIP_ROUTE_SOFTMAX = 1 };
 
 typedef struct {
-    int hidden;            /* H (the expert input width; no latent path)       */
+    int hidden;            /* H: the router's, shared expert's and output width */
     int inter;             /* moe_intermediate_size                            */
     int n_experts;         /* E                                                */
     int top_k;             /* K <= 64                                          */
@@ -139,6 +139,12 @@ typedef struct {
                             * layer L's input (WASTE_LOOKAHEAD,
                             * src/model.c:2680-2711)                           */
     int device;            /* HIP device ordinal                               */
+    int latent;            /* routed_expert_hidden_size: the experts run on a
+                            * latent projection of this width (0: on H); see
+                            * warp_hip_set_latent                              */
+    int latent_norm;       /* latent_moe_use_norm: RMS norm of the experts'
+                            * combined latent output                          */
+    float norm_eps;        /* rms_norm_eps for that norm                       */
 } warp_hip_cfg;
 
 typedef struct warp_hip_ctx warp_hip_ctx;
@@ -195,6 +201,18 @@ int warp_hip_set_router_q(warp_hip_ctx *c, int layer, int bits, int group, const
 int warp_hip_set_shared(warp_hip_ctx *c, int layer, int bits, int group, int inter_shared,
                         const int8_t *const q[3], const uint16_t *const scales[3],
                         const size_t rowbytes[3]);
+
+/* The latent MoE of real K3 (src/model.c:2789-2795, 2913-2921), for a context
+ * with cfg.latent: routed_expert_down_proj [latent][H] and
+ * routed_expert_up_proj [H][latent] as quantised trunk rows (Q8G, Q4G or Q3G,
+ * one bits/group for both), routed_expert_norm [latent] f32 (read when
+ * cfg.latent_norm). The layer then routes on x, runs its experts on
+ * down . x, combines them in the latent width, normalises, and adds up .
+ * (that) to the shared expert's output. Expert records have the latent shape
+ * (gate/up [inter][latent], down [latent][inter]). */
+int warp_hip_set_latent(warp_hip_ctx *c, int layer, int bits, int group, const int8_t *down_q,
+                        const uint16_t *down_s, size_t down_rowbytes, const int8_t *up_q, const uint16_t *up_s,
+                        size_t up_rowbytes, const float *norm_w);
 
 /* Expert records. put copies one record into the cache now (checked as
  * record_check does, src/model.c:1698-1745, plus the offsets the kernels

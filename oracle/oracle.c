@@ -531,31 +531,68 @@ static void shared_ffn(const or_layer *L, const float *in, float *tmp, int batch
     free(a); free(b);
 }
 
+void or_rmsnorm(float *o, const float *x, const float *w, int n, float eps)
+{
+    float s = 0;
+    for (int i = 0; i < n; i++) s += x[i] * x[i];
+    const float r = 1.0f / sqrtf(s / (float)n + eps);
+    for (int i = 0; i < n; i++) o[i] = x[i] * r * w[i];
+}
+
+/* The latent projections: matvec_t for one token (mvq_rows_f32,
+ * src/model.c:385-399), waste_matmul_t for a chunk (mmq_rows,
+ * src/model.c:3366-3398). kind 0: down [latent][hidden], 1: up. */
+static void latent_proj(const or_layer *L, int kind, const float *x, float *y, int batched)
+{
+    const int out = kind == 0 ? L->latent : L->hidden, in = kind == 0 ? L->hidden : L->latent;
+    const int g = L->lat_group, ng = (in + g - 1) / g;
+    if (batched)
+        or_mmq_rows(0, out, y, L->lat_q[kind], L->lat_s[kind], x, in, ng, g, L->lat_bits, L->lat_rowbytes[kind]);
+    else
+        or_mvq_rows_f32(0, out, y, L->lat_q[kind], L->lat_s[kind], x, in, ng, g, L->lat_bits, L->lat_rowbytes[kind],
+                        L->mvq_isa);
+}
+
 int or_moe_layer(const or_layer *L, const float *in, float *out, int *idx,
                  float *w, float *logits)
 {
     const int E = L->n_experts, K = L->top_k, hid = L->hidden;
-    const int S = or_fmt_stages(L->fmt), En = or_fmt_entries(L->fmt), nv = hid / 8;
+    /* the experts' width, and their view of the layer */
+    const int lat = L->latent ? L->latent : hid;
+    or_layer Le = *L;
+    Le.hidden = lat;
+    const int S = or_fmt_stages(L->fmt), En = or_fmt_entries(L->fmt), nv = lat / 8;
     float *sc = (float *)malloc((size_t)E * sizeof(float));
-    float *acc = (float *)malloc((size_t)hid * sizeof(float));
+    float *acc = (float *)malloc((size_t)lat * sizeof(float));
     float *tmp = (float *)malloc((size_t)hid * sizeof(float));
+    float *xl = (float *)malloc((size_t)lat * sizeof(float)), *ys = (float *)malloc((size_t)lat * sizeof(float));
     const size_t lsz = (size_t)nv * S * En;
     float *lg = (float *)malloc(lsz * sizeof(float)), *lu = (float *)malloc(lsz * sizeof(float));
     int8_t *qg = (int8_t *)malloc(lsz), *qu = (int8_t *)malloc(lsz);
     float *qsg = (float *)malloc(((size_t)nv / OR_LUT_BLK + 2) * sizeof(float));
     float *qsu = (float *)malloc(((size_t)nv / OR_LUT_BLK + 2) * sizeof(float));
     int rc = -1;
-    if (!sc || !acc || !tmp || !lg || !lu || !qg || !qu || !qsg || !qsu) goto out;
+    if (!sc || !acc || !tmp || !xl || !ys || !lg || !lu || !qg || !qu || !qsg || !qsu) goto out;
     router_logits(L, in, sc);
     if (logits) memcpy(logits, sc, (size_t)E * sizeof(float));
     or_route(sc, L->bias, E, K, L->router_act, L->renorm, L->routed_scale, idx, w, NULL);
-    memset(out, 0, (size_t)hid * sizeof(float));
+    const float *xin = in;
+    if (L->latent) {
+        latent_proj(L, 0, in, xl, 0);
+        xin = xl;
+    }
+    float *ysum = L->latent ? ys : out;
+    memset(ysum, 0, (size_t)lat * sizeof(float));
     for (int j = 0; j < K; j++) {
         const uint8_t *rec = L->recs[idx[j]];
-        if (j == 0) build_gate_up(L, rec, in, lg, lu, qg, qsg, qu, qsu);
-        or_expert_ffn(L, rec, lg, lu, qg, qsg, qu, qsu, acc);
+        if (j == 0) build_gate_up(&Le, rec, xin, lg, lu, qg, qsg, qu, qsu);
+        or_expert_ffn(&Le, rec, lg, lu, qg, qsg, qu, qsu, acc);
         const float wj = w[j];
-        for (int i = 0; i < hid; i++) out[i] += wj * acc[i];
+        for (int i = 0; i < lat; i++) ysum[i] += wj * acc[i];
+    }
+    if (L->latent) {
+        if (L->lat_norm) or_rmsnorm(ysum, ysum, L->lat_norm, lat, L->eps);
+        latent_proj(L, 1, ysum, out, 0);
     }
     if (L->sh_q[0]) {
         shared_ffn(L, in, tmp, 0);
@@ -563,7 +600,7 @@ int or_moe_layer(const or_layer *L, const float *in, float *out, int *idx,
     }
     rc = 0;
 out:
-    free(sc); free(acc); free(tmp); free(lg); free(lu); free(qg); free(qu); free(qsg); free(qsu);
+    free(sc); free(acc); free(tmp); free(xl); free(ys); free(lg); free(lu); free(qg); free(qu); free(qsg); free(qsu);
     return rc;
 }
 
@@ -571,22 +608,33 @@ int or_moe_chunk(const or_layer *L, const float *in, float *out, int nT,
                  int *route, float *rw)
 {
     const int E = L->n_experts, K = L->top_k, hid = L->hidden;
-    const int S = or_fmt_stages(L->fmt), En = or_fmt_entries(L->fmt), nv = hid / 8;
+    const int lat = L->latent ? L->latent : hid;
+    or_layer Le = *L;
+    Le.hidden = lat;
+    const int S = or_fmt_stages(L->fmt), En = or_fmt_entries(L->fmt), nv = lat / 8;
     const size_t lsz = (size_t)nv * S * En, nsc = (size_t)nv / OR_LUT_BLK + 2;
     float *sc = (float *)malloc((size_t)E * sizeof(float));
-    float *acc = (float *)malloc((size_t)hid * sizeof(float));
+    float *acc = (float *)malloc((size_t)lat * sizeof(float));
     float *tmp = (float *)malloc((size_t)hid * sizeof(float));
+    float *xl = (float *)malloc((size_t)nT * lat * sizeof(float));
+    float *ys = (float *)malloc((size_t)nT * lat * sizeof(float));
     float *lgu = (float *)malloc((size_t)nT * 2 * lsz * sizeof(float));
     int8_t *qgu = (int8_t *)malloc((size_t)nT * 2 * lsz);
     float *qsgu = (float *)malloc((size_t)nT * 2 * nsc * sizeof(float));
     int rc = -1;
-    if (!sc || !acc || !tmp || !lgu || !qgu || !qsgu) goto out;
+    if (!sc || !acc || !tmp || !xl || !ys || !lgu || !qgu || !qsgu) goto out;
     for (int t = 0; t < nT; t++) {
         router_logits(L, in + (size_t)t * hid, sc);
         or_route(sc, L->bias, E, K, L->router_act, L->renorm, L->routed_scale,
                  route + (size_t)t * K, rw + (size_t)t * K, NULL);
     }
-    memset(out, 0, (size_t)nT * hid * sizeof(float));
+    const float *xin = in;
+    if (L->latent) {
+        for (int t = 0; t < nT; t++) latent_proj(L, 0, in + (size_t)t * hid, xl + (size_t)t * lat, 1);
+        xin = xl;
+    }
+    float *ysum = L->latent ? ys : out;
+    memset(ysum, 0, (size_t)nT * lat * sizeof(float));
     int lut_ready = 0;
     for (int e = 0; e < E; e++) {               /* distinct experts, ascending */
         int used = 0;
@@ -595,7 +643,7 @@ int or_moe_chunk(const or_layer *L, const float *in, float *out, int nT,
         const uint8_t *rec = L->recs[e];
         if (!lut_ready) {
             for (int t = 0; t < nT; t++)
-                build_gate_up(L, rec, in + (size_t)t * hid, lgu + (size_t)(2 * t) * lsz,
+                build_gate_up(&Le, rec, xin + (size_t)t * lat, lgu + (size_t)(2 * t) * lsz,
                               lgu + (size_t)(2 * t + 1) * lsz, qgu + (size_t)(2 * t) * lsz,
                               qsgu + (size_t)(2 * t) * nsc, qgu + (size_t)(2 * t + 1) * lsz,
                               qsgu + (size_t)(2 * t + 1) * nsc);
@@ -606,13 +654,19 @@ int or_moe_chunk(const or_layer *L, const float *in, float *out, int nT,
             for (int j = 0; j < K; j++)
                 if (route[(size_t)t * K + j] == e) { wj = rw[(size_t)t * K + j]; break; }
             if (wj == 0.0f) continue;
-            or_expert_ffn(L, rec, lgu + (size_t)(2 * t) * lsz, lgu + (size_t)(2 * t + 1) * lsz,
+            or_expert_ffn(&Le, rec, lgu + (size_t)(2 * t) * lsz, lgu + (size_t)(2 * t + 1) * lsz,
                           qgu + (size_t)(2 * t) * lsz, qsgu + (size_t)(2 * t) * nsc,
                           qgu + (size_t)(2 * t + 1) * lsz, qsgu + (size_t)(2 * t + 1) * nsc, acc);
-            float *dst = out + (size_t)t * hid;
-            for (int i = 0; i < hid; i++) dst[i] += wj * acc[i];
+            float *dst = ysum + (size_t)t * lat;
+            for (int i = 0; i < lat; i++) dst[i] += wj * acc[i];
         }
     }
+    if (L->latent)
+        for (int t = 0; t < nT; t++) {
+            float *y = ysum + (size_t)t * lat;
+            if (L->lat_norm) or_rmsnorm(y, y, L->lat_norm, lat, L->eps);
+            latent_proj(L, 1, y, out + (size_t)t * hid, 1);
+        }
     if (L->sh_q[0])
         for (int t = 0; t < nT; t++) {
             shared_ffn(L, in + (size_t)t * hid, tmp, 1);
@@ -621,7 +675,7 @@ int or_moe_chunk(const or_layer *L, const float *in, float *out, int nT,
         }
     rc = 0;
 out:
-    free(sc); free(acc); free(tmp); free(lgu); free(qgu); free(qsgu);
+    free(sc); free(acc); free(tmp); free(xl); free(ys); free(lgu); free(qgu); free(qsgu);
     return rc;
 }
 

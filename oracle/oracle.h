@@ -173,6 +173,16 @@ typedef struct {
     int sh_group, sh_bits, sh_inter;
     int fused_lutb;           /* 1: the AVX-512/AVX2 LUT build            */
     int mvq_isa;              /* which mvq_rows_f32 the host would run    */
+    /* latent MoE (src/model.c:2789-2795, 2913-2921): latent > 0 runs the
+     * experts on lat_q[0] . x (rows [latent][hidden]), then rmsnorm with
+     * lat_norm (NULL: none) and eps, then lat_q[1] (rows [hidden][latent]) */
+    int latent;
+    const int8_t *lat_q[2];
+    const uint16_t *lat_s[2];
+    size_t lat_rowbytes[2];
+    int lat_bits, lat_group;
+    const float *lat_norm;
+    float eps;
 } or_layer;
 
 /* One routed expert on one input (the body of the loop at
@@ -183,7 +193,11 @@ void or_expert_ffn(const or_layer *L, const uint8_t *rec, const float *lut_gate,
                    const float *lut_up, const int8_t *q_gate, const float *qs_gate,
                    const int8_t *q_up, const float *qs_up, float *acc);
 
-/* moe_layer (src/model.c:2713-2940), decode, no latent projection.
+/* waste_rmsnorm (src/model.c:132-138): o = x * (1/sqrt(sum x^2 / n + eps)) * w. */
+void or_rmsnorm(float *o, const float *x, const float *w, int n, float eps);
+
+/* moe_layer (src/model.c:2713-2940), decode, with the latent projection when
+ * L->latent.
  * logits (E floats) may be NULL. Returns 0, or -1 on allocation failure. */
 int or_moe_layer(const or_layer *L, const float *in, float *out, int *idx,
                  float *w, float *logits);

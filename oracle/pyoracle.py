@@ -59,6 +59,7 @@ def _declare(L):
         "or_crc32": (C.c_uint32, [vp, sz]),
         "or_expf_mismatches": (C.c_uint64, [C.c_uint32, C.c_uint64, i, vp]),
         "or_kda_step": (None, [i, i, i, vp, vp, vp, vp, vp, vp, vp]),
+        "or_rmsnorm": (None, [vp, vp, vp, i, f]),
         "or_expf_array": (None, [vp, vp, C.c_long]),
         "or_sigmoid_array": (None, [vp, vp, C.c_long]),
         "or_record_check": (i, [vp, sz, i, i, i, i, i, vp, i]),
@@ -81,6 +82,8 @@ class OrLayer(C.Structure):
         ("sh_q", C.c_void_p * 3), ("sh_s", C.c_void_p * 3), ("sh_rowbytes", C.c_size_t * 3),
         ("sh_group", C.c_int), ("sh_bits", C.c_int), ("sh_inter", C.c_int),
         ("fused_lutb", C.c_int), ("mvq_isa", C.c_int),
+        ("latent", C.c_int), ("lat_q", C.c_void_p * 2), ("lat_s", C.c_void_p * 2), ("lat_rowbytes", C.c_size_t * 2),
+        ("lat_bits", C.c_int), ("lat_group", C.c_int), ("lat_norm", C.c_void_p), ("eps", C.c_float),
     ]
 
 
@@ -141,6 +144,17 @@ class LayerView:
             st.sh_group, st.sh_bits = spec.shared_group, spec.shared_bits
             st.sh_inter = spec.inter * spec.n_shared
         st.fused_lutb, st.mvq_isa = fused_lutb, mvq_isa
+        st.eps = 1e-5                           # the containers' rms_norm_eps
+        if getattr(lay, "latent", None) is not None:
+            dq, uq, nw = lay.latent
+            st.latent = spec.latent
+            for k, q in enumerate((dq, uq)):
+                self.keep += [q[0], q[1]]
+                st.lat_q[k], st.lat_s[k], st.lat_rowbytes[k] = q[0].ctypes.data, q[1].ctypes.data, q[2]
+            st.lat_bits, st.lat_group = dq[3], dq[4]
+            if nw is not None:
+                self.keep.append(nw)
+                st.lat_norm = nw.ctypes.data
         self.st = st
 
     def moe_layer(self, x: np.ndarray):

@@ -82,7 +82,8 @@ int ref_vq_matvec(void *p, int L, int expert, int kind, const float *x, float *y
     if (!rec) return -1;
     const waste_expert_hdr *h = (const waste_expert_hdr *)rec;
     const uint16_t *sc = (const uint16_t *)(rec + h->chan_corr_off);
-    const int inter = m->cfg.moe_inter, hid = m->cfg.hidden;
+    /* the experts' width: the latent size on a latent MoE */
+    const int inter = m->cfg.moe_inter, hid = m->cfg.latent_dim ? m->cfg.latent_dim : m->cfg.hidden;
     const uint32_t off = kind == 0 ? h->gate_off : kind == 1 ? h->up_off : h->down_off;
     const int M = kind == 2 ? hid : inter, N = kind == 2 ? inter : hid;
     const uint16_t *s = sc + (kind == 0 ? 0 : kind == 1 ? inter : 2 * inter);
@@ -117,7 +118,7 @@ int ref_expert_ffn(void *p, int L, int expert, const float *x, float *y)
     if (!rec) return -1;
     const waste_expert_hdr *h = (const waste_expert_hdr *)rec;
     const uint16_t *sc = (const uint16_t *)(rec + h->chan_corr_off);
-    const int inter = m->cfg.moe_inter, hid = m->cfg.hidden;
+    const int inter = m->cfg.moe_inter, hid = m->cfg.latent_dim ? m->cfg.latent_dim : m->cfg.hidden;
     const size_t lin = (size_t)(hid / m->vec_dim) * m->stages * m->cb_entries;
     const size_t ldn = (size_t)(inter / m->vec_dim) * m->stages * m->cb_entries;
     float *lg = (float *)malloc(lin * sizeof(float)), *lu = (float *)malloc(lin * sizeof(float));

@@ -69,6 +69,8 @@ class Spec:
     keep_codes: bool = True      # keep the per-matrix code arrays (small shapes)
     dup_rows: tuple = ()         # (a, b): router row b is a copy of row a (exact ties)
     materialize: tuple = ()      # expert ids that get records; () = all (large shapes)
+    latent: int = 0              # routed_expert_hidden_size: experts on a latent projection (0 = none)
+    latent_norm: bool = True     # latent_moe_use_norm (with latent)
 
 
 def index_bytes(fmt: str, M: int, N: int) -> int:
@@ -126,6 +128,9 @@ class Layer:
     codes: list = field(default_factory=list)   # per expert: [gate, up, down] code arrays [S][M][nv]
     scales: list = field(default_factory=list)  # per expert: [gate, up, down] fp16 bits
     records: list = field(default_factory=list)  # per expert: bytes (whole record)
+    # latent MoE: (down (payload, scales, rowbytes, bits, group) [lat][H],
+    # up [H][lat], norm weight [lat] f32 or None), or None
+    latent: tuple | None = None
 
 
 @dataclass
@@ -143,6 +148,7 @@ def build(spec: Spec) -> Model:
     rng = np.random.Generator(np.random.PCG64(spec.seed))
     S, E = FMT_STAGES[spec.fmt], FMT_ENTRIES[spec.fmt]
     H, I = spec.hidden, spec.inter
+    Hx = spec.latent or H                # the experts' width
     n_books = spec.layers * 3 * S
     books = rng.normal(0.0, spec.book_std, size=(n_books, E, 8)).astype(np.float16)
     if spec.subnormals:
@@ -151,9 +157,9 @@ def build(spec: Spec) -> Model:
         books[0, 2, 5] = np.float16(-4.0e-5)
         books[-1, E - 1, 7] = np.float16(1.0e-7)
     books_raw = books.view(np.uint16)
-    shapes = [(I, H), (I, H), (H, I)]
+    shapes = [(I, Hx), (I, Hx), (Hx, I)]
     layers = []
-    rec_len = HDR + sum(index_bytes(spec.fmt, M, N) for M, N in shapes) + 2 * (2 * I + H)
+    rec_len = HDR + sum(index_bytes(spec.fmt, M, N) for M, N in shapes) + 2 * (2 * I + Hx)
     rec_bytes = (rec_len + ALIGN - 1) // ALIGN * ALIGN
     for L in range(spec.layers):
         router = rng.normal(0.0, spec.router_std, size=(spec.experts, H)).astype(np.float32)
@@ -170,7 +176,13 @@ def build(spec: Spec) -> Model:
             si = I * spec.n_shared
             for (M, N) in [(si, H), (si, H), (H, si)]:
                 shared.append(quant_rows(rng, M, N, spec.shared_bits, spec.shared_group, spec.shared_scale))
-        lay = Layer(router=router, router_q=router_q, bias=bias, shared=shared)
+        latent = None
+        if spec.latent:
+            dq = quant_rows(rng, Hx, H, 8, 128) + (8, 128)
+            uq = quant_rows(rng, H, Hx, 8, 128) + (8, 128)
+            nw = rng.uniform(0.5, 1.5, size=Hx).astype(np.float32) if spec.latent_norm else None
+            latent = (dq, uq, nw)
+        lay = Layer(router=router, router_q=router_q, bias=bias, shared=shared, latent=latent)
         for e in range(spec.experts):
             if spec.materialize and e not in spec.materialize:
                 lay.codes.append(None)
@@ -247,6 +259,12 @@ def digest(model: Model) -> str:
         for q in lay.shared:
             h.update(q[0].tobytes())
             h.update(q[1].tobytes())
+        if lay.latent is not None:
+            for q in lay.latent[:2]:
+                h.update(q[0].tobytes())
+                h.update(q[1].tobytes())
+            if lay.latent[2] is not None:
+                h.update(lay.latent[2].tobytes())
         for r in lay.records:
             if r is not None:
                 h.update(r)
@@ -276,6 +294,10 @@ def write(model: Model, out: str) -> str:
     }
     if spec.renorm:
         cfg["moe_renormalize"] = True
+    if spec.latent:
+        cfg["routed_expert_hidden_size"] = spec.latent
+        if spec.latent_norm:
+            cfg["latent_moe_use_norm"] = True
     if spec.act == "situ":
         cfg["hidden_act"] = "situ"
         cfg["activation_situ_beta"] = spec.situ_beta
@@ -305,6 +327,12 @@ def write(model: Model, out: str) -> str:
                                   ([si, H], [si, H], [H, si]), lay.shared):
                 t.quant(m + f"shared_experts.{nm}.weight", shp,
                         q + (spec.shared_bits, spec.shared_group))
+        if lay.latent is not None:
+            dq, uq, nw = lay.latent
+            t.quant(m + "routed_expert_down_proj.weight", [spec.latent, H], dq)
+            t.quant(m + "routed_expert_up_proj.weight", [H, spec.latent], uq)
+            if nw is not None:
+                t.f32(m + "routed_expert_norm.weight", nw)
     t.f32("model.norm.weight", np.ones(H, np.float32))
     t.quant("lm_head.weight", [spec.vocab, H])
     with open(os.path.join(out, "trunk.bin"), "wb") as f:

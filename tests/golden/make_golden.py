@@ -32,6 +32,7 @@ def main():
         ref = po.Ref(d)
         rng = np.random.default_rng(1000 + spec.seed)
         H, I, E, K = spec.hidden, spec.inter, spec.experts, spec.top_k
+        Hx = spec.latent or H                # the experts' width
         S, EN = ct.FMT_STAGES[spec.fmt], ct.FMT_ENTRIES[spec.fmt]
         out = {"digest": np.frombuffer(ct.digest(model).encode(), np.uint8), "backend": np.frombuffer(ref.backend().encode(), np.uint8)}
         for L in range(spec.layers):
@@ -52,13 +53,13 @@ def main():
             out[f"L{L}_chunk_route"] = cr
             out[f"L{L}_chunk_w"] = cw
             for kind in range(3):
-                M, N = (I, H) if kind < 2 else (H, I)
+                M, N = (I, Hx) if kind < 2 else (Hx, I)
                 x = rng.normal(size=N).astype(np.float32)
                 out[f"L{L}_mv{kind}_x"] = x
                 out[f"L{L}_mv{kind}_y"] = ref.vq_matvec(L, 1, kind, x, M)
-            x = rng.normal(size=H).astype(np.float32)
+            x = rng.normal(size=Hx).astype(np.float32)
             out[f"L{L}_lut_x"] = x
-            out[f"L{L}_lut"] = ref.build_lut(L, 0, x, (H // 8) * S * EN)
+            out[f"L{L}_lut"] = ref.build_lut(L, 0, x, (Hx // 8) * S * EN)
         ref.close()
         path = os.path.join(HERE, f"{name}.npz")
         np.savez_compressed(path, **out)

@@ -20,4 +20,8 @@ SPECS = {
     # router rows 2 and 6 identical and no bias: exact ties, lowest id wins
     "vq3r_ties": ct.Spec(fmt="VQ3R", router="f32", bias=False, renorm=True, routed_scale=1.0,
                          top_k=3, shared_bits=8, shared_group=32, dup_rows=(2, 6), seed=105),
+    # K3's latent MoE: experts on a 64-wide projection of the 128-wide hidden
+    # state (Q8G down/up projections, RMS norm between), Q8G shared expert
+    "vq3r_latent": ct.Spec(fmt="VQ3R", router="f32", bias=True, renorm=True, routed_scale=2.5,
+                           latent=64, latent_norm=True, shared_bits=8, shared_group=32, seed=106),
 }

@@ -67,5 +67,5 @@ def open_ctx(model, max_tokens=1, cache_slots=None, **kw):
                            n_layers=s.layers, fmt=s.fmt, renorm=s.renorm, routed_scale=s.routed_scale,
                            act_situ=s.act == "situ", situ_beta=s.situ_beta, situ_linear_beta=s.situ_lbeta,
                            max_tokens=max_tokens, rec_bytes=model.rec_bytes,
-                           cache_bytes=n * model.rec_bytes, **kw)
+                           cache_bytes=n * model.rec_bytes, latent=s.latent, latent_norm=s.latent_norm, **kw)
     return ctx

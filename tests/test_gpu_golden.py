@@ -8,7 +8,8 @@ expert 1. Here the same container bytes go through the C ABI, and each
 result is compared with those stored outputs directly, not through the
 oracle. The specs cover the F32, Q8G and Q4G routers (the quantised ones
 through the mvq rows kernel), the SiTU activation, the VQ3R, VQ2R and
-VQ4P formats and an exact router tie.
+VQ4P formats, an exact router tie and a latent MoE (experts on a
+projection of the hidden state, RMS norm and up projection after them).
 
 Bars: selection and chunk routes bit-exact; strict F32 router logits
 bit-exact; VQ4P matvecs bit-exact; everything else max|d|/max|ref| <= 1e-4.
@@ -80,7 +81,7 @@ def test_vq_matvec_against_reference_outputs(golden):
         rec = ctx.resident(L, 1)
         assert rec
         for kind in range(3):
-            M = spec.inter if kind < 2 else spec.hidden
+            M = spec.inter if kind < 2 else (spec.latent or spec.hidden)
             y = empty(M)
             ctx.vq_matvec(L, kind, rec, dev(g[f"L{L}_mv{kind}_x"]), y)
             ref = g[f"L{L}_mv{kind}_y"]

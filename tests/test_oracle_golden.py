@@ -69,11 +69,12 @@ def test_vq_matvec_and_lut_bitexact(case):
     name, spec, model, g = case
     S, EN = ct.FMT_STAGES[spec.fmt], ct.FMT_ENTRIES[spec.fmt]
     bT = po.books_T(model.books_raw)
+    Hx = spec.latent or spec.hidden                  # the experts' width
     for L in range(spec.layers):
         rec = np.frombuffer(model.layers[L].records[1], np.uint8)
         hdr = np.frombuffer(model.layers[L].records[1][:48], np.uint32)
         for kind in range(3):
-            M, N = (spec.inter, spec.hidden) if kind < 2 else (spec.hidden, spec.inter)
+            M, N = (spec.inter, Hx) if kind < 2 else (Hx, spec.inter)
             soff = [0, spec.inter, 2 * spec.inter][kind]
             corr = int(hdr[8])
             scale = rec[corr + 2 * soff: corr + 2 * (soff + M)].view(np.uint16).copy()
@@ -81,8 +82,8 @@ def test_vq_matvec_and_lut_bitexact(case):
                              L * 3 * S + kind * S, M, N, fused=1)
             assert np.array_equal(bits(y), bits(g[f"L{L}_mv{kind}_y"])), (name, L, kind)
         x = g[f"L{L}_lut_x"]
-        lut = np.empty((spec.hidden // 8) * S * EN, np.float32)
-        po.lib().or_lutb_range(0, spec.hidden // 8, lut.ctypes.data, bT.ctypes.data, x.ctypes.data,
+        lut = np.empty((Hx // 8) * S * EN, np.float32)
+        po.lib().or_lutb_range(0, Hx // 8, lut.ctypes.data, bT.ctypes.data, x.ctypes.data,
                                L * 3 * S, S, EN, 8, 1)
         assert np.array_equal(bits(lut), bits(g[f"L{L}_lut"]))
 

@@ -263,6 +263,9 @@ typedef struct {
     int8_t *sq[3]; uint16_t *ss[3];
     size_t s_rowbytes[3]; int s_bits, s_group, s_inter;
     int s_small;    /* every shared scale finite and below 256 in magnitude */
+    int8_t *lq[2]; uint16_t *ls[2];  /* latent down [latent][H], up [H][latent] */
+    size_t l_rowbytes[2]; int l_bits, l_group;
+    float *lnorm;               /* [latent] or NULL                        */
     int resident;               /* records of this layer in the cache      */
 } layer_t;
 
@@ -274,6 +277,7 @@ typedef struct {
 
 struct warp_hip_ctx {
     warp_hip_cfg cfg;
+    int He;                     /* the experts' width: cfg.latent, or cfg.hidden */
     int S, En, SB, P6, P_max, max_jobs;
     size_t gate_bytes, down_bytes;
     hipStream_t st, cp, la;
@@ -342,6 +346,7 @@ struct warp_hip_ctx {
     int *runs;                    /* prefill: runs of one expert's jobs (first << 3 | count) */
     float *pair_w;
     float *xin, *xout;
+    float *xlat, *ylat, *yup;     /* latent MoE: experts' input and output, up projection */
     float *la_logits;
     int *la_idx;
     float *la_w;
@@ -418,11 +423,12 @@ static int ctx_alloc(warp_hip_ctx *c)
 {
     const warp_hip_cfg *g = &c->cfg;
     const int E = g->n_experts, K = g->top_k, H = g->hidden, I = g->inter, T = g->max_tokens;
+    const int He = c->He, Hm = H > He ? H : He;    /* experts' width; the wider of the two */
     const size_t P = (size_t)T * K;
     c->P_max = (int)P;
     c->max_jobs = (int)(P / WARP_TPJ + (size_t)E + 1);
     if (c->max_jobs < K) c->max_jobs = K;
-    const size_t nvH = (size_t)H / 8, nvI = (size_t)I / 8;
+    const size_t nvH = (size_t)He / 8, nvI = (size_t)I / 8;
     const size_t nblkH = (nvH + WARP_LUT_BLK - 1) / WARP_LUT_BLK, nblkI = (nvI + WARP_LUT_BLK - 1) / WARP_LUT_BLK;
     /* at least two rows: one token's scores and biased scores (wk_router_scored) */
     DMALLOC(c, c->logits, (size_t)(T > 2 ? T : 2) * E * 4);
@@ -431,17 +437,22 @@ static int ctx_alloc(warp_hip_ctx *c)
     DMALLOC(c, c->jobs, (size_t)3 * c->max_jobs * sizeof(warp_job));
     DMALLOC(c, c->njobs, 4 * sizeof(int));
     DMALLOC(c, c->missing, sizeof(int));
-    DMALLOC(c, c->xs, (size_t)T * H * 2 * 2);
+    DMALLOC(c, c->xs, (size_t)T * Hm * 2 * 2);
     DMALLOC(c, c->xscale, (size_t)T * 4);
     DMALLOC(c, c->yg, P * I * 4);
     DMALLOC(c, c->yu, P * I * 4);
-    DMALLOC(c, c->yd, P * H * 4);
+    DMALLOC(c, c->yd, P * He * 4);
     DMALLOC(c, c->xsh, P * I * 2 * 2);
     DMALLOC(c, c->xscaleh, P * 4);
     DMALLOC(c, c->hbuf, P * I * 4);
     DMALLOC(c, c->sho, (size_t)T * H * 4);
     DMALLOC(c, c->xin, (size_t)T * H * 4);
     DMALLOC(c, c->xout, (size_t)T * H * 4);
+    if (g->latent) {
+        DMALLOC(c, c->xlat, (size_t)T * He * 4);
+        DMALLOC(c, c->ylat, (size_t)T * He * 4);
+        DMALLOC(c, c->yup, (size_t)T * H * 4);
+    }
     DMALLOC(c, c->counts, ((size_t)E + 1) * 4);
     DMALLOC(c, c->offsets, ((size_t)E + 1) * 4);
     DMALLOC(c, c->pair_tok, P * 4);
@@ -456,10 +467,10 @@ static int ctx_alloc(warp_hip_ctx *c)
         /* decode: gate+up over K jobs sharing x, then down per job */
         int gr, sp;
         size_t need = 0;
-        if (!wk_lut_plan(I, H, K, 2, 1, c->n_cu, (size_t)-1, &gr, &sp))
+        if (!wk_lut_plan(I, He, K, 2, 1, c->n_cu, (size_t)-1, &gr, &sp))
             need = (size_t)2 * sp * K * (((size_t)I + 63) / 64) * 64;
-        if (!wk_lut_plan(H, I, K, 1, 0, c->n_cu, (size_t)-1, &gr, &sp))
-            need += (size_t)sp * K * (((size_t)H + 63) / 64) * 64;   /* down partials after the gate/up ones */
+        if (!wk_lut_plan(He, I, K, 1, 0, c->n_cu, (size_t)-1, &gr, &sp))
+            need += (size_t)sp * K * (((size_t)He + 63) / 64) * 64;   /* down partials after the gate/up ones */
         c->part_cap = need;
         DMALLOC(c, c->part, need * sizeof(float));
     }
@@ -525,25 +536,28 @@ int warp_hip_open(const warp_hip_cfg *cfg, warp_hip_ctx **out)
     c->SB = fmt_slot(g->fmt);
     c->P6 = g->fmt == WARP_HIP_VQ4P;
     if (g->max_tokens < 1) g->max_tokens = 1;
+    c->He = g->latent > 0 ? g->latent : g->hidden;
+    const int He = c->He;
     int rc = WARP_HIP_E_ARG;
     if (!c->S || g->hidden <= 0 || g->inter <= 0 || g->n_experts <= 0 || g->top_k <= 0 ||
         g->top_k > WARP_MAX_K || g->top_k > g->n_experts || g->n_layers <= 0 || g->n_layers > 65535 ||
-        g->n_experts > 65535 || (g->rec_bytes % 4096) != 0 || g->lookahead < 0) {
+        g->n_experts > 65535 || (g->rec_bytes % 4096) != 0 || g->lookahead < 0 || g->latent < 0 ||
+        (g->latent && g->latent_norm && !(g->norm_eps > 0.0f))) {
         set_err(c, rc, -1, -1, "configuration out of range");
         goto fail;
     }
-    if (!c->P6 && (g->hidden % 32 || g->inter % 32)) {
-        set_err(c, rc, -1, -1, "hidden and inter must be multiples of 32 (4 vector positions)");
+    if (!c->P6 && (He % 32 || g->inter % 32 || g->hidden % 32)) {
+        set_err(c, rc, -1, -1, "hidden, latent and inter must be multiples of 32 (4 vector positions)");
         goto fail;
     }
-    if (g->hidden % 8 || g->inter % 8) {
-        set_err(c, rc, -1, -1, "hidden and inter must be multiples of vec_dim 8");
+    if (He % 8 || g->inter % 8 || g->hidden % 8) {
+        set_err(c, rc, -1, -1, "hidden, latent and inter must be multiples of vec_dim 8");
         goto fail;
     }
-    c->gate_bytes = index_bytes(g->fmt, g->inter, g->hidden);
-    c->down_bytes = index_bytes(g->fmt, g->hidden, g->inter);
+    c->gate_bytes = index_bytes(g->fmt, g->inter, He);
+    c->down_bytes = index_bytes(g->fmt, He, g->inter);
     if (g->rec_bytes && WARP_HDR_BYTES + 2 * c->gate_bytes + c->down_bytes +
-                            2 * (2 * (size_t)g->inter + g->hidden) > g->rec_bytes) {
+                            2 * (2 * (size_t)g->inter + He) > g->rec_bytes) {
         set_err(c, rc, -1, -1, "rec_bytes %zu cannot hold a record of this shape", g->rec_bytes);
         goto fail;
     }
@@ -584,7 +598,7 @@ int warp_hip_open(const warp_hip_cfg *cfg, warp_hip_ctx **out)
         c->n_cu = 256;
     /* the LUT matvec serves decode for the float-LUT formats; it walks the
      * positions two at a time */
-    c->lut_ok = !c->P6 && g->hidden % 16 == 0 && g->inter % 16 == 0;
+    c->lut_ok = !c->P6 && He % 16 == 0 && g->inter % 16 == 0;
     c->L = (layer_t *)calloc((size_t)g->n_layers, sizeof(layer_t));
     if (!c->L) { rc = WARP_HIP_E_NOMEM; goto fail; }
     if ((rc = ctx_alloc(c)) != 0) goto fail;
@@ -610,13 +624,15 @@ void warp_hip_close(warp_hip_ctx *c)
             layer_t *L = &c->L[l];
             hfree(L->books); hfree(L->router); hfree(L->rq); hfree(L->rs); hfree(L->bias);
             for (int k = 0; k < 3; k++) { hfree(L->sq[k]); hfree(L->ss[k]); }
+            for (int k = 0; k < 2; k++) { hfree(L->lq[k]); hfree(L->ls[k]); }
+            hfree(L->lnorm);
         }
     free(c->L);
     void *d[] = { c->logits, c->idx, c->w, c->jobs, c->njobs, c->missing, c->xs, c->xscale, c->yg, c->yu,
                   c->yd, c->xsh, c->xscaleh, c->hbuf, c->shg, c->shu, c->shh, c->sho, c->lut8, c->lut8d,
                   c->lscale, c->lscaled, c->counts, c->offsets, c->pair_tok, c->pair_exp, c->pair_w, c->tok_slots, c->runs,
                   c->xin, c->xout, c->la_logits, c->la_idx, c->la_w, c->table_dev, c->pool, c->part,
-                  c->shxs, c->shxscale, c->tq_dev, c->crc_tmp, c->crc_bad, c->crc_err };
+                  c->shxs, c->shxscale, c->tq_dev, c->crc_tmp, c->crc_bad, c->crc_err, c->xlat, c->ylat, c->yup };
     for (size_t i = 0; i < sizeof d / sizeof d[0]; i++) hfree(d[i]);
     hhfree(c->h_idx); hhfree(c->h_w); hhfree(c->h_la_idx); hhfree(c->h_missing); hhfree(c->staging);
     hhfree(c->h_crc_err); hhfree(c->h_word);
@@ -746,6 +762,35 @@ int warp_hip_set_router_q(warp_hip_ctx *c, int layer, int bits, int group, const
     return 0;
 }
 
+int warp_hip_set_latent(warp_hip_ctx *c, int layer, int bits, int group, const int8_t *down_q,
+                        const uint16_t *down_s, size_t down_rowbytes, const int8_t *up_q, const uint16_t *up_s,
+                        size_t up_rowbytes, const float *norm_w)
+{
+    int rc = check_layer(c, layer);
+    if (rc) return rc;
+    const warp_hip_cfg *g = &c->cfg;
+    if (!g->latent) return set_err(c, WARP_HIP_E_ARG, layer, -1, "the context has no latent width");
+    if ((bits != 8 && bits != 4 && bits != 3) || group <= 0 || !down_q || !down_s || !up_q || !up_s ||
+        (g->latent_norm && !norm_w))
+        return set_err(c, WARP_HIP_E_ARG, layer, -1, "latent projection arguments");
+    layer_t *L = &c->L[layer];
+    const int H = g->hidden, lat = g->latent;
+    const int rows[2] = { lat, H }, cols[2] = { H, lat };
+    const int8_t *q[2] = { down_q, up_q };
+    const uint16_t *sc[2] = { down_s, up_s };
+    const size_t rb[2] = { down_rowbytes, up_rowbytes };
+    for (int k = 0; k < 2; k++) {
+        const int ng = (cols[k] + group - 1) / group;
+        if ((rc = upload(c, (void **)&L->lq[k], q[k], (size_t)rows[k] * rb[k]))) return rc;
+        if ((rc = upload(c, (void **)&L->ls[k], sc[k], (size_t)rows[k] * ng * 2))) return rc;
+        L->l_rowbytes[k] = rb[k];
+    }
+    L->l_bits = bits;
+    L->l_group = group;
+    if (g->latent_norm) return upload(c, (void **)&L->lnorm, norm_w, (size_t)lat * sizeof(float));
+    return 0;
+}
+
 int warp_hip_set_shared(warp_hip_ctx *c, int layer, int bits, int group, int inter_shared,
                         const int8_t *const q[3], const uint16_t *const scales[3], const size_t rowbytes[3])
 {
@@ -817,7 +862,7 @@ static int check_record(warp_hip_ctx *c, const uint8_t *rec, int layer, int expe
     if (c->L[layer].has_books && cbid != (uint16_t)c->L[layer].cb_base)
         return set_err(c, WARP_HIP_E_HEADER, layer, expert, "record codebook_id %u, layer base %d", cbid,
                        c->L[layer].cb_base);
-    const size_t scales = 2u * (2 * (size_t)g->inter + g->hidden);
+    const size_t scales = 2u * (2 * (size_t)g->inter + c->He);
     if (!(off[0] == WARP_HDR_BYTES && (size_t)off[0] + c->gate_bytes <= off[1] &&
           (size_t)off[1] + c->gate_bytes <= off[2] && (size_t)off[2] + c->down_bytes <= off[3] &&
           (size_t)off[3] + scales <= g->rec_bytes))
@@ -953,7 +998,7 @@ static int publish_slot(warp_hip_ctx *c, int layer, int expert, int s, const uin
     const int key = layer * c->cfg.n_experts + expert;
     const uint8_t *slot = c->pool + (size_t)s * c->cfg.rec_bytes;
     if (c->cfg.verify) {
-        const size_t scales = 2u * (2 * (size_t)c->cfg.inter + c->cfg.hidden);
+        const size_t scales = 2u * (2 * (size_t)c->cfg.inter + c->He);
         KRN(c, wk_crc32(slot + WARP_HDR_BYTES, (size_t)off[3] + scales - WARP_HDR_BYTES, c->crc_tmp, NULL,
                         (const uint32_t *)(slot + WARP_HDR_CRC_OFF), key, c->crc_bad, c->cp));
         c->crc_pending = 1;
@@ -1059,7 +1104,7 @@ int warp_hip_put_expert_synth(warp_hip_ctx *c, int layer, int expert, uint64_t s
     uint8_t *slot = c->pool + (size_t)s * g->rec_bytes;
     KRN(c, wk_fill_random(slot, g->rec_bytes, seed, c->cp));
     DEV(c, hipMemcpyAsync(slot, hdr, sizeof hdr, hipMemcpyHostToDevice, c->cp));
-    DEV(c, hipMemcpyAsync(slot + off[3], scales, 2 * (2 * (size_t)g->inter + g->hidden), hipMemcpyHostToDevice, c->cp));
+    DEV(c, hipMemcpyAsync(slot + off[3], scales, 2 * (2 * (size_t)g->inter + c->He), hipMemcpyHostToDevice, c->cp));
     DEV(c, hipStreamSynchronize(c->cp));
     /* a synthetic record carries no checksum: never verified */
     if ((rc = queue_slot(c, key, slot, off, 0))) return rc;
@@ -1446,6 +1491,20 @@ static int lookahead_issue(warp_hip_ctx *c, int layer, int n)
     return prefetch_after(c, layer + 1, ids, m, c->pin_layer == layer ? c->ev_before : c->ev_after, 1);
 }
 
+/* The latent MoE's tail (src/model.c:2913-2921, 2934-2939): the combined
+ * expert outputs ylat [T][latent], RMS-normalised with routed_expert_norm,
+ * projected up to H, plus the shared expert's output, plus the caller's
+ * residual, in that order. */
+static int latent_tail(warp_hip_ctx *c, const layer_t *L, int T, const float *resid, float *out)
+{
+    const warp_hip_cfg *g = &c->cfg;
+    if (g->latent_norm) KRN(c, wk_rmsnorm(c->ylat, L->lnorm, T, c->He, g->norm_eps, c->ylat, c->st));
+    KRN(c, wk_mvq(L->lq[1], L->ls[1], L->l_rowbytes[1], L->l_group, L->l_bits, c->ylat, g->hidden, c->He, T, c->yup,
+                  c->st));
+    KRN(c, wk_add3(c->yup, L->sq[0] ? c->sho : NULL, resid, (size_t)T * g->hidden, out, c->st));
+    return 0;
+}
+
 int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *out_dev, const float *resid_dev,
                         int *idx, float *w)
 {
@@ -1458,21 +1517,30 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
         return set_err(c, WARP_HIP_E_ARG, layer, -1, "layer %d has no codebooks or router", layer);
     const warp_slot *table = c->table_dev + (size_t)layer * E;
     const int use_lut = c->lut_ok && c->mv_path == WARP_HIP_PATH_AUTO && L->books;
+    /* the latent MoE: the experts see xe = down . x and return into the
+     * latent width He; routing and the shared expert stay on x */
+    const int lat = g->latent > 0, He = c->He;
+    if (lat && !L->lq[0]) return set_err(c, WARP_HIP_E_ARG, layer, -1, "layer %d has no latent projections", layer);
+    const float *xe = x_dev;
+    if (lat) {
+        KRN(c, wk_mvq(L->lq[0], L->ls[0], L->l_rowbytes[0], L->l_group, L->l_bits, x_dev, He, H, 1, c->xlat, c->st));
+        xe = c->xlat;
+    }
 
     /* inputs for the gate/up matvecs, then the router */
     if (use_lut) {
         /* the table kernel reads x in f32 */
     } else if (c->P6) {
-        const size_t nvH = (size_t)H / 8, nblkH = (nvH + WARP_LUT_BLK - 1) / WARP_LUT_BLK;
-        KRN(c, wk_lut_p6(x_dev, 1, H, books_kind(c, L, 0), c->lut8, c->lscale, c->st));
-        KRN(c, wk_lut_p6(x_dev, 1, H, books_kind(c, L, 1), c->lut8 + nvH * 256, c->lscale + nblkH, c->st));
+        const size_t nvH = (size_t)He / 8, nblkH = (nvH + WARP_LUT_BLK - 1) / WARP_LUT_BLK;
+        KRN(c, wk_lut_p6(xe, 1, He, books_kind(c, L, 0), c->lut8, c->lscale, c->st));
+        KRN(c, wk_lut_p6(xe, 1, He, books_kind(c, L, 1), c->lut8 + nvH * 256, c->lscale + nblkH, c->st));
     } else {
-        KRN(c, wk_split(x_dev, 1, H, c->xs, c->xscale, c->st));
+        KRN(c, wk_split(xe, 1, He, c->xs, c->xscale, c->st));
     }
     /* with the table kernel, a Q8G/Q4G shared expert runs inside the router
      * launch (gate, up, act) and the combine (down) */
     warp_shared_args sa;
-    const int fuse_shared = use_lut && shared_args(c, L, &sa) && wk_shared_fast_ok(H, &sa);
+    const int fuse_shared = use_lut && !lat && shared_args(c, L, &sa) && wk_shared_fast_ok(H, &sa);
     /* where the device routes with the expert table, the table kernel's
      * gate/up launch does the routing itself (one launch less) */
     const int fuse_route = use_lut && (L->resident == E || !can_fetch(c)) && wk_lut_route_ok(g->fmt, E, K, 1, 0, 2);
@@ -1527,7 +1595,7 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
         const warp_route_args ra = { c->logits, L->bias, table, E, g->router_act, g->renorm, I, g->routed_scale,
                                      c->idx, c->w, c->jobs, c->njobs, c->missing, scored };
         if ((rc = timing_begin(c, 0))) return rc;
-        KRN(c, wk_vq_lut(g->fmt, c->jobs, c->njobs, K, 0, 2, L->books, L->books_x31, x_dev, 1, c->part, c->part_cap, I, H,
+        KRN(c, wk_vq_lut(g->fmt, c->jobs, c->njobs, K, 0, 2, L->books, L->books_x31, xe, 1, c->part, c->part_cap, I, He,
                          c->n_cu, NULL, 0, 0, 0.0f, 0.0f, fuse_route ? &ra : NULL, &sp_gu, c->st));
         if ((rc = timing_end(c))) return rc;
         /* the down launch makes its inputs from the gate/up partials (SwiGLU
@@ -1535,34 +1603,38 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
         const size_t gu_floats = (size_t)2 * sp_gu * K * (((size_t)I + 63) / 64) * 64;
         if ((rc = timing_begin(c, 1))) return rc;
         KRN(c, wk_vq_lut(g->fmt, c->jobs, c->njobs, K, 2, 1, L->books, L->books_x31, NULL, 0, c->part + gu_floats,
-                         c->part_cap - gu_floats, H, I, c->n_cu, c->part, sp_gu, g->act_situ, g->situ_beta,
+                         c->part_cap - gu_floats, He, I, c->n_cu, c->part, sp_gu, g->act_situ, g->situ_beta,
                          g->situ_linear_beta, NULL, &sp_d, c->st));
         d_off = gu_floats;
         if ((rc = timing_end(c))) return rc;
     } else if (c->P6) {
-        const size_t nvH = (size_t)H / 8, nblkH = (nvH + WARP_LUT_BLK - 1) / WARP_LUT_BLK;
-        KRN(c, wk_apply_p6(c->jobs, c->njobs, K, 0, c->lut8, c->lscale, c->yg, I, H, c->st));
-        KRN(c, wk_apply_p6(c->jobs, c->njobs, K, 1, c->lut8 + nvH * 256, c->lscale + nblkH, c->yu, I, H, c->st));
+        const size_t nvH = (size_t)He / 8, nblkH = (nvH + WARP_LUT_BLK - 1) / WARP_LUT_BLK;
+        KRN(c, wk_apply_p6(c->jobs, c->njobs, K, 0, c->lut8, c->lscale, c->yg, I, He, c->st));
+        KRN(c, wk_apply_p6(c->jobs, c->njobs, K, 1, c->lut8 + nvH * 256, c->lscale + nblkH, c->yu, I, He, c->st));
         KRN(c, wk_act(c->yg, c->yu, K, I, g->act_situ, g->situ_beta, g->situ_linear_beta, c->hbuf, c->st));
         KRN(c, wk_lut_p6(c->hbuf, K, I, books_kind(c, L, 2), c->lut8d, c->lscaled, c->st));
-        KRN(c, wk_apply_p6(c->jobs, c->njobs, K, 2, c->lut8d, c->lscaled, c->yd, H, I, c->st));
+        KRN(c, wk_apply_p6(c->jobs, c->njobs, K, 2, c->lut8d, c->lscaled, c->yd, He, I, c->st));
     } else {
         if ((rc = timing_begin(c, 0))) return rc;
-        KRN(c, wk_vq_matvec(g->fmt, c->jobs, c->njobs, K, 0, 2, L->books, c->xs, c->xscale, yk, I, H, 1, c->st));
+        KRN(c, wk_vq_matvec(g->fmt, c->jobs, c->njobs, K, 0, 2, L->books, c->xs, c->xscale, yk, I, He, 1, c->st));
         if ((rc = timing_end(c))) return rc;
         KRN(c, wk_act_split(c->yg, c->yu, K, I, g->act_situ, g->situ_beta, g->situ_linear_beta, c->xsh, c->xscaleh,
                             NULL, c->st));
         if ((rc = timing_begin(c, 1))) return rc;
-        KRN(c, wk_vq_matvec(g->fmt, c->jobs, c->njobs, K, 2, 1, L->books, c->xsh, c->xscaleh, yk, H, I, 1, c->st));
+        KRN(c, wk_vq_matvec(g->fmt, c->jobs, c->njobs, K, 2, 1, L->books, c->xsh, c->xscaleh, yk, He, I, 1, c->st));
         if ((rc = timing_end(c))) return rc;
     }
     if (L->sq[0] && !fuse_shared && (rc = shared_ffn(c, L, x_dev, 1))) return rc;
+    /* the weighted sum of the experts: into the latent width first on a
+     * latent MoE, else straight into out with the shared expert and residual */
+    const float *add0 = lat ? NULL : L->sq[0] && !fuse_shared ? c->sho : NULL, *add1 = lat ? NULL : resid_dev;
+    float *ysum = lat ? c->ylat : out_dev;
     if (use_lut)
-        KRN(c, wk_combine_lut(c->jobs + 2 * (size_t)K, c->part + d_off, sp_d, K, c->w, K, H,
-                              L->sq[0] && !fuse_shared ? c->sho : NULL, resid_dev, c->missing,
-                              fuse_shared ? &sa : NULL, out_dev, c->st));
+        KRN(c, wk_combine_lut(c->jobs + 2 * (size_t)K, c->part + d_off, sp_d, K, c->w, K, He, add0, add1, c->missing,
+                              fuse_shared ? &sa : NULL, ysum, c->st));
     else
-        KRN(c, wk_combine(c->yd, c->w, K, H, L->sq[0] ? c->sho : NULL, resid_dev, c->missing, out_dev, c->st));
+        KRN(c, wk_combine(c->yd, c->w, K, He, add0, add1, c->missing, ysum, c->st));
+    if (lat && (rc = latent_tail(c, L, 1, resid_dev, out_dev))) return rc;
     DEV(c, hipEventRecord(c->ev_after, c->st));
 
     if ((rc = lookahead_issue(c, layer, n_la))) return rc;
@@ -1583,7 +1655,7 @@ int warp_hip_expert_ffn(warp_hip_ctx *c, int layer, int expert, const float *x_d
     if (rc) return rc;
     const warp_hip_cfg *g = &c->cfg;
     const layer_t *L = &c->L[layer];
-    const int H = g->hidden, I = g->inter;
+    const int H = c->He, I = g->inter; /* the expert's width: latent on a latent MoE */
     if (expert < 0 || expert >= g->n_experts || !x_dev || !out_dev)
         return set_err(c, WARP_HIP_E_ARG, layer, expert, "expert_ffn arguments");
     if (!L->has_books) return set_err(c, WARP_HIP_E_ARG, layer, -1, "layer %d has no codebooks", layer);
@@ -1649,7 +1721,7 @@ static int chunk_experts(warp_hip_ctx *c, int layer, const float *X_dev, int T, 
 {
     const warp_hip_cfg *g = &c->cfg;
     const layer_t *L = &c->L[layer];
-    const int E = g->n_experts, K = g->top_k, H = g->hidden, I = g->inter, P = T * K;
+    const int E = g->n_experts, K = g->top_k, H = c->He, I = g->inter, P = T * K; /* H: the experts' width */
     const warp_slot *table = c->table_dev + (size_t)layer * E;
     KRN(c, wait_copies(c));
     KRN(c, wk_plan_chunk(c->idx, c->w, T, K, E, table, c->counts, c->offsets, c->pair_tok, c->pair_exp, c->pair_w,
@@ -1696,6 +1768,14 @@ int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *ou
     if (!L->has_books || (!L->router && !L->rq))
         return set_err(c, WARP_HIP_E_ARG, layer, -1, "layer %d has no codebooks or router", layer);
     const int P = T * K;
+    const int lat = g->latent > 0;
+    if (lat && !L->lq[0]) return set_err(c, WARP_HIP_E_ARG, layer, -1, "layer %d has no latent projections", layer);
+    /* the experts' inputs: x itself, or its latent projection */
+    const float *Xe = X_dev;
+    if (lat) {
+        KRN(c, wk_mvq(L->lq[0], L->ls[0], L->l_rowbytes[0], L->l_group, L->l_bits, X_dev, c->He, H, T, c->xlat, c->st));
+        Xe = c->xlat;
+    }
 
     KRN(c, logits_of(c, L, X_dev, T, c->logits, c->st));
     KRN(c, wk_route(c->logits, L->bias, E, K, T, g->router_act, g->renorm, g->routed_scale, c->idx, c->w, NULL, NULL,
@@ -1716,7 +1796,7 @@ int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *ou
         for (int e = 0; e < E; e++) if (used[e]) ids[n++] = e;
         free(used);
         if (n == 0) {
-            rc = chunk_experts(c, layer, X_dev, T, 0, E - 1, 1);
+            rc = chunk_experts(c, layer, Xe, T, 0, E - 1, 1);
         } else {
             /* Windows of distinct experts that the cache holds at once, in
              * ascending id: the reference streams a chunk's experts through
@@ -1735,18 +1815,23 @@ int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *ou
                     if (e != hipSuccess) { rc = dev_err(c, "window order", e); break; }
                 }
                 if ((rc = ensure_selected(c, layer, ids + a, b - a)) != 0) break;
-                rc = chunk_experts(c, layer, X_dev, T, ids[a], ids[b - 1], a == 0);
+                rc = chunk_experts(c, layer, Xe, T, ids[a], ids[b - 1], a == 0);
             }
         }
         free(ids);
         if (rc) return rc;
     } else {
         release_hold(c, layer);
-        if ((rc = chunk_experts(c, layer, X_dev, T, 0, E - 1, 1))) return rc;
+        if ((rc = chunk_experts(c, layer, Xe, T, 0, E - 1, 1))) return rc;
     }
     if (L->sq[0] && (rc = shared_ffn(c, L, X_dev, T))) return rc;
-    KRN(c, wk_combine_chunk(c->yd, c->tok_slots, c->pair_w, T, K, H, L->sq[0] ? c->sho : NULL, resid_dev, out_dev,
-                            c->st));
+    if (lat) {
+        KRN(c, wk_combine_chunk(c->yd, c->tok_slots, c->pair_w, T, K, c->He, NULL, NULL, c->ylat, c->st));
+        if ((rc = latent_tail(c, L, T, resid_dev, out_dev))) return rc;
+    } else {
+        KRN(c, wk_combine_chunk(c->yd, c->tok_slots, c->pair_w, T, K, H, L->sq[0] ? c->sho : NULL, resid_dev, out_dev,
+                                c->st));
+    }
     DEV(c, hipEventRecord(c->ev_after, c->st));
     if ((rc = lookahead_issue(c, layer, n_la))) return rc;
     DEV(c, hipMemcpyAsync(c->h_missing, c->missing, sizeof(int), hipMemcpyDeviceToHost, c->st));
@@ -1779,8 +1864,8 @@ int warp_hip_moe_chunk_host(warp_hip_ctx *c, int layer, const float *X, float *o
 static int matrix_shape(const warp_hip_ctx *c, int kind, int *M, int *N)
 {
     if (kind < 0 || kind > 2) return -1;
-    *M = kind == 2 ? c->cfg.hidden : c->cfg.inter;
-    *N = kind == 2 ? c->cfg.inter : c->cfg.hidden;
+    *M = kind == 2 ? c->He : c->cfg.inter;
+    *N = kind == 2 ? c->cfg.inter : c->He;
     return 0;
 }
 
@@ -1796,7 +1881,7 @@ int warp_hip_vq_matvec(warp_hip_ctx *c, int layer, int kind, const uint8_t *rec_
     DEV(c, hipMemcpy(hdr, rec_dev, sizeof hdr, hipMemcpyDeviceToHost));
     uint32_t off[4];
     memcpy(off, hdr + 20, 16);
-    if (off[3] + 2 * (2 * (size_t)c->cfg.inter + c->cfg.hidden) > c->cfg.rec_bytes || off[kind] >= off[3])
+    if (off[3] + 2 * (2 * (size_t)c->cfg.inter + c->He) > c->cfg.rec_bytes || off[kind] >= off[3])
         return set_err(c, WARP_HIP_E_HEADER, layer, -1, "record offsets");
     warp_job jb;
     memset(&jb, 0, sizeof jb);
@@ -1847,7 +1932,7 @@ int warp_hip_decode_weights(warp_hip_ctx *c, int layer, int kind, const uint8_t 
     uint32_t off[4];
     memcpy(off, hdr + 20, 16);
     const size_t soff = kind == 0 ? 0 : kind == 1 ? (size_t)c->cfg.inter : 2 * (size_t)c->cfg.inter;
-    if (off[3] + 2 * (2 * (size_t)c->cfg.inter + c->cfg.hidden) > c->cfg.rec_bytes || off[kind] >= off[3])
+    if (off[3] + 2 * (2 * (size_t)c->cfg.inter + c->He) > c->cfg.rec_bytes || off[kind] >= off[3])
         return set_err(c, WARP_HIP_E_HEADER, layer, -1, "record offsets");
     KRN(c, wk_decode_weights(c->cfg.fmt, rec_dev + off[kind], (const uint16_t *)(rec_dev + off[3]) + soff,
                              books_kind(c, L, kind), M, N, W_dev, c->st));

@@ -3240,6 +3240,56 @@ extern "C" int wk_set_slots(warp_slot *table, const warp_slot_upd *u, int n, con
     return 0;
 }
 
+// ---- the latent MoE's tail ----------------------------------------------------------
+//
+// waste_rmsnorm (src/model.c:132-138) per token, in place allowed: o = x *
+// r * w with r = 1 / sqrt(sum x^2 / n + eps). The sum runs in a fixed tree
+// (each thread a strided partial, then the waves, in order), so it is
+// deterministic; it differs from the reference's sequential sum by fp32
+// rounding only. One block per token.
+__global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x, const float *__restrict__ w, int n,
+                                                 float eps, float *__restrict__ o) {
+    __shared__ float red[4];
+    const float *xt = x + (size_t)blockIdx.x * n;
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < n; i += 256) s = __fadd_rn(s, __fmul_rn(xt[i], xt[i]));
+    s = wave_sum(s);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    s = __fadd_rn(__fadd_rn(red[0], red[1]), __fadd_rn(red[2], red[3]));
+    const float r = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(s, (float)n), eps)));
+    float *ot = o + (size_t)blockIdx.x * n;
+    for (int i = threadIdx.x; i < n; i += 256) ot[i] = __fmul_rn(__fmul_rn(xt[i], r), w[i]);
+}
+
+extern "C" int wk_rmsnorm(const float *x, const float *w, int T, int n, float eps, float *o, void *stream) {
+    if (!x || !w || !o || T <= 0 || n <= 0) return -1;
+    hipLaunchKernelGGL(k_rmsnorm, dim3(T), dim3(256), 0, (hipStream_t)stream, x, w, n, eps, o);
+    CHECK_LAUNCH();
+    return 0;
+}
+
+// out = (y + a0) + a1 elementwise, each addend optional: the routed part, then
+// the shared expert, then the caller's residual (src/model.c:2934-2939).
+__global__ __launch_bounds__(256) void k_add3(const float *__restrict__ y, const float *a0, const float *a1, size_t n,
+                                              float *out) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+        float v = y[i];
+        if (a0) v = __fadd_rn(v, a0[i]);
+        if (a1) v = __fadd_rn(v, a1[i]);
+        out[i] = v;
+    }
+}
+
+extern "C" int wk_add3(const float *y, const float *a0, const float *a1, size_t n, float *out, void *stream) {
+    if (!y || !out || n == 0) return -1;
+    const size_t blocks = (n + 255) / 256;
+    hipLaunchKernelGGL(k_add3, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, (hipStream_t)stream, y,
+                       a0, a1, n, out);
+    CHECK_LAUNCH();
+    return 0;
+}
+
 // One expert's three matvec jobs from its device table entry (one input,
 // one output row block each), its combine weight 1 and the job counts:
 // the single-expert FFN without routing.

@@ -262,6 +262,11 @@ int wk_plan_chunk(const int *idx, const float *w, int T, int K, int E,
 int wk_combine_chunk(const float *y, const int *tok_slots, const float *pair_w, int T, int K, int H,
                      const float *add0, const float *add1, float *out, void *stream);
 
+/* The latent MoE's tail: RMS norm per token of [T][n] (o may be x), and
+ * out = (y + a0) + a1 over n floats (a0, a1 may be NULL). */
+int wk_rmsnorm(const float *x, const float *w, int T, int n, float eps, float *o, void *stream);
+int wk_add3(const float *y, const float *a0, const float *a1, size_t n, float *out, void *stream);
+
 /* The single-expert FFN's jobs from one device table entry: jobs[0..2] =
  * gate, up, down (list stride 1, input 0, output 0), njobs = {1, 1, 1, 0},
  * w[0] = 1; a missing record gives empty lists and sets *missing. */

@@ -38,7 +38,8 @@ class Cfg(C.Structure):
         ("router_act", C.c_int), ("router_strict", C.c_int), ("act_situ", C.c_int),
         ("situ_beta", C.c_float), ("situ_linear_beta", C.c_float), ("max_tokens", C.c_int),
         ("rec_bytes", C.c_size_t), ("cache_bytes", C.c_size_t), ("verify", C.c_int),
-        ("lookahead", C.c_int), ("device", C.c_int),
+        ("lookahead", C.c_int), ("device", C.c_int), ("latent", C.c_int), ("latent_norm", C.c_int),
+        ("norm_eps", C.c_float),
     ]
 
 
@@ -69,6 +70,8 @@ SIGNATURES = {
                                         C.c_size_t, C.c_void_p]),
     "warp_hip_set_shared": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p * 3,
                                       C.c_void_p * 3, C.c_size_t * 3]),
+    "warp_hip_set_latent": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_size_t,
+                                      C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
     "warp_hip_set_fetch": (C.c_int, [C.c_void_p, FETCH_FN, C.c_void_p]),
     "warp_hip_set_fetch_host": (C.c_int, [C.c_void_p, FETCH_HOST_FN, C.c_void_p]),
     "warp_hip_host_alloc": (C.c_void_p, [C.c_void_p, C.c_size_t]),
@@ -145,10 +148,11 @@ class Context:
     def __init__(self, *, hidden, inter, n_experts, top_k, n_layers, fmt, renorm=True,
                  routed_scale=1.0, router_act=ROUTE_SIGMOID, router_strict=False, act_situ=False,
                  situ_beta=1.0, situ_linear_beta=0.0, max_tokens=1, rec_bytes, cache_bytes,
-                 verify=False, lookahead=0, device=0):
+                 verify=False, lookahead=0, device=0, latent=0, latent_norm=True, norm_eps=1e-5):
         self.cfg = Cfg(hidden, inter, n_experts, top_k, n_layers, FMT.get(fmt, fmt), int(renorm),
                        routed_scale, router_act, int(router_strict), int(act_situ), situ_beta,
-                       situ_linear_beta, max_tokens, rec_bytes, cache_bytes, int(verify), lookahead, device)
+                       situ_linear_beta, max_tokens, rec_bytes, cache_bytes, int(verify), lookahead, device,
+                       latent, int(latent_norm), norm_eps)
         self.h = C.c_void_p()
         self._keep = []
         rc = lib().warp_hip_open(C.byref(self.cfg), C.byref(self.h))
@@ -196,6 +200,12 @@ class Context:
         sa = (C.c_void_p * 3)(*[_addr(s) for s in ss])
         ra = (C.c_size_t * 3)(*rowbytes)
         self._check(lib().warp_hip_set_shared(self.h, layer, bits, group, inter_shared, qa, sa, ra))
+
+    def set_latent(self, layer, bits, group, down, up, norm_w=None):
+        """down/up: (payload, scales, rowbytes) of routed_expert_down_proj
+        [latent][H] and routed_expert_up_proj [H][latent]."""
+        self._check(lib().warp_hip_set_latent(self.h, layer, bits, group, _addr(down[0]), _addr(down[1]), down[2],
+                                              _addr(up[0]), _addr(up[1]), up[2], _addr(norm_w)))
 
     # -- experts
     def put_expert(self, layer, expert, rec):
@@ -392,9 +402,11 @@ def vq_lloyd(X, C):
                      "vq_lloyd")
 
 
-def load_container_model(ctx: Context, model, layers=None):
+def load_container_model(ctx: Context, model, layers=None, records=True):
     """Upload one tests/golden/container.Model (or anything with the same
-    attributes) into a context: codebooks, routers, shared experts, records."""
+    attributes) into a context: codebooks, routers, latent projections,
+    shared experts and (unless records is False, for a context that fetches
+    them on a miss) the expert records."""
     import numpy as np
     spec = model.spec
     S = {"VQ3R": 3, "VQ2R": 2, "VQ4P": 4, "VQ12": 2}[spec.fmt]
@@ -409,10 +421,14 @@ def load_container_model(ctx: Context, model, layers=None):
         else:
             pl, sc, rb, bits, group = lay.router_q
             ctx.set_router_q(L, bits, group, np.ascontiguousarray(pl), np.ascontiguousarray(sc), rb, lay.bias)
+        if getattr(lay, "latent", None) is not None:
+            dq, uq, nw = lay.latent
+            ctx.set_latent(L, dq[3], dq[4], (np.ascontiguousarray(dq[0]), np.ascontiguousarray(dq[1]), dq[2]),
+                           (np.ascontiguousarray(uq[0]), np.ascontiguousarray(uq[1]), uq[2]), nw)
         if lay.shared:
             ctx.set_shared(L, spec.shared_bits, spec.shared_group, spec.inter * spec.n_shared,
                            [np.ascontiguousarray(s[0]) for s in lay.shared],
                            [np.ascontiguousarray(s[1]) for s in lay.shared], [s[2] for s in lay.shared])
-        for e, rec in enumerate(lay.records):
+        for e, rec in enumerate(lay.records if records else ()):
             if rec is not None:                  # experts without a record stay out of the cache
                 ctx.put_expert(L, e, np.frombuffer(rec, np.uint8))
