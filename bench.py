@@ -205,11 +205,13 @@ def kernels_sha256():
         return hashlib.sha256(f.read()).hexdigest()
 
 
-def measured_traffic(kernel):
+def measured_traffic(kernel, launches):
     """HBM traffic per launch of the expert matvec from the committed counter
     summary (L2-to-memory read requests by size, write requests), when it
     was taken on this kernel from this very kernels.hip (its sha256 is
-    recorded with the counters); None otherwise, with the reason."""
+    recorded with the counters); None otherwise, with the reason. launches:
+    the launch names the summary must hold ("fused", or "gate_up" and
+    "down")."""
     try:
         with open(TRAFFIC_FILE) as f:
             t = json.load(f)
@@ -219,8 +221,37 @@ def measured_traffic(kernel):
         return None, f"counters were taken on {t.get('kernel')}"
     if t.get("kernels_sha256") != kernels_sha256():
         return None, "counters were taken on another build of kernels.hip"
-    return ({k: t[k]["read_bytes"] + t[k]["write_bytes"] for k in ("gate_up", "down")} | {"source": t["source"]},
-            None)
+    if any(k not in t for k in launches):
+        return None, "the counter summary does not hold these launches"
+    return {k: t[k]["read_bytes"] + t[k]["write_bytes"] for k in launches} | {"source": t["source"]}, None
+
+
+def matvec_roofline(kms, kn, b0, b1, path):
+    """The expert matvec's roofline terms from the per-launch timing classes:
+    class 0 alone is the fused launch (gate/up, down and combine in one),
+    else class 0 the gate/up and class 1 the down launches. b0, b1: the
+    algorithmic bytes (codes and row scales of the picks) of gate/up and of
+    down for one token."""
+    fused = kn[0] > 0 and kn[1] == 0
+    if path == "mfma":
+        kernel = "k_vq_mfma"
+    else:
+        kernel = "k_moe_fused" if fused else "k_vq_lut"
+    if fused:
+        t = kms[0]
+        nbytes = kn[0] * (b0 + b1)
+        per = {"bytes_per_launch": {"fused": b0 + b1},
+               "avg_launch_us": {"fused": round(kms[0] / kn[0] * 1e3, 2)},
+               "what": kernel + " (gate/up, down and combine of the routed experts in one launch per layer)"}
+    else:
+        t = kms[0] + kms[1]
+        nbytes = kn[0] * b0 + kn[1] * b1
+        per = {"bytes_per_launch": {"gate_up": b0, "down": b1},
+               "avg_launch_us": {"gate_up": round(kms[0] / max(kn[0], 1) * 1e3, 2),
+                                 "down": round(kms[1] / max(kn[1], 1) * 1e3, 2)},
+               "what": kernel + " (expert matvec, gate/up and down launches)"}
+    achieved = nbytes / (t / 1e3) / 1e9 if t > 0 else None
+    return kernel, fused, achieved, per
 
 
 def cpu_threads():
@@ -660,12 +691,10 @@ def run_kimi_decode(args):
     n_lt = args.steps * layers
     b0 = KK * (2 * gate + 2 * 2 * KI)
     b1 = KK * (down + 2 * KH)
-    kern_ms = kms[0] + kms[1]
-    achieved = (kn[0] * b0 + kn[1] * b1) / (kern_ms / 1e3) / 1e9
+    kernel, fused, achieved, per = matvec_roofline(kms, kn, b0, b1, args.matvec_path)
     per_layer = (KK * (2 * gate + down + scales_b) + shared_bytes + KE * KH * 4 + 3 * S * EN * 8 * 2 + KE * 4
                  + 2 * KH * 4)
     layer_gbs = per_layer * n_lt / (ms / 1e3) / 1e9
-    kernel = "k_vq_lut" if args.matvec_path == "auto" else "k_vq_mfma"
     return {
         "metric": "MoE-layer decode tokens/s, Kimi-Linear shape, 1 MI355X",
         "value": round(n_lt / (ms / 1e3), 2),
@@ -684,10 +713,9 @@ def run_kimi_decode(args):
         "layer_hbm_frac": round(layer_gbs / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": kernel + " (expert matvec, gate/up and down launches)",
-                     "bytes_per_launch": {"gate_up": b0, "down": b1},
-                     "avg_launch_us": {"gate_up": round(kms[0] / max(kn[0], 1) * 1e3, 2),
-                                       "down": round(kms[1] / max(kn[1], 1) * 1e3, 2)},
+                     "kernel": per["what"],
+                     "bytes_per_launch": per["bytes_per_launch"],
+                     "avg_launch_us": per["avg_launch_us"],
                      "router_avg_us": round(kms[2] / max(kn[2], 1) * 1e3, 2)},
         "wall_s": round(wall, 3),
         "cpu_baseline": None if args.no_cpu else cpu_baseline_kimi_decode(args, args.cpu_seconds),
@@ -1071,8 +1099,9 @@ def main():
     ap.add_argument("--no-graph", dest="graph", action="store_false",
                     help="k3-decode, kimi-decode: launch every kernel from the host instead of replaying one "
                          "captured step")
-    ap.add_argument("--matvec-path", choices=["auto", "mfma"], default="auto",
-                    help="expert matvec kernel: auto = the LUT kernel, mfma = decode-then-dot on the matrix cores")
+    ap.add_argument("--matvec-path", choices=["auto", "mfma", "fused"], default="auto",
+                    help="expert matvec kernel: auto = the LUT kernel, mfma = decode-then-dot on the matrix cores, "
+                         "fused = the LUT kernel's gate/up, down and combine in one launch per layer")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="before timing, one device-to-device copy of this many MiB (a known-size "
                          "kernel for scaling the profiler's traffic counters)")
@@ -1122,15 +1151,13 @@ def main():
     gate, down, scales_b, _ = rec_layout()
     b0 = K * (2 * gate + 2 * 2 * I)               # codes + gate/up row scales per gate/up launch
     b1 = K * (down + 2 * H)                       # codes + down row scales per down launch
-    kern_ms = kms[0] + kms[1]
-    kern_bytes = kn[0] * b0 + kn[1] * b1
-    achieved = kern_bytes / (kern_ms / 1e3) / 1e9
+    kernel, fused, achieved, per = matvec_roofline(kms, kn, b0, b1, args.matvec_path)
     layer_gbs = layer_bytes() * layer_tokens / (ms / 1e3) / 1e9
-    kernel = "k_vq_lut" if args.matvec_path == "auto" else "k_vq_mfma"
-    tr, tr_why = measured_traffic(kernel)
+    tr, tr_why = measured_traffic(kernel, ("fused",) if fused else ("gate_up", "down"))
     traffic = None
     if tr:
-        traffic = round((kn[0] * tr["gate_up"] + kn[1] * tr["down"]) / max(kn[0] + kn[1], 1))
+        traffic = tr["fused"] if fused else round((kn[0] * tr["gate_up"] + kn[1] * tr["down"]) /
+                                                  max(kn[0] + kn[1], 1))
     cpu = None if args.no_cpu else cpu_baseline(args, args.cpu_seconds)
     rec = {
         "metric": METRIC,
@@ -1155,14 +1182,12 @@ def main():
         "layer_bytes": layer_bytes(),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "traffic_per_launch": ({"gate_up": tr["gate_up"], "down": tr["down"], "source": tr["source"]}
-                                            if tr else {"unmeasured": tr_why}),
-                     "kernel": kernel + " (expert matvec, gate/up and down launches)",
+                     "traffic_per_launch": tr if tr else {"unmeasured": tr_why},
+                     "kernel": per["what"],
                      "timing": "HIP events around each launch on the compute stream, in a second pass of the "
                                "same steps",
-                     "bytes_per_launch": {"gate_up": b0, "down": b1},
-                     "avg_launch_us": {"gate_up": round(kms[0] / max(kn[0], 1) * 1e3, 2),
-                                       "down": round(kms[1] / max(kn[1], 1) * 1e3, 2)},
+                     "bytes_per_launch": per["bytes_per_launch"],
+                     "avg_launch_us": per["avg_launch_us"],
                      "router_avg_us": round(kms[2] / max(kn[2], 1) * 1e3, 2)},
         "cache": {"hits": st["hits"], "misses": st["misses"], "resident": st["resident"]},
         "wall_s": round(wall, 3),

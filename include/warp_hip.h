@@ -323,10 +323,15 @@ int warp_hip_put_expert_synth(warp_hip_ctx *c, int layer, int expert, uint64_t s
 /* Expert matvec kernels for single-token decode (no counterpart in the
  * reference, which has one CPU path). AUTO (the default) runs the LUT
  * kernel -- the reference's LUT algorithm, fp32 tables in LDS -- for the
- * float-LUT formats when hidden and inter are multiples of 16; MFMA forces
- * the decode-then-dot matrix-core kernel that prefill always uses. Applies
- * to warp_hip_moe_decode* and warp_hip_vq_matvec. */
-enum { WARP_HIP_PATH_AUTO = 0, WARP_HIP_PATH_MFMA = 1 };
+ * float-LUT formats when hidden and inter are multiples of 16, as gate/up,
+ * down and combine launches; MFMA forces the decode-then-dot matrix-core
+ * kernel that prefill always uses; LUT_FUSED runs the LUT kernel's gate/up,
+ * down and combine as work items of one launch per layer where the token's
+ * routing runs inside it (the same results bit for bit; slower than AUTO at
+ * the K3 shape, where the waits between its work items cost more than the
+ * launch boundaries they replace). Applies to warp_hip_moe_decode* and
+ * warp_hip_vq_matvec. */
+enum { WARP_HIP_PATH_AUTO = 0, WARP_HIP_PATH_MFMA = 1, WARP_HIP_PATH_LUT_FUSED = 2 };
 int warp_hip_set_matvec_path(warp_hip_ctx *c, int path);
 /* Per-launch timing with HIP events on the compute stream: when on, every
  * warp_hip_moe_decode brackets its launches of class 0 (gate/up expert

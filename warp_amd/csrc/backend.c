@@ -339,6 +339,7 @@ struct warp_hip_ctx {
     int8_t *lut8, *lut8d;
     float *lscale, *lscaled;
     float *part;                /* LUT matvec partial sums                 */
+    unsigned *fz_sync;          /* the fused decode launch's counters (zero between launches) */
     size_t part_cap;            /* floats                                  */
     int n_cu, lut_ok, mv_path;
     int *counts, *offsets, *pair_tok, *pair_exp;
@@ -479,6 +480,10 @@ static int ctx_alloc(warp_hip_ctx *c)
         DMALLOC(c, c->lscale, (size_t)T * 2 * nblkH * 4);
         DMALLOC(c, c->lut8d, P * nvI * 256);
         DMALLOC(c, c->lscaled, P * nblkI * 4);
+    }
+    if (c->lut_ok) {
+        DMALLOC(c, c->fz_sync, WARP_FZ_WORDS * sizeof(unsigned));
+        DEV(c, hipMemset(c->fz_sync, 0, WARP_FZ_WORDS * sizeof(unsigned)));
     }
     DEV(c, hipMemset(c->missing, 0, sizeof(int)));
     DEV(c, hipHostMalloc((void **)&c->h_idx, P * 4, 0));
@@ -632,7 +637,8 @@ void warp_hip_close(warp_hip_ctx *c)
                   c->yd, c->xsh, c->xscaleh, c->hbuf, c->shg, c->shu, c->shh, c->sho, c->lut8, c->lut8d,
                   c->lscale, c->lscaled, c->counts, c->offsets, c->pair_tok, c->pair_exp, c->pair_w, c->tok_slots, c->runs,
                   c->xin, c->xout, c->la_logits, c->la_idx, c->la_w, c->table_dev, c->pool, c->part,
-                  c->shxs, c->shxscale, c->tq_dev, c->crc_tmp, c->crc_bad, c->crc_err, c->xlat, c->ylat, c->yup };
+                  c->shxs, c->shxscale, c->tq_dev, c->crc_tmp, c->crc_bad, c->crc_err, c->xlat, c->ylat, c->yup,
+                  c->fz_sync };
     for (size_t i = 0; i < sizeof d / sizeof d[0]; i++) hfree(d[i]);
     hhfree(c->h_idx); hhfree(c->h_w); hhfree(c->h_la_idx); hhfree(c->h_missing); hhfree(c->staging);
     hhfree(c->h_crc_err); hhfree(c->h_word);
@@ -669,7 +675,11 @@ static int take_missing(warp_hip_ctx *c)
     DEV(c, hipMemcpy(c->h_missing, c->missing, sizeof(int), hipMemcpyDeviceToHost));
     c->missing_pending = 0;
     if (*c->h_missing) {
+        const int flag = *c->h_missing;
         DEV(c, hipMemset(c->missing, 0, sizeof(int)));
+        if (flag & 4)
+            return set_err(c, WARP_HIP_E_DEVICE, -1, -1,
+                           "a fused decode launch gave up waiting for its work items: its outputs are not valid");
         return set_err(c, WARP_HIP_E_MISSING, -1, -1,
                        "a selected expert was not resident: the affected layers were not computed");
     }
@@ -1337,7 +1347,8 @@ static int timing_end(warp_hip_ctx *c)
 
 int warp_hip_set_matvec_path(warp_hip_ctx *c, int path)
 {
-    if (!c || (path != WARP_HIP_PATH_AUTO && path != WARP_HIP_PATH_MFMA)) return WARP_HIP_E_ARG;
+    if (!c || (path != WARP_HIP_PATH_AUTO && path != WARP_HIP_PATH_MFMA && path != WARP_HIP_PATH_LUT_FUSED))
+        return WARP_HIP_E_ARG;
     c->mv_path = path;
     return 0;
 }
@@ -1516,7 +1527,7 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
     if (!L->has_books || (!L->router && !L->rq))
         return set_err(c, WARP_HIP_E_ARG, layer, -1, "layer %d has no codebooks or router", layer);
     const warp_slot *table = c->table_dev + (size_t)layer * E;
-    const int use_lut = c->lut_ok && c->mv_path == WARP_HIP_PATH_AUTO && L->books;
+    const int use_lut = c->lut_ok && c->mv_path != WARP_HIP_PATH_MFMA && L->books;
     /* the latent MoE: the experts see xe = down . x and return into the
      * latent width He; routing and the shared expert stay on x */
     const int lat = g->latent > 0, He = c->He;
@@ -1586,6 +1597,24 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
     }
     DEV(c, hipEventRecord(c->ev_before, c->st));
 
+    /* the weighted sum of the experts: into the latent width first on a
+     * latent MoE, else straight into out with the shared expert and residual */
+    const float *add0 = lat ? NULL : L->sq[0] && !fuse_shared ? c->sho : NULL, *add1 = lat ? NULL : resid_dev;
+    float *ysum = lat ? c->ylat : out_dev;
+    if (use_lut && fuse_route && !fuse_shared && c->mv_path == WARP_HIP_PATH_LUT_FUSED) {
+        /* gate/up, down and the combine in one launch */
+        if (L->sq[0] && (rc = shared_ffn(c, L, x_dev, 1))) return rc;
+        const warp_route_args ra = { c->logits, L->bias, table, E, g->router_act, g->renorm, I, g->routed_scale,
+                                     c->idx, c->w, c->jobs, c->njobs, c->missing, scored };
+        if ((rc = timing_begin(c, 0))) return rc;
+        KRN(c, wk_moe_fused(g->fmt, L->books, L->books_x31, xe, K, I, He, c->part, c->part_cap, c->n_cu,
+                            g->act_situ, g->situ_beta, g->situ_linear_beta, &ra, add0, add1, ysum, c->fz_sync,
+                            WARP_FZ_WORDS, c->st));
+        if ((rc = timing_end(c))) return rc;
+        c->missing_pending = 1;
+        goto tail;
+    }
+
     /* gate and up, activation, down */
     float *yk[3] = { c->yg, c->yu, c->yd };
     int sp_d = 0;
@@ -1625,15 +1654,12 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
         if ((rc = timing_end(c))) return rc;
     }
     if (L->sq[0] && !fuse_shared && (rc = shared_ffn(c, L, x_dev, 1))) return rc;
-    /* the weighted sum of the experts: into the latent width first on a
-     * latent MoE, else straight into out with the shared expert and residual */
-    const float *add0 = lat ? NULL : L->sq[0] && !fuse_shared ? c->sho : NULL, *add1 = lat ? NULL : resid_dev;
-    float *ysum = lat ? c->ylat : out_dev;
     if (use_lut)
         KRN(c, wk_combine_lut(c->jobs + 2 * (size_t)K, c->part + d_off, sp_d, K, c->w, K, He, add0, add1, c->missing,
                               fuse_shared ? &sa : NULL, ysum, c->st));
     else
         KRN(c, wk_combine(c->yd, c->w, K, He, add0, add1, c->missing, ysum, c->st));
+tail:
     if (lat && (rc = latent_tail(c, L, 1, resid_dev, out_dev))) return rc;
     DEV(c, hipEventRecord(c->ev_after, c->st));
 
@@ -1666,7 +1692,7 @@ int warp_hip_expert_ffn(warp_hip_ctx *c, int layer, int expert, const float *x_d
     KRN(c, wk_expert_jobs(c->table_dev + (size_t)layer * g->n_experts + expert, I, c->jobs, c->njobs, c->w,
                           c->missing, c->st));
     c->missing_pending = 1;
-    if (c->lut_ok && c->mv_path == WARP_HIP_PATH_AUTO) {
+    if (c->lut_ok && c->mv_path != WARP_HIP_PATH_MFMA) {
         int sp_gu = 0, sp_d = 0;
         if ((rc = timing_begin(c, 0))) return rc;
         KRN(c, wk_vq_lut(g->fmt, c->jobs, c->njobs, 1, 0, 2, L->books, L->books_x31, x_dev, 1, c->part, c->part_cap,
@@ -1902,7 +1928,7 @@ int warp_hip_vq_matvec(warp_hip_ctx *c, int layer, int kind, const uint8_t *rec_
         float *ls = kind == 2 ? c->lscaled : c->lscale;
         KRN(c, wk_lut_p6(x_dev, 1, N, books_kind(c, L, kind), lut, ls, c->st));
         KRN(c, wk_apply_p6(c->jobs, c->njobs, 1, kind, lut, ls, y_dev, M, N, c->st));
-    } else if (c->lut_ok && c->mv_path == WARP_HIP_PATH_AUTO && L->books) {
+    } else if (c->lut_ok && c->mv_path != WARP_HIP_PATH_MFMA && L->books) {
         float *yk[3] = { y_dev, y_dev, y_dev };
         int sp = 0;
         KRN(c, wk_vq_lut(c->cfg.fmt, c->jobs, c->njobs, 1, kind, 1, L->books, L->books_x31, x_dev, 1, c->part, c->part_cap, M, N,

@@ -46,9 +46,9 @@
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,\
 }
 
-WARP_EXPF_QUAL float warp_expf(float x)
+/* tab: the 32 entries of WARP_EXP2_TAB (a copy anywhere, e.g. in LDS) */
+WARP_EXPF_QUAL float warp_expf_t(float x, const uint64_t *tab)
 {
-    static const uint64_t tab[32] = WARP_EXP2_TAB;
     const double inv_ln2_32 = 0x1.71547652b82fep+0 * 32;
     const double shift = 0x1.8p+52;
     const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32;
@@ -77,6 +77,12 @@ WARP_EXPF_QUAL float warp_expf(float x)
     double y = fma(c2, r, 1.0);
     y = fma(z, r2, y);
     return (float)(y * s);
+}
+
+WARP_EXPF_QUAL float warp_expf(float x)
+{
+    static const uint64_t tab[32] = WARP_EXP2_TAB;
+    return warp_expf_t(x, tab);
 }
 
 #endif /* WARP_EXPF_GLIBC_H */

@@ -57,18 +57,28 @@ __device__ __forceinline__ float f16_flushed(uint16_t h) {
 
 // glibc's expf bit for bit (the reference's scores and SiLU call it):
 // warp_expf, the table-and-cubic algorithm in double precision.
+// A kernel that has issued a long prefetch reads the table from an LDS copy
+// (etab): loads complete in issue order, so waiting for a table entry
+// loaded after the prefetch would wait for all of it.
 #define WARP_EXPF_QUAL __device__ __forceinline__
 #include "expf_glibc.h"
 
-__device__ __forceinline__ float silu_ref(float v) {
-    // src/model.c:501: v / (1 + expf(-v))
-    return __fdiv_rn(v, __fadd_rn(1.0f, warp_expf(-v)));
+__device__ const uint64_t g_exp2_tab[32] = WARP_EXP2_TAB;
+
+__device__ __forceinline__ float expf_ref(float v, const uint64_t *etab) {
+    return etab ? warp_expf_t(v, etab) : warp_expf(v);
 }
 
-__device__ __forceinline__ float act_pair(float g, float u, int situ, float beta, float lbeta) {
-    if (!situ) return __fmul_rn(silu_ref(g), u);
+__device__ __forceinline__ float silu_ref(float v, const uint64_t *etab = nullptr) {
+    // src/model.c:501: v / (1 + expf(-v))
+    return __fdiv_rn(v, __fadd_rn(1.0f, expf_ref(-v, etab)));
+}
+
+__device__ __forceinline__ float act_pair(float g, float u, int situ, float beta, float lbeta,
+                                          const uint64_t *etab = nullptr) {
+    if (!situ) return __fmul_rn(silu_ref(g, etab), u);
     // src/model.c:505-509
-    const float a = __fdiv_rn(__fmul_rn(beta, tanhf(__fdiv_rn(g, beta))), __fadd_rn(1.0f, warp_expf(-g)));
+    const float a = __fdiv_rn(__fmul_rn(beta, tanhf(__fdiv_rn(g, beta))), __fadd_rn(1.0f, expf_ref(-g, etab)));
     return __fmul_rn(a, lbeta > 0.0f ? __fmul_rn(lbeta, tanhf(__fdiv_rn(u, lbeta))) : u);
 }
 
@@ -856,7 +866,7 @@ __device__ __forceinline__ int route_key(float v) {
 template <bool REGS, int NT>
 __device__ __forceinline__ int route_pick_lds(int E, int K, int act, int renorm, float routed_scale, float *score,
                                               float *biased, int *sel, float *wsel, bool want_w = true,
-                                              bool scored = false) {
+                                              bool scored = false, const uint64_t *etab = nullptr) {
     __shared__ float red[NT / 64];
     __shared__ int np_s;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -871,14 +881,14 @@ __device__ __forceinline__ int route_pick_lds(int E, int K, int act, int renorm,
             __syncthreads();
             mx = red[0];
             for (int i = 1; i < NT / 64; i++) mx = fmaxf(mx, red[i]);
-            for (int e = tid; e < E; e += NT) score[e] = warp_expf(__fsub_rn(score[e], mx));
+            for (int e = tid; e < E; e += NT) score[e] = expf_ref(__fsub_rn(score[e], mx), etab);
             __syncthreads();
             if (tid == 0) red[0] = seq_sum_lds(score, E);   // sequential, as the reference sums
             __syncthreads();
             const float s = red[0];
             for (int e = tid; e < E; e += NT) score[e] = __fdiv_rn(score[e], s);
         } else {
-            for (int e = tid; e < E; e += NT) score[e] = __fdiv_rn(1.0f, __fadd_rn(1.0f, warp_expf(-score[e])));
+            for (int e = tid; e < E; e += NT) score[e] = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_ref(-score[e], etab)));
         }
         for (int e = tid; e < E; e += NT) biased[e] = __fadd_rn(score[e], biased[e]);
         __syncthreads();
@@ -1648,6 +1658,25 @@ struct LutArgs {
     warp_route_args r;
 };
 
+// Coherent accesses, for what one block of the fused decode launch writes
+// for another, which may run on another XCD (another L2): 16-byte stores
+// that write through every cache (a volatile store: sc0 sc1; a wave's
+// stores then cover whole lines), agent-coherent loads (sc1) that do not
+// hit a stale cached copy. A wave's
+// stores are complete once wait_stores() returns, so with a barrier after
+// it the block can raise a count that others poll, without writing back
+// the L2 (which an agent-scope release fence does, at a cost that grows
+// with everything the XCD's other blocks have written).
+typedef float f4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void st_through4(float *p, float a, float b, float c, float d) {   // p in global memory, 16-byte aligned
+    const f4v v = {a, b, c, d};
+    *(volatile __attribute__((address_space(1))) f4v *)(__attribute__((address_space(1))) float *)p = v;
+}
+__device__ __forceinline__ float ld_agent(const float *p) {
+    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0x0F70); }   // vmcnt(0)
+
 // Sum of a row's partials over the splits, in split order. Up to 32 splits
 // every load is issued before the first add (one memory latency per row).
 __device__ __forceinline__ float lut_rowsum(const float *p, int splits, size_t stride) {
@@ -1680,13 +1709,18 @@ __device__ __forceinline__ float lut_rowsum_n(const float *p, int splits, size_t
     return v;
 }
 
-// The same sum with at most 8 loads in flight (few registers).
+// The same sum with at most 8 loads in flight (few registers); CO: the
+// loads are agent-coherent.
+template <bool CO = false>
 __device__ __forceinline__ float lut_rowsum8(const float *p, int splits, size_t stride) {
     float v = 0.0f;
     for (int s0 = 0; s0 < splits; s0 += 8) {
         float a8[8];
 #pragma unroll
-        for (int s = 0; s < 8; s++) a8[s] = p[(size_t)min(s0 + s, splits - 1) * stride];
+        for (int s = 0; s < 8; s++) {
+            const float *q = p + (size_t)min(s0 + s, splits - 1) * stride;
+            a8[s] = CO ? ld_agent(q) : *q;
+        }
 #pragma unroll
         for (int s = 0; s < 8; s++)
             if (s0 + s < splits) v += a8[s];
@@ -1706,25 +1740,108 @@ __device__ __forceinline__ half4 half4_of(uint32_t lo, uint32_t hi) {
     return __builtin_bit_cast(half4, make_uint2(lo, hi));
 }
 
+// One expert's routing inputs (thread e of a routing block): its score (the
+// logit, or with pre-scored logits the sigmoid score), the biased score
+// input, and its expert-table entry, loaded together and then staged in LDS.
+struct RouteIn {
+    float lg, bs;
+    const uint8_t *rec;
+    uint2 off01, off23;
+};
+__device__ __forceinline__ RouteIn route_in_load(const warp_route_args &r, int e) {
+    RouteIn v = {0.0f, 0.0f, nullptr, make_uint2(0u, 0u), make_uint2(0u, 0u)};
+    if (e < r.E) {
+        v.lg = r.logits[e];
+        v.bs = r.scored ? r.logits[r.E + e] : r.bias ? r.bias[e] : 0.0f;
+        // (the slot by fields: an aggregate copy would go through scratch)
+        v.rec = r.table[e].rec;
+        v.off01 = *(const uint2 *)&r.table[e].off[0];
+        v.off23 = *(const uint2 *)&r.table[e].off[2];
+    }
+    return v;
+}
+__device__ __forceinline__ void route_in_store(const RouteIn &v, int E, int e, float *score, float *biased,
+                                               warp_slot *slots) {
+    if (e < E) {
+        score[e] = v.lg;
+        biased[e] = v.bs;
+        slots[e].rec = v.rec;
+        *(uint2 *)&slots[e].off[0] = v.off01;
+        *(uint2 *)&slots[e].off[2] = v.off23;
+    }
+}
+
+// The fused decode launch (k_moe_fused) runs gate/up, down and combine work
+// items in one grid. Its blocks route the token once and keep the picks'
+// records here; its counters say when the inputs of an item are complete.
+struct LutPicks {
+    const uint8_t *rec[WARP_MAX_K];    // the picks' records, in selection order
+    uint32_t off[WARP_MAX_K][4];       // their header offsets (warp_slot.off)
+    int nj;                            // K, or 0 when a pick has no record
+};
+// Counter i of the fused launch is word i * FZ_LINE: one 128-byte line per
+// counter, so that its polls and increments load one memory channel each.
+constexpr int FZ_LINE = 32;
+struct FzSync {
+    unsigned *ctr;                     // counters: 0 claims, 1 exits, 2 down items done,
+                                       // 3 + g gate/up items of row group g done
+    int *flag;                         // the missing flag: bit 2 set when a wait gives up
+    unsigned limit;                    // polls before a wait gives up
+};
+
+// Thread 0 of a block: wait until counters lo..hi of ctr all reach target. The counted
+// items wrote their results with agent-coherent stores that were complete
+// before the counts rose, and the block reads them with agent-coherent
+// loads once its threads pass the barrier after this. A wait that exceeds
+// the poll limit raises bit 2 of the flag and returns, so that every wave
+// of the grid ends.
+__device__ __forceinline__ void fz_wait(const unsigned *ctr, int lo, int hi, unsigned target, const FzSync &sy) {
+    for (int g = lo; g <= hi; g++) {
+        unsigned n = 0;
+        while (__hip_atomic_load(ctr + g * FZ_LINE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+            if (++n > sy.limit) {
+                __hip_atomic_fetch_or(sy.flag, 4, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                return;
+            }
+            __builtin_amdgcn_s_sleep(8);
+        }
+    }
+}
+
+// One unit (row group bx / a.splits, split bx % a.splits, kind a.kind_lo +
+// by) of a LUT launch, by the whole block.
 // SHX = true: the jobs of the list share one input and a row group spans
 // them (gate and up); false: one input per job (down). ACT (with SHX false):
 // the inputs are made from the gate/up partial sums (a.act_part). RT (with
 // SHX): the jobs are picked in the prologue from the router logits (a.r).
-template <int FMT, bool X31, bool SHX, bool ACT, bool RT>
-__global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
+// FZ: a work item of the fused launch: the jobs are the picks in pk, and
+// (ACT) the gate/up partial sums are read once the row groups that hold
+// them are counted complete in sy.
+template <int FMT, bool X31, bool SHX, bool ACT, bool RT, bool FZ>
+__device__ __forceinline__ void lut_item(const LutArgs &a, const unsigned bx, const unsigned by, const LutPicks *pk,
+                                         const FzSync *sy) {
     typedef FmtT<FMT> F;
     constexpr int SE = F::S * F::E;                        // table entries per position
     constexpr int NG = SE / 64;                            // 64-entry groups
     constexpr int GPW = (NG + LUT_NW - 1) / LUT_NW;        // groups per wave
     constexpr int BUF = 2 * SE;                            // floats per buffer
     static_assert(SE % 64 == 0, "table groups");
+    // (in the fused launch, opaque per item: what derives from it is
+    // computed per item, not held in registers across the item loop)
+    unsigned tid = threadIdx.x;
+    if constexpr (FZ) asm volatile("" : "+v"(tid));
+    // the expf table for the activation and the routing scores, loaded
+    // before every other load and kept in LDS (see expf_ref)
+    __shared__ uint64_t s_exp[32];
+    uint64_t etv = 0;
+    if constexpr (ACT || RT) etv = g_exp2_tab[tid & 31];
     extern __shared__ __attribute__((aligned(16))) float lut[];   // [2][S][E][2], then x of the split
-    const int kind = a.kind_lo + blockIdx.y;
+    const int kind = a.kind_lo + by;
     const warp_job *jobs = a.jobs + (size_t)kind * a.max_jobs;
     const int nv = a.N >> 3, nrb = (a.M + 63) >> 6, nc = nv >> 1;
-    const int grp = blockIdx.x / a.splits, split = blockIdx.x % a.splits;
+    const int grp = bx / a.splits, split = bx % a.splits;
     const int c0 = split * nc / a.splits, c1 = (split + 1) * nc / a.splits;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = tid & 63, wave = tid >> 6;
     const int pl = (lane >> 4) & 1, rbsel = lane >> 5, quad = lane & 15;
     int fb0, xj;
     if (SHX) {
@@ -1752,7 +1869,7 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
     // (128 KiB per block for 2 x 4096 entries). vw rotates the waves' groups
     // by block, so that the blocks of a launch, which all load the same
     // codebook at once, start on different lines.
-    const int vw = (wave + (int)blockIdx.x) & (LUT_NW - 1);
+    const int vw = (wave + (int)bx) & (LUT_NW - 1);
     uint4 cb[GPW];
     auto load_cb = [&]() {
         const uint4 *bk = (const uint4 *)(a.books + (size_t)kind * SE * 8);
@@ -1768,50 +1885,35 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
         //    inputs staged in the table buffers, which are not built yet; the
         //    picks; then the record of every pair straight from the staged
         //    expert table.
-        const int E = a.r.E, E2 = (E + 1) & ~1, K = a.max_jobs, e = threadIdx.x;
+        const int E = a.r.E, E2 = (E + 1) & ~1, K = a.max_jobs, e = tid;
         float *score = lut, *biased = lut + E2;
         warp_slot *slots = (warp_slot *)(lut + 2 * E2);
         __shared__ int r_sel[WARP_MAX_K];
         __shared__ float r_wsel[WARP_MAX_K];
-        // (the slot by fields: an aggregate copy would go through scratch)
-        float lg = 0.0f, bs = 0.0f;
-        const uint8_t *srec = nullptr;
-        uint2 so01 = make_uint2(0u, 0u), so23 = make_uint2(0u, 0u);
-        if (e < E) {
-            lg = a.r.logits[e];
-            bs = a.r.scored ? a.r.logits[E + e] : a.r.bias ? a.r.bias[e] : 0.0f;
-            srec = a.r.table[e].rec;
-            so01 = *(const uint2 *)&a.r.table[e].off[0];
-            so23 = *(const uint2 *)&a.r.table[e].off[2];
-        }
+        const RouteIn ri = route_in_load(a.r, e);
         __builtin_amdgcn_sched_barrier(0);
         const float *xg = a.x + (size_t)c0 * 16;
 #pragma unroll
         for (int k = 0; k < XPT; k++) {
-            const int i = threadIdx.x + k * LUT_NW * 64;
+            const int i = tid + k * LUT_NW * 64;
             const float v = xg[min(i, nx - 1)];
             xr[k] = i < nx ? v : 0.0f;
         }
         __builtin_amdgcn_sched_barrier(0);
         load_cb();                                         // streams in while the picks are made
         __builtin_amdgcn_sched_barrier(0);
-        if (e < E) {
-            score[e] = lg;
-            biased[e] = bs;
-            slots[e].rec = srec;
-            *(uint2 *)&slots[e].off[0] = so01;
-            *(uint2 *)&slots[e].off[2] = so23;
-        }
+        route_in_store(ri, E, e, score, biased, slots);
+        if (tid < 32) s_exp[tid] = etv;
         // only the block that publishes the routing needs the weights
         const bool pub = blockIdx.x == 0 && blockIdx.y == 0;
         route_pick_lds<true, LUT_NW * 64>(E, K, a.r.act, a.r.renorm, a.r.routed_scale, score, biased, r_sel, r_wsel,
-                                          pub, a.r.scored != 0);
+                                          pub, a.r.scored != 0, s_exp);
         bool miss = false;                                 // a pick without a record (the same in every block)
         for (int j = 0; j < K; j++) miss |= slots[r_sel[j]].rec == nullptr;
         if (pub) {                                         // uniform per block
-            if (threadIdx.x < K) {
-                a.r.idx[threadIdx.x] = r_sel[threadIdx.x];
-                a.r.w[threadIdx.x] = r_wsel[threadIdx.x];
+            if (tid < K) {
+                a.r.idx[tid] = r_sel[tid];
+                a.r.w[tid] = r_wsel[tid];
             }
             route_jobs<LUT_NW * 64>(r_sel, K, slots, a.r.jobs, a.r.njobs, a.r.missing, a.r.inter);
         }
@@ -1826,6 +1928,25 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
         xi = 0;
         nj = miss ? 0 : K;
         __syncthreads();                                   // the staging area is reused below
+    } else if constexpr (FZ) {
+        // 1. The records of the block's picks (LDS), the input index and,
+        //    for the down items, the gate/up row scales.
+        const int K = a.max_jobs;
+#pragma unroll
+        for (int q = 0; q < LUT_PPW; q++) {
+            const int fb = fb0 + 2 * (q * LUT_NW + wave) + rbsel;
+            const int j = min(fb / nrb, K - 1);
+            jrec[q] = pk->rec[j] + pk->off[j][kind];
+        }
+        const int j0 = min(fb0 / nrb, K - 1);
+        jrec0 = pk->rec[j0] + pk->off[j0][kind];
+        xi = 0;
+        if constexpr (act) {
+            const uint16_t *sc = (const uint16_t *)(pk->rec[xj] + pk->off[xj][3]);
+            sg = (gu32 *)sc;
+            su = (gu32 *)(sc + a.N);
+        }
+        nj = pk->nj;
     } else {
         // 1. The job list, written by the routing launch: the record of every
         //    pair (the job of a pair follows from the block's position; the
@@ -1850,22 +1971,25 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
     //    [kind 0, 1][split s] of nx values, spread over the block (one load
     //    per thread per row-chunk; indices past the end are clamped and their
     //    values dropped), to be staged in the table buffers.
+    //    (FZ: after step 4, once the row groups are complete.)
     const size_t arows = (size_t)((a.N + 63) >> 6) * 64, astride = (size_t)a.max_jobs * arows;
     const int atot = act ? 2 * a.act_splits * nx : 0;
     const bool astage = act && atot <= ACT_LD * LUT_NW * 64 && atot <= 2 * BUF;   // uniform
     float av[ACT_LD];
-    if (astage) {
+    auto stage_partials = [&]() {
         const float *pa = a.act_part + (size_t)xj * arows + (size_t)c0 * 16;
         const int drow = (LUT_NW * 64) / nx, dv = (LUT_NW * 64) % nx, rmax = 2 * a.act_splits - 1;
-        int row = threadIdx.x / nx, v = threadIdx.x % nx;
+        int row = tid / nx, v = tid % nx;
 #pragma unroll
         for (int k = 0; k < ACT_LD; k++) {
-            av[k] = pa[(size_t)min(row, rmax) * astride + v];
+            const float *q = pa + (size_t)min(row, rmax) * astride + v;
+            av[k] = FZ ? ld_agent(q) : *q;
             row += drow;
             v += dv;
             if (v >= nx) { v -= nx; row++; }
         }
-    }
+    };
+    if (!FZ && astage) stage_partials();
     __builtin_amdgcn_sched_barrier(0);
 
     const int fb_end = SHX ? nj * nrb : (xj < nj ? (xj + 1) * nrb : 0);
@@ -1879,7 +2003,7 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
     if constexpr (act) {
 #pragma unroll
         for (int k = 0; k < XPT; k++) {
-            const int i = min((int)threadIdx.x + k * LUT_NW * 64, nx - 1) + c0 * 16;
+            const int i = min((int)tid + k * LUT_NW * 64, nx - 1) + c0 * 16;
             gs[k] = sg[i >> 1];
             us[k] = su[i >> 1];
         }
@@ -1887,7 +2011,7 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
         const float *xg = a.x + (size_t)xi * a.N + (size_t)c0 * 16;
 #pragma unroll
         for (int k = 0; k < XPT; k++) {
-            const int i = threadIdx.x + k * LUT_NW * 64;
+            const int i = tid + k * LUT_NW * 64;
             const float v = xg[min(i, nx - 1)];
             xr[k] = i < nx ? v : 0.0f;
         }
@@ -1916,13 +2040,24 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
 #pragma unroll
     for (int q = 0; q < LUT_PPW; q++) wd[q].load_keep(cp[q] + (size_t)(2 * c0) * 64 * F::SB);
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (FZ && act) {
+        // the gate/up row groups that hold this item's inputs (rows
+        // 16 c0 .. 16 c1 - 1 of pick xj), every split of both kinds
+        const int nrbg = (a.N + 63) >> 6;
+        if (tid == 0)
+            fz_wait(sy->ctr + 3 * FZ_LINE, (xj * nrbg + (c0 * 16) / 64) / LUT_RBG, (xj * nrbg + (c1 * 16 - 1) / 64) / LUT_RBG,
+                    2u * a.act_splits, *sy);
+        __syncthreads();
+        if (astage) stage_partials();
+    }
 
     // 5. Down launch: h = act(gate, up) from the partial sums, added over the
     //    splits in split order (through the staging area when it fits).
     if constexpr (act) {
+        if (tid < 32) s_exp[tid] = etv;
         if (astage) {
             const int drow = (LUT_NW * 64) / nx, dv = (LUT_NW * 64) % nx;
-            int row = threadIdx.x / nx, v = threadIdx.x % nx;
+            int row = tid / nx, v = tid % nx;
 #pragma unroll
             for (int k = 0; k < ACT_LD; k++) {
                 if (row * nx + v < atot) lut[row * nx + v] = av[k];
@@ -1940,7 +2075,7 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
             while (P > 1 && atot + 2 * P * nx > 2 * BUF) P--;
             float *ps = lut + atot;                        // [gate, up][P][nx]
             if (P > 1) {
-                const int i = (int)threadIdx.x % nx, p = (int)threadIdx.x / nx;
+                const int i = (int)tid % nx, p = (int)tid / nx;
                 if (p < P) {
                     const int s1 = (p + 1) * S / P;
                     float g = 0.0f, u = 0.0f;
@@ -1955,7 +2090,7 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
             }
 #pragma unroll
             for (int k = 0; k < XPT; k++) {
-                const int i = threadIdx.x + k * LUT_NW * 64;
+                const int i = tid + k * LUT_NW * 64;
                 xr[k] = 0.0f;
                 if (i < nx) {
                     float g = 0.0f, u = 0.0f;
@@ -1986,21 +2121,22 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
                     }
                     const int sh = 16 * (i & 1);
                     xr[k] = act_pair(g * f16_keep((uint16_t)(gs[k] >> sh)), u * f16_keep((uint16_t)(us[k] >> sh)),
-                                     a.act_situ, a.act_beta, a.act_lbeta);
+                                     a.act_situ, a.act_beta, a.act_lbeta, s_exp);
                 }
             }
         } else {
+            __syncthreads();                               // s_exp
             const float *pg = a.act_part + (size_t)xj * arows + (size_t)c0 * 16;
             const float *pu = pg + (size_t)a.act_splits * astride;
 #pragma unroll
             for (int k = 0; k < XPT; k++) {
-                const int i = threadIdx.x + k * LUT_NW * 64;
+                const int i = tid + k * LUT_NW * 64;
                 xr[k] = 0.0f;
                 if (i < nx) {
                     const int sh = 16 * (i & 1);
-                    const float g = lut_rowsum8(pg + i, a.act_splits, astride) * f16_keep((uint16_t)(gs[k] >> sh));
-                    const float u = lut_rowsum8(pu + i, a.act_splits, astride) * f16_keep((uint16_t)(us[k] >> sh));
-                    xr[k] = act_pair(g, u, a.act_situ, a.act_beta, a.act_lbeta);
+                    const float g = lut_rowsum8<FZ>(pg + i, a.act_splits, astride) * f16_keep((uint16_t)(gs[k] >> sh));
+                    const float u = lut_rowsum8<FZ>(pu + i, a.act_splits, astride) * f16_keep((uint16_t)(us[k] >> sh));
+                    xr[k] = act_pair(g, u, a.act_situ, a.act_beta, a.act_lbeta, s_exp);
                 }
             }
         }
@@ -2012,7 +2148,7 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
         float *xst = lut + 2 * BUF;
 #pragma unroll
         for (int k = 0; k < XPT; k++) {
-            const int i = threadIdx.x + k * LUT_NW * 64;
+            const int i = tid + k * LUT_NW * 64;
             if (i < nx) xst[i] = xr[k];
         }
     } else {
@@ -2023,7 +2159,7 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
         _Float16 *xh = (_Float16 *)(lut + 2 * BUF);
 #pragma unroll
         for (int k = 0; k < XPT; k++) {
-            const int i = threadIdx.x + k * LUT_NW * 64;
+            const int i = tid + k * LUT_NW * 64;
             if (i < nx) {
                 const int o = (i >> 4) * 32 + ((i >> 3) & 1) * 16 + (i & 7);
                 split_store(xr[k], ks, &xh[o], &xh[o + 8]);
@@ -2142,15 +2278,203 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
     }
 
     // even + odd positions, unscaled: one partial per row of this split
-    float *po = a.part + ((size_t)blockIdx.y * a.splits + split) * a.max_jobs * nrb * 64;
+    float *po = a.part + ((size_t)by * a.splits + split) * a.max_jobs * nrb * 64;
 #pragma unroll
     for (int q = 0; q < LUT_PPW; q++) {
         float v[4];
 #pragma unroll
         for (int t = 0; t < 4; t++) v[t] = ldexpf(acc[q][t] + __shfl_xor(acc[q][t], 16), -ks);
         const int fb = fb0 + 2 * (q * LUT_NW + wave) + rbsel;
-        if (pl == 0 && fb < fb_end) *(float4 *)(po + fb * 64 + 4 * quad) = make_float4(v[0], v[1], v[2], v[3]);
+        if (pl == 0 && fb < fb_end) {
+            float *d = po + fb * 64 + 4 * quad;
+            if constexpr (FZ) {
+                st_through4(d, v[0], v[1], v[2], v[3]);
+            } else {
+                *(float4 *)d = make_float4(v[0], v[1], v[2], v[3]);
+            }
+        }
     }
+}
+
+template <int FMT, bool X31, bool SHX, bool ACT, bool RT>
+__global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
+    lut_item<FMT, X31, SHX, ACT, RT, false>(a, blockIdx.x, blockIdx.y, nullptr, nullptr);
+}
+
+// ---- the fused decode launch ---------------------------------------------------------
+//
+// One launch per decode layer instead of three (gate/up, down, combine): the
+// units of the two LUT launches and the combine are work items, claimed in
+// order from a counter: [0, n_gu) gate/up (row group major, then kind, then
+// split), [n_gu, n_gu + n_d) down (pick major, then split), then the
+// combine, 64 output rows each. A down item needs the gate/up row groups of
+// its inputs complete, the combine every down item: a block counts each
+// item it finishes once the item's partial sums are stored (agent-coherent
+// stores, complete), waits for the counts it needs (bounded by a poll
+// limit) and reads with agent-coherent loads. Items are claimed in order by running blocks,
+// so every item an item waits for was claimed before it by a block that
+// runs: the launch completes on however many CUs the device gives it. A
+// down item loads its codebook, row scales and first code words before it
+// waits. Every block routes the token itself (the same picks everywhere)
+// and keeps the picks' records and weights in LDS; block 0 also publishes
+// idx, w and the job lists. The last block to leave resets the counters for
+// the next launch, so a graph can replay it. Partial sums, their layouts,
+// split counts and summation orders are those of the three launches, so the
+// results are identical to theirs bit for bit.
+
+struct MoeArgs {
+    LutArgs gu, dn;            // the gate/up units (kinds 0, 1; routed, gu.r) and the down units (kind 2, act)
+    int groups_gu, groups_d, n_comb;
+    const float *add0, *add1;  // added to each output in this order (shared expert, residual), or NULL
+    float *out;                // [H]
+    FzSync sy;
+};
+
+// Rows 64 ci .. 64 ci + 63 of the output: each pick's row (its down partial
+// sums added in split order, times its row scale), then the weighted sum in
+// selection order, then add0 and add1 (k_combine_lut's arithmetic); NaN when a pick,
+// in this or an earlier unreported layer, was not computed. yd: LDS, K x 64.
+__device__ __forceinline__ void moe_combine_rows(const MoeArgs &m, int ci, const LutPicks &pk, const float *wl,
+                                                 int miss, float *yd) {
+    const int H = m.dn.M, I = m.dn.N, K = m.dn.max_jobs, splits = m.dn.splits;
+    const int row = threadIdx.x & 63, jq = threadIdx.x >> 6, r0 = ci * 64;
+    const int i = min(r0 + row, H - 1);
+    const size_t nrows = (size_t)((H + 63) >> 6) * 64, stride = (size_t)K * nrows;
+    if (!miss) {
+        for (int j = jq; j < K; j += LUT_NW) {
+            const float *p = m.dn.part + (size_t)j * nrows + i;
+            const float v = lut_rowsum8<true>(p, splits, stride);
+            gu32 *sc = (gu32 *)((const uint16_t *)(pk.rec[j] + pk.off[j][3]) + 2 * I);
+            yd[j * 64 + row] = v * f16_keep((uint16_t)(sc[i >> 1] >> (16 * (i & 1))));
+        }
+    }
+    __syncthreads();
+    if (jq == 0 && r0 + row < H) {
+        float s = __builtin_nanf("");
+        if (!miss) {
+            s = 0.0f;
+            for (int j = 0; j < K; j++) s = __fadd_rn(s, __fmul_rn(wl[j], yd[j * 64 + row]));
+            if (m.add0) s = __fadd_rn(s, m.add0[i]);
+            if (m.add1) s = __fadd_rn(s, m.add1[i]);
+        }
+        m.out[i] = s;
+    }
+    __syncthreads();
+}
+
+// The launch's arguments, read from the kernel argument segment where they
+// are used: the address is opaque to the compiler, so that it loads fields
+// per item instead of holding every field of both units in scalar registers
+// across the item loop.
+__device__ __forceinline__ const MoeArgs &moe_args() {
+    uint64_t p = (uint64_t)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(p));
+    return *(const MoeArgs *)(const __attribute__((address_space(4))) MoeArgs *)p;
+}
+
+template <int FMT, bool X31>
+__global__ __launch_bounds__(LUT_NW * 64) void k_moe_fused(MoeArgs) {
+    extern __shared__ __attribute__((aligned(16))) float lut[];
+    __shared__ LutPicks pk;
+    __shared__ int r_sel[WARP_MAX_K];
+    __shared__ float r_wsel[WARP_MAX_K];
+    __shared__ int s_item, s_miss;
+    const int tid = threadIdx.x;
+    int total;
+    unsigned nxt = 0;
+    {
+    const MoeArgs &m = moe_args();
+    const warp_route_args &r = m.gu.r;
+    const int E = r.E, E2 = (E + 1) & ~1, K = m.gu.max_jobs;
+    total = 2 * m.groups_gu * m.gu.splits + m.groups_d * m.dn.splits + m.n_comb;
+    unsigned *ctr = m.sy.ctr;
+
+    // the first claim, the flag an earlier layer may have left, the routing
+    int prev = 0;
+    if (tid == 0) {
+        nxt = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        prev = *(volatile const int *)r.missing & 3;
+    }
+    float *score = lut, *biased = lut + E2;
+    warp_slot *slots = (warp_slot *)(lut + 2 * E2);
+    route_in_store(route_in_load(r, tid), E, tid, score, biased, slots);
+    route_pick_lds<true, LUT_NW * 64>(E, K, r.act, r.renorm, r.routed_scale, score, biased, r_sel, r_wsel, true,
+                                      r.scored != 0);
+    bool miss = false;
+    for (int j = 0; j < K; j++) miss |= slots[r_sel[j]].rec == nullptr;
+    if (tid < K) {
+        const warp_slot &sl = slots[r_sel[tid]];
+        pk.rec[tid] = sl.rec;
+#pragma unroll
+        for (int k = 0; k < 4; k++) pk.off[tid][k] = sl.off[k];
+    }
+    if (blockIdx.x == 0) {                                  // uniform per block
+        if (tid < K) {
+            r.idx[tid] = r_sel[tid];
+            r.w[tid] = r_wsel[tid];
+        }
+        route_jobs<LUT_NW * 64>(r_sel, K, slots, r.jobs, r.njobs, r.missing, r.inter);
+    }
+    if (tid == 0) {
+        pk.nj = miss ? 0 : K;
+        s_miss = prev || miss;
+        s_item = (int)nxt;
+    }
+    }
+    __syncthreads();                                       // the staging area is the items' from here
+
+    for (;;) {
+        const int item = s_item;
+        if (item >= total) break;                          // uniform
+        const MoeArgs &m = moe_args();
+        const int S = m.gu.splits, n_gu = 2 * m.groups_gu * S, n_d = m.groups_d * m.dn.splits;
+        unsigned *ctr = m.sy.ctr;
+        if (tid == 0) nxt = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (item < n_gu) {
+            const int grp = item / (2 * S), rem = item - grp * 2 * S;
+            lut_item<FMT, X31, true, false, false, true>(m.gu, grp * S + rem % S, rem / S, &pk, &m.sy);
+            wait_stores();
+            __syncthreads();
+            if (tid == 0)
+                __hip_atomic_fetch_add(ctr + (3 + grp) * FZ_LINE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else if (item < n_gu + n_d) {
+            lut_item<FMT, X31, false, true, false, true>(m.dn, item - n_gu, 0, &pk, &m.sy);
+            wait_stores();
+            __syncthreads();
+            if (tid == 0) __hip_atomic_fetch_add(ctr + 2 * FZ_LINE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            if (tid == 0) fz_wait(ctr + 2 * FZ_LINE, 0, 0, (unsigned)n_d, m.sy);
+            __syncthreads();
+            moe_combine_rows(m, item - n_gu - n_d, pk, r_wsel, s_miss, lut);
+        }
+        if (tid == 0) s_item = (int)nxt;
+        __syncthreads();
+    }
+    if (tid == 0) {
+        const MoeArgs &m = moe_args();
+        unsigned *ctr = m.sy.ctr;
+        const unsigned left = __hip_atomic_fetch_add(ctr + FZ_LINE, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        if (left == gridDim.x - 1)
+            for (int g = 0; g < 3 + m.groups_gu; g++)
+                __hip_atomic_store(ctr + g * FZ_LINE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+template <int FMT, bool X31>
+static int launch_moe_fused(const MoeArgs &m, int blocks, void *stream) {
+    typedef FmtT<FMT> F;
+    const size_t lds = ((size_t)2 * 2 * F::S * F::E + LUT_XCH * 16) * sizeof(float);
+    if (lds > 163840) return -2;
+    static bool attr = false;
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute((const void *)k_moe_fused<FMT, X31>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return -(int)e - 1000;
+        attr = true;
+    }
+    hipLaunchKernelGGL((k_moe_fused<FMT, X31>), dim3(blocks), dim3(LUT_NW * 64), lds, (hipStream_t)stream, m);
+    CHECK_LAUNCH();
+    return 0;
 }
 
 extern "C" int wk_lut_plan(int M, int N, int max_jobs, int nkinds, int shared_x, int target_blocks,
@@ -2257,6 +2581,70 @@ extern "C" int wk_vq_lut(int fmt, const warp_job *jobs, const int *njobs, int ma
     case WARP_FMT_VQ3R: return launch_lut_x<WARP_FMT_VQ3R>(a, groups, nkinds, books_x31, stream);
     case WARP_FMT_VQ2R: return launch_lut_x<WARP_FMT_VQ2R>(a, groups, nkinds, books_x31, stream);
     case WARP_FMT_VQ12: return launch_lut_x<WARP_FMT_VQ12>(a, groups, nkinds, books_x31, stream);
+    }
+    return -1;
+}
+
+extern "C" int wk_moe_fused(int fmt, const uint16_t *books, int books_x31, const float *x, int K, int I, int H,
+                            float *part, size_t cap_floats, int n_cu, int act_situ, float act_beta,
+                            float act_lbeta, const warp_route_args *route, const float *add0, const float *add1,
+                            float *out, unsigned *sync, int sync_words, void *stream) {
+    if (!books || !x || !part || !route || !out || !sync || n_cu < 1) return -1;
+    if (!wk_lut_route_ok(fmt, route->E, K, 1, 0, 2)) return -1;
+    int groups_gu, splits_gu, groups_d, splits_d;
+    if (wk_lut_plan(I, H, K, 2, 1, n_cu, cap_floats, &groups_gu, &splits_gu)) return -1;
+    const size_t gu_floats = (size_t)2 * splits_gu * K * (((size_t)I + 63) / 64) * 64;
+    if (gu_floats > cap_floats || wk_lut_plan(H, I, K, 1, 0, n_cu, cap_floats - gu_floats, &groups_d, &splits_d))
+        return -1;
+    if ((size_t)(3 + groups_gu) * FZ_LINE > (size_t)sync_words) return -1;
+    MoeArgs m = {};
+    LutArgs &g = m.gu, &d = m.dn;
+    g.jobs = route->jobs;
+    g.njobs = route->njobs;
+    g.max_jobs = K;
+    g.kind_lo = 0;
+    g.books = books;
+    g.x = x;
+    g.part = part;
+    g.M = I;
+    g.N = H;
+    g.splits = splits_gu;
+    g.shared_x = 1;
+    g.r = *route;
+    d = g;
+    d.kind_lo = 2;
+    d.x = nullptr;
+    d.part = part + gu_floats;
+    d.M = H;
+    d.N = I;
+    d.splits = splits_d;
+    d.shared_x = 0;
+    d.act_part = part;
+    d.act_splits = splits_gu;
+    d.act_situ = act_situ;
+    d.act_beta = act_beta;
+    d.act_lbeta = act_lbeta;
+    m.groups_gu = groups_gu;
+    m.groups_d = groups_d;
+    m.n_comb = (H + 63) / 64;
+    m.add0 = add0;
+    m.add1 = add1;
+    m.out = out;
+    m.sy.ctr = sync;
+    m.sy.flag = route->missing;
+    m.sy.limit = 1u << 20;
+    const int items = 2 * groups_gu * splits_gu + groups_d * splits_d + m.n_comb;
+    const int blocks = n_cu < items ? n_cu : items;
+    switch (fmt) {
+    case WARP_FMT_VQ3R:
+        return books_x31 ? launch_moe_fused<WARP_FMT_VQ3R, true>(m, blocks, stream)
+                         : launch_moe_fused<WARP_FMT_VQ3R, false>(m, blocks, stream);
+    case WARP_FMT_VQ2R:
+        return books_x31 ? launch_moe_fused<WARP_FMT_VQ2R, true>(m, blocks, stream)
+                         : launch_moe_fused<WARP_FMT_VQ2R, false>(m, blocks, stream);
+    case WARP_FMT_VQ12:
+        return books_x31 ? launch_moe_fused<WARP_FMT_VQ12, true>(m, blocks, stream)
+                         : launch_moe_fused<WARP_FMT_VQ12, false>(m, blocks, stream);
     }
     return -1;
 }

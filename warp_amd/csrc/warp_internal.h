@@ -198,6 +198,19 @@ int wk_vq_lut(int fmt, const warp_job *jobs, const int *njobs, int max_jobs, int
  * reading jobs/njobs; route->jobs/njobs/idx/w/missing get what wk_route
  * writes. Only where wk_lut_route_ok says so; NULL otherwise.) */
 int wk_lut_route_ok(int fmt, int E, int K, int shared_x, int kind_lo, int nkinds);
+/* One decode step of a layer in one launch (the table kernel's gate/up
+ * units with the routing, its down units, the combine), bit for bit what
+ * wk_vq_lut (gate/up, routed), wk_vq_lut (down, act) and wk_combine_lut
+ * give: out [H] = sum_j w_j y_j + add0 + add1, NaN when a pick has no
+ * record (the missing flag as wk_route sets it). route as for wk_vq_lut;
+ * part and cap_floats hold both launches' partial sums. sync: WARP_FZ_WORDS
+ * zeroed words the launch leaves zeroed; a wait that exceeds its poll limit
+ * sets bit 2 (value 4) of route->missing. Only where wk_lut_route_ok holds. */
+#define WARP_FZ_WORDS 16384
+int wk_moe_fused(int fmt, const uint16_t *books, int books_x31, const float *x, int K, int I, int H,
+                 float *part, size_t cap_floats, int n_cu, int act_situ, float act_beta,
+                 float act_lbeta, const warp_route_args *route, const float *add0, const float *add1,
+                 float *out, unsigned *sync, int sync_words, void *stream);
 /* y[k][yi][r] = (sum over splits) * row scale, for the kinds of one LUT launch. */
 int wk_lut_reduce(const warp_job *jobs, const int *njobs, int max_jobs, int kind_lo, int nkinds,
                   const float *part, int splits, int M, float *const *y, void *stream);
