@@ -92,12 +92,12 @@ def layer_bytes():
     return K * pair_bytes() + E * H * 4 + 3 * S * EN * 8 * 2 + E * 4 + 2 * H * 4
 
 
-def setup(layers, resident, seed=1234):
+def setup(layers, resident, seed=1234, router_strict=False):
     import warp_amd
     gate, down, scales_b, rec_bytes = rec_layout()
     ctx = warp_amd.Context(hidden=H, inter=I, n_experts=E, top_k=K, n_layers=layers, fmt="VQ12",
                            renorm=True, routed_scale=1.0, max_tokens=1, rec_bytes=rec_bytes,
-                           cache_bytes=layers * resident * rec_bytes)
+                           cache_bytes=layers * resident * rec_bytes, router_strict=router_strict)
     rng = np.random.Generator(np.random.PCG64(seed))
     t0 = time.time()
     for L in range(layers):
@@ -119,7 +119,7 @@ def setup(layers, resident, seed=1234):
 
 def run_gpu(args):
     from warp_amd.device import Buf, Event
-    ctx, rec_bytes = setup(args.layers, args.resident)
+    ctx, rec_bytes = setup(args.layers, args.resident, router_strict=args.router_strict)
     ctx.set_matvec_path(args.matvec_path)
     n_in = max(args.steps, args.warmup, 1)
     X = Buf.of(np.random.default_rng(7).standard_normal((n_in, H), dtype=np.float32))
@@ -1099,6 +1099,8 @@ def main():
     ap.add_argument("--no-graph", dest="graph", action="store_false",
                     help="k3-decode, kimi-decode: launch every kernel from the host instead of replaying one "
                          "captured step")
+    ap.add_argument("--router-strict", action="store_true",
+                    help="K3 decode: router logits in the reference's sequential summation order (bit-exact)")
     ap.add_argument("--matvec-path", choices=["auto", "mfma", "fused"], default="auto",
                     help="expert matvec kernel: auto = the LUT kernel, mfma = decode-then-dot on the matrix cores, "
                          "fused = the LUT kernel's gate/up, down and combine in one launch per layer")
@@ -1173,6 +1175,7 @@ def main():
         "dtype": "fp32",
         "data": "synthetic (random codes, codebooks, scales and routers of the K3 shapes)",
         "launch": "one step captured as a HIP graph and replayed per token" if args.graph else "host launches",
+        "router": "strict (sequential sums, bit-exact logits)" if args.router_strict else "fast (fixed-order tree)",
         "config": {"workload": "K3-scale MoE decode layer, batch 1, 60-layer stack",
                    "hidden": H, "inter": I, "experts": E, "top_k": K, "layers": layers,
                    "format": "RVQ 2x4096 12-bit codes (3.00 b/w)", "resident_per_layer": args.resident,
@@ -1211,7 +1214,7 @@ def run_children(args):
         cmd = [sys.executable, os.path.abspath(__file__), "--workload", wl, "--twin-dir", args.twin_dir,
                "--cpu-seconds", str(args.cpu_seconds), "--matvec-path", args.matvec_path]
         if wl == "k3-miss":
-            cmd += ["--steps", "3", "--warmup", "1"]
+            cmd += ["--steps", "8", "--warmup", "2"]
         else:
             cmd += ["--steps", str(args.steps), "--warmup", str(args.warmup)]
         if args.no_cpu:

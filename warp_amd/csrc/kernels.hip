@@ -377,24 +377,94 @@ __global__ __launch_bounds__(256) void k_router_mfma(const float *__restrict__ W
 
 // The reference's dotf on x86 (src/model.c:155-160): one sequential, unfused
 // sum per row, bit for bit.
+// Strict logits: each (token, expert) row summed in index order, w[i] * x[i]
+// rounded and then added (unfused), as the reference's loop does, bit for
+// bit. A row's adds form one dependent chain; the rows' chains are
+// independent, so a wave runs 16 rows side by side, one per lane: 64
+// columns at a time, all 64 lanes form the tile's products from coalesced
+// 16-byte loads into LDS (rows 68 floats apart: the 16 lanes' 16-byte reads
+// hit distinct banks), the loads of the next RS_D steps in flight (a step's
+// adds take far less than a load's latency), and each of lanes 0-15 adds
+// its row's 64 products in order, four per LDS read.
+constexpr int RS_R = 16;                   // rows per wave
+constexpr int RS_C = 64;                   // columns per step
+constexpr int RS_P = RS_C + 4;             // LDS row pitch (floats)
+constexpr int RS_D = 8;                    // steps whose loads are in flight
 __global__ __launch_bounds__(64) void k_router_strict(const float *__restrict__ W, const float *__restrict__ x,
                                                       int E, int H, int T, float *__restrict__ logits) {
-    const int row = blockIdx.x * 64 + threadIdx.x;
-    if (row >= E * T) return;
-    const int t = row / E, e = row % E;
-    const float *w = W + (size_t)e * H, *xt = x + (size_t)t * H;
+    __shared__ __attribute__((aligned(16))) float tp[RS_R * RS_P];
+    const int lane = threadIdx.x;
+    const int gpt = (E + RS_R - 1) / RS_R;                 // waves per token
+    const int t = blockIdx.x / gpt, e0 = (blockIdx.x % gpt) * RS_R;
+    const float *xt = x + (size_t)t * H;
+    // this lane's share of a step: rows 4 k + lane / 16 (k < 4), columns
+    // 4 (lane % 16) .. + 3
+    const int lr = lane >> 4, lc = (lane & 15) * 4;
+    float4 wv[RS_D][4], xv[RS_D];
+    // Every load is a whole, in-bounds 16-byte load (H % 4 == 0): columns
+    // past H and steps past the end reload the row's last four columns,
+    // and their products are not added. No load sits under a branch, so
+    // the waits stay exact and the RS_D steps stay in flight.
+    auto load = [&](int d, int c) {
+        const int i = min(c + lc, H - 4);
+#pragma unroll
+        for (int k = 0; k < 4; k++) wv[d][k] = *(const float4 *)(W + (size_t)min(e0 + 4 * k + lr, E - 1) * H + i);
+        xv[d] = *(const float4 *)(xt + i);
+    };
+#pragma unroll
+    for (int d = 0; d < RS_D; d++) load(d, d * RS_C);
     float acc = 0.0f;
-    for (int i = 0; i < H; i++) acc = __fadd_rn(acc, __fmul_rn(w[i], xt[i]));
-    logits[row] = acc;
+    for (int cb = 0; cb < H; cb += RS_D * RS_C)
+#pragma unroll
+    for (int d = 0; d < RS_D; d++) {
+        const int c = cb + d * RS_C;
+        if (c >= H) break;                                 // uniform
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            *(float4 *)&tp[(4 * k + lr) * RS_P + lc] =
+                make_float4(__fmul_rn(wv[d][k].x, xv[d].x), __fmul_rn(wv[d][k].y, xv[d].y),
+                            __fmul_rn(wv[d][k].z, xv[d].z), __fmul_rn(wv[d][k].w, xv[d].w));
+        load(d, c + RS_D * RS_C);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (lane < RS_R) {
+            const float *pr = &tp[lane * RS_P];
+            const int n = min(RS_C, H - c);
+            if (n == RS_C) {
+                // all 64 products to registers first, then the adds (reads
+                // interleaved with the chain would expose their latency)
+                float4 v[RS_C / 4];
+#pragma unroll
+                for (int i = 0; i < RS_C / 4; i++) v[i] = *(const float4 *)(pr + 4 * i);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int i = 0; i < RS_C / 4; i++) {
+                    acc = __fadd_rn(acc, v[i].x);
+                    acc = __fadd_rn(acc, v[i].y);
+                    acc = __fadd_rn(acc, v[i].z);
+                    acc = __fadd_rn(acc, v[i].w);
+                }
+            } else {
+                for (int i = 0; i < n; i++) acc = __fadd_rn(acc, pr[i]);
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    if (lane < RS_R && e0 + lane < E) logits[(size_t)t * E + e0 + lane] = acc;
 }
 
 extern "C" int wk_router_logits(const float *W, const float *x, int E, int H, int T, int strict,
                                 float *logits, void *stream) {
     if (E <= 0 || H <= 0 || T <= 0) return -1;
     const int rows = E * T;
+    if (strict && (H % 4))
+        return -1;
     if (strict)
-        hipLaunchKernelGGL(k_router_strict, dim3((rows + 63) / 64), dim3(64), 0, (hipStream_t)stream, W, x, E, H,
-                           T, logits);
+        hipLaunchKernelGGL(k_router_strict, dim3(T * ((E + RS_R - 1) / RS_R)), dim3(64), 0, (hipStream_t)stream, W, x,
+                           E, H, T, logits);
     else if (T >= WARP_ROUTER_MFMA_T && (H & 15) == 0)
         hipLaunchKernelGGL(k_router_mfma, dim3((T + 15) / 16, (E + 15) / 16), dim3(256), 0, (hipStream_t)stream, W, x,
                            E, H, T, logits);
