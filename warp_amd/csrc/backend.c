@@ -18,6 +18,8 @@
 #include "warp_hip.h"
 #include "warp_internal.h"
 
+#define SLOT_LEAD 80            /* record start in its slot: header + 80 = 128 */
+
 #define HIPOK(x) ((x) == hipSuccess)
 
 /* ---- small utilities ----------------------------------------------------- */
@@ -287,6 +289,7 @@ struct warp_hip_ctx {
     /* expert cache */
     uint8_t *pool;
     int n_slots, next_free;
+    size_t slot_stride;         /* bytes between slots (see slot_rec)       */
     int *slot_key, *key_slot;
     uint32_t *hits;
     uint64_t *last, clock;
@@ -513,7 +516,8 @@ static int ctx_alloc(warp_hip_ctx *c)
     DEV(c, hipMemset(c->crc_err, 0, sizeof(warp_crc_err)));
     DEV(c, hipHostMalloc((void **)&c->h_crc_err, sizeof(warp_crc_err), 0));
     DEV(c, hipHostMalloc((void **)&c->h_word, sizeof(uint32_t), 0));
-    if (c->n_slots > 0) DMALLOC(c, c->pool, (size_t)c->n_slots * g->rec_bytes);
+    c->slot_stride = (g->rec_bytes + SLOT_LEAD + 255) / 256 * 256;
+    if (c->n_slots > 0) DMALLOC(c, c->pool, (size_t)c->n_slots * c->slot_stride);
     DEV(c, hipHostMalloc((void **)&c->staging, (size_t)N_STAGE * g->rec_bytes, 0));
     /* a batch touches each expert of one layer at most twice over (the
      * records it places and the ones they evict) */
@@ -661,6 +665,17 @@ void warp_hip_close(warp_hip_ctx *c)
     if (c->cp) (void)hipStreamDestroy(c->cp);
     if (c->la) (void)hipStreamDestroy(c->la);
     free(c);
+}
+
+/* Where slot s's record starts. Slots are SLOT_LEAD + rec_bytes rounded up
+ * to 256 bytes apart (the pool is 256-byte aligned), and a record starts
+ * SLOT_LEAD bytes into its slot, so that its first index block, right after
+ * the 48-byte header, starts on a 128-byte line: a chunk's code words of
+ * one row block (a multiple of 128 bytes at the K3 shapes) then never share
+ * a line with the next chunk's, which another block of the launch reads. */
+static uint8_t *slot_rec(const warp_hip_ctx *c, int s)
+{
+    return c->pool + (size_t)s * c->slot_stride + SLOT_LEAD;
 }
 
 /* Reads and clears the sticky missing-expert flag once the compute stream
@@ -1006,7 +1021,7 @@ static int publish_slot(warp_hip_ctx *c, int layer, int expert, int s, const uin
     uint32_t off[4];
     memcpy(off, hdr + WARP_HDR_GATE_OFF, sizeof off);
     const int key = layer * c->cfg.n_experts + expert;
-    const uint8_t *slot = c->pool + (size_t)s * c->cfg.rec_bytes;
+    const uint8_t *slot = slot_rec(c, s);
     if (c->cfg.verify) {
         const size_t scales = 2u * (2 * (size_t)c->cfg.inter + c->He);
         KRN(c, wk_crc32(slot + WARP_HDR_BYTES, (size_t)off[3] + scales - WARP_HDR_BYTES, c->crc_tmp, NULL,
@@ -1051,7 +1066,7 @@ int warp_hip_put_expert(warp_hip_ctx *c, int layer, int expert, const uint8_t *r
     DEV(c, hipStreamWaitEvent(c->cp, c->ev_before, 0));
     int s = c->key_slot[key];
     if (s < 0 && (s = claim_slot(c, layer, expert)) < 0) return s;
-    DEV(c, hipMemcpyAsync(c->pool + (size_t)s * c->cfg.rec_bytes, rec, c->cfg.rec_bytes, hipMemcpyHostToDevice, c->cp));
+    DEV(c, hipMemcpyAsync(slot_rec(c, s), rec, c->cfg.rec_bytes, hipMemcpyHostToDevice, c->cp));
     DEV(c, hipStreamSynchronize(c->cp));
     if ((rc = publish_slot(c, layer, expert, s, rec)) || (rc = flush_table(c))) return rc;
     return crc_report(c);
@@ -1074,7 +1089,7 @@ int warp_hip_put_expert_dev(warp_hip_ctx *c, int layer, int expert, const uint8_
     DEV(c, hipStreamWaitEvent(c->cp, c->ev_before, 0));
     int s = c->key_slot[key];
     if (s < 0 && (s = claim_slot(c, layer, expert)) < 0) return s;
-    DEV(c, hipMemcpyAsync(c->pool + (size_t)s * c->cfg.rec_bytes, rec_dev, c->cfg.rec_bytes,
+    DEV(c, hipMemcpyAsync(slot_rec(c, s), rec_dev, c->cfg.rec_bytes,
                           hipMemcpyDeviceToDevice, c->cp));
     DEV(c, hipStreamSynchronize(c->cp));
     if ((rc = publish_slot(c, layer, expert, s, hdr)) || (rc = flush_table(c))) return rc;
@@ -1111,7 +1126,7 @@ int warp_hip_put_expert_synth(warp_hip_ctx *c, int layer, int expert, uint64_t s
     DEV(c, hipStreamWaitEvent(c->cp, c->ev_before, 0));
     int s = c->key_slot[key];
     if (s < 0 && (s = claim_slot(c, layer, expert)) < 0) return s;
-    uint8_t *slot = c->pool + (size_t)s * g->rec_bytes;
+    uint8_t *slot = slot_rec(c, s);
     KRN(c, wk_fill_random(slot, g->rec_bytes, seed, c->cp));
     DEV(c, hipMemcpyAsync(slot, hdr, sizeof hdr, hipMemcpyHostToDevice, c->cp));
     DEV(c, hipMemcpyAsync(slot + off[3], scales, 2 * (2 * (size_t)g->inter + c->He), hipMemcpyHostToDevice, c->cp));
@@ -1125,7 +1140,7 @@ const uint8_t *warp_hip_resident(warp_hip_ctx *c, int layer, int expert)
 {
     if (!c || layer < 0 || layer >= c->cfg.n_layers || expert < 0 || expert >= c->cfg.n_experts) return NULL;
     const int s = c->key_slot[layer * c->cfg.n_experts + expert];
-    return s < 0 ? NULL : c->pool + (size_t)s * c->cfg.rec_bytes;
+    return s < 0 ? NULL : slot_rec(c, s);
 }
 
 int warp_hip_set_fetch(warp_hip_ctx *c, warp_hip_fetch_fn fetch, void *user)
@@ -1193,7 +1208,7 @@ static int fill_from_fetch(warp_hip_ctx *c, int layer, int expert)
         if (rc) return rc;
         const int s = claim_slot(c, layer, expert);
         if (s < 0) return s;
-        DEV(c, hipMemcpyAsync(c->pool + (size_t)s * c->cfg.rec_bytes, src, c->cfg.rec_bytes, hipMemcpyHostToDevice,
+        DEV(c, hipMemcpyAsync(slot_rec(c, s), src, c->cfg.rec_bytes, hipMemcpyHostToDevice,
                               c->cp));
         c->stats.bytes_read += c->cfg.rec_bytes;
         return publish_slot(c, layer, expert, s, src);
@@ -1208,7 +1223,7 @@ static int fill_from_fetch(warp_hip_ctx *c, int layer, int expert)
     if (rc) return rc;
     const int s = claim_slot(c, layer, expert);
     if (s < 0) return s;
-    DEV(c, hipMemcpyAsync(c->pool + (size_t)s * c->cfg.rec_bytes, dst, c->cfg.rec_bytes, hipMemcpyHostToDevice, c->cp));
+    DEV(c, hipMemcpyAsync(slot_rec(c, s), dst, c->cfg.rec_bytes, hipMemcpyHostToDevice, c->cp));
     DEV(c, hipEventRecord(c->ev_stage[i], c->cp));
     c->stage_used[i] = 1;
     c->stats.bytes_read += c->cfg.rec_bytes;
