@@ -1570,12 +1570,21 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
     /* where the device routes with the expert table, the table kernel's
      * gate/up launch does the routing itself (one launch less) */
     const int fuse_route = use_lut && (L->resident == E || !can_fetch(c)) && wk_lut_route_ok(g->fmt, E, K, 1, 0, 2);
+    /* and where that launch leaves CUs idle, one more row of its blocks
+     * computes the shared expert's gate/up rows (one row per wave) instead
+     * of the router launch */
+    int sh_in_gu = 0;
+    if (fuse_shared && fuse_route) {
+        int gr, sp;
+        sh_in_gu = !wk_lut_plan(I, He, K, 2, 1, c->n_cu, c->part_cap, &gr, &sp) && 2 * gr * sp < c->n_cu &&
+                   gr * sp * 16 >= sa.inter && (size_t)H * sizeof(float) <= 64 * 1024;
+    }
     /* then, for sigmoid scores from an fp32 router, the router launch also
      * scores (one pass less in the routing prologue) */
-    const int scored = fuse_route && !fuse_shared && L->router && !g->router_strict &&
+    const int scored = fuse_route && (!fuse_shared || sh_in_gu) && L->router && !g->router_strict &&
                        g->router_act == WARP_HIP_ROUTE_SIGMOID;
     if ((rc = timing_begin(c, 2))) return rc;
-    if (fuse_shared) KRN(c, wk_router_shared(L->router, x_dev, E, H, c->logits, &sa, c->st));
+    if (fuse_shared && !sh_in_gu) KRN(c, wk_router_shared(L->router, x_dev, E, H, c->logits, &sa, c->st));
     else if (scored) KRN(c, wk_router_scored(L->router, x_dev, E, H, L->bias, c->logits, c->st));
     else KRN(c, logits_of(c, L, x_dev, 1, c->logits, c->st));
     if ((rc = timing_end(c))) return rc;
@@ -1640,7 +1649,8 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
                                      c->idx, c->w, c->jobs, c->njobs, c->missing, scored };
         if ((rc = timing_begin(c, 0))) return rc;
         KRN(c, wk_vq_lut(g->fmt, c->jobs, c->njobs, K, 0, 2, L->books, L->books_x31, xe, 1, c->part, c->part_cap, I, He,
-                         c->n_cu, NULL, 0, 0, 0.0f, 0.0f, fuse_route ? &ra : NULL, &sp_gu, c->st));
+                         c->n_cu, NULL, 0, 0, 0.0f, 0.0f, fuse_route ? &ra : NULL, sh_in_gu ? &sa : NULL, &sp_gu,
+                         c->st));
         if ((rc = timing_end(c))) return rc;
         /* the down launch makes its inputs from the gate/up partials (SwiGLU
          * in its prologue); its partials go after the gate/up ones */
@@ -1648,7 +1658,7 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
         if ((rc = timing_begin(c, 1))) return rc;
         KRN(c, wk_vq_lut(g->fmt, c->jobs, c->njobs, K, 2, 1, L->books, L->books_x31, NULL, 0, c->part + gu_floats,
                          c->part_cap - gu_floats, He, I, c->n_cu, c->part, sp_gu, g->act_situ, g->situ_beta,
-                         g->situ_linear_beta, NULL, &sp_d, c->st));
+                         g->situ_linear_beta, NULL, NULL, &sp_d, c->st));
         d_off = gu_floats;
         if ((rc = timing_end(c))) return rc;
     } else if (c->P6) {
@@ -1711,13 +1721,13 @@ int warp_hip_expert_ffn(warp_hip_ctx *c, int layer, int expert, const float *x_d
         int sp_gu = 0, sp_d = 0;
         if ((rc = timing_begin(c, 0))) return rc;
         KRN(c, wk_vq_lut(g->fmt, c->jobs, c->njobs, 1, 0, 2, L->books, L->books_x31, x_dev, 1, c->part, c->part_cap,
-                         I, H, c->n_cu, NULL, 0, 0, 0.0f, 0.0f, NULL, &sp_gu, c->st));
+                         I, H, c->n_cu, NULL, 0, 0, 0.0f, 0.0f, NULL, NULL, &sp_gu, c->st));
         if ((rc = timing_end(c))) return rc;
         const size_t gu_floats = (size_t)2 * sp_gu * (((size_t)I + 63) / 64) * 64;
         if ((rc = timing_begin(c, 1))) return rc;
         KRN(c, wk_vq_lut(g->fmt, c->jobs, c->njobs, 1, 2, 1, L->books, L->books_x31, NULL, 0, c->part + gu_floats,
                          c->part_cap - gu_floats, H, I, c->n_cu, c->part, sp_gu, g->act_situ, g->situ_beta,
-                         g->situ_linear_beta, NULL, &sp_d, c->st));
+                         g->situ_linear_beta, NULL, NULL, &sp_d, c->st));
         if ((rc = timing_end(c))) return rc;
         KRN(c, wk_combine_lut(c->jobs + 2, c->part + gu_floats, sp_d, 1, c->w, 1, H, NULL, NULL, c->missing, NULL,
                               out_dev, c->st));
@@ -1947,7 +1957,7 @@ int warp_hip_vq_matvec(warp_hip_ctx *c, int layer, int kind, const uint8_t *rec_
         float *yk[3] = { y_dev, y_dev, y_dev };
         int sp = 0;
         KRN(c, wk_vq_lut(c->cfg.fmt, c->jobs, c->njobs, 1, kind, 1, L->books, L->books_x31, x_dev, 1, c->part, c->part_cap, M, N,
-                         c->n_cu, NULL, 0, 0, 0.0f, 0.0f, NULL, &sp, c->st));
+                         c->n_cu, NULL, 0, 0, 0.0f, 0.0f, NULL, NULL, &sp, c->st));
         KRN(c, wk_lut_reduce(c->jobs, c->njobs, 1, kind, 1, c->part, sp, M, yk, c->st));
     } else {
         float *yk[3] = { y_dev, y_dev, y_dev };

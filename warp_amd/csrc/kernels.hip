@@ -1726,6 +1726,10 @@ struct LutArgs {
     // block 0 writes idx, w, the job lists of all three kinds (into jobs),
     // njobs and the missing flag for the launches that follow
     warp_route_args r;
+    // (routed launches) the blocks of one extra grid row instead compute
+    // the shared expert's h = act(gate . x, up . x), one row per wave, as
+    // k_router_shared does, when sh.h is set
+    warp_shared_args sh;
 };
 
 // Coherent accesses, for what one block of the fused decode launch writes
@@ -2366,8 +2370,50 @@ __device__ __forceinline__ void lut_item(const LutArgs &a, const unsigned bx, co
     }
 }
 
+// A routed gate/up launch's extra grid row: the shared expert's gate and up
+// rows for the token, one row per wave (k_router_shared's loads, sums and
+// activation), into sh.h. x is staged in the table buffers.
+template <int BITS, int MC>
+__device__ __forceinline__ void lut_shared_rows(const LutArgs &a) {
+    extern __shared__ __attribute__((aligned(16))) float lut[];
+    float *xl = lut;
+    using Q = QRow<BITS, MC>;
+    const warp_shared_args &sa = a.sh;
+    const int H = a.N;
+    const int r = (int)blockIdx.x * LUT_NW + (int)(threadIdx.x >> 6), rr = min(r, sa.inter - 1);
+    const int nc = H / Q::WPC, ng = H / sa.group;
+    Q qg, qu;
+    qg.load(sa.q[0] + (size_t)rr * sa.rowbytes[0], sa.s[0] + (size_t)rr * ng, sa.group, nc);
+    qu.load(sa.q[1] + (size_t)rr * sa.rowbytes[1], sa.s[1] + (size_t)rr * ng, sa.group, nc);
+    for (int i = threadIdx.x; i < H / 4; i += LUT_NW * 64) ((float4 *)xl)[i] = ((const float4 *)a.x)[i];
+    __syncthreads();
+    const float gv = qg.dot(xl, nc), uv = qu.dot(xl, nc);
+    if (r < sa.inter && (threadIdx.x & 63) == 0) sa.h[r] = act_pair(gv, uv, sa.situ, sa.beta, sa.lbeta);
+}
+
+__device__ __forceinline__ void lut_shared(const LutArgs &a) {
+    const int mc = (a.N / (a.sh.bits == 8 ? 16 : 32) + 63) / 64;
+    if (a.sh.bits == 8) {
+        if (mc <= 1) lut_shared_rows<8, 1>(a);
+        else if (mc <= 2) lut_shared_rows<8, 2>(a);
+        else if (mc <= 4) lut_shared_rows<8, 4>(a);
+        else lut_shared_rows<8, SH_MAXC>(a);
+    } else {
+        if (mc <= 1) lut_shared_rows<4, 1>(a);
+        else if (mc <= 2) lut_shared_rows<4, 2>(a);
+        else if (mc <= 4) lut_shared_rows<4, 4>(a);
+        else lut_shared_rows<4, SH_MAXC>(a);
+    }
+}
+
 template <int FMT, bool X31, bool SHX, bool ACT, bool RT>
 __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
+    if constexpr (RT) {
+        if (a.sh.h && blockIdx.y == gridDim.y - 1) {      // uniform per block
+            lut_shared(a);
+            return;
+        }
+    }
     lut_item<FMT, X31, SHX, ACT, RT, false>(a, blockIdx.x, blockIdx.y, nullptr, nullptr);
 }
 
@@ -2581,8 +2627,8 @@ static int launch_lut(const LutArgs &a, int groups, int nkinds, void *stream) {
         if (e != hipSuccess) return -(int)e - 1000;
         attr = true;
     }
-    hipLaunchKernelGGL((k_vq_lut<FMT, X31, SHX, ACT, RT>), dim3(groups * a.splits, nkinds), dim3(LUT_NW * 64), lds,
-                       (hipStream_t)stream, a);
+    hipLaunchKernelGGL((k_vq_lut<FMT, X31, SHX, ACT, RT>), dim3(groups * a.splits, nkinds + (a.sh.h ? 1 : 0)),
+                       dim3(LUT_NW * 64), lds, (hipStream_t)stream, a);
     CHECK_LAUNCH();
     return 0;
 }
@@ -2622,8 +2668,9 @@ extern "C" int wk_vq_lut(int fmt, const warp_job *jobs, const int *njobs, int ma
                          const uint16_t *books, int books_x31, const float *x, int shared_x, float *part,
                          size_t cap_floats, int M, int N, int target_blocks, const float *act_part,
                          int act_splits, int act_situ, float act_beta, float act_lbeta,
-                         const warp_route_args *route, int *splits_out, void *stream) {
+                         const warp_route_args *route, const warp_shared_args *sh, int *splits_out, void *stream) {
     if (kind_lo < 0 || kind_lo + nkinds > 3 || !books || !part) return -1;
+    if (sh && (!route || !wk_shared_fast_ok(N, sh) || (size_t)N * sizeof(float) > 64 * 1024)) return -1;
     if (act_part && (shared_x || kind_lo != 2 || nkinds != 1 || act_splits <= 0)) return -1;
     if (route && !wk_lut_route_ok(fmt, route->E, max_jobs, shared_x, kind_lo, nkinds)) return -1;
     int groups, splits;
@@ -2646,6 +2693,8 @@ extern "C" int wk_vq_lut(int fmt, const warp_job *jobs, const int *njobs, int ma
     a.act_beta = act_beta;
     a.act_lbeta = act_lbeta;
     a.r = route ? *route : warp_route_args{};
+    a.sh = sh ? *sh : warp_shared_args{};
+    if (sh && groups * splits * LUT_NW < sh->inter) return -1;   // one row per wave of the extra grid row
     if (splits_out) *splits_out = splits;
     switch (fmt) {
     case WARP_FMT_VQ3R: return launch_lut_x<WARP_FMT_VQ3R>(a, groups, nkinds, books_x31, stream);
