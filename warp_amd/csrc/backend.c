@@ -1572,12 +1572,15 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
     const int fuse_route = use_lut && (L->resident == E || !can_fetch(c)) && wk_lut_route_ok(g->fmt, E, K, 1, 0, 2);
     /* and where that launch leaves CUs idle, one more row of its blocks
      * computes the shared expert's gate/up rows (one row per wave) instead
-     * of the router launch */
+     * of the router launch, and blocks appended to the down launch its down
+     * rows (four per wave) instead of the combine */
     int sh_in_gu = 0;
     if (fuse_shared && fuse_route) {
         int gr, sp;
         sh_in_gu = !wk_lut_plan(I, He, K, 2, 1, c->n_cu, c->part_cap, &gr, &sp) && 2 * gr * sp < c->n_cu &&
-                   gr * sp * 16 >= sa.inter && (size_t)H * sizeof(float) <= 64 * 1024;
+                   gr * sp * 16 >= sa.inter && (size_t)H * sizeof(float) <= 64 * 1024 &&
+                   (size_t)sa.inter * sizeof(float) <= 64 * 1024 && sa.inter / (sa.bits == 8 ? 16 : 32) <= 256 &&
+                   (H + 63) / 64 < c->n_cu / 2;
     }
     /* then, for sigmoid scores from an fp32 router, the router launch also
      * scores (one pass less in the routing prologue) */
@@ -1649,7 +1652,7 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
                                      c->idx, c->w, c->jobs, c->njobs, c->missing, scored };
         if ((rc = timing_begin(c, 0))) return rc;
         KRN(c, wk_vq_lut(g->fmt, c->jobs, c->njobs, K, 0, 2, L->books, L->books_x31, xe, 1, c->part, c->part_cap, I, He,
-                         c->n_cu, NULL, 0, 0, 0.0f, 0.0f, fuse_route ? &ra : NULL, sh_in_gu ? &sa : NULL, &sp_gu,
+                         c->n_cu, NULL, 0, 0, 0.0f, 0.0f, fuse_route ? &ra : NULL, sh_in_gu ? &sa : NULL, NULL, &sp_gu,
                          c->st));
         if ((rc = timing_end(c))) return rc;
         /* the down launch makes its inputs from the gate/up partials (SwiGLU
@@ -1658,7 +1661,8 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
         if ((rc = timing_begin(c, 1))) return rc;
         KRN(c, wk_vq_lut(g->fmt, c->jobs, c->njobs, K, 2, 1, L->books, L->books_x31, NULL, 0, c->part + gu_floats,
                          c->part_cap - gu_floats, He, I, c->n_cu, c->part, sp_gu, g->act_situ, g->situ_beta,
-                         g->situ_linear_beta, NULL, NULL, &sp_d, c->st));
+                         g->situ_linear_beta, NULL, sh_in_gu ? &sa : NULL, sh_in_gu ? c->sho : NULL, &sp_d,
+                         c->st));
         d_off = gu_floats;
         if ((rc = timing_end(c))) return rc;
     } else if (c->P6) {
@@ -1680,8 +1684,9 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
     }
     if (L->sq[0] && !fuse_shared && (rc = shared_ffn(c, L, x_dev, 1))) return rc;
     if (use_lut)
-        KRN(c, wk_combine_lut(c->jobs + 2 * (size_t)K, c->part + d_off, sp_d, K, c->w, K, He, add0, add1, c->missing,
-                              fuse_shared ? &sa : NULL, ysum, c->st));
+        KRN(c, wk_combine_lut(c->jobs + 2 * (size_t)K, c->part + d_off, sp_d, K, c->w, K, He,
+                              sh_in_gu ? c->sho : add0, add1, c->missing, fuse_shared && !sh_in_gu ? &sa : NULL, ysum,
+                              c->st));
     else
         KRN(c, wk_combine(c->yd, c->w, K, He, add0, add1, c->missing, ysum, c->st));
 tail:
@@ -1721,13 +1726,13 @@ int warp_hip_expert_ffn(warp_hip_ctx *c, int layer, int expert, const float *x_d
         int sp_gu = 0, sp_d = 0;
         if ((rc = timing_begin(c, 0))) return rc;
         KRN(c, wk_vq_lut(g->fmt, c->jobs, c->njobs, 1, 0, 2, L->books, L->books_x31, x_dev, 1, c->part, c->part_cap,
-                         I, H, c->n_cu, NULL, 0, 0, 0.0f, 0.0f, NULL, NULL, &sp_gu, c->st));
+                         I, H, c->n_cu, NULL, 0, 0, 0.0f, 0.0f, NULL, NULL, NULL, &sp_gu, c->st));
         if ((rc = timing_end(c))) return rc;
         const size_t gu_floats = (size_t)2 * sp_gu * (((size_t)I + 63) / 64) * 64;
         if ((rc = timing_begin(c, 1))) return rc;
         KRN(c, wk_vq_lut(g->fmt, c->jobs, c->njobs, 1, 2, 1, L->books, L->books_x31, NULL, 0, c->part + gu_floats,
                          c->part_cap - gu_floats, H, I, c->n_cu, c->part, sp_gu, g->act_situ, g->situ_beta,
-                         g->situ_linear_beta, NULL, NULL, &sp_d, c->st));
+                         g->situ_linear_beta, NULL, NULL, NULL, &sp_d, c->st));
         if ((rc = timing_end(c))) return rc;
         KRN(c, wk_combine_lut(c->jobs + 2, c->part + gu_floats, sp_d, 1, c->w, 1, H, NULL, NULL, c->missing, NULL,
                               out_dev, c->st));
@@ -1957,7 +1962,7 @@ int warp_hip_vq_matvec(warp_hip_ctx *c, int layer, int kind, const uint8_t *rec_
         float *yk[3] = { y_dev, y_dev, y_dev };
         int sp = 0;
         KRN(c, wk_vq_lut(c->cfg.fmt, c->jobs, c->njobs, 1, kind, 1, L->books, L->books_x31, x_dev, 1, c->part, c->part_cap, M, N,
-                         c->n_cu, NULL, 0, 0, 0.0f, 0.0f, NULL, NULL, &sp, c->st));
+                         c->n_cu, NULL, 0, 0, 0.0f, 0.0f, NULL, NULL, NULL, &sp, c->st));
         KRN(c, wk_lut_reduce(c->jobs, c->njobs, 1, kind, 1, c->part, sp, M, yk, c->st));
     } else {
         float *yk[3] = { y_dev, y_dev, y_dev };

@@ -1728,8 +1728,13 @@ struct LutArgs {
     warp_route_args r;
     // (routed launches) the blocks of one extra grid row instead compute
     // the shared expert's h = act(gate . x, up . x), one row per wave, as
-    // k_router_shared does, when sh.h is set
+    // k_router_shared does, when sh.h is set;
+    // (down launches, sh_out set) blocks sh_first.. instead compute the
+    // shared expert's down rows sh_out = down . sh.h, four rows per wave,
+    // as k_combine_lut does
     warp_shared_args sh;
+    float *sh_out;
+    int sh_first;
 };
 
 // Coherent accesses, for what one block of the fused decode launch writes
@@ -2406,11 +2411,54 @@ __device__ __forceinline__ void lut_shared(const LutArgs &a) {
     }
 }
 
+// A down launch's appended blocks: the shared expert's down rows, four per
+// wave (k_combine_lut's row loads and sums), h staged in the table buffers.
+template <int BITS, int MC>
+__device__ __forceinline__ void lut_shared_down_rows(const LutArgs &a) {
+    extern __shared__ __attribute__((aligned(16))) float lut[];
+    using Q = QRow<BITS, MC>;
+    const warp_shared_args &sa = a.sh;
+    const int M = a.M, snc = sa.inter / Q::WPC, sng = sa.inter / sa.group;
+    const int r0 = ((int)blockIdx.x - a.sh_first) * LUT_NW * 4 + (int)(threadIdx.x >> 6) * 4;
+    Q qd[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int rr = min(r0 + k, M - 1);
+        qd[k].load(sa.q[2] + (size_t)rr * sa.rowbytes[2], sa.s[2] + (size_t)rr * sng, sa.group, snc);
+    }
+    for (int i = threadIdx.x; i < sa.inter / 4; i += LUT_NW * 64) ((float4 *)lut)[i] = ((const float4 *)sa.h)[i];
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const float v = qd[k].dot(lut, snc);
+        if ((threadIdx.x & 63) == 0 && r0 + k < M) a.sh_out[r0 + k] = v;
+    }
+}
+
+__device__ __forceinline__ void lut_shared_down(const LutArgs &a) {
+    const int mc = (a.sh.inter / (a.sh.bits == 8 ? 16 : 32) + 63) / 64;
+    if (a.sh.bits == 8) {
+        if (mc <= 1) lut_shared_down_rows<8, 1>(a);
+        else if (mc <= 2) lut_shared_down_rows<8, 2>(a);
+        else lut_shared_down_rows<8, 4>(a);
+    } else {
+        if (mc <= 1) lut_shared_down_rows<4, 1>(a);
+        else if (mc <= 2) lut_shared_down_rows<4, 2>(a);
+        else lut_shared_down_rows<4, 4>(a);
+    }
+}
+
 template <int FMT, bool X31, bool SHX, bool ACT, bool RT>
 __global__ __launch_bounds__(LUT_NW * 64) void k_vq_lut(LutArgs a) {
     if constexpr (RT) {
         if (a.sh.h && blockIdx.y == gridDim.y - 1) {      // uniform per block
             lut_shared(a);
+            return;
+        }
+    }
+    if constexpr (ACT && !SHX) {
+        if (a.sh_out && (int)blockIdx.x >= a.sh_first) {  // uniform per block
+            lut_shared_down(a);
             return;
         }
     }
@@ -2627,7 +2675,8 @@ static int launch_lut(const LutArgs &a, int groups, int nkinds, void *stream) {
         if (e != hipSuccess) return -(int)e - 1000;
         attr = true;
     }
-    hipLaunchKernelGGL((k_vq_lut<FMT, X31, SHX, ACT, RT>), dim3(groups * a.splits, nkinds + (a.sh.h ? 1 : 0)),
+    const int gx = groups * a.splits, nsh = a.sh_out ? (a.M + LUT_NW * 4 - 1) / (LUT_NW * 4) : 0;
+    hipLaunchKernelGGL((k_vq_lut<FMT, X31, SHX, ACT, RT>), dim3(gx + nsh, nkinds + (a.sh.h && !a.sh_out ? 1 : 0)),
                        dim3(LUT_NW * 64), lds, (hipStream_t)stream, a);
     CHECK_LAUNCH();
     return 0;
@@ -2668,9 +2717,16 @@ extern "C" int wk_vq_lut(int fmt, const warp_job *jobs, const int *njobs, int ma
                          const uint16_t *books, int books_x31, const float *x, int shared_x, float *part,
                          size_t cap_floats, int M, int N, int target_blocks, const float *act_part,
                          int act_splits, int act_situ, float act_beta, float act_lbeta,
-                         const warp_route_args *route, const warp_shared_args *sh, int *splits_out, void *stream) {
+                         const warp_route_args *route, const warp_shared_args *sh, float *sh_out,
+                         int *splits_out, void *stream) {
     if (kind_lo < 0 || kind_lo + nkinds > 3 || !books || !part) return -1;
-    if (sh && (!route || !wk_shared_fast_ok(N, sh) || (size_t)N * sizeof(float) > 64 * 1024)) return -1;
+    if (sh && !sh_out && (!route || !wk_shared_fast_ok(N, sh) || (size_t)N * sizeof(float) > 64 * 1024)) return -1;
+    // the shared down rows: M rows of sh->inter weights, four per wave
+    const int nsh = sh && sh_out ? (M + LUT_NW * 4 - 1) / (LUT_NW * 4) : 0;
+    if (sh_out && (!sh || !act_part || sh->inter / (sh->bits == 8 ? 16 : 32) > 64 * 4 ||
+                   (size_t)sh->inter * sizeof(float) > 64 * 1024 || nsh >= target_blocks))
+        return -1;
+    target_blocks -= nsh;
     if (act_part && (shared_x || kind_lo != 2 || nkinds != 1 || act_splits <= 0)) return -1;
     if (route && !wk_lut_route_ok(fmt, route->E, max_jobs, shared_x, kind_lo, nkinds)) return -1;
     int groups, splits;
@@ -2694,7 +2750,9 @@ extern "C" int wk_vq_lut(int fmt, const warp_job *jobs, const int *njobs, int ma
     a.act_lbeta = act_lbeta;
     a.r = route ? *route : warp_route_args{};
     a.sh = sh ? *sh : warp_shared_args{};
-    if (sh && groups * splits * LUT_NW < sh->inter) return -1;   // one row per wave of the extra grid row
+    a.sh_out = sh_out;
+    a.sh_first = groups * splits;
+    if (sh && !sh_out && groups * splits * LUT_NW < sh->inter) return -1;   // one row per wave of the extra grid row
     if (splits_out) *splits_out = splits;
     switch (fmt) {
     case WARP_FMT_VQ3R: return launch_lut_x<WARP_FMT_VQ3R>(a, groups, nkinds, books_x31, stream);

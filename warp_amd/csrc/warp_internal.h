@@ -189,11 +189,15 @@ int wk_vq_lut(int fmt, const warp_job *jobs, const int *njobs, int max_jobs, int
               int nkinds, const uint16_t *books, int books_x31, const float *x, int shared_x, float *part,
               size_t cap_floats, int M, int N, int target_blocks, const float *act_part,
               int act_splits, int act_situ, float act_beta, float act_lbeta,
-              const warp_route_args *route, const warp_shared_args *sh, int *splits_out, void *stream);
+              const warp_route_args *route, const warp_shared_args *sh, float *sh_out, int *splits_out,
+              void *stream);
 /* (sh, with route: one more grid row of blocks computes the shared
  * expert's h = act(gate . x, up . x) into sh->h, as wk_router_shared does,
  * one row per wave; the launch must have as many waves per row as the
- * shared expert has rows, else -1. NULL otherwise.
+ * shared expert has rows, else -1. sh with sh_out, on a down launch
+ * (act_part): M / 64 blocks appended to the plan's (which gets that many
+ * fewer) compute the shared expert's down rows sh_out [M] = down . sh->h,
+ * as wk_combine_lut does with its sa. NULL otherwise.
  * act_part: the down launch makes each job's input itself, h = act(gate,
  * up) from the gate/up partial sums -- kinds 0 and 1 of the previous launch
  * with act_splits splits -- instead of reading x; NULL otherwise.
