@@ -524,7 +524,8 @@ def run_prefill(args):
     gate, down, scales_b, rec_bytes = kimi_rec_layout()
     ctx = warp_amd.Context(hidden=KH, inter=KI, n_experts=KE, top_k=KK, n_layers=layers, fmt="VQ12",
                            renorm=True, routed_scale=1.0, router_act=ROUTE_SOFTMAX, max_tokens=T,
-                           rec_bytes=rec_bytes, cache_bytes=layers * KE * rec_bytes)
+                           rec_bytes=rec_bytes, cache_bytes=layers * KE * rec_bytes,
+                           prefill_fp16=args.prefill == "fp16")
     rng = np.random.Generator(np.random.PCG64(4321))
     X = rng.standard_normal((T, KH), dtype=np.float32)
     shared_bytes = kimi_layers(ctx, layers, rng, lambda L, router: zipf_bias(router, X, seed=5 + L))
@@ -573,7 +574,7 @@ def run_prefill(args):
         "unit": "MoE-layer tokens/s",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms / args.steps, 4),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16" if args.prefill == "fp16" else "fp32",
         "data": "synthetic (random codes, codebooks, scales, shared expert and routers of the Kimi-Linear shapes; "
                 "a per-expert bias that skews tokens per expert towards Zipf(1.1))",
         "config": {"workload": f"Kimi-Linear-shape MoE layer, prefill of {T} tokens, {layers}-layer stack",
@@ -586,8 +587,13 @@ def run_prefill(args):
         "hbm": {"achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)},
         "mfma": {"achieved": round(tfs, 2), "peak": 2500.0, "unit": "TFLOP/s",
                  "frac": round(tfs / 2500.0, 5),
-                 "note": "useful FLOPs (2 x 3 x H x I per pair, plus the shared expert); the expert matvecs run "
-                         "fp16 hi/lo halves of x on the matrix cores, twice the useful MFMA work"},
+                 "note": "useful FLOPs (2 x 3 x H x I per pair, plus the shared expert); " +
+                         ("the expert products run one fp16 operand per position (stages added) against x's fp16 "
+                          "high half" if args.prefill == "fp16" else
+                          "the expert products run fp16 hi/lo halves of x and every stage on the matrix cores, "
+                          "2 x stages times the useful MFMA work")},
+        "precision": ("fp16 operands, fp32 accumulation (outputs within 2e-3 of the reference)"
+                      if args.prefill == "fp16" else "exact products (outputs within 1e-4 of the reference)"),
         "wall_s": round(wall, 3),
         "cpu_baseline": None if args.no_cpu else cpu_baseline_prefill(args, args.cpu_seconds, T),
     }
@@ -1104,6 +1110,10 @@ def main():
     ap.add_argument("--matvec-path", choices=["auto", "mfma", "fused"], default="auto",
                     help="expert matvec kernel: auto = the LUT kernel, mfma = decode-then-dot on the matrix cores, "
                          "fused = the LUT kernel's gate/up, down and combine in one launch per layer")
+    ap.add_argument("--prefill", choices=["exact", "fp16"], default="exact",
+                    help="kimi-prefill: the expert products' precision: exact (fp16 hi/lo halves of x, every stage "
+                         "a product of its own) or fp16 (stages added into one fp16 operand, x's high half only: a "
+                         "quarter of the matrix-core work, outputs within 2e-3)")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="before timing, one device-to-device copy of this many MiB (a known-size "
                          "kernel for scaling the profiler's traffic counters)")
@@ -1212,7 +1222,8 @@ def run_children(args):
     out = {}
     for key, wl in CHILDREN:
         cmd = [sys.executable, os.path.abspath(__file__), "--workload", wl, "--twin-dir", args.twin_dir,
-               "--cpu-seconds", str(args.cpu_seconds), "--matvec-path", args.matvec_path]
+               "--cpu-seconds", str(args.cpu_seconds), "--matvec-path", args.matvec_path,
+               "--prefill", args.prefill]
         if wl == "k3-miss":
             cmd += ["--steps", "8", "--warmup", "2"]
         else:

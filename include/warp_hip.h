@@ -145,6 +145,13 @@ typedef struct {
     int latent_norm;       /* latent_moe_use_norm: RMS norm of the experts'
                             * combined latent output                          */
     float norm_eps;        /* rms_norm_eps for that norm                       */
+    int prefill_fp16;      /* chunks (warp_hip_moe_chunk*): the routed experts'
+                            * matrix-core products in fp16 -- the stages'
+                            * codebook vectors added into one fp16 value, x's
+                            * fp16 high half only -- a quarter of the MFMAs,
+                            * outputs within about 1e-3 of the reference
+                            * instead of 1e-4 (the reference CPU path has no
+                            * such mode; 0 keeps the exact products)          */
 } warp_hip_cfg;
 
 typedef struct warp_hip_ctx warp_hip_ctx;

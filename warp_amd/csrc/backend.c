@@ -283,6 +283,8 @@ struct warp_hip_ctx {
     int S, En, SB, P6, P_max, max_jobs;
     size_t gate_bytes, down_bytes;
     hipStream_t st, cp, la;
+    hipStream_t sx;                 /* a chunk's shared expert, beside its routed experts */
+    hipEvent_t ev_sx0, ev_sx1;      /* fork from st, join back into st */
     hipEvent_t ev_copy, ev_before, ev_after, ev_la, ev_x, ev_stage[N_STAGE];
     int copy_pending;
     layer_t *L;
@@ -335,9 +337,13 @@ struct warp_hip_ctx {
     float *yg, *yu, *yd;
     uint16_t *xsh;
     float *xscaleh, *hbuf;
+    uint16_t *xsp;                /* prefill_fp16: x per pair slot, position-group-major */
+    float *xscalep;
     float *shg, *shu, *shh, *sho;
     uint16_t *shxs;               /* the shared expert's h split for the matrix cores */
     float *shxscale;
+    uint16_t *shxin;              /* its x split (a chunk's routed experts use xs meanwhile) */
+    float *shxinscale;
     int sh_cap;
     int8_t *lut8, *lut8d;
     float *lscale, *lscaled;
@@ -449,6 +455,10 @@ static int ctx_alloc(warp_hip_ctx *c)
     DMALLOC(c, c->xsh, P * I * 2 * 2);
     DMALLOC(c, c->xscaleh, P * 4);
     DMALLOC(c, c->hbuf, P * I * 4);
+    if (g->prefill_fp16) {
+        DMALLOC(c, c->xsp, P * He * 2);
+        DMALLOC(c, c->xscalep, P * 4);
+    }
     DMALLOC(c, c->sho, (size_t)T * H * 4);
     DMALLOC(c, c->xin, (size_t)T * H * 4);
     DMALLOC(c, c->xout, (size_t)T * H * 4);
@@ -584,6 +594,9 @@ int warp_hip_open(const warp_hip_cfg *cfg, warp_hip_ctx **out)
     if (!HIPOK(hipSetDevice(g->device)) || !HIPOK(hipStreamCreateWithFlags(&c->st, hipStreamNonBlocking)) ||
         !HIPOK(hipStreamCreateWithFlags(&c->cp, hipStreamNonBlocking)) ||
         !HIPOK(hipStreamCreateWithFlags(&c->la, hipStreamNonBlocking)) ||
+        !HIPOK(hipStreamCreateWithFlags(&c->sx, hipStreamNonBlocking)) ||
+        !HIPOK(hipEventCreateWithFlags(&c->ev_sx0, hipEventDisableTiming)) ||
+        !HIPOK(hipEventCreateWithFlags(&c->ev_sx1, hipEventDisableTiming)) ||
         !HIPOK(hipEventCreateWithFlags(&c->ev_copy, hipEventDisableTiming)) ||
         !HIPOK(hipEventCreateWithFlags(&c->ev_before, hipEventDisableTiming)) ||
         !HIPOK(hipEventCreateWithFlags(&c->ev_after, hipEventDisableTiming)) ||
@@ -628,6 +641,7 @@ void warp_hip_close(warp_hip_ctx *c)
     if (c->st) (void)hipStreamSynchronize(c->st);
     if (c->cp) (void)hipStreamSynchronize(c->cp);
     if (c->la) (void)hipStreamSynchronize(c->la);
+    if (c->sx) (void)hipStreamSynchronize(c->sx);
     if (c->L)
         for (int l = 0; l < c->cfg.n_layers; l++) {
             layer_t *L = &c->L[l];
@@ -637,11 +651,12 @@ void warp_hip_close(warp_hip_ctx *c)
             hfree(L->lnorm);
         }
     free(c->L);
-    void *d[] = { c->logits, c->idx, c->w, c->jobs, c->njobs, c->missing, c->xs, c->xscale, c->yg, c->yu,
+    void *d[] = { c->logits, c->idx, c->w, c->jobs, c->njobs, c->missing, c->xs, c->xscale, c->xsp, c->xscalep,
+                  c->yg, c->yu,
                   c->yd, c->xsh, c->xscaleh, c->hbuf, c->shg, c->shu, c->shh, c->sho, c->lut8, c->lut8d,
                   c->lscale, c->lscaled, c->counts, c->offsets, c->pair_tok, c->pair_exp, c->pair_w, c->tok_slots, c->runs,
                   c->xin, c->xout, c->la_logits, c->la_idx, c->la_w, c->table_dev, c->pool, c->part,
-                  c->shxs, c->shxscale, c->tq_dev, c->crc_tmp, c->crc_bad, c->crc_err, c->xlat, c->ylat, c->yup,
+                  c->shxs, c->shxscale, c->shxin, c->shxinscale, c->tq_dev, c->crc_tmp, c->crc_bad, c->crc_err, c->xlat, c->ylat, c->yup,
                   c->fz_sync };
     for (size_t i = 0; i < sizeof d / sizeof d[0]; i++) hfree(d[i]);
     hhfree(c->h_idx); hhfree(c->h_w); hhfree(c->h_la_idx); hhfree(c->h_missing); hhfree(c->staging);
@@ -664,6 +679,9 @@ void warp_hip_close(warp_hip_ctx *c)
     if (c->st) (void)hipStreamDestroy(c->st);
     if (c->cp) (void)hipStreamDestroy(c->cp);
     if (c->la) (void)hipStreamDestroy(c->la);
+    if (c->ev_sx0) (void)hipEventDestroy(c->ev_sx0);
+    if (c->ev_sx1) (void)hipEventDestroy(c->ev_sx1);
+    if (c->sx) (void)hipStreamDestroy(c->sx);
     free(c);
 }
 
@@ -845,9 +863,10 @@ int warp_hip_set_shared(warp_hip_ctx *c, int layer, int bits, int group, int int
     for (int l = 0; l < c->cfg.n_layers; l++) if (c->L[l].s_inter > max_is) max_is = c->L[l].s_inter;
     if (max_is > c->sh_cap) {
         hfree(c->shg); hfree(c->shu); hfree(c->shh); hfree(c->shxs); hfree(c->shxscale);
+        hfree(c->shxin); hfree(c->shxinscale);
         c->shg = c->shu = c->shh = NULL;
-        c->shxs = NULL;
-        c->shxscale = NULL;
+        c->shxs = c->shxin = NULL;
+        c->shxscale = c->shxinscale = NULL;
         c->sh_cap = 0;
         const size_t bytes = (size_t)c->cfg.max_tokens * max_is * 4;
         DMALLOC(c, c->shg, bytes);
@@ -855,6 +874,8 @@ int warp_hip_set_shared(warp_hip_ctx *c, int layer, int bits, int group, int int
         DMALLOC(c, c->shh, bytes);
         DMALLOC(c, c->shxs, bytes);
         DMALLOC(c, c->shxscale, (size_t)c->cfg.max_tokens * 4);
+        DMALLOC(c, c->shxin, (size_t)c->cfg.max_tokens * c->cfg.hidden * 2 * 2);
+        DMALLOC(c, c->shxinscale, (size_t)c->cfg.max_tokens * 4);
         c->sh_cap = max_is;
     }
     return 0;
@@ -1434,7 +1455,10 @@ static int shared_args(const warp_hip_ctx *c, const layer_t *L, warp_shared_args
     return 1;
 }
 
-static int shared_ffn(warp_hip_ctx *c, const layer_t *L, const float *x, int T)
+/* The shared expert of T tokens into sho, on stream s; it touches only the
+ * shared expert's own scratch (sh*), so it may run beside the routed
+ * experts. */
+static int shared_ffn(warp_hip_ctx *c, const layer_t *L, const float *x, int T, hipStream_t s)
 {
     const warp_hip_cfg *g = &c->cfg;
     const int H = g->hidden, Is = L->s_inter;
@@ -1444,23 +1468,23 @@ static int shared_ffn(warp_hip_ctx *c, const layer_t *L, const float *x, int T)
         const int8_t *wq[2] = {L->sq[0], L->sq[1]};
         const uint16_t *wsc[2] = {L->ss[0], L->ss[1]};
         float *gu[2] = {c->shg, c->shu};
-        KRN(c, wk_split(x, T, H, c->xs, c->xscale, c->st));
+        KRN(c, wk_split(x, T, H, c->shxin, c->shxinscale, s));
         /* gate and up in one launch: they share x */
-        KRN(c, wk_mvq_gemm(2, wq, wsc, L->s_rowbytes, L->s_group, L->s_bits, c->xs, c->xscale, Is, H, T, gu,
-                           c->st));
+        KRN(c, wk_mvq_gemm(2, wq, wsc, L->s_rowbytes, L->s_group, L->s_bits, c->shxin, c->shxinscale, Is, H, T, gu,
+                           s));
         KRN(c, wk_act_split(c->shg, c->shu, T, Is, g->act_situ, g->situ_beta, g->situ_linear_beta, c->shxs,
-                            c->shxscale, NULL, c->st));
+                            c->shxscale, NULL, s));
         const int8_t *dq = L->sq[2];
         const uint16_t *dsc = L->ss[2];
         float *dy = c->sho;
         KRN(c, wk_mvq_gemm(1, &dq, &dsc, &L->s_rowbytes[2], L->s_group, L->s_bits, c->shxs, c->shxscale, H, Is, T,
-                           &dy, c->st));
+                           &dy, s));
         return 0;
     }
-    KRN(c, wk_mvq(L->sq[0], L->ss[0], L->s_rowbytes[0], L->s_group, L->s_bits, x, Is, H, T, c->shg, c->st));
-    KRN(c, wk_mvq(L->sq[1], L->ss[1], L->s_rowbytes[1], L->s_group, L->s_bits, x, Is, H, T, c->shu, c->st));
-    KRN(c, wk_act(c->shg, c->shu, T, Is, g->act_situ, g->situ_beta, g->situ_linear_beta, c->shh, c->st));
-    KRN(c, wk_mvq(L->sq[2], L->ss[2], L->s_rowbytes[2], L->s_group, L->s_bits, c->shh, H, Is, T, c->sho, c->st));
+    KRN(c, wk_mvq(L->sq[0], L->ss[0], L->s_rowbytes[0], L->s_group, L->s_bits, x, Is, H, T, c->shg, s));
+    KRN(c, wk_mvq(L->sq[1], L->ss[1], L->s_rowbytes[1], L->s_group, L->s_bits, x, Is, H, T, c->shu, s));
+    KRN(c, wk_act(c->shg, c->shu, T, Is, g->act_situ, g->situ_beta, g->situ_linear_beta, c->shh, s));
+    KRN(c, wk_mvq(L->sq[2], L->ss[2], L->s_rowbytes[2], L->s_group, L->s_bits, c->shh, H, Is, T, c->sho, s));
     return 0;
 }
 
@@ -1630,7 +1654,7 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
     float *ysum = lat ? c->ylat : out_dev;
     if (use_lut && fuse_route && !fuse_shared && c->mv_path == WARP_HIP_PATH_LUT_FUSED) {
         /* gate/up, down and the combine in one launch */
-        if (L->sq[0] && (rc = shared_ffn(c, L, x_dev, 1))) return rc;
+        if (L->sq[0] && (rc = shared_ffn(c, L, x_dev, 1, c->st))) return rc;
         const warp_route_args ra = { c->logits, L->bias, table, E, g->router_act, g->renorm, I, g->routed_scale,
                                      c->idx, c->w, c->jobs, c->njobs, c->missing, scored };
         if ((rc = timing_begin(c, 0))) return rc;
@@ -1682,7 +1706,7 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
         KRN(c, wk_vq_matvec(g->fmt, c->jobs, c->njobs, K, 2, 1, L->books, c->xsh, c->xscaleh, yk, He, I, 1, c->st));
         if ((rc = timing_end(c))) return rc;
     }
-    if (L->sq[0] && !fuse_shared && (rc = shared_ffn(c, L, x_dev, 1))) return rc;
+    if (L->sq[0] && !fuse_shared && (rc = shared_ffn(c, L, x_dev, 1, c->st))) return rc;
     if (use_lut)
         KRN(c, wk_combine_lut(c->jobs + 2 * (size_t)K, c->part + d_off, sp_d, K, c->w, K, He,
                               sh_in_gu ? c->sho : add0, add1, c->missing, fuse_shared && !sh_in_gu ? &sa : NULL, ysum,
@@ -1801,13 +1825,27 @@ static int chunk_experts(warp_hip_ctx *c, int layer, const float *X_dev, int T, 
         KRN(c, wk_apply_p6(c->jobs, c->njobs, c->max_jobs, 2, c->lut8d, c->lscaled, c->yd, H, I, c->st));
     } else {
         /* by runs: each expert's records decoded once per WARP_RUN_J jobs */
-        if (first) KRN(c, wk_split(X_dev, T, H, c->xs, c->xscale, c->st));
-        KRN(c, wk_vq_runs(g->fmt, c->jobs, c->njobs, c->max_jobs, c->runs, 0, 2, L->books, c->xs, c->xscale, yk, I,
-                          H, c->st));
-        KRN(c, wk_act_split(c->yg, c->yu, P, I, g->act_situ, g->situ_beta, g->situ_linear_beta, c->xsh, c->xscaleh,
-                            NULL, c->st));
-        KRN(c, wk_vq_runs(g->fmt, c->jobs, c->njobs, c->max_jobs, c->runs, 2, 1, L->books, c->xsh, c->xscaleh, yk, H,
-                          I, c->st));
+        if (g->prefill_fp16) {
+            /* reduced precision: inputs by pair slot, position-group-major
+             * (x replicated per pair once the first plan has placed them) */
+            if (first)
+                KRN(c, wk_split_pgm(X_dev, NULL, c->pair_tok, c->offsets + E, P, H, 0, 0, 0.0f, 0.0f, c->xsp,
+                                    c->xscalep, c->st));
+            KRN(c, wk_vq_runs(g->fmt, c->jobs, c->njobs, c->max_jobs, c->runs, 0, 2, L->books, c->xsp, c->xscalep,
+                              yk, I, H, P, c->st));
+            KRN(c, wk_split_pgm(c->yg, c->yu, NULL, c->offsets + E, P, I, 1, g->act_situ, g->situ_beta,
+                                g->situ_linear_beta, c->xsh, c->xscaleh, c->st));
+            KRN(c, wk_vq_runs(g->fmt, c->jobs, c->njobs, c->max_jobs, c->runs, 2, 1, L->books, c->xsh, c->xscaleh,
+                              yk, H, I, P, c->st));
+        } else {
+            if (first) KRN(c, wk_split(X_dev, T, H, c->xs, c->xscale, c->st));
+            KRN(c, wk_vq_runs(g->fmt, c->jobs, c->njobs, c->max_jobs, c->runs, 0, 2, L->books, c->xs, c->xscale, yk,
+                              I, H, 0, c->st));
+            KRN(c, wk_act_split(c->yg, c->yu, P, I, g->act_situ, g->situ_beta, g->situ_linear_beta, c->xsh,
+                                c->xscaleh, NULL, c->st));
+            KRN(c, wk_vq_runs(g->fmt, c->jobs, c->njobs, c->max_jobs, c->runs, 2, 1, L->books, c->xsh, c->xscaleh,
+                              yk, H, I, 0, c->st));
+        }
     }
     return 0;
 }
@@ -1833,6 +1871,14 @@ int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *ou
         Xe = c->xlat;
     }
 
+    /* the shared expert on its own stream, beside routing, grouping and the
+     * routed experts; the combine waits for it */
+    if (L->sq[0]) {
+        DEV(c, hipEventRecord(c->ev_sx0, c->st));
+        DEV(c, hipStreamWaitEvent(c->sx, c->ev_sx0, 0));
+        if ((rc = shared_ffn(c, L, X_dev, T, c->sx))) return rc;
+        DEV(c, hipEventRecord(c->ev_sx1, c->sx));
+    }
     KRN(c, logits_of(c, L, X_dev, T, c->logits, c->st));
     KRN(c, wk_route(c->logits, L->bias, E, K, T, g->router_act, g->renorm, g->routed_scale, c->idx, c->w, NULL, NULL,
                     NULL, NULL, 0, c->st));
@@ -1880,7 +1926,7 @@ int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *ou
         release_hold(c, layer);
         if ((rc = chunk_experts(c, layer, Xe, T, 0, E - 1, 1))) return rc;
     }
-    if (L->sq[0] && (rc = shared_ffn(c, L, X_dev, T))) return rc;
+    if (L->sq[0]) DEV(c, hipStreamWaitEvent(c->st, c->ev_sx1, 0));
     if (lat) {
         KRN(c, wk_combine_chunk(c->yd, c->tok_slots, c->pair_w, T, K, c->He, NULL, NULL, c->ylat, c->st));
         if ((rc = latent_tail(c, L, T, resid_dev, out_dev))) return rc;

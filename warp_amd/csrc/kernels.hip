@@ -158,15 +158,24 @@ __global__ __launch_bounds__(1024) void k_split(const float *__restrict__ x, int
 // position's hi and lo halves leave as one 16-byte store each. ACT: the row
 // is act(g, u) of two inputs (the SwiGLU of a batch), optionally also
 // written to h_out. Same values as the block-per-row kernels, bit for bit
-// (the same exponent from the same maximum).
-template <int NP, bool ACT>
+// (the same exponent from the same maximum). PGM: only the hi halves, in
+// the position-group-major order of the reduced-precision products (see
+// k_split_pgm), rows p < *nrows, x's row rowmap[p] when rowmap is given.
+struct PgmOut {
+    const int *rowmap, *nrows;
+    int R;
+};
+
+template <int NP, bool ACT, bool PGM>
 __global__ __launch_bounds__(256) void k_split_w(const float *__restrict__ g, const float *__restrict__ u, int P, int N,
                                                  int situ, float beta, float lbeta, half8 *__restrict__ xs,
-                                                 float *__restrict__ xscale, float *__restrict__ h_out) {
+                                                 float *__restrict__ xscale, float *__restrict__ h_out, PgmOut pm) {
     const int lane = threadIdx.x & 63, p = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     if (p >= P) return;                                    // uniform per wave
+    if (PGM && p >= *pm.nrows) return;                     // uniform per wave
     const int nv = N >> 3;
-    const float4 *gp = (const float4 *)(g + (size_t)p * N), *up = ACT ? (const float4 *)(u + (size_t)p * N) : nullptr;
+    const size_t src = PGM && pm.rowmap ? (size_t)pm.rowmap[p] : (size_t)p;
+    const float4 *gp = (const float4 *)(g + src * N), *up = ACT ? (const float4 *)(u + src * N) : nullptr;
     float4 gv[NP][2], uv[NP][2] = {};
 #pragma unroll
     for (int j = 0; j < NP; j++) {
@@ -205,8 +214,12 @@ __global__ __launch_bounds__(256) void k_split_w(const float *__restrict__ g, co
                 hi[e] = (_Float16)v;
                 lo[e] = (_Float16)(v - (float)hi[e]);
             }
-            o[2 * pos] = hi;
-            o[2 * pos + 1] = lo;
+            if constexpr (PGM) {
+                xs[((size_t)(pos >> 2) * pm.R + p) * 4 + (pos & 3)] = hi;
+            } else {
+                o[2 * pos] = hi;
+                o[2 * pos + 1] = lo;
+            }
             if (ACT && h_out) {
                 float4 *ho = (float4 *)(h_out + (size_t)p * N) + 2 * pos;
                 ho[0] = make_float4(h[j][0], h[j][1], h[j][2], h[j][3]);
@@ -217,16 +230,16 @@ __global__ __launch_bounds__(256) void k_split_w(const float *__restrict__ g, co
     if (lane == 0) xscale[p] = ldexpf(1.0f, -k);
 }
 
-template <bool ACT>
+template <bool ACT, bool PGM = false>
 static int launch_split_w(const float *g, const float *u, int P, int N, int situ, float beta, float lbeta,
-                          uint16_t *xs, float *xscale, float *h_out, void *stream) {
+                          uint16_t *xs, float *xscale, float *h_out, void *stream, PgmOut pm = PgmOut{}) {
     const int np = (N / 8 + 63) / 64;
     const int rpb = P >= 2048 ? 4 : 1;                    // rows per block: small batches spread over more CUs
     const dim3 grid((P + rpb - 1) / rpb);
 #define SPLIT_W(n)                                                                                                  \
     case n:                                                                                                         \
-        hipLaunchKernelGGL((k_split_w<n, ACT>), grid, dim3(64 * rpb), 0, (hipStream_t)stream, g, u, P, N, situ,    \
-                           beta, lbeta, (half8 *)xs, xscale, h_out);                                                \
+        hipLaunchKernelGGL((k_split_w<n, ACT, PGM>), grid, dim3(64 * rpb), 0, (hipStream_t)stream, g, u, P, N,     \
+                           situ, beta, lbeta, (half8 *)xs, xscale, h_out, pm);                                      \
         break;
     switch (np) {
         SPLIT_W(1)
@@ -240,6 +253,79 @@ static int launch_split_w(const float *g, const float *u, int P, int N, int situ
     default: return -1;
     }
 #undef SPLIT_W
+    CHECK_LAUNCH();
+    return 0;
+}
+
+// fp16 hi halves of rows in position-group-major order, the B operands of a
+// chunk's reduced-precision products: dims 32 pg .. 32 pg + 31 of row p at
+// xs[(pg * R + p) * 32 ..], so the consecutive pair slots of a run are side
+// by side in every position group. Each row is scaled by a power of two
+// (max |v| * 2^k in [2^14, 2^15), 2^-k to xscale[p]) as wk_split does. ACT:
+// row p is act(g, u) of pair row p; otherwise row rowmap[p] of x (a chunk's
+// pairs in slot order, x replicated per pair). Rows at or past *nrows are
+// not written. One 256-thread block per row: a pass for the max, a pass for
+// the stores (the row comes from L2 the second time).
+template <bool ACT>
+__global__ __launch_bounds__(256) void k_split_pgm(const float *__restrict__ g, const float *__restrict__ u,
+                                                   const int *__restrict__ rowmap, const int *__restrict__ nrows,
+                                                   int N, int R, int situ, float beta, float lbeta,
+                                                   half8 *__restrict__ xs, float *__restrict__ xscale) {
+    const int p = blockIdx.x;
+    if (p >= *nrows) return;                               // uniform per block
+    const size_t src = rowmap ? (size_t)rowmap[p] : (size_t)p;
+    const float4 *gr = (const float4 *)(g + src * N), *ur = ACT ? (const float4 *)(u + src * N) : nullptr;
+    const int nv = N >> 3;
+    auto row8 = [&](int v, float (&h)[8]) {
+        const float4 a0 = gr[2 * v], a1 = gr[2 * v + 1];
+        const float gx[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+        if constexpr (ACT) {
+            const float4 b0 = ur[2 * v], b1 = ur[2 * v + 1];
+            const float ux[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) h[e] = act_pair(gx[e], ux[e], situ, beta, lbeta);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++) h[e] = gx[e];
+        }
+    };
+    float m = 0.0f;
+    for (int v = threadIdx.x; v < nv; v += blockDim.x) {
+        float h[8];
+        row8(v, h);
+#pragma unroll
+        for (int e = 0; e < 8; e++) m = fmaxf(m, fabsf(h[e]));
+    }
+    const int k = split_exp(block_absmax(m));
+    for (int v = threadIdx.x; v < nv; v += blockDim.x) {
+        float h[8];
+        row8(v, h);
+        half8 hi;
+#pragma unroll
+        for (int e = 0; e < 8; e++) hi[e] = (_Float16)ldexpf(h[e], k);
+        xs[((size_t)(v >> 2) * R + p) * 4 + (v & 3)] = hi;
+    }
+    if (threadIdx.x == 0) xscale[p] = ldexpf(1.0f, -k);
+}
+
+extern "C" int wk_split_pgm(const float *g, const float *u, const int *rowmap, const int *nrows, int P, int N,
+                            int act, int act_situ, float beta, float lbeta, uint16_t *xs, float *xscale,
+                            void *stream) {
+    if (P <= 0 || N <= 0 || (N % 32) || !nrows || (act && !u) || (!act && u) ||
+        (((uintptr_t)g | (uintptr_t)u | (uintptr_t)xs) & 15))
+        return -1;
+    // rows of up to 4096 values one wave each, in registers; longer rows a block each
+    if (N <= 4096)
+        return act ? launch_split_w<true, true>(g, u, P, N, act_situ, beta, lbeta, xs, xscale, nullptr, stream,
+                                                PgmOut{nullptr, nrows, P})
+                   : launch_split_w<false, true>(g, nullptr, P, N, 0, 0.0f, 0.0f, xs, xscale, nullptr, stream,
+                                                 PgmOut{rowmap, nrows, P});
+    if (act)
+        hipLaunchKernelGGL(k_split_pgm<true>, dim3(P), dim3(256), 0, (hipStream_t)stream, g, u, rowmap, nrows, N, P,
+                           act_situ, beta, lbeta, (half8 *)xs, xscale);
+    else
+        hipLaunchKernelGGL(k_split_pgm<false>, dim3(P), dim3(256), 0, (hipStream_t)stream, g, u, rowmap, nrows, N, P,
+                           0, 0.0f, 0.0f, (half8 *)xs, xscale);
     CHECK_LAUNCH();
     return 0;
 }
@@ -1272,6 +1358,7 @@ struct VqArgs {
     const float *xscale;        // [nx]
     float *y[3];                // per kind: [ny][M]
     int M, N;
+    int xrows;                  // reduced-precision kernel: xs is [N/32][xrows][32] fp16
 };
 
 // waves per block (NW) and code words in flight per wave (D) are template
@@ -1614,12 +1701,142 @@ static int launch_vq_run(const VqArgs &a, const int *runs, int nkinds, int max_u
     return 0;
 }
 
+// A chunk's reduced-precision mode, by runs as above: the stages' codebook
+// vectors of a position are added into one fp16 A operand (v_pk_add_f16,
+// each addition rounded once) and B holds only the fp16 hi halves of x, 16
+// tokens (two jobs) per MFMA, so a position group takes a quarter of the
+// exact kernel's MFMAs: products of fp16 values accumulated in fp32. With
+// that few MFMAs the loop is bound by issue and latency, so a block holds
+// 16 waves (4 per SIMD, each within 128 VGPRs): the gathers are single-
+// buffered (the other waves cover their latency), and the code words and B
+// operands are both loaded WD groups ahead. Vector loads retire in issue
+// order, so B loaded nearer than the code words would hold the code words
+// to its own depth.
+template <int FMT, int WD>
+__global__ __launch_bounds__(1024) void k_vq_run_f16(VqArgs a, const int *__restrict__ runs) {
+    typedef FmtT<FMT> F;
+    constexpr int NWB = 16, RB = WARP_RUN_J / 2;            // waves per block; B operands (2 jobs each) per step
+    extern __shared__ __attribute__((aligned(16))) unsigned char lds_vq[];
+    const int kind = a.kind_lo + blockIdx.y;
+    const warp_job *jobs = a.jobs + (size_t)kind * a.max_jobs;
+    const int M = a.M, N = a.N, nv = N >> 3, npg = nv >> 2, nrb = (M + 63) >> 6;
+    const int units = a.njobs[3] * nrb;
+    if ((int)(blockIdx.x * NWB) >= units) return;   // uniform per block
+    {
+        const uint4 *src = (const uint4 *)(a.books + (size_t)kind * F::S * F::E * 8);
+        uint4 *dst = (uint4 *)lds_vq;
+        for (int i = threadIdx.x; i < F::S * F::E; i += blockDim.x) dst[i] = src[i];
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, jc = lane & 15;
+    for (int u = blockIdx.x * NWB + wave; u < units; u += gridDim.x * NWB) {
+        const int rv = __builtin_amdgcn_readfirstlane(runs[u / nrb]);   // uniform: u is
+        const int j0 = rv >> 3, nt = rv & 7, rb = u % nrb;
+        const uint8_t *cp = jobs[j0].idx + ((size_t)rb * nv) * 64 * F::SB + (size_t)lane * 4 * F::SB;
+        // B column jc: pair slot jc % 8 of job 2 q + jc / 8 (xs holds the
+        // inputs by pair slot, position-group-major, so a run's slots are
+        // contiguous); a column past the run's jobs or a job's tokens points
+        // at a slot of the run (the grouping fills every slot), so the loads
+        // are unconditional and the column is not written out
+        const size_t pgs = (size_t)a.xrows * 32;              // halves per position group
+        const _Float16 *xrow[RB];
+#pragma unroll
+        for (int q = 0; q < RB; q++)
+            xrow[q] = a.xs + (size_t)jobs[j0 + min(2 * q + (jc >> 3), nt - 1)].yi[jc & 7] * 32 + (size_t)g * 8;
+        f4 acc[RB][4];
+#pragma unroll
+        for (int q = 0; q < RB; q++)
+#pragma unroll
+            for (int t = 0; t < 4; t++) acc[q][t] = f4{0.f, 0.f, 0.f, 0.f};
+        Word<F::SB> buf[WD];
+        half8 bb[WD][RB];
+#pragma unroll
+        for (int k = 0; k < WD; k++) {
+            const size_t pk = (size_t)min(k, npg - 1);
+            buf[k].load_keep(cp + pk * 256 * F::SB);
+#pragma unroll
+            for (int q = 0; q < RB; q++) bb[k][q] = *(const half8 *)(xrow[q] + pk * pgs);
+        }
+        // one position group: its gathers, the code word WD groups ahead,
+        // the stage sums and MFMAs, then B WD groups ahead into the slot the
+        // MFMAs have read
+        auto step = [&](int k, int pg) {
+            half8 av[4][F::S];
+            gather_group<FMT, F::SB>(lds_vq, buf[k], av);
+            const size_t pn = (size_t)min(pg + WD, npg - 1);
+            buf[k].load_keep(cp + pn * 256 * F::SB);
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int s = 1; s < F::S; s++) av[t][0] = av[t][0] + av[t][s];
+#pragma unroll
+            for (int q = 0; q < RB; q++)
+                if (2 * q < nt)                               // uniform
+#pragma unroll
+                    for (int t = 0; t < 4; t++)
+                        acc[q][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[t][0], bb[k][q], acc[q][t], 0, 0, 0);
+#pragma unroll
+            for (int q = 0; q < RB; q++) bb[k][q] = *(const half8 *)(xrow[q] + pn * pgs);
+        };
+        const int npg_full = npg - npg % WD;
+        for (int pgb = 0; pgb < npg_full; pgb += WD) {
+#pragma unroll
+            for (int k = 0; k < WD; k++) step(k, pgb + k);
+        }
+#pragma unroll
+        for (int k = 0; k < WD; k++)
+            if (npg_full + k < npg) step(k, npg_full + k);    // uniform
+        // lane (g, jc) holds C[4g + r][jc] of row tile t: block row
+        // 16g + 4r + t, token jc % 8 of job 2 q + jc / 8
+#pragma unroll
+        for (int q = 0; q < RB; q++) {
+            if (2 * q >= nt) break;                           // uniform
+            const int jq_i = 2 * q + (jc >> 3), tk = jc & 7;
+            const warp_job &jq = jobs[j0 + min(jq_i, nt - 1)];
+            const bool tv = jq_i < nt && tk < jq.n;
+            const int yrow = tv ? jq.yi[tk] : 0;
+            const float xsc = tv ? a.xscale[yrow] : 0.0f;
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int row = rb * 64 + 16 * g + 4 * r + t;
+                    if (tv && row < M) a.y[kind][(size_t)yrow * M + row] = (acc[q][t][r] * xsc) * f16_keep(jq.scale[row]);
+                }
+        }
+    }
+}
+
+template <int FMT>
+static int launch_vq_run_f16(const VqArgs &a, const int *runs, int nkinds, int max_units, void *stream) {
+    typedef FmtT<FMT> F;
+    constexpr int WD = F::S == 3 ? 2 : 3;                   // code words and B operands in flight
+    const size_t lds = (size_t)F::S * F::E * 16;
+    static bool attr = false;
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute((const void *)k_vq_run_f16<FMT, WD>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return -(int)e - 1000;
+        attr = true;
+    }
+    int grid = (max_units + 15) / 16;
+    const int cap = FMT == WARP_FMT_VQ12 ? 256 : 512;
+    if (grid > cap) grid = cap;
+    if (grid < 1) grid = 1;
+    hipLaunchKernelGGL((k_vq_run_f16<FMT, WD>), dim3(grid, nkinds), dim3(1024), lds, (hipStream_t)stream, a, runs);
+    CHECK_LAUNCH();
+    return 0;
+}
+
 extern "C" int wk_vq_runs(int fmt, const warp_job *jobs, const int *njobs, int max_jobs, const int *runs,
                           int kind_lo, int nkinds, const uint16_t *books, const uint16_t *xs, const float *xscale,
-                          float *const *y, int M, int N, void *stream) {
-    if (M <= 0 || N <= 0 || (N % 32) || max_jobs <= 0 || !runs || kind_lo < 0 || nkinds < 1 || kind_lo + nkinds > 3)
+                          float *const *y, int M, int N, int fp16_rows, void *stream) {
+    if (M <= 0 || N <= 0 || (N % 32) || max_jobs <= 0 || !runs || kind_lo < 0 || nkinds < 1 || kind_lo + nkinds > 3 ||
+        fp16_rows < 0)
         return -1;
-    VqArgs a;
+    const int fp16 = fp16_rows > 0;
+    VqArgs a{};
     a.jobs = jobs;
     a.njobs = njobs;
     a.max_jobs = max_jobs;
@@ -1630,11 +1847,16 @@ extern "C" int wk_vq_runs(int fmt, const warp_job *jobs, const int *njobs, int m
     for (int k = 0; k < 3; k++) a.y[k] = y[k];
     a.M = M;
     a.N = N;
+    a.xrows = fp16_rows;
     const int max_units = max_jobs * ((M + 63) / 64);
     switch (fmt) {
-    case WARP_FMT_VQ3R: return launch_vq_run<WARP_FMT_VQ3R>(a, runs, nkinds, max_units, stream);
-    case WARP_FMT_VQ2R: return launch_vq_run<WARP_FMT_VQ2R>(a, runs, nkinds, max_units, stream);
-    case WARP_FMT_VQ12: return launch_vq_run<WARP_FMT_VQ12>(a, runs, nkinds, max_units, stream);
+#define VR(F)                                                                                                      \
+    return fp16 ? launch_vq_run_f16<F>(a, runs, nkinds, max_units, stream)                                         \
+                : launch_vq_run<F>(a, runs, nkinds, max_units, stream)
+    case WARP_FMT_VQ3R: VR(WARP_FMT_VQ3R);
+    case WARP_FMT_VQ2R: VR(WARP_FMT_VQ2R);
+    case WARP_FMT_VQ12: VR(WARP_FMT_VQ12);
+#undef VR
     }
     return -1;
 }
@@ -1645,7 +1867,7 @@ extern "C" int wk_vq_matvec(int fmt, const warp_job *jobs, const int *njobs, int
     if (M <= 0 || N <= 0 || (N % 32) || max_jobs <= 0 || kind_lo < 0 || nkinds < 1 || kind_lo + nkinds > 3)
         return -1;
     if (tokens_per_job != 1 && tokens_per_job != WARP_TPJ) return -1;
-    VqArgs a;
+    VqArgs a{};
     a.jobs = jobs;
     a.njobs = njobs;
     a.max_jobs = max_jobs;
@@ -3268,16 +3490,19 @@ __global__ __launch_bounds__(1024) void k_plan_chunk(const int *__restrict__ idx
                                                      int *__restrict__ njobs, int *__restrict__ runs,
                                                      int *__restrict__ missing, int inter, int bitmaps,
                                                      int e_lo, int e_hi, int or_missing) {
-    extern __shared__ int lds_plan[];
-    const int P = T * K, NW = (T + 31) >> 5;
-    int *pid = lds_plan;                            // [P]
+    extern __shared__ __attribute__((aligned(16))) int lds_plan[];
+    // token bitmap rows of NWP words: an odd stride, so the rows that a
+    // wave's pairs read in one step fall on different LDS banks
+    const int P = T * K, NWP = ((T + 31) >> 5) | 1;
+    warp_slot *stab = (warp_slot *)lds_plan;        // [E] the expert table, read once
+    int *pid = (int *)(stab + E);                   // [P]
     int *cnt = pid + P;                             // [E]
     int *off = cnt + E;                             // [E]
     int *tile0 = off + E;                           // [E]
     int *run0 = tile0 + E;                          // [E] place of the expert's first full run
     int *runr = run0 + E;                           // [E] place of its last, partial run
-    unsigned *bm = (unsigned *)(runr + E);          // [E][NW] when bitmaps
-    int *ptok = (int *)(bm + (bitmaps ? E * NW : 0));                     // [P] pair_tok, kept on chip
+    unsigned *bm = (unsigned *)(runr + E);          // [E][NWP] when bitmaps
+    int *ptok = (int *)(bm + (bitmaps ? E * NWP : 0));                    // [P] pair_tok, kept on chip
     unsigned char *pv = (unsigned char *)(ptok + P);                     // [P] pair computed
     // Up to PPT pairs per thread: their picks and weights loaded at once
     // (clamped, so no load waits on another) and the weights kept in
@@ -3299,9 +3524,12 @@ __global__ __launch_bounds__(1024) void k_plan_chunk(const int *__restrict__ idx
     } else {
         for (int q = threadIdx.x; q < P; q += blockDim.x) pid[q] = idx[q];
     }
-    for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[e] = 0;
+    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+        stab[e] = table[e];
+        cnt[e] = 0;
+    }
     if (bitmaps)
-        for (int i = threadIdx.x; i < E * NW; i += blockDim.x) bm[i] = 0u;
+        for (int i = threadIdx.x; i < E * NWP; i += blockDim.x) bm[i] = 0u;
     __syncthreads();
     // each pair's test once (no earlier pick of the token has its expert,
     // and its weight is not 0), kept in LDS for the loops below
@@ -3312,7 +3540,7 @@ __global__ __launch_bounds__(1024) void k_plan_chunk(const int *__restrict__ idx
         pv[q] = v;
         if (v) {
             atomicAdd(&cnt[e], 1);
-            if (bitmaps) atomicOr(&bm[e * NW + (t >> 5)], 1u << (t & 31));
+            if (bitmaps) atomicOr(&bm[e * NWP + (t >> 5)], 1u << (t & 31));
         }
     };
     if (regs) {
@@ -3365,7 +3593,7 @@ __global__ __launch_bounds__(1024) void k_plan_chunk(const int *__restrict__ idx
             tile0[e] = pt;
             run0[e] = pf;
             runr[e] = r ? pr : -1;            // rank among the partial runs of its size, placed below
-            if (cw && !table[e].rec) miss_s = 1;
+            if (cw && !stab[e].rec) miss_s = 1;
         }
         carry[0] += tc;
     }
@@ -3410,7 +3638,7 @@ __global__ __launch_bounds__(1024) void k_plan_chunk(const int *__restrict__ idx
         }
         int pos = off[e];
         if (bitmaps) {
-            const unsigned *row = bm + e * NW;
+            const unsigned *row = bm + e * NWP;
             for (int i = 0; i < (t >> 5); i++) pos += __popc(row[i]);
             pos += __popc(row[t >> 5] & ((1u << (t & 31)) - 1u));
         } else {
@@ -3453,9 +3681,8 @@ __global__ __launch_bounds__(1024) void k_plan_chunk(const int *__restrict__ idx
         const int e = lo, i = j - tile0[e], c = cnt[e];
         const int base = off[e] + i * WARP_TPJ, n = min(WARP_TPJ, c - i * WARP_TPJ);
         // the record and the job's tokens, each read once, all loads in flight
-        const uint8_t *rec = table[e].rec;
-        const uint2 o01 = *(const uint2 *)&table[e].off[0], o23 = *(const uint2 *)&table[e].off[2];
-        const uint4 offs = make_uint4(o01.x, o01.y, o23.x, o23.y);
+        const uint8_t *rec = stab[e].rec;
+        const uint4 offs = make_uint4(stab[e].off[0], stab[e].off[1], stab[e].off[2], stab[e].off[3]);
         int tk[WARP_TPJ];
 #pragma unroll
         for (int s = 0; s < WARP_TPJ; s++) tk[s] = ptok[base + (s < n ? s : 0)];
@@ -3484,8 +3711,9 @@ extern "C" int wk_plan_chunk(const int *idx, const float *w, int T, int K, int E
     if (T <= 0 || K <= 0 || E <= 0 || max_jobs <= 0 || !runs || e_lo < 0 || e_hi >= E || e_lo > e_hi) return -1;
     // the picks, the per-expert tables, each pair's token and a flag per pair
     // in LDS; the token bitmaps too when they fit
-    const size_t base = ((size_t)2 * T * K + 5 * (size_t)E) * sizeof(int) + (size_t)T * K;
-    const size_t bms = (size_t)E * ((T + 31) / 32) * sizeof(unsigned);
+    const size_t base = (size_t)E * sizeof(warp_slot) + ((size_t)2 * T * K + 5 * (size_t)E) * sizeof(int) +
+                        (size_t)T * K;
+    const size_t bms = (size_t)E * (((T + 31) / 32) | 1) * sizeof(unsigned);
     // dynamic LDS up to 152 KiB: the kernel's static shared memory takes the rest of the 160
     constexpr size_t LDS_MAX = 152 * 1024;
     if (base > LDS_MAX) return -1;

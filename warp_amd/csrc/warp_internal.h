@@ -154,10 +154,21 @@ int wk_vq_matvec(int fmt, const warp_job *jobs, const int *njobs, int max_jobs,
                  void *stream);
 /* The same for prefill by runs: runs[0..njobs[3]) = (first job << 3) | jobs,
  * up to WARP_RUN_J consecutive jobs of one expert (wk_plan_chunk writes
- * them); each run's records are decoded once for all its jobs. */
+ * them); each run's records are decoded once for all its jobs.
+ * fp16_rows = 0: exact products, xs/xscale as for wk_vq_matvec (rows by
+ * xi). fp16_rows > 0: the reduced-precision products (stage vectors added
+ * in fp16, x's fp16 high half), xs [N/32][fp16_rows][32] and xscale
+ * [fp16_rows] by pair slot (yi), from wk_split_pgm. */
 int wk_vq_runs(int fmt, const warp_job *jobs, const int *njobs, int max_jobs, const int *runs,
                int kind_lo, int nkinds, const uint16_t *books, const uint16_t *xs, const float *xscale,
-               float *const *y, int M, int N, void *stream);
+               float *const *y, int M, int N, int fp16_rows, void *stream);
+/* Inputs of the reduced-precision products: rows p < *nrows of
+ * act(g, u) (act = 1, pair rows) or of x row rowmap[p] (act = 0, u NULL),
+ * each scaled by a power of two (2^-k to xscale[p]) and rounded to fp16,
+ * into xs [N/32][P][32]. N % 32 == 0, pointers 16-byte aligned. */
+int wk_split_pgm(const float *g, const float *u, const int *rowmap, const int *nrows, int P, int N,
+                 int act, int act_situ, float beta, float lbeta, uint16_t *xs, float *xscale,
+                 void *stream);
 
 /* The LUT matvec (decode, one input per job): for each kind
  * kind_lo..kind_lo+nkinds-1, every job's rows against the f32 input

@@ -39,7 +39,7 @@ class Cfg(C.Structure):
         ("situ_beta", C.c_float), ("situ_linear_beta", C.c_float), ("max_tokens", C.c_int),
         ("rec_bytes", C.c_size_t), ("cache_bytes", C.c_size_t), ("verify", C.c_int),
         ("lookahead", C.c_int), ("device", C.c_int), ("latent", C.c_int), ("latent_norm", C.c_int),
-        ("norm_eps", C.c_float),
+        ("norm_eps", C.c_float), ("prefill_fp16", C.c_int),
     ]
 
 
@@ -148,11 +148,12 @@ class Context:
     def __init__(self, *, hidden, inter, n_experts, top_k, n_layers, fmt, renorm=True,
                  routed_scale=1.0, router_act=ROUTE_SIGMOID, router_strict=False, act_situ=False,
                  situ_beta=1.0, situ_linear_beta=0.0, max_tokens=1, rec_bytes, cache_bytes,
-                 verify=False, lookahead=0, device=0, latent=0, latent_norm=True, norm_eps=1e-5):
+                 verify=False, lookahead=0, device=0, latent=0, latent_norm=True, norm_eps=1e-5,
+                 prefill_fp16=False):
         self.cfg = Cfg(hidden, inter, n_experts, top_k, n_layers, FMT.get(fmt, fmt), int(renorm),
                        routed_scale, router_act, int(router_strict), int(act_situ), situ_beta,
                        situ_linear_beta, max_tokens, rec_bytes, cache_bytes, int(verify), lookahead, device,
-                       latent, int(latent_norm), norm_eps)
+                       latent, int(latent_norm), norm_eps, int(prefill_fp16))
         self.h = C.c_void_p()
         self._keep = []
         rc = lib().warp_hip_open(C.byref(self.cfg), C.byref(self.h))
