@@ -1712,11 +1712,25 @@ static int launch_vq_run(const VqArgs &a, const int *runs, int nkinds, int max_u
 // operands are both loaded WD groups ahead. Vector loads retire in issue
 // order, so B loaded nearer than the code words would hold the code words
 // to its own depth.
+// Buffer descriptor word 3 for gfx9 raw buffers (32-bit data format, no
+// swizzle); records up to 4 GiB.
+constexpr int BUF_RSRC_W3 = 0x00020000;
+
+template <int SB> __device__ __forceinline__ void word_load(Word<SB> &w, __amdgpu_buffer_rsrc_t r, unsigned vo, int so);
+template <> __device__ __forceinline__ void word_load<3>(Word<3> &w, __amdgpu_buffer_rsrc_t r, unsigned vo, int so) {
+    w.w = __builtin_bit_cast(u3v, __builtin_amdgcn_raw_buffer_load_b96(r, vo, so, 0));
+}
+template <> __device__ __forceinline__ void word_load<2>(Word<2> &w, __amdgpu_buffer_rsrc_t r, unsigned vo, int so) {
+    w.w = __builtin_bit_cast(u2v, __builtin_amdgcn_raw_buffer_load_b64(r, vo, so, 0));
+}
+
 template <int FMT, int WD>
 __global__ __launch_bounds__(1024) void k_vq_run_f16(VqArgs a, const int *__restrict__ runs) {
     typedef FmtT<FMT> F;
     constexpr int NWB = 16, RB = WARP_RUN_J / 2;            // waves per block; B operands (2 jobs each) per step
-    extern __shared__ __attribute__((aligned(16))) unsigned char lds_vq[];
+    // the codebook at a fixed LDS address, so the gathers' addresses need no base
+    __shared__ uint4 cb_lds[F::S * F::E];
+    const unsigned char *lds_vq = (const unsigned char *)cb_lds;
     const int kind = a.kind_lo + blockIdx.y;
     const warp_job *jobs = a.jobs + (size_t)kind * a.max_jobs;
     const int M = a.M, N = a.N, nv = N >> 3, npg = nv >> 2, nrb = (M + 63) >> 6;
@@ -1724,26 +1738,35 @@ __global__ __launch_bounds__(1024) void k_vq_run_f16(VqArgs a, const int *__rest
     if ((int)(blockIdx.x * NWB) >= units) return;   // uniform per block
     {
         const uint4 *src = (const uint4 *)(a.books + (size_t)kind * F::S * F::E * 8);
-        uint4 *dst = (uint4 *)lds_vq;
-        for (int i = threadIdx.x; i < F::S * F::E; i += blockDim.x) dst[i] = src[i];
+        for (int i = threadIdx.x; i < F::S * F::E; i += blockDim.x) cb_lds[i] = src[i];
     }
     __syncthreads();
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, jc = lane & 15;
+    // B and the code words through buffer loads: a per-lane offset fixed for
+    // the unit and a per-group offset in a scalar register
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void *)a.xs, 0, -1, BUF_RSRC_W3);
+    const int pgb_x = a.xrows * 64;                          // bytes per position group of xs
     for (int u = blockIdx.x * NWB + wave; u < units; u += gridDim.x * NWB) {
         const int rv = __builtin_amdgcn_readfirstlane(runs[u / nrb]);   // uniform: u is
         const int j0 = rv >> 3, nt = rv & 7, rb = u % nrb;
-        const uint8_t *cp = jobs[j0].idx + ((size_t)rb * nv) * 64 * F::SB + (size_t)lane * 4 * F::SB;
+        // the unit's code words (uniform: the descriptor lives in scalar registers)
+        const uint64_t cba = (uint64_t)(uintptr_t)(jobs[j0].idx + ((size_t)rb * nv) * 64 * F::SB);
+        // (readfirstlane returns int: each half goes through unsigned, so the
+        // low half is not sign-extended into the high one)
+        const uint64_t cbu = ((uint64_t)(unsigned)__builtin_amdgcn_readfirstlane((unsigned)(cba >> 32)) << 32) |
+                             (uint64_t)(unsigned)__builtin_amdgcn_readfirstlane((unsigned)cba);
+        const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc((void *)(uintptr_t)cbu, 0, -1, BUF_RSRC_W3);
+        const unsigned co = (unsigned)lane * 4 * F::SB;
         // B column jc: pair slot jc % 8 of job 2 q + jc / 8 (xs holds the
         // inputs by pair slot, position-group-major, so a run's slots are
         // contiguous); a column past the run's jobs or a job's tokens points
         // at a slot of the run (the grouping fills every slot), so the loads
         // are unconditional and the column is not written out
-        const size_t pgs = (size_t)a.xrows * 32;              // halves per position group
-        const _Float16 *xrow[RB];
+        unsigned xo[RB];
 #pragma unroll
         for (int q = 0; q < RB; q++)
-            xrow[q] = a.xs + (size_t)jobs[j0 + min(2 * q + (jc >> 3), nt - 1)].yi[jc & 7] * 32 + (size_t)g * 8;
+            xo[q] = (unsigned)jobs[j0 + min(2 * q + (jc >> 3), nt - 1)].yi[jc & 7] * 64 + (unsigned)g * 16;
         f4 acc[RB][4];
 #pragma unroll
         for (int q = 0; q < RB; q++)
@@ -1753,10 +1776,11 @@ __global__ __launch_bounds__(1024) void k_vq_run_f16(VqArgs a, const int *__rest
         half8 bb[WD][RB];
 #pragma unroll
         for (int k = 0; k < WD; k++) {
-            const size_t pk = (size_t)min(k, npg - 1);
-            buf[k].load_keep(cp + pk * 256 * F::SB);
+            const int pk = min(k, npg - 1);
+            word_load<F::SB>(buf[k], cr, co, pk * 256 * F::SB);
 #pragma unroll
-            for (int q = 0; q < RB; q++) bb[k][q] = *(const half8 *)(xrow[q] + pk * pgs);
+            for (int q = 0; q < RB; q++)
+                bb[k][q] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(xr, xo[q], pk * pgb_x, 0));
         }
         // one position group: its gathers, the code word WD groups ahead,
         // the stage sums and MFMAs, then B WD groups ahead into the slot the
@@ -1764,8 +1788,8 @@ __global__ __launch_bounds__(1024) void k_vq_run_f16(VqArgs a, const int *__rest
         auto step = [&](int k, int pg) {
             half8 av[4][F::S];
             gather_group<FMT, F::SB>(lds_vq, buf[k], av);
-            const size_t pn = (size_t)min(pg + WD, npg - 1);
-            buf[k].load_keep(cp + pn * 256 * F::SB);
+            const int pn = min(pg + WD, npg - 1);
+            word_load<F::SB>(buf[k], cr, co, pn * 256 * F::SB);
 #pragma unroll
             for (int t = 0; t < 4; t++)
 #pragma unroll
@@ -1777,7 +1801,8 @@ __global__ __launch_bounds__(1024) void k_vq_run_f16(VqArgs a, const int *__rest
                     for (int t = 0; t < 4; t++)
                         acc[q][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[t][0], bb[k][q], acc[q][t], 0, 0, 0);
 #pragma unroll
-            for (int q = 0; q < RB; q++) bb[k][q] = *(const half8 *)(xrow[q] + pn * pgs);
+            for (int q = 0; q < RB; q++)
+                bb[k][q] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(xr, xo[q], pn * pgb_x, 0));
         };
         const int npg_full = npg - npg % WD;
         for (int pgb = 0; pgb < npg_full; pgb += WD) {
@@ -1812,19 +1837,11 @@ template <int FMT>
 static int launch_vq_run_f16(const VqArgs &a, const int *runs, int nkinds, int max_units, void *stream) {
     typedef FmtT<FMT> F;
     constexpr int WD = F::S == 3 ? 2 : 3;                   // code words and B operands in flight
-    const size_t lds = (size_t)F::S * F::E * 16;
-    static bool attr = false;
-    if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_vq_run_f16<FMT, WD>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return -(int)e - 1000;
-        attr = true;
-    }
     int grid = (max_units + 15) / 16;
     const int cap = FMT == WARP_FMT_VQ12 ? 256 : 512;
     if (grid > cap) grid = cap;
     if (grid < 1) grid = 1;
-    hipLaunchKernelGGL((k_vq_run_f16<FMT, WD>), dim3(grid, nkinds), dim3(1024), lds, (hipStream_t)stream, a, runs);
+    hipLaunchKernelGGL((k_vq_run_f16<FMT, WD>), dim3(grid, nkinds), dim3(1024), 0, (hipStream_t)stream, a, runs);
     CHECK_LAUNCH();
     return 0;
 }
@@ -1833,7 +1850,7 @@ extern "C" int wk_vq_runs(int fmt, const warp_job *jobs, const int *njobs, int m
                           int kind_lo, int nkinds, const uint16_t *books, const uint16_t *xs, const float *xscale,
                           float *const *y, int M, int N, int fp16_rows, void *stream) {
     if (M <= 0 || N <= 0 || (N % 32) || max_jobs <= 0 || !runs || kind_lo < 0 || nkinds < 1 || kind_lo + nkinds > 3 ||
-        fp16_rows < 0)
+        fp16_rows < 0 || (size_t)fp16_rows * N * 2 >= ((size_t)1 << 31))
         return -1;
     const int fp16 = fp16_rows > 0;
     VqArgs a{};
