@@ -1110,10 +1110,11 @@ def main():
     ap.add_argument("--matvec-path", choices=["auto", "mfma", "fused"], default="auto",
                     help="expert matvec kernel: auto = the LUT kernel, mfma = decode-then-dot on the matrix cores, "
                          "fused = the LUT kernel's gate/up, down and combine in one launch per layer")
-    ap.add_argument("--prefill", choices=["exact", "fp16"], default="exact",
-                    help="kimi-prefill: the expert products' precision: exact (fp16 hi/lo halves of x, every stage "
-                         "a product of its own) or fp16 (stages added into one fp16 operand, x's high half only: a "
-                         "quarter of the matrix-core work, outputs within 2e-3)")
+    ap.add_argument("--prefill", choices=["exact", "fp16"], default="fp16",
+                    help="kimi-prefill: the expert products' precision: fp16 (the configuration's decode-to-16-bit + "
+                         "MFMA design: stages added into one fp16 operand against x's fp16 high half, outputs within "
+                         "2e-3) or exact (fp16 hi/lo halves of x, every stage a product of its own, within 1e-4); "
+                         "the default run also times the exact mode in a child of its own")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="before timing, one device-to-device copy of this many MiB (a known-size "
                          "kernel for scaling the profiler's traffic counters)")
@@ -1210,17 +1211,22 @@ def main():
     print(json.dumps(rec))
 
 
-CHILDREN = [("single_expert", "single-expert"), ("kimi_decode", "kimi-decode"), ("kimi_prefill", "kimi-prefill"),
-            ("k3_miss", "k3-miss")]
+# (key, workload, extra arguments): the prefill twice, in the precision
+# mode asked for and in the exact mode (its CPU baseline is the same)
+CHILDREN = [("single_expert", "single-expert", []), ("kimi_decode", "kimi-decode", []),
+            ("kimi_prefill", "kimi-prefill", []), ("kimi_prefill_exact", "kimi-prefill", ["--prefill", "exact", "--no-cpu"]),
+            ("k3_miss", "k3-miss", [])]
 
 
 def run_children(args):
-    """The other four configurations, each `bench.py --workload X` in a child
+    """The other configurations (the prefill in both precision modes), each `bench.py --workload X` in a child
     process (its own HIP context and memory), with this run's step counts
     and CPU-baseline seconds; a child that fails is reported, not fatal."""
     import subprocess
     out = {}
-    for key, wl in CHILDREN:
+    for key, wl, extra in CHILDREN:
+        if key == "kimi_prefill_exact" and args.prefill == "exact":
+            continue
         cmd = [sys.executable, os.path.abspath(__file__), "--workload", wl, "--twin-dir", args.twin_dir,
                "--cpu-seconds", str(args.cpu_seconds), "--matvec-path", args.matvec_path,
                "--prefill", args.prefill]
@@ -1232,7 +1238,8 @@ def run_children(args):
             cmd.append("--no-cpu")
         if not args.graph:
             cmd.append("--no-graph")
-        log(f"bench: configuration {wl} in a child process")
+        cmd += extra
+        log(f"bench: configuration {key} in a child process")
         t0 = time.perf_counter()
         try:
             r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=None, text=True, timeout=args.child_timeout)
@@ -1244,7 +1251,7 @@ def run_children(args):
                 out[key] = {"error": f"exit status {r.returncode}", "stdout_tail": r.stdout[-400:]}
         except subprocess.TimeoutExpired:
             out[key] = {"error": f"did not finish in {args.child_timeout:.0f}s"}
-        log(f"bench: configuration {wl}: " + ("ok" if "error" not in out[key] else out[key]["error"]))
+        log(f"bench: configuration {key}: " + ("ok" if "error" not in out[key] else out[key]["error"]))
     return out
 
 

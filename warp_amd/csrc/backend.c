@@ -1555,6 +1555,24 @@ static int latent_tail(warp_hip_ctx *c, const layer_t *L, int T, const float *re
     return 0;
 }
 
+/* Codebook values with exponent 31 are finite in the reference (its fp16
+ * conversion rebiases every exponent, src/simd.h:49-67) but inf/NaN as the
+ * fp16 operands of the matrix-core kernels: such a layer's expert matvecs
+ * take the table kernel (its exact conversion) on every path. */
+static int use_table(const warp_hip_ctx *c, const layer_t *L)
+{
+    return c->lut_ok && L->books && (c->mv_path != WARP_HIP_PATH_MFMA || L->books_x31);
+}
+
+/* E_ARG where such a layer's shapes rule the table kernel out. */
+static int x31_check(warp_hip_ctx *c, const layer_t *L, int layer)
+{
+    if (L->books_x31 && !c->P6 && !c->lut_ok)
+        return set_err(c, WARP_HIP_E_ARG, layer, -1,
+                       "codebooks with exponent-31 values need the table kernel (widths multiples of 16)");
+    return 0;
+}
+
 int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *out_dev, const float *resid_dev,
                         int *idx, float *w)
 {
@@ -1566,7 +1584,8 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
     if (!L->has_books || (!L->router && !L->rq))
         return set_err(c, WARP_HIP_E_ARG, layer, -1, "layer %d has no codebooks or router", layer);
     const warp_slot *table = c->table_dev + (size_t)layer * E;
-    const int use_lut = c->lut_ok && c->mv_path != WARP_HIP_PATH_MFMA && L->books;
+    if ((rc = x31_check(c, L, layer))) return rc;
+    const int use_lut = use_table(c, L);
     /* the latent MoE: the experts see xe = down . x and return into the
      * latent width He; routing and the shared expert stay on x */
     const int lat = g->latent > 0, He = c->He;
@@ -1746,7 +1765,8 @@ int warp_hip_expert_ffn(warp_hip_ctx *c, int layer, int expert, const float *x_d
     KRN(c, wk_expert_jobs(c->table_dev + (size_t)layer * g->n_experts + expert, I, c->jobs, c->njobs, c->w,
                           c->missing, c->st));
     c->missing_pending = 1;
-    if (c->lut_ok && c->mv_path != WARP_HIP_PATH_MFMA) {
+    if ((rc = x31_check(c, L, layer))) return rc;
+    if (use_table(c, L)) {
         int sp_gu = 0, sp_d = 0;
         if ((rc = timing_begin(c, 0))) return rc;
         KRN(c, wk_vq_lut(g->fmt, c->jobs, c->njobs, 1, 0, 2, L->books, L->books_x31, x_dev, 1, c->part, c->part_cap,
@@ -1864,6 +1884,20 @@ int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *ou
     const int P = T * K;
     const int lat = g->latent > 0;
     if (lat && !L->lq[0]) return set_err(c, WARP_HIP_E_ARG, layer, -1, "layer %d has no latent projections", layer);
+    if (L->books_x31 && !c->P6) {
+        /* the chunk's matrix-core kernels cannot take exponent-31 codebook
+         * values: the tokens go one at a time through the table kernel,
+         * each with the chunk's routing (the same rule per token) */
+        if ((rc = x31_check(c, L, layer))) return rc;
+        for (int t = 0; t < T; t++) {
+            rc = warp_hip_moe_decode(c, layer, X_dev + (size_t)t * H, out_dev + (size_t)t * H,
+                                     resid_dev ? resid_dev + (size_t)t * H : NULL, route ? route + (size_t)t * K : NULL,
+                                     rw ? rw + (size_t)t * K : NULL);
+            if (rc) return rc;
+        }
+        DEV(c, hipStreamSynchronize(c->st));
+        return take_missing(c);
+    }
     /* the experts' inputs: x itself, or its latent projection */
     const float *Xe = X_dev;
     if (lat) {
@@ -2004,7 +2038,7 @@ int warp_hip_vq_matvec(warp_hip_ctx *c, int layer, int kind, const uint8_t *rec_
         float *ls = kind == 2 ? c->lscaled : c->lscale;
         KRN(c, wk_lut_p6(x_dev, 1, N, books_kind(c, L, kind), lut, ls, c->st));
         KRN(c, wk_apply_p6(c->jobs, c->njobs, 1, kind, lut, ls, y_dev, M, N, c->st));
-    } else if (c->lut_ok && c->mv_path != WARP_HIP_PATH_MFMA && L->books) {
+    } else if (use_table(c, L)) {
         float *yk[3] = { y_dev, y_dev, y_dev };
         int sp = 0;
         KRN(c, wk_vq_lut(c->cfg.fmt, c->jobs, c->njobs, 1, kind, 1, L->books, L->books_x31, x_dev, 1, c->part, c->part_cap, M, N,
