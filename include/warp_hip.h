@@ -149,9 +149,12 @@ typedef struct {
                             * matrix-core products in fp16 -- the stages'
                             * codebook vectors added into one fp16 value, x's
                             * fp16 high half only -- a quarter of the MFMAs,
-                            * outputs within about 1e-3 of the reference
-                            * instead of 1e-4 (the reference CPU path has no
-                            * such mode; 0 keeps the exact products)          */
+                            * outputs within 2e-3 of the reference instead of
+                            * 1e-4 (the reference CPU path has no such mode;
+                            * 0 keeps the exact products). Needs max_tokens x
+                            * top_k x max(hidden, inter) x 2 bytes under 2 GiB
+                            * (else chunks stay exact) and allocates that much
+                            * at open; VQ4P chunks stay on their int8 tables */
 } warp_hip_cfg;
 
 typedef struct warp_hip_ctx warp_hip_ctx;

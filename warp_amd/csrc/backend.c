@@ -429,6 +429,16 @@ static int dmalloc(warp_hip_ctx *c, void **p, size_t bytes)
 
 #define DMALLOC(c, p, bytes) do { if (dmalloc((c), (void **)&(p), (bytes))) return WARP_HIP_E_NOMEM; } while (0)
 
+/* A chunk's reduced-precision mode, while its inputs by pair slot stay
+ * under 2 GiB (32-bit buffer offsets); past that, chunks keep the exact
+ * by-token kernel. */
+static int prefill_fp16(const warp_hip_ctx *c)
+{
+    const size_t w = (size_t)(c->He > c->cfg.inter ? c->He : c->cfg.inter);
+    return c->cfg.prefill_fp16 && !c->P6 &&
+           (size_t)c->cfg.max_tokens * c->cfg.top_k * w * 2 < ((size_t)1 << 31);
+}
+
 static int ctx_alloc(warp_hip_ctx *c)
 {
     const warp_hip_cfg *g = &c->cfg;
@@ -455,7 +465,7 @@ static int ctx_alloc(warp_hip_ctx *c)
     DMALLOC(c, c->xsh, P * I * 2 * 2);
     DMALLOC(c, c->xscaleh, P * 4);
     DMALLOC(c, c->hbuf, P * I * 4);
-    if (g->prefill_fp16) {
+    if (prefill_fp16(c)) {
         DMALLOC(c, c->xsp, P * He * 2);
         DMALLOC(c, c->xscalep, P * 4);
     }
@@ -1845,7 +1855,7 @@ static int chunk_experts(warp_hip_ctx *c, int layer, const float *X_dev, int T, 
         KRN(c, wk_apply_p6(c->jobs, c->njobs, c->max_jobs, 2, c->lut8d, c->lscaled, c->yd, H, I, c->st));
     } else {
         /* by runs: each expert's records decoded once per WARP_RUN_J jobs */
-        if (g->prefill_fp16) {
+        if (prefill_fp16(c)) {
             /* reduced precision: inputs by pair slot, position-group-major
              * (x replicated per pair once the first plan has placed them) */
             if (first)
