@@ -1003,6 +1003,14 @@ __device__ __forceinline__ int route_key(float v) {
     return b ^ ((b >> 31) & 0x7fffffff);
 }
 
+// Whether a pick has no record: lane j of every wave checks pick j (K <= 64),
+// one ballot, no chain of dependent LDS reads.
+__device__ __forceinline__ bool picks_missing(const warp_slot *slots, const int *sel, int K) {
+    const int l = threadIdx.x & 63;
+    const bool m = l < K && slots[sel[min(l, K - 1)]].rec == nullptr;
+    return __ballot(m) != 0ull;
+}
+
 // Decode routing (one token). The logits, the bias and this layer's expert
 // table go to LDS in one pass of independent loads; one wave then takes the
 // K picks by repeated arg-max -- larger biased score first, the lower id on
@@ -2226,8 +2234,7 @@ __device__ __forceinline__ void lut_item(const LutArgs &a, const unsigned bx, co
         const bool pub = blockIdx.x == 0 && blockIdx.y == 0;
         route_pick_lds<true, LUT_NW * 64>(E, K, a.r.act, a.r.renorm, a.r.routed_scale, score, biased, r_sel, r_wsel,
                                           pub, a.r.scored != 0, s_exp);
-        bool miss = false;                                 // a pick without a record (the same in every block)
-        for (int j = 0; j < K; j++) miss |= slots[r_sel[j]].rec == nullptr;
+        const bool miss = picks_missing(slots, r_sel, K);  // a pick without a record (the same in every block)
         if (pub) {                                         // uniform per block
             if (tid < K) {
                 a.r.idx[tid] = r_sel[tid];
@@ -2803,8 +2810,7 @@ __global__ __launch_bounds__(LUT_NW * 64) void k_moe_fused(MoeArgs) {
     route_in_store(route_in_load(r, tid), E, tid, score, biased, slots);
     route_pick_lds<true, LUT_NW * 64>(E, K, r.act, r.renorm, r.routed_scale, score, biased, r_sel, r_wsel, true,
                                       r.scored != 0);
-    bool miss = false;
-    for (int j = 0; j < K; j++) miss |= slots[r_sel[j]].rec == nullptr;
+    const bool miss = picks_missing(slots, r_sel, K);
     if (tid < K) {
         const warp_slot &sl = slots[r_sel[tid]];
         pk.rec[tid] = sl.rec;
