@@ -15,7 +15,9 @@ outside the bar.
   moe_chunk, both routings, Zipf-skewed runs (odd and even job counts);
 - 512 tokens: token order changes no result bit, and every token stays
   within the bar of the exact mode's chunk output;
-- chunks of 1, 3 and 9 tokens (runs of a single partial job).
+- chunks of 1, 3 and 9 tokens (runs of a single partial job);
+- more distinct experts than cache slots (windows), bit-identical to a
+  cache that holds them all.
 """
 import os
 
@@ -124,3 +126,38 @@ def test_fp16_small_chunks(T):
         log(f"fp16 chunk of {T} tokens: rel err {e:.2e}")
     finally:
         ctx.close()
+
+
+def test_fp16_chunk_in_windows():
+    """More distinct experts than cache slots: the chunk's experts stream
+    through the cache in windows (x is split per pair in the first window
+    only); outputs bit-identical to a cache that holds every expert, and
+    within the bar of the oracle."""
+    import warp_amd
+    spec = ct.Spec(hidden=1024, inter=512, experts=32, top_k=4, layers=1, fmt="VQ12", seed=31, subnormals=False,
+                   keep_codes=False, **BALANCED)
+    model = ct.build(spec)
+    X = np.random.default_rng(17).normal(size=(24, spec.hidden)).astype(np.float32)
+    outs = {}
+    for slots in (None, 8):
+        ctx = open_ctx(model, max_tokens=24, cache_slots=slots, prefill_fp16=True)
+        try:
+            if slots is None:
+                warp_amd.load_container_model(ctx, model)
+            else:
+                warp_amd.load_container_model(ctx, model, records=False)
+                recs = model.layers[0].records
+                ctx.set_fetch(lambda L, e: recs[e])
+            outs[slots] = ctx.moe_chunk_host(0, X)
+        finally:
+            ctx.close()
+    (o1, r1, w1), (o2, r2, w2) = outs[None], outs[8]
+    n = len(np.unique(r1))
+    assert n > 8, n
+    assert np.array_equal(r1, r2) and np.array_equal(w1.view(np.uint32), w2.view(np.uint32))
+    assert np.array_equal(o1.view(np.uint32), o2.view(np.uint32)), float(np.max(np.abs(o1 - o2)))
+    ro, rr, _ = po.LayerView(model, 0).moe_chunk(X)
+    assert np.array_equal(r1, rr)
+    e = rel_err(o1, ro)
+    assert e <= TOL16, e
+    log(f"fp16 chunk of 24 over {n} distinct experts in windows of 8: bit-identical to all resident, rel err {e:.2e}")
