@@ -285,6 +285,7 @@ struct warp_hip_ctx {
     hipStream_t st, cp, la;
     hipStream_t sx;                 /* a chunk's shared expert, beside its routed experts */
     hipEvent_t ev_sx0, ev_sx1;      /* fork from st, join back into st */
+    int sx_pending;                 /* a fork whose join a failed call skipped */
     hipEvent_t ev_copy, ev_before, ev_after, ev_la, ev_x, ev_stage[N_STAGE];
     int copy_pending;
     layer_t *L;
@@ -743,6 +744,12 @@ static int check_layer(warp_hip_ctx *c, int layer)
 {
     if (!c || layer < 0 || layer >= c->cfg.n_layers)
         return c ? set_err(c, WARP_HIP_E_ARG, layer, -1, "layer %d out of range", layer) : WARP_HIP_E_ARG;
+    /* a chunk that failed after forking its shared expert left the side
+     * stream unjoined: nothing on the compute stream may overtake it */
+    if (c->sx_pending) {
+        c->sx_pending = 0;
+        DEV(c, hipStreamWaitEvent(c->st, c->ev_sx1, 0));
+    }
     return 0;
 }
 
@@ -1922,6 +1929,7 @@ int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *ou
         DEV(c, hipStreamWaitEvent(c->sx, c->ev_sx0, 0));
         if ((rc = shared_ffn(c, L, X_dev, T, c->sx))) return rc;
         DEV(c, hipEventRecord(c->ev_sx1, c->sx));
+        c->sx_pending = 1;
     }
     KRN(c, logits_of(c, L, X_dev, T, c->logits, c->st));
     KRN(c, wk_route(c->logits, L->bias, E, K, T, g->router_act, g->renorm, g->routed_scale, c->idx, c->w, NULL, NULL,
@@ -1970,7 +1978,10 @@ int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *ou
         release_hold(c, layer);
         if ((rc = chunk_experts(c, layer, Xe, T, 0, E - 1, 1))) return rc;
     }
-    if (L->sq[0]) DEV(c, hipStreamWaitEvent(c->st, c->ev_sx1, 0));
+    if (L->sq[0]) {
+        c->sx_pending = 0;
+        DEV(c, hipStreamWaitEvent(c->st, c->ev_sx1, 0));
+    }
     if (lat) {
         KRN(c, wk_combine_chunk(c->yd, c->tok_slots, c->pair_w, T, K, c->He, NULL, NULL, c->ylat, c->st));
         if ((rc = latent_tail(c, L, T, resid_dev, out_dev))) return rc;
