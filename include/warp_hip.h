@@ -266,7 +266,10 @@ int warp_hip_expert_ffn(warp_hip_ctx *c, int layer, int expert, const float *x_d
  * ascending expert id, shared expert. resid_dev ([T][H], may be NULL) is
  * added to out. route/rw (host, may be NULL) get [T][K]. With lookahead,
  * the next layer's experts predicted for each token are fetched while this
- * layer computes (the reference has no lookahead on this path). */
+ * layer computes (the reference has no lookahead on this path). Returns
+ * after the layer's work is queued without waiting for it when every record
+ * of the layer is resident and route and rw are NULL (no pick can miss);
+ * otherwise it waits and reports E_MISSING for a pick without a record. */
 int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *out_dev,
                        const float *resid_dev, int T, int *route, float *rw);
 int warp_hip_moe_chunk_host(warp_hip_ctx *c, int layer, const float *X, float *out, int T,

@@ -8,6 +8,10 @@ also with eager work and synchronisations of the same context between the
 replays: the K3-shape path (routing inside the gate/up launch, no shared
 expert) and a layer with a Q8G shared expert (inside the router and combine
 launches).
+
+The same for a stack of chunks: with every record resident and no routes
+asked for, warp_hip_moe_chunk queues its work (the shared expert on a side
+stream joined back by events) and returns, so a step can be captured too.
 """
 import numpy as np
 import pytest
@@ -62,5 +66,54 @@ def test_decode_graph_replays_equal_eager(shared):
             g.free()
         log(f"decode graph ({'Q8G shared expert' if shared else 'no shared expert'}): 12 replays of a "
             f"{Lyr}-layer step equal eager bit for bit")
+    finally:
+        ctx.close()
+
+
+@pytest.mark.parametrize("fp16", [False, True])
+def test_chunk_graph_replays_equal_eager(fp16):
+    """A 2-layer stack of chunks (every record resident, no routes asked
+    for, so a chunk queues its work and returns; a Q8G shared expert on its
+    side stream) captured into a graph and replayed 4 times, with eager
+    chunks and synchronisations between the replays: every replay's outputs
+    equal the eager step's bit for bit, in both precision modes."""
+    import warp_amd
+    from warp_amd.device import D2D, Graph, copy_async
+    spec = ct.Spec(hidden=512, inter=256, experts=32, top_k=4, layers=2, fmt="VQ12", seed=37, shared_bits=8,
+                   **BALANCED)
+    model = ct.build(spec)
+    T = 24
+    ctx = open_ctx(model, max_tokens=T, prefill_fp16=fp16)
+    try:
+        warp_amd.load_container_model(ctx, model)
+        H, Lyr = spec.hidden, spec.layers
+        rng = np.random.default_rng(41)
+        Xs = [dev(rng.normal(size=(T, H)).astype(np.float32)) for _ in range(4)]
+        stage = empty((T, H))
+        outs = [empty((T, H)) for _ in range(Lyr)]
+
+        def step(x_ptr):
+            for L in range(Lyr):
+                ctx.moe_chunk(L, x_ptr if L == 0 else outs[L - 1].ptr, outs[L].ptr, T)
+
+        # eager references
+        ref = []
+        for x in Xs:
+            step(x.ptr)
+            ctx.sync()
+            ref.append([host(o).copy() for o in outs])
+        g = Graph(ctx.stream, lambda: step(stage.ptr))
+        try:
+            for rep in range(4):
+                ctx.moe_chunk(0, Xs[(rep + 1) % 4].ptr, empty((T, H)).ptr, T)      # eager work between replays
+                ctx.sync()
+                copy_async(stage.ptr, Xs[rep].ptr, T * H * 4, D2D, ctx.stream)
+                g.launch()
+                ctx.sync()
+                for L in range(Lyr):
+                    assert np.array_equal(host(outs[L]).view(np.uint32), ref[rep][L].view(np.uint32)), (rep, L)
+        finally:
+            g.free()
+        log(f"chunk stack (prefill_fp16={fp16}): 4 graph replays bit-identical to the eager steps")
     finally:
         ctx.close()

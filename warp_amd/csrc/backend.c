@@ -1901,6 +1901,9 @@ int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *ou
     const int P = T * K;
     const int lat = g->latent > 0;
     if (lat && !L->lq[0]) return set_err(c, WARP_HIP_E_ARG, layer, -1, "layer %d has no latent projections", layer);
+    /* a missing pick an earlier decode left unreported: this chunk's plan
+     * rewrites the device flag, so report it first */
+    if (c->missing_pending && (rc = take_missing(c))) return rc;
     if (L->books_x31 && !c->P6) {
         /* the chunk's matrix-core kernels cannot take exponent-31 codebook
          * values: the tokens go one at a time through the table kernel,
@@ -1991,6 +1994,11 @@ int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *ou
     }
     DEV(c, hipEventRecord(c->ev_after, c->st));
     if ((rc = lookahead_issue(c, layer, n_la))) return rc;
+    /* every record of the layer resident and no selection asked for: no
+     * pick can miss and the plan's job count always fits, so there is
+     * nothing to report and the stream is not waited for (the outputs are
+     * ready when the stream is) */
+    if (!route && !rw && L->resident == E) return 0;
     DEV(c, hipMemcpyAsync(c->h_missing, c->missing, sizeof(int), hipMemcpyDeviceToHost, c->st));
     if (route) DEV(c, hipMemcpyAsync(c->h_idx, c->idx, (size_t)P * sizeof(int), hipMemcpyDeviceToHost, c->st));
     if (rw) DEV(c, hipMemcpyAsync(c->h_w, c->w, (size_t)P * sizeof(float), hipMemcpyDeviceToHost, c->st));
