@@ -350,6 +350,7 @@ struct warp_hip_ctx {
     float *lscale, *lscaled;
     float *part;                /* LUT matvec partial sums                 */
     unsigned *fz_sync;          /* the fused decode launch's counters (zero between launches) */
+    unsigned *run_queue;        /* the prefill run launches' unit queues (zero between launches) */
     size_t part_cap;            /* floats                                  */
     int n_cu, lut_ok, mv_path;
     int *counts, *offsets, *pair_tok, *pair_exp;
@@ -505,6 +506,8 @@ static int ctx_alloc(warp_hip_ctx *c)
         DMALLOC(c, c->lut8d, P * nvI * 256);
         DMALLOC(c, c->lscaled, P * nblkI * 4);
     }
+    DMALLOC(c, c->run_queue, WARP_RUNQ_WORDS * sizeof(unsigned));
+    DEV(c, hipMemset(c->run_queue, 0, WARP_RUNQ_WORDS * sizeof(unsigned)));
     if (c->lut_ok) {
         DMALLOC(c, c->fz_sync, WARP_FZ_WORDS * sizeof(unsigned));
         DEV(c, hipMemset(c->fz_sync, 0, WARP_FZ_WORDS * sizeof(unsigned)));
@@ -668,7 +671,7 @@ void warp_hip_close(warp_hip_ctx *c)
                   c->lscale, c->lscaled, c->counts, c->offsets, c->pair_tok, c->pair_exp, c->pair_w, c->tok_slots, c->runs,
                   c->xin, c->xout, c->la_logits, c->la_idx, c->la_w, c->table_dev, c->pool, c->part,
                   c->shxs, c->shxscale, c->shxin, c->shxinscale, c->tq_dev, c->crc_tmp, c->crc_bad, c->crc_err, c->xlat, c->ylat, c->yup,
-                  c->fz_sync };
+                  c->fz_sync, c->run_queue };
     for (size_t i = 0; i < sizeof d / sizeof d[0]; i++) hfree(d[i]);
     hhfree(c->h_idx); hhfree(c->h_w); hhfree(c->h_la_idx); hhfree(c->h_missing); hhfree(c->staging);
     hhfree(c->h_crc_err); hhfree(c->h_word);
@@ -1869,19 +1872,19 @@ static int chunk_experts(warp_hip_ctx *c, int layer, const float *X_dev, int T, 
                 KRN(c, wk_split_pgm(X_dev, NULL, c->pair_tok, c->offsets + E, P, H, 0, 0, 0.0f, 0.0f, c->xsp,
                                     c->xscalep, c->st));
             KRN(c, wk_vq_runs(g->fmt, c->jobs, c->njobs, c->max_jobs, c->runs, 0, 2, L->books, c->xsp, c->xscalep,
-                              yk, I, H, P, c->st));
+                              yk, I, H, P, c->run_queue, c->st));
             KRN(c, wk_split_pgm(c->yg, c->yu, NULL, c->offsets + E, P, I, 1, g->act_situ, g->situ_beta,
                                 g->situ_linear_beta, c->xsh, c->xscaleh, c->st));
             KRN(c, wk_vq_runs(g->fmt, c->jobs, c->njobs, c->max_jobs, c->runs, 2, 1, L->books, c->xsh, c->xscaleh,
-                              yk, H, I, P, c->st));
+                              yk, H, I, P, c->run_queue, c->st));
         } else {
             if (first) KRN(c, wk_split(X_dev, T, H, c->xs, c->xscale, c->st));
             KRN(c, wk_vq_runs(g->fmt, c->jobs, c->njobs, c->max_jobs, c->runs, 0, 2, L->books, c->xs, c->xscale, yk,
-                              I, H, 0, c->st));
+                              I, H, 0, c->run_queue, c->st));
             KRN(c, wk_act_split(c->yg, c->yu, P, I, g->act_situ, g->situ_beta, g->situ_linear_beta, c->xsh,
                                 c->xscaleh, NULL, c->st));
             KRN(c, wk_vq_runs(g->fmt, c->jobs, c->njobs, c->max_jobs, c->runs, 2, 1, L->books, c->xsh, c->xscaleh,
-                              yk, H, I, 0, c->st));
+                              yk, H, I, 0, c->run_queue, c->st));
         }
     }
     return 0;

@@ -1367,17 +1367,68 @@ struct VqArgs {
     float *y[3];                // per kind: [ny][M]
     int M, N;
     int xrows;                  // reduced-precision kernel: xs is [N/32][xrows][32] fp16
+    unsigned *queue;            // run kernels: per kind, a ticket and a waves-done counter
 };
 
-// waves per block (NW) and code words in flight per wave (D) are template
-// parameters of the kernel below
+// Units of the run kernels are dealt in chunks of NW consecutive units (a
+// block's waves) to RQ_GROUPS queues, one per XCD (blocks go to the XCDs
+// round-robin, and the grid is a multiple of RQ_GROUPS): queue g holds
+// chunks g, g + 8, g + 16, ... and serves blocks g, g + 8, .... A wave's
+// first unit is its block's own chunk (block b, wave w: unit b NW + w);
+// after each unit it takes a ticket from its queue, so a wave that finishes
+// early takes the next unit of its queue, and the last, partial round
+// spreads over the CUs instead of falling on the waves of the first blocks.
+// A queue per XCD keeps the atomics off one address (a single counter
+// serialised them: 130 us more per layer of 512 tokens). Each unit writes
+// only its own outputs, so which wave runs it changes no result bit. Queue
+// (kind k, group g) is a ticket counter at line 2 (RQ_GROUPS k + g)
+// (RQ_LINE words a line) and a waves-done counter on the next line; the
+// last wave of the group out clears both, so every launch (graph replays
+// included) starts from zero without a memset.
+constexpr int RQ_LINE = 32, RQ_GROUPS = 8;
 
-// Block = 16 waves, grid.y = kind. A unit is (job, 64-row block); WPU waves
-// share one unit, each over a contiguous range of 4-position groups, and
-// their partial sums meet in LDS (fixed order, so results are deterministic).
-// Code words and B operands run VQ_D groups ahead of their use. With DB the
-// codebook gathers of the next group are issued before the current group's
-// MFMAs, so each wave keeps two groups of LDS reads in flight.
+struct RunQueue {
+    unsigned *q;                // the ticket counter; waves done one line on
+    int n;                      // units of this queue
+    int nwaves;                 // waves of this queue's blocks
+};
+
+template <int NW> __device__ __forceinline__ RunQueue rq_open(unsigned *base, int kind, int units) {
+    constexpr int span = NW * RQ_GROUPS;
+    const int g = blockIdx.x % RQ_GROUPS;
+    RunQueue r;
+    r.n = (units / span) * NW + min(max(units % span - g * NW, 0), NW);
+    r.nwaves = (int)(gridDim.x / RQ_GROUPS) * NW;
+    r.q = base + 2 * (kind * RQ_GROUPS + g) * RQ_LINE;
+    return r;
+}
+
+// this block's first local index, and local index l of its queue -> unit
+template <int NW> __device__ __forceinline__ int rq_first() { return (int)(blockIdx.x / RQ_GROUPS) * NW; }
+template <int NW> __device__ __forceinline__ int rq_unit(int l) {
+    return (l / NW) * NW * RQ_GROUPS + (int)(blockIdx.x % RQ_GROUPS) * NW + l % NW;
+}
+
+__device__ __forceinline__ int rq_take(const RunQueue &r, int lane) {
+    unsigned t = 0;
+    if (lane == 0) t = __hip_atomic_fetch_add(r.q, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return r.nwaves + __builtin_amdgcn_readfirstlane((int)t);
+}
+
+// n waves leave (a block that had no unit leaves as one): each wave's
+// ticket past the end has returned before it leaves, so the last one out
+// clears both counters
+__device__ __forceinline__ void rq_leave(const RunQueue &r, int lane, unsigned n) {
+    if (lane == 0) {
+        unsigned *done = r.q + RQ_LINE;
+        const unsigned old = __hip_atomic_fetch_add(done, n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old + n == (unsigned)r.nwaves) {
+            __hip_atomic_store(r.q, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
 template <int FMT, int SB>
 __device__ __forceinline__ void gather_group(const unsigned char *lds, const Word<SB> &wd, half8 (&a)[4][FmtT<FMT>::S]) {
 #pragma unroll
@@ -1599,8 +1650,11 @@ __global__ __launch_bounds__(512) void k_vq_mfma_run(VqArgs a, const int *__rest
     const int kind = a.kind_lo + blockIdx.y;
     const warp_job *jobs = a.jobs + (size_t)kind * a.max_jobs;
     const int M = a.M, N = a.N, nv = N >> 3, npg = nv >> 2, nrb = (M + 63) >> 6;
-    const int units = a.njobs[3] * nrb;
-    if ((int)(blockIdx.x * 8) >= units) return;   // uniform per block
+    const RunQueue rq = rq_open<8>(a.queue, kind, a.njobs[3] * nrb);
+    if (rq_first<8>() >= rq.n) {                    // uniform per block
+        rq_leave(rq, threadIdx.x, 8);
+        return;
+    }
     {
         const uint4 *src = (const uint4 *)(a.books + (size_t)kind * F::S * F::E * 8);
         uint4 *dst = (uint4 *)lds_vq;
@@ -1609,7 +1663,8 @@ __global__ __launch_bounds__(512) void k_vq_mfma_run(VqArgs a, const int *__rest
     __syncthreads();
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, jc = lane & 15, ts = jc >> 1, hl = jc & 1;
-    for (int u = blockIdx.x * 8 + wave; u < units; u += gridDim.x * 8) {
+    for (int l = rq_first<8>() + wave; l < rq.n;) {
+        const int u = rq_unit<8>(l);
         const int rv = __builtin_amdgcn_readfirstlane(runs[u / nrb]);   // uniform: u is
         const int j0 = rv >> 3, nt = rv & 7, rb = u % nrb;
         const uint8_t *cp = jobs[j0].idx + ((size_t)rb * nv) * 64 * F::SB + (size_t)lane * 4 * F::SB;
@@ -1667,6 +1722,7 @@ __global__ __launch_bounds__(512) void k_vq_mfma_run(VqArgs a, const int *__rest
 #pragma unroll
         for (int k = 0; k < WD; k++)
             if (npg_full + k < npg) step(k, npg_full + k);    // uniform
+        l = rq_take(rq, lane);                                // returns while the outputs are stored
         // lane (g, jc) holds C[4g + r][jc] of row tile t: block row 16g + 4r + t,
         // token slot jc / 2 of the job, half jc % 2
 #pragma unroll
@@ -1686,6 +1742,7 @@ __global__ __launch_bounds__(512) void k_vq_mfma_run(VqArgs a, const int *__rest
                 }
         }
     }
+    rq_leave(rq, lane, 1);
 }
 
 template <int FMT>
@@ -1703,7 +1760,7 @@ static int launch_vq_run(const VqArgs &a, const int *runs, int nkinds, int max_u
     int grid = (max_units + 7) / 8;
     const int cap = FMT == WARP_FMT_VQ12 ? 256 : 1024;
     if (grid > cap) grid = cap;
-    if (grid < 1) grid = 1;
+    grid = (grid + RQ_GROUPS - 1) / RQ_GROUPS * RQ_GROUPS;   // the unit queues' groups
     hipLaunchKernelGGL((k_vq_mfma_run<FMT, WD>), dim3(grid, nkinds), dim3(512), lds, (hipStream_t)stream, a, runs);
     CHECK_LAUNCH();
     return 0;
@@ -1742,8 +1799,11 @@ __global__ __launch_bounds__(1024) void k_vq_run_f16(VqArgs a, const int *__rest
     const int kind = a.kind_lo + blockIdx.y;
     const warp_job *jobs = a.jobs + (size_t)kind * a.max_jobs;
     const int M = a.M, N = a.N, nv = N >> 3, npg = nv >> 2, nrb = (M + 63) >> 6;
-    const int units = a.njobs[3] * nrb;
-    if ((int)(blockIdx.x * NWB) >= units) return;   // uniform per block
+    const RunQueue rq = rq_open<NWB>(a.queue, kind, a.njobs[3] * nrb);
+    if (rq_first<NWB>() >= rq.n) {                  // uniform per block
+        rq_leave(rq, threadIdx.x, NWB);
+        return;
+    }
     {
         const uint4 *src = (const uint4 *)(a.books + (size_t)kind * F::S * F::E * 8);
         for (int i = threadIdx.x; i < F::S * F::E; i += blockDim.x) cb_lds[i] = src[i];
@@ -1755,7 +1815,8 @@ __global__ __launch_bounds__(1024) void k_vq_run_f16(VqArgs a, const int *__rest
     // the unit and a per-group offset in a scalar register
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void *)a.xs, 0, -1, BUF_RSRC_W3);
     const int pgb_x = a.xrows * 64;                          // bytes per position group of xs
-    for (int u = blockIdx.x * NWB + wave; u < units; u += gridDim.x * NWB) {
+    for (int l = rq_first<NWB>() + wave; l < rq.n;) {
+        const int u = rq_unit<NWB>(l);
         const int rv = __builtin_amdgcn_readfirstlane(runs[u / nrb]);   // uniform: u is
         const int j0 = rv >> 3, nt = rv & 7, rb = u % nrb;
         // the unit's code words (uniform: the descriptor lives in scalar registers)
@@ -1820,6 +1881,7 @@ __global__ __launch_bounds__(1024) void k_vq_run_f16(VqArgs a, const int *__rest
 #pragma unroll
         for (int k = 0; k < WD; k++)
             if (npg_full + k < npg) step(k, npg_full + k);    // uniform
+        l = rq_take(rq, lane);                                // returns while the outputs are stored
         // lane (g, jc) holds C[4g + r][jc] of row tile t: block row
         // 16g + 4r + t, token jc % 8 of job 2 q + jc / 8
 #pragma unroll
@@ -1839,6 +1901,7 @@ __global__ __launch_bounds__(1024) void k_vq_run_f16(VqArgs a, const int *__rest
                 }
         }
     }
+    rq_leave(rq, lane, 1);
 }
 
 template <int FMT>
@@ -1848,7 +1911,7 @@ static int launch_vq_run_f16(const VqArgs &a, const int *runs, int nkinds, int m
     int grid = (max_units + 15) / 16;
     const int cap = FMT == WARP_FMT_VQ12 ? 256 : 512;
     if (grid > cap) grid = cap;
-    if (grid < 1) grid = 1;
+    grid = (grid + RQ_GROUPS - 1) / RQ_GROUPS * RQ_GROUPS;   // the unit queues' groups
     hipLaunchKernelGGL((k_vq_run_f16<FMT, WD>), dim3(grid, nkinds), dim3(1024), 0, (hipStream_t)stream, a, runs);
     CHECK_LAUNCH();
     return 0;
@@ -1856,8 +1919,8 @@ static int launch_vq_run_f16(const VqArgs &a, const int *runs, int nkinds, int m
 
 extern "C" int wk_vq_runs(int fmt, const warp_job *jobs, const int *njobs, int max_jobs, const int *runs,
                           int kind_lo, int nkinds, const uint16_t *books, const uint16_t *xs, const float *xscale,
-                          float *const *y, int M, int N, int fp16_rows, void *stream) {
-    if (M <= 0 || N <= 0 || (N % 32) || max_jobs <= 0 || !runs || kind_lo < 0 || nkinds < 1 || kind_lo + nkinds > 3 ||
+                          float *const *y, int M, int N, int fp16_rows, unsigned *queue, void *stream) {
+    if (M <= 0 || N <= 0 || (N % 32) || max_jobs <= 0 || !runs || !queue || kind_lo < 0 || nkinds < 1 || kind_lo + nkinds > 3 ||
         fp16_rows < 0 || (size_t)fp16_rows * N * 2 >= ((size_t)1 << 31))
         return -1;
     const int fp16 = fp16_rows > 0;
@@ -1873,6 +1936,7 @@ extern "C" int wk_vq_runs(int fmt, const warp_job *jobs, const int *njobs, int m
     a.M = M;
     a.N = N;
     a.xrows = fp16_rows;
+    a.queue = queue;
     const int max_units = max_jobs * ((M + 63) / 64);
     switch (fmt) {
 #define VR(F)                                                                                                      \

@@ -158,10 +158,14 @@ int wk_vq_matvec(int fmt, const warp_job *jobs, const int *njobs, int max_jobs,
  * fp16_rows = 0: exact products, xs/xscale as for wk_vq_matvec (rows by
  * xi). fp16_rows > 0: the reduced-precision products (stage vectors added
  * in fp16, x's fp16 high half), xs [N/32][fp16_rows][32] and xscale
- * [fp16_rows] by pair slot (yi), from wk_split_pgm. */
+ * [fp16_rows] by pair slot (yi), from wk_split_pgm.
+ * queue: WARP_RUNQ_WORDS words, zero before the first launch; the launch
+ * hands units out through it (a ticket and a waves-done counter per kind
+ * and XCD) and leaves it zero (launches on one queue must not overlap). */
+#define WARP_RUNQ_WORDS 1536
 int wk_vq_runs(int fmt, const warp_job *jobs, const int *njobs, int max_jobs, const int *runs,
                int kind_lo, int nkinds, const uint16_t *books, const uint16_t *xs, const float *xscale,
-               float *const *y, int M, int N, int fp16_rows, void *stream);
+               float *const *y, int M, int N, int fp16_rows, unsigned *queue, void *stream);
 /* Inputs of the reduced-precision products: rows p < *nrows of
  * act(g, u) (act = 1, pair rows) or of x row rowmap[p] (act = 0, u NULL),
  * each scaled by a power of two (2^-k to xscale[p]) and rounded to fp16,
