@@ -148,7 +148,8 @@ typedef struct {
     int prefill_fp16;      /* chunks (warp_hip_moe_chunk*): the routed experts'
                             * matrix-core products in fp16 -- the stages'
                             * codebook vectors added into one fp16 value, x's
-                            * fp16 high half only -- a quarter of the MFMAs,
+                            * fp16 high half only, SwiGLU's SiLU with the
+                            * hardware exp -- a quarter of the MFMAs,
                             * outputs within 2e-3 of the reference instead of
                             * 1e-4 (the reference CPU path has no such mode;
                             * 0 keeps the exact products). Needs max_tokens x

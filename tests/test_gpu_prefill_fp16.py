@@ -1,6 +1,7 @@
 """A chunk's reduced-precision mode (prefill_fp16: each position's stage
-vectors added into one fp16 value, x's fp16 high half only, products
-accumulated in fp32 on the matrix cores) against the reference's outputs
+vectors added into one fp16 value, x's fp16 high half only, SwiGLU's SiLU
+with the hardware exp, products accumulated in fp32 on the matrix cores)
+against the reference's outputs
 and the oracle, through the C ABI.
 
 The bar for this mode is max|d|/max|ref| <= 2e-3, ten times inside the

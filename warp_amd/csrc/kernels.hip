@@ -166,6 +166,14 @@ struct PgmOut {
     int R;
 };
 
+// The SwiGLU of the reduced-precision inputs: SiLU with the hardware exp
+// (a few ulp of fp32), whose result is then rounded to fp16 (2^-11); SiTU
+// keeps the exact form.
+__device__ __forceinline__ float act_f16(float g, float u, int situ, float beta, float lbeta) {
+    if (situ) return act_pair(g, u, situ, beta, lbeta);
+    return g / (1.0f + __expf(-g)) * u;
+}
+
 template <int NP, bool ACT, bool PGM>
 __global__ __launch_bounds__(256) void k_split_w(const float *__restrict__ g, const float *__restrict__ u, int P, int N,
                                                  int situ, float beta, float lbeta, half8 *__restrict__ xs,
@@ -196,7 +204,8 @@ __global__ __launch_bounds__(256) void k_split_w(const float *__restrict__ g, co
         const bool in = lane + 64 * j < nv;
 #pragma unroll
         for (int e = 0; e < 8; e++) {
-            h[j][e] = ACT ? act_pair(gx[e], ux[e], situ, beta, lbeta) : gx[e];
+            h[j][e] = ACT ? (PGM ? act_f16(gx[e], ux[e], situ, beta, lbeta) : act_pair(gx[e], ux[e], situ, beta, lbeta))
+                          : gx[e];
             if (in) m = fmaxf(m, fabsf(h[j][e]));
         }
     }
@@ -262,7 +271,7 @@ static int launch_split_w(const float *g, const float *u, int P, int N, int situ
 // xs[(pg * R + p) * 32 ..], so the consecutive pair slots of a run are side
 // by side in every position group. Each row is scaled by a power of two
 // (max |v| * 2^k in [2^14, 2^15), 2^-k to xscale[p]) as wk_split does. ACT:
-// row p is act(g, u) of pair row p; otherwise row rowmap[p] of x (a chunk's
+// row p is act_f16(g, u) of pair row p; otherwise row rowmap[p] of x (a chunk's
 // pairs in slot order, x replicated per pair). Rows at or past *nrows are
 // not written. One 256-thread block per row: a pass for the max, a pass for
 // the stores (the row comes from L2 the second time).
@@ -283,7 +292,7 @@ __global__ __launch_bounds__(256) void k_split_pgm(const float *__restrict__ g, 
             const float4 b0 = ur[2 * v], b1 = ur[2 * v + 1];
             const float ux[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
 #pragma unroll
-            for (int e = 0; e < 8; e++) h[e] = act_pair(gx[e], ux[e], situ, beta, lbeta);
+            for (int e = 0; e < 8; e++) h[e] = act_f16(gx[e], ux[e], situ, beta, lbeta);
         } else {
 #pragma unroll
             for (int e = 0; e < 8; e++) h[e] = gx[e];
@@ -1372,7 +1381,8 @@ struct VqArgs {
 
 // Units of the run kernels are dealt in chunks of NW consecutive units (a
 // block's waves) to RQ_GROUPS queues, one per XCD (blocks go to the XCDs
-// round-robin, and the grid is a multiple of RQ_GROUPS): queue g holds
+// round-robin, which matters only for speed: the queues are correct
+// wherever the blocks run; the grid is a multiple of RQ_GROUPS): queue g holds
 // chunks g, g + 8, g + 16, ... and serves blocks g, g + 8, .... A wave's
 // first unit is its block's own chunk (block b, wave w: unit b NW + w);
 // after each unit it takes a ticket from its queue, so a wave that finishes

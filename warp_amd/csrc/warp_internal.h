@@ -167,7 +167,8 @@ int wk_vq_runs(int fmt, const warp_job *jobs, const int *njobs, int max_jobs, co
                int kind_lo, int nkinds, const uint16_t *books, const uint16_t *xs, const float *xscale,
                float *const *y, int M, int N, int fp16_rows, unsigned *queue, void *stream);
 /* Inputs of the reduced-precision products: rows p < *nrows of
- * act(g, u) (act = 1, pair rows) or of x row rowmap[p] (act = 0, u NULL),
+ * act(g, u) (act = 1, pair rows; SiLU with the hardware exp, SiTU exact)
+ * or of x row rowmap[p] (act = 0, u NULL),
  * each scaled by a power of two (2^-k to xscale[p]) and rounded to fp16,
  * into xs [N/32][P][32]. N % 32 == 0, pointers 16-byte aligned. */
 int wk_split_pgm(const float *g, const float *u, const int *rowmap, const int *nrows, int P, int N,
