@@ -3176,6 +3176,18 @@ extern "C" int wk_lut_reduce(const warp_job *jobs, const int *njobs, int max_job
 // the weights, the addends); only the row scale waits for its job entry.
 // SHB (8 or 4): add0 is the shared expert's down rows of this block against
 // sa.h, one wave per 4 rows, their weights loaded first.
+// A block of the combine takes 16 rows, half of a 128-byte line of every
+// partial-sum row it reads. Blocks go to the XCDs round-robin, so blocks b
+// and b + 8 of each group of 16 take the two halves of one line: it is then
+// fetched into one XCD's L2 once, not into two (placement matters only for
+// speed; the rows are each block's whatever XCD runs it). The blocks of a
+// last, partial group keep their own rows.
+__device__ __forceinline__ int combine_r0() {
+    const int b = blockIdx.x, full = (int)gridDim.x & ~15;
+    if (b >= full) return b * 16;
+    return ((b >> 4) * 16 + (b & 7) * 2 + ((b >> 3) & 1)) * 16;
+}
+
 template <int SHB, int MC>
 __global__ __launch_bounds__(256) void k_combine_lut(const warp_job *__restrict__ jobs2, const float *__restrict__ part,
                                                      int splits, int max_jobs, const float *__restrict__ w, int K,
@@ -3186,7 +3198,7 @@ __global__ __launch_bounds__(256) void k_combine_lut(const warp_job *__restrict_
     __shared__ float wl[WARP_MAX_K];
     __shared__ float shd[16];
     extern __shared__ float hl[];
-    const int r0 = blockIdx.x * 16, row = threadIdx.x & 15, jq = threadIdx.x >> 4;
+    const int r0 = combine_r0(), row = threadIdx.x & 15, jq = threadIdx.x >> 4;
     const int i = min(r0 + row, H - 1);
     using Q = QRow<SHB ? SHB : 8, MC>;
     Q qd[4];
