@@ -1868,7 +1868,9 @@ static int chunk_experts(warp_hip_ctx *c, int layer, const float *X_dev, int T, 
         if (prefill_fp16(c)) {
             /* reduced precision: inputs by pair slot, position-group-major
              * (x replicated per pair once the first plan has placed them) */
-            if (first)
+            if (first && H <= 4096)
+                KRN(c, wk_split_pgm_pairs(X_dev, c->tok_slots, T, K, H, c->xsp, c->xscalep, c->st));
+            else if (first)
                 KRN(c, wk_split_pgm(X_dev, NULL, c->pair_tok, c->offsets + E, P, H, 0, 0, 0.0f, 0.0f, c->xsp,
                                     c->xscalep, c->st));
             KRN(c, wk_vq_runs(g->fmt, c->jobs, c->njobs, c->max_jobs, c->runs, 0, 2, L->books, c->xsp, c->xscalep,

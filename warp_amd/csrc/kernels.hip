@@ -164,6 +164,8 @@ __global__ __launch_bounds__(1024) void k_split(const float *__restrict__ x, int
 struct PgmOut {
     const int *rowmap, *nrows;
     int R;
+    const int *tok_slots;       // by pair in token order: wave q takes x row q / K to slot tok_slots[q]
+    int K;
 };
 
 // The SwiGLU of the reduced-precision inputs: SiLU with the hardware exp
@@ -180,9 +182,15 @@ __global__ __launch_bounds__(256) void k_split_w(const float *__restrict__ g, co
                                                  float *__restrict__ xscale, float *__restrict__ h_out, PgmOut pm) {
     const int lane = threadIdx.x & 63, p = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     if (p >= P) return;                                    // uniform per wave
-    if (PGM && p >= *pm.nrows) return;                     // uniform per wave
+    if (PGM && !pm.tok_slots && p >= *pm.nrows) return;    // uniform per wave
     const int nv = N >> 3;
-    const size_t src = PGM && pm.rowmap ? (size_t)pm.rowmap[p] : (size_t)p;
+    size_t src = PGM && pm.rowmap ? (size_t)pm.rowmap[p] : (size_t)p;
+    int dst = p;                                           // the output row (PGM)
+    if (PGM && pm.tok_slots) {
+        dst = pm.tok_slots[p];
+        if (dst < 0) return;                               // uniform per wave: a pair not computed
+        src = (size_t)(p / pm.K);
+    }
     const float4 *gp = (const float4 *)(g + src * N), *up = ACT ? (const float4 *)(u + src * N) : nullptr;
     float4 gv[NP][2], uv[NP][2] = {};
 #pragma unroll
@@ -224,7 +232,7 @@ __global__ __launch_bounds__(256) void k_split_w(const float *__restrict__ g, co
                 lo[e] = (_Float16)(v - (float)hi[e]);
             }
             if constexpr (PGM) {
-                xs[((size_t)(pos >> 2) * pm.R + p) * 4 + (pos & 3)] = hi;
+                xs[((size_t)(pos >> 2) * pm.R + dst) * 4 + (pos & 3)] = hi;
             } else {
                 o[2 * pos] = hi;
                 o[2 * pos + 1] = lo;
@@ -236,7 +244,7 @@ __global__ __launch_bounds__(256) void k_split_w(const float *__restrict__ g, co
             }
         }
     }
-    if (lane == 0) xscale[p] = ldexpf(1.0f, -k);
+    if (lane == 0) xscale[PGM ? dst : p] = ldexpf(1.0f, -k);
 }
 
 template <bool ACT, bool PGM = false>
@@ -326,9 +334,9 @@ extern "C" int wk_split_pgm(const float *g, const float *u, const int *rowmap, c
     // rows of up to 4096 values one wave each, in registers; longer rows a block each
     if (N <= 4096)
         return act ? launch_split_w<true, true>(g, u, P, N, act_situ, beta, lbeta, xs, xscale, nullptr, stream,
-                                                PgmOut{nullptr, nrows, P})
+                                                PgmOut{nullptr, nrows, P, nullptr, 0})
                    : launch_split_w<false, true>(g, nullptr, P, N, 0, 0.0f, 0.0f, xs, xscale, nullptr, stream,
-                                                 PgmOut{rowmap, nrows, P});
+                                                 PgmOut{rowmap, nrows, P, nullptr, 0});
     if (act)
         hipLaunchKernelGGL(k_split_pgm<true>, dim3(P), dim3(256), 0, (hipStream_t)stream, g, u, rowmap, nrows, N, P,
                            act_situ, beta, lbeta, (half8 *)xs, xscale);
@@ -337,6 +345,14 @@ extern "C" int wk_split_pgm(const float *g, const float *u, const int *rowmap, c
                            0, 0.0f, 0.0f, (half8 *)xs, xscale);
     CHECK_LAUNCH();
     return 0;
+}
+
+extern "C" int wk_split_pgm_pairs(const float *x, const int *tok_slots, int T, int K, int N, uint16_t *xs,
+                                  float *xscale, void *stream) {
+    if (T <= 0 || K <= 0 || N <= 0 || N > 4096 || (N % 32) || !tok_slots || (((uintptr_t)x | (uintptr_t)xs) & 15))
+        return -1;
+    return launch_split_w<false, true>(x, nullptr, T * K, N, 0, 0.0f, 0.0f, xs, xscale, nullptr, stream,
+                                       PgmOut{nullptr, nullptr, T * K, tok_slots, K});
 }
 
 extern "C" int wk_split(const float *x, int T, int N, uint16_t *xs, float *xscale, void *stream) {

@@ -174,6 +174,13 @@ int wk_vq_runs(int fmt, const warp_job *jobs, const int *njobs, int max_jobs, co
 int wk_split_pgm(const float *g, const float *u, const int *rowmap, const int *nrows, int P, int N,
                  int act, int act_situ, float beta, float lbeta, uint16_t *xs, float *xscale,
                  void *stream);
+/* The x rows of the same, walked by pair in token order: pair q = t K + k
+ * takes x row t to its slot tok_slots[q] (the grouping's slots; -1: not
+ * computed), so a token's pairs run in neighbouring blocks and its row is
+ * fetched by few XCDs. The values of wk_split_pgm with rowmap = pair_tok,
+ * into xs [N/32][T K][32] and xscale [T K]. N <= 4096, else -1. */
+int wk_split_pgm_pairs(const float *x, const int *tok_slots, int T, int K, int N, uint16_t *xs, float *xscale,
+                       void *stream);
 
 /* The LUT matvec (decode, one input per job): for each kind
  * kind_lo..kind_lo+nkinds-1, every job's rows against the f32 input
