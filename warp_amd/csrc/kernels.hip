@@ -161,6 +161,19 @@ __global__ __launch_bounds__(1024) void k_split(const float *__restrict__ x, int
 // (the same exponent from the same maximum). PGM: only the hi halves, in
 // the position-group-major order of the reduced-precision products (see
 // k_split_pgm), rows p < *nrows, x's row rowmap[p] when rowmap is given.
+// Blocks go to the XCDs round-robin. For launches whose neighbouring blocks
+// 2x and 2x + 1 read the same data (the two halves of a line, or one
+// token's rows), block b of each group of 16 takes work block
+// 16 (b / 16) + 2 (b % 8) + (b / 8) % 2, so that blocks b and b + 8, which
+// share an XCD, take work blocks 2x and 2x + 1 and the data is fetched into
+// one L2. Placement matters only for speed: each block's work is the same
+// whatever XCD runs it. The blocks of a last, partial group keep their own.
+__device__ __forceinline__ int xcd_pair_block(int b) {
+    const int full = (int)gridDim.x & ~15;
+    if (b >= full) return b;
+    return (b >> 4) * 16 + (b & 7) * 2 + ((b >> 3) & 1);
+}
+
 struct PgmOut {
     const int *rowmap, *nrows;
     int R;
@@ -180,7 +193,9 @@ template <int NP, bool ACT, bool PGM>
 __global__ __launch_bounds__(256) void k_split_w(const float *__restrict__ g, const float *__restrict__ u, int P, int N,
                                                  int situ, float beta, float lbeta, half8 *__restrict__ xs,
                                                  float *__restrict__ xscale, float *__restrict__ h_out, PgmOut pm) {
-    const int lane = threadIdx.x & 63, p = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    // by pair in token order, a token's neighbouring blocks on one XCD
+    const int blk = PGM && pm.tok_slots ? xcd_pair_block((int)blockIdx.x) : (int)blockIdx.x;
+    const int lane = threadIdx.x & 63, p = blk * (blockDim.x >> 6) + (threadIdx.x >> 6);
     if (p >= P) return;                                    // uniform per wave
     if (PGM && !pm.tok_slots && p >= *pm.nrows) return;    // uniform per wave
     const int nv = N >> 3;
@@ -3193,16 +3208,9 @@ extern "C" int wk_lut_reduce(const warp_job *jobs, const int *njobs, int max_job
 // SHB (8 or 4): add0 is the shared expert's down rows of this block against
 // sa.h, one wave per 4 rows, their weights loaded first.
 // A block of the combine takes 16 rows, half of a 128-byte line of every
-// partial-sum row it reads. Blocks go to the XCDs round-robin, so blocks b
-// and b + 8 of each group of 16 take the two halves of one line: it is then
-// fetched into one XCD's L2 once, not into two (placement matters only for
-// speed; the rows are each block's whatever XCD runs it). The blocks of a
-// last, partial group keep their own rows.
-__device__ __forceinline__ int combine_r0() {
-    const int b = blockIdx.x, full = (int)gridDim.x & ~15;
-    if (b >= full) return b * 16;
-    return ((b >> 4) * 16 + (b & 7) * 2 + ((b >> 3) & 1)) * 16;
-}
+// partial-sum row it reads: neighbouring blocks share each line, and
+// xcd_pair_block puts them on one XCD, so the line is fetched into one L2.
+__device__ __forceinline__ int combine_r0() { return xcd_pair_block((int)blockIdx.x) * 16; }
 
 template <int SHB, int MC>
 __global__ __launch_bounds__(256) void k_combine_lut(const warp_job *__restrict__ jobs2, const float *__restrict__ part,
