@@ -66,8 +66,9 @@ typedef struct {
 const char *waste_register_hip(waste_kernels *t);
 
 /* Replaces: src/waste_backend.h:112-114 for this backend. Drops the device
- * mirrors of trunk tensors keyed by host pointer; call before the model frees
- * its host buffers. */
+ * mirrors of trunk tensors keyed by host pointer and the MoE slots' device
+ * state (their contexts, keyed by model); call before the model frees its
+ * host buffers. */
 void waste_hip_release_host_buffers(void);
 
 /* Calls of the mvq_rows_f32 slot that ran on the device / fell back. */
@@ -83,6 +84,107 @@ void warp_hip_kda_stats(uint64_t *device_calls, uint64_t *fallback_calls);
  * T calls of waste_kda_step. */
 int warp_hip_kda_forward(int T, int H, int K, int V, const float *q_dev, const float *k_dev, const float *v_dev,
                          const float *g_dev, const float *beta_dev, float *S_dev, float *o_dev, void *stream);
+
+/* ---- 1b. the MoE path behind a table of the same style -----------------------
+ *
+ * The reference's table has no slot for the routed-expert path: moe_layer
+ * (src/model.c:2713) and moe_chunk (src/model.c:3512) are static, and call
+ * vq_apply, the routing and the combine directly. This second table, beside
+ * waste_kernels and in its style (function pointers the engine calls,
+ * defaults that leave the CPU path in charge, filled by a registration
+ * function), gives the engine one backend-neutral call per call site:
+ *
+ *     if (waste_km.moe_ffn_decode && waste_km.moe_ffn_decode(&a) == 0) return;
+ *
+ * at the top of moe_layer, and the same with moe_ffn_batch in moe_chunk.
+ * A slot returns 0 when it has written every output, or a negative
+ * WARP_HIP_E_* code when it declined or failed, having written nothing the
+ * caller reads: the caller then runs its own CPU code with the same
+ * arguments. A separate struct, rather than members appended to
+ * waste_kernels, keeps waste_kernels' layout, so a registration function
+ * never writes past the end of an engine's older table. */
+
+/* A trunk tensor as waste_tensor holds it (src/model.h:30-45): F32 rows in
+ * `data`, or quantised rows (Q8G, Q4G, Q3G) in q / qs. */
+typedef struct {
+    const float *data;        /* F32 [out][in], or NULL                     */
+    const int8_t *q;          /* quantised rows, `rowbytes` apart           */
+    const uint16_t *qs;       /* fp16 scale per group of `group`            */
+    int group, bits;          /* bits 8, 4 or 3 when quantised              */
+    size_t rowbytes;
+} warp_trunk_tensor;
+
+/* Everything moe_layer / moe_chunk read for one MoE layer, as plain host
+ * pointers into the engine's model (waste_model), and the call's own
+ * inputs and outputs. The backend keeps device copies keyed by `model`
+ * and by these pointers (the way src/metal.m:98-150 keys its buffers),
+ * until waste_hip_release_host_buffers. */
+typedef struct {
+    const void *model;        /* identity of the engine's model            */
+    int layer, n_layers;
+    /* waste_config (src/model.h) */
+    int hidden, moe_inter, n_experts, top_k;
+    int latent_dim;           /* 0: the experts run on hidden               */
+    int latent_norm;          /* latent_moe_use_norm                        */
+    float norm_eps;
+    int renorm;               /* moe_renormalize present                    */
+    float routed_scale;
+    int act_situ;
+    float situ_beta, situ_linear_beta;
+    /* the expert format: index_bits 8 (stages 3 or 2, entries 256) or 6
+     * (4 x 64), as waste_model keeps them; 12 with 2 x 4096 for the
+     * 12-bit extension */
+    int index_bits, stages, cb_entries, vec_dim;
+    /* m->codebooks: [n_books][cb_entries][vec_dim] f32, flushed as the
+     * loader flushes (src/model.c:1277-1286); this layer's bank base */
+    const float *codebooks;
+    int n_books, cb_base;
+    /* block_sparse_moe.gate.weight and .e_score_correction_bias (NULL) */
+    warp_trunk_tensor router;
+    const float *bias;
+    /* shared_experts.{gate,up,down}_proj (q NULL and data NULL: none),
+     * inter_shared = moe_inter * n_shared */
+    warp_trunk_tensor shared[3];
+    int inter_shared;
+    /* routed_expert_{down,up}_proj and routed_expert_norm (latent only) */
+    warp_trunk_tensor latent[2];
+    const float *latent_norm_w;
+    /* expert records: the bank's stride, and how a miss is read
+     * (bank_fetch and its model, src/model.c:1767-1812); the HBM cache
+     * size the backend may use, and the engine's verify and lookahead */
+    size_t rec_bytes, cache_bytes;
+    int verify, lookahead;
+    int (*fetch)(void *user, int layer, int expert, uint8_t *dst);
+    void *fetch_user;
+    /* the call: n_tokens inputs [n_tokens][hidden] -> out [n_tokens][hidden]
+     * (routed sum plus the shared expert; not the residual), and per token
+     * its top_k ids (route) and weights (rw, may be NULL) in selection
+     * order. moe_ffn_decode takes n_tokens = 1. */
+    int n_tokens;
+    const float *x;
+    float *out;
+    int *route;
+    float *rw;
+} warp_moe_args;
+
+typedef struct {
+    int (*moe_ffn_decode)(const warp_moe_args *a);  /* moe_layer, one token   */
+    int (*moe_ffn_batch)(const warp_moe_args *a);   /* moe_chunk              */
+    int on_device;
+} waste_moe_kernels;
+
+/* Fills both slots with this backend's (when a gfx950 device is present;
+ * otherwise returns NULL and leaves the table), keeping each slot's previous
+ * value: a call this backend declines or fails goes to it with the same
+ * arguments, and with the CPU default (NULL) the slot returns the negative
+ * code and the engine runs its CPU path. Returns "HIP gfx950". The device
+ * state it builds is dropped by waste_hip_release_host_buffers(). No
+ * counterpart in the reference beyond the style of
+ * waste_register_metal (src/waste_backend.h:116-120). */
+const char *waste_register_hip_moe(waste_moe_kernels *t);
+/* Calls of the MoE slots that ran on the device / were declined or failed
+ * (and went to the previous slot or the CPU path). */
+void warp_hip_moe_table_stats(uint64_t *device_calls, uint64_t *fallback_calls);
 
 /* ---- 2. MoE slots ---------------------------------------------------------- */
 
@@ -107,6 +209,13 @@ enum {
     WARP_HIP_E_NOSLOT = -7,    /* cache could not free a slot (REC_E_NOSLOT)   */
     WARP_HIP_E_MISSING = -8,   /* a selected expert is neither resident nor
                                 * fetchable: the layer was not computed       */
+    WARP_HIP_E_BOOKS = -9,     /* a selected record names codebooks other than
+                                * its layer's (its codebook_id is not the
+                                * layer's cb_base): the reference decodes it
+                                * with its own (src/model.c:2889-2907), this
+                                * backend with one set per layer, so the layer
+                                * was not computed and the caller's CPU path
+                                * runs it                                    */
 };
 
 enum { WARP_HIP_ROUTE_SIGMOID = 0, WARP_HIP_ROUTE_SOFTMAX = 1 };
@@ -156,6 +265,11 @@ typedef struct {
                             * top_k x max(hidden, inter) x 2 bytes under 2 GiB
                             * (else chunks stay exact) and allocates that much
                             * at open; VQ4P chunks stay on their int8 tables */
+    int n_books;           /* codebooks in the container (codebooks.bin,
+                            * src/model.c:1274): a record's codebook_id must
+                            * satisfy codebook_id + 3*stages <= n_books, as
+                            * record_check requires (src/model.c:1721-1723);
+                            * 0: n_layers * 3 * stages, one set per layer    */
 } warp_hip_cfg;
 
 typedef struct warp_hip_ctx warp_hip_ctx;

@@ -243,6 +243,10 @@ class Ref:
         L.ref_expert_ffn.argtypes = [vp, i, i, vp, vp]
         L.ref_trunk_matvec.restype = i
         L.ref_trunk_matvec.argtypes = [vp, C.c_char_p, vp, vp, i, i]
+        L.ref_record_check.restype = i
+        L.ref_record_check.argtypes = [vp, i, i, vp, i]
+        L.ref_n_books.restype = i
+        L.ref_n_books.argtypes = [vp]
         self.m = L.ref_open(container_dir.encode(), cache_bytes, n_threads)
         if not self.m:
             raise RuntimeError(f"reference refused {container_dir}")
@@ -297,11 +301,30 @@ class Ref:
     def save_usage(self, path):
         assert self.L.ref_save_usage(self.m, os.fsencode(path)) == 0
 
+    def record_check(self, L, expert, rec, verify):
+        """The reference's record_check on `rec` (uint8, the bank's record
+        stride) as a record of (L, expert): 0 OK, 2 E_HEADER, 3 E_CRC."""
+        rec = np.ascontiguousarray(rec, np.uint8)
+        return self.L.ref_record_check(self.m, L, expert, _p(rec), int(verify))
+
+    def n_books(self):
+        return self.L.ref_n_books(self.m)
+
     def build_lut(self, L, kind, x, n_out):
         x = np.ascontiguousarray(x, np.float32)
         lut = np.empty(n_out, np.float32)
         self.L.ref_build_lut(self.m, L, kind, _p(x), x.shape[0], _p(lut))
         return lut
+
+
+def record_check(rec, layer, expert, fmt, stages, n_books, expert_m, verify):
+    """or_record_check: the oracle's restatement of record_check
+    (src/model.c:1698-1745) on a record of len(rec) bytes. fmt names the
+    container's format (its index width); expert_m = rows of gate, up, down."""
+    rec = np.ascontiguousarray(rec, np.uint8)
+    bits = {"VQ3R": 8, "VQ2R": 8, "VQ4P": 6, "VQ12": 12}[fmt]
+    m = np.ascontiguousarray(expert_m, np.int32)
+    return lib().or_record_check(_p(rec), rec.size, layer, expert, bits, stages, n_books, _p(m), int(verify))
 
 
 def kda_forward(q, k, v, g, beta, S):

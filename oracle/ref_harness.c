@@ -146,3 +146,19 @@ void ref_pool_reset(void) { waste_pool_shutdown(); }
 /* The reference's usage file of its expert cache (waste_model_save_usage,
  * src/model.c:2991-2995). */
 int ref_save_usage(void *p, const char *path) { return waste_model_save_usage((waste_model *)p, path); }
+
+/* The reference's record_check (src/model.c:1698-1745) on a record of layer
+ * L's bank, with its checksum switch (m->verify) set to `verify` for the
+ * call. Returns its rec_status: 0 OK, 2 E_HEADER, 3 E_CRC. */
+int ref_record_check(void *p, int L, int expert, const uint8_t *rec, int verify)
+{
+    waste_model *m = (waste_model *)p;
+    const int keep = m->verify;
+    m->verify = verify;
+    const int st = (int)record_check(m, L, expert, rec);
+    m->verify = keep;
+    return st;
+}
+
+/* The container's codebook count (src/model.c:1274). */
+int ref_n_books(void *p) { return ((waste_model *)p)->n_books; }

@@ -50,14 +50,16 @@ def build(verbose: bool = True) -> str:
     n_obj = os.path.join(BUILD, "noalloc.o")
     c_obj = os.path.join(BUILD, "crc.o")
     d_obj = os.path.join(BUILD, "kda.o")
+    m_obj = os.path.join(BUILD, "moe_table.o")
     _run([hipcc, *HIP_FLAGS, *inc, "-c", os.path.join(CSRC, "kernels.hip"), "-o", k_obj])
     _run([hipcc, *HIP_FLAGS, *inc, "-c", os.path.join(CSRC, "noalloc.hip"), "-o", n_obj])
     _run([hipcc, *HIP_FLAGS, *inc, "-c", os.path.join(CSRC, "crc.hip"), "-o", c_obj])
     _run([hipcc, *HIP_FLAGS, *inc, "-c", os.path.join(CSRC, "kda.hip"), "-o", d_obj])
     _run(["gcc", *C_FLAGS, *inc, "-c", os.path.join(CSRC, "backend.c"), "-o", b_obj])
     _run(["gcc", *C_FLAGS, *inc, "-c", os.path.join(CSRC, "encode.c"), "-o", e_obj])
+    _run(["gcc", *C_FLAGS, *inc, "-c", os.path.join(CSRC, "moe_table.c"), "-o", m_obj])
     tmp = LIB + ".tmp"
-    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, k_obj, n_obj, c_obj, d_obj, b_obj, e_obj,
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, k_obj, n_obj, c_obj, d_obj, b_obj, e_obj, m_obj,
           f"-L{ROCM}/lib", "-lamdhip64", "-lpthread", f"-Wl,-rpath,{ROCM}/lib",
           "-Wl,--no-undefined"])
     os.replace(tmp, LIB)

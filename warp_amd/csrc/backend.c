@@ -83,6 +83,8 @@ typedef void (*kda_fn)(int, int, int, const float *, const float *, const float 
 static kda_fn g_prev_kda;
 static float *g_kda_buf;
 static size_t g_kda_cap;
+static float *g_kda_stage;        /* pinned: the stepped state and output before they are committed */
+static size_t g_kda_stage_cap;
 static uint64_t g_kda_calls, g_kda_fallbacks;
 static mirror_t *g_mirrors;
 static int g_n_mirrors, g_cap_mirrors;
@@ -161,7 +163,10 @@ static void hip_mvq_rows_f32(int b, int e, void *p)
 
 /* The kda_step slot (src/waste_backend.h:69-72): host pointers, so the
  * inputs and the state go to the device and the state and output come back
- * on every call; one block per head does the step (wk_kda). */
+ * on every call; one block per head does the step (wk_kda). The results
+ * land in a pinned staging buffer and reach the caller's S and o only once
+ * the stream has completed, so a failure leaves S as it was and the CPU
+ * fallback steps it exactly once. */
 static int kda_on_device(int H, int K, int V, const float *q, const float *k, const float *v, const float *g,
                          const float *beta, float *S, float *o)
 {
@@ -182,10 +187,20 @@ static int kda_on_device(int H, int K, int V, const float *q, const float *k, co
         if (!HIPOK(hipMemcpyAsync(in[i].d, in[i].h, in[i].n * sizeof(float), hipMemcpyHostToDevice, g_tab_stream)))
             return -1;
     if (wk_kda(1, H, K, V, dq, dk, dv, dg, db, dS, dob, g_tab_stream)) return -1;
-    if (!HIPOK(hipMemcpyAsync(S, dS, ns * sizeof(float), hipMemcpyDeviceToHost, g_tab_stream)) ||
-        !HIPOK(hipMemcpyAsync(o, dob, hv * sizeof(float), hipMemcpyDeviceToHost, g_tab_stream)))
+    if (g_kda_stage_cap < ns + hv) {
+        if (g_kda_stage) (void)hipHostFree(g_kda_stage);
+        g_kda_stage = NULL;
+        g_kda_stage_cap = 0;
+        if (!HIPOK(hipHostMalloc((void **)&g_kda_stage, (ns + hv) * sizeof(float), 0))) return -1;
+        g_kda_stage_cap = ns + hv;
+    }
+    if (!HIPOK(hipMemcpyAsync(g_kda_stage, dS, ns * sizeof(float), hipMemcpyDeviceToHost, g_tab_stream)) ||
+        !HIPOK(hipMemcpyAsync(g_kda_stage + ns, dob, hv * sizeof(float), hipMemcpyDeviceToHost, g_tab_stream)) ||
+        !HIPOK(hipStreamSynchronize(g_tab_stream)))
         return -1;
-    return HIPOK(hipStreamSynchronize(g_tab_stream)) ? 0 : -1;
+    memcpy(S, g_kda_stage, ns * sizeof(float));
+    memcpy(o, g_kda_stage + ns, hv * sizeof(float));
+    return 0;
 }
 
 static void hip_kda_step(int H, int K, int V, const float *q, const float *k, const float *v, const float *g_log,
@@ -226,6 +241,7 @@ void waste_hip_release_host_buffers(void)
     for (int i = 0; i < g_n_mirrors; i++) (void)hipFree(g_mirrors[i].dev);
     g_n_mirrors = 0;
     pthread_mutex_unlock(&g_tab_mu);
+    warp_moe_release();
 }
 
 void warp_hip_table_stats(uint64_t *device_calls, uint64_t *fallback_calls)
@@ -294,6 +310,9 @@ struct warp_hip_ctx {
     int n_slots, next_free;
     size_t slot_stride;         /* bytes between slots (see slot_rec)       */
     int *slot_key, *key_slot;
+    uint16_t *rec_cb;           /* [layer][expert]: the codebook_id of the
+                                 * record the key last placed             */
+    int n_books;                /* cfg.n_books, or n_layers * 3 * stages  */
     uint32_t *hits;
     uint64_t *last, clock;
     unsigned rng;
@@ -524,10 +543,12 @@ static int ctx_alloc(warp_hip_ctx *c)
     c->slot_key = (int *)malloc(((size_t)c->n_slots + 1) * sizeof(int));
     c->hits = (uint32_t *)calloc((size_t)c->n_slots + 1, sizeof(uint32_t));
     c->pin_gen = (uint32_t *)calloc(nkeys, sizeof(uint32_t));
+    c->rec_cb = (uint16_t *)calloc(nkeys, sizeof(uint16_t));
     c->la_votes = (int *)calloc((size_t)E, sizeof(int));
     c->la_order = (int *)calloc((size_t)E, sizeof(int));
     c->last = (uint64_t *)calloc((size_t)c->n_slots + 1, sizeof(uint64_t));
-    if (!c->key_slot || !c->slot_key || !c->hits || !c->last || !c->pin_gen || !c->la_votes || !c->la_order)
+    if (!c->key_slot || !c->slot_key || !c->hits || !c->last || !c->pin_gen || !c->rec_cb || !c->la_votes ||
+        !c->la_order)
         return set_err(c, WARP_HIP_E_NOMEM, -1, -1, "host allocation failed");
     for (size_t i = 0; i < nkeys; i++) c->key_slot[i] = -1;
     for (int i = 0; i < c->n_slots; i++) c->slot_key[i] = -1;
@@ -575,10 +596,11 @@ int warp_hip_open(const warp_hip_cfg *cfg, warp_hip_ctx **out)
     if (!c->S || g->hidden <= 0 || g->inter <= 0 || g->n_experts <= 0 || g->top_k <= 0 ||
         g->top_k > WARP_MAX_K || g->top_k > g->n_experts || g->n_layers <= 0 || g->n_layers > 65535 ||
         g->n_experts > 65535 || (g->rec_bytes % 4096) != 0 || g->lookahead < 0 || g->latent < 0 ||
-        (g->latent && g->latent_norm && !(g->norm_eps > 0.0f))) {
+        (g->latent && g->latent_norm && !(g->norm_eps > 0.0f)) || g->n_books < 0) {
         set_err(c, rc, -1, -1, "configuration out of range");
         goto fail;
     }
+    c->n_books = g->n_books > 0 ? g->n_books : g->n_layers * 3 * c->S;
     if (!c->P6 && (He % 32 || g->inter % 32 || g->hidden % 32)) {
         set_err(c, rc, -1, -1, "hidden, latent and inter must be multiples of 32 (4 vector positions)");
         goto fail;
@@ -677,7 +699,7 @@ void warp_hip_close(warp_hip_ctx *c)
     hhfree(c->h_crc_err); hhfree(c->h_word);
     for (int i = 0; i < N_TQ; i++) hhfree(c->tq_host[i]);
     free(c->tq_pos);
-    free(c->key_slot); free(c->slot_key); free(c->hits); free(c->last); free(c->pin_gen);
+    free(c->key_slot); free(c->slot_key); free(c->hits); free(c->last); free(c->pin_gen); free(c->rec_cb);
     free(c->la_votes); free(c->la_order);
     if (c->tev) {
         for (int i = 0; i < 2 * WARP_TIMING_N; i++) if (c->tev[i]) (void)hipEventDestroy(c->tev[i]);
@@ -768,6 +790,11 @@ int warp_hip_set_codebooks(warp_hip_ctx *c, int layer, int cb_base, const uint16
 {
     int rc = check_layer(c, layer);
     if (rc) return rc;
+    /* the bank's codebook_base, bounded as the loader bounds it
+     * (src/model.c:1341-1343) */
+    if (!books || cb_base < 0 || cb_base > c->n_books - 3 * c->S)
+        return set_err(c, WARP_HIP_E_ARG, layer, -1, "codebook base %d with %d books of %d stages", cb_base,
+                       c->n_books, c->S);
     const size_t n = (size_t)3 * c->S * c->En * 8;
     uint16_t *tmp = (uint16_t *)malloc(n * sizeof(uint16_t));
     if (!tmp) return set_err(c, WARP_HIP_E_NOMEM, layer, -1, "host allocation failed");
@@ -903,13 +930,16 @@ int warp_hip_set_shared(warp_hip_ctx *c, int layer, int bits, int group, int int
 
 /* ---- expert cache ----------------------------------------------------------------------- */
 
-/* record_check (src/model.c:1698-1745), plus the offsets the kernels index
- * with: every index block at least as long as its shape needs, the scales
- * after them, all inside the record, so no kernel read leaves the slot. */
+/* record_check (src/model.c:1698-1745), its conditions in its order, then
+ * one more that the kernels need: every index block at least as long as its
+ * shape, and the scales after them (the reference accepts any increasing
+ * offsets, and a short block then reads into the next one; here a kernel
+ * would read past what the header describes). The payload checksum is taken
+ * on the device (publish_slot), the codebook_id kept per key (rec_cb). */
 static int check_record(warp_hip_ctx *c, const uint8_t *rec, int layer, int expert)
 {
     const warp_hip_cfg *g = &c->cfg;
-    uint32_t magic, blocks, off[4], crc;
+    uint32_t magic, blocks, off[4];
     uint16_t lay, eid, cbid, lowrank;
     uint8_t fmt;
     memcpy(&magic, rec + 0, 4);
@@ -920,21 +950,88 @@ static int check_record(warp_hip_ctx *c, const uint8_t *rec, int layer, int expe
     memcpy(&lowrank, rec + 12, 2);
     memcpy(&blocks, rec + 16, 4);
     memcpy(off, rec + 20, 16);
-    memcpy(&crc, rec + 36, 4);
-    if (magic != 0x50584557u || lay != (uint16_t)layer || eid != (uint16_t)expert ||
-        (size_t)blocks * 4096u != g->rec_bytes || lowrank != 0)
-        return set_err(c, WARP_HIP_E_HEADER, layer, expert, "record header: magic/identity/size");
-    if (fmt != g->fmt) return set_err(c, WARP_HIP_E_HEADER, layer, expert, "record fmt %d, context fmt %d", fmt, g->fmt);
-    if (c->L[layer].has_books && cbid != (uint16_t)c->L[layer].cb_base)
-        return set_err(c, WARP_HIP_E_HEADER, layer, expert, "record codebook_id %u, layer base %d", cbid,
-                       c->L[layer].cb_base);
+    if (g->rec_bytes < WARP_HDR_BYTES || magic != 0x50584557u)
+        return set_err(c, WARP_HIP_E_HEADER, layer, expert, "record header: magic");
+    if (lay != (uint16_t)layer || eid != (uint16_t)expert)
+        return set_err(c, WARP_HIP_E_HEADER, layer, expert, "record header names layer %u expert %u", lay, eid);
+    if ((size_t)blocks * 4096u != g->rec_bytes)
+        return set_err(c, WARP_HIP_E_HEADER, layer, expert, "record of %u 4 KiB blocks, stride %zu", blocks,
+                       g->rec_bytes);
+    /* the label must be the one the container's index width implies; byte
+     * codes also take the 2-stage label (the stage count is the
+     * container's, not the record's) */
+    const int bits8 = g->fmt == WARP_HIP_VQ3R || g->fmt == WARP_HIP_VQ2R;
+    const int want = g->fmt == WARP_HIP_VQ4P ? WARP_HIP_VQ4P : g->fmt == WARP_HIP_VQ12 ? WARP_HIP_VQ12
+                                                                                        : WARP_HIP_VQ3R;
+    if (fmt != want && !(bits8 && fmt == WARP_HIP_VQ2R))
+        return set_err(c, WARP_HIP_E_HEADER, layer, expert, "record fmt %d in a container of fmt %d", fmt, g->fmt);
+    if (lowrank != 0) return set_err(c, WARP_HIP_E_HEADER, layer, expert, "record lowrank_id %u", lowrank);
+    if ((long)cbid + 3L * c->S > c->n_books)
+        return set_err(c, WARP_HIP_E_HEADER, layer, expert, "record codebook_id %u with %d books", cbid,
+                       c->n_books);
+    if (!(off[0] == WARP_HDR_BYTES && off[0] < off[1] && off[1] < off[2] && off[2] < off[3] &&
+          off[3] <= g->rec_bytes))
+        return set_err(c, WARP_HIP_E_HEADER, layer, expert, "record offsets out of order");
     const size_t scales = 2u * (2 * (size_t)g->inter + c->He);
-    if (!(off[0] == WARP_HDR_BYTES && (size_t)off[0] + c->gate_bytes <= off[1] &&
-          (size_t)off[1] + c->gate_bytes <= off[2] && (size_t)off[2] + c->down_bytes <= off[3] &&
-          (size_t)off[3] + scales <= g->rec_bytes))
-        return set_err(c, WARP_HIP_E_HEADER, layer, expert, "record offsets do not fit the shape");
-    (void)crc;                       /* the payload checksum is taken on the device (verify_slot) */
+    if (scales > g->rec_bytes - off[3])
+        return set_err(c, WARP_HIP_E_HEADER, layer, expert, "record scales past its end");
+    if (!((size_t)off[0] + c->gate_bytes <= off[1] && (size_t)off[1] + c->gate_bytes <= off[2] &&
+          (size_t)off[2] + c->down_bytes <= off[3]))
+        return set_err(c, WARP_HIP_E_HEADER, layer, expert, "record index blocks shorter than the shape");
     return 0;
+}
+
+/* A key whose resident record names codebooks other than its layer's. */
+static int key_foreign(const warp_hip_ctx *c, int key)
+{
+    const layer_t *L = &c->L[key / c->cfg.n_experts];
+    return c->key_slot[key] >= 0 && c->rec_cb[key] != (uint16_t)L->cb_base;
+}
+
+/* Any resident record of `layer` whose codebook_id is not the layer's. */
+static int layer_foreign(const warp_hip_ctx *c, int layer)
+{
+    const int E = c->cfg.n_experts;
+    if (c->L[layer].resident == 0) return 0;
+    for (int e = 0; e < E; e++)
+        if (key_foreign(c, layer * E + e)) return 1;
+    return 0;
+}
+
+/* The codebooks the resident records `ids` of `layer` decode with. The
+ * reference builds the gate/up tables from the first selected record's
+ * codebook_id and each down table from the record's own (src/model.c:
+ * 2886-2907, 3612-3653). When every record of the selection names the same
+ * id, that is one set: the codebooks given to the layer whose cb_base it is
+ * (normally `layer` itself). Mixed ids, an id no layer has codebooks for, or
+ * a set that would change the kernel choice (exponent-31 values) give
+ * E_BOOKS, and the caller's CPU path runs the layer. */
+static const layer_t *books_by_id(const warp_hip_ctx *c, const layer_t *L, int cb)
+{
+    if (cb == L->cb_base) return L;
+    for (int l = 0; l < c->cfg.n_layers; l++)
+        if (c->L[l].has_books && c->L[l].cb_base == cb && c->L[l].books_x31 == L->books_x31) return &c->L[l];
+    return NULL;
+}
+
+static int books_of(warp_hip_ctx *c, int layer, const int *ids, int n, const layer_t **B)
+{
+    const int E = c->cfg.n_experts;
+    const layer_t *L = &c->L[layer];
+    int cb = -1, bad = -1;
+    for (int j = 0; j < n && bad < 0; j++) {
+        if (ids[j] < 0 || ids[j] >= E || c->key_slot[layer * E + ids[j]] < 0) continue;
+        const int id = c->rec_cb[layer * E + ids[j]];
+        if (cb < 0) cb = id;
+        else if (id != cb) bad = ids[j];
+    }
+    *B = L;
+    if (bad < 0 && cb < 0) return 0;
+    if (bad < 0 && (*B = books_by_id(c, L, cb)) != NULL) return 0;
+    if (bad < 0) bad = ids[0];
+    *B = L;
+    return set_err(c, WARP_HIP_E_BOOKS, layer, bad, "selected records name codebook_id %u; layer codebook base %d",
+                   c->rec_cb[layer * E + bad], L->cb_base);
 }
 
 static int is_pinned(const warp_hip_ctx *c, int key)
@@ -1062,6 +1159,7 @@ static int publish_slot(warp_hip_ctx *c, int layer, int expert, int s, const uin
     uint32_t off[4];
     memcpy(off, hdr + WARP_HDR_GATE_OFF, sizeof off);
     const int key = layer * c->cfg.n_experts + expert;
+    memcpy(&c->rec_cb[key], hdr + 10, sizeof c->rec_cb[key]);
     const uint8_t *slot = slot_rec(c, s);
     if (c->cfg.verify) {
         const size_t scales = 2u * (2 * (size_t)c->cfg.inter + c->He);
@@ -1074,21 +1172,38 @@ static int publish_slot(warp_hip_ctx *c, int layer, int expert, int s, const uin
 
 /* Waits for the copy stream and reports the records whose device checksum
  * failed since the last report: their slots are freed and the call fails
- * with E_CRC naming the first of them. */
+ * with E_CRC naming the first of them. Updates still queued are applied
+ * first, so every checked fill has had its verdict. The device lists the
+ * first WARP_CRC_ERR_KEYS refused keys; past that, the per-key verdicts
+ * (crc_bad: 1 exactly where a key's last table update was a refusal) are
+ * read back whole, so no refused key stays claimed on the host. */
 static int crc_report(warp_hip_ctx *c)
 {
     if (!c->crc_pending) return 0;
+    int rc = flush_table(c);
+    if (rc) return rc;
     DEV(c, hipMemcpyAsync(c->h_crc_err, c->crc_err, sizeof *c->h_crc_err, hipMemcpyDeviceToHost, c->cp));
     DEV(c, hipStreamSynchronize(c->cp));
     c->crc_pending = 0;
     const int n = c->h_crc_err->n;
     if (n == 0) return 0;
-    const int nk = n < WARP_CRC_ERR_KEYS ? n : WARP_CRC_ERR_KEYS;
-    for (int i = 0; i < nk; i++) unclaim(c, c->h_crc_err->keys[i]);
+    int first = c->h_crc_err->keys[0];
+    if (n <= WARP_CRC_ERR_KEYS) {
+        for (int i = 0; i < n; i++) unclaim(c, c->h_crc_err->keys[i]);
+    } else {
+        const size_t nkeys = (size_t)c->cfg.n_layers * c->cfg.n_experts;
+        int8_t *bad = (int8_t *)malloc(nkeys);
+        if (!bad) return set_err(c, WARP_HIP_E_NOMEM, -1, -1, "host allocation failed");
+        hipError_t e = hipMemcpy(bad, c->crc_bad, nkeys, hipMemcpyDeviceToHost);
+        if (e != hipSuccess) { free(bad); return dev_err(c, "crc verdicts", e); }
+        for (size_t k = 0; k < nkeys; k++)
+            if (bad[k] && c->key_slot[k] >= 0) unclaim(c, (int)k);
+        free(bad);
+    }
     DEV(c, hipMemsetAsync(c->crc_err, 0, sizeof c->crc_err->n, c->cp));
     DEV(c, hipStreamSynchronize(c->cp));
-    const int E = c->cfg.n_experts, k0 = c->h_crc_err->keys[0];
-    return set_err(c, WARP_HIP_E_CRC, k0 / E, k0 % E, "record payload checksum (%d record%s refused)", n,
+    const int E = c->cfg.n_experts;
+    return set_err(c, WARP_HIP_E_CRC, first / E, first % E, "record payload checksum (%d record%s refused)", n,
                    n > 1 ? "s" : "");
 }
 
@@ -1173,6 +1288,7 @@ int warp_hip_put_expert_synth(warp_hip_ctx *c, int layer, int expert, uint64_t s
     DEV(c, hipMemcpyAsync(slot + off[3], scales, 2 * (2 * (size_t)g->inter + c->He), hipMemcpyHostToDevice, c->cp));
     DEV(c, hipStreamSynchronize(c->cp));
     /* a synthetic record carries no checksum: never verified */
+    c->rec_cb[key] = cb;
     if ((rc = queue_slot(c, key, slot, off, 0))) return rc;
     return flush_table(c);
 }
@@ -1605,7 +1721,14 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
         return set_err(c, WARP_HIP_E_ARG, layer, -1, "layer %d has no codebooks or router", layer);
     const warp_slot *table = c->table_dev + (size_t)layer * E;
     if ((rc = x31_check(c, L, layer))) return rc;
+    /* fills since the last report that the device refused leave the cache
+     * now, before this layer reads the table */
+    if (c->crc_pending && (rc = crc_report(c))) return rc;
     const int use_lut = use_table(c, L);
+    /* a resident record naming other codebooks than the layer's: the
+     * selection goes through the host, which picks the codebooks */
+    const int foreign = layer_foreign(c, layer);
+    const layer_t *B = L;
     /* the latent MoE: the experts see xe = down . x and return into the
      * latent width He; routing and the shared expert stay on x */
     const int lat = g->latent > 0, He = c->He;
@@ -1632,7 +1755,8 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
     const int fuse_shared = use_lut && !lat && shared_args(c, L, &sa) && wk_shared_fast_ok(H, &sa);
     /* where the device routes with the expert table, the table kernel's
      * gate/up launch does the routing itself (one launch less) */
-    const int fuse_route = use_lut && (L->resident == E || !can_fetch(c)) && wk_lut_route_ok(g->fmt, E, K, 1, 0, 2);
+    const int fuse_route = use_lut && !foreign && (L->resident == E || !can_fetch(c)) &&
+                           wk_lut_route_ok(g->fmt, E, K, 1, 0, 2);
     /* and where that launch leaves CUs idle, one more row of its blocks
      * computes the shared expert's gate/up rows (one row per wave) instead
      * of the router launch, and blocks appended to the down launch its down
@@ -1656,7 +1780,7 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
     if ((rc = timing_end(c))) return rc;
     const int n_la = lookahead_launch(c, layer, x_dev, 1);
     if (n_la < 0) return n_la;
-    if (L->resident == E) {
+    if (L->resident == E && !foreign) {
         /* everything resident: route and build the jobs on the device, no
          * host round trip */
         KRN(c, wait_copies(c));
@@ -1665,7 +1789,7 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
                             table, c->jobs, c->njobs, c->missing, I, c->st));
         c->stats.hits += (uint64_t)K;
         release_hold(c, layer);
-    } else if (!can_fetch(c)) {
+    } else if (!can_fetch(c) && !foreign) {
         /* nothing to fetch with: the device flags a selected expert that is
          * not resident (sticky), the combine poisons this layer's output with
          * NaN, and the next synchronising call reports E_MISSING */
@@ -1681,6 +1805,13 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
         DEV(c, hipMemcpyAsync(c->h_idx, c->idx, (size_t)K * sizeof(int), hipMemcpyDeviceToHost, c->st));
         DEV(c, hipStreamSynchronize(c->st));
         if ((rc = ensure_selected(c, layer, c->h_idx, K))) return rc;
+        if ((rc = books_of(c, layer, c->h_idx, K, &B))) return rc;
+        if (B != L && c->P6 && !use_lut) {
+            /* the gate/up tables again, from the selection's codebooks */
+            const size_t nvH = (size_t)He / 8, nblkH = (nvH + WARP_LUT_BLK - 1) / WARP_LUT_BLK;
+            KRN(c, wk_lut_p6(xe, 1, He, books_kind(c, B, 0), c->lut8, c->lscale, c->st));
+            KRN(c, wk_lut_p6(xe, 1, He, books_kind(c, B, 1), c->lut8 + nvH * 256, c->lscale + nblkH, c->st));
+        }
         KRN(c, wait_copies(c));
         KRN(c, wk_route(c->logits, L->bias, E, K, 1, g->router_act, g->renorm, g->routed_scale, c->idx, c->w, table,
                         c->jobs, c->njobs, c->missing, I, c->st));
@@ -1697,7 +1828,7 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
         const warp_route_args ra = { c->logits, L->bias, table, E, g->router_act, g->renorm, I, g->routed_scale,
                                      c->idx, c->w, c->jobs, c->njobs, c->missing, scored };
         if ((rc = timing_begin(c, 0))) return rc;
-        KRN(c, wk_moe_fused(g->fmt, L->books, L->books_x31, xe, K, I, He, c->part, c->part_cap, c->n_cu,
+        KRN(c, wk_moe_fused(g->fmt, B->books, B->books_x31, xe, K, I, He, c->part, c->part_cap, c->n_cu,
                             g->act_situ, g->situ_beta, g->situ_linear_beta, &ra, add0, add1, ysum, c->fz_sync,
                             WARP_FZ_WORDS, c->st));
         if ((rc = timing_end(c))) return rc;
@@ -1714,7 +1845,7 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
         const warp_route_args ra = { c->logits, L->bias, table, E, g->router_act, g->renorm, I, g->routed_scale,
                                      c->idx, c->w, c->jobs, c->njobs, c->missing, scored };
         if ((rc = timing_begin(c, 0))) return rc;
-        KRN(c, wk_vq_lut(g->fmt, c->jobs, c->njobs, K, 0, 2, L->books, L->books_x31, xe, 1, c->part, c->part_cap, I, He,
+        KRN(c, wk_vq_lut(g->fmt, c->jobs, c->njobs, K, 0, 2, B->books, B->books_x31, xe, 1, c->part, c->part_cap, I, He,
                          c->n_cu, NULL, 0, 0, 0.0f, 0.0f, fuse_route ? &ra : NULL, sh_in_gu ? &sa : NULL, NULL, &sp_gu,
                          c->st));
         if ((rc = timing_end(c))) return rc;
@@ -1722,7 +1853,7 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
          * in its prologue); its partials go after the gate/up ones */
         const size_t gu_floats = (size_t)2 * sp_gu * K * (((size_t)I + 63) / 64) * 64;
         if ((rc = timing_begin(c, 1))) return rc;
-        KRN(c, wk_vq_lut(g->fmt, c->jobs, c->njobs, K, 2, 1, L->books, L->books_x31, NULL, 0, c->part + gu_floats,
+        KRN(c, wk_vq_lut(g->fmt, c->jobs, c->njobs, K, 2, 1, B->books, B->books_x31, NULL, 0, c->part + gu_floats,
                          c->part_cap - gu_floats, He, I, c->n_cu, c->part, sp_gu, g->act_situ, g->situ_beta,
                          g->situ_linear_beta, NULL, sh_in_gu ? &sa : NULL, sh_in_gu ? c->sho : NULL, &sp_d,
                          c->st));
@@ -1733,16 +1864,16 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
         KRN(c, wk_apply_p6(c->jobs, c->njobs, K, 0, c->lut8, c->lscale, c->yg, I, He, c->st));
         KRN(c, wk_apply_p6(c->jobs, c->njobs, K, 1, c->lut8 + nvH * 256, c->lscale + nblkH, c->yu, I, He, c->st));
         KRN(c, wk_act(c->yg, c->yu, K, I, g->act_situ, g->situ_beta, g->situ_linear_beta, c->hbuf, c->st));
-        KRN(c, wk_lut_p6(c->hbuf, K, I, books_kind(c, L, 2), c->lut8d, c->lscaled, c->st));
+        KRN(c, wk_lut_p6(c->hbuf, K, I, books_kind(c, B, 2), c->lut8d, c->lscaled, c->st));
         KRN(c, wk_apply_p6(c->jobs, c->njobs, K, 2, c->lut8d, c->lscaled, c->yd, He, I, c->st));
     } else {
         if ((rc = timing_begin(c, 0))) return rc;
-        KRN(c, wk_vq_matvec(g->fmt, c->jobs, c->njobs, K, 0, 2, L->books, c->xs, c->xscale, yk, I, He, 1, c->st));
+        KRN(c, wk_vq_matvec(g->fmt, c->jobs, c->njobs, K, 0, 2, B->books, c->xs, c->xscale, yk, I, He, 1, c->st));
         if ((rc = timing_end(c))) return rc;
         KRN(c, wk_act_split(c->yg, c->yu, K, I, g->act_situ, g->situ_beta, g->situ_linear_beta, c->xsh, c->xscaleh,
                             NULL, c->st));
         if ((rc = timing_begin(c, 1))) return rc;
-        KRN(c, wk_vq_matvec(g->fmt, c->jobs, c->njobs, K, 2, 1, L->books, c->xsh, c->xscaleh, yk, He, I, 1, c->st));
+        KRN(c, wk_vq_matvec(g->fmt, c->jobs, c->njobs, K, 2, 1, B->books, c->xsh, c->xscaleh, yk, He, I, 1, c->st));
         if ((rc = timing_end(c))) return rc;
     }
     if (L->sq[0] && !fuse_shared && (rc = shared_ffn(c, L, x_dev, 1, c->st))) return rc;
@@ -1780,21 +1911,24 @@ int warp_hip_expert_ffn(warp_hip_ctx *c, int layer, int expert, const float *x_d
     if (!L->has_books) return set_err(c, WARP_HIP_E_ARG, layer, -1, "layer %d has no codebooks", layer);
     if (c->key_slot[layer * g->n_experts + expert] < 0)
         return set_err(c, WARP_HIP_E_MISSING, layer, expert, "expert not resident");
+    /* the record's own codebook_id names its codebooks (src/model.c:2889-2907) */
+    const layer_t *B;
+    if ((rc = books_of(c, layer, &expert, 1, &B))) return rc;
     /* the record's table entry may still be on its way (copy stream) */
     KRN(c, wait_copies(c));
     KRN(c, wk_expert_jobs(c->table_dev + (size_t)layer * g->n_experts + expert, I, c->jobs, c->njobs, c->w,
                           c->missing, c->st));
     c->missing_pending = 1;
-    if ((rc = x31_check(c, L, layer))) return rc;
-    if (use_table(c, L)) {
+    if ((rc = x31_check(c, B, layer))) return rc;
+    if (use_table(c, B)) {
         int sp_gu = 0, sp_d = 0;
         if ((rc = timing_begin(c, 0))) return rc;
-        KRN(c, wk_vq_lut(g->fmt, c->jobs, c->njobs, 1, 0, 2, L->books, L->books_x31, x_dev, 1, c->part, c->part_cap,
+        KRN(c, wk_vq_lut(g->fmt, c->jobs, c->njobs, 1, 0, 2, B->books, B->books_x31, x_dev, 1, c->part, c->part_cap,
                          I, H, c->n_cu, NULL, 0, 0, 0.0f, 0.0f, NULL, NULL, NULL, &sp_gu, c->st));
         if ((rc = timing_end(c))) return rc;
         const size_t gu_floats = (size_t)2 * sp_gu * (((size_t)I + 63) / 64) * 64;
         if ((rc = timing_begin(c, 1))) return rc;
-        KRN(c, wk_vq_lut(g->fmt, c->jobs, c->njobs, 1, 2, 1, L->books, L->books_x31, NULL, 0, c->part + gu_floats,
+        KRN(c, wk_vq_lut(g->fmt, c->jobs, c->njobs, 1, 2, 1, B->books, B->books_x31, NULL, 0, c->part + gu_floats,
                          c->part_cap - gu_floats, H, I, c->n_cu, c->part, sp_gu, g->act_situ, g->situ_beta,
                          g->situ_linear_beta, NULL, NULL, NULL, &sp_d, c->st));
         if ((rc = timing_end(c))) return rc;
@@ -1805,20 +1939,20 @@ int warp_hip_expert_ffn(warp_hip_ctx *c, int layer, int expert, const float *x_d
     float *yk[3] = { c->yg, c->yu, out_dev };
     if (c->P6) {
         const size_t nvH = (size_t)H / 8, nblkH = (nvH + WARP_LUT_BLK - 1) / WARP_LUT_BLK;
-        KRN(c, wk_lut_p6(x_dev, 1, H, books_kind(c, L, 0), c->lut8, c->lscale, c->st));
-        KRN(c, wk_lut_p6(x_dev, 1, H, books_kind(c, L, 1), c->lut8 + nvH * 256, c->lscale + nblkH, c->st));
+        KRN(c, wk_lut_p6(x_dev, 1, H, books_kind(c, B, 0), c->lut8, c->lscale, c->st));
+        KRN(c, wk_lut_p6(x_dev, 1, H, books_kind(c, B, 1), c->lut8 + nvH * 256, c->lscale + nblkH, c->st));
         KRN(c, wk_apply_p6(c->jobs, c->njobs, 1, 0, c->lut8, c->lscale, c->yg, I, H, c->st));
         KRN(c, wk_apply_p6(c->jobs, c->njobs, 1, 1, c->lut8 + nvH * 256, c->lscale + nblkH, c->yu, I, H, c->st));
         KRN(c, wk_act(c->yg, c->yu, 1, I, g->act_situ, g->situ_beta, g->situ_linear_beta, c->hbuf, c->st));
-        KRN(c, wk_lut_p6(c->hbuf, 1, I, books_kind(c, L, 2), c->lut8d, c->lscaled, c->st));
+        KRN(c, wk_lut_p6(c->hbuf, 1, I, books_kind(c, B, 2), c->lut8d, c->lscaled, c->st));
         KRN(c, wk_apply_p6(c->jobs, c->njobs, 1, 2, c->lut8d, c->lscaled, out_dev, H, I, c->st));
         return 0;
     }
     KRN(c, wk_split(x_dev, 1, H, c->xs, c->xscale, c->st));
-    KRN(c, wk_vq_matvec(g->fmt, c->jobs, c->njobs, 1, 0, 2, L->books, c->xs, c->xscale, yk, I, H, 1, c->st));
+    KRN(c, wk_vq_matvec(g->fmt, c->jobs, c->njobs, 1, 0, 2, B->books, c->xs, c->xscale, yk, I, H, 1, c->st));
     KRN(c, wk_act_split(c->yg, c->yu, 1, I, g->act_situ, g->situ_beta, g->situ_linear_beta, c->xsh, c->xscaleh, NULL,
                         c->st));
-    KRN(c, wk_vq_matvec(g->fmt, c->jobs, c->njobs, 1, 2, 1, L->books, c->xsh, c->xscaleh, yk, H, I, 1, c->st));
+    KRN(c, wk_vq_matvec(g->fmt, c->jobs, c->njobs, 1, 2, 1, B->books, c->xsh, c->xscaleh, yk, H, I, 1, c->st));
     return 0;
 }
 
@@ -1837,10 +1971,10 @@ int warp_hip_moe_decode_host(warp_hip_ctx *c, int layer, const float *x, float *
 /* The routed experts of a chunk whose experts e_lo..e_hi (in the windowed
  * case, the window's) are resident and held: grouping, then the matvecs of
  * their pairs into the pair rows of yd. */
-static int chunk_experts(warp_hip_ctx *c, int layer, const float *X_dev, int T, int e_lo, int e_hi, int first)
+static int chunk_experts(warp_hip_ctx *c, int layer, const layer_t *B, const float *X_dev, int T, int e_lo, int e_hi,
+                         int first)
 {
     const warp_hip_cfg *g = &c->cfg;
-    const layer_t *L = &c->L[layer];
     const int E = g->n_experts, K = g->top_k, H = c->He, I = g->inter, P = T * K; /* H: the experts' width */
     const warp_slot *table = c->table_dev + (size_t)layer * E;
     KRN(c, wait_copies(c));
@@ -1853,15 +1987,15 @@ static int chunk_experts(warp_hip_ctx *c, int layer, const float *X_dev, int T, 
         const size_t nvH = (size_t)H / 8, nblkH = (nvH + WARP_LUT_BLK - 1) / WARP_LUT_BLK;
         if (first) {
             /* per token: gate LUT at [t][0], up LUT at [t][1] */
-            KRN(c, wk_lut_p6(X_dev, T, H, books_kind(c, L, 0), c->lut8, c->lscale, c->st));
-            KRN(c, wk_lut_p6(X_dev, T, H, books_kind(c, L, 1), c->lut8 + (size_t)T * nvH * 256,
+            KRN(c, wk_lut_p6(X_dev, T, H, books_kind(c, B, 0), c->lut8, c->lscale, c->st));
+            KRN(c, wk_lut_p6(X_dev, T, H, books_kind(c, B, 1), c->lut8 + (size_t)T * nvH * 256,
                              c->lscale + (size_t)T * nblkH, c->st));
         }
         KRN(c, wk_apply_p6(c->jobs, c->njobs, c->max_jobs, 0, c->lut8, c->lscale, c->yg, I, H, c->st));
         KRN(c, wk_apply_p6(c->jobs, c->njobs, c->max_jobs, 1, c->lut8 + (size_t)T * nvH * 256,
                            c->lscale + (size_t)T * nblkH, c->yu, I, H, c->st));
         KRN(c, wk_act(c->yg, c->yu, P, I, g->act_situ, g->situ_beta, g->situ_linear_beta, c->hbuf, c->st));
-        KRN(c, wk_lut_p6(c->hbuf, P, I, books_kind(c, L, 2), c->lut8d, c->lscaled, c->st));
+        KRN(c, wk_lut_p6(c->hbuf, P, I, books_kind(c, B, 2), c->lut8d, c->lscaled, c->st));
         KRN(c, wk_apply_p6(c->jobs, c->njobs, c->max_jobs, 2, c->lut8d, c->lscaled, c->yd, H, I, c->st));
     } else {
         /* by runs: each expert's records decoded once per WARP_RUN_J jobs */
@@ -1873,19 +2007,19 @@ static int chunk_experts(warp_hip_ctx *c, int layer, const float *X_dev, int T, 
             else if (first)
                 KRN(c, wk_split_pgm(X_dev, NULL, c->pair_tok, c->offsets + E, P, H, 0, 0, 0.0f, 0.0f, c->xsp,
                                     c->xscalep, c->st));
-            KRN(c, wk_vq_runs(g->fmt, c->jobs, c->njobs, c->max_jobs, c->runs, 0, 2, L->books, c->xsp, c->xscalep,
+            KRN(c, wk_vq_runs(g->fmt, c->jobs, c->njobs, c->max_jobs, c->runs, 0, 2, B->books, c->xsp, c->xscalep,
                               yk, I, H, P, c->run_queue, c->st));
             KRN(c, wk_split_pgm(c->yg, c->yu, NULL, c->offsets + E, P, I, 1, g->act_situ, g->situ_beta,
                                 g->situ_linear_beta, c->xsh, c->xscaleh, c->st));
-            KRN(c, wk_vq_runs(g->fmt, c->jobs, c->njobs, c->max_jobs, c->runs, 2, 1, L->books, c->xsh, c->xscaleh,
+            KRN(c, wk_vq_runs(g->fmt, c->jobs, c->njobs, c->max_jobs, c->runs, 2, 1, B->books, c->xsh, c->xscaleh,
                               yk, H, I, P, c->run_queue, c->st));
         } else {
             if (first) KRN(c, wk_split(X_dev, T, H, c->xs, c->xscale, c->st));
-            KRN(c, wk_vq_runs(g->fmt, c->jobs, c->njobs, c->max_jobs, c->runs, 0, 2, L->books, c->xs, c->xscale, yk,
+            KRN(c, wk_vq_runs(g->fmt, c->jobs, c->njobs, c->max_jobs, c->runs, 0, 2, B->books, c->xs, c->xscale, yk,
                               I, H, 0, c->run_queue, c->st));
             KRN(c, wk_act_split(c->yg, c->yu, P, I, g->act_situ, g->situ_beta, g->situ_linear_beta, c->xsh,
                                 c->xscaleh, NULL, c->st));
-            KRN(c, wk_vq_runs(g->fmt, c->jobs, c->njobs, c->max_jobs, c->runs, 2, 1, L->books, c->xsh, c->xscaleh,
+            KRN(c, wk_vq_runs(g->fmt, c->jobs, c->njobs, c->max_jobs, c->runs, 2, 1, B->books, c->xsh, c->xscaleh,
                               yk, H, I, 0, c->run_queue, c->st));
         }
     }
@@ -1909,6 +2043,12 @@ int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *ou
     /* a missing pick an earlier decode left unreported: this chunk's plan
      * rewrites the device flag, so report it first */
     if (c->missing_pending && (rc = take_missing(c))) return rc;
+    /* fills since the last report that the device refused leave the cache
+     * now, before this chunk reads the table (a lookahead's claims raise
+     * resident before their checksums are known) */
+    if (c->crc_pending && (rc = crc_report(c))) return rc;
+    const layer_t *B = L;
+    const int foreign = layer_foreign(c, layer);
     if (L->books_x31 && !c->P6) {
         /* the chunk's matrix-core kernels cannot take exponent-31 codebook
          * values: the tokens go one at a time through the table kernel,
@@ -1944,7 +2084,7 @@ int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *ou
                     NULL, NULL, 0, c->st));
     const int n_la = lookahead_launch(c, layer, X_dev, T);
     if (n_la < 0) return n_la;
-    if (L->resident != E && can_fetch(c)) {
+    if ((L->resident != E && can_fetch(c)) || foreign) {
         DEV(c, hipMemcpyAsync(c->h_idx, c->idx, (size_t)P * sizeof(int), hipMemcpyDeviceToHost, c->st));
         DEV(c, hipStreamSynchronize(c->st));
         /* each distinct record once, ascending (src/model.c:3595-3603) */
@@ -1958,7 +2098,7 @@ int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *ou
         for (int e = 0; e < E; e++) if (used[e]) ids[n++] = e;
         free(used);
         if (n == 0) {
-            rc = chunk_experts(c, layer, Xe, T, 0, E - 1, 1);
+            rc = chunk_experts(c, layer, B, Xe, T, 0, E - 1, 1);
         } else {
             /* Windows of distinct experts that the cache holds at once, in
              * ascending id: the reference streams a chunk's experts through
@@ -1977,14 +2117,22 @@ int warp_hip_moe_chunk(warp_hip_ctx *c, int layer, const float *X_dev, float *ou
                     if (e != hipSuccess) { rc = dev_err(c, "window order", e); break; }
                 }
                 if ((rc = ensure_selected(c, layer, ids + a, b - a)) != 0) break;
-                rc = chunk_experts(c, layer, Xe, T, ids[a], ids[b - 1], a == 0);
+                /* one codebook set for the whole chunk: the first window's */
+                const layer_t *Bw;
+                if ((rc = books_of(c, layer, ids + a, b - a, &Bw)) != 0) break;
+                if (a == 0) B = Bw;
+                else if (Bw != B) {
+                    rc = set_err(c, WARP_HIP_E_BOOKS, layer, ids[a], "a chunk's records name different codebooks");
+                    break;
+                }
+                rc = chunk_experts(c, layer, B, Xe, T, ids[a], ids[b - 1], a == 0);
             }
         }
         free(ids);
         if (rc) return rc;
     } else {
         release_hold(c, layer);
-        if ((rc = chunk_experts(c, layer, Xe, T, 0, E - 1, 1))) return rc;
+        if ((rc = chunk_experts(c, layer, B, Xe, T, 0, E - 1, 1))) return rc;
     }
     if (L->sq[0]) {
         c->sx_pending = 0;
@@ -2051,7 +2199,13 @@ int warp_hip_vq_matvec(warp_hip_ctx *c, int layer, int kind, const uint8_t *rec_
     DEV(c, hipMemcpy(hdr, rec_dev, sizeof hdr, hipMemcpyDeviceToHost));
     uint32_t off[4];
     memcpy(off, hdr + 20, 16);
-    if (off[3] + 2 * (2 * (size_t)c->cfg.inter + c->He) > c->cfg.rec_bytes || off[kind] >= off[3])
+    /* decoded with the record's own codebook_id (src/model.c:2286, 2907) */
+    uint16_t cbid;
+    memcpy(&cbid, hdr + 10, sizeof cbid);
+    const layer_t *B = books_by_id(c, L, cbid);
+    if (!B) return set_err(c, WARP_HIP_E_BOOKS, layer, -1, "record codebook_id %u: no layer has those codebooks", cbid);
+    if (off[3] + 2 * (2 * (size_t)c->cfg.inter + c->He) > c->cfg.rec_bytes ||
+        (size_t)off[kind] + (kind == 2 ? c->down_bytes : c->gate_bytes) > off[3])
         return set_err(c, WARP_HIP_E_HEADER, layer, -1, "record offsets");
     warp_job jb;
     memset(&jb, 0, sizeof jb);
@@ -2070,12 +2224,12 @@ int warp_hip_vq_matvec(warp_hip_ctx *c, int layer, int kind, const uint8_t *rec_
     if (c->P6) {
         int8_t *lut = kind == 2 ? c->lut8d : c->lut8;
         float *ls = kind == 2 ? c->lscaled : c->lscale;
-        KRN(c, wk_lut_p6(x_dev, 1, N, books_kind(c, L, kind), lut, ls, c->st));
+        KRN(c, wk_lut_p6(x_dev, 1, N, books_kind(c, B, kind), lut, ls, c->st));
         KRN(c, wk_apply_p6(c->jobs, c->njobs, 1, kind, lut, ls, y_dev, M, N, c->st));
-    } else if (use_table(c, L)) {
+    } else if (use_table(c, B)) {
         float *yk[3] = { y_dev, y_dev, y_dev };
         int sp = 0;
-        KRN(c, wk_vq_lut(c->cfg.fmt, c->jobs, c->njobs, 1, kind, 1, L->books, L->books_x31, x_dev, 1, c->part, c->part_cap, M, N,
+        KRN(c, wk_vq_lut(c->cfg.fmt, c->jobs, c->njobs, 1, kind, 1, B->books, B->books_x31, x_dev, 1, c->part, c->part_cap, M, N,
                          c->n_cu, NULL, 0, 0, 0.0f, 0.0f, NULL, NULL, NULL, &sp, c->st));
         KRN(c, wk_lut_reduce(c->jobs, c->njobs, 1, kind, 1, c->part, sp, M, yk, c->st));
     } else {
@@ -2083,7 +2237,7 @@ int warp_hip_vq_matvec(warp_hip_ctx *c, int layer, int kind, const uint8_t *rec_
         uint16_t *xs = kind == 2 ? c->xsh : c->xs;
         float *xsc = kind == 2 ? c->xscaleh : c->xscale;
         KRN(c, wk_split(x_dev, 1, N, xs, xsc, c->st));
-        KRN(c, wk_vq_matvec(c->cfg.fmt, c->jobs, c->njobs, 1, kind, 1, L->books, xs, xsc, yk, M, N, 1, c->st));
+        KRN(c, wk_vq_matvec(c->cfg.fmt, c->jobs, c->njobs, 1, kind, 1, B->books, xs, xsc, yk, M, N, 1, c->st));
     }
     DEV(c, hipStreamSynchronize(c->st));
     return 0;
@@ -2101,11 +2255,17 @@ int warp_hip_decode_weights(warp_hip_ctx *c, int layer, int kind, const uint8_t 
     DEV(c, hipMemcpy(hdr, rec_dev, sizeof hdr, hipMemcpyDeviceToHost));
     uint32_t off[4];
     memcpy(off, hdr + 20, 16);
+    /* decoded with the record's own codebook_id (src/model.c:2286, 2907) */
+    uint16_t cbid;
+    memcpy(&cbid, hdr + 10, sizeof cbid);
+    const layer_t *B = books_by_id(c, L, cbid);
+    if (!B) return set_err(c, WARP_HIP_E_BOOKS, layer, -1, "record codebook_id %u: no layer has those codebooks", cbid);
     const size_t soff = kind == 0 ? 0 : kind == 1 ? (size_t)c->cfg.inter : 2 * (size_t)c->cfg.inter;
-    if (off[3] + 2 * (2 * (size_t)c->cfg.inter + c->He) > c->cfg.rec_bytes || off[kind] >= off[3])
+    if (off[3] + 2 * (2 * (size_t)c->cfg.inter + c->He) > c->cfg.rec_bytes ||
+        (size_t)off[kind] + (kind == 2 ? c->down_bytes : c->gate_bytes) > off[3])
         return set_err(c, WARP_HIP_E_HEADER, layer, -1, "record offsets");
     KRN(c, wk_decode_weights(c->cfg.fmt, rec_dev + off[kind], (const uint16_t *)(rec_dev + off[3]) + soff,
-                             books_kind(c, L, kind), M, N, W_dev, c->st));
+                             books_kind(c, B, kind), M, N, W_dev, c->st));
     DEV(c, hipStreamSynchronize(c->st));
     return 0;
 }

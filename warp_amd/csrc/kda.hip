@@ -15,6 +15,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "lds_limit.h"
 #include "warp_internal.h"
 
 #define WARP_EXPF_QUAL __device__ __forceinline__
@@ -85,13 +86,8 @@ extern "C" int wk_kda(int T, int H, int K, int V, const float *q, const float *k
     if (T <= 0 || H <= 0 || K <= 0 || K > KDA_MAX_K || V <= 0 || V > 1024) return -1;
     const size_t lds = (size_t)K * V * sizeof(float);
     if (lds > 150 * 1024) return -1;
-    static bool attr = false;
-    if (!attr) {
-        if (hipFuncSetAttribute((const void *)k_kda, hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024) !=
-            hipSuccess)
-            return -2;
-        attr = true;
-    }
+    static std::atomic<uint64_t> attr{0};
+    if (int r_ = lds_limit((const void *)k_kda, 150 * 1024, attr, stream)) return r_;
     hipLaunchKernelGGL(k_kda, dim3(H), dim3(V), lds, (hipStream_t)stream, T, H, K, V, q, k, v, g, beta, S, o);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : -(int)e - 1000;

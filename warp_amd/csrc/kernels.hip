@@ -21,6 +21,7 @@
 
 #include <type_traits>
 
+#include "lds_limit.h"
 #include "warp_internal.h"
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
@@ -963,23 +964,13 @@ extern "C" int wk_mvq_gemm(int nmat, const int8_t *const *W, const uint16_t *con
     const MvqMat b = nmat > 1 ? MvqMat{W[1], ws[1], rowbytes[1], y[1]} : a;
     const dim3 grid((M + MQ_MB - 1) / MQ_MB, (T + MQ_TB - 1) / MQ_TB, nmat);
     if (bits == 8) {
-        static bool attr = false;
-        if (!attr) {
-            hipError_t e = hipFuncSetAttribute((const void *)k_mvq_gemm<8>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                               160 * 1024);
-            if (e != hipSuccess) return -(int)e - 1000;
-            attr = true;
-        }
+        static std::atomic<uint64_t> attr{0};
+        if (int r_ = lds_limit((const void *)k_mvq_gemm<8>, 160 * 1024, attr, stream)) return r_;
         hipLaunchKernelGGL(k_mvq_gemm<8>, grid, dim3(256), lds, (hipStream_t)stream, a, b, group,
                            (const half8 *)xs, xscale, M, N, T);
     } else if (bits == 4) {
-        static bool attr = false;
-        if (!attr) {
-            hipError_t e = hipFuncSetAttribute((const void *)k_mvq_gemm<4>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                               160 * 1024);
-            if (e != hipSuccess) return -(int)e - 1000;
-            attr = true;
-        }
+        static std::atomic<uint64_t> attr{0};
+        if (int r_ = lds_limit((const void *)k_mvq_gemm<4>, 160 * 1024, attr, stream)) return r_;
         hipLaunchKernelGGL(k_mvq_gemm<4>, grid, dim3(256), lds, (hipStream_t)stream, a, b, group,
                            (const half8 *)xs, xscale, M, N, T);
     } else {
@@ -1609,13 +1600,8 @@ static int launch_vq(const VqArgs &a, int nkinds, int max_units, void *stream) {
     constexpr int UPW = NW / WPU;
     const size_t lds = (size_t)F::S * F::E * 16 + (size_t)NW * TPJ * 64 * 4;
     if (lds > 163840) return -2;
-    static bool attr = false;
-    if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_vq_mfma<FMT, TPJ, WPU, DB, NW, D>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return -(int)e - 1000;
-        attr = true;
-    }
+    static std::atomic<uint64_t> attr{0};
+    if (int r_ = lds_limit((const void *)k_vq_mfma<FMT, TPJ, WPU, DB, NW, D>, (int)lds, attr, stream)) return r_;
     int grid = (max_units + UPW - 1) / UPW;
     const int cap = FMT == WARP_FMT_VQ12 ? 256 : 512;
     if (grid > cap) grid = cap;
@@ -1791,13 +1777,8 @@ static int launch_vq_run(const VqArgs &a, const int *runs, int nkinds, int max_u
     typedef FmtT<FMT> F;
     constexpr int WD = F::S == 3 ? 2 : 8;                   // three stages leave room for fewer words
     const size_t lds = (size_t)F::S * F::E * 16;
-    static bool attr = false;
-    if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_vq_mfma_run<FMT, WD>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return -(int)e - 1000;
-        attr = true;
-    }
+    static std::atomic<uint64_t> attr{0};
+    if (int r_ = lds_limit((const void *)k_vq_mfma_run<FMT, WD>, (int)lds, attr, stream)) return r_;
     int grid = (max_units + 7) / 8;
     const int cap = FMT == WARP_FMT_VQ12 ? 256 : 1024;
     if (grid > cap) grid = cap;
@@ -2090,18 +2071,20 @@ struct LutArgs {
 };
 
 // Coherent accesses, for what one block of the fused decode launch writes
-// for another, which may run on another XCD (another L2): 16-byte stores
-// that write through every cache (a volatile store: sc0 sc1; a wave's
-// stores then cover whole lines), agent-coherent loads (sc1) that do not
-// hit a stale cached copy. A wave's
-// stores are complete once wait_stores() returns, so with a barrier after
-// it the block can raise a count that others poll, without writing back
-// the L2 (which an agent-scope release fence does, at a cost that grows
-// with everything the XCD's other blocks have written).
-typedef float f4v __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ void st_through4(float *p, float a, float b, float c, float d) {   // p in global memory, 16-byte aligned
-    const f4v v = {a, b, c, d};
-    *(volatile __attribute__((address_space(1))) f4v *)(__attribute__((address_space(1))) float *)p = v;
+// for another, which may run on another XCD (another L2): agent-scope
+// atomic stores and loads (relaxed), which the memory model lowers to
+// accesses that bypass a stale or write-back copy in the XCD's L2 (sc1), so
+// the values reach, and are read from, memory every XCD sees. Nothing here
+// rests on how a plain or volatile access is lowered. A wave's stores are
+// complete once wait_stores() returns, so with a barrier after it the block
+// can raise a count that others poll, without writing back the L2 (which an
+// agent-scope release fence does, at a cost that grows with everything the
+// XCD's other blocks have written).
+__device__ __forceinline__ void st_through4(float *p, float a, float b, float c, float d) {   // p in global memory
+    __hip_atomic_store(p + 0, a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(p + 1, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(p + 2, c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(p + 3, d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ float ld_agent(const float *p) {
     return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -2979,13 +2962,8 @@ static int launch_moe_fused(const MoeArgs &m, int blocks, void *stream) {
     typedef FmtT<FMT> F;
     const size_t lds = ((size_t)2 * 2 * F::S * F::E + LUT_XCH * 16) * sizeof(float);
     if (lds > 163840) return -2;
-    static bool attr = false;
-    if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_moe_fused<FMT, X31>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return -(int)e - 1000;
-        attr = true;
-    }
+    static std::atomic<uint64_t> attr{0};
+    if (int r_ = lds_limit((const void *)k_moe_fused<FMT, X31>, (int)lds, attr, stream)) return r_;
     hipLaunchKernelGGL((k_moe_fused<FMT, X31>), dim3(blocks), dim3(LUT_NW * 64), lds, (hipStream_t)stream, m);
     CHECK_LAUNCH();
     return 0;
@@ -3018,13 +2996,8 @@ static int launch_lut(const LutArgs &a, int groups, int nkinds, void *stream) {
     typedef FmtT<FMT> F;
     const size_t lds = ((size_t)2 * 2 * F::S * F::E + LUT_XCH * 16) * sizeof(float);
     if (lds > 163840) return -2;
-    static bool attr = false;
-    if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_vq_lut<FMT, X31, SHX, ACT, RT>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return -(int)e - 1000;
-        attr = true;
-    }
+    static std::atomic<uint64_t> attr{0};
+    if (int r_ = lds_limit((const void *)k_vq_lut<FMT, X31, SHX, ACT, RT>, (int)lds, attr, stream)) return r_;
     const int gx = groups * a.splits, nsh = a.sh_out ? (a.M + LUT_NW * 4 - 1) / (LUT_NW * 4) : 0;
     hipLaunchKernelGGL((k_vq_lut<FMT, X31, SHX, ACT, RT>), dim3(gx + nsh, nkinds + (a.sh.h && !a.sh_out ? 1 : 0)),
                        dim3(LUT_NW * 64), lds, (hipStream_t)stream, a);
@@ -3851,13 +3824,8 @@ extern "C" int wk_plan_chunk(const int *idx, const float *w, int T, int K, int E
     constexpr size_t LDS_MAX = 152 * 1024;
     if (base > LDS_MAX) return -1;
     const int bitmaps = base + bms <= LDS_MAX;
-    static bool attr = false;
-    if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_plan_chunk, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           (int)LDS_MAX);
-        if (e != hipSuccess) return -(int)e - 1000;
-        attr = true;
-    }
+    static std::atomic<uint64_t> attr{0};
+    if (int r_ = lds_limit((const void *)k_plan_chunk, (int)LDS_MAX, attr, stream)) return r_;
     hipLaunchKernelGGL(k_plan_chunk, dim3(1), dim3(1024), base + (bitmaps ? bms : 0), (hipStream_t)stream, idx, w, T,
                        K, E, table, counts, offsets, pair_tok, pair_exp, pair_w, tok_slots, jobs, max_jobs, njobs,
                        runs, missing, inter, bitmaps, e_lo, e_hi, or_missing);
@@ -3981,13 +3949,8 @@ extern "C" int wk_vq_encode(const float *X, long n, const float *books, int stag
     if (n <= 0 || stages < 1 || entries < 1 || entries > 4096) return -1;
     if (((uintptr_t)X | (uintptr_t)books | (uintptr_t)cur) & 15) return -1;
     const size_t lds = (size_t)entries * 8 * sizeof(float);
-    static bool attr = false;
-    if (!attr) {
-        if (hipFuncSetAttribute((const void *)k_vq_encode_stage, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                4096 * 8 * (int)sizeof(float)) != hipSuccess)
-            return -2;
-        attr = true;
-    }
+    static std::atomic<uint64_t> attr{0};
+    if (int r_ = lds_limit((const void *)k_vq_encode_stage, 4096 * 8 * (int)sizeof(float), attr, stream)) return r_;
     const unsigned grid = (unsigned)((n + ENC_NT - 1) / ENC_NT);
     for (int s = 0; s < stages; s++) {
         hipLaunchKernelGGL(k_vq_encode_stage, dim3(grid), dim3(ENC_NT), lds, (hipStream_t)stream, X, cur,
@@ -4142,7 +4105,7 @@ extern "C" int wk_fill_random(uint8_t *p, size_t n, uint64_t seed, void *stream)
 }
 
 __global__ __launch_bounds__(256) void k_set_slots(warp_slot *__restrict__ table, const warp_slot_upd *__restrict__ u,
-                                                   int n, const int8_t *__restrict__ crc_bad,
+                                                   int n, int8_t *__restrict__ crc_bad,
                                                    warp_crc_err *__restrict__ err) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
@@ -4152,11 +4115,13 @@ __global__ __launch_bounds__(256) void k_set_slots(warp_slot *__restrict__ table
         v.rec = nullptr;                       // refused: the record stays out of the table
         const int k = atomicAdd(&err->n, 1);
         if (k < WARP_CRC_ERR_KEYS) err->keys[k] = key;
+    } else if (!u[i].checked && crc_bad) {
+        crc_bad[key] = 0;                      // an unchecked entry (eviction, synthetic record) is no refusal
     }
     table[key] = v;
 }
 
-extern "C" int wk_set_slots(warp_slot *table, const warp_slot_upd *u, int n, const int8_t *crc_bad, warp_crc_err *err,
+extern "C" int wk_set_slots(warp_slot *table, const warp_slot_upd *u, int n, int8_t *crc_bad, warp_crc_err *err,
                             void *stream) {
     if (n <= 0) return 0;
     if (crc_bad && !err) return -1;

@@ -325,7 +325,9 @@ int wk_fill_random(uint8_t *p, size_t n, uint64_t seed, void *stream);
  * checked = 1: the record was checksummed on the device (wk_crc32 with this
  * key); if crc_bad[key] is set, the entry becomes NULL (not resident) and the
  * key is appended to err (the first WARP_CRC_ERR_KEYS keys; n counts every
- * failure). */
+ * failure). checked = 0 clears crc_bad[key], so that after the launch
+ * crc_bad[key] is 1 exactly for the keys whose last update was refused (the
+ * complete list when more than WARP_CRC_ERR_KEYS were). */
 typedef struct {
     warp_slot v;
     int key;
@@ -336,7 +338,7 @@ typedef struct {
     int n;
     int keys[WARP_CRC_ERR_KEYS];
 } warp_crc_err;
-int wk_set_slots(warp_slot *table, const warp_slot_upd *u, int n, const int8_t *crc_bad, warp_crc_err *err,
+int wk_set_slots(warp_slot *table, const warp_slot_upd *u, int n, int8_t *crc_bad, warp_crc_err *err,
                  void *stream);
 
 /* zlib's crc32 of p[0, n) in device memory (crc.hip). tmp holds
@@ -355,6 +357,9 @@ int wk_kda(int T, int H, int K, int V, const float *q, const float *k, const flo
 
 /* Device properties the host needs: returns the gfx name into buf. */
 int wk_device_arch(int device, char *buf, int n);
+
+/* Drops the MoE table slots' device state (moe_table.c). */
+void warp_moe_release(void);
 
 #ifdef __cplusplus
 }

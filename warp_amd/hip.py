@@ -19,8 +19,8 @@ VQ3R, VQ2R, VQ4P, VQ12 = 4, 5, 8, 9
 FMT = {"VQ3R": VQ3R, "VQ2R": VQ2R, "VQ4P": VQ4P, "VQ12": VQ12}
 ROUTE_SIGMOID, ROUTE_SOFTMAX = 0, 1
 ERRORS = {-1: "E_ARG", -2: "E_DEVICE", -3: "E_NOMEM", -4: "E_READ", -5: "E_HEADER",
-          -6: "E_CRC", -7: "E_NOSLOT", -8: "E_MISSING"}
-E_ARG, E_DEVICE, E_NOMEM, E_READ, E_HEADER, E_CRC, E_NOSLOT, E_MISSING = range(-1, -9, -1)
+          -6: "E_CRC", -7: "E_NOSLOT", -8: "E_MISSING", -9: "E_BOOKS"}
+E_ARG, E_DEVICE, E_NOMEM, E_READ, E_HEADER, E_CRC, E_NOSLOT, E_MISSING, E_BOOKS = range(-1, -10, -1)
 
 _lib = None
 
@@ -39,7 +39,7 @@ class Cfg(C.Structure):
         ("situ_beta", C.c_float), ("situ_linear_beta", C.c_float), ("max_tokens", C.c_int),
         ("rec_bytes", C.c_size_t), ("cache_bytes", C.c_size_t), ("verify", C.c_int),
         ("lookahead", C.c_int), ("device", C.c_int), ("latent", C.c_int), ("latent_norm", C.c_int),
-        ("norm_eps", C.c_float), ("prefill_fp16", C.c_int),
+        ("norm_eps", C.c_float), ("prefill_fp16", C.c_int), ("n_books", C.c_int),
     ]
 
 
@@ -52,10 +52,43 @@ class CacheStats(C.Structure):
 FETCH_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_int, C.c_int, C.POINTER(C.c_uint8))
 FETCH_HOST_FN = C.CFUNCTYPE(C.c_void_p, C.c_void_p, C.c_int, C.c_int)
 
+
+class TrunkTensor(C.Structure):
+    """warp_trunk_tensor: a waste_tensor's F32 rows or quantised rows."""
+    _fields_ = [("data", C.c_void_p), ("q", C.c_void_p), ("qs", C.c_void_p), ("group", C.c_int),
+                ("bits", C.c_int), ("rowbytes", C.c_size_t)]
+
+
+class MoeArgs(C.Structure):
+    """warp_moe_args: one MoE layer of the engine's model and one call."""
+    _fields_ = [
+        ("model", C.c_void_p), ("layer", C.c_int), ("n_layers", C.c_int),
+        ("hidden", C.c_int), ("moe_inter", C.c_int), ("n_experts", C.c_int), ("top_k", C.c_int),
+        ("latent_dim", C.c_int), ("latent_norm", C.c_int), ("norm_eps", C.c_float), ("renorm", C.c_int),
+        ("routed_scale", C.c_float), ("act_situ", C.c_int), ("situ_beta", C.c_float),
+        ("situ_linear_beta", C.c_float), ("index_bits", C.c_int), ("stages", C.c_int), ("cb_entries", C.c_int),
+        ("vec_dim", C.c_int), ("codebooks", C.c_void_p), ("n_books", C.c_int), ("cb_base", C.c_int),
+        ("router", TrunkTensor), ("bias", C.c_void_p), ("shared", TrunkTensor * 3), ("inter_shared", C.c_int),
+        ("latent", TrunkTensor * 2), ("latent_norm_w", C.c_void_p), ("rec_bytes", C.c_size_t),
+        ("cache_bytes", C.c_size_t), ("verify", C.c_int), ("lookahead", C.c_int), ("fetch", FETCH_FN),
+        ("fetch_user", C.c_void_p), ("n_tokens", C.c_int), ("x", C.c_void_p), ("out", C.c_void_p),
+        ("route", C.c_void_p), ("rw", C.c_void_p),
+    ]
+
+
+MOE_SLOT = C.CFUNCTYPE(C.c_int, C.POINTER(MoeArgs))
+
+
+class MoeKernels(C.Structure):
+    """waste_moe_kernels: the MoE slots' table."""
+    _fields_ = [("moe_ffn_decode", MOE_SLOT), ("moe_ffn_batch", MOE_SLOT), ("on_device", C.c_int)]
+
 # name -> (restype, argtypes); also the list of symbols the header declares
 SIGNATURES = {
     "waste_register_hip": (C.c_char_p, [C.c_void_p]),
     "waste_hip_release_host_buffers": (None, []),
+    "waste_register_hip_moe": (C.c_char_p, [C.c_void_p]),
+    "warp_hip_moe_table_stats": (None, [C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
     "warp_hip_table_stats": (None, [C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
     "warp_hip_kda_stats": (None, [C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
     "warp_hip_kda_forward": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p,
@@ -149,11 +182,11 @@ class Context:
                  routed_scale=1.0, router_act=ROUTE_SIGMOID, router_strict=False, act_situ=False,
                  situ_beta=1.0, situ_linear_beta=0.0, max_tokens=1, rec_bytes, cache_bytes,
                  verify=False, lookahead=0, device=0, latent=0, latent_norm=True, norm_eps=1e-5,
-                 prefill_fp16=False):
+                 prefill_fp16=False, n_books=0):
         self.cfg = Cfg(hidden, inter, n_experts, top_k, n_layers, FMT.get(fmt, fmt), int(renorm),
                        routed_scale, router_act, int(router_strict), int(act_situ), situ_beta,
                        situ_linear_beta, max_tokens, rec_bytes, cache_bytes, int(verify), lookahead, device,
-                       latent, int(latent_norm), norm_eps, int(prefill_fp16))
+                       latent, int(latent_norm), norm_eps, int(prefill_fp16), n_books)
         self.h = C.c_void_p()
         self._keep = []
         rc = lib().warp_hip_open(C.byref(self.cfg), C.byref(self.h))
