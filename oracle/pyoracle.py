@@ -317,6 +317,22 @@ class Ref:
         return lut
 
 
+def ecache_replay(ids, n_slots):
+    """The compiled reference's expert cache (oracle/_ref, src/ecache.c) on a
+    routing trace ids [tokens][layers][K], one get per id in order (read-ahead
+    and lookahead off): (hits, misses, evictions, records read)."""
+    if not os.path.exists(REF_LIB):
+        raise RuntimeError(f"{REF_LIB} is not built")
+    L = C.CDLL(REF_LIB)
+    L.ref_ecache_replay.restype = C.c_int
+    L.ref_ecache_replay.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p]
+    ids = np.ascontiguousarray(ids, np.int32)
+    out = np.zeros(4, np.uint64)
+    n_tok, n_layers, K = ids.shape
+    assert L.ref_ecache_replay(_p(ids), n_tok, n_layers, K, n_slots, _p(out)) == 0
+    return tuple(int(v) for v in out)
+
+
 def record_check(rec, layer, expert, fmt, stages, n_books, expert_m, verify):
     """or_record_check: the oracle's restatement of record_check
     (src/model.c:1698-1745) on a record of len(rec) bytes. fmt names the

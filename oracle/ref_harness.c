@@ -162,3 +162,35 @@ int ref_record_check(void *p, int L, int expert, const uint8_t *rec, int verify)
 
 /* The container's codebook count (src/model.c:1274). */
 int ref_n_books(void *p) { return ((waste_model *)p)->n_books; }
+
+/* The reference's expert cache (src/ecache.c) driven by a routing trace the
+ * way moe_layer drives it with read-ahead off and no lookahead: for every
+ * token, every layer, one waste_ecache_get per selected expert in order
+ * (src/model.c:2862-2868). ids [n_tok][n_layers][K]; a cache of n_slots
+ * records under the LFRU policy; the fetch reads nothing. out: hits,
+ * misses, evictions, bytes_read / rec_bytes. */
+static int replay_fetch(void *user, int layer, int expert, uint8_t *dst)
+{
+    (void)user; (void)layer; (void)expert; (void)dst;
+    return 0;
+}
+
+int ref_ecache_replay(const int *ids, int n_tok, int n_layers, int K, int n_slots, uint64_t out[4])
+{
+    waste_ecache c;
+    const size_t rec = 4096;
+    if (waste_ecache_init(&c, (size_t)n_slots * rec, rec, 0) != 0) return -1;
+    for (int t = 0; t < n_tok; t++)
+        for (int L = 0; L < n_layers; L++)
+            for (int j = 0; j < K; j++)
+                if (!waste_ecache_get(&c, L, ids[((size_t)t * n_layers + L) * K + j], replay_fetch, NULL)) {
+                    waste_ecache_free(&c);
+                    return -2;
+                }
+    out[0] = c.hits;
+    out[1] = c.misses;
+    out[2] = c.evictions;
+    out[3] = c.bytes_read / rec;
+    waste_ecache_free(&c);
+    return 0;
+}

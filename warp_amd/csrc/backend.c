@@ -307,7 +307,7 @@ struct warp_hip_ctx {
     layer_t *L;
     /* expert cache */
     uint8_t *pool;
-    int n_slots, next_free;
+    int n_slots, next_free, n_empty;   /* n_empty: freed slots below next_free */
     size_t slot_stride;         /* bytes between slots (see slot_rec)       */
     int *slot_key, *key_slot;
     uint16_t *rec_cb;           /* [layer][expert]: the codebook_id of the
@@ -1046,16 +1046,26 @@ static uint32_t new_hold(warp_hip_ctx *c)
     return c->hold_next;
 }
 
-/* A slot to fill: a never-used one, else the least-frequent (then least
- * recent) of 16 sampled slots that no hold keeps, else the first such slot
- * (the LFRU sampled victim of src/ecache.c:432-460). */
+/* A slot to fill, as the reference's ec_victim chooses one
+ * (src/ecache.c:432-460): the lowest-numbered empty slot, else the
+ * least-frequent (then least recently used) of 16 slots sampled with its
+ * generator (rng * 1664525 + 1013904223, rng % n_slots, seeded 0x9e3779b9)
+ * that no hold keeps, else the first such slot. A hold keeps the selection
+ * in flight whole, where the reference, which multiplies one record at a
+ * time, keeps only the record in use. */
 static int pick_victim(warp_hip_ctx *c)
 {
+    if (c->n_empty > 0) {
+        /* slots freed by a refused record, below the never-used ones */
+        for (int s = 0; s < c->next_free; s++)
+            if (c->slot_key[s] < 0) { c->n_empty--; return s; }
+        c->n_empty = 0;
+    }
     if (c->next_free < c->n_slots) return c->next_free++;
     int best = -1;
     for (int k = 0; k < 16; k++) {
         c->rng = c->rng * 1664525u + 1013904223u;
-        const int s = (int)((c->rng >> 8) % (unsigned)c->n_slots);
+        const int s = (int)(c->rng % (unsigned)c->n_slots);
         if (c->slot_key[s] >= 0 && is_pinned(c, c->slot_key[s])) continue;
         if (best < 0 || c->hits[s] < c->hits[best] || (c->hits[s] == c->hits[best] && c->last[s] < c->last[best]))
             best = s;
@@ -1144,6 +1154,7 @@ static void unclaim(warp_hip_ctx *c, int key)
     c->key_slot[key] = -1;
     c->slot_key[s] = -1;
     c->hits[s] = 0;
+    c->n_empty++;
     c->L[key / c->cfg.n_experts].resident--;
 }
 
