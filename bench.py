@@ -26,9 +26,10 @@ Reported:
                process may use (at most 16, one GPU's share of the box),
                with a one-thread row beside it
 
-The default run also measures the other four configurations, each in a
-child process of its own (the same code as --workload), and carries their
-lines in "workloads": single-expert, kimi-decode, kimi-prefill, k3-miss.
+The default run also measures the other configurations, each in a child
+process of its own (the same code as --workload), and carries their lines
+in "workloads": single-expert, kimi-decode, kimi-prefill (and its exact
+mode), k3-miss, table-slots.
 
 Workloads (--workload), each printing its own JSON line:
   single-expert one expert's SwiGLU FFN on one token (hidden 2304,
@@ -45,6 +46,10 @@ Workloads (--workload), each printing its own JSON line:
                 an HBM cache of 0.69 of the stack's records, misses copied
                 from pinned host memory on the copy stream; passes without
                 lookahead, with lookahead, and all resident
+  table-slots   the reference's dispatch-table slots mvq_rows_f32 and
+                kda_step through waste_register_hip, called as the engine
+                calls them (host pointers), beside the reference's own
+                AVX-512 slots on the host
 """
 from __future__ import annotations
 
@@ -306,10 +311,14 @@ def ref_rows(d, cache_bytes, warm, one, units, seconds, describe):
         ref.close(reset_pool=True)
         rows.append((n * units / dt, n, dt, used, isa))
     (v, n, dt, used, isa), (v1, n1, dt1, _, _) = rows
-    return {"value": v, "unit": describe["unit"], "cores": used, "kind": "reference", "isa": isa,
-            "sample": describe["sample"].format(n=n * units, threads=used, secs=dt, isa=isa),
-            "one_thread": {"value": v1, "cores": 1,
-                           "sample": describe["sample"].format(n=n1 * units, threads=1, secs=dt1, isa=isa)}}
+    all_row = {"value": v, "cores": used, "sample": describe["sample"].format(n=n * units, threads=used, secs=dt,
+                                                                              isa=isa)}
+    one_row = {"value": v1, "cores": 1, "sample": describe["sample"].format(n=n1 * units, threads=1, secs=dt1,
+                                                                            isa=isa)}
+    best = all_row if v >= v1 else one_row
+    return {"value": best["value"], "unit": describe["unit"], "cores": best["cores"], "kind": "reference",
+            "isa": isa, "sample": best["sample"], "chosen": "the better of the two rows",
+            "all_threads": all_row, "one_thread": one_row}
 
 
 def k3_twin_spec():
@@ -595,7 +604,11 @@ def run_prefill(args):
         "per_layer": {"distinct_experts": round(float(np.mean(distinct)), 1), "pairs": T * KK,
                       "tokens_on_busiest_5": counts[:5].tolist(), "algorithmic_bytes": int(per_layer),
                       "useful_flops": int(flops)},
-        "hbm": {"achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "what": "algorithmic bytes of the layer (records of the distinct experts picked, shared "
+                             "expert, router, codebooks, activations) over the step time: HBM-bound, the "
+                             "arithmetic intensity (about 85 FLOP/B) is below the bf16 ridge"},
         "mfma": {"achieved": round(tfs, 2), "peak": 2500.0, "unit": "TFLOP/s",
                  "frac": round(tfs / 2500.0, 5),
                  "note": "useful FLOPs (2 x 3 x H x I per pair, plus the shared expert); " +
@@ -986,9 +999,9 @@ def run_miss(args):
                    "cache_slots": slots, "record_bytes": rec_layout()[3], "lookahead_per_token": args.lookahead,
                    "parallelism": "single GPU"},
         "passes": res,
-        "copy_roofline": {"bound": "host-to-device copy", "achieved": la["h2d_gbs"], "peak": round(peak, 2),
-                          "unit": "GB/s", "frac": round(la["h2d_gbs"] / peak, 4),
-                          "peak_source": "best of 3 synchronous 1 GiB copies from the pinned host tier"},
+        "roofline": {"bound": "host-to-device copy", "achieved": la["h2d_gbs"], "peak": round(peak, 2),
+                     "unit": "GB/s", "frac": round(la["h2d_gbs"] / peak, 4), "traffic": None,
+                     "peak_source": "best of 3 synchronous 1 GiB copies from the pinned host tier"},
         "layer_ms_bounds": {"copy_at_peak": round(copy_ms, 3), "compute_resident": res["resident"]["ms_per_layer"],
                             "measured": la["ms_per_layer"]},
         "cpu_baseline": None if args.no_cpu else cpu_baseline_miss(args, args.cpu_seconds, T),
@@ -1083,16 +1096,169 @@ def cpu_baseline_encode(seconds):
                       f"8-bit codes; it has no 4096-entry encoder) over {threads} threads, {dt:.1f}s"}
 
 
+# ---- the dispatch table's slots as the engine calls them -------------------------------------
+
+def _tables():
+    """ctypes types of the reference's dispatch table (src/waste_backend.h:67-90)
+    and mvq_arg (src/simd.h:35-39)."""
+    import ctypes as C
+
+    class MvqArg(C.Structure):
+        _fields_ = [("y", C.c_void_p), ("W", C.c_void_p), ("ws", C.c_void_p), ("xq", C.c_void_p),
+                    ("xs", C.c_void_p), ("in_", C.c_int), ("ng", C.c_int), ("group", C.c_int), ("bits", C.c_int),
+                    ("rowbytes", C.c_size_t)]
+
+    class Table(C.Structure):
+        _fields_ = [("kda_step", C.c_void_p), ("short_conv_step", C.c_void_p), ("rmsnorm_gated", C.c_void_p),
+                    ("mvq_rows_f32", C.c_void_p), ("lutb_range", C.c_void_p), ("on_device", C.c_int)]
+    slot = C.CFUNCTYPE(None, C.c_int, C.c_int, C.c_void_p)
+    kda = C.CFUNCTYPE(None, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                      C.c_void_p, C.c_void_p, C.c_void_p)
+    return MvqArg, Table, slot, kda
+
+
+def _time_calls(fn, seconds, min_calls=5):
+    n, t0 = 0, time.perf_counter()
+    while n < min_calls or time.perf_counter() - t0 < seconds:
+        fn()
+        n += 1
+    return (time.perf_counter() - t0) / n, n
+
+
+# (name, rows, in, bits, group): a Kimi-Linear shared expert's gate rows, a
+# quantised K3 router, a K3 trunk projection, a slice of a K3 lm_head
+MVQ_SHAPES = [("kimi_shared_gate_q8g32", 1024, 2304, 8, 32), ("k3_router_q8g128", 384, 7168, 8, 128),
+              ("k3_proj_q8g128", 7168, 7168, 8, 128), ("k3_lm_head_slice_q8g128", 16384, 7168, 8, 128)]
+KDA_SHAPES = [("kimi_linear_kda_h32_k128_v128", 32, 128, 128)]
+
+
+def run_table_slots(args):
+    """The reference's dispatch-table slots as its engine calls them, with
+    host pointers: mvq_rows_f32 (run_rows hands a device backend the whole row
+    range in one call, src/model.c:356-360) and kda_step (one decode step of
+    every head, src/kda.c:26-68), through the table waste_register_hip fills,
+    against the same slots of the reference's own table (oracle/_ref,
+    waste_backend_init's AVX-512 build) on this host: its mvq rows split over
+    the host threads in 64-row ranges as its pool splits them, and over one
+    thread; its kda_step on one thread, as the engine calls it."""
+    import ctypes as C
+    from concurrent.futures import ThreadPoolExecutor
+    import warp_amd
+    from oracle import pyoracle as po
+    MvqArg, Table, Slot, Kda = _tables()
+    t = Table()
+    assert warp_amd.lib().waste_register_hip(C.byref(t)), "no gfx950 device"
+    dev_mvq, dev_kda = Slot(t.mvq_rows_f32), Kda(t.kda_step)
+    ref_mvq = ref_kda = None
+    isa = None
+    if not args.no_cpu and os.path.exists(po.REF_LIB):
+        R = C.CDLL(po.REF_LIB)
+        R.waste_backend_init.argtypes = [C.c_uint]
+        R.waste_backend_init(0)
+        R.waste_backend_name.restype = C.c_char_p
+        isa = R.waste_backend_name().decode()
+        rt = Table.in_dll(R, "waste_k")
+        ref_mvq, ref_kda = Slot(rt.mvq_rows_f32), Kda(rt.kda_step)
+    threads = cpu_threads()
+    pool = ThreadPoolExecutor(threads)          # the reference's pool keeps its threads too
+    secs = max(0.5, args.cpu_seconds / 8)
+    rng = np.random.default_rng(42)
+    out = {"mvq_rows_f32": {}, "kda_step": {}}
+    for name, rows, n, bits, group in MVQ_SHAPES:
+        ng = n // group
+        W = rng.integers(-127, 128, size=(rows, n), dtype=np.int8)
+        ws = rng.uniform(0.002, 0.02, size=(rows, ng)).astype(np.float16).view(np.uint16)
+        x = rng.standard_normal(n).astype(np.float32)
+        yd, yc = np.empty(rows, np.float32), np.empty(rows, np.float32)
+        ad = MvqArg(yd.ctypes.data, W.ctypes.data, ws.ctypes.data, None, x.ctypes.data, n, ng, group, bits, n)
+        ac = MvqArg(yc.ctypes.data, W.ctypes.data, ws.ctypes.data, None, x.ctypes.data, n, ng, group, bits, n)
+        pd, pc = C.cast(C.pointer(ad), C.c_void_p), C.cast(C.pointer(ac), C.c_void_p)
+        dev_mvq(0, rows, pd)                                      # the device mirror of W is made once
+        s_dev, k_dev = _time_calls(lambda: dev_mvq(0, rows, pd), secs)
+        nbytes = rows * (n + 2 * ng)
+        row = {"rows": rows, "in": n, "bits": bits, "group": group, "weight_bytes": nbytes,
+               "device_us_per_call": round(s_dev * 1e6, 1), "device_calls": k_dev,
+               "device_weight_gbs": round(nbytes / s_dev / 1e9, 1)}
+        if ref_mvq is not None:
+            ref_mvq(0, rows, pc)
+            assert np.allclose(yd, yc, rtol=1e-4, atol=1e-3 * float(np.max(np.abs(yc)))), name
+
+            step = max(64, (rows // threads + 63) // 64 * 64)
+            cut = [(b, min(b + step, rows)) for b in range(0, rows, step)]
+
+            def pooled():
+                for f in [pool.submit(ref_mvq, b, e, pc) for b, e in cut]:
+                    f.result()
+            s_cpu, _ = _time_calls(pooled, secs)
+            s_one, _ = _time_calls(lambda: ref_mvq(0, rows, pc), secs / 2)
+            row.update({"cpu_us_per_call": round(s_cpu * 1e6, 1), "cpu_threads": threads,
+                        "cpu_one_thread_us_per_call": round(s_one * 1e6, 1),
+                        "speedup_vs_cpu": round(min(s_cpu, s_one) / s_dev, 2)})
+        out["mvq_rows_f32"][name] = row
+        log(f"bench: mvq slot {name}: device {s_dev * 1e6:.1f} us" +
+            (f", reference {row['cpu_us_per_call']:.1f} us ({threads} threads) / "
+             f"{row['cpu_one_thread_us_per_call']:.1f} us (1)" if "cpu_us_per_call" in row else ""))
+        warp_amd.lib().waste_hip_release_host_buffers()
+    for name, Hh, Kk, Vv in KDA_SHAPES:
+        q, k = rng.standard_normal((Hh, Kk)).astype(np.float32), rng.standard_normal((Hh, Kk)).astype(np.float32)
+        v = rng.standard_normal((Hh, Vv)).astype(np.float32)
+        g = -np.abs(rng.standard_normal((Hh, Kk))).astype(np.float32) * 0.1
+        beta = rng.uniform(0.1, 0.9, Hh).astype(np.float32)
+        S0 = (rng.standard_normal((Hh, Kk, Vv)) * 0.1).astype(np.float32)
+        o = np.empty((Hh, Vv), np.float32)
+        scratch = np.empty(Vv, np.float32)              # waste_kda_step's u [V]
+        Sd, Sc = S0.copy(), S0.copy()
+        ptrs = lambda S_: [a.ctypes.data for a in (q, k, v, g, beta)] + [S_.ctypes.data, o.ctypes.data,
+                                                                          scratch.ctypes.data]
+        pd_, pc_ = ptrs(Sd), ptrs(Sc)
+        s_dev, k_dev = _time_calls(lambda: dev_kda(Hh, Kk, Vv, *pd_), secs)
+        sbytes = Hh * Kk * Vv * 4
+        row = {"H": Hh, "K": Kk, "V": Vv, "state_bytes": sbytes, "device_us_per_call": round(s_dev * 1e6, 1),
+               "device_calls": k_dev}
+        if ref_kda is not None:
+            s_one, _ = _time_calls(lambda: ref_kda(Hh, Kk, Vv, *pc_), secs)
+            row.update({"cpu_one_thread_us_per_call": round(s_one * 1e6, 1),
+                        "speedup_vs_cpu": round(s_one / s_dev, 2)})
+        out["kda_step"][name] = row
+        log(f"bench: kda slot {name}: device {s_dev * 1e6:.1f} us" +
+            (f", reference {row['cpu_one_thread_us_per_call']:.1f} us (1 thread)" if ref_kda is not None else ""))
+    dstat, fstat = (C.c_uint64(), C.c_uint64())
+    warp_amd.lib().warp_hip_table_stats(C.byref(dstat), C.byref(fstat))
+    main = out["mvq_rows_f32"]["k3_proj_q8g128"]
+    return {
+        "metric": "dispatch-table slot calls/s as the engine calls them (host pointers), 1 MI355X",
+        "value": round(1.0 / (main["device_us_per_call"] / 1e6), 1),
+        "unit": "mvq_rows_f32 calls/s (K3 trunk projection, 7168 x 7168 Q8G g128)",
+        "n_gpus": 1, "steps": None, "warmup": 1, "ms_per_step": round(main["device_us_per_call"] / 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8 x fp32",
+        "data": "synthetic (random Q8G rows, fp16 scales, N(0,1) activations; KDA inputs and state)",
+        "config": {"workload": "the mvq_rows_f32 and kda_step slots of the reference's table through "
+                               "waste_register_hip, per call: inputs host to device, kernel, outputs back",
+                   "parallelism": "single GPU"},
+        "slots": out, "cpu_isa": isa, "fallback_calls": fstat.value,
+        "roofline": {"bound": "hbm", "achieved": main["device_weight_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(main["device_weight_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_mvq through the mvq_rows_f32 slot, whole call (copies and wait included)"},
+        "cpu_baseline": None if ref_mvq is None else {
+            "value": round(1.0 / (min(main["cpu_us_per_call"], main["cpu_one_thread_us_per_call"]) / 1e6), 1),
+            "unit": "mvq_rows_f32 calls/s", "cores": threads if main["cpu_us_per_call"] <=
+            main["cpu_one_thread_us_per_call"] else 1, "kind": "reference",
+            "sample": f"the reference's {isa} mvq_rows_f32 slot on the same rows, split in 64-row ranges over "
+                      f"{threads} threads and on one thread (the better kept)"},
+    }
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--workload", choices=["k3-decode", "single-expert", "kimi-prefill", "k3-miss", "kimi-decode",
-                                           "vq-encode"],
+                                           "vq-encode", "table-slots"],
                     default="k3-decode",
                     help="k3-decode (the headline line), single-expert (one expert's FFN, decode), kimi-prefill "
                          "(a 512-token Kimi-Linear-shape prefill), k3-miss (a 32-token K3 decode batch with half its "
                          "expert records streamed from host), kimi-decode (Kimi-Linear-shape decode, batch 1, with "
-                         "its shared expert) or vq-encode (the encoder on one K3 matrix)")
+                         "its shared expert), vq-encode (the encoder on one K3 matrix) or table-slots (the "
+                         "dispatch table's mvq_rows_f32 and kda_step slots as the engine calls them)")
     ap.add_argument("--only", action="store_true",
                     help="k3-decode: the headline line alone, without the other configurations' children")
     ap.add_argument("--twin-dir", default=None,
@@ -1146,6 +1312,9 @@ def main():
         return
     if args.workload == "vq-encode":
         print(json.dumps(run_vq_encode(args)))
+        return
+    if args.workload == "table-slots":
+        print(json.dumps(run_table_slots(args)))
         return
     if args.workload == "kimi-decode":
         args.layers = args.layers or 26
@@ -1226,7 +1395,7 @@ def main():
 # mode asked for and in the exact mode (its CPU baseline is the same)
 CHILDREN = [("single_expert", "single-expert", []), ("kimi_decode", "kimi-decode", []),
             ("kimi_prefill", "kimi-prefill", []), ("kimi_prefill_exact", "kimi-prefill", ["--prefill", "exact", "--no-cpu"]),
-            ("k3_miss", "k3-miss", [])]
+            ("k3_miss", "k3-miss", []), ("table_slots", "table-slots", [])]
 
 
 def run_children(args):
@@ -1263,6 +1432,11 @@ def run_children(args):
         except subprocess.TimeoutExpired:
             out[key] = {"error": f"did not finish in {args.child_timeout:.0f}s"}
         log(f"bench: configuration {key}: " + ("ok" if "error" not in out[key] else out[key]["error"]))
+    # the two prefill modes share their CPU baseline (the same 512 tokens
+    # through the reference's moe_chunk), measured once
+    fp, ex = out.get("kimi_prefill"), out.get("kimi_prefill_exact")
+    if fp and ex and "error" not in fp and "error" not in ex and fp.get("cpu_baseline") and not ex.get("cpu_baseline"):
+        ex["cpu_baseline"] = dict(fp["cpu_baseline"], shared_with="kimi_prefill")
     return out
 
 

@@ -639,15 +639,6 @@ __global__ __launch_bounds__(256) void k_mvq(const int8_t *__restrict__ W, const
     if (lane == 0) y[row] = acc;
 }
 
-extern "C" int wk_mvq(const int8_t *W, const uint16_t *ws, size_t rowbytes, int group, int bits,
-                      const float *x, int M, int N, int T, float *y, void *stream) {
-    if (M <= 0 || N <= 0 || T <= 0 || group <= 0 || (bits != 8 && bits != 4 && bits != 3)) return -1;
-    hipLaunchKernelGGL(k_mvq, dim3((M * T + 3) / 4), dim3(256), 0, (hipStream_t)stream, W, ws, rowbytes, group,
-                       bits, x, M, N, T, y);
-    CHECK_LAUNCH();
-    return 0;
-}
-
 // ---- decode: the shared expert inside the router and combine launches ---------------------
 
 // One wave's dot of a quantised row (Q8G: 16 weights per 16-byte chunk, Q4G:
@@ -696,6 +687,82 @@ struct QRow {
 };
 
 constexpr int SH_MAXC = 8;       // chunks per lane: rows up to 8192 (Q8G) or 16384 (Q4G) weights
+
+// Q8G / Q4G rows whose width is a whole number of 16-byte chunks and whose
+// group is a whole number of chunks (no chunk straddles a group or the row's
+// end), 16-byte aligned: a block of 4 waves takes MQF_RPB rows of one token,
+// with x staged in LDS once for them. A wave takes its rows one at a time;
+// lane l loads chunks l, l + 64, ... of the row as 16-byte loads (every load
+// of the row issued before the first multiply), multiplies each chunk with x
+// from LDS, scales the chunk's sum by its group's fp16 scale and the lanes'
+// sums are reduced. The loads of the wave's next row are issued before the
+// current row's arithmetic, so a wave keeps two rows in flight.
+constexpr int MQF_RPW = 4;                 // rows per wave
+constexpr int MQF_RPB = 4 * MQF_RPW;       // rows per block
+constexpr int MQF_MAXC = 8;                // chunks per lane: rows up to 8192 (Q8G) / 16384 (Q4G) weights
+
+template <int BITS, int MC>
+__global__ __launch_bounds__(256) void k_mvq_fast(const int8_t *__restrict__ W, const uint16_t *__restrict__ ws,
+                                                  size_t rowbytes, int g, const float *__restrict__ x, int M, int N,
+                                                  float *__restrict__ y) {
+    extern __shared__ __attribute__((aligned(16))) float xl[];
+    using Q = QRow<BITS, MC>;
+    const int t = blockIdx.y, wave = threadIdx.x >> 6;
+    const int nc = N / Q::WPC, ng = (N + g - 1) / g;
+    const int r0 = blockIdx.x * MQF_RPB + wave * MQF_RPW;
+    Q cur, nxt;
+    {
+        const int rr = min(r0, M - 1);
+        cur.load(W + (size_t)rr * rowbytes, ws + (size_t)rr * ng, g, nc);
+    }
+    const float *xt = x + (size_t)t * N;
+    for (int i = threadIdx.x; i < N / 4; i += 256) ((float4 *)xl)[i] = ((const float4 *)xt)[i];
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < MQF_RPW; q++) {
+        if (q + 1 < MQF_RPW) {
+            const int rr = min(r0 + q + 1, M - 1);
+            nxt.load(W + (size_t)rr * rowbytes, ws + (size_t)rr * ng, g, nc);
+        }
+        const float v = cur.dot(xl, nc);
+        if ((threadIdx.x & 63) == 0 && r0 + q < M) y[(size_t)t * M + r0 + q] = v;
+        if (q + 1 < MQF_RPW) cur = nxt;
+    }
+}
+
+template <int BITS>
+static int launch_mvq_fast(const int8_t *W, const uint16_t *ws, size_t rowbytes, int group, const float *x, int M,
+                           int N, int T, float *y, void *stream) {
+    const int mc = (N / (BITS == 8 ? 16 : 32) + 63) / 64;
+    const dim3 grid((M + MQF_RPB - 1) / MQF_RPB, T);
+    const size_t lds = (size_t)N * sizeof(float);
+#define MQF(n) hipLaunchKernelGGL((k_mvq_fast<BITS, n>), grid, dim3(256), lds, (hipStream_t)stream, W, ws, rowbytes, \
+                                  group, x, M, N, y)
+    if (mc <= 1) MQF(1);
+    else if (mc <= 2) MQF(2);
+    else if (mc <= 4) MQF(4);
+    else MQF(MQF_MAXC);
+#undef MQF
+    CHECK_LAUNCH();
+    return 0;
+}
+
+extern "C" int wk_mvq(const int8_t *W, const uint16_t *ws, size_t rowbytes, int group, int bits,
+                      const float *x, int M, int N, int T, float *y, void *stream) {
+    if (M <= 0 || N <= 0 || T <= 0 || group <= 0 || (bits != 8 && bits != 4 && bits != 3)) return -1;
+    if (bits != 3) {
+        const int wpc = bits == 8 ? 16 : 32;
+        if (N % wpc == 0 && group % wpc == 0 && N / wpc <= 64 * MQF_MAXC && (size_t)N * sizeof(float) <= 64 * 1024 &&
+            (rowbytes & 15) == 0 && ((uintptr_t)W & 15) == 0 && ((uintptr_t)x & 15) == 0 && (N & 3) == 0)
+            return bits == 8 ? launch_mvq_fast<8>(W, ws, rowbytes, group, x, M, N, T, y, stream)
+                             : launch_mvq_fast<4>(W, ws, rowbytes, group, x, M, N, T, y, stream);
+    }
+    hipLaunchKernelGGL(k_mvq, dim3((M * T + 3) / 4), dim3(256), 0, (hipStream_t)stream, W, ws, rowbytes, group,
+                       bits, x, M, N, T, y);
+    CHECK_LAUNCH();
+    return 0;
+}
+
 
 extern "C" int wk_shared_fast_ok(int H, const warp_shared_args *sa) {
     if (!sa || (sa->bits != 8 && sa->bits != 4) || H <= 0 || sa->inter <= 0 || (H & 3) || (sa->inter & 3))
