@@ -195,6 +195,7 @@ def run_gpu(args):
     ctx.sync()
     kms, kn = ctx.get_timing()
     ctx.set_timing(False)
+    args.kernel = ctx.matvec_kernel(0)
     out = bufs[(args.layers - 1) & 1].numpy()
     assert np.isfinite(out).all(), "non-finite hidden state after the stack"
     st = ctx.cache_stats()
@@ -231,17 +232,13 @@ def measured_traffic(kernel, launches):
     return {k: t[k]["read_bytes"] + t[k]["write_bytes"] for k in launches} | {"source": t["source"]}, None
 
 
-def matvec_roofline(kms, kn, b0, b1, path):
+def matvec_roofline(kms, kn, b0, b1, kernel):
     """The expert matvec's roofline terms from the per-launch timing classes:
     class 0 alone is the fused launch (gate/up, down and combine in one),
     else class 0 the gate/up and class 1 the down launches. b0, b1: the
     algorithmic bytes (codes and row scales of the picks) of gate/up and of
-    down for one token."""
+    down for one token; kernel: the one the context ran (matvec_kernel)."""
     fused = kn[0] > 0 and kn[1] == 0
-    if path == "mfma":
-        kernel = "k_vq_mfma"
-    else:
-        kernel = "k_moe_fused" if fused else "k_vq_lut"
     if fused:
         t = kms[0]
         nbytes = kn[0] * (b0 + b1)
@@ -407,6 +404,7 @@ def run_single_expert(args):
     ctx.sync()
     kms, kn = ctx.get_timing()
     ctx.set_timing(False)
+    ctx_kernel = ctx.matvec_kernel(0, expert_ffn=True)
     assert np.isfinite(Y.numpy()).all(), "non-finite expert output"
     if graph is not None:
         graph.free()
@@ -418,7 +416,7 @@ def run_single_expert(args):
     b1 = down + 2 * KH
     achieved = (kn[0] * b0 + kn[1] * b1) / ((kms[0] + kms[1]) / 1e3) / 1e9 if kn[0] and kn[1] else None
     ffn_gbs = pair / (us_ffn * 1e-6) / 1e9
-    kernel = "k_vq_lut" if args.matvec_path == "auto" else "k_vq_mfma"
+    kernel = ctx_kernel
     return {
         "metric": "single-expert SwiGLU FFN decode tokens/s (one expert per token), 1 MI355X",
         "value": round(n_ffn / (ms / 1e3), 1),
@@ -714,6 +712,7 @@ def run_kimi_decode(args):
     ctx.sync()
     kms, kn = ctx.get_timing()
     ctx.set_timing(False)
+    mv_kernel = ctx.matvec_kernel(0)
     assert np.isfinite(bufs[(layers - 1) & 1].numpy()).all(), "non-finite hidden state after the stack"
     if graph is not None:
         graph.free()
@@ -721,7 +720,7 @@ def run_kimi_decode(args):
     n_lt = args.steps * layers
     b0 = KK * (2 * gate + 2 * 2 * KI)
     b1 = KK * (down + 2 * KH)
-    kernel, fused, achieved, per = matvec_roofline(kms, kn, b0, b1, args.matvec_path)
+    kernel, fused, achieved, per = matvec_roofline(kms, kn, b0, b1, mv_kernel)
     per_layer = (KK * (2 * gate + down + scales_b) + shared_bytes + KE * KH * 4 + 3 * S * EN * 8 * 2 + KE * 4
                  + 2 * KH * 4)
     layer_gbs = per_layer * n_lt / (ms / 1e3) / 1e9
@@ -1344,7 +1343,7 @@ def main():
     gate, down, scales_b, _ = rec_layout()
     b0 = K * (2 * gate + 2 * 2 * I)               # codes + gate/up row scales per gate/up launch
     b1 = K * (down + 2 * H)                       # codes + down row scales per down launch
-    kernel, fused, achieved, per = matvec_roofline(kms, kn, b0, b1, args.matvec_path)
+    kernel, fused, achieved, per = matvec_roofline(kms, kn, b0, b1, args.kernel)
     layer_gbs = layer_bytes() * layer_tokens / (ms / 1e3) / 1e9
     tr, tr_why = measured_traffic(kernel, ("fused",) if fused else ("gate_up", "down"))
     traffic = None

@@ -1711,6 +1711,14 @@ static int use_table(const warp_hip_ctx *c, const layer_t *L)
     return c->lut_ok && L->books && (c->mv_path != WARP_HIP_PATH_MFMA || L->books_x31);
 }
 
+const char *warp_hip_matvec_kernel(warp_hip_ctx *c, int layer, int experts)
+{
+    if (!c || layer < 0 || layer >= c->cfg.n_layers) return "none";
+    const layer_t *L = &c->L[layer];
+    if (use_table(c, L)) return c->mv_path == WARP_HIP_PATH_LUT_FUSED && experts > 1 ? "k_moe_fused" : "k_vq_lut";
+    return c->P6 ? "k_apply_p6" : "k_vq_mfma";
+}
+
 /* E_ARG where such a layer's shapes rule the table kernel out. */
 static int x31_check(warp_hip_ctx *c, const layer_t *L, int layer)
 {

@@ -134,6 +134,7 @@ SIGNATURES = {
     "warp_hip_put_expert_dev": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p]),
     "warp_hip_put_expert_synth": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_uint64, C.c_void_p]),
     "warp_hip_set_matvec_path": (C.c_int, [C.c_void_p, C.c_int]),
+    "warp_hip_matvec_kernel": (C.c_char_p, [C.c_void_p, C.c_int, C.c_int]),
     "warp_hip_set_timing": (C.c_int, [C.c_void_p, C.c_int]),
     "warp_hip_get_timing": (C.c_int, [C.c_void_p, C.POINTER(C.c_double), C.POINTER(C.c_uint64)]),
     "warp_hip_sync": (C.c_int, [C.c_void_p]),
@@ -373,6 +374,10 @@ class Context:
         per layer where it routes the token itself)."""
         code = {"auto": 0, "mfma": 1, "fused": 2}[path]
         self._check(lib().warp_hip_set_matvec_path(self.h, code))
+
+    def matvec_kernel(self, layer, expert_ffn=False):
+        """The expert matvec kernel a decode of `layer` runs on the current path."""
+        return lib().warp_hip_matvec_kernel(self.h, layer, 1 if expert_ffn else self.cfg.top_k).decode()
 
     def set_timing(self, on):
         self._check(lib().warp_hip_set_timing(self.h, int(on)))
