@@ -97,12 +97,21 @@ def layer_bytes():
     return K * pair_bytes() + E * H * 4 + 3 * S * EN * 8 * 2 + E * 4 + 2 * H * 4
 
 
-def setup(layers, resident, seed=1234, router_strict=False):
+ROUTERS = {
+    "cert": "certified (fast exact-sum logits with error bounds; rows whose bounds leave the picks or their order "
+            "open recomputed in the reference's sequential order: the reference's picks by construction)",
+    "fast": "fast (fixed-order tree logits, picks not certified)",
+    "strict": "strict (every logit summed sequentially: bit-exact logits)",
+}
+
+
+def setup(layers, resident, seed=1234, router="cert"):
     import warp_amd
     gate, down, scales_b, rec_bytes = rec_layout()
     ctx = warp_amd.Context(hidden=H, inter=I, n_experts=E, top_k=K, n_layers=layers, fmt="VQ12",
                            renorm=True, routed_scale=1.0, max_tokens=1, rec_bytes=rec_bytes,
-                           cache_bytes=layers * resident * rec_bytes, router_strict=router_strict)
+                           cache_bytes=layers * resident * rec_bytes, router_strict=router == "strict",
+                           router_fast=router == "fast")
     rng = np.random.Generator(np.random.PCG64(seed))
     t0 = time.time()
     for L in range(layers):
@@ -124,7 +133,7 @@ def setup(layers, resident, seed=1234, router_strict=False):
 
 def run_gpu(args):
     from warp_amd.device import Buf, Event
-    ctx, rec_bytes = setup(args.layers, args.resident, router_strict=args.router_strict)
+    ctx, rec_bytes = setup(args.layers, args.resident, router=args.router)
     ctx.set_matvec_path(args.matvec_path)
     n_in = max(args.steps, args.warmup, 1)
     X = Buf.of(np.random.default_rng(7).standard_normal((n_in, H), dtype=np.float32))
@@ -175,6 +184,7 @@ def run_gpu(args):
             timed(s)
         ctx.sync()
     e0, e1 = Event(), Event()
+    rs0 = ctx.route_stats()
     # timed steps: nothing but the layers on the stream
     log(f"bench: timing {args.steps} steps of {args.layers} layers" + (" (graph replays)" if graph else ""))
     t0 = time.perf_counter()
@@ -186,6 +196,43 @@ def run_gpu(args):
     ctx.sync()
     wall = time.perf_counter() - t0
     ms = e0.elapsed_ms(e1)
+    rs1 = ctx.route_stats()
+    routings = args.steps * args.layers
+    args.route_recompute = {"routings": routings, "recomputed": rs1["recomputed"] - rs0["recomputed"],
+                            "rows": rs1["rows"] - rs0["rows"],
+                            "rate": round((rs1["recomputed"] - rs0["recomputed"]) / routings, 4)}
+    args.router_cost = None
+    if args.router == "cert":
+        # what the certificate costs: the same steps from the fast logits'
+        # picks, uncertified, in this process on the same inputs
+        ctx.set_router_fast(True)
+        g2 = Graph(stream, body) if graph is not None else None
+
+        def timed_fast(s):
+            if g2 is None:
+                step(s)
+                return
+            copy_async(stage.ptr, X.ptr + (s % n_in) * H * 4, H * 4, D2D, stream)
+            g2.launch()
+
+        for s in range(args.warmup):
+            timed_fast(s)
+        ctx.sync()
+        f0, f1 = Event(), Event()
+        f0.record(stream)
+        for s in range(args.steps):
+            timed_fast(s)
+        f1.record(stream)
+        f1.synchronize()
+        ms_fast = f0.elapsed_ms(f1)
+        if g2 is not None:
+            g2.free()
+        ctx.set_router_fast(False)
+        args.router_cost = {"certified_ms_per_step": round(ms / args.steps, 4),
+                            "uncertified_ms_per_step": round(ms_fast / args.steps, 4),
+                            "overhead": round(ms / ms_fast - 1.0, 4)}
+        log(f"bench: certified selection {ms / args.steps:.3f} ms/step, uncertified {ms_fast / args.steps:.3f} "
+            f"ms/step ({100 * (ms / ms_fast - 1):.1f}% overhead), recompute rate {args.route_recompute['rate']}")
     # the same steps again with HIP events around each expert-matvec and
     # router launch, for the per-kernel durations
     log("bench: per-launch timing pass")
@@ -1281,8 +1328,10 @@ def main():
     ap.add_argument("--no-graph", dest="graph", action="store_false",
                     help="k3-decode, kimi-decode: launch every kernel from the host instead of replaying one "
                          "captured step")
-    ap.add_argument("--router-strict", action="store_true",
-                    help="K3 decode: router logits in the reference's sequential summation order (bit-exact)")
+    ap.add_argument("--router", choices=sorted(ROUTERS), default="cert",
+                    help="K3 decode: cert = certified selection (the reference's picks by construction), fast = "
+                         "the fast logits' picks uncertified, strict = every logit in the reference's sequential "
+                         "order")
     ap.add_argument("--matvec-path", choices=["auto", "mfma", "fused"], default="auto",
                     help="expert matvec kernel: auto = the LUT kernel, mfma = decode-then-dot on the matrix cores, "
                          "fused = the LUT kernel's gate/up, down and combine in one launch per layer")
@@ -1365,7 +1414,9 @@ def main():
         "dtype": "fp32",
         "data": "synthetic (random codes, codebooks, scales and routers of the K3 shapes)",
         "launch": "one step captured as a HIP graph and replayed per token" if args.graph else "host launches",
-        "router": "strict (sequential sums, bit-exact logits)" if args.router_strict else "fast (fixed-order tree)",
+        "router": ROUTERS[args.router],
+        "router_recompute": args.route_recompute if args.router == "cert" else None,
+        "router_cost": args.router_cost,
         "config": {"workload": "K3-scale MoE decode layer, batch 1, 60-layer stack",
                    "hidden": H, "inter": I, "experts": E, "top_k": K, "layers": layers,
                    "format": "RVQ 2x4096 12-bit codes (3.00 b/w)", "resident_per_layer": args.resident,

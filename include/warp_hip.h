@@ -232,7 +232,9 @@ typedef struct {
     int router_act;        /* WARP_HIP_ROUTE_SIGMOID is the reference; SOFTMAX
                             * is the extension                                 */
     int router_strict;     /* 1: F32 router logits in the reference's
-                            * sequential fp32 order (bit-identical logits)     */
+                            * sequential fp32 order (bit-identical logits)
+                            * everywhere; 2: so in chunks, while decode
+                            * certifies its selection (router_fast)          */
     int act_situ;          /* hidden_act == "situ"                             */
     float situ_beta, situ_linear_beta;
     int max_tokens;        /* largest chunk warp_hip_moe_chunk will be given   */
@@ -270,6 +272,18 @@ typedef struct {
                             * satisfy codebook_id + 3*stages <= n_books, as
                             * record_check requires (src/model.c:1721-1723);
                             * 0: n_layers * 3 * stages, one set per layer    */
+    int router_fast;       /* decode with an F32 router and sigmoid scores
+                            * certifies its selection by default: the router
+                            * launch bounds each logit's distance from the
+                            * reference's sequential sum, and the routing
+                            * recomputes, in the reference's order, the rows
+                            * whose bounds leave the picks or their order
+                            * open, so the picks are the reference's (see
+                            * warp_hip_get_route_stats). 1: the fast logits'
+                            * picks as they are (a near-tie may order
+                            * differently); router_strict overrides both.
+                            * Chunks take the fast logits unless
+                            * router_strict                                  */
 } warp_hip_cfg;
 
 typedef struct warp_hip_ctx warp_hip_ctx;
@@ -355,6 +369,22 @@ int warp_hip_put_expert(warp_hip_ctx *c, int layer, int expert, const uint8_t *r
  * the copy stream; not counted as misses. */
 int warp_hip_prefetch(warp_hip_ctx *c, int layer, const int *ids, int n);
 void warp_hip_get_cache_stats(const warp_hip_ctx *c, warp_hip_cache_stats *st);
+
+/* The certified router's arrays for one token of `layer` (sigmoid scores,
+ * F32 router): out_dev [4][E] = point scores, point biased scores, and
+ * lower and upper bounds of the biased score that the reference's
+ * sequential logit gives (src/model.c:155-160, 2723-2726). For checking and
+ * for callers that rank themselves; no counterpart in the reference. */
+int warp_hip_router_cert(warp_hip_ctx *c, int layer, const float *x_dev, float *out_dev);
+
+/* Certified selection's counters since open: decode routings certified,
+ * how many of them recomputed rows, and the rows recomputed. Waits for the
+ * context's stream. No counterpart in the reference (whose router is the
+ * sequential sum itself). */
+typedef struct {
+    uint64_t certified, recomputed, rows;
+} warp_hip_route_stats;
+int warp_hip_get_route_stats(warp_hip_ctx *c, warp_hip_route_stats *st);
 
 /* Replaces moe_layer (src/model.c:2713-2940) for one token: router, top-k,
  * K expert FFNs, combine in selection order, shared expert. x_dev, out_dev:
@@ -461,6 +491,10 @@ int warp_hip_put_expert_synth(warp_hip_ctx *c, int layer, int expert, uint64_t s
  * warp_hip_expert_ffn and warp_hip_vq_matvec. */
 enum { WARP_HIP_PATH_AUTO = 0, WARP_HIP_PATH_MFMA = 1, WARP_HIP_PATH_LUT_FUSED = 2 };
 int warp_hip_set_matvec_path(warp_hip_ctx *c, int path);
+/* cfg.router_fast after open: 1 decodes from the fast logits' picks without
+ * certifying them, 0 certifies (the default). For measuring what the
+ * certificate costs; no counterpart in the reference. */
+int warp_hip_set_router_fast(warp_hip_ctx *c, int fast);
 /* The expert matvec kernel the current path runs for a decode of `layer`
  * (experts = 1: warp_hip_expert_ffn's single expert, else the layer's
  * top_k): "k_vq_lut", "k_moe_fused", "k_vq_mfma" or "k_apply_p6". For

@@ -348,6 +348,9 @@ struct warp_hip_ctx {
     int pin_layer;                  /* the layer `hold` belongs to, or -1  */
     /* device scratch */
     float *logits;
+    unsigned long long *cert_ctr;  /* certified decode routings that recomputed, rows recomputed */
+    unsigned *cert_done;           /* the certifying router's row words (after cert_ctr) */
+    warp_hip_route_stats route_stats;
     int *idx;
     float *w;
     warp_job *jobs;
@@ -471,8 +474,13 @@ static int ctx_alloc(warp_hip_ctx *c)
     if (c->max_jobs < K) c->max_jobs = K;
     const size_t nvH = (size_t)He / 8, nvI = (size_t)I / 8;
     const size_t nblkH = (nvH + WARP_LUT_BLK - 1) / WARP_LUT_BLK, nblkI = (nvI + WARP_LUT_BLK - 1) / WARP_LUT_BLK;
-    /* at least two rows: one token's scores and biased scores (wk_router_scored) */
-    DMALLOC(c, c->logits, (size_t)(T > 2 ? T : 2) * E * 4);
+    /* at least four rows: one token's scores, biased scores and their
+     * bounds (wk_router_cert) */
+    DMALLOC(c, c->logits, (size_t)(T > 4 ? T : 4) * E * 4);
+    /* the certification's counters, then one word per expert */
+    DMALLOC(c, c->cert_ctr, 2 * sizeof(unsigned long long) + (size_t)E * sizeof(unsigned));
+    DEV(c, hipMemset(c->cert_ctr, 0, 2 * sizeof(unsigned long long) + (size_t)E * sizeof(unsigned)));
+    c->cert_done = (unsigned *)(c->cert_ctr + 2);
     DMALLOC(c, c->idx, P * 4);
     DMALLOC(c, c->w, P * 4);
     DMALLOC(c, c->jobs, (size_t)3 * c->max_jobs * sizeof(warp_job));
@@ -693,7 +701,7 @@ void warp_hip_close(warp_hip_ctx *c)
                   c->lscale, c->lscaled, c->counts, c->offsets, c->pair_tok, c->pair_exp, c->pair_w, c->tok_slots, c->runs,
                   c->xin, c->xout, c->la_logits, c->la_idx, c->la_w, c->table_dev, c->pool, c->part,
                   c->shxs, c->shxscale, c->shxin, c->shxinscale, c->tq_dev, c->crc_tmp, c->crc_bad, c->crc_err, c->xlat, c->ylat, c->yup,
-                  c->fz_sync, c->run_queue };
+                  c->fz_sync, c->run_queue, c->cert_ctr };
     for (size_t i = 0; i < sizeof d / sizeof d[0]; i++) hfree(d[i]);
     hhfree(c->h_idx); hhfree(c->h_w); hhfree(c->h_la_idx); hhfree(c->h_missing); hhfree(c->staging);
     hhfree(c->h_crc_err); hhfree(c->h_word);
@@ -748,7 +756,8 @@ static int take_missing(warp_hip_ctx *c)
         DEV(c, hipMemset(c->missing, 0, sizeof(int)));
         if (flag & 4)
             return set_err(c, WARP_HIP_E_DEVICE, -1, -1,
-                           "a fused decode launch gave up waiting for its work items: its outputs are not valid");
+                           "a decode launch gave up waiting (the fused launch for its work items, or the "
+                           "certifying router for its rows): its outputs are not valid");
         return set_err(c, WARP_HIP_E_MISSING, -1, -1,
                        "a selected expert was not resident: the affected layers were not computed");
     }
@@ -1358,6 +1367,18 @@ void warp_hip_get_cache_stats(const warp_hip_ctx *c, warp_hip_cache_stats *st)
     st->resident = r;
 }
 
+int warp_hip_get_route_stats(warp_hip_ctx *c, warp_hip_route_stats *st)
+{
+    if (!c || !st) return WARP_HIP_E_ARG;
+    unsigned long long d[2];
+    DEV(c, hipStreamSynchronize(c->st));
+    DEV(c, hipMemcpy(d, c->cert_ctr, sizeof d, hipMemcpyDeviceToHost));
+    *st = c->route_stats;
+    st->recomputed = d[0];
+    st->rows = d[1];
+    return 0;
+}
+
 /* Fetch (layer, expert) through the caller's fetch function into a pinned
  * staging buffer (or find it in the caller's pinned memory), check it, and
  * copy it into a slot on the copy stream. The caller orders the copy stream
@@ -1536,6 +1557,13 @@ int warp_hip_set_matvec_path(warp_hip_ctx *c, int path)
     return 0;
 }
 
+int warp_hip_set_router_fast(warp_hip_ctx *c, int fast)
+{
+    if (!c) return WARP_HIP_E_ARG;
+    c->cfg.router_fast = fast != 0;
+    return 0;
+}
+
 int warp_hip_set_timing(warp_hip_ctx *c, int on)
 {
     if (!c) return WARP_HIP_E_ARG;
@@ -1580,13 +1608,24 @@ static int logits_of(warp_hip_ctx *c, const layer_t *L, const float *x, int T, f
     return -1;
 }
 
+/* Whether a decode of this layer certifies its selection: sigmoid scores
+ * from an fp32 router, neither strict logits (router_strict 1) nor plain
+ * fast ones asked for, a shape the certifying kernels take. */
+static int cert_ok(const warp_hip_ctx *c, const layer_t *L)
+{
+    const warp_hip_cfg *g = &c->cfg;
+    return L->router && g->router_strict != 1 && !g->router_fast && g->router_act == WARP_HIP_ROUTE_SIGMOID &&
+           g->hidden % 4 == 0 && g->hidden <= 16384 && g->n_experts <= 4096;
+}
+
 /* The layer's shared expert as the fused decode kernels take it: an fp32
- * router with the fast (tree) sum, the hidden state in shh. */
+ * router with the fast (tree) sum or the certifying one, the hidden state
+ * in shh. */
 static int shared_args(const warp_hip_ctx *c, const layer_t *L, warp_shared_args *sa)
 {
     const warp_hip_cfg *g = &c->cfg;
     memset(sa, 0, sizeof *sa);
-    if (!L->sq[0] || !L->router || g->router_strict || !c->shh) return 0;
+    if (!L->sq[0] || !L->router || (g->router_strict && !cert_ok(c, L)) || !c->shh) return 0;
     for (int k = 0; k < 3; k++) {
         sa->q[k] = L->sq[k];
         sa->s[k] = L->ss[k];
@@ -1728,6 +1767,27 @@ static int x31_check(warp_hip_ctx *c, const layer_t *L, int layer)
     return 0;
 }
 
+/* One token's routing from c->logits into idx / w, and with jobs = 1 the
+ * job lists from the layer's table (ra->table); certified where ra says so. */
+static int route_one(warp_hip_ctx *c, const warp_route_args *ra, int K, int jobs, hipStream_t s)
+{
+    const warp_hip_cfg *g = &c->cfg;
+    if (ra->scored == 2) {
+        warp_route_args r = *ra;
+        if (!jobs) {
+            r.cctr = NULL;                     /* counted on the call with the job lists */
+            r.table = NULL;
+            r.jobs = NULL;
+            r.njobs = NULL;
+            r.missing = NULL;
+        }
+        return wk_route_cert(&r, K, s);
+    }
+    return wk_route(ra->logits, ra->bias, ra->E, K, 1, g->router_act, g->renorm, g->routed_scale, ra->idx, ra->w,
+                    jobs ? ra->table : NULL, jobs ? ra->jobs : NULL, jobs ? ra->njobs : NULL,
+                    jobs ? ra->missing : NULL, ra->inter, s);
+}
+
 int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *out_dev, const float *resid_dev,
                         int *idx, float *w)
 {
@@ -1771,7 +1831,7 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
     /* with the table kernel, a Q8G/Q4G shared expert runs inside the router
      * launch (gate, up, act) and the combine (down) */
     warp_shared_args sa;
-    const int fuse_shared = use_lut && !lat && shared_args(c, L, &sa) && wk_shared_fast_ok(H, &sa);
+    int fuse_shared = use_lut && !lat && shared_args(c, L, &sa) && wk_shared_fast_ok(H, &sa);
     /* where the device routes with the expert table, the table kernel's
      * gate/up launch does the routing itself (one launch less) */
     const int fuse_route = use_lut && !foreign && (L->resident == E || !can_fetch(c)) &&
@@ -1788,24 +1848,43 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
                    (size_t)sa.inter * sizeof(float) <= 64 * 1024 && sa.inter / (sa.bits == 8 ? 16 : 32) <= 256 &&
                    (H + 63) / 64 < c->n_cu / 2;
     }
-    /* then, for sigmoid scores from an fp32 router, the router launch also
+    /* sigmoid scores from an fp32 router: the selection is certified (the
+     * router launch bounds every logit against the reference's sequential
+     * sum, and its last block recomputes the rows those bounds leave
+     * unordered), unless the caller asked for the plain fast logits or
+     * strict ones; the certifying router launch computes no shared expert */
+    const int cert = cert_ok(c, L);
+    if (cert && fuse_shared && !sh_in_gu) fuse_shared = 0;
+    /* else, for sigmoid scores from an fp32 router, the router launch also
      * scores (one pass less in the routing prologue) */
     const int scored = fuse_route && (!fuse_shared || sh_in_gu) && L->router && !g->router_strict &&
                        g->router_act == WARP_HIP_ROUTE_SIGMOID;
     if ((rc = timing_begin(c, 2))) return rc;
-    if (fuse_shared && !sh_in_gu) KRN(c, wk_router_shared(L->router, x_dev, E, H, c->logits, &sa, c->st));
+    if (cert)
+        KRN(c, wk_router_cert(L->router, x_dev, E, H, L->bias, c->logits, c->cert_done, K, c->cert_ctr, c->missing,
+                              c->st));
+    else if (fuse_shared && !sh_in_gu) KRN(c, wk_router_shared(L->router, x_dev, E, H, c->logits, &sa, c->st));
     else if (scored) KRN(c, wk_router_scored(L->router, x_dev, E, H, L->bias, c->logits, c->st));
     else KRN(c, logits_of(c, L, x_dev, 1, c->logits, c->st));
     if ((rc = timing_end(c))) return rc;
+    if (cert) {
+        c->route_stats.certified++;
+        c->missing_pending = 1;            /* (the flag's bit 2 if the router's last block gave up) */
+    }
+    /* the routing's arguments: the table kernel's fused routing reads the
+     * (certified) scores and biased scores, the routing launch all four
+     * certified arrays; table and jobs are set where the job lists are
+     * wanted */
+    warp_route_args ra = { c->logits, L->bias, table, E, g->router_act, g->renorm, I, g->routed_scale,
+                           c->idx, c->w, c->jobs, c->njobs, c->missing, cert ? (fuse_route ? 1 : 2) : scored,
+                           L->router, x_dev, H, c->cert_ctr };
     const int n_la = lookahead_launch(c, layer, x_dev, 1);
     if (n_la < 0) return n_la;
     if (L->resident == E && !foreign) {
         /* everything resident: route and build the jobs on the device, no
          * host round trip */
         KRN(c, wait_copies(c));
-        if (!fuse_route)
-            KRN(c, wk_route(c->logits, L->bias, E, K, 1, g->router_act, g->renorm, g->routed_scale, c->idx, c->w,
-                            table, c->jobs, c->njobs, c->missing, I, c->st));
+        if (!fuse_route) KRN(c, route_one(c, &ra, K, 1, c->st));
         c->stats.hits += (uint64_t)K;
         release_hold(c, layer);
     } else if (!can_fetch(c) && !foreign) {
@@ -1813,14 +1892,11 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
          * not resident (sticky), the combine poisons this layer's output with
          * NaN, and the next synchronising call reports E_MISSING */
         KRN(c, wait_copies(c));
-        if (!fuse_route)
-            KRN(c, wk_route(c->logits, L->bias, E, K, 1, g->router_act, g->renorm, g->routed_scale, c->idx, c->w,
-                            table, c->jobs, c->njobs, c->missing, I, c->st));
+        if (!fuse_route) KRN(c, route_one(c, &ra, K, 1, c->st));
         c->missing_pending = 1;
         release_hold(c, layer);
     } else {
-        KRN(c, wk_route(c->logits, L->bias, E, K, 1, g->router_act, g->renorm, g->routed_scale, c->idx, c->w, NULL,
-                        NULL, NULL, NULL, 0, c->st));
+        KRN(c, route_one(c, &ra, K, 0, c->st));
         DEV(c, hipMemcpyAsync(c->h_idx, c->idx, (size_t)K * sizeof(int), hipMemcpyDeviceToHost, c->st));
         DEV(c, hipStreamSynchronize(c->st));
         if ((rc = ensure_selected(c, layer, c->h_idx, K))) return rc;
@@ -1832,8 +1908,8 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
             KRN(c, wk_lut_p6(xe, 1, He, books_kind(c, B, 1), c->lut8 + nvH * 256, c->lscale + nblkH, c->st));
         }
         KRN(c, wait_copies(c));
-        KRN(c, wk_route(c->logits, L->bias, E, K, 1, g->router_act, g->renorm, g->routed_scale, c->idx, c->w, table,
-                        c->jobs, c->njobs, c->missing, I, c->st));
+        /* (the selection again, now with the job lists: the same picks) */
+        KRN(c, route_one(c, &ra, K, 1, c->st));
     }
     DEV(c, hipEventRecord(c->ev_before, c->st));
 
@@ -1844,8 +1920,6 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
     if (use_lut && fuse_route && !fuse_shared && c->mv_path == WARP_HIP_PATH_LUT_FUSED) {
         /* gate/up, down and the combine in one launch */
         if (L->sq[0] && (rc = shared_ffn(c, L, x_dev, 1, c->st))) return rc;
-        const warp_route_args ra = { c->logits, L->bias, table, E, g->router_act, g->renorm, I, g->routed_scale,
-                                     c->idx, c->w, c->jobs, c->njobs, c->missing, scored };
         if ((rc = timing_begin(c, 0))) return rc;
         KRN(c, wk_moe_fused(g->fmt, B->books, B->books_x31, xe, K, I, He, c->part, c->part_cap, c->n_cu,
                             g->act_situ, g->situ_beta, g->situ_linear_beta, &ra, add0, add1, ysum, c->fz_sync,
@@ -1861,8 +1935,6 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
     size_t d_off = 0;
     if (use_lut) {
         int sp_gu = 0;
-        const warp_route_args ra = { c->logits, L->bias, table, E, g->router_act, g->renorm, I, g->routed_scale,
-                                     c->idx, c->w, c->jobs, c->njobs, c->missing, scored };
         if ((rc = timing_begin(c, 0))) return rc;
         KRN(c, wk_vq_lut(g->fmt, c->jobs, c->njobs, K, 0, 2, B->books, B->books_x31, xe, 1, c->part, c->part_cap, I, He,
                          c->n_cu, NULL, 0, 0, 0.0f, 0.0f, fuse_route ? &ra : NULL, sh_in_gu ? &sa : NULL, NULL, &sp_gu,
@@ -2294,6 +2366,19 @@ int warp_hip_router_logits(warp_hip_ctx *c, int layer, const float *x_dev, int T
     int rc = check_layer(c, layer);
     if (rc) return rc;
     KRN(c, logits_of(c, &c->L[layer], x_dev, T, logits_dev, c->st));
+    DEV(c, hipStreamSynchronize(c->st));
+    return 0;
+}
+
+int warp_hip_router_cert(warp_hip_ctx *c, int layer, const float *x_dev, float *out_dev)
+{
+    int rc = check_layer(c, layer);
+    if (rc) return rc;
+    const warp_hip_cfg *g = &c->cfg;
+    const layer_t *L = &c->L[layer];
+    if (!L->router || g->router_act != WARP_HIP_ROUTE_SIGMOID)
+        return set_err(c, WARP_HIP_E_ARG, layer, -1, "certified router needs an F32 router and sigmoid scores");
+    KRN(c, wk_router_cert(L->router, x_dev, g->n_experts, g->hidden, L->bias, out_dev, NULL, 0, NULL, NULL, c->st));
     DEV(c, hipStreamSynchronize(c->st));
     return 0;
 }

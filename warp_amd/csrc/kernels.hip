@@ -444,6 +444,411 @@ __global__ __launch_bounds__(256) void k_router_scored(const float *__restrict__
     }
 }
 
+// Coherent accesses, for what one block of the fused decode launch writes
+// for another, which may run on another XCD (another L2): agent-scope
+// atomic stores and loads (relaxed), which the memory model lowers to
+// accesses that bypass a stale or write-back copy in the XCD's L2 (sc1), so
+// the values reach, and are read from, memory every XCD sees. Nothing here
+// rests on how a plain or volatile access is lowered. A wave's stores are
+// complete once wait_stores() returns, so with a barrier after it the block
+// can raise a count that others poll, without writing back the L2 (which an
+// agent-scope release fence does, at a cost that grows with everything the
+// XCD's other blocks have written).
+__device__ __forceinline__ void st_through4(float *p, float a, float b, float c, float d) {   // p in global memory
+    __hip_atomic_store(p + 0, a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(p + 1, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(p + 2, c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(p + 3, d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(float *p, float a) {
+    __hip_atomic_store(p, a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float *p) {
+    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0x0F70); }   // vmcnt(0)
+
+// ---- certified routing (decode, sigmoid scores, fp32 router) ---------------------------
+//
+// The reference's router logit is a sequential, unfused fp32 sum
+// (dotf, src/model.c:155-160): s_k = fl(s_{k-1} + fl(w_k x_k)). Its rounding
+// errors are bounded by u (sum_k |s_k| + sum_k |w_k x_k|), u = 2^-24. A
+// certified row computes the exact sum S* (the fp32 products are exact in
+// double, summed in double), the running sums' magnitudes from a prefix
+// scan, and that bound B; the reference's logit lies in [S* - B, S* + B].
+// The routing ranks the point scores of fp32(S*) and keeps, for each
+// expert, the interval its biased score can take (the score function and
+// the bias addition are monotone; one ulp is added each way). Where the
+// interval of a pick overlaps one ranked after it, the order is not certain
+// from the bounds alone: those rows' logits are recomputed with the
+// reference's own sequential sum (route_certify) and the picks made again.
+// The picks and their order are then the reference's by construction.
+constexpr double CERT_U = 5.9604644775390625e-08;         // 2^-24
+constexpr int CERT_MAXV = 16;                               // float4 per thread: H <= 16384
+constexpr int CERT_EMAX = 4096;                             // experts the certification takes
+
+// The neighbouring floats toward -inf and +inf (NaN and the infinity on that
+// side unchanged).
+__device__ __forceinline__ float f_down(float v) {
+    if (v != v || v == -INFINITY) return v;
+    if (v == 0.0f) return -__uint_as_float(1u);
+    const uint32_t u = __float_as_uint(v);
+    return __uint_as_float(v > 0.0f ? u - 1u : u + 1u);
+}
+__device__ __forceinline__ float f_up(float v) { return -f_down(-v); }
+
+__device__ __forceinline__ float cert_score(float l, const uint64_t *etab = nullptr) {
+    return __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_ref(-l, etab)));
+}
+
+// Row e's outputs from its exact sum S, the sum of its running sums'
+// magnitudes (as) and of its products' magnitudes (ap): the reference's
+// rounding errors are bounded by u (as + ap) up to terms of relative size
+// n u (its running sums are within that bound of these), plus this code's
+// own double arithmetic; products that underflow in fp32 are off by at most
+// 2^-149 each. The logit interval is widened to floats outward, and the
+// biased-score bounds by one more ulp each way for the score and the sum.
+__device__ __forceinline__ void cert_finish(double S, double as, double ap, int H, int E, int e,
+                                            const float *__restrict__ bias, float *__restrict__ out) {
+    const double n = (double)H;
+    const double B = CERT_U * (as + 1.01 * ap) * (1.0 + 4.0 * n * CERT_U) + 1e-12 * (as + ap) + n * 1.4e-45;
+    const float l = (float)S;
+    const float lo = f_down((float)(S - B)), hi = f_up((float)(S + B));
+    const float bv = bias ? bias[e] : 0.0f;
+    const float sc = cert_score(l);
+    st_agent(out + e, sc);
+    st_agent(out + E + e, __fadd_rn(sc, bv));
+    const bool ok = isfinite(S) && isfinite(B) && isfinite(lo) && isfinite(hi);
+    st_agent(out + 2 * E + e, ok ? f_down(__fadd_rn(f_down(cert_score(lo)), bv)) : -INFINITY);
+    st_agent(out + 3 * E + e, ok ? f_up(__fadd_rn(f_up(cert_score(hi)), bv)) : INFINITY);
+}
+
+// The same by three lanes (lane 0 the point score, 1 the lower bound, 2 the
+// upper bound), from S and upper bounds as, ap of the sums of magnitudes.
+__device__ __forceinline__ void cert_finish3(double S, double as, double ap, int H, int E, int e, int lane,
+                                             const float *__restrict__ bias, float *__restrict__ out) {
+    const double n = (double)H;
+    const double B = CERT_U * (as + ap) * (1.0 + 4.0 * n * CERT_U) + 1e-12 * (as + ap) + n * 1.4e-45;
+    const float lo = f_down((float)(S - B)), hi = f_up((float)(S + B));
+    const bool ok = isfinite(S) && isfinite(B) && isfinite(lo) && isfinite(hi);
+    const float l = lane == 0 ? (float)S : !ok ? 0.0f : lane == 1 ? lo : hi;
+    const float sc = cert_score(l);
+    const float bv = bias ? bias[e] : 0.0f;
+    if (lane == 0) {
+        st_agent(out + e, sc);
+        st_agent(out + E + e, __fadd_rn(sc, bv));
+    } else if (lane == 1) {
+        st_agent(out + 2 * E + e, ok ? f_down(__fadd_rn(f_down(sc), bv)) : -INFINITY);
+    } else {
+        st_agent(out + 3 * E + e, ok ? f_up(__fadd_rn(f_up(sc), bv)) : INFINITY);
+    }
+}
+
+// The same by one lane, without the reference's expf, for |S| + B < 30:
+// sigma(S) in double from the hardware exponential (relative error at most
+// (|S| + 2) 2^-20 for it, with the rounding of S to float), the biased
+// score's bounds from sigma' = sigma (1 - sigma) at S and |sigma''| <= 0.1
+// over the logit interval: sigma(S +- B) lies within sigma(S) +- (sigma' B +
+// 0.05 B^2). The reference's score is sigma of its logit to within a
+// relative 2^-22 (its expf, the add and the division, each under an ulp).
+// The point score is sigma(S) rounded to float: within the bounds, and
+// within a few ulps of the reference's operations on fp32(S).
+__device__ __forceinline__ bool cert_finish1(double S, double B, int E, int e, const float *__restrict__ bias,
+                                             float *__restrict__ out) {
+    if (!(fabs(S) + B < 30.0)) return false;
+    const float ef = __expf(-(float)S);
+    const double sg = 1.0 / (1.0 + (double)ef);
+    const double d1 = sg * (1.0 - sg);
+    const double r = (fabs(S) + 2.0) * 0x1p-20 + fabs(S) * 0x1p-23;
+    const double err = d1 * r * 1.01 + d1 * B + 0.05 * B * B + (sg + d1 * B) * 0x1p-22 + 1e-300;
+    const float bv = bias ? bias[e] : 0.0f;
+    const float sc = (float)sg;
+    st_agent(out + e, sc);
+    st_agent(out + E + e, __fadd_rn(sc, bv));
+    st_agent(out + 2 * E + e, f_down(__fadd_rn(f_down((float)(sg - err)), bv)));
+    st_agent(out + 3 * E + e, f_up(__fadd_rn(f_up((float)(sg + err)), bv)));
+    return true;
+}
+
+// out: [0, E) point score, [E, 2E) point biased score, [2E, 3E) the biased
+// score's lower bound, [3E, 4E) its upper bound. One 256-thread block per
+// row; each thread a contiguous run of the row. H % 4 == 0.
+__device__ __forceinline__ void router_row_cert(const float *__restrict__ W, const float *__restrict__ x, int E,
+                                                int H, int e, const float *__restrict__ bias, float *__restrict__ out) {
+    __shared__ double r_sum[4], r_abs_s[4];
+    __shared__ double r_scan[4];
+    __shared__ float r_abs_p[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n4 = H >> 2, per = (n4 + 255) / 256;
+    const float4 *w4 = (const float4 *)(W + (size_t)e * H), *x4 = (const float4 *)x;
+    float4 a[CERT_MAXV], b[CERT_MAXV];
+#pragma unroll
+    for (int v = 0; v < CERT_MAXV; v++) {
+        const int i = min(tid * per + v, n4 - 1);
+        if (v < per) {
+            a[v] = w4[i];
+            b[v] = x4[i];
+        }
+    }
+    // this thread's run: its exact sum and the magnitudes of its products
+    double loc = 0.0;
+    float absp = 0.0f;
+#pragma unroll
+    for (int v = 0; v < CERT_MAXV; v++) {
+        if (v < per && tid * per + v < n4) {
+            const double p0 = (double)a[v].x * b[v].x, p1 = (double)a[v].y * b[v].y;
+            const double p2 = (double)a[v].z * b[v].z, p3 = (double)a[v].w * b[v].w;
+            loc += p0; loc += p1; loc += p2; loc += p3;
+            absp += fabsf((float)p0) + fabsf((float)p1) + fabsf((float)p2) + fabsf((float)p3);
+        }
+    }
+    // exclusive scan of the runs' sums over the block, in thread order
+    double inc = loc;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const double t = __shfl_up(inc, o);
+        if (lane >= o) inc += t;
+    }
+    if (lane == 63) r_scan[wave] = inc;
+    __syncthreads();
+    double off = inc - loc;
+    for (int w = 0; w < wave; w++) off += r_scan[w];
+    // sum of the running sums' magnitudes over this run
+    double abss = 0.0, s = off;
+#pragma unroll
+    for (int v = 0; v < CERT_MAXV; v++) {
+        if (v < per && tid * per + v < n4) {
+            s += (double)a[v].x * b[v].x; abss += fabs(s);
+            s += (double)a[v].y * b[v].y; abss += fabs(s);
+            s += (double)a[v].z * b[v].z; abss += fabs(s);
+            s += (double)a[v].w * b[v].w; abss += fabs(s);
+        }
+    }
+    // block totals (fixed order)
+    double tot = loc, ta = abss;
+    float tp = absp;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        tot += __shfl_xor(tot, o);
+        ta += __shfl_xor(ta, o);
+        tp += __shfl_xor(tp, o);
+    }
+    if (lane == 0) {
+        r_sum[wave] = tot;
+        r_abs_s[wave] = ta;
+        r_abs_p[wave] = tp;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        const double S = (r_sum[0] + r_sum[1]) + (r_sum[2] + r_sum[3]);
+        const double as = (r_abs_s[0] + r_abs_s[1]) + (r_abs_s[2] + r_abs_s[3]);
+        const double ap = ((double)r_abs_p[0] + r_abs_p[1]) + ((double)r_abs_p[2] + r_abs_p[3]);
+        cert_finish(S, as, ap, H, E, e, bias, out);
+    }
+}
+
+// The certification of the selection, by the router's last block
+// (cert_last): done holds one word per row, set by the row's block once the
+// row is out (zero between launches; the last block clears them), K picks,
+// cctr the counters (or NULL), flag the route's missing flag. done = NULL:
+// the arrays only.
+struct CertTail {
+    unsigned *done;
+    int K;
+    unsigned long long *cctr;
+    int *flag;                  // a wait past CERT_POLLS sets bit 2 (value 4)
+};
+constexpr unsigned CERT_POLLS = 1u << 16;   // polls of the rows' words before the last block gives up
+template <int NT>
+__device__ void cert_last(const float *__restrict__ W, const float *__restrict__ x, int E, int H,
+                          const float *__restrict__ bias, float *__restrict__ out, const CertTail &t, float *lds,
+                          int lds_floats);
+
+__global__ __launch_bounds__(256) void k_router_cert(const float *__restrict__ W, const float *__restrict__ x, int E,
+                                                     int H, const float *__restrict__ bias, float *__restrict__ out,
+                                                     CertTail t, int lds_floats) {
+    extern __shared__ __attribute__((aligned(16))) float rcg_lds[];
+    if ((int)blockIdx.x < E) router_row_cert(W, x, E, H, blockIdx.x, bias, out);   // (block E: the certifier)
+    if (t.done) cert_last<256>(W, x, E, H, bias, out, t, rcg_lds, lds_floats);
+}
+
+// The same arrays, faster: one 256-thread block per row, W's row and x
+// staged in LDS by coalesced loads, T = H / (4 R4) threads taking one
+// contiguous run of R = 4 R4 columns each (runs padded in LDS so that the
+// lanes' 16-byte reads fall on distinct banks). The centre is the exact sum
+// of the fp32 products p = fl(w x) -- the reference's own summands -- by
+// TwoSum within a run, then in double; the reference's sequential sum s_n of
+// them is within u sum_k |S_k| (1 + 2 n u) of it, S_k the exact prefix sums,
+// with no term for the products (the same rounded products on both sides).
+// sum_k |S_k| is taken from fp32 running sums from each run's offset: each
+// is off by at most 2 (R + 2) u sum|p| (the offset rounded once, then R
+// roundings of sums of magnitude at most 2 sum|p|), and the fp32 sums of
+// magnitudes by a relative (R + 10) u (the run, the wave's six levels, the
+// four waves).
+template <int R4>
+__global__ __launch_bounds__(256) void k_router_cert_b(const float *__restrict__ W, const float *__restrict__ x,
+                                                       int E, int H, const float *__restrict__ bias,
+                                                       float *__restrict__ out, CertTail t, int lds_floats) {
+    constexpr int R = 4 * R4, S4 = R4 + ((R4 & 1) ? 2 : 1);     // run stride: an odd number of float4
+    extern __shared__ __attribute__((aligned(16))) float4 rc_lds[];
+    __shared__ double rc_wt[4];
+    __shared__ float rc_as[4], rc_ap[4];
+    if ((int)blockIdx.x == E) {                            // uniform: the certifying block
+        cert_last<256>(W, x, E, H, bias, out, t, (float *)rc_lds, lds_floats);
+        return;
+    }
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n4 = H >> 2, T = n4 / R4, e = blockIdx.x;
+    float4 *wl = rc_lds, *xl = rc_lds + 256 * S4;
+    const float4 *w4 = (const float4 *)(W + (size_t)e * H), *x4 = (const float4 *)x;
+    float4 ws[R4], xs[R4];
+#pragma unroll
+    for (int v = 0; v < R4; v++) {
+        const int i = min(tid + 256 * v, n4 - 1);
+        ws[v] = w4[i];
+        xs[v] = x4[i];
+    }
+#pragma unroll
+    for (int v = 0; v < R4; v++) {
+        const int i = tid + 256 * v;
+        if (i < n4) {
+            const int r = i / R4, j = i - r * R4;
+            wl[r * S4 + j] = ws[v];
+            xl[r * S4 + j] = xs[v];
+        }
+    }
+    __syncthreads();
+    const bool act = tid < T;
+    float p[R], hi = 0.0f, lo = 0.0f, absp = 0.0f;
+#pragma unroll
+    for (int v = 0; v < R4; v++) {
+        const float4 a = act ? wl[tid * S4 + v] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const float4 b = act ? xl[tid * S4 + v] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        p[4 * v] = __fmul_rn(a.x, b.x);
+        p[4 * v + 1] = __fmul_rn(a.y, b.y);
+        p[4 * v + 2] = __fmul_rn(a.z, b.z);
+        p[4 * v + 3] = __fmul_rn(a.w, b.w);
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const float q = p[4 * v + c];
+            const float t = __fadd_rn(hi, q), z = __fsub_rn(t, hi);      // TwoSum: hi + q = t + err exactly
+            lo = __fadd_rn(lo, __fadd_rn(__fsub_rn(hi, __fsub_rn(t, z)), __fsub_rn(q, z)));
+            hi = t;
+            absp = __fadd_rn(absp, fabsf(q));
+        }
+    }
+    // the runs' exclusive prefix over the block (thread order = index order)
+    const double run = (double)hi + (double)lo;
+    double inc = run;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const double t = __shfl_up(inc, o);
+        if (lane >= o) inc += t;
+    }
+    if (lane == 63) rc_wt[wave] = inc;
+    __syncthreads();
+    double off = inc - run;
+    for (int w = 0; w < wave; w++) off += rc_wt[w];
+    float sr = (float)off, abss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < R; k++) {
+        sr = __fadd_rn(sr, p[k]);
+        abss = __fadd_rn(abss, fabsf(sr));
+    }
+    if (!act) abss = 0.0f;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        abss = __fadd_rn(abss, __shfl_xor(abss, o));
+        absp = __fadd_rn(absp, __shfl_xor(absp, o));
+    }
+    if (lane == 0) {
+        rc_as[wave] = abss;
+        rc_ap[wave] = absp;
+    }
+    __syncthreads();
+    const double S = (rc_wt[0] + rc_wt[1]) + (rc_wt[2] + rc_wt[3]);
+    const double g = 1.0 + 2.0 * (R + 10.0) * CERT_U, n = (double)H;
+    const double ap = ((double)(rc_ap[0] + rc_ap[1]) + (double)(rc_ap[2] + rc_ap[3])) * g;
+    const double dsr = 2.0 * (R + 2.0) * CERT_U * ap;     // the running sums' own error, each
+    const double as = ((double)(rc_as[0] + rc_as[1]) + (double)(rc_as[2] + rc_as[3])) * g + n * dsr;
+    const double B1 = CERT_U * as * (1.0 + 4.0 * n * CERT_U) + 1e-12 * as + n * 1.4e-45;
+    // A tighter bound from the same running sums: the reference's step k
+    // rounds a sum t_k with |t_k| <= |sr_k| + dsr + B1 (B1 bounds every
+    // earlier partial sum's error too), so its error is at most half an ulp
+    // of t_k's binade, 2^(e - 24) for |t_k| in [2^e, 2^(e+1)) -- about 0.7
+    // of u |t_k| on average. The binade of fl(|sr_k| + dB) is at least that
+    // of |t_k| (rounding to nearest never leaves a binade downward).
+    const float dB = (float)((dsr + B1) * (1.0 + 0x1p-20));
+    float sr2 = (float)off, hus = 0.0f;
+#pragma unroll
+    for (int k = 0; k < R; k++) {
+        sr2 = __fadd_rn(sr2, p[k]);
+        const float y = __fadd_rn(fabsf(sr2), dB);
+        const int ex = (__float_as_int(y) >> 23) & 0xff;
+        hus = __fadd_rn(hus, ex >= 25 ? __int_as_float((ex - 24) << 23) : 0x1p-126f);   // (below 2^-102: 2^-126)
+    }
+    if (!act) hus = 0.0f;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) hus = __fadd_rn(hus, __shfl_xor(hus, o));
+    if (lane == 0) rc_as[wave] = hus;
+    __syncthreads();
+    if (tid < 64) {                                       // wave 0 (uniform values)
+        const double hsum = ((double)(rc_as[0] + rc_as[1]) + (double)(rc_as[2] + rc_as[3])) * g;
+        const double B = fmin(B1, hsum * (1.0 + 4.0 * n * CERT_U) + 1e-12 * as + n * 1.4e-45);
+        if (!(fabs(S) + B < 30.0)) {                       // uniform
+            if (tid < 3) cert_finish3(S, B / (CERT_U * (1.0 + 4.0 * n * CERT_U) + 1e-12), 0.0, H, E, e, tid,
+                                      bias, out);
+        } else if (tid == 0) {
+            cert_finish1(S, B, E, e, bias, out);
+        }
+    }
+    if (t.done) cert_last<256>(W, x, E, H, bias, out, t, (float *)rc_lds, lds_floats);
+}
+
+// Launches k_router_cert_b<R4> when H / (4 R4) threads of the block make
+// whole waves (the callers try the shortest runs first).
+// LDS floats of cert_last: the four arrays, the recompute's row and segments.
+static size_t cert_last_floats(int E, int H) {
+    return (size_t)((4 * ((E + 1) & ~1) + 3) & ~3) + (size_t)H + 128 * 4 + 64;
+}
+
+template <int R4>
+static bool router_cert_b(const float *W, const float *x, int E, int H, const float *bias, float *out,
+                          const CertTail &t, hipStream_t s) {
+    const int n4 = H >> 2;
+    if ((H & 3) || n4 % R4 || n4 / R4 > 256 || (n4 / R4) % 64) return false;
+    const size_t lds = std::max((size_t)2 * 256 * (R4 + ((R4 & 1) ? 2 : 1)) * sizeof(float4),
+                                t.done ? cert_last_floats(E, H) * sizeof(float) : (size_t)0);
+    if (lds > 160 * 1024) return false;
+    static std::atomic<uint64_t> attr{0};
+    if (lds_limit((const void *)k_router_cert_b<R4>, (int)lds, attr, s)) return false;
+    hipLaunchKernelGGL(k_router_cert_b<R4>, dim3(E + (t.done ? 1 : 0)), dim3(256), lds, s, W, x, E, H, bias, out,
+                       t, (int)(lds / sizeof(float)));
+    return true;
+}
+
+extern "C" int wk_router_cert(const float *W, const float *x, int E, int H, const float *bias, float *out,
+                              unsigned *done, int K, unsigned long long *cctr, int *flag, void *stream) {
+    if (E <= 0 || H <= 0 || (H & 3) || H > 1024 * CERT_MAXV) return -1;
+    if (done && (K <= 0 || K > WARP_MAX_K || K > E || E > CERT_EMAX)) return -1;
+    const CertTail t = {done, K, cctr, flag};
+    // hidden sizes of the reference's models (Kimi-Linear 2304, K3 7168) and
+    // their neighbours take the staged kernel
+    const hipStream_t st = (hipStream_t)stream;
+    if (!(router_cert_b<3>(W, x, E, H, bias, out, t, st) || router_cert_b<4>(W, x, E, H, bias, out, t, st) ||
+          router_cert_b<5>(W, x, E, H, bias, out, t, st) || router_cert_b<6>(W, x, E, H, bias, out, t, st) ||
+          router_cert_b<7>(W, x, E, H, bias, out, t, st) || router_cert_b<8>(W, x, E, H, bias, out, t, st))) {
+        const size_t lds = done ? cert_last_floats(E, H) * sizeof(float) : 0;
+        if (lds > 160 * 1024) return -1;
+        static std::atomic<uint64_t> attr{0};
+        if (int r_ = lds_limit((const void *)k_router_cert, (int)lds, attr, stream)) return r_;
+        hipLaunchKernelGGL(k_router_cert, dim3(E + (done ? 1 : 0)), dim3(256), lds, st, W, x, E, H, bias, out, t,
+                           (int)(lds / sizeof(float)));
+    }
+    CHECK_LAUNCH();
+    return 0;
+}
+
 extern "C" int wk_router_scored(const float *W, const float *x, int E, int H, const float *bias, float *out,
                                 void *stream) {
     if (E <= 0 || H <= 0) return -1;
@@ -1109,6 +1514,83 @@ __device__ __forceinline__ bool picks_missing(const warp_slot *slots, const int 
     return __ballot(m) != 0ull;
 }
 
+// Certified selection's test by wave 0 of the picking block (E <= 512, the
+// ids lane + 64 m of each lane), with the picks in rank order in lanes
+// 0..np-1 (mine) and the biased scores and their bounds in LDS: the
+// ambiguous experts, as cert_check defines them, into amb (nonzero bits)
+// and their number into *namb, without a block barrier. A non-pick is an
+// id whose (key, ~id) is below the last pick's. The usual case is settled
+// first with a shorter test: when each pick's lower bound is above the
+// next pick's upper bound, the picks' intervals are ordered pairwise (by
+// induction along the ranks) and the last pick's lower bound is their
+// lowest, so no expert is ambiguous if no non-pick's upper bound reaches it.
+__device__ __forceinline__ void route_cert_wave(int E, int np, int mine, const float *biased, const float *lo,
+                                                const float *hi, unsigned long long *amb, int *namb) {
+    const int lane = threadIdx.x & 63;
+    const bool pk = lane < np;
+    const float plo = pk ? lo[mine] : INFINITY, phi = pk ? hi[mine] : -INFINITY;
+    const int last = __builtin_amdgcn_readlane(mine, max(np, 1) - 1);
+    const unsigned long long kmin =
+        np > 0 ? ((unsigned long long)((unsigned)route_key(biased[last]) ^ 0x80000000u) << 32) | (unsigned)~last
+               : ~0ull;
+    float h[8];
+    bool non[8];
+#pragma unroll
+    for (int m = 0; m < 8; m++) {
+        const int e = lane + 64 * m, ec = min(e, E - 1);
+        const unsigned long long pkd =
+            ((unsigned long long)((unsigned)route_key(biased[ec]) ^ 0x80000000u) << 32) | (unsigned)~ec;
+        non[m] = e < E && pkd < kmin;
+        h[m] = hi[ec];
+    }
+    // the short test
+    const float nhi = __shfl_down(phi, 1);                 // the next pick's upper bound
+    const bool sep = lane + 1 >= np || plo > nhi;
+    const float lastlo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(plo), max(np, 1) - 1));
+    bool reach = false;
+#pragma unroll
+    for (int m = 0; m < 8; m++) reach |= non[m] && h[m] >= lastlo;
+    if (__ballot(!sep || reach) == 0ull) {                 // uniform: nothing ambiguous
+        if (lane == 0) *namb = 0;
+        return;
+    }
+    // the full test: every pair
+    float pm = plo, sm = phi;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const float u = __shfl_up(pm, o), d = __shfl_down(sm, o);
+        if (lane >= o) pm = fminf(pm, u);
+        if (lane + o < 64) sm = fmaxf(sm, d);
+    }
+    float before = __shfl_up(pm, 1), after = __shfl_down(sm, 1);
+    if (lane == 0) before = INFINITY;
+    if (lane == 63) after = -INFINITY;
+    const float minlo = __shfl(pm, 63);                   // the lowest lower bound of a pick
+    float mnp = -INFINITY;
+    bool np_amb[8];
+    int n = 0;
+#pragma unroll
+    for (int m = 0; m < 8; m++) {
+        mnp = non[m] ? fmaxf(mnp, h[m]) : mnp;
+        np_amb[m] = non[m] && h[m] >= minlo;
+    }
+    mnp = wave_max(mnp);
+    const bool pa = pk && (before <= phi || after >= plo || mnp >= plo);
+#pragma unroll
+    for (int m = 0; m < 8; m++) {
+        const unsigned long long b = __ballot(np_amb[m]);
+        n += __popcll(b);
+        if (lane == 0 && 64 * m < E) amb[m] = b;
+    }
+    const unsigned long long pb = __ballot(pa);
+    n += __popcll(pb);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (pa) atomicOr(&amb[mine >> 6], 1ull << (mine & 63));
+    if (lane == 0) *namb = n;
+}
+
 // Decode routing (one token). The logits, the bias and this layer's expert
 // table go to LDS in one pass of independent loads; one wave then takes the
 // K picks by repeated arg-max -- larger biased score first, the lower id on
@@ -1125,10 +1607,15 @@ __device__ __forceinline__ bool picks_missing(const warp_slot *slots, const int 
 // computed and wsel is left at 0 (a block that only needs the picks).
 // scored (uniform): score and biased already hold the sigmoid scores and the
 // biased scores (k_router_scored), so the scoring pass is skipped.
+// clo/chi (REGS, certified selection): the biased scores' lower and upper
+// bounds; wave 0 then also marks the ambiguous experts (as cert_check
+// defines them) in camb (E / 64 words) and their number in *namb.
 template <bool REGS, int NT>
 __device__ __forceinline__ int route_pick_lds(int E, int K, int act, int renorm, float routed_scale, float *score,
                                               float *biased, int *sel, float *wsel, bool want_w = true,
-                                              bool scored = false, const uint64_t *etab = nullptr) {
+                                              bool scored = false, const uint64_t *etab = nullptr,
+                                              const float *clo = nullptr, const float *chi = nullptr,
+                                              unsigned long long *camb = nullptr, int *namb = nullptr) {
     __shared__ float red[NT / 64];
     __shared__ int np_s;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1288,10 +1775,400 @@ __device__ __forceinline__ int route_pick_lds(int E, int K, int act, int renorm,
             wv = __fmul_rn(wv, routed_scale);
             if (lane < K) wsel[lane] = wv;
         }
+        if (REGS && clo) route_cert_wave(E, npick, mine, biased, clo, chi, camb, namb);
         if (lane == 0) np_s = npick;
     }
     __syncthreads();
     return np_s;
+}
+
+constexpr int CERT_NB = 16;                 // rows recomputed together (lanes of wave 0)
+constexpr int CERT_PT = 16;                 // products per thread per chunk
+
+// The certified selection's counters: one routing that recomputed, n rows.
+__device__ __forceinline__ void cert_count(const warp_route_args &r, int n) {
+    if (threadIdx.x == 0 && r.cctr) {
+        __hip_atomic_fetch_add(r.cctr, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(r.cctr + 1, (unsigned long long)n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// The recompute of the ambiguous rows cert_check flags (see there), for
+// buffers too small for cert_recompute: amb, their mask (nw words,
+// consumed); the rows' scores and biased scores are rewritten. Rows in
+// batches of up to CERT_NB: the block forms the products fl(w_k x_k) of a
+// chunk of columns into stg (the next chunk's loads in flight meanwhile)
+// and lanes of wave 0 add them in index order, one row per lane, unfused:
+// the reference's dotf (src/model.c:155-160).
+template <int NT>
+__device__ __forceinline__ void cert_recompute_seq(const warp_route_args &r, float *score, float *biased,
+                                                   unsigned long long *amb, int nw, float *stg, int cap,
+                                                   const uint64_t *etab) {
+    const float *cw = r.cw, *cx = r.cx, *bias = r.bias;
+    const int H = r.ch;
+    __shared__ int c_ids[CERT_NB];
+    __shared__ int c_na;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (;;) {
+        if (tid == 0) {                                  // the next batch, ascending ids
+            int na = 0;
+            for (int i = 0; i < nw && na < CERT_NB; i++) {
+                unsigned long long m = amb[i];
+                while (m && na < CERT_NB) {
+                    c_ids[na++] = i * 64 + __ffsll((long long)m) - 1;
+                    m &= m - 1ull;
+                }
+                amb[i] = m;
+            }
+            c_na = na;
+        }
+        __syncthreads();
+        const int na = c_na;
+        if (na == 0) break;                              // uniform
+        // a chunk: na rows of C columns (C % 4 == 0), [C / 4][na][4] in stg
+        const int C = min(min(cap / na, NT * CERT_PT / na) & ~3, H);
+        float pr[CERT_PT];
+        auto load = [&](int k0) {
+#pragma unroll
+            for (int i = 0; i < CERT_PT; i++) {
+                const int t = tid + i * NT, a = t / C, k = t - a * C;
+                const bool ok = a < na && k0 + k < H;
+                const int kk = ok ? k0 + k : 0;
+                const float w = cw[(size_t)c_ids[ok ? a : 0] * H + kk], xv = cx[kk];
+                pr[i] = ok ? __fmul_rn(w, xv) : 0.0f;
+            }
+        };
+        load(0);
+        float s = 0.0f;
+        for (int k0 = 0; k0 < H; k0 += C) {
+#pragma unroll
+            for (int i = 0; i < CERT_PT; i++) {
+                const int t = tid + i * NT, a = t / C, k = t - a * C;
+                if (a < na) stg[((k >> 2) * na + a) * 4 + (k & 3)] = pr[i];
+            }
+            __syncthreads();
+            if (k0 + C < H) load(k0 + C);                // in flight while the chain runs
+            if (wave == 0 && lane < na) {
+                // row lane's products in index order, one unfused add each;
+                // the next eight reads in flight while eight are added
+                const int n4 = min(C, H - k0) >> 2;
+                const float4 *s4 = (const float4 *)stg + lane;
+                int q = 0;
+                if (n4 >= 8) {
+                    float4 c[8];
+#pragma unroll
+                    for (int j = 0; j < 8; j++) c[j] = s4[(size_t)j * na];
+                    for (; q + 8 <= n4; q += 8) {
+                        float4 nx[8];
+                        const int qn = min(q + 8, n4 - 8);         // (the last group reads itself again)
+#pragma unroll
+                        for (int j = 0; j < 8; j++) nx[j] = s4[(size_t)(qn + j) * na];
+#pragma unroll
+                        for (int j = 0; j < 8; j++) {
+                            s = __fadd_rn(s, c[j].x);
+                            s = __fadd_rn(s, c[j].y);
+                            s = __fadd_rn(s, c[j].z);
+                            s = __fadd_rn(s, c[j].w);
+                        }
+#pragma unroll
+                        for (int j = 0; j < 8; j++) c[j] = nx[j];
+                    }
+                }
+                for (; q < n4; q++) {
+                    const float4 v = s4[(size_t)q * na];
+                    s = __fadd_rn(s, v.x);
+                    s = __fadd_rn(s, v.y);
+                    s = __fadd_rn(s, v.z);
+                    s = __fadd_rn(s, v.w);
+                }
+            }
+            __syncthreads();
+        }
+        if (wave == 0 && lane < na) {
+            const int e = c_ids[lane];
+            const float sc = cert_score(s, etab);
+            score[e] = sc;
+            biased[e] = __fadd_rn(sc, bias ? bias[e] : 0.0f);
+        }
+        __syncthreads();
+    }
+}
+
+// Floats in order as integers: consecutive floats are consecutive keys
+// (-0 just below +0).
+__device__ __forceinline__ long long fkey(float f) {
+    const int b = __float_as_int(f);
+    return b >= 0 ? (long long)b : -(long long)(b & 0x7fffffff) - 1;
+}
+__device__ __forceinline__ float fkey_inv(long long k) {
+    return k >= 0 ? __int_as_float((int)k) : __int_as_float((int)((-(k + 1)) | 0x80000000ll));
+}
+
+// v + p[0] + p[1] + ... + p[4 n4 - 1], one fp32 add at a time in that order
+// (the reference's dotf chain), p 16-byte aligned in LDS, the next four
+// float4 read while four are added.
+__device__ __forceinline__ float chain_add(float v, const float4 *p, int n4) {
+    int q = 0;
+    if (n4 >= 4) {
+        float4 c[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) c[j] = p[j];
+        for (; q + 4 <= n4; q += 4) {
+            float4 nx[4];
+            const int qn = min(q + 4, n4 - 4);             // (the last group reads itself again)
+#pragma unroll
+            for (int j = 0; j < 4; j++) nx[j] = p[qn + j];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                v = __fadd_rn(v, c[j].x);
+                v = __fadd_rn(v, c[j].y);
+                v = __fadd_rn(v, c[j].z);
+                v = __fadd_rn(v, c[j].w);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) c[j] = nx[j];
+        }
+    }
+    for (; q < n4; q++) {
+        const float4 c = p[q];
+        v = __fadd_rn(v, c.x);
+        v = __fadd_rn(v, c.y);
+        v = __fadd_rn(v, c.z);
+        v = __fadd_rn(v, c.w);
+    }
+    return v;
+}
+
+// One DPP move of a double (its two halves): rows masked out, or lanes with
+// no source under bound_ctrl, read 0.
+template <int CTRL, int ROWS, bool BC>
+__device__ __forceinline__ double dpp_f64(double x) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, x);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, ROWS, 0xf, BC);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, ROWS, 0xf, BC);
+    return __builtin_bit_cast(double, ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+
+// The sum over the wave into lane 63 (the other lanes hold partial sums):
+// row shifts by 1, 2, 4, 8, then lane 15 of each row added into the next
+// (rows 1 and 3) and lane 31 into rows 2 and 3.
+__device__ __forceinline__ double wave_sum63_f64(double v) {
+    v += dpp_f64<0x111, 0xf, true>(v);
+    v += dpp_f64<0x112, 0xf, true>(v);
+    v += dpp_f64<0x114, 0xf, true>(v);
+    v += dpp_f64<0x118, 0xf, true>(v);
+    v += dpp_f64<0x142, 0xa, false>(v);
+    v += dpp_f64<0x143, 0xc, false>(v);
+    return v;
+}
+
+// The sequential sum v + P[0] + ... + P[n - 1] (fp32, one add at a time) by a
+// block of NT threads, by speculation over segments: the chain is cut into
+// G = NT / 64 segments of L = n / G, and wave g runs segment g from 64
+// starts at once -- the 64 floats around the exact prefix sum before it
+// (rounded to float), one per lane; the sequential running sum there is
+// that prefix plus its rounding so far, usually within a few tens of ulps.
+// Wave 0 then follows the chain: from segment 0's end (its start, v, is
+// exact) it takes the lane of segment 1 whose start is that value, and so
+// on; where the value is not among a segment's starts, it adds that segment
+// itself. Returns the sum in every thread (uniform). n % (4 G) == 0; P in
+// LDS, 16-byte aligned; U: 64 G floats of LDS.
+template <int NT>
+__device__ __forceinline__ float spec_chain(float v, const float *P, int n, float *U) {
+    constexpr int G = NT / 64;
+    __shared__ double sc_seg[G];
+    __shared__ float sc_ctr[G], sc_v;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, L = n / G;
+    double t = 0.0;                                       // the segments' exact sums
+    for (int k = wave * L + lane; k < (wave + 1) * L; k += 64) t += (double)P[k];
+    t = wave_sum63_f64(t);
+    if (lane == 63) sc_seg[wave] = t;
+    __syncthreads();
+    if (tid == 0) {
+        double acc = (double)v;
+        for (int g = 0; g < G; g++) {
+            sc_ctr[g] = (float)acc;
+            acc += sc_seg[g];
+        }
+    }
+    __syncthreads();
+    const float v0 = wave == 0 ? v : fkey_inv(fkey(sc_ctr[wave]) + lane - 32);
+    U[wave * 64 + lane] = chain_add(v0, (const float4 *)(P + wave * L), L >> 2);
+    __syncthreads();
+    if (wave == 0) {                                      // (every lane the same values)
+        // lane c holds the end of each segment's start c, lane g the key of
+        // segment g's centre
+        float ug[G];
+#pragma unroll
+        for (int g = 0; g < G; g++) ug[g] = U[g * 64 + lane];
+        const int kc = (int)fkey(sc_ctr[min(lane, G - 1)]);
+        float w = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(ug[0])));
+#pragma unroll
+        for (int g = 1; g < G; g++) {
+            const int c = __builtin_amdgcn_readlane(kc, g);
+            const int d = __builtin_amdgcn_readfirstlane((int)((unsigned)fkey(w) - (unsigned)c + 32u));
+            // (32-bit keys: a wrapped difference fails the equality test)
+            if ((unsigned)d < 64u && isfinite(w) && fkey_inv((long long)c + d - 32) == w)
+                w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ug[g]), d));
+            else
+                w = chain_add(w, (const float4 *)(P + g * L), L >> 2);
+        }
+        if (lane == 0) sc_v = w;
+    }
+    __syncthreads();
+    return sc_v;
+}
+
+// The recompute of the ambiguous rows: as many rows' products fl(w_k x_k)
+// as the buffer holds go to LDS at once, then each row's sequential sum by
+// spec_chain. H % (4 G) == 0 (G = NT / 64) and cap >= H + 128 G, else the
+// chunked single-lane recompute (cert_recompute_seq).
+template <int NT>
+__device__ __forceinline__ void cert_recompute(const warp_route_args &r, float *score, float *biased,
+                                               unsigned long long *amb, int nw, float *stg, int cap,
+                                               const uint64_t *etab) {
+    constexpr int G = NT / 64;
+    constexpr int NR = 4;                                 // rows filled together, at most
+    const int H = r.ch;
+    if (H % (4 * G) || cap < H + 128 * G) {
+        cert_recompute_seq<NT>(r, score, biased, amb, nw, stg, cap, etab);
+        return;
+    }
+    __shared__ int c_rows[NR];
+    __shared__ int c_nr;
+    const int tid = threadIdx.x;
+    const int fit = min(NR, (cap - 128 * G) / H);
+    float *U = stg + (size_t)fit * H;
+    for (;;) {
+        if (tid == 0) {                                  // the next rows, ascending ids
+            int n = 0;
+            for (int i = 0; i < nw && n < fit; i++) {
+                unsigned long long m = amb[i];
+                while (m && n < fit) {
+                    c_rows[n++] = i * 64 + __ffsll((long long)m) - 1;
+                    m &= m - 1ull;
+                }
+                amb[i] = m;
+            }
+            c_nr = n;
+        }
+        __syncthreads();
+        const int nr = c_nr;
+        if (nr == 0) break;                               // uniform
+        const float4 *x4 = (const float4 *)r.cx;
+        for (int i = tid; i < nr * (H >> 2); i += NT) {
+            const int q = i / (H >> 2), j = i - q * (H >> 2);
+            const float4 a = ((const float4 *)(r.cw + (size_t)c_rows[q] * H))[j], b = x4[j];
+            ((float4 *)stg)[i] = make_float4(__fmul_rn(a.x, b.x), __fmul_rn(a.y, b.y), __fmul_rn(a.z, b.z),
+                                             __fmul_rn(a.w, b.w));
+        }
+        __syncthreads();
+        for (int q = 0; q < nr; q++) {
+            const float v = spec_chain<NT>(0.0f, stg + (size_t)q * H, H, U);
+            if (tid == 0) {
+                const int e = c_rows[q];
+                const float sc = cert_score(v, etab);
+                score[e] = sc;
+                biased[e] = __fadd_rn(sc, r.bias ? r.bias[e] : 0.0f);
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// Certified selection (sigmoid scores from k_router_cert's bounds). After
+// route_pick_lds has picked sel[0..np) by the point biased scores: an expert
+// is ambiguous when its biased-score interval [lo, hi] (which holds both the
+// point value and the reference's) leaves its order against another expert
+// open -- a non-pick whose upper bound reaches the lowest lower bound of a
+// pick, a pick whose lower bound is reached by a later pick's upper bound or
+// a non-pick's, a pick whose upper bound reaches an earlier pick's lower
+// bound. Every pair involving an expert that is not ambiguous is ordered by
+// the intervals themselves, so once the ambiguous experts' logits are the
+// reference's, the picks made again from these values are the reference's
+// picks in the reference's order. The ambiguous rows are recomputed
+// (cert_recompute, which the caller runs when this returns non-zero, then
+// picks again) in batches of up to CERT_NB: the block forms the products
+// fl(w_k x_k) of a chunk of columns into stg (the next chunk's loads in
+// flight meanwhile) and lanes of wave 0 add them in index order, one row per
+// lane, unfused: the reference's dotf (src/model.c:155-160). The row's score
+// and biased score then follow with the routing's own operations.
+// Returns the number of ambiguous experts (uniform; 0: the picks stand) and
+// their mask in amb. MW: mask words, E <= 64 MW. stg: cap floats of LDS
+// (16-byte aligned), cap >= 64 * CERT_NB. count: the block adds to the
+// route's counters.
+template <int NT, int MW>
+__device__ __forceinline__ int cert_check(const warp_route_args &r, int E, int np, float *score, float *biased,
+                                          const float *lo, const float *hi, const int *sel, bool count,
+                                          unsigned long long *&amb) {
+    __shared__ unsigned long long c_pick[MW], c_amb[MW];
+    amb = c_amb;
+    __shared__ float c_red[NT / 64];
+    __shared__ int c_tot;
+    __shared__ float c_minlo;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nw = (E + 63) >> 6;
+    for (int i = tid; i < nw; i += NT) {
+        c_pick[i] = 0ull;
+        c_amb[i] = 0ull;
+    }
+    __syncthreads();
+    if (tid < np) atomicOr(&c_pick[sel[tid] >> 6], 1ull << (sel[tid] & 63));
+    __syncthreads();
+    float mnp = -INFINITY;                               // the highest upper bound of a non-pick
+    for (int e = tid; e < E; e += NT)
+        if (!((c_pick[e >> 6] >> (e & 63)) & 1ull)) mnp = fmaxf(mnp, hi[e]);
+    mnp = wave_max(mnp);
+    if (lane == 0) c_red[wave] = mnp;
+    // the picks by rank in wave 0, lane j = rank j: the lowest lower bound
+    // of the ranks before j, the highest upper bound of those after it
+    const bool pk = wave == 0 && lane < np;
+    const float plo = pk ? lo[sel[lane]] : INFINITY, phi = pk ? hi[sel[lane]] : -INFINITY;
+    float before = INFINITY, after = -INFINITY;
+    if (wave == 0) {                                     // uniform per wave
+        float pm = plo, sm = phi;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const float u = __shfl_up(pm, o), d = __shfl_down(sm, o);
+            if (lane >= o) pm = fminf(pm, u);
+            if (lane + o < 64) sm = fmaxf(sm, d);
+        }
+        before = __shfl_up(pm, 1);
+        after = __shfl_down(sm, 1);
+        if (lane == 0) before = INFINITY;
+        if (lane == 63) after = -INFINITY;
+        const float mn = -wave_max(-plo);
+        if (lane == 0) c_minlo = mn;
+    }
+    __syncthreads();
+    if (pk) {
+        float m2 = c_red[0];
+        for (int i = 1; i < NT / 64; i++) m2 = fmaxf(m2, c_red[i]);
+        if (before <= phi || after >= plo || m2 >= plo) atomicOr(&c_amb[sel[lane] >> 6], 1ull << (sel[lane] & 63));
+    }
+    {
+        const float minlo = c_minlo;
+        for (int e = tid; e < E; e += NT)
+            if (!((c_pick[e >> 6] >> (e & 63)) & 1ull) && hi[e] >= minlo)
+                atomicOr(&c_amb[e >> 6], 1ull << (e & 63));
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int n = 0;
+        for (int i = 0; i < nw; i++) n += __popcll(c_amb[i]);
+        c_tot = n;
+    }
+    __syncthreads();
+    const int total = c_tot;
+    if (total == 0) return 0;                            // uniform
+    // the picking loop may have taken the picks' biased scores out: their
+    // point values again (the router kernel's operations)
+    if (tid < np) {
+        const int e = sel[tid];
+        biased[e] = __fadd_rn(score[e], r.bias ? r.bias[e] : 0.0f);
+    }
+    if (count) cert_count(r, total);
+    return total;
 }
 
 // The decode job lists from the picks, by a block of NT threads: jobs[0..K)
@@ -1384,6 +2261,170 @@ extern "C" int wk_route(const float *logits, const float *bias, int E, int K, in
     else
         hipLaunchKernelGGL(k_route1<false>, dim3(T), dim3(256), lds, (hipStream_t)stream, logits, bias, E, K, act,
                            renorm, routed_scale, idx, w, table, tl, jobs, njobs, missing, inter);
+    CHECK_LAUNCH();
+    return 0;
+}
+
+// The last router block to finish certifies the selection: it loads the
+// four arrays every block wrote, picks as the routing will (the larger
+// biased score first, the lower id on ties), tests them (route_cert_wave,
+// or cert_check above 512 experts), and where that leaves experts
+// ambiguous, recomputes their logits in the reference's sequential order
+// and writes their exact score and biased score back (both bounds set to
+// the biased score). The routing that follows, from these arrays, picks
+// the reference's experts in the reference's order. lds: lds_floats of the
+// block's dynamic LDS (cert_last_floats).
+template <int NT>
+__device__ void cert_last(const float *__restrict__ W, const float *__restrict__ x, int E, int H,
+                          const float *__restrict__ bias, float *__restrict__ out, const CertTail &t, float *lds,
+                          int lds_floats) {
+    __shared__ int cl_last, cl_namb;
+    __shared__ unsigned long long cl_amb[8], cl_rows[CERT_EMAX / 64];
+    __shared__ int sel[WARP_MAX_K];
+    __shared__ float wsel[WARP_MAX_K];
+    const int tid = threadIdx.x;
+    // A row's block writes its row with agent-coherent stores (st_agent),
+    // complete once wait_stores() returns, and then sets the row's word.
+    // The certifying block (one more block, gridDim.x - 1 = E, no row of its
+    // own) polls the words and loads each row as soon as it is out, so the
+    // last row's arrival leaves it one load behind; a wait past CERT_POLLS
+    // polls raises bit 2 of the flag (the call reports it) and leaves the
+    // arrays uncertified. It clears the words for the next launch.
+    if ((int)blockIdx.x != E) {
+        wait_stores();
+        __syncthreads();
+        if (tid == 0) __hip_atomic_store(t.done + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    const int E2 = (E + 1) & ~1, s0 = (4 * E2 + 3) & ~3, nw = (E + 63) >> 6;
+    float *score = lds, *biased = lds + E2, *lo = lds + 2 * E2, *hi = lds + 3 * E2;
+    unsigned pend = 0;                                    // this thread's rows not yet loaded
+    for (int i = 0; i < CERT_EMAX / NT; i++)
+        if (tid + i * NT < E) pend |= 1u << i;
+    if (tid == 0) cl_last = 1;
+    for (unsigned n = 0;; n++) {
+        for (int i = 0; i < CERT_EMAX / NT; i++) {
+            const int e = tid + i * NT;
+            if (((pend >> i) & 1u) && __hip_atomic_load(t.done + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+                score[e] = ld_agent(out + e);
+                biased[e] = ld_agent(out + E + e);
+                lo[e] = ld_agent(out + 2 * E + e);
+                hi[e] = ld_agent(out + 3 * E + e);
+                pend &= ~(1u << i);
+            }
+        }
+        if (__syncthreads_and(pend == 0)) break;          // uniform
+        if (n >= CERT_POLLS) {
+            if (tid == 0) cl_last = 0;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    __syncthreads();
+    if (!cl_last) {                                       // (never in practice)
+        if (tid == 0 && t.flag) __hip_atomic_fetch_or(t.flag, 4, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    for (int e = tid; e < E; e += NT) __hip_atomic_store(t.done + e, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    warp_route_args r = {};
+    r.bias = bias;
+    r.E = E;
+    r.cw = W;
+    r.cx = x;
+    r.ch = H;
+    r.cctr = t.cctr;
+    int n;
+    unsigned long long *amb = cl_amb;
+    if (E <= 512) {
+        route_pick_lds<true, NT>(E, t.K, 0, 0, 1.0f, score, biased, sel, wsel, false, true, nullptr, lo, hi, cl_amb,
+                                 &cl_namb);
+        n = cl_namb;
+    } else {
+        const int np = route_pick_lds<false, NT>(E, t.K, 0, 0, 1.0f, score, biased, sel, wsel, false, true);
+        n = cert_check<NT, CERT_EMAX / 64>(r, E, np, score, biased, lo, hi, sel, false, amb);
+    }
+    if (n) {                                              // uniform
+        cert_count(r, n);
+        for (int i = tid; i < nw; i += NT) cl_rows[i] = amb[i];   // (the recompute consumes amb)
+        __syncthreads();
+        cert_recompute<NT>(r, score, biased, amb, nw, lds + s0, lds_floats - s0, nullptr);
+        for (int e = tid; e < E; e += NT)
+            if ((cl_rows[e >> 6] >> (e & 63)) & 1ull) {
+                out[e] = score[e];
+                out[E + e] = biased[e];
+                out[2 * E + e] = biased[e];
+                out[3 * E + e] = biased[e];
+            }
+    }
+}
+
+// Certified routing of one token by a CERT_NT-thread block: the four arrays of
+// k_router_cert, the picks, cert_resolve, the picks again where it
+// recomputed; idx/w, and the job lists when a table is given. LDS: scores,
+// biased scores, bounds [4][E2], the table when table_lds, then the
+// recompute buffer (cap floats).
+constexpr int CERT_NT = 1024;                // threads of the certified routing block
+template <bool REGS>
+__global__ __launch_bounds__(CERT_NT) void k_route_cert(warp_route_args r, int K, int table_lds, int cap) {
+    extern __shared__ __attribute__((aligned(16))) float lds_rc[];
+    const int E = r.E, E2 = (E + 1) & ~1;
+    float *score = lds_rc, *biased = lds_rc + E2, *lo = lds_rc + 2 * E2, *hi = lds_rc + 3 * E2;
+    warp_slot *slots = (warp_slot *)(lds_rc + 4 * E2);
+    float *stg = lds_rc + ((4 * E2 + (table_lds ? 6 * E2 : 0) + 3) & ~3);
+    __shared__ int sel[WARP_MAX_K];
+    __shared__ float wsel[WARP_MAX_K];
+    const int tid = threadIdx.x;
+    for (int e = tid; e < E; e += CERT_NT) {
+        score[e] = r.logits[e];
+        biased[e] = r.logits[E + e];
+        lo[e] = r.logits[2 * E + e];
+        hi[e] = r.logits[3 * E + e];
+    }
+    if (r.table && table_lds)
+        for (int e = tid; e < E; e += CERT_NT) slots[e] = r.table[e];
+    __shared__ unsigned long long r_amb[8];
+    __shared__ int r_namb;
+    const int np = route_pick_lds<REGS, CERT_NT>(E, K, r.act, r.renorm, r.routed_scale, score, biased, sel, wsel, true,
+                                             true, nullptr, REGS ? lo : nullptr, hi, r_amb, &r_namb);
+    unsigned long long *amb = r_amb;
+    int n_amb;
+    if (REGS) {
+        n_amb = r_namb;
+        if (n_amb) cert_count(r, n_amb);
+    } else {
+        // (above 512 experts: the block's test; the picking loop took the
+        // picks' biased scores out, and the test puts them back)
+        n_amb = cert_check<CERT_NT, CERT_EMAX / 64>(r, E, np, score, biased, lo, hi, sel, true, amb);
+    }
+    if (n_amb) {                                           // uniform
+        cert_recompute<CERT_NT>(r, score, biased, amb, (E + 63) >> 6, stg, cap, nullptr);
+        route_pick_lds<REGS, CERT_NT>(E, K, r.act, r.renorm, r.routed_scale, score, biased, sel, wsel, true, true);
+    }
+    if (tid < K) {
+        r.idx[tid] = sel[tid];
+        r.w[tid] = wsel[tid];
+    }
+    if (r.table) route_jobs<CERT_NT>(sel, K, table_lds ? slots : r.table, r.jobs, r.njobs, r.missing, r.inter);
+}
+
+extern "C" int wk_route_cert(const warp_route_args *r, int K, void *stream) {
+    if (!r || r->scored != 2 || r->act != 0 || !r->cw || !r->cx || r->ch <= 0 || (r->ch & 3))
+        return -1;
+    const int E = r->E;
+    if (E <= 0 || E > CERT_EMAX || K <= 0 || K > WARP_MAX_K || K > E) return -1;
+    const int E2 = (E + 1) & ~1, tl = r->table && E <= 2048;
+    const int cap = 16384;                                  // 64 KiB: a row's products up to H = 15360
+    const size_t lds = (size_t)(((4 * E2 + (tl ? 6 * E2 : 0) + 3) & ~3) + cap) * sizeof(float);
+    if (lds > 160 * 1024) return -1;
+    if (E <= 512) {
+        static std::atomic<uint64_t> attr{0};
+        if (int r_ = lds_limit((const void *)k_route_cert<true>, (int)lds, attr, stream)) return r_;
+        hipLaunchKernelGGL(k_route_cert<true>, dim3(1), dim3(CERT_NT), lds, (hipStream_t)stream, *r, K, tl, cap);
+    } else {
+        static std::atomic<uint64_t> attr{0};
+        if (int r_ = lds_limit((const void *)k_route_cert<false>, (int)lds, attr, stream)) return r_;
+        hipLaunchKernelGGL(k_route_cert<false>, dim3(1), dim3(CERT_NT), lds, (hipStream_t)stream, *r, K, tl, cap);
+    }
     CHECK_LAUNCH();
     return 0;
 }
@@ -2137,26 +3178,6 @@ struct LutArgs {
     int sh_first;
 };
 
-// Coherent accesses, for what one block of the fused decode launch writes
-// for another, which may run on another XCD (another L2): agent-scope
-// atomic stores and loads (relaxed), which the memory model lowers to
-// accesses that bypass a stale or write-back copy in the XCD's L2 (sc1), so
-// the values reach, and are read from, memory every XCD sees. Nothing here
-// rests on how a plain or volatile access is lowered. A wave's stores are
-// complete once wait_stores() returns, so with a barrier after it the block
-// can raise a count that others poll, without writing back the L2 (which an
-// agent-scope release fence does, at a cost that grows with everything the
-// XCD's other blocks have written).
-__device__ __forceinline__ void st_through4(float *p, float a, float b, float c, float d) {   // p in global memory
-    __hip_atomic_store(p + 0, a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(p + 1, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(p + 2, c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(p + 3, d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_agent(const float *p) {
-    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0x0F70); }   // vmcnt(0)
 
 // Sum of a row's partials over the splits, in split order. Up to 32 splits
 // every load is issued before the first add (one memory latency per row).

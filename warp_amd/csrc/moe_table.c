@@ -95,9 +95,10 @@ static int moe_cfg(const warp_moe_args *a, int tokens, warp_hip_cfg *g)
     g->renorm = a->renorm;
     g->routed_scale = a->routed_scale;
     g->router_act = WARP_HIP_ROUTE_SIGMOID;
-    /* F32 router logits in the reference's sequential order, so the
-     * selection is the reference's on every input */
-    g->router_strict = 1;
+    /* the selection is the reference's on every input: chunks sum the F32
+     * router's logits in the reference's sequential order, decode certifies
+     * its picks against that order (recomputing rows only where needed) */
+    g->router_strict = 2;
     g->act_situ = a->act_situ;
     g->situ_beta = a->situ_beta;
     g->situ_linear_beta = a->situ_linear_beta;

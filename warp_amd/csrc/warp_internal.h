@@ -96,6 +96,17 @@ int wk_router_logits(const float *W, const float *x, int E, int H, int T, int st
  * out[0..E) and biased scores out[E..2E) (score + bias, bias may be NULL), as
  * the routing computes them: the input of warp_route_args with scored = 1. */
 int wk_router_scored(const float *W, const float *x, int E, int H, const float *bias, float *out, void *stream);
+/* Certified routing inputs of one token (sigmoid scores, fp32 router): out
+ * [4][E] = point scores, point biased scores, and the lower and upper bounds
+ * of the biased score the reference's sequential logit gives. H % 4 == 0,
+ * H <= 16384. done (E zeroed words the launch leaves zeroed; or NULL): the
+ * last block also certifies the top-K selection and rewrites the rows whose
+ * order the bounds leave open with their exact (sequential) values, so that
+ * a routing from [0, 2E) (scored = 1) picks the reference's experts in its
+ * order; cctr as in warp_route_args; flag (or NULL): bit 2 (value 4) set
+ * when the last block's wait for the rows gives up. E <= 4096 with done. */
+int wk_router_cert(const float *W, const float *x, int E, int H, const float *bias, float *out, unsigned *done,
+                   int K, unsigned long long *cctr, int *flag, void *stream);
 
 /* Quantised router / dense trunk rows (Q8G, Q4G, Q3G with the reference's
  * packing): y [T][M] = dequant(W) [M][N] . x [T][N]. */
@@ -196,7 +207,11 @@ int wk_lut_plan(int M, int N, int max_jobs, int nkinds, int shared_x, int target
 /* Routing done inside the gate/up launch of a decode step (see wk_vq_lut):
  * the arguments of wk_route with a table, for one token. scored = 1: logits
  * holds the sigmoid scores [E] and the biased scores [E] (wk_router_scored),
- * not the logits. */
+ * not the logits. scored = 2 (certified selection): logits holds the four
+ * arrays of wk_router_cert, and cw [E][ch] / cx [ch] are the router rows
+ * and the token's input the routing recomputes ambiguous logits from
+ * (sequentially, as the reference sums); cctr (or NULL) [2] counts the
+ * routings that recomputed and the rows recomputed. */
 typedef struct {
     const float *logits, *bias;
     const warp_slot *table;
@@ -207,6 +222,9 @@ typedef struct {
     warp_job *jobs;           /* written: the lists of all three kinds */
     int *njobs, *missing;
     int scored;
+    const float *cw, *cx;
+    int ch;
+    unsigned long long *cctr;
 } warp_route_args;
 int wk_vq_lut(int fmt, const warp_job *jobs, const int *njobs, int max_jobs, int kind_lo,
               int nkinds, const uint16_t *books, int books_x31, const float *x, int shared_x, float *part,
@@ -229,6 +247,10 @@ int wk_vq_lut(int fmt, const warp_job *jobs, const int *njobs, int max_jobs, int
  * reading jobs/njobs; route->jobs/njobs/idx/w/missing get what wk_route
  * writes. Only where wk_lut_route_ok says so; NULL otherwise.) */
 int wk_lut_route_ok(int fmt, int E, int K, int shared_x, int kind_lo, int nkinds);
+/* Certified routing of one decode token (route->scored == 2, sigmoid): what
+ * wk_route writes, with route->table (or NULL) for the job lists, from
+ * wk_router_cert's arrays; ambiguous rows recomputed from cw / cx. E <= 4096. */
+int wk_route_cert(const warp_route_args *route, int K, void *stream);
 /* One decode step of a layer in one launch (the table kernel's gate/up
  * units with the routing, its down units, the combine), bit for bit what
  * wk_vq_lut (gate/up, routed), wk_vq_lut (down, act) and wk_combine_lut

@@ -39,8 +39,12 @@ class Cfg(C.Structure):
         ("situ_beta", C.c_float), ("situ_linear_beta", C.c_float), ("max_tokens", C.c_int),
         ("rec_bytes", C.c_size_t), ("cache_bytes", C.c_size_t), ("verify", C.c_int),
         ("lookahead", C.c_int), ("device", C.c_int), ("latent", C.c_int), ("latent_norm", C.c_int),
-        ("norm_eps", C.c_float), ("prefill_fp16", C.c_int), ("n_books", C.c_int),
+        ("norm_eps", C.c_float), ("prefill_fp16", C.c_int), ("n_books", C.c_int), ("router_fast", C.c_int),
     ]
+
+
+class RouteStats(C.Structure):
+    _fields_ = [("certified", C.c_uint64), ("recomputed", C.c_uint64), ("rows", C.c_uint64)]
 
 
 class CacheStats(C.Structure):
@@ -112,6 +116,8 @@ SIGNATURES = {
     "warp_hip_put_expert": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p]),
     "warp_hip_prefetch": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_int]),
     "warp_hip_get_cache_stats": (None, [C.c_void_p, C.POINTER(CacheStats)]),
+    "warp_hip_get_route_stats": (C.c_int, [C.c_void_p, C.POINTER(RouteStats)]),
+    "warp_hip_router_cert": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p]),
     "warp_hip_moe_decode": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                       C.c_void_p]),
     "warp_hip_moe_decode_host": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]),
@@ -134,6 +140,7 @@ SIGNATURES = {
     "warp_hip_put_expert_dev": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p]),
     "warp_hip_put_expert_synth": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_uint64, C.c_void_p]),
     "warp_hip_set_matvec_path": (C.c_int, [C.c_void_p, C.c_int]),
+    "warp_hip_set_router_fast": (C.c_int, [C.c_void_p, C.c_int]),
     "warp_hip_matvec_kernel": (C.c_char_p, [C.c_void_p, C.c_int, C.c_int]),
     "warp_hip_set_timing": (C.c_int, [C.c_void_p, C.c_int]),
     "warp_hip_get_timing": (C.c_int, [C.c_void_p, C.POINTER(C.c_double), C.POINTER(C.c_uint64)]),
@@ -183,11 +190,11 @@ class Context:
                  routed_scale=1.0, router_act=ROUTE_SIGMOID, router_strict=False, act_situ=False,
                  situ_beta=1.0, situ_linear_beta=0.0, max_tokens=1, rec_bytes, cache_bytes,
                  verify=False, lookahead=0, device=0, latent=0, latent_norm=True, norm_eps=1e-5,
-                 prefill_fp16=False, n_books=0):
+                 prefill_fp16=False, n_books=0, router_fast=False):
         self.cfg = Cfg(hidden, inter, n_experts, top_k, n_layers, FMT.get(fmt, fmt), int(renorm),
                        routed_scale, router_act, int(router_strict), int(act_situ), situ_beta,
                        situ_linear_beta, max_tokens, rec_bytes, cache_bytes, int(verify), lookahead, device,
-                       latent, int(latent_norm), norm_eps, int(prefill_fp16), n_books)
+                       latent, int(latent_norm), norm_eps, int(prefill_fp16), n_books, int(router_fast))
         self.h = C.c_void_p()
         self._keep = []
         rc = lib().warp_hip_open(C.byref(self.cfg), C.byref(self.h))
@@ -300,6 +307,18 @@ class Context:
     def resident(self, layer, expert):
         return lib().warp_hip_resident(self.h, layer, expert)
 
+    def router_cert(self, layer, x_dev, out_dev):
+        """The certified router's [4][E] arrays for one token: point scores,
+        point biased scores, lower and upper bounds of the biased score."""
+        self._check(lib().warp_hip_router_cert(self.h, layer, _addr(x_dev), _addr(out_dev)))
+
+    def route_stats(self):
+        """Certified selection's counters: decode routings certified, those
+        that recomputed rows, and the rows recomputed."""
+        st = RouteStats()
+        self._check(lib().warp_hip_get_route_stats(self.h, C.byref(st)))
+        return {k: getattr(st, k) for k, _ in RouteStats._fields_}
+
     def cache_stats(self):
         st = CacheStats()
         lib().warp_hip_get_cache_stats(self.h, C.byref(st))
@@ -374,6 +393,11 @@ class Context:
         per layer where it routes the token itself)."""
         code = {"auto": 0, "mfma": 1, "fused": 2}[path]
         self._check(lib().warp_hip_set_matvec_path(self.h, code))
+
+    def set_router_fast(self, fast):
+        """True: decode from the fast logits' picks uncertified; False: certify."""
+        self._check(lib().warp_hip_set_router_fast(self.h, int(bool(fast))))
+        self.cfg.router_fast = int(bool(fast))
 
     def matvec_kernel(self, layer, expert_ffn=False):
         """The expert matvec kernel a decode of `layer` runs on the current path."""
