@@ -58,6 +58,7 @@ def _declare(L):
         "or_vq_encode": (None, [vp, i, vp, i, i, i, vp]),
         "or_crc32": (C.c_uint32, [vp, sz]),
         "or_expf_mismatches": (C.c_uint64, [C.c_uint32, C.c_uint64, i, vp]),
+        "or_expf_decreases": (C.c_uint64, [i]),
         "or_kda_step": (None, [i, i, i, vp, vp, vp, vp, vp, vp, vp]),
         "or_rmsnorm": (None, [vp, vp, vp, i, f]),
         "or_expf_array": (None, [vp, vp, C.c_long]),

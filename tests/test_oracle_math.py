@@ -196,6 +196,18 @@ def test_device_expf_is_glibc_on_every_float():
     assert np.count_nonzero(cr.view(np.uint32) != gl.view(np.uint32)) > 0
 
 
+def test_glibc_expf_is_monotone():
+    """glibc's expf never decreases from one float to the next, over every
+    float from -inf to +inf (the device's warp_expf is the same function, by
+    the test above). The certified router bounds a score by the scores at
+    its logit interval's ends when the logits are large, which rests on this
+    (the add and the division that follow are correctly rounded, so
+    monotone). The walk visits the 2^32 - 2^24 + 2 non-NaN patterns in
+    value order (-0 and +0 both)."""
+    import os
+    assert po.lib().or_expf_decreases(max(1, min(os.cpu_count() or 1, 16))) == 0
+
+
 def test_kda_step_against_float64():
     """The KDA recurrence in float64 (q, k L2-normalised, q by 1/sqrt(K);
     S <- diag(exp g) S; d = beta (v - S^T k); S <- S + k d^T; o = S^T q)
