@@ -1332,9 +1332,10 @@ def main():
                     help="K3 decode: cert = certified selection (the reference's picks by construction), fast = "
                          "the fast logits' picks uncertified, strict = every logit in the reference's sequential "
                          "order")
-    ap.add_argument("--matvec-path", choices=["auto", "mfma", "fused"], default="auto",
-                    help="expert matvec kernel: auto = the LUT kernel, mfma = decode-then-dot on the matrix cores, "
-                         "fused = the LUT kernel's gate/up, down and combine in one launch per layer")
+    ap.add_argument("--matvec-path", choices=["auto", "mfma", "fused", "gather"], default="auto",
+                    help="expert matvec kernel: auto = the LUT kernel (the gather kernel for small shapes), mfma = "
+                         "decode-then-dot on the matrix cores, fused = the LUT kernel's gate/up, down and combine in "
+                         "one launch per layer, gather = decode-then-dot with codebook gathers")
     ap.add_argument("--prefill", choices=["exact", "fp16"], default="fp16",
                     help="kimi-prefill: the expert products' precision: fp16 (the configuration's decode-to-16-bit + "
                          "MFMA design: stages added into one fp16 operand against x's fp16 high half, outputs within "

@@ -487,9 +487,12 @@ int warp_hip_put_expert_synth(warp_hip_ctx *c, int layer, int expert, uint64_t s
  * down and combine as work items of one launch per layer where the token's
  * routing runs inside it (the same results bit for bit; slower than AUTO at
  * the K3 shape, where the waits between its work items cost more than the
- * launch boundaries they replace). Applies to warp_hip_moe_decode*,
- * warp_hip_expert_ffn and warp_hip_vq_matvec. */
-enum { WARP_HIP_PATH_AUTO = 0, WARP_HIP_PATH_MFMA = 1, WARP_HIP_PATH_LUT_FUSED = 2 };
+ * launch boundaries they replace); GATHER forces the decode-then-dot
+ * kernel with codebook gathers (no tables: each lane decodes its rows'
+ * weights from the fp16 codebook in L2), which AUTO takes where few rows
+ * share a position (one expert's FFN, small matrices). Applies to
+ * warp_hip_moe_decode*, warp_hip_expert_ffn and warp_hip_vq_matvec. */
+enum { WARP_HIP_PATH_AUTO = 0, WARP_HIP_PATH_MFMA = 1, WARP_HIP_PATH_LUT_FUSED = 2, WARP_HIP_PATH_GATHER = 3 };
 int warp_hip_set_matvec_path(warp_hip_ctx *c, int path);
 /* cfg.router_fast after open: 1 decodes from the fast logits' picks without
  * certifying them, 0 certifies (the default). For measuring what the

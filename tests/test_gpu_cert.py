@@ -109,7 +109,7 @@ def test_certified_picks_on_planted_near_ties(E):
     ctx = open_ctx(model)
     fast = open_ctx(model, router_fast=True)
     import warp_amd
-    paths = ("auto", "mfma", "fused") if E <= 512 else ("auto", "mfma")
+    paths = ("auto", "mfma", "fused", "gather") if E <= 512 else ("auto", "mfma", "gather")
     fast_wrong = 0
     try:
         for t in range(n_tok):
@@ -157,7 +157,7 @@ def test_certified_exact_ties_take_lowest_ids():
         x = rng.normal(size=H).astype(np.float32)
         model.layers[0].router = plant(rng, E, x, cluster, copies=True)
         warp_amd.load_container_model(ctx, model)
-        ri, rl, got, rw = decode_case(model, ctx, x, ("auto", "mfma", "fused"))
+        ri, rl, got, rw = decode_case(model, ctx, x, ("auto", "mfma", "fused", "gather"))
         assert list(ri) == list(range(40, 48)), ri            # exact ties: the lowest ids, in order
         for path, (idx, err, w) in got.items():
             assert np.array_equal(idx, ri), (path, idx, ri)

@@ -67,7 +67,7 @@ def test_config1_single_expert(fmt):
             soff = [0, spec.inter, 2 * spec.inter][kind]
             scale = r[corr + 2 * soff: corr + 2 * (soff + M)].view(np.uint16).copy()
             yr = po.vq_matvec(fmt, r[off:].copy(), scale, x, bT, kind * S, M, N)
-            for path in ("auto", "mfma"):
+            for path in ("auto", "mfma", "fused"):
                 ctx.set_matvec_path(path)
                 y = empty(M)
                 ctx.vq_matvec(0, kind, rec, dev(x), y)
@@ -89,7 +89,7 @@ def test_config1_single_expert(fmt):
             u = po.vq_matvec(fmt, mats[1][0], mats[1][1], x, bT, S0[1], spec.inter, spec.hidden)
             h = np.array([po.lib().or_silu(float(v)) for v in g], np.float32) * u
             yr = po.vq_matvec(fmt, mats[2][0], mats[2][1], h.astype(np.float32), bT, S0[2], spec.hidden, spec.inter)
-            for path in ("auto", "mfma"):
+            for path in ("auto", "mfma", "fused"):
                 ctx.set_matvec_path(path)
                 y = empty(spec.hidden)
                 ctx.expert_ffn(0, 1, dev(x), y)
@@ -100,7 +100,8 @@ def test_config1_single_expert(fmt):
             ctx.expert_ffn(0, 2, dev(x), empty(spec.hidden))      # expert 2 of 2 does not exist
         assert ei.value.code == warp_amd.E_ARG
         ctx.set_matvec_path("auto")
-        log(f"config 1 ({fmt}): gate, up, down and the whole expert FFN within the bar on both kernels")
+        log(f"config 1 ({fmt}): gate, up, down and the whole expert FFN within the bar on the gather (auto), "
+            f"matrix-core and table (fused) kernels")
     finally:
         ctx.close()
 
@@ -126,7 +127,7 @@ def test_config2_kimi_layer(act):
                 share = routed_share(model, 0, x)
                 assert share > 0.05, share
             outs = {}
-            for path in ("auto", "mfma"):
+            for path in ("auto", "mfma", "gather"):
                 ctx.set_matvec_path(path)
                 out = empty(KIMI["hidden"])
                 idx, w = ctx.moe_decode(0, dev(x), out, want_route=True)

@@ -42,7 +42,7 @@ def golden(request):
     ctx.close()
 
 
-@pytest.mark.parametrize("path", ["auto", "mfma"])
+@pytest.mark.parametrize("path", ["auto", "mfma", "gather"])
 def test_moe_layer_against_reference_outputs(golden, path):
     name, spec, model, g, ctx = golden
     ctx.set_matvec_path(path)

@@ -38,7 +38,7 @@ def k3(request):
     ctx.close()
 
 
-@pytest.mark.parametrize("path", ["auto", "mfma"])
+@pytest.mark.parametrize("path", ["auto", "mfma", "gather"])
 def test_k3_decode_full_size(k3, path):
     shared, model, ctx = k3
     ctx.set_matvec_path(path)

@@ -42,7 +42,7 @@ def k3real():
     ctx.close()
 
 
-@pytest.mark.parametrize("path", ["auto", "mfma"])
+@pytest.mark.parametrize("path", ["auto", "mfma", "gather"])
 def test_k3_real_decode(k3real, path):
     model, ctx = k3real
     ctx.set_matvec_path(path)

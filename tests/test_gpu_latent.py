@@ -40,7 +40,7 @@ def test_latent_decode(fmt, norm):
         warp_amd.load_container_model(ctx, model)
         rng = np.random.default_rng(5)
         worst = {}
-        for path in ("auto", "mfma"):
+        for path in ("auto", "mfma", "gather"):
             ctx.set_matvec_path(path)
             w = 0.0
             for t in range(6):
@@ -114,7 +114,7 @@ def test_latent_expert_ffn():
         u = po.vq_matvec("VQ3R", *mat(1)[:2], x, bT, S, I, lat)
         h = (np.array([po.lib().or_silu(float(v)) for v in g], np.float32) * u).astype(np.float32)
         yr = po.vq_matvec("VQ3R", *mat(2)[:2], h, bT, 2 * S, lat, I)
-        for path in ("auto", "mfma"):
+        for path in ("auto", "mfma", "gather"):
             ctx.set_matvec_path(path)
             y = empty(lat)
             ctx.expert_ffn(0, 7, dev(x), y)

@@ -40,13 +40,13 @@ def test_lut_decode_and_matvec(fmt, shape):
         log(f"[{fmt} {SHAPES[shape]}] loaded")
         lv = po.LayerView(model, 0)
         rng = np.random.default_rng(17)
-        worst = {"auto": 0.0, "mfma": 0.0}
+        worst = {"auto": 0.0, "mfma": 0.0, "gather": 0.0}
         for t in range(3):
             x = rng.normal(size=spec.hidden).astype(np.float32)
             ro, ri, rw, _ = lv.moe_layer(x)
             if t == 0 and spec.shared_bits:
                 assert routed_share(model, 0, x) > 0.05
-            for path in ("auto", "mfma"):
+            for path in ("auto", "mfma", "gather"):
                 ctx.set_matvec_path(path)
                 out = empty(spec.hidden)
                 idx, w = ctx.moe_decode(0, dev(x), out, want_route=True)
@@ -55,9 +55,8 @@ def test_lut_decode_and_matvec(fmt, shape):
                 worst[path] = max(worst[path], e)
                 assert e <= TOL, (path, t, e)
         log(f"[{fmt} {SHAPES[shape]}] moe_decode worst rel err lut {worst['auto']:.2e} "
-            f"mfma {worst['mfma']:.2e}")
+            f"mfma {worst['mfma']:.2e} gather {worst['gather']:.2e}")
 
-        ctx.set_matvec_path("auto")
         S = ct.FMT_STAGES[fmt]
         bT = po.books_T(model.books_raw)
         for e in (0, spec.experts - 1):
@@ -67,14 +66,18 @@ def test_lut_decode_and_matvec(fmt, shape):
             for kind in range(3):
                 M, N = (spec.inter, spec.hidden) if kind < 2 else (spec.hidden, spec.inter)
                 x = rng.normal(size=N).astype(np.float32)
-                y = empty(M)
-                ctx.vq_matvec(0, kind, rec, dev(x), y)
                 off, corr = int(hdr[5 + kind]), int(hdr[8])
                 soff = [0, spec.inter, 2 * spec.inter][kind]
                 scale = r[corr + 2 * soff: corr + 2 * (soff + M)].view(np.uint16).copy()
                 yr = po.vq_matvec(fmt, r[off:].copy(), scale, x, bT, kind * S, M, N)
-                err = rel_err(host(y), yr)
-                assert err <= TOL, (e, kind, err)
-        log(f"[{fmt} {SHAPES[shape]}] vq_matvec (lut) within bar")
+                # auto: the gather kernel for one matrix; fused: the table kernel
+                for path in ("auto", "fused"):
+                    ctx.set_matvec_path(path)
+                    y = empty(M)
+                    ctx.vq_matvec(0, kind, rec, dev(x), y)
+                    err = rel_err(host(y), yr)
+                    assert err <= TOL, (e, kind, path, err)
+        ctx.set_matvec_path("auto")
+        log(f"[{fmt} {SHAPES[shape]}] vq_matvec (gather and table kernels) within bar")
     finally:
         ctx.close()

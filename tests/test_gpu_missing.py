@@ -23,7 +23,7 @@ SPEC = dict(hidden=256, inter=128, experts=32, top_k=4, layers=1, fmt="VQ12", se
 RESIDENT = np.arange(0, 32, 4)                     # experts 0, 4, ..., 28 have records
 
 
-@pytest.mark.parametrize("path", ["auto", "mfma"])
+@pytest.mark.parametrize("path", ["auto", "mfma", "gather"])
 def test_missing_expert_is_reported(path):
     import warp_amd
     model = ct.build(ct.Spec(materialize=tuple(int(i) for i in RESIDENT), **SPEC))

@@ -60,7 +60,7 @@ def test_decode_weights_bitexact(loaded):
     log(f"[{fmt}] decoded weights bit-exact")
 
 
-@pytest.mark.parametrize("path", ["auto", "mfma"])
+@pytest.mark.parametrize("path", ["auto", "mfma", "fused"])
 def test_vq_matvec(loaded, path):
     fmt, model, ctx = loaded
     spec = model.spec
@@ -119,7 +119,7 @@ def test_router_strict_and_route(loaded):
     log(f"[{fmt}] strict router bit-exact, selection and weights bit-exact")
 
 
-@pytest.mark.parametrize("path", ["auto", "mfma"])
+@pytest.mark.parametrize("path", ["auto", "mfma", "gather"])
 def test_moe_decode(loaded, path):
     fmt, model, ctx = loaded
     spec = model.spec

@@ -1551,7 +1551,8 @@ static int timing_end(warp_hip_ctx *c)
 
 int warp_hip_set_matvec_path(warp_hip_ctx *c, int path)
 {
-    if (!c || (path != WARP_HIP_PATH_AUTO && path != WARP_HIP_PATH_MFMA && path != WARP_HIP_PATH_LUT_FUSED))
+    if (!c || (path != WARP_HIP_PATH_AUTO && path != WARP_HIP_PATH_MFMA && path != WARP_HIP_PATH_LUT_FUSED &&
+               path != WARP_HIP_PATH_GATHER))
         return WARP_HIP_E_ARG;
     c->mv_path = path;
     return 0;
@@ -1750,10 +1751,28 @@ static int use_table(const warp_hip_ctx *c, const layer_t *L)
     return c->lut_ok && L->books && (c->mv_path != WARP_HIP_PATH_MFMA || L->books_x31);
 }
 
+/* The gather kernel (decode-then-dot, codebook vectors gathered from L2)
+ * instead of the table kernel, for `experts` experts of a decode: where few
+ * rows share each position's tables, building them costs more than
+ * gathering the rows' codebook vectors. */
+static int use_gather(const warp_hip_ctx *c, const layer_t *L, int experts)
+{
+    if (!use_table(c, L) || L->books_x31 || c->He % 32 || c->cfg.inter % 32) return 0;
+    if (c->mv_path == WARP_HIP_PATH_GATHER) return 1;
+    /* AUTO: one expert's matvecs (an expert FFN or one matrix: 1.3-1.8x the
+     * table kernel at [1024 x 2304]); from two experts on, the tables are
+     * shared by enough rows to pay for themselves */
+    return c->mv_path == WARP_HIP_PATH_AUTO && experts == 1;
+}
+
+/* blocks a gather launch aims at */
+#define GATHER_BLOCKS(c) (4 * (c)->n_cu)
+
 const char *warp_hip_matvec_kernel(warp_hip_ctx *c, int layer, int experts)
 {
     if (!c || layer < 0 || layer >= c->cfg.n_layers) return "none";
     const layer_t *L = &c->L[layer];
+    if (use_gather(c, L, experts)) return "k_vq_gather";
     if (use_table(c, L)) return c->mv_path == WARP_HIP_PATH_LUT_FUSED && experts > 1 ? "k_moe_fused" : "k_vq_lut";
     return c->P6 ? "k_apply_p6" : "k_vq_mfma";
 }
@@ -1804,6 +1823,9 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
      * now, before this layer reads the table */
     if (c->crc_pending && (rc = crc_report(c))) return rc;
     const int use_lut = use_table(c, L);
+    /* the gather kernel reads x in f32 and leaves its partial sums where the
+     * table kernel does; it routes in a launch of its own */
+    const int gat = use_gather(c, L, K);
     /* a resident record naming other codebooks than the layer's: the
      * selection goes through the host, which picks the codebooks */
     const int foreign = layer_foreign(c, layer);
@@ -1832,9 +1854,18 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
      * launch (gate, up, act) and the combine (down) */
     warp_shared_args sa;
     int fuse_shared = use_lut && !lat && shared_args(c, L, &sa) && wk_shared_fast_ok(H, &sa);
-    /* where the device routes with the expert table, the table kernel's
-     * gate/up launch does the routing itself (one launch less) */
-    const int fuse_route = use_lut && !foreign && (L->resident == E || !can_fetch(c)) &&
+    /* sigmoid scores from an fp32 router: the selection is certified (the
+     * router launch bounds every logit against the reference's sequential
+     * sum, and its last block recomputes the rows those bounds leave
+     * unordered), unless the caller asked for the plain fast logits or
+     * strict ones. Where the device routes with the expert table and the
+     * layer has no shared expert, that last block also routes (picks,
+     * weights, job lists) */
+    const int cert = cert_ok(c, L);
+    const int cert_route = cert && !foreign && (L->resident == E || !can_fetch(c)) && !L->sq[0];
+    /* else, where the device routes with the expert table, the table
+     * kernel's gate/up launch does the routing itself (one launch less) */
+    const int fuse_route = use_lut && !gat && !cert_route && !foreign && (L->resident == E || !can_fetch(c)) &&
                            wk_lut_route_ok(g->fmt, E, K, 1, 0, 2);
     /* and where that launch leaves CUs idle, one more row of its blocks
      * computes the shared expert's gate/up rows (one row per wave) instead
@@ -1848,21 +1879,20 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
                    (size_t)sa.inter * sizeof(float) <= 64 * 1024 && sa.inter / (sa.bits == 8 ? 16 : 32) <= 256 &&
                    (H + 63) / 64 < c->n_cu / 2;
     }
-    /* sigmoid scores from an fp32 router: the selection is certified (the
-     * router launch bounds every logit against the reference's sequential
-     * sum, and its last block recomputes the rows those bounds leave
-     * unordered), unless the caller asked for the plain fast logits or
-     * strict ones; the certifying router launch computes no shared expert */
-    const int cert = cert_ok(c, L);
+    /* (the certifying router launch computes no shared expert) */
     if (cert && fuse_shared && !sh_in_gu) fuse_shared = 0;
     /* else, for sigmoid scores from an fp32 router, the router launch also
      * scores (one pass less in the routing prologue) */
     const int scored = fuse_route && (!fuse_shared || sh_in_gu) && L->router && !g->router_strict &&
                        g->router_act == WARP_HIP_ROUTE_SIGMOID;
+    if (cert_route) KRN(c, wait_copies(c));       /* (the router's last block reads the expert table) */
     if ((rc = timing_begin(c, 2))) return rc;
-    if (cert)
+    if (cert) {
+        const warp_route_args pick = { NULL, NULL, table, E, g->router_act, g->renorm, I, g->routed_scale, c->idx,
+                                       c->w, c->jobs, c->njobs, c->missing, 2, NULL, NULL, 0, NULL };
         KRN(c, wk_router_cert(L->router, x_dev, E, H, L->bias, c->logits, c->cert_done, K, c->cert_ctr, c->missing,
-                              c->st));
+                              cert_route ? &pick : NULL, c->st));
+    }
     else if (fuse_shared && !sh_in_gu) KRN(c, wk_router_shared(L->router, x_dev, E, H, c->logits, &sa, c->st));
     else if (scored) KRN(c, wk_router_scored(L->router, x_dev, E, H, L->bias, c->logits, c->st));
     else KRN(c, logits_of(c, L, x_dev, 1, c->logits, c->st));
@@ -1884,7 +1914,7 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
         /* everything resident: route and build the jobs on the device, no
          * host round trip */
         KRN(c, wait_copies(c));
-        if (!fuse_route) KRN(c, route_one(c, &ra, K, 1, c->st));
+        if (!fuse_route && !cert_route) KRN(c, route_one(c, &ra, K, 1, c->st));
         c->stats.hits += (uint64_t)K;
         release_hold(c, layer);
     } else if (!can_fetch(c) && !foreign) {
@@ -1892,7 +1922,7 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
          * not resident (sticky), the combine poisons this layer's output with
          * NaN, and the next synchronising call reports E_MISSING */
         KRN(c, wait_copies(c));
-        if (!fuse_route) KRN(c, route_one(c, &ra, K, 1, c->st));
+        if (!fuse_route && !cert_route) KRN(c, route_one(c, &ra, K, 1, c->st));
         c->missing_pending = 1;
         release_hold(c, layer);
     } else {
@@ -1933,7 +1963,20 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
     float *yk[3] = { c->yg, c->yu, c->yd };
     int sp_d = 0;
     size_t d_off = 0;
-    if (use_lut) {
+    if (gat && !B->books_x31) {
+        int sp_gu = 0;
+        if ((rc = timing_begin(c, 0))) return rc;
+        KRN(c, wk_vq_gather(g->fmt, c->jobs, c->njobs, K, 0, 2, B->books, xe, 1, c->part, c->part_cap, I, He,
+                            GATHER_BLOCKS(c), NULL, 0, 0, 0.0f, 0.0f, NULL, 0, NULL, NULL, NULL, &sp_gu, c->st));
+        if ((rc = timing_end(c))) return rc;
+        const size_t gu_floats = (size_t)2 * sp_gu * K * (((size_t)I + 63) / 64) * 64;
+        if ((rc = timing_begin(c, 1))) return rc;
+        KRN(c, wk_vq_gather(g->fmt, c->jobs, c->njobs, K, 2, 1, B->books, NULL, 0, c->part + gu_floats,
+                            c->part_cap - gu_floats, He, I, GATHER_BLOCKS(c), c->part, sp_gu, g->act_situ,
+                            g->situ_beta, g->situ_linear_beta, NULL, 0, NULL, NULL, NULL, &sp_d, c->st));
+        d_off = gu_floats;
+        if ((rc = timing_end(c))) return rc;
+    } else if (use_lut) {
         int sp_gu = 0;
         if ((rc = timing_begin(c, 0))) return rc;
         KRN(c, wk_vq_lut(g->fmt, c->jobs, c->njobs, K, 0, 2, B->books, B->books_x31, xe, 1, c->part, c->part_cap, I, He,
@@ -2007,10 +2050,29 @@ int warp_hip_expert_ffn(warp_hip_ctx *c, int layer, int expert, const float *x_d
     if ((rc = books_of(c, layer, &expert, 1, &B))) return rc;
     /* the record's table entry may still be on its way (copy stream) */
     KRN(c, wait_copies(c));
-    KRN(c, wk_expert_jobs(c->table_dev + (size_t)layer * g->n_experts + expert, I, c->jobs, c->njobs, c->w,
-                          c->missing, c->st));
+    const warp_slot *entry = c->table_dev + (size_t)layer * g->n_experts + expert;
     c->missing_pending = 1;
     if ((rc = x31_check(c, B, layer))) return rc;
+    if (use_gather(c, B, 1)) {
+        /* two launches: gate/up from the expert's table entry, and down, whose
+         * last block per row block writes the rows (no job-list or combine
+         * launch); a missing record sets the flag and out to NaN */
+        int sp_gu = 0;
+        if ((rc = timing_begin(c, 0))) return rc;
+        KRN(c, wk_vq_gather(g->fmt, NULL, NULL, 1, 0, 2, B->books, x_dev, 1, c->part, c->part_cap, I, H,
+                            GATHER_BLOCKS(c), NULL, 0, 0, 0.0f, 0.0f, entry, I, NULL, NULL, c->missing, &sp_gu,
+                            c->st));
+        if ((rc = timing_end(c))) return rc;
+        const size_t gu_floats = (size_t)2 * sp_gu * (((size_t)I + 63) / 64) * 64;
+        if ((rc = timing_begin(c, 1))) return rc;
+        KRN(c, wk_vq_gather(g->fmt, NULL, NULL, 1, 2, 1, B->books, NULL, 0, c->part + gu_floats,
+                            c->part_cap - gu_floats, H, I, GATHER_BLOCKS(c), c->part, sp_gu, g->act_situ,
+                            g->situ_beta, g->situ_linear_beta, entry, I, out_dev, c->fz_sync, c->missing, NULL,
+                            c->st));
+        if ((rc = timing_end(c))) return rc;
+        return 0;
+    }
+    KRN(c, wk_expert_jobs(entry, I, c->jobs, c->njobs, c->w, c->missing, c->st));
     if (use_table(c, B)) {
         int sp_gu = 0, sp_d = 0;
         if ((rc = timing_begin(c, 0))) return rc;
@@ -2317,6 +2379,11 @@ int warp_hip_vq_matvec(warp_hip_ctx *c, int layer, int kind, const uint8_t *rec_
         float *ls = kind == 2 ? c->lscaled : c->lscale;
         KRN(c, wk_lut_p6(x_dev, 1, N, books_kind(c, B, kind), lut, ls, c->st));
         KRN(c, wk_apply_p6(c->jobs, c->njobs, 1, kind, lut, ls, y_dev, M, N, c->st));
+    } else if (use_gather(c, B, 1) && N % 32 == 0) {
+        /* one launch: its last block per row block writes the rows */
+        KRN(c, wk_vq_gather(c->cfg.fmt, c->jobs, c->njobs, 1, kind, 1, B->books, x_dev, 1, c->part, c->part_cap, M,
+                            N, GATHER_BLOCKS(c), NULL, 0, 0, 0.0f, 0.0f, NULL, 0, y_dev, c->fz_sync, NULL, NULL,
+                            c->st));
     } else if (use_table(c, B)) {
         float *yk[3] = { y_dev, y_dev, y_dev };
         int sp = 0;
@@ -2378,7 +2445,8 @@ int warp_hip_router_cert(warp_hip_ctx *c, int layer, const float *x_dev, float *
     const layer_t *L = &c->L[layer];
     if (!L->router || g->router_act != WARP_HIP_ROUTE_SIGMOID)
         return set_err(c, WARP_HIP_E_ARG, layer, -1, "certified router needs an F32 router and sigmoid scores");
-    KRN(c, wk_router_cert(L->router, x_dev, g->n_experts, g->hidden, L->bias, out_dev, NULL, 0, NULL, NULL, c->st));
+    KRN(c, wk_router_cert(L->router, x_dev, g->n_experts, g->hidden, L->bias, out_dev, NULL, 0, NULL, NULL, NULL,
+                          c->st));
     DEV(c, hipStreamSynchronize(c->st));
     return 0;
 }

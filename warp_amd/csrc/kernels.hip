@@ -657,6 +657,7 @@ struct CertTail {
     int K;
     unsigned long long *cctr;
     int *flag;                  // a wait past CERT_POLLS sets bit 2 (value 4)
+    warp_route_args pk;         // pk.idx set: the routing's outputs (idx, w; with pk.table the job lists)
 };
 constexpr unsigned CERT_POLLS = 1u << 16;   // polls of the rows' words before the last block gives up
 template <int NT>
@@ -828,10 +829,14 @@ static bool router_cert_b(const float *W, const float *x, int E, int H, const fl
 }
 
 extern "C" int wk_router_cert(const float *W, const float *x, int E, int H, const float *bias, float *out,
-                              unsigned *done, int K, unsigned long long *cctr, int *flag, void *stream) {
+                              unsigned *done, int K, unsigned long long *cctr, int *flag,
+                              const warp_route_args *pick, void *stream) {
     if (E <= 0 || H <= 0 || (H & 3) || H > 1024 * CERT_MAXV) return -1;
     if (done && (K <= 0 || K > WARP_MAX_K || K > E || E > CERT_EMAX)) return -1;
-    const CertTail t = {done, K, cctr, flag};
+    if (pick && (!done || !pick->idx || !pick->w || (pick->table && (!pick->jobs || !pick->njobs || !flag))))
+        return -1;
+    CertTail t = {done, K, cctr, flag, {}};
+    if (pick) t.pk = *pick;
     // hidden sizes of the reference's models (Kimi-Linear 2304, K3 7168) and
     // their neighbours take the staged kernel
     const hipStream_t st = (hipStream_t)stream;
@@ -2333,17 +2338,25 @@ __device__ void cert_last(const float *__restrict__ W, const float *__restrict__
     r.cx = x;
     r.ch = H;
     r.cctr = t.cctr;
-    int n;
     unsigned long long *amb = cl_amb;
-    if (E <= 512) {
-        route_pick_lds<true, NT>(E, t.K, 0, 0, 1.0f, score, biased, sel, wsel, false, true, nullptr, lo, hi, cl_amb,
-                                 &cl_namb);
-        n = cl_namb;
-    } else {
-        const int np = route_pick_lds<false, NT>(E, t.K, 0, 0, 1.0f, score, biased, sel, wsel, false, true);
-        n = cert_check<NT, CERT_EMAX / 64>(r, E, np, score, biased, lo, hi, sel, false, amb);
-    }
-    if (n) {                                              // uniform
+    const warp_route_args &pk = t.pk;
+    const bool want = pk.idx != nullptr;                  // the routing's outputs too (its weights)
+    // pass 0 picks and tests; where it recomputed rows, pass 1 picks again
+    // from the exact values, for the routing's outputs (one call site per
+    // picking kernel: the block's registers are the row blocks' too)
+#pragma nounroll
+    for (int pass = 0; pass < 2; pass++) {
+        int n;
+        if (E <= 512) {
+            route_pick_lds<true, NT>(E, t.K, 0, pk.renorm, pk.routed_scale, score, biased, sel, wsel, want, true,
+                                     nullptr, pass ? nullptr : lo, hi, cl_amb, &cl_namb);
+            n = pass ? 0 : cl_namb;
+        } else {
+            const int np = route_pick_lds<false, NT>(E, t.K, 0, pk.renorm, pk.routed_scale, score, biased, sel, wsel,
+                                                     want, true);
+            n = pass ? 0 : cert_check<NT, CERT_EMAX / 64>(r, E, np, score, biased, lo, hi, sel, false, amb);
+        }
+        if (!n) break;                                    // uniform
         cert_count(r, n);
         for (int i = tid; i < nw; i += NT) cl_rows[i] = amb[i];   // (the recompute consumes amb)
         __syncthreads();
@@ -2355,7 +2368,16 @@ __device__ void cert_last(const float *__restrict__ W, const float *__restrict__
                 out[2 * E + e] = biased[e];
                 out[3 * E + e] = biased[e];
             }
+        if (!want) return;                                // uniform
     }
+    if (!want) return;                                    // uniform
+    // the routing of these arrays, as wk_route does it (route1_block): the
+    // picks and weights, and the job lists
+    if (tid < t.K) {
+        pk.idx[tid] = sel[tid];
+        pk.w[tid] = wsel[tid];
+    }
+    if (pk.table) route_jobs<NT>(sel, t.K, pk.table, pk.jobs, pk.njobs, t.flag, pk.inter);
 }
 
 // Certified routing of one token by a CERT_NT-thread block: the four arrays of
@@ -4169,6 +4191,315 @@ extern "C" int wk_vq_lut(int fmt, const warp_job *jobs, const int *njobs, int ma
     case WARP_FMT_VQ3R: return launch_lut_x<WARP_FMT_VQ3R>(a, groups, nkinds, books_x31, stream);
     case WARP_FMT_VQ2R: return launch_lut_x<WARP_FMT_VQ2R>(a, groups, nkinds, books_x31, stream);
     case WARP_FMT_VQ12: return launch_lut_x<WARP_FMT_VQ12>(a, groups, nkinds, books_x31, stream);
+    }
+    return -1;
+}
+
+// ---- small shapes: decode-then-dot with codebook gathers ----------------------------
+//
+// One token's expert matvecs where few rows share a position (one expert's
+// FFN, a Kimi-Linear-shape decode): the table kernel would build S x E
+// entries per position, and stage a 2 x 4096-entry codebook per block, for a
+// few thousand rows. Here each lane decodes its weights instead: the code
+// word of 4 rows at one position, each row's S codebook vectors gathered
+// from the fp16 codebook in global memory (L2-resident: 128 KiB per kind for
+// 2 x 4096 entries), added in fp32 and dotted with the position's 8 inputs.
+// A block (GA_NW waves) takes one 64-row block of one job and a range of
+// position groups (4 positions, the record's 256-slot [position][row] unit);
+// wave w takes groups pg0 + w, pg0 + w + GA_NW, ...; lane l the group's
+// position l / 16 and rows 4 (l % 16) .. + 3. The unscaled partial sums of a
+// split go where the table kernel puts them ([kind][split][job][row]), so
+// the down launch's act prologue and the combine read either kernel's.
+constexpr int GA_NW = 4;            // waves per block
+constexpr int GA_W = 8;             // code words a lane loads ahead
+constexpr int GA_XMAX = 16384;      // inputs a block stages in LDS (64 KiB)
+
+template <int FMT>
+__device__ __forceinline__ float ga_row(const uint4 (&v)[FmtT<FMT>::S], const float4 &x0, const float4 &x1,
+                                        float acc) {
+    float w[8];
+    {
+        const half8 h = __builtin_bit_cast(half8, v[0]);
+#pragma unroll
+        for (int i = 0; i < 8; i++) w[i] = (float)h[i];
+    }
+#pragma unroll
+    for (int s = 1; s < FmtT<FMT>::S; s++) {
+        const half8 h = __builtin_bit_cast(half8, v[s]);
+#pragma unroll
+        for (int i = 0; i < 8; i++) w[i] += (float)h[i];
+    }
+    acc = __builtin_fmaf(w[0], x0.x, acc);
+    acc = __builtin_fmaf(w[1], x0.y, acc);
+    acc = __builtin_fmaf(w[2], x0.z, acc);
+    acc = __builtin_fmaf(w[3], x0.w, acc);
+    acc = __builtin_fmaf(w[4], x1.x, acc);
+    acc = __builtin_fmaf(w[5], x1.y, acc);
+    acc = __builtin_fmaf(w[6], x1.z, acc);
+    return __builtin_fmaf(w[7], x1.w, acc);
+}
+
+// The gather kernel's arguments: those of the table kernel it stands in for
+// (jobs, inputs, the partial-sum layout, the down launch's act inputs) and
+// two of its own. slot (or NULL): one expert's FFN, whose jobs come from its
+// expert-table entry (record, header offsets; inter gives the scale arrays'
+// places) instead of a job list -- no job-list launch. out (or NULL, one
+// job, one kind): the launch also finishes the matvec -- the last block of
+// each row block to arrive (ctr, one zeroed word per row block, left
+// zeroed) adds the row block's partial sums in split order and writes out =
+// sum x the row scale -- no reduction launch. missing: set when the slot has
+// no record (out then gets NaN).
+struct GatherArgs {
+    const warp_job *jobs;
+    const int *njobs;
+    int max_jobs, kind_lo;
+    const warp_slot *slot;
+    int inter;
+    const uint16_t *books;     // [3][S][E][8] fp16, subnormals flushed
+    const float *x;
+    float *part;               // [nkinds][splits][max_jobs][nrb * 64]
+    int M, N, splits, shared_x;
+    const float *act_part;
+    int act_splits, act_situ;
+    float act_beta, act_lbeta;
+    float *out;
+    unsigned *ctr;
+    int *missing;
+};
+
+// Job j of a kind: its index block, row scales and input row (a job list's
+// entry, or the slot's record); false when the record is missing.
+__device__ __forceinline__ bool ga_job(const GatherArgs &a, int kind, int j, const uint8_t *&idx,
+                                       const uint16_t *&scale, int &xi) {
+    if (a.slot) {
+        const uint8_t *rec = a.slot->rec;
+        if (!rec) return false;
+        idx = rec + a.slot->off[kind];
+        scale = (const uint16_t *)(rec + a.slot->off[3]) + (kind == 0 ? 0 : kind == 1 ? a.inter : 2 * a.inter);
+        xi = 0;
+        return true;
+    }
+    const warp_job &jb = a.jobs[(size_t)kind * a.max_jobs + j];
+    idx = jb.idx;
+    scale = jb.scale;
+    xi = jb.xi[0];
+    return true;
+}
+
+// SHX: every job reads x (gate and up); ACT: job j's input is act(gate, up)
+// from the gate/up partial sums (a.act_part, a.act_splits), as the table
+// kernel's down launch makes it; neither: job j reads x + xi[0] N.
+template <int FMT, bool SHX, bool ACT>
+__global__ __launch_bounds__(GA_NW * 64) void k_vq_gather(GatherArgs a) {
+    typedef FmtT<FMT> F;
+    extern __shared__ __attribute__((aligned(16))) float gx[];   // the split's inputs
+    __shared__ float red[GA_NW][64];
+    __shared__ uint64_t s_exp[32];
+    __shared__ unsigned s_last;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kind = a.kind_lo + (int)blockIdx.y;
+    const int nv = a.N >> 3, npg = nv >> 2, nrb = (a.M + 63) >> 6;
+    const int fb = (int)blockIdx.x / a.splits, split = (int)blockIdx.x % a.splits;
+    const int j = fb / nrb, rb = fb - j * nrb;
+    const uint8_t *jidx;
+    const uint16_t *jscale;
+    int jxi;
+    if (!ga_job(a, kind, j, jidx, jscale, jxi)) {          // uniform: the slot has no record
+        if (a.out && split == 0 && tid < 64 && rb * 64 + tid < a.M) a.out[rb * 64 + tid] = __builtin_nanf("");
+        if (blockIdx.x == 0 && blockIdx.y == 0 && tid == 0 && a.missing) *a.missing = 1;
+        return;
+    }
+    if (!a.slot && j >= a.njobs[kind]) return;             // uniform per block
+    const int pg0 = split * npg / a.splits, pg1 = (split + 1) * npg / a.splits;
+    const int nx = (pg1 - pg0) * 32;                       // inputs of this split
+    const int ng = pg1 - pg0 > wave ? (pg1 - pg0 - wave + GA_NW - 1) / GA_NW : 0;   // this wave's groups
+
+    // the first code words (from HBM) before anything else
+    const uint8_t *cp = jidx + (size_t)rb * nv * 64 * F::SB + (size_t)lane * 4 * F::SB +
+                        (size_t)(pg0 + wave) * 256 * F::SB;
+    constexpr size_t GSTEP = (size_t)GA_NW * 256 * F::SB;     // a wave's next group
+    Word<F::SB> wd[GA_W];
+#pragma unroll
+    for (int k = 0; k < GA_W; k++)
+        if (k < ng) wd[k].load(cp + k * GSTEP);
+
+    // the inputs of the split, into LDS
+    const int c0 = pg0 * 32;
+    if constexpr (ACT) {
+        if (tid < 32) s_exp[tid] = g_exp2_tab[tid];
+        const size_t arows = (size_t)((a.N + 63) >> 6) * 64, astride = (size_t)a.max_jobs * arows;
+        const uint8_t *i0, *i1;
+        const uint16_t *sc0, *sc1;
+        int x0, x1;
+        ga_job(a, 0, j, i0, sc0, x0);
+        ga_job(a, 1, j, i1, sc1, x1);
+        gu32 *sg = (gu32 *)sc0;
+        gu32 *su = (gu32 *)sc1;
+        const float *pg = a.act_part + (size_t)j * arows + c0;
+        const float *pu = pg + (size_t)a.act_splits * astride;
+        __syncthreads();                                   // s_exp
+        for (int i = tid; i < nx; i += GA_NW * 64) {
+            const int sh = 16 * ((c0 + i) & 1);
+            const float g = lut_rowsum8(pg + i, a.act_splits, astride) * f16_keep((uint16_t)(sg[(c0 + i) >> 1] >> sh));
+            const float u = lut_rowsum8(pu + i, a.act_splits, astride) * f16_keep((uint16_t)(su[(c0 + i) >> 1] >> sh));
+            gx[i] = act_pair(g, u, a.act_situ, a.act_beta, a.act_lbeta, s_exp);
+        }
+    } else {
+        const float *xs = a.x + (SHX ? (size_t)0 : (size_t)jxi * a.N) + c0;
+        for (int i = tid * 4; i < nx; i += GA_NW * 64 * 4) *(float4 *)(gx + i) = *(const float4 *)(xs + i);
+    }
+    __syncthreads();
+
+    const uint4 *bk = (const uint4 *)(a.books + (size_t)kind * F::S * F::E * 8);
+    const float *xl = gx + (size_t)wave * 32 + (lane >> 4) * 8;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int k0 = 0; k0 < ng; k0 += GA_W) {
+#pragma unroll
+        for (int k = 0; k < GA_W; k++) {
+            const int g = k0 + k;
+            if (g < ng) {                                  // uniform per wave
+                const Word<F::SB> w = wd[k];
+                if (g + GA_W < ng) wd[k].load(cp + (size_t)(g + GA_W) * GSTEP);
+                uint4 v[4][F::S];
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    const unsigned sl = w.slot(t);
+#pragma unroll
+                    for (int s = 0; s < F::S; s++) v[t][s] = bk[s * F::E + lut_code<FMT>(sl, s)];
+                }
+                const float4 x0 = *(const float4 *)(xl + (size_t)g * GA_NW * 32);
+                const float4 x1 = *(const float4 *)(xl + (size_t)g * GA_NW * 32 + 4);
+#pragma unroll
+                for (int t = 0; t < 4; t++) acc[t] = ga_row<FMT>(v[t], x0, x1, acc[t]);
+            }
+        }
+    }
+    // the four positions of a lane's rows, then the waves, in order
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        acc[t] += __shfl_xor(acc[t], 16);
+        acc[t] += __shfl_xor(acc[t], 32);
+    }
+    if (lane < 16) *(float4 *)&red[wave][4 * lane] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    __syncthreads();
+    const size_t kstride = (size_t)a.max_jobs * nrb * 64;  // one split of one kind
+    float *po = a.part + ((size_t)blockIdx.y * a.splits * kstride) + (size_t)fb * 64 + tid;
+    if (!a.out) {
+        if (tid < 64) {
+            float s = red[0][tid];
+#pragma unroll
+            for (int w = 1; w < GA_NW; w++) s += red[w][tid];
+            po[(size_t)split * kstride] = s;
+        }
+        return;
+    }
+    // Finishing the matvec: the row block's partial sums go out with
+    // agent-coherent stores, complete before the block's count rises; the
+    // block that raises it to the split count reads them all (agent-coherent
+    // loads) and writes the rows.
+    if (tid < 64) {
+        float s = red[0][tid];
+#pragma unroll
+        for (int w = 1; w < GA_NW; w++) s += red[w][tid];
+        st_agent(po + (size_t)split * kstride, s);
+        wait_stores();
+    }
+    __syncthreads();
+    if (tid == 0) s_last = __hip_atomic_fetch_add(a.ctr + fb, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (s_last != (unsigned)a.splits - 1) return;          // uniform
+    const int row = rb * 64 + tid;
+    if (tid < 64 && row < a.M) {
+        float v = 0.0f;
+        for (int s0 = 0; s0 < a.splits; s0 += 8) {
+            float a8[8];
+#pragma unroll
+            for (int q = 0; q < 8; q++) a8[q] = ld_agent(po + (size_t)min(s0 + q, a.splits - 1) * kstride);
+#pragma unroll
+            for (int q = 0; q < 8; q++)
+                if (s0 + q < a.splits) v += a8[q];
+        }
+        a.out[row] = v * f16_keep(jscale[row]);
+    }
+    if (tid == 0) __hip_atomic_store(a.ctr + fb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Splits of the gather kernel: about target_blocks blocks, each wave at
+// least one position group where the shape allows, at most GA_XMAX inputs a
+// block, and the partial sums within cap_floats.
+extern "C" int wk_gather_plan(int M, int N, int max_jobs, int nkinds, int target_blocks, size_t cap_floats,
+                              int *splits_out) {
+    if (M <= 0 || N <= 0 || (N % 32) || max_jobs <= 0 || nkinds < 1 || nkinds > 3) return -1;
+    const long nrb = (M + 63) / 64, npg = N / 32, units = (long)nkinds * max_jobs * nrb;
+    long splits = target_blocks > units ? target_blocks / units : 1;
+    if (splits > npg / GA_NW) splits = npg / GA_NW;
+    if (splits > 32) splits = 32;
+    if (splits < 1) splits = 1;
+    const long smin = (npg * 32 + GA_XMAX - 1) / GA_XMAX;
+    if (splits < smin) splits = smin;
+    if ((size_t)nkinds * splits * max_jobs * nrb * 64 > cap_floats) return -1;
+    if (units * splits > 0x7fffffffL) return -1;
+    *splits_out = (int)splits;
+    return 0;
+}
+
+template <int FMT, bool SHX, bool ACT>
+static int launch_gather(const GatherArgs &a, int nkinds, void *stream) {
+    const int npg = a.N / 32, nrb = (a.M + 63) / 64;
+    const size_t lds = (size_t)((npg + a.splits - 1) / a.splits) * 32 * sizeof(float);
+    static std::atomic<uint64_t> attr{0};
+    if (int r_ = lds_limit((const void *)k_vq_gather<FMT, SHX, ACT>, (int)lds, attr, stream)) return r_;
+    hipLaunchKernelGGL((k_vq_gather<FMT, SHX, ACT>), dim3(a.max_jobs * nrb * a.splits, nkinds), dim3(GA_NW * 64),
+                       lds, (hipStream_t)stream, a);
+    CHECK_LAUNCH();
+    return 0;
+}
+
+template <int FMT>
+static int launch_gather_x(const GatherArgs &a, int nkinds, void *stream) {
+    if (a.act_part) return launch_gather<FMT, false, true>(a, nkinds, stream);
+    if (a.shared_x) return launch_gather<FMT, true, false>(a, nkinds, stream);
+    return launch_gather<FMT, false, false>(a, nkinds, stream);
+}
+
+extern "C" int wk_vq_gather(int fmt, const warp_job *jobs, const int *njobs, int max_jobs, int kind_lo, int nkinds,
+                            const uint16_t *books, const float *x, int shared_x, float *part, size_t cap_floats,
+                            int M, int N, int target_blocks, const float *act_part, int act_splits, int act_situ,
+                            float act_beta, float act_lbeta, const warp_slot *slot, int inter, float *out,
+                            unsigned *ctr, int *missing, int *splits_out, void *stream) {
+    if (kind_lo < 0 || kind_lo + nkinds > 3 || !books || !part) return -1;
+    if (slot ? (max_jobs != 1 || inter <= 0) : (!jobs || !njobs)) return -1;
+    if (act_part ? (shared_x || kind_lo != 2 || nkinds != 1 || act_splits <= 0) : !x) return -1;
+    if (out && (max_jobs != 1 || nkinds != 1 || !ctr)) return -1;
+    int splits;
+    if (wk_gather_plan(M, N, max_jobs, nkinds, target_blocks, cap_floats, &splits)) return -1;
+    GatherArgs a = {};
+    a.jobs = jobs;
+    a.njobs = njobs;
+    a.max_jobs = max_jobs;
+    a.kind_lo = kind_lo;
+    a.slot = slot;
+    a.inter = inter;
+    a.books = books;
+    a.x = x;
+    a.part = part;
+    a.M = M;
+    a.N = N;
+    a.splits = splits;
+    a.shared_x = shared_x;
+    a.act_part = act_part;
+    a.act_splits = act_splits;
+    a.act_situ = act_situ;
+    a.act_beta = act_beta;
+    a.act_lbeta = act_lbeta;
+    a.out = out;
+    a.ctr = ctr;
+    a.missing = missing;
+    if (splits_out) *splits_out = splits;
+    switch (fmt) {
+    case WARP_FMT_VQ3R: return launch_gather_x<WARP_FMT_VQ3R>(a, nkinds, stream);
+    case WARP_FMT_VQ2R: return launch_gather_x<WARP_FMT_VQ2R>(a, nkinds, stream);
+    case WARP_FMT_VQ12: return launch_gather_x<WARP_FMT_VQ12>(a, nkinds, stream);
     }
     return -1;
 }

@@ -104,9 +104,14 @@ int wk_router_scored(const float *W, const float *x, int E, int H, const float *
  * order the bounds leave open with their exact (sequential) values, so that
  * a routing from [0, 2E) (scored = 1) picks the reference's experts in its
  * order; cctr as in warp_route_args; flag (or NULL): bit 2 (value 4) set
- * when the last block's wait for the rows gives up. E <= 4096 with done. */
+ * when the last block's wait for the rows gives up. E <= 4096 with done.
+ * pick (with done, or NULL): the last block also writes what wk_route
+ * writes from those arrays -- pick->idx and pick->w (renorm, routed_scale),
+ * and with pick->table the job lists (pick->jobs, njobs, inter; a pick
+ * without a record sets *flag) -- so that no routing launch follows. */
+struct warp_route_args_s;
 int wk_router_cert(const float *W, const float *x, int E, int H, const float *bias, float *out, unsigned *done,
-                   int K, unsigned long long *cctr, int *flag, void *stream);
+                   int K, unsigned long long *cctr, int *flag, const struct warp_route_args_s *pick, void *stream);
 
 /* Quantised router / dense trunk rows (Q8G, Q4G, Q3G with the reference's
  * packing): y [T][M] = dequant(W) [M][N] . x [T][N]. */
@@ -212,7 +217,7 @@ int wk_lut_plan(int M, int N, int max_jobs, int nkinds, int shared_x, int target
  * and the token's input the routing recomputes ambiguous logits from
  * (sequentially, as the reference sums); cctr (or NULL) [2] counts the
  * routings that recomputed and the rows recomputed. */
-typedef struct {
+typedef struct warp_route_args_s {
     const float *logits, *bias;
     const warp_slot *table;
     int E, act, renorm, inter;
@@ -247,6 +252,22 @@ int wk_vq_lut(int fmt, const warp_job *jobs, const int *njobs, int max_jobs, int
  * reading jobs/njobs; route->jobs/njobs/idx/w/missing get what wk_route
  * writes. Only where wk_lut_route_ok says so; NULL otherwise.) */
 int wk_lut_route_ok(int fmt, int E, int K, int shared_x, int kind_lo, int nkinds);
+/* The decode-then-dot kernel with codebook gathers, for one token's
+ * matvecs where few rows share a position: the arguments and the partial
+ * sums of wk_vq_lut (no routing, no shared rows, no exponent-31 codebooks;
+ * N % 32 == 0). target_blocks: about how many blocks to launch.
+ * slot (or NULL; max_jobs = 1): one expert's jobs from its expert-table
+ * entry instead of jobs/njobs (inter: the scale arrays' places); a missing
+ * record sets *missing. out (or NULL; one job of one kind): the launch also
+ * writes out [M] = the rows' sum times their scale, its last block per row
+ * block adding the splits (ctr: zeroed words, one per row block, left
+ * zeroed; NaN rows where the slot's record is missing). */
+int wk_vq_gather(int fmt, const warp_job *jobs, const int *njobs, int max_jobs, int kind_lo, int nkinds,
+                 const uint16_t *books, const float *x, int shared_x, float *part, size_t cap_floats, int M, int N,
+                 int target_blocks, const float *act_part, int act_splits, int act_situ, float act_beta,
+                 float act_lbeta, const warp_slot *slot, int inter, float *out, unsigned *ctr, int *missing,
+                 int *splits_out, void *stream);
+int wk_gather_plan(int M, int N, int max_jobs, int nkinds, int target_blocks, size_t cap_floats, int *splits_out);
 /* Certified routing of one decode token (route->scored == 2, sigmoid): what
  * wk_route writes, with route->table (or NULL) for the job lists, from
  * wk_router_cert's arrays; ambiguous rows recomputed from cw / cx. E <= 4096. */

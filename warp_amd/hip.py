@@ -388,10 +388,11 @@ class Context:
         self._check(lib().warp_hip_put_expert_synth(self.h, layer, expert, seed, _addr(scales_u16)))
 
     def set_matvec_path(self, path):
-        """"auto" (the LUT kernel for decode where it applies), "mfma" or
-        "fused" (the LUT kernel's gate/up, down and combine in one launch
-        per layer where it routes the token itself)."""
-        code = {"auto": 0, "mfma": 1, "fused": 2}[path]
+        """"auto" (the LUT kernel for decode where it applies, the gather
+        kernel for small shapes), "mfma", "fused" (the LUT kernel's gate/up,
+        down and combine in one launch per layer where it routes the token
+        itself) or "gather" (decode-then-dot with codebook gathers)."""
+        code = {"auto": 0, "mfma": 1, "fused": 2, "gather": 3}[path]
         self._check(lib().warp_hip_set_matvec_path(self.h, code))
 
     def set_router_fast(self, fast):
