@@ -1772,7 +1772,7 @@ const char *warp_hip_matvec_kernel(warp_hip_ctx *c, int layer, int experts)
 {
     if (!c || layer < 0 || layer >= c->cfg.n_layers) return "none";
     const layer_t *L = &c->L[layer];
-    if (use_gather(c, L, experts)) return "k_vq_gather";
+    if (use_gather(c, L, experts)) return experts == 1 ? "k_vq_rows" : "k_vq_gather";
     if (use_table(c, L)) return c->mv_path == WARP_HIP_PATH_LUT_FUSED && experts > 1 ? "k_moe_fused" : "k_vq_lut";
     return c->P6 ? "k_apply_p6" : "k_vq_mfma";
 }
@@ -1967,13 +1967,13 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
         int sp_gu = 0;
         if ((rc = timing_begin(c, 0))) return rc;
         KRN(c, wk_vq_gather(g->fmt, c->jobs, c->njobs, K, 0, 2, B->books, xe, 1, c->part, c->part_cap, I, He,
-                            GATHER_BLOCKS(c), NULL, 0, 0, 0.0f, 0.0f, NULL, 0, NULL, NULL, NULL, &sp_gu, c->st));
+                            GATHER_BLOCKS(c), NULL, 0, 0, 0.0f, 0.0f, &sp_gu, c->st));
         if ((rc = timing_end(c))) return rc;
         const size_t gu_floats = (size_t)2 * sp_gu * K * (((size_t)I + 63) / 64) * 64;
         if ((rc = timing_begin(c, 1))) return rc;
         KRN(c, wk_vq_gather(g->fmt, c->jobs, c->njobs, K, 2, 1, B->books, NULL, 0, c->part + gu_floats,
                             c->part_cap - gu_floats, He, I, GATHER_BLOCKS(c), c->part, sp_gu, g->act_situ,
-                            g->situ_beta, g->situ_linear_beta, NULL, 0, NULL, NULL, NULL, &sp_d, c->st));
+                            g->situ_beta, g->situ_linear_beta, &sp_d, c->st));
         d_off = gu_floats;
         if ((rc = timing_end(c))) return rc;
     } else if (use_lut) {
@@ -2054,21 +2054,18 @@ int warp_hip_expert_ffn(warp_hip_ctx *c, int layer, int expert, const float *x_d
     c->missing_pending = 1;
     if ((rc = x31_check(c, B, layer))) return rc;
     if (use_gather(c, B, 1)) {
-        /* two launches: gate/up from the expert's table entry, and down, whose
-         * last block per row block writes the rows (no job-list or combine
-         * launch); a missing record sets the flag and out to NaN */
-        int sp_gu = 0;
+        /* two launches of the row kernel, from the expert's table entry (no
+         * job-list launch): gate and up rows, then the down rows from
+         * act(gate, up) straight into out (no combine launch); a missing
+         * record sets the flag and out to NaN */
+        float *yk[3] = { c->yg, c->yu, out_dev };
         if ((rc = timing_begin(c, 0))) return rc;
-        KRN(c, wk_vq_gather(g->fmt, NULL, NULL, 1, 0, 2, B->books, x_dev, 1, c->part, c->part_cap, I, H,
-                            GATHER_BLOCKS(c), NULL, 0, 0, 0.0f, 0.0f, entry, I, NULL, NULL, c->missing, &sp_gu,
-                            c->st));
+        KRN(c, wk_vq_rows(g->fmt, NULL, NULL, 0, 2, B->books, x_dev, I, H, entry, I, 0, 0.0f, 0.0f, yk, c->missing,
+                          c->n_cu, c->st));
         if ((rc = timing_end(c))) return rc;
-        const size_t gu_floats = (size_t)2 * sp_gu * (((size_t)I + 63) / 64) * 64;
         if ((rc = timing_begin(c, 1))) return rc;
-        KRN(c, wk_vq_gather(g->fmt, NULL, NULL, 1, 2, 1, B->books, NULL, 0, c->part + gu_floats,
-                            c->part_cap - gu_floats, H, I, GATHER_BLOCKS(c), c->part, sp_gu, g->act_situ,
-                            g->situ_beta, g->situ_linear_beta, entry, I, out_dev, c->fz_sync, c->missing, NULL,
-                            c->st));
+        KRN(c, wk_vq_rows(g->fmt, NULL, NULL, 2, 1, B->books, NULL, H, I, entry, I, g->act_situ, g->situ_beta,
+                          g->situ_linear_beta, yk, c->missing, c->n_cu, c->st));
         if ((rc = timing_end(c))) return rc;
         return 0;
     }
@@ -2380,10 +2377,10 @@ int warp_hip_vq_matvec(warp_hip_ctx *c, int layer, int kind, const uint8_t *rec_
         KRN(c, wk_lut_p6(x_dev, 1, N, books_kind(c, B, kind), lut, ls, c->st));
         KRN(c, wk_apply_p6(c->jobs, c->njobs, 1, kind, lut, ls, y_dev, M, N, c->st));
     } else if (use_gather(c, B, 1) && N % 32 == 0) {
-        /* one launch: its last block per row block writes the rows */
-        KRN(c, wk_vq_gather(c->cfg.fmt, c->jobs, c->njobs, 1, kind, 1, B->books, x_dev, 1, c->part, c->part_cap, M,
-                            N, GATHER_BLOCKS(c), NULL, 0, 0, 0.0f, 0.0f, NULL, 0, y_dev, c->fz_sync, NULL, NULL,
-                            c->st));
+        /* one launch of the row kernel: the whole matvec */
+        float *yk[3] = { y_dev, y_dev, y_dev };
+        KRN(c, wk_vq_rows(c->cfg.fmt, c->jobs, c->njobs, kind, 1, B->books, x_dev, M, N, NULL, 0, 0, 0.0f, 0.0f, yk,
+                          NULL, c->n_cu, c->st));
     } else if (use_table(c, B)) {
         float *yk[3] = { y_dev, y_dev, y_dev };
         int sp = 0;

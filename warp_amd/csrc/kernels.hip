@@ -4239,16 +4239,12 @@ __device__ __forceinline__ float ga_row(const uint4 (&v)[FmtT<FMT>::S], const fl
     return __builtin_fmaf(w[7], x1.w, acc);
 }
 
-// The gather kernel's arguments: those of the table kernel it stands in for
-// (jobs, inputs, the partial-sum layout, the down launch's act inputs) and
-// two of its own. slot (or NULL): one expert's FFN, whose jobs come from its
-// expert-table entry (record, header offsets; inter gives the scale arrays'
-// places) instead of a job list -- no job-list launch. out (or NULL, one
-// job, one kind): the launch also finishes the matvec -- the last block of
-// each row block to arrive (ctr, one zeroed word per row block, left
-// zeroed) adds the row block's partial sums in split order and writes out =
-// sum x the row scale -- no reduction launch. missing: set when the slot has
-// no record (out then gets NaN).
+// The gather kernels' arguments: those of the table kernel they stand in
+// for (jobs, inputs, the partial-sum layout, the down launch's act inputs)
+// and, for the row kernel (k_vq_rows), slot (or NULL): one expert's FFN,
+// whose jobs come from its expert-table entry (record, header offsets;
+// inter gives the scale arrays' places) instead of a job list -- no
+// job-list launch; missing: set when the slot has no record.
 struct GatherArgs {
     const warp_job *jobs;
     const int *njobs;
@@ -4262,8 +4258,6 @@ struct GatherArgs {
     const float *act_part;
     int act_splits, act_situ;
     float act_beta, act_lbeta;
-    float *out;
-    unsigned *ctr;
     int *missing;
 };
 
@@ -4295,7 +4289,6 @@ __global__ __launch_bounds__(GA_NW * 64) void k_vq_gather(GatherArgs a) {
     extern __shared__ __attribute__((aligned(16))) float gx[];   // the split's inputs
     __shared__ float red[GA_NW][64];
     __shared__ uint64_t s_exp[32];
-    __shared__ unsigned s_last;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int kind = a.kind_lo + (int)blockIdx.y;
     const int nv = a.N >> 3, npg = nv >> 2, nrb = (a.M + 63) >> 6;
@@ -4304,12 +4297,8 @@ __global__ __launch_bounds__(GA_NW * 64) void k_vq_gather(GatherArgs a) {
     const uint8_t *jidx;
     const uint16_t *jscale;
     int jxi;
-    if (!ga_job(a, kind, j, jidx, jscale, jxi)) {          // uniform: the slot has no record
-        if (a.out && split == 0 && tid < 64 && rb * 64 + tid < a.M) a.out[rb * 64 + tid] = __builtin_nanf("");
-        if (blockIdx.x == 0 && blockIdx.y == 0 && tid == 0 && a.missing) *a.missing = 1;
-        return;
-    }
-    if (!a.slot && j >= a.njobs[kind]) return;             // uniform per block
+    ga_job(a, kind, j, jidx, jscale, jxi);                 // (a job list: always there)
+    if (j >= a.njobs[kind]) return;                        // uniform per block
     const int pg0 = split * npg / a.splits, pg1 = (split + 1) * npg / a.splits;
     const int nx = (pg1 - pg0) * 32;                       // inputs of this split
     const int ng = pg1 - pg0 > wave ? (pg1 - pg0 - wave + GA_NW - 1) / GA_NW : 0;   // this wave's groups
@@ -4382,46 +4371,12 @@ __global__ __launch_bounds__(GA_NW * 64) void k_vq_gather(GatherArgs a) {
     }
     if (lane < 16) *(float4 *)&red[wave][4 * lane] = make_float4(acc[0], acc[1], acc[2], acc[3]);
     __syncthreads();
-    const size_t kstride = (size_t)a.max_jobs * nrb * 64;  // one split of one kind
-    float *po = a.part + ((size_t)blockIdx.y * a.splits * kstride) + (size_t)fb * 64 + tid;
-    if (!a.out) {
-        if (tid < 64) {
-            float s = red[0][tid];
-#pragma unroll
-            for (int w = 1; w < GA_NW; w++) s += red[w][tid];
-            po[(size_t)split * kstride] = s;
-        }
-        return;
-    }
-    // Finishing the matvec: the row block's partial sums go out with
-    // agent-coherent stores, complete before the block's count rises; the
-    // block that raises it to the split count reads them all (agent-coherent
-    // loads) and writes the rows.
     if (tid < 64) {
         float s = red[0][tid];
 #pragma unroll
         for (int w = 1; w < GA_NW; w++) s += red[w][tid];
-        st_agent(po + (size_t)split * kstride, s);
-        wait_stores();
+        a.part[(((size_t)blockIdx.y * a.splits + split) * a.max_jobs * nrb + fb) * 64 + tid] = s;
     }
-    __syncthreads();
-    if (tid == 0) s_last = __hip_atomic_fetch_add(a.ctr + fb, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    if (s_last != (unsigned)a.splits - 1) return;          // uniform
-    const int row = rb * 64 + tid;
-    if (tid < 64 && row < a.M) {
-        float v = 0.0f;
-        for (int s0 = 0; s0 < a.splits; s0 += 8) {
-            float a8[8];
-#pragma unroll
-            for (int q = 0; q < 8; q++) a8[q] = ld_agent(po + (size_t)min(s0 + q, a.splits - 1) * kstride);
-#pragma unroll
-            for (int q = 0; q < 8; q++)
-                if (s0 + q < a.splits) v += a8[q];
-        }
-        a.out[row] = v * f16_keep(jscale[row]);
-    }
-    if (tid == 0) __hip_atomic_store(a.ctr + fb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Splits of the gather kernel: about target_blocks blocks, each wave at
@@ -4465,12 +4420,9 @@ static int launch_gather_x(const GatherArgs &a, int nkinds, void *stream) {
 extern "C" int wk_vq_gather(int fmt, const warp_job *jobs, const int *njobs, int max_jobs, int kind_lo, int nkinds,
                             const uint16_t *books, const float *x, int shared_x, float *part, size_t cap_floats,
                             int M, int N, int target_blocks, const float *act_part, int act_splits, int act_situ,
-                            float act_beta, float act_lbeta, const warp_slot *slot, int inter, float *out,
-                            unsigned *ctr, int *missing, int *splits_out, void *stream) {
-    if (kind_lo < 0 || kind_lo + nkinds > 3 || !books || !part) return -1;
-    if (slot ? (max_jobs != 1 || inter <= 0) : (!jobs || !njobs)) return -1;
+                            float act_beta, float act_lbeta, int *splits_out, void *stream) {
+    if (kind_lo < 0 || kind_lo + nkinds > 3 || !books || !part || !jobs || !njobs) return -1;
     if (act_part ? (shared_x || kind_lo != 2 || nkinds != 1 || act_splits <= 0) : !x) return -1;
-    if (out && (max_jobs != 1 || nkinds != 1 || !ctr)) return -1;
     int splits;
     if (wk_gather_plan(M, N, max_jobs, nkinds, target_blocks, cap_floats, &splits)) return -1;
     GatherArgs a = {};
@@ -4478,8 +4430,6 @@ extern "C" int wk_vq_gather(int fmt, const warp_job *jobs, const int *njobs, int
     a.njobs = njobs;
     a.max_jobs = max_jobs;
     a.kind_lo = kind_lo;
-    a.slot = slot;
-    a.inter = inter;
     a.books = books;
     a.x = x;
     a.part = part;
@@ -4492,14 +4442,204 @@ extern "C" int wk_vq_gather(int fmt, const warp_job *jobs, const int *njobs, int
     a.act_situ = act_situ;
     a.act_beta = act_beta;
     a.act_lbeta = act_lbeta;
-    a.out = out;
-    a.ctr = ctr;
-    a.missing = missing;
     if (splits_out) *splits_out = splits;
     switch (fmt) {
     case WARP_FMT_VQ3R: return launch_gather_x<WARP_FMT_VQ3R>(a, nkinds, stream);
     case WARP_FMT_VQ2R: return launch_gather_x<WARP_FMT_VQ2R>(a, nkinds, stream);
     case WARP_FMT_VQ12: return launch_gather_x<WARP_FMT_VQ12>(a, nkinds, stream);
+    }
+    return -1;
+}
+
+// ---- one expert's matvecs, whole rows per wave ------------------------------------
+//
+// One matrix, or one expert's FFN, for one token: no rows share a table
+// enough to pay for it, and a split over positions would need a reduction
+// across blocks. Each block stages its kind's fp16 codebook in LDS (128 KiB
+// for 2 x 4096 entries, one block per CU; 12 KiB for 3 x 256) and the input,
+// then takes row quads (4 consecutive rows: one code word of the record's
+// blocked layout per position) RQ at a time: wave w takes quad w % RQ and
+// position slice w / RQ of NS, lane l the slice's positions l, l + 64, ...,
+// gathering each row's S codebook vectors from LDS, adding them in fp32 and
+// dotting them with the position's 8 inputs. The lanes' sums, then the
+// slices' in order, give each row; times its scale it is written out. No
+// partial sums leave the block, so a launch is the whole matvec. A codebook
+// of at most RW_L1 bytes a kind (3 x 256 or 2 x 256 entries) is read from
+// global memory instead, where it stays in the L1 cache, so that the
+// gathers need not wait for a staging pass.
+constexpr int RW_L1 = 16384;
+
+struct RowsArgs {
+    GatherArgs g;              // jobs (or slot), books, x, M, N; act inputs below
+    float *y[3];               // per kind: the rows out (scaled); ACT reads y[0], y[1]
+    int nkinds;
+};
+
+template <int FMT, bool ACT, int NW>
+__global__ __launch_bounds__(NW * 64) void k_vq_rows(RowsArgs ra) {
+    typedef FmtT<FMT> F;
+    constexpr bool STAGE = F::S * F::E * 16 > RW_L1;      // the codebook in LDS
+    const GatherArgs &a = ra.g;
+    extern __shared__ __attribute__((aligned(16))) uint4 rw_lds[];
+    const uint4 *bk = (const uint4 *)(a.books + (size_t)(a.kind_lo + (int)blockIdx.y) * F::S * F::E * 8);
+    uint4 *cbl = rw_lds;                                   // [S][E] half8 (STAGE)
+    const uint4 *cb = STAGE ? (const uint4 *)cbl : bk;
+    float *xl = (float *)(rw_lds + (STAGE ? F::S * F::E : 0));   // [N]
+    __shared__ float red[NW][4];
+    __shared__ uint64_t s_exp[32];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kind = a.kind_lo + (int)blockIdx.y;
+    const int nv = a.N >> 3, nrq = (a.M + 3) >> 2;
+    const uint8_t *jidx;
+    const uint16_t *jscale;
+    int jxi;
+    // this block's quads [q0, q1)
+    const int G = gridDim.x, per = (nrq + G - 1) / G;
+    const int q0 = min((int)blockIdx.x * per, nrq), q1 = min(q0 + per, nrq);
+    if (!ga_job(a, kind, 0, jidx, jscale, jxi)) {          // uniform: the slot has no record
+        for (int r = q0 * 4 + tid; r < min(q1 * 4, a.M); r += NW * 64) ra.y[kind][r] = __builtin_nanf("");
+        if (blockIdx.x == 0 && blockIdx.y == 0 && tid == 0 && a.missing) *a.missing = 1;
+        return;
+    }
+    if (!a.slot && a.njobs[kind] < 1) return;              // uniform
+    if (q0 >= q1) return;                                  // uniform
+    const int RQ = min(per, NW), NS = NW / RQ;
+    const int qw = wave % RQ, sw = wave / RQ;              // this wave's quad in a round, its slice
+    const int p0 = sw * nv / NS, p1 = (sw + 1) * nv / NS;  // the slice's positions
+    const bool live = sw < NS;
+    constexpr int PPL = 4;                                 // positions a lane holds at once
+    // the first round's code words (from HBM) before anything else
+    auto word_at = [&](int q, int p) -> const uint8_t * {
+        return jidx + ((size_t)(q >> 4) * nv + p) * 64 * F::SB + (size_t)(q & 15) * 4 * F::SB;
+    };
+    Word<F::SB> wd[PPL];
+    {
+        const int q = q0 + qw;
+#pragma unroll
+        for (int k = 0; k < PPL; k++) {
+            const int p = p0 + lane + 64 * k;
+            if (live && q < q1 && p < p1) wd[k].load_keep(word_at(q, p));
+        }
+    }
+    // the codebook and the input, into LDS
+    if constexpr (STAGE)
+        for (int i = tid; i < F::S * F::E; i += NW * 64) cbl[i] = bk[i];
+    if constexpr (ACT) {
+        if (tid < 32) s_exp[tid] = g_exp2_tab[tid];
+        __syncthreads();
+        for (int i = tid; i < a.N; i += NW * 64)
+            xl[i] = act_pair(ra.y[0][i], ra.y[1][i], a.act_situ, a.act_beta, a.act_lbeta, s_exp);
+    } else {
+        const float *xs = a.x + (a.shared_x ? (size_t)0 : (size_t)jxi * a.N);
+        for (int i = tid * 4; i < a.N; i += NW * 64 * 4) *(float4 *)(xl + i) = *(const float4 *)(xs + i);
+    }
+    __syncthreads();
+
+    for (int qb = q0; qb < q1; qb += RQ) {
+        const int q = qb + qw;
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (live && q < q1) {                              // uniform per wave
+            for (int pb = p0; pb < p1; pb += 64 * PPL) {
+#pragma unroll
+                for (int k = 0; k < PPL; k++) {
+                    const int p = pb + lane + 64 * k;
+                    if (p < p1) {
+                        const Word<F::SB> w = wd[k];
+                        if (p + 64 * PPL < p1) wd[k].load_keep(word_at(q, p + 64 * PPL));
+                        const float4 x0 = *(const float4 *)(xl + 8 * p);
+                        const float4 x1 = *(const float4 *)(xl + 8 * p + 4);
+#pragma unroll
+                        for (int t = 0; t < 4; t++) {
+                            const unsigned sl = w.slot(t);
+                            uint4 v[F::S];
+#pragma unroll
+                            for (int s = 0; s < F::S; s++) v[s] = cb[s * F::E + lut_code<FMT>(sl, s)];
+                            acc[t] = ga_row<FMT>(v, x0, x1, acc[t]);
+                        }
+                    }
+                }
+            }
+            // the next round's first code words
+            const int qn = q + RQ;
+#pragma unroll
+            for (int k = 0; k < PPL; k++) {
+                const int p = p0 + lane + 64 * k;
+                if (qn < q1 && p < p1) wd[k].load_keep(word_at(qn, p));
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < 4; t++) acc[t] = wave_sum(acc[t]);
+        if (lane == 0) *(float4 *)red[wave] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+        __syncthreads();
+        if (tid < 4 * RQ) {
+            const int qq = qb + tid / 4, r = 4 * qq + (tid & 3);
+            if (qq < q1 && r < a.M) {
+                float v = red[tid / 4][tid & 3];
+                for (int s = 1; s < NS; s++) v += red[s * RQ + tid / 4][tid & 3];
+                ra.y[kind][r] = v * f16_keep(jscale[r]);
+            }
+        }
+        __syncthreads();
+    }
+}
+
+template <int FMT, bool ACT>
+static int launch_rows(const RowsArgs &ra, int target_blocks, void *stream) {
+    typedef FmtT<FMT> F;
+    // a staged codebook: one block of 16 waves per CU; else blocks of 4
+    // waves, four per CU
+    constexpr bool STAGE = F::S * F::E * 16 > RW_L1;
+    constexpr int NW = STAGE ? 16 : 4;
+    if (!STAGE) target_blocks *= 4;
+    const size_t lds = (F::S * F::E * 16 > RW_L1 ? (size_t)F::S * F::E * 16 : 0) + (size_t)ra.g.N * sizeof(float);
+    if (lds > 160 * 1024 - 1024) return -2;
+    static std::atomic<uint64_t> attr{0};
+    if (int r_ = lds_limit((const void *)k_vq_rows<FMT, ACT, NW>, (int)lds, attr, stream)) return r_;
+    const int nrq = (ra.g.M + 3) / 4;
+    int G = target_blocks / ra.nkinds;
+    if (G > nrq) G = nrq;
+    if (G < 1) G = 1;
+    hipLaunchKernelGGL((k_vq_rows<FMT, ACT, NW>), dim3(G, ra.nkinds), dim3(NW * 64), lds, (hipStream_t)stream, ra);
+    CHECK_LAUNCH();
+    return 0;
+}
+
+extern "C" int wk_vq_rows(int fmt, const warp_job *jobs, const int *njobs, int kind_lo, int nkinds,
+                          const uint16_t *books, const float *x, int M, int N, const warp_slot *slot, int inter,
+                          int act_situ, float act_beta, float act_lbeta, float *const *y, int *missing,
+                          int target_blocks, void *stream) {
+    if (kind_lo < 0 || kind_lo + nkinds > 3 || !books || !y || M <= 0 || N <= 0 || (N % 32)) return -1;
+    if (slot ? inter <= 0 : (!jobs || !njobs)) return -1;
+    const bool act = x == nullptr;                         // down: inputs act(y[0], y[1])
+    if (act && (kind_lo != 2 || nkinds != 1 || !y[0] || !y[1])) return -1;
+    for (int k = kind_lo; k < kind_lo + nkinds; k++)
+        if (!y[k]) return -1;
+    RowsArgs ra = {};
+    GatherArgs &a = ra.g;
+    a.jobs = jobs;
+    a.njobs = njobs;
+    a.max_jobs = 1;
+    a.kind_lo = kind_lo;
+    a.slot = slot;
+    a.inter = inter;
+    a.books = books;
+    a.x = x;
+    a.M = M;
+    a.N = N;
+    a.shared_x = 1;
+    a.act_situ = act_situ;
+    a.act_beta = act_beta;
+    a.act_lbeta = act_lbeta;
+    a.missing = missing;
+    for (int k = 0; k < 3; k++) ra.y[k] = y[k];
+    ra.nkinds = nkinds;
+    switch (fmt) {
+    case WARP_FMT_VQ3R: return act ? launch_rows<WARP_FMT_VQ3R, true>(ra, target_blocks, stream)
+                                   : launch_rows<WARP_FMT_VQ3R, false>(ra, target_blocks, stream);
+    case WARP_FMT_VQ2R: return act ? launch_rows<WARP_FMT_VQ2R, true>(ra, target_blocks, stream)
+                                   : launch_rows<WARP_FMT_VQ2R, false>(ra, target_blocks, stream);
+    case WARP_FMT_VQ12: return act ? launch_rows<WARP_FMT_VQ12, true>(ra, target_blocks, stream)
+                                   : launch_rows<WARP_FMT_VQ12, false>(ra, target_blocks, stream);
     }
     return -1;
 }
