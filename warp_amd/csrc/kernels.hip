@@ -808,9 +808,12 @@ __global__ __launch_bounds__(256) void k_router_cert_b(const float *__restrict__
 
 // Launches k_router_cert_b<R4> when H / (4 R4) threads of the block make
 // whole waves (the callers try the shortest runs first).
-// LDS floats of cert_last: the four arrays, the recompute's row and segments.
-static size_t cert_last_floats(int E, int H) {
-    return (size_t)((4 * ((E + 1) & ~1) + 3) & ~3) + (size_t)H + 128 * 4 + 64;
+// LDS floats of cert_last: the four arrays, the expert table (when it
+// writes the job lists), the recompute's row and segments.
+static_assert(sizeof(warp_slot) == 24, "warp_slot: six floats of LDS");
+static size_t cert_last_floats(int E, int H, bool table) {
+    return (size_t)((4 * ((E + 1) & ~1) + 3) & ~3) + (table ? (size_t)6 * ((E + 1) & ~1) : 0) + (size_t)H + 128 * 4 +
+           64;
 }
 
 template <int R4>
@@ -819,7 +822,7 @@ static bool router_cert_b(const float *W, const float *x, int E, int H, const fl
     const int n4 = H >> 2;
     if ((H & 3) || n4 % R4 || n4 / R4 > 256 || (n4 / R4) % 64) return false;
     const size_t lds = std::max((size_t)2 * 256 * (R4 + ((R4 & 1) ? 2 : 1)) * sizeof(float4),
-                                t.done ? cert_last_floats(E, H) * sizeof(float) : (size_t)0);
+                                t.done ? cert_last_floats(E, H, t.pk.table) * sizeof(float) : (size_t)0);
     if (lds > 160 * 1024) return false;
     static std::atomic<uint64_t> attr{0};
     if (lds_limit((const void *)k_router_cert_b<R4>, (int)lds, attr, s)) return false;
@@ -843,7 +846,7 @@ extern "C" int wk_router_cert(const float *W, const float *x, int E, int H, cons
     if (!(router_cert_b<3>(W, x, E, H, bias, out, t, st) || router_cert_b<4>(W, x, E, H, bias, out, t, st) ||
           router_cert_b<5>(W, x, E, H, bias, out, t, st) || router_cert_b<6>(W, x, E, H, bias, out, t, st) ||
           router_cert_b<7>(W, x, E, H, bias, out, t, st) || router_cert_b<8>(W, x, E, H, bias, out, t, st))) {
-        const size_t lds = done ? cert_last_floats(E, H) * sizeof(float) : 0;
+        const size_t lds = done ? cert_last_floats(E, H, t.pk.table) * sizeof(float) : 0;
         if (lds > 160 * 1024) return -1;
         static std::atomic<uint64_t> attr{0};
         if (int r_ = lds_limit((const void *)k_router_cert, (int)lds, attr, stream)) return r_;
@@ -2301,8 +2304,21 @@ __device__ void cert_last(const float *__restrict__ W, const float *__restrict__
         if (tid == 0) __hip_atomic_store(t.done + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
-    const int E2 = (E + 1) & ~1, s0 = (4 * E2 + 3) & ~3, nw = (E + 63) >> 6;
+    const int E2 = (E + 1) & ~1, nw = (E + 63) >> 6;
     float *score = lds, *biased = lds + E2, *lo = lds + 2 * E2, *hi = lds + 3 * E2;
+    // the expert table, for the job lists, staged while the rows come in;
+    // the recompute's buffers after it
+    warp_slot *slots = (warp_slot *)(lds + ((4 * E2 + 3) & ~3));
+    const int s0 = ((4 * E2 + 3) & ~3) + (t.pk.table ? 6 * E2 : 0);
+    if (t.pk.table)
+        for (int e = tid; e < E; e += NT) {
+            const uint2 *src = (const uint2 *)(t.pk.table + e);
+            uint2 *dst = (uint2 *)(slots + e);
+            const uint2 a0 = src[0], a1 = src[1], a2 = src[2];
+            dst[0] = a0;
+            dst[1] = a1;
+            dst[2] = a2;
+        }
     unsigned pend = 0;                                    // this thread's rows not yet loaded
     for (int i = 0; i < CERT_EMAX / NT; i++)
         if (tid + i * NT < E) pend |= 1u << i;
@@ -2377,7 +2393,7 @@ __device__ void cert_last(const float *__restrict__ W, const float *__restrict__
         pk.idx[tid] = sel[tid];
         pk.w[tid] = wsel[tid];
     }
-    if (pk.table) route_jobs<NT>(sel, t.K, pk.table, pk.jobs, pk.njobs, t.flag, pk.inter);
+    if (pk.table) route_jobs<NT>(sel, t.K, slots, pk.jobs, pk.njobs, t.flag, pk.inter);
 }
 
 // Certified routing of one token by a CERT_NT-thread block: the four arrays of
