@@ -4509,9 +4509,13 @@ __global__ __launch_bounds__(NW * 64) void k_vq_rows(RowsArgs ra) {
     const uint8_t *jidx;
     const uint16_t *jscale;
     int jxi;
-    // this block's quads [q0, q1)
-    const int G = gridDim.x, per = (nrq + G - 1) / G;
-    const int q0 = min((int)blockIdx.x * per, nrq), q1 = min(q0 + per, nrq);
+    // this block's quads [q0, q1): the blocks go to the 8 XCDs in turn
+    // (block b to XCD b % 8), so each XCD takes a contiguous eighth of the
+    // quads, shared by its blocks: the record lines a row block's quads
+    // share are then fetched into one XCD's L2, not into each
+    const int G = gridDim.x, xcd = (int)blockIdx.x % 8, nb = (G - xcd + 7) / 8, slot = (int)blockIdx.x / 8;
+    const int qx0 = xcd * nrq / 8, nqx = (xcd + 1) * nrq / 8 - qx0;
+    const int q0 = qx0 + slot * nqx / nb, q1 = qx0 + (slot + 1) * nqx / nb, per = q1 - q0;
     if (!ga_job(a, kind, 0, jidx, jscale, jxi)) {          // uniform: the slot has no record
         for (int r = q0 * 4 + tid; r < min(q1 * 4, a.M); r += NW * 64) ra.y[kind][r] = __builtin_nanf("");
         if (blockIdx.x == 0 && blockIdx.y == 0 && tid == 0 && a.missing) *a.missing = 1;
