@@ -1751,10 +1751,10 @@ static int use_table(const warp_hip_ctx *c, const layer_t *L)
     return c->lut_ok && L->books && (c->mv_path != WARP_HIP_PATH_MFMA || L->books_x31);
 }
 
-/* The gather kernel (decode-then-dot, codebook vectors gathered from L2)
- * instead of the table kernel, for `experts` experts of a decode: where few
- * rows share each position's tables, building them costs more than
- * gathering the rows' codebook vectors. */
+/* The row kernel (decode-then-dot, whole rows per wave, the codebook in
+ * LDS) instead of the table kernel, for `experts` experts of a decode:
+ * where few rows share each position's tables, building them costs more
+ * than gathering the rows' codebook vectors. */
 static int use_gather(const warp_hip_ctx *c, const layer_t *L, int experts)
 {
     if (!use_table(c, L) || L->books_x31 || c->He % 32 || c->cfg.inter % 32) return 0;
@@ -1765,14 +1765,11 @@ static int use_gather(const warp_hip_ctx *c, const layer_t *L, int experts)
     return c->mv_path == WARP_HIP_PATH_AUTO && experts == 1;
 }
 
-/* blocks a gather launch aims at */
-#define GATHER_BLOCKS(c) (4 * (c)->n_cu)
-
 const char *warp_hip_matvec_kernel(warp_hip_ctx *c, int layer, int experts)
 {
     if (!c || layer < 0 || layer >= c->cfg.n_layers) return "none";
     const layer_t *L = &c->L[layer];
-    if (use_gather(c, L, experts)) return experts == 1 ? "k_vq_rows" : "k_vq_gather";
+    if (use_gather(c, L, experts)) return "k_vq_rows";
     if (use_table(c, L)) return c->mv_path == WARP_HIP_PATH_LUT_FUSED && experts > 1 ? "k_moe_fused" : "k_vq_lut";
     return c->P6 ? "k_apply_p6" : "k_vq_mfma";
 }
@@ -1964,18 +1961,22 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
     int sp_d = 0;
     size_t d_off = 0;
     if (gat && !B->books_x31) {
-        int sp_gu = 0;
+        /* the row kernel: the picks' gate and up rows (scaled), then their down
+         * rows from act(gate, up), unscaled, as one split of partial sums for
+         * the combine */
+        float *ykr[3] = { c->yg, c->yu, NULL };
+        if ((size_t)K * (((size_t)He + 63) / 64) * 64 > c->part_cap)
+            return set_err(c, WARP_HIP_E_ARG, layer, -1, "partial-sum buffer");
         if ((rc = timing_begin(c, 0))) return rc;
-        KRN(c, wk_vq_gather(g->fmt, c->jobs, c->njobs, K, 0, 2, B->books, xe, 1, c->part, c->part_cap, I, He,
-                            GATHER_BLOCKS(c), NULL, 0, 0, 0.0f, 0.0f, &sp_gu, c->st));
+        KRN(c, wk_vq_rows(g->fmt, c->jobs, c->njobs, K, 0, 2, B->books, xe, I, He, NULL, 0, 0, 0.0f, 0.0f, ykr, NULL,
+                          NULL, c->n_cu, c->st));
         if ((rc = timing_end(c))) return rc;
-        const size_t gu_floats = (size_t)2 * sp_gu * K * (((size_t)I + 63) / 64) * 64;
         if ((rc = timing_begin(c, 1))) return rc;
-        KRN(c, wk_vq_gather(g->fmt, c->jobs, c->njobs, K, 2, 1, B->books, NULL, 0, c->part + gu_floats,
-                            c->part_cap - gu_floats, He, I, GATHER_BLOCKS(c), c->part, sp_gu, g->act_situ,
-                            g->situ_beta, g->situ_linear_beta, &sp_d, c->st));
-        d_off = gu_floats;
+        KRN(c, wk_vq_rows(g->fmt, c->jobs, c->njobs, K, 2, 1, B->books, NULL, He, I, NULL, 0, g->act_situ,
+                          g->situ_beta, g->situ_linear_beta, ykr, c->part, NULL, c->n_cu, c->st));
         if ((rc = timing_end(c))) return rc;
+        sp_d = 1;
+        d_off = 0;
     } else if (use_lut) {
         int sp_gu = 0;
         if ((rc = timing_begin(c, 0))) return rc;
@@ -2060,12 +2061,12 @@ int warp_hip_expert_ffn(warp_hip_ctx *c, int layer, int expert, const float *x_d
          * record sets the flag and out to NaN */
         float *yk[3] = { c->yg, c->yu, out_dev };
         if ((rc = timing_begin(c, 0))) return rc;
-        KRN(c, wk_vq_rows(g->fmt, NULL, NULL, 0, 2, B->books, x_dev, I, H, entry, I, 0, 0.0f, 0.0f, yk, c->missing,
-                          c->n_cu, c->st));
+        KRN(c, wk_vq_rows(g->fmt, NULL, NULL, 1, 0, 2, B->books, x_dev, I, H, entry, I, 0, 0.0f, 0.0f, yk, NULL,
+                          c->missing, c->n_cu, c->st));
         if ((rc = timing_end(c))) return rc;
         if ((rc = timing_begin(c, 1))) return rc;
-        KRN(c, wk_vq_rows(g->fmt, NULL, NULL, 2, 1, B->books, NULL, H, I, entry, I, g->act_situ, g->situ_beta,
-                          g->situ_linear_beta, yk, c->missing, c->n_cu, c->st));
+        KRN(c, wk_vq_rows(g->fmt, NULL, NULL, 1, 2, 1, B->books, NULL, H, I, entry, I, g->act_situ, g->situ_beta,
+                          g->situ_linear_beta, yk, NULL, c->missing, c->n_cu, c->st));
         if ((rc = timing_end(c))) return rc;
         return 0;
     }
@@ -2379,8 +2380,8 @@ int warp_hip_vq_matvec(warp_hip_ctx *c, int layer, int kind, const uint8_t *rec_
     } else if (use_gather(c, B, 1) && N % 32 == 0) {
         /* one launch of the row kernel: the whole matvec */
         float *yk[3] = { y_dev, y_dev, y_dev };
-        KRN(c, wk_vq_rows(c->cfg.fmt, c->jobs, c->njobs, kind, 1, B->books, x_dev, M, N, NULL, 0, 0, 0.0f, 0.0f, yk,
-                          NULL, c->n_cu, c->st));
+        KRN(c, wk_vq_rows(c->cfg.fmt, c->jobs, c->njobs, 1, kind, 1, B->books, x_dev, M, N, NULL, 0, 0, 0.0f, 0.0f,
+                          yk, NULL, NULL, c->n_cu, c->st));
     } else if (use_table(c, B)) {
         float *yk[3] = { y_dev, y_dev, y_dev };
         int sp = 0;

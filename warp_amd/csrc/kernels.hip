@@ -4211,25 +4211,11 @@ extern "C" int wk_vq_lut(int fmt, const warp_job *jobs, const int *njobs, int ma
     return -1;
 }
 
-// ---- small shapes: decode-then-dot with codebook gathers ----------------------------
+// ---- few experts: decode-then-dot, whole rows per wave --------------------------------
 //
-// One token's expert matvecs where few rows share a position (one expert's
-// FFN, a Kimi-Linear-shape decode): the table kernel would build S x E
-// entries per position, and stage a 2 x 4096-entry codebook per block, for a
-// few thousand rows. Here each lane decodes its weights instead: the code
-// word of 4 rows at one position, each row's S codebook vectors gathered
-// from the fp16 codebook in global memory (L2-resident: 128 KiB per kind for
-// 2 x 4096 entries), added in fp32 and dotted with the position's 8 inputs.
-// A block (GA_NW waves) takes one 64-row block of one job and a range of
-// position groups (4 positions, the record's 256-slot [position][row] unit);
-// wave w takes groups pg0 + w, pg0 + w + GA_NW, ...; lane l the group's
-// position l / 16 and rows 4 (l % 16) .. + 3. The unscaled partial sums of a
-// split go where the table kernel puts them ([kind][split][job][row]), so
-// the down launch's act prologue and the combine read either kernel's.
-constexpr int GA_NW = 4;            // waves per block
-constexpr int GA_W = 8;             // code words a lane loads ahead
-constexpr int GA_XMAX = 16384;      // inputs a block stages in LDS (64 KiB)
-
+// One row's share at one position: its S codebook vectors (fp16, as the
+// codebook holds them) added in fp32, dotted with the position's 8 inputs,
+// added to acc.
 template <int FMT>
 __device__ __forceinline__ float ga_row(const uint4 (&v)[FmtT<FMT>::S], const float4 &x0, const float4 &x1,
                                         float acc) {
@@ -4255,12 +4241,11 @@ __device__ __forceinline__ float ga_row(const uint4 (&v)[FmtT<FMT>::S], const fl
     return __builtin_fmaf(w[7], x1.w, acc);
 }
 
-// The gather kernels' arguments: those of the table kernel they stand in
-// for (jobs, inputs, the partial-sum layout, the down launch's act inputs)
-// and, for the row kernel (k_vq_rows), slot (or NULL): one expert's FFN,
-// whose jobs come from its expert-table entry (record, header offsets;
-// inter gives the scale arrays' places) instead of a job list -- no
-// job-list launch; missing: set when the slot has no record.
+// The row kernel's jobs and inputs: jobs/njobs (max_jobs per kind) or slot
+// (or NULL): one expert's FFN, whose jobs come from its expert-table entry
+// (record, header offsets; inter gives the scale arrays' places) instead of
+// a job list -- no job-list launch; missing: set when the slot has no
+// record.
 struct GatherArgs {
     const warp_job *jobs;
     const int *njobs;
@@ -4269,10 +4254,8 @@ struct GatherArgs {
     int inter;
     const uint16_t *books;     // [3][S][E][8] fp16, subnormals flushed
     const float *x;
-    float *part;               // [nkinds][splits][max_jobs][nrb * 64]
-    int M, N, splits, shared_x;
-    const float *act_part;
-    int act_splits, act_situ;
+    int M, N, shared_x;
+    int act_situ;
     float act_beta, act_lbeta;
     int *missing;
 };
@@ -4296,182 +4279,10 @@ __device__ __forceinline__ bool ga_job(const GatherArgs &a, int kind, int j, con
     return true;
 }
 
-// SHX: every job reads x (gate and up); ACT: job j's input is act(gate, up)
-// from the gate/up partial sums (a.act_part, a.act_splits), as the table
-// kernel's down launch makes it; neither: job j reads x + xi[0] N.
-template <int FMT, bool SHX, bool ACT>
-__global__ __launch_bounds__(GA_NW * 64) void k_vq_gather(GatherArgs a) {
-    typedef FmtT<FMT> F;
-    extern __shared__ __attribute__((aligned(16))) float gx[];   // the split's inputs
-    __shared__ float red[GA_NW][64];
-    __shared__ uint64_t s_exp[32];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int kind = a.kind_lo + (int)blockIdx.y;
-    const int nv = a.N >> 3, npg = nv >> 2, nrb = (a.M + 63) >> 6;
-    const int fb = (int)blockIdx.x / a.splits, split = (int)blockIdx.x % a.splits;
-    const int j = fb / nrb, rb = fb - j * nrb;
-    const uint8_t *jidx;
-    const uint16_t *jscale;
-    int jxi;
-    ga_job(a, kind, j, jidx, jscale, jxi);                 // (a job list: always there)
-    if (j >= a.njobs[kind]) return;                        // uniform per block
-    const int pg0 = split * npg / a.splits, pg1 = (split + 1) * npg / a.splits;
-    const int nx = (pg1 - pg0) * 32;                       // inputs of this split
-    const int ng = pg1 - pg0 > wave ? (pg1 - pg0 - wave + GA_NW - 1) / GA_NW : 0;   // this wave's groups
-
-    // the first code words (from HBM) before anything else
-    const uint8_t *cp = jidx + (size_t)rb * nv * 64 * F::SB + (size_t)lane * 4 * F::SB +
-                        (size_t)(pg0 + wave) * 256 * F::SB;
-    constexpr size_t GSTEP = (size_t)GA_NW * 256 * F::SB;     // a wave's next group
-    Word<F::SB> wd[GA_W];
-#pragma unroll
-    for (int k = 0; k < GA_W; k++)
-        if (k < ng) wd[k].load(cp + k * GSTEP);
-
-    // the inputs of the split, into LDS
-    const int c0 = pg0 * 32;
-    if constexpr (ACT) {
-        if (tid < 32) s_exp[tid] = g_exp2_tab[tid];
-        const size_t arows = (size_t)((a.N + 63) >> 6) * 64, astride = (size_t)a.max_jobs * arows;
-        const uint8_t *i0, *i1;
-        const uint16_t *sc0, *sc1;
-        int x0, x1;
-        ga_job(a, 0, j, i0, sc0, x0);
-        ga_job(a, 1, j, i1, sc1, x1);
-        gu32 *sg = (gu32 *)sc0;
-        gu32 *su = (gu32 *)sc1;
-        const float *pg = a.act_part + (size_t)j * arows + c0;
-        const float *pu = pg + (size_t)a.act_splits * astride;
-        __syncthreads();                                   // s_exp
-        for (int i = tid; i < nx; i += GA_NW * 64) {
-            const int sh = 16 * ((c0 + i) & 1);
-            const float g = lut_rowsum8(pg + i, a.act_splits, astride) * f16_keep((uint16_t)(sg[(c0 + i) >> 1] >> sh));
-            const float u = lut_rowsum8(pu + i, a.act_splits, astride) * f16_keep((uint16_t)(su[(c0 + i) >> 1] >> sh));
-            gx[i] = act_pair(g, u, a.act_situ, a.act_beta, a.act_lbeta, s_exp);
-        }
-    } else {
-        const float *xs = a.x + (SHX ? (size_t)0 : (size_t)jxi * a.N) + c0;
-        for (int i = tid * 4; i < nx; i += GA_NW * 64 * 4) *(float4 *)(gx + i) = *(const float4 *)(xs + i);
-    }
-    __syncthreads();
-
-    const uint4 *bk = (const uint4 *)(a.books + (size_t)kind * F::S * F::E * 8);
-    const float *xl = gx + (size_t)wave * 32 + (lane >> 4) * 8;
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int k0 = 0; k0 < ng; k0 += GA_W) {
-#pragma unroll
-        for (int k = 0; k < GA_W; k++) {
-            const int g = k0 + k;
-            if (g < ng) {                                  // uniform per wave
-                const Word<F::SB> w = wd[k];
-                if (g + GA_W < ng) wd[k].load(cp + (size_t)(g + GA_W) * GSTEP);
-                uint4 v[4][F::S];
-#pragma unroll
-                for (int t = 0; t < 4; t++) {
-                    const unsigned sl = w.slot(t);
-#pragma unroll
-                    for (int s = 0; s < F::S; s++) v[t][s] = bk[s * F::E + lut_code<FMT>(sl, s)];
-                }
-                const float4 x0 = *(const float4 *)(xl + (size_t)g * GA_NW * 32);
-                const float4 x1 = *(const float4 *)(xl + (size_t)g * GA_NW * 32 + 4);
-#pragma unroll
-                for (int t = 0; t < 4; t++) acc[t] = ga_row<FMT>(v[t], x0, x1, acc[t]);
-            }
-        }
-    }
-    // the four positions of a lane's rows, then the waves, in order
-#pragma unroll
-    for (int t = 0; t < 4; t++) {
-        acc[t] += __shfl_xor(acc[t], 16);
-        acc[t] += __shfl_xor(acc[t], 32);
-    }
-    if (lane < 16) *(float4 *)&red[wave][4 * lane] = make_float4(acc[0], acc[1], acc[2], acc[3]);
-    __syncthreads();
-    if (tid < 64) {
-        float s = red[0][tid];
-#pragma unroll
-        for (int w = 1; w < GA_NW; w++) s += red[w][tid];
-        a.part[(((size_t)blockIdx.y * a.splits + split) * a.max_jobs * nrb + fb) * 64 + tid] = s;
-    }
-}
-
-// Splits of the gather kernel: about target_blocks blocks, each wave at
-// least one position group where the shape allows, at most GA_XMAX inputs a
-// block, and the partial sums within cap_floats.
-extern "C" int wk_gather_plan(int M, int N, int max_jobs, int nkinds, int target_blocks, size_t cap_floats,
-                              int *splits_out) {
-    if (M <= 0 || N <= 0 || (N % 32) || max_jobs <= 0 || nkinds < 1 || nkinds > 3) return -1;
-    const long nrb = (M + 63) / 64, npg = N / 32, units = (long)nkinds * max_jobs * nrb;
-    long splits = target_blocks > units ? target_blocks / units : 1;
-    if (splits > npg / GA_NW) splits = npg / GA_NW;
-    if (splits > 32) splits = 32;
-    if (splits < 1) splits = 1;
-    const long smin = (npg * 32 + GA_XMAX - 1) / GA_XMAX;
-    if (splits < smin) splits = smin;
-    if ((size_t)nkinds * splits * max_jobs * nrb * 64 > cap_floats) return -1;
-    if (units * splits > 0x7fffffffL) return -1;
-    *splits_out = (int)splits;
-    return 0;
-}
-
-template <int FMT, bool SHX, bool ACT>
-static int launch_gather(const GatherArgs &a, int nkinds, void *stream) {
-    const int npg = a.N / 32, nrb = (a.M + 63) / 64;
-    const size_t lds = (size_t)((npg + a.splits - 1) / a.splits) * 32 * sizeof(float);
-    static std::atomic<uint64_t> attr{0};
-    if (int r_ = lds_limit((const void *)k_vq_gather<FMT, SHX, ACT>, (int)lds, attr, stream)) return r_;
-    hipLaunchKernelGGL((k_vq_gather<FMT, SHX, ACT>), dim3(a.max_jobs * nrb * a.splits, nkinds), dim3(GA_NW * 64),
-                       lds, (hipStream_t)stream, a);
-    CHECK_LAUNCH();
-    return 0;
-}
-
-template <int FMT>
-static int launch_gather_x(const GatherArgs &a, int nkinds, void *stream) {
-    if (a.act_part) return launch_gather<FMT, false, true>(a, nkinds, stream);
-    if (a.shared_x) return launch_gather<FMT, true, false>(a, nkinds, stream);
-    return launch_gather<FMT, false, false>(a, nkinds, stream);
-}
-
-extern "C" int wk_vq_gather(int fmt, const warp_job *jobs, const int *njobs, int max_jobs, int kind_lo, int nkinds,
-                            const uint16_t *books, const float *x, int shared_x, float *part, size_t cap_floats,
-                            int M, int N, int target_blocks, const float *act_part, int act_splits, int act_situ,
-                            float act_beta, float act_lbeta, int *splits_out, void *stream) {
-    if (kind_lo < 0 || kind_lo + nkinds > 3 || !books || !part || !jobs || !njobs) return -1;
-    if (act_part ? (shared_x || kind_lo != 2 || nkinds != 1 || act_splits <= 0) : !x) return -1;
-    int splits;
-    if (wk_gather_plan(M, N, max_jobs, nkinds, target_blocks, cap_floats, &splits)) return -1;
-    GatherArgs a = {};
-    a.jobs = jobs;
-    a.njobs = njobs;
-    a.max_jobs = max_jobs;
-    a.kind_lo = kind_lo;
-    a.books = books;
-    a.x = x;
-    a.part = part;
-    a.M = M;
-    a.N = N;
-    a.splits = splits;
-    a.shared_x = shared_x;
-    a.act_part = act_part;
-    a.act_splits = act_splits;
-    a.act_situ = act_situ;
-    a.act_beta = act_beta;
-    a.act_lbeta = act_lbeta;
-    if (splits_out) *splits_out = splits;
-    switch (fmt) {
-    case WARP_FMT_VQ3R: return launch_gather_x<WARP_FMT_VQ3R>(a, nkinds, stream);
-    case WARP_FMT_VQ2R: return launch_gather_x<WARP_FMT_VQ2R>(a, nkinds, stream);
-    case WARP_FMT_VQ12: return launch_gather_x<WARP_FMT_VQ12>(a, nkinds, stream);
-    }
-    return -1;
-}
-
-// ---- one expert's matvecs, whole rows per wave ------------------------------------
-//
-// One matrix, or one expert's FFN, for one token: no rows share a table
-// enough to pay for it, and a split over positions would need a reduction
-// across blocks. Each block stages its kind's fp16 codebook in LDS (128 KiB
+// One matrix, one expert's FFN, or the few experts of a decode, for one
+// token: too few rows share a table to pay for it, and a split over
+// positions would need a reduction across blocks. Each block (one job's
+// quads; blocks of several jobs in turn) stages its kind's fp16 codebook in LDS (128 KiB
 // for 2 x 4096 entries, one block per CU; 12 KiB for 3 x 256) and the input,
 // then takes row quads (4 consecutive rows: one code word of the record's
 // blocked layout per position) RQ at a time: wave w takes quad w % RQ and
@@ -4486,9 +4297,12 @@ extern "C" int wk_vq_gather(int fmt, const warp_job *jobs, const int *njobs, int
 constexpr int RW_L1 = 16384;
 
 struct RowsArgs {
-    GatherArgs g;              // jobs (or slot), books, x, M, N; act inputs below
-    float *y[3];               // per kind: the rows out (scaled); ACT reads y[0], y[1]
-    int nkinds;
+    GatherArgs g;              // jobs (or slot), max_jobs, books, x, M, N; act inputs below
+    float *y[3];               // per kind: job j's rows out (scaled) at y[kind] + j M; ACT
+                               // reads job j's gate and up rows at y[0], y[1] + j N
+    float *part;               // or NULL: the rows unscaled at part + j nrb 64 (the table
+                               // kernel's one-split partial sums, for k_combine_lut)
+    int nkinds, gj;            // kinds; blocks per (job, kind): blockIdx.x = j gj + b
 };
 
 template <int FMT, bool ACT, int NW>
@@ -4506,22 +4320,32 @@ __global__ __launch_bounds__(NW * 64) void k_vq_rows(RowsArgs ra) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int kind = a.kind_lo + (int)blockIdx.y;
     const int nv = a.N >> 3, nrq = (a.M + 3) >> 2;
+    const int G = ra.gj, j = (int)blockIdx.x / G, b = (int)blockIdx.x - j * G;
     const uint8_t *jidx;
     const uint16_t *jscale;
     int jxi;
-    // this block's quads [q0, q1): the blocks go to the 8 XCDs in turn
-    // (block b to XCD b % 8), so each XCD takes a contiguous eighth of the
-    // quads, shared by its blocks: the record lines a row block's quads
-    // share are then fetched into one XCD's L2, not into each
-    const int G = gridDim.x, xcd = (int)blockIdx.x % 8, nb = (G - xcd + 7) / 8, slot = (int)blockIdx.x / 8;
-    const int qx0 = xcd * nrq / 8, nqx = (xcd + 1) * nrq / 8 - qx0;
-    const int q0 = qx0 + slot * nqx / nb, q1 = qx0 + (slot + 1) * nqx / nb, per = q1 - q0;
-    if (!ga_job(a, kind, 0, jidx, jscale, jxi)) {          // uniform: the slot has no record
+    // this block's quads [q0, q1) of job j: the blocks go to the 8 XCDs in
+    // turn (block b to XCD b % 8 when G is a multiple of 8), so each XCD takes
+    // a contiguous eighth of the quads, shared by its blocks: the record lines
+    // a row block's quads share are then fetched into one XCD's L2, not into
+    // each. (Fewer than 8 blocks: contiguous shares.)
+    int q0, q1;
+    if (G >= 8) {
+        const int xcd = b % 8, nb = (G - xcd + 7) / 8, slot = b / 8;
+        const int qx0 = xcd * nrq / 8, nqx = (xcd + 1) * nrq / 8 - qx0;
+        q0 = qx0 + slot * nqx / nb;
+        q1 = qx0 + (slot + 1) * nqx / nb;
+    } else {
+        q0 = b * nrq / G;
+        q1 = (b + 1) * nrq / G;
+    }
+    const int per = q1 - q0;
+    if (!ga_job(a, kind, j, jidx, jscale, jxi)) {          // uniform: the slot has no record
         for (int r = q0 * 4 + tid; r < min(q1 * 4, a.M); r += NW * 64) ra.y[kind][r] = __builtin_nanf("");
         if (blockIdx.x == 0 && blockIdx.y == 0 && tid == 0 && a.missing) *a.missing = 1;
         return;
     }
-    if (!a.slot && a.njobs[kind] < 1) return;              // uniform
+    if (!a.slot && j >= a.njobs[kind]) return;             // uniform
     if (q0 >= q1) return;                                  // uniform
     const int RQ = min(per, NW), NS = NW / RQ;
     const int qw = wave % RQ, sw = wave / RQ;              // this wave's quad in a round, its slice
@@ -4547,8 +4371,8 @@ __global__ __launch_bounds__(NW * 64) void k_vq_rows(RowsArgs ra) {
     if constexpr (ACT) {
         if (tid < 32) s_exp[tid] = g_exp2_tab[tid];
         __syncthreads();
-        for (int i = tid; i < a.N; i += NW * 64)
-            xl[i] = act_pair(ra.y[0][i], ra.y[1][i], a.act_situ, a.act_beta, a.act_lbeta, s_exp);
+        const float *g0 = ra.y[0] + (size_t)j * a.N, *u0 = ra.y[1] + (size_t)j * a.N;
+        for (int i = tid; i < a.N; i += NW * 64) xl[i] = act_pair(g0[i], u0[i], a.act_situ, a.act_beta, a.act_lbeta, s_exp);
     } else {
         const float *xs = a.x + (a.shared_x ? (size_t)0 : (size_t)jxi * a.N);
         for (int i = tid * 4; i < a.N; i += NW * 64 * 4) *(float4 *)(xl + i) = *(const float4 *)(xs + i);
@@ -4596,7 +4420,8 @@ __global__ __launch_bounds__(NW * 64) void k_vq_rows(RowsArgs ra) {
             if (qq < q1 && r < a.M) {
                 float v = red[tid / 4][tid & 3];
                 for (int s = 1; s < NS; s++) v += red[s * RQ + tid / 4][tid & 3];
-                ra.y[kind][r] = v * f16_keep(jscale[r]);
+                if (ra.part) ra.part[(size_t)j * (((a.M + 63) >> 6) * 64) + r] = v;
+                else ra.y[kind][(size_t)j * a.M + r] = v * f16_keep(jscale[r]);
             }
         }
         __syncthreads();
@@ -4616,29 +4441,35 @@ static int launch_rows(const RowsArgs &ra, int target_blocks, void *stream) {
     static std::atomic<uint64_t> attr{0};
     if (int r_ = lds_limit((const void *)k_vq_rows<FMT, ACT, NW>, (int)lds, attr, stream)) return r_;
     const int nrq = (ra.g.M + 3) / 4;
-    int G = target_blocks / ra.nkinds;
+    RowsArgs r = ra;
+    int G = target_blocks / (ra.nkinds * ra.g.max_jobs);
     if (G > nrq) G = nrq;
     if (G < 1) G = 1;
-    hipLaunchKernelGGL((k_vq_rows<FMT, ACT, NW>), dim3(G, ra.nkinds), dim3(NW * 64), lds, (hipStream_t)stream, ra);
+    r.gj = G;
+    hipLaunchKernelGGL((k_vq_rows<FMT, ACT, NW>), dim3(G * ra.g.max_jobs, ra.nkinds), dim3(NW * 64), lds,
+                       (hipStream_t)stream, r);
     CHECK_LAUNCH();
     return 0;
 }
 
-extern "C" int wk_vq_rows(int fmt, const warp_job *jobs, const int *njobs, int kind_lo, int nkinds,
+extern "C" int wk_vq_rows(int fmt, const warp_job *jobs, const int *njobs, int max_jobs, int kind_lo, int nkinds,
                           const uint16_t *books, const float *x, int M, int N, const warp_slot *slot, int inter,
-                          int act_situ, float act_beta, float act_lbeta, float *const *y, int *missing,
+                          int act_situ, float act_beta, float act_lbeta, float *const *y, float *part, int *missing,
                           int target_blocks, void *stream) {
-    if (kind_lo < 0 || kind_lo + nkinds > 3 || !books || !y || M <= 0 || N <= 0 || (N % 32)) return -1;
-    if (slot ? inter <= 0 : (!jobs || !njobs)) return -1;
+    if (kind_lo < 0 || kind_lo + nkinds > 3 || !books || !y || M <= 0 || N <= 0 || (N % 32) || max_jobs < 1)
+        return -1;
+    if (slot ? (inter <= 0 || max_jobs != 1) : (!jobs || !njobs)) return -1;
     const bool act = x == nullptr;                         // down: inputs act(y[0], y[1])
     if (act && (kind_lo != 2 || nkinds != 1 || !y[0] || !y[1])) return -1;
+    if (part && (kind_lo != 2 || nkinds != 1)) return -1;
     for (int k = kind_lo; k < kind_lo + nkinds; k++)
-        if (!y[k]) return -1;
+        if (!y[k] && !part) return -1;
     RowsArgs ra = {};
     GatherArgs &a = ra.g;
     a.jobs = jobs;
     a.njobs = njobs;
-    a.max_jobs = 1;
+    a.max_jobs = max_jobs;
+    ra.part = part;
     a.kind_lo = kind_lo;
     a.slot = slot;
     a.inter = inter;

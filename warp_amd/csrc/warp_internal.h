@@ -252,25 +252,20 @@ int wk_vq_lut(int fmt, const warp_job *jobs, const int *njobs, int max_jobs, int
  * reading jobs/njobs; route->jobs/njobs/idx/w/missing get what wk_route
  * writes. Only where wk_lut_route_ok says so; NULL otherwise.) */
 int wk_lut_route_ok(int fmt, int E, int K, int shared_x, int kind_lo, int nkinds);
-/* The decode-then-dot kernel with codebook gathers, for one token's
- * matvecs where few rows share a position: the arguments and the partial
- * sums of wk_vq_lut (no routing, no shared rows, no exponent-31 codebooks;
- * N % 32 == 0). target_blocks: about how many blocks to launch. */
-int wk_vq_gather(int fmt, const warp_job *jobs, const int *njobs, int max_jobs, int kind_lo, int nkinds,
-                 const uint16_t *books, const float *x, int shared_x, float *part, size_t cap_floats, int M, int N,
-                 int target_blocks, const float *act_part, int act_splits, int act_situ, float act_beta,
-                 float act_lbeta, int *splits_out, void *stream);
-int wk_gather_plan(int M, int N, int max_jobs, int nkinds, int target_blocks, size_t cap_floats, int *splits_out);
-/* One expert's matvecs (one job: jobs/njobs, or slot: its expert-table
+/* Expert matvecs by whole rows per wave, the kind's codebook staged in LDS
+ * (or, at most 16 KiB, read through L1): jobs/njobs (max_jobs per kind, one
+ * input each: x shared, or act inputs), or slot (one expert's expert-table
  * entry, inter giving the scale arrays' places; a missing record sets
- * *missing and its rows to NaN), whole rows per wave with the kind's
- * codebook staged in LDS (or, at most 16 KiB, read through L1): y[kind] [M] =
- * the rows times their scales, for kinds kind_lo .. kind_lo + nkinds - 1.
- * x NULL (kind 2 only): the inputs are act(y[0], y[1]) [N], the expert's
- * gate and up rows. About target_blocks blocks; N % 32 == 0. */
-int wk_vq_rows(int fmt, const warp_job *jobs, const int *njobs, int kind_lo, int nkinds, const uint16_t *books,
-               const float *x, int M, int N, const warp_slot *slot, int inter, int act_situ, float act_beta,
-               float act_lbeta, float *const *y, int *missing, int target_blocks, void *stream);
+ * *missing and its rows to NaN). y[kind] [max_jobs][M] = the rows times
+ * their scales, for kinds kind_lo .. kind_lo + nkinds - 1; x NULL (kind 2
+ * only): job j's inputs are act(y[0], y[1]) at j N. part (kind 2 only, or
+ * NULL): the rows unscaled at part + j (M rounded up to 64) instead, the
+ * table kernel's one-split partial sums that wk_combine_lut reads. About
+ * target_blocks blocks; N % 32 == 0. */
+int wk_vq_rows(int fmt, const warp_job *jobs, const int *njobs, int max_jobs, int kind_lo, int nkinds,
+               const uint16_t *books, const float *x, int M, int N, const warp_slot *slot, int inter, int act_situ,
+               float act_beta, float act_lbeta, float *const *y, float *part, int *missing, int target_blocks,
+               void *stream);
 /* Certified routing of one decode token (route->scored == 2, sigmoid): what
  * wk_route writes, with route->table (or NULL) for the job lists, from
  * wk_router_cert's arrays; ambiguous rows recomputed from cw / cx. E <= 4096. */
