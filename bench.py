@@ -69,6 +69,8 @@ sys.path.insert(0, os.path.join(HERE, "tests", "golden"))
 
 METRIC = "MoE-layer tokens/s + achieved HBM GB/s (% of peak), K3-scale RVQ, 1 MI355X"
 TRAFFIC_FILE = os.path.join(HERE, "profiles", "k_vq_lut_k3_decode_traffic.json")
+TRAFFIC_SINGLE = os.path.join(HERE, "profiles", "k_vq_rows_single_expert_traffic.json")
+TRAFFIC_KIMI = os.path.join(HERE, "profiles", "k_vq_lut_kimi_decode_traffic.json")
 HBM_PEAK_GBS = 8000.0
 H, I, E, K = 7168, 2048, 384, 16
 S, EN = 2, 4096
@@ -258,7 +260,7 @@ def kernels_sha256():
         return hashlib.sha256(f.read()).hexdigest()
 
 
-def measured_traffic(kernel, launches):
+def measured_traffic(kernel, launches, path=TRAFFIC_FILE):
     """HBM traffic per launch of the expert matvec from the committed counter
     summary (L2-to-memory read requests by size, write requests), when it
     was taken on this kernel from this very kernels.hip (its sha256 is
@@ -266,7 +268,7 @@ def measured_traffic(kernel, launches):
     the launch names the summary must hold ("fused", or "gate_up" and
     "down")."""
     try:
-        with open(TRAFFIC_FILE) as f:
+        with open(path) as f:
             t = json.load(f)
     except (OSError, ValueError):
         return None, "no counter summary"
@@ -464,6 +466,8 @@ def run_single_expert(args):
     achieved = (kn[0] * b0 + kn[1] * b1) / ((kms[0] + kms[1]) / 1e3) / 1e9 if kn[0] and kn[1] else None
     ffn_gbs = pair / (us_ffn * 1e-6) / 1e9
     kernel = ctx_kernel
+    tr, tr_why = measured_traffic(kernel, ("gate_up", "down"), TRAFFIC_SINGLE)
+    traffic = round((kn[0] * tr["gate_up"] + kn[1] * tr["down"]) / max(kn[0] + kn[1], 1)) if tr else None
     return {
         "metric": "single-expert SwiGLU FFN decode tokens/s (one expert per token), 1 MI355X",
         "value": round(n_ffn / (ms / 1e3), 1),
@@ -484,7 +488,8 @@ def run_single_expert(args):
         "ffn_hbm_frac": round(ffn_gbs / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "achieved": None if achieved is None else round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": None if achieved is None else round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": None if achieved is None else round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_per_launch": tr if tr else {"unmeasured": tr_why},
                      "kernel": kernel + " (expert matvec, gate/up and down launches)",
                      "bytes_per_launch": {"gate_up": b0, "down": b1},
                      "avg_launch_us": {"gate_up": round(kms[0] / max(kn[0], 1) * 1e3, 2),
@@ -768,6 +773,11 @@ def run_kimi_decode(args):
     b0 = KK * (2 * gate + 2 * 2 * KI)
     b1 = KK * (down + 2 * KH)
     kernel, fused, achieved, per = matvec_roofline(kms, kn, b0, b1, mv_kernel)
+    tr, tr_why = measured_traffic(kernel, ("fused",) if fused else ("gate_up", "down"), TRAFFIC_KIMI)
+    traffic = None
+    if tr:
+        traffic = tr["fused"] if fused else round((kn[0] * tr["gate_up"] + kn[1] * tr["down"]) /
+                                                  max(kn[0] + kn[1], 1))
     per_layer = (KK * (2 * gate + down + scales_b) + shared_bytes + KE * KH * 4 + 3 * S * EN * 8 * 2 + KE * 4
                  + 2 * KH * 4)
     layer_gbs = per_layer * n_lt / (ms / 1e3) / 1e9
@@ -788,7 +798,8 @@ def run_kimi_decode(args):
         "layer_hbm_gbs": round(layer_gbs, 1),
         "layer_hbm_frac": round(layer_gbs / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_per_launch": tr if tr else {"unmeasured": tr_why},
                      "kernel": per["what"],
                      "bytes_per_launch": per["bytes_per_launch"],
                      "avg_launch_us": per["avg_launch_us"],
