@@ -71,6 +71,8 @@ METRIC = "MoE-layer tokens/s + achieved HBM GB/s (% of peak), K3-scale RVQ, 1 MI
 TRAFFIC_FILE = os.path.join(HERE, "profiles", "k_vq_lut_k3_decode_traffic.json")
 TRAFFIC_SINGLE = os.path.join(HERE, "profiles", "k_vq_rows_single_expert_traffic.json")
 TRAFFIC_KIMI = os.path.join(HERE, "profiles", "k_vq_lut_kimi_decode_traffic.json")
+TRAFFIC_PREFILL = {"fp16": ("k_vq_run_f16", os.path.join(HERE, "profiles", "k_vq_run_f16_kimi_prefill_traffic.json")),
+                   "exact": ("k_vq_mfma_run", os.path.join(HERE, "profiles", "k_vq_mfma_run_kimi_prefill_traffic.json"))}
 HBM_PEAK_GBS = 8000.0
 H, I, E, K = 7168, 2048, 384, 16
 S, EN = 2, 4096
@@ -637,6 +639,10 @@ def run_prefill(args):
     n_lt = args.steps * layers
     gbs = per_layer * n_lt / sec / 1e9
     tfs = flops * n_lt / sec / 1e12
+    # the routed launches' HBM bytes per launch (one gate+up and one down per layer)
+    pk, ppath = TRAFFIC_PREFILL[args.prefill]
+    tr, tr_why = measured_traffic(pk, ("gate_up", "down"), ppath)
+    traffic = round((tr["gate_up"] + tr["down"]) / 2) if tr else None
     return {
         "metric": "MoE-layer prefill tokens/s, Kimi-Linear shape, 1 MI355X",
         "value": round(T * n_lt / sec, 1),
@@ -655,7 +661,9 @@ def run_prefill(args):
                       "tokens_on_busiest_5": counts[:5].tolist(), "algorithmic_bytes": int(per_layer),
                       "useful_flops": int(flops)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_per_launch": tr if tr else {"unmeasured": tr_why},
+                     "kernel": pk + " (routed experts, one gate+up and one down launch per layer)",
                      "what": "algorithmic bytes of the layer (records of the distinct experts picked, shared "
                              "expert, router, codebooks, activations) over the step time: HBM-bound, the "
                              "arithmetic intensity (about 85 FLOP/B) is below the bf16 ridge"},
