@@ -25,6 +25,8 @@ SHAPES = [
     dict(hidden=160, inter=96, experts=8, top_k=3, shared_bits=0),
     # gate/up: 8 jobs x 32 row blocks = 2 row groups spanning jobs; 1 chunk per split
     dict(hidden=1024, inter=2048, experts=12, top_k=8),
+    # tiny: 8 row quads of gate/up (the row kernel's one-quad-per-XCD split) and 16 of down
+    dict(hidden=64, inter=32, experts=4, top_k=2, shared_bits=0),
 ]
 
 
