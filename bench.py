@@ -1352,7 +1352,7 @@ def main():
                          "the fast logits' picks uncertified, strict = every logit in the reference's sequential "
                          "order")
     ap.add_argument("--matvec-path", choices=["auto", "mfma", "fused", "gather"], default="auto",
-                    help="expert matvec kernel: auto = the LUT kernel (the gather kernel for small shapes), mfma = "
+                    help="expert matvec kernel: auto = the LUT kernel (the row kernel for one expert), mfma = "
                          "decode-then-dot on the matrix cores, fused = the LUT kernel's gate/up, down and combine in "
                          "one launch per layer, gather = decode-then-dot with codebook gathers")
     ap.add_argument("--prefill", choices=["exact", "fp16"], default="fp16",

@@ -487,10 +487,10 @@ int warp_hip_put_expert_synth(warp_hip_ctx *c, int layer, int expert, uint64_t s
  * down and combine as work items of one launch per layer where the token's
  * routing runs inside it (the same results bit for bit; slower than AUTO at
  * the K3 shape, where the waits between its work items cost more than the
- * launch boundaries they replace); GATHER forces the decode-then-dot
- * kernel with codebook gathers (no tables: each lane decodes its rows'
- * weights from the fp16 codebook in L2), which AUTO takes where few rows
- * share a position (one expert's FFN, small matrices). Applies to
+ * launch boundaries they replace); GATHER forces the row kernel
+ * (decode-then-dot, no tables: whole rows per wave, each lane decoding its
+ * rows' weights from the kind's fp16 codebook staged in LDS), which AUTO
+ * takes for one expert (warp_hip_expert_ffn, warp_hip_vq_matvec). Applies to
  * warp_hip_moe_decode*, warp_hip_expert_ffn and warp_hip_vq_matvec. */
 enum { WARP_HIP_PATH_AUTO = 0, WARP_HIP_PATH_MFMA = 1, WARP_HIP_PATH_LUT_FUSED = 2, WARP_HIP_PATH_GATHER = 3 };
 int warp_hip_set_matvec_path(warp_hip_ctx *c, int path);
@@ -500,7 +500,7 @@ int warp_hip_set_matvec_path(warp_hip_ctx *c, int path);
 int warp_hip_set_router_fast(warp_hip_ctx *c, int fast);
 /* The expert matvec kernel the current path runs for a decode of `layer`
  * (experts = 1: warp_hip_expert_ffn's single expert, else the layer's
- * top_k): "k_vq_lut", "k_moe_fused", "k_vq_mfma" or "k_apply_p6". For
+ * top_k): "k_vq_lut", "k_vq_rows", "k_moe_fused", "k_vq_mfma" or "k_apply_p6". For
  * reports; never NULL. */
 const char *warp_hip_matvec_kernel(warp_hip_ctx *c, int layer, int experts);
 /* Per-launch timing with HIP events on the compute stream: when on, every

@@ -1820,7 +1820,7 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
      * now, before this layer reads the table */
     if (c->crc_pending && (rc = crc_report(c))) return rc;
     const int use_lut = use_table(c, L);
-    /* the gather kernel reads x in f32 and leaves its partial sums where the
+    /* the row kernel reads x in f32 and leaves its partial sums where the
      * table kernel does; it routes in a launch of its own */
     const int gat = use_gather(c, L, K);
     /* a resident record naming other codebooks than the layer's: the
