@@ -1758,6 +1758,10 @@ static int use_table(const warp_hip_ctx *c, const layer_t *L)
 static int use_gather(const warp_hip_ctx *c, const layer_t *L, int experts)
 {
     if (!use_table(c, L) || L->books_x31 || c->He % 32 || c->cfg.inter % 32) return 0;
+    /* its LDS: the kind's codebook when staged (2 x 4096 entries: 128 KiB)
+     * and the input */
+    const size_t in = (size_t)(c->He > c->cfg.inter ? c->He : c->cfg.inter) * sizeof(float);
+    if ((c->cfg.fmt == WARP_HIP_VQ12 ? (size_t)131072 : 0) + in > 160 * 1024 - 1024) return 0;
     if (c->mv_path == WARP_HIP_PATH_GATHER) return 1;
     /* AUTO: one expert's matvecs (an expert FFN or one matrix: 1.3-1.8x the
      * table kernel at [1024 x 2304]); from two experts on, the tables are
