@@ -349,7 +349,7 @@ struct warp_hip_ctx {
     /* device scratch */
     float *logits;
     unsigned long long *cert_ctr;  /* certified decode routings that recomputed, rows recomputed */
-    unsigned *cert_done;           /* the certifying router's row words (after cert_ctr) */
+    unsigned *cert_done;           /* the certifying router's launch counter and tagged rows (after cert_ctr) */
     warp_hip_route_stats route_stats;
     int *idx;
     float *w;
@@ -477,9 +477,10 @@ static int ctx_alloc(warp_hip_ctx *c)
     /* at least four rows: one token's scores, biased scores and their
      * bounds (wk_router_cert) */
     DMALLOC(c, c->logits, (size_t)(T > 4 ? T : 4) * E * 4);
-    /* the certification's counters, then one word per expert */
-    DMALLOC(c, c->cert_ctr, 2 * sizeof(unsigned long long) + (size_t)E * sizeof(unsigned));
-    DEV(c, hipMemset(c->cert_ctr, 0, 2 * sizeof(unsigned long long) + (size_t)E * sizeof(unsigned)));
+    /* the certification's counters, then the certifier's launch counter and
+     * tagged rows */
+    DMALLOC(c, c->cert_ctr, 2 * sizeof(unsigned long long) + WK_CERT_SYNC_WORDS(E) * sizeof(unsigned));
+    DEV(c, hipMemset(c->cert_ctr, 0, 2 * sizeof(unsigned long long) + WK_CERT_SYNC_WORDS(E) * sizeof(unsigned)));
     c->cert_done = (unsigned *)(c->cert_ctr + 2);
     DMALLOC(c, c->idx, P * 4);
     DMALLOC(c, c->w, P * 4);

@@ -501,6 +501,24 @@ __device__ __forceinline__ float cert_score(float l, const uint64_t *etab = null
     return __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_ref(-l, etab)));
 }
 
+// A row's four values for the certifying block, each with this launch's tag
+// in the same 64-bit store (tg = NULL: none): the block sees a value and its
+// tag together or not at all, so it needs no separate ready word.
+struct CertTag {
+    unsigned long long *tg;     // [E][4]: point score, biased score, lower, upper bound
+    unsigned tag;
+};
+__device__ __forceinline__ void st_tag(const CertTag &ct, int e, int i, float v) {
+    if (ct.tg)
+        __hip_atomic_store(ct.tg + 4 * (size_t)e + i, ((unsigned long long)ct.tag << 32) | __float_as_uint(v),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// the four values of row e: the store to out and the tagged one
+__device__ __forceinline__ void cert_put(float *out, int E, int e, int i, float v, const CertTag &ct) {
+    st_agent(out + (size_t)i * E + e, v);
+    st_tag(ct, e, i, v);
+}
+
 // Row e's outputs from its exact sum S, the sum of its running sums'
 // magnitudes (as) and of its products' magnitudes (ap): the reference's
 // rounding errors are bounded by u (as + ap) up to terms of relative size
@@ -509,24 +527,26 @@ __device__ __forceinline__ float cert_score(float l, const uint64_t *etab = null
 // 2^-149 each. The logit interval is widened to floats outward, and the
 // biased-score bounds by one more ulp each way for the score and the sum.
 __device__ __forceinline__ void cert_finish(double S, double as, double ap, int H, int E, int e,
-                                            const float *__restrict__ bias, float *__restrict__ out) {
+                                            const float *__restrict__ bias, float *__restrict__ out,
+                                            const CertTag &ct) {
     const double n = (double)H;
     const double B = CERT_U * (as + 1.01 * ap) * (1.0 + 4.0 * n * CERT_U) + 1e-12 * (as + ap) + n * 1.4e-45;
     const float l = (float)S;
     const float lo = f_down((float)(S - B)), hi = f_up((float)(S + B));
     const float bv = bias ? bias[e] : 0.0f;
     const float sc = cert_score(l);
-    st_agent(out + e, sc);
-    st_agent(out + E + e, __fadd_rn(sc, bv));
+    cert_put(out, E, e, 0, sc, ct);
+    cert_put(out, E, e, 1, __fadd_rn(sc, bv), ct);
     const bool ok = isfinite(S) && isfinite(B) && isfinite(lo) && isfinite(hi);
-    st_agent(out + 2 * E + e, ok ? f_down(__fadd_rn(f_down(cert_score(lo)), bv)) : -INFINITY);
-    st_agent(out + 3 * E + e, ok ? f_up(__fadd_rn(f_up(cert_score(hi)), bv)) : INFINITY);
+    cert_put(out, E, e, 2, ok ? f_down(__fadd_rn(f_down(cert_score(lo)), bv)) : -INFINITY, ct);
+    cert_put(out, E, e, 3, ok ? f_up(__fadd_rn(f_up(cert_score(hi)), bv)) : INFINITY, ct);
 }
 
 // The same by three lanes (lane 0 the point score, 1 the lower bound, 2 the
 // upper bound), from S and upper bounds as, ap of the sums of magnitudes.
 __device__ __forceinline__ void cert_finish3(double S, double as, double ap, int H, int E, int e, int lane,
-                                             const float *__restrict__ bias, float *__restrict__ out) {
+                                             const float *__restrict__ bias, float *__restrict__ out,
+                                             const CertTag &ct) {
     const double n = (double)H;
     const double B = CERT_U * (as + ap) * (1.0 + 4.0 * n * CERT_U) + 1e-12 * (as + ap) + n * 1.4e-45;
     const float lo = f_down((float)(S - B)), hi = f_up((float)(S + B));
@@ -535,12 +555,12 @@ __device__ __forceinline__ void cert_finish3(double S, double as, double ap, int
     const float sc = cert_score(l);
     const float bv = bias ? bias[e] : 0.0f;
     if (lane == 0) {
-        st_agent(out + e, sc);
-        st_agent(out + E + e, __fadd_rn(sc, bv));
+        cert_put(out, E, e, 0, sc, ct);
+        cert_put(out, E, e, 1, __fadd_rn(sc, bv), ct);
     } else if (lane == 1) {
-        st_agent(out + 2 * E + e, ok ? f_down(__fadd_rn(f_down(sc), bv)) : -INFINITY);
+        cert_put(out, E, e, 2, ok ? f_down(__fadd_rn(f_down(sc), bv)) : -INFINITY, ct);
     } else {
-        st_agent(out + 3 * E + e, ok ? f_up(__fadd_rn(f_up(sc), bv)) : INFINITY);
+        cert_put(out, E, e, 3, ok ? f_up(__fadd_rn(f_up(sc), bv)) : INFINITY, ct);
     }
 }
 
@@ -554,7 +574,7 @@ __device__ __forceinline__ void cert_finish3(double S, double as, double ap, int
 // The point score is sigma(S) rounded to float: within the bounds, and
 // within a few ulps of the reference's operations on fp32(S).
 __device__ __forceinline__ bool cert_finish1(double S, double B, int E, int e, const float *__restrict__ bias,
-                                             float *__restrict__ out) {
+                                             float *__restrict__ out, const CertTag &ct) {
     if (!(fabs(S) + B < 30.0)) return false;
     const float ef = __expf(-(float)S);
     const double sg = 1.0 / (1.0 + (double)ef);
@@ -563,10 +583,10 @@ __device__ __forceinline__ bool cert_finish1(double S, double B, int E, int e, c
     const double err = d1 * r * 1.01 + d1 * B + 0.05 * B * B + (sg + d1 * B) * 0x1p-22 + 1e-300;
     const float bv = bias ? bias[e] : 0.0f;
     const float sc = (float)sg;
-    st_agent(out + e, sc);
-    st_agent(out + E + e, __fadd_rn(sc, bv));
-    st_agent(out + 2 * E + e, f_down(__fadd_rn(f_down((float)(sg - err)), bv)));
-    st_agent(out + 3 * E + e, f_up(__fadd_rn(f_up((float)(sg + err)), bv)));
+    cert_put(out, E, e, 0, sc, ct);
+    cert_put(out, E, e, 1, __fadd_rn(sc, bv), ct);
+    cert_put(out, E, e, 2, f_down(__fadd_rn(f_down((float)(sg - err)), bv)), ct);
+    cert_put(out, E, e, 3, f_up(__fadd_rn(f_up((float)(sg + err)), bv)), ct);
     return true;
 }
 
@@ -574,7 +594,8 @@ __device__ __forceinline__ bool cert_finish1(double S, double B, int E, int e, c
 // score's lower bound, [3E, 4E) its upper bound. One 256-thread block per
 // row; each thread a contiguous run of the row. H % 4 == 0.
 __device__ __forceinline__ void router_row_cert(const float *__restrict__ W, const float *__restrict__ x, int E,
-                                                int H, int e, const float *__restrict__ bias, float *__restrict__ out) {
+                                                int H, int e, const float *__restrict__ bias, float *__restrict__ out,
+                                                const CertTag &ct) {
     __shared__ double r_sum[4], r_abs_s[4];
     __shared__ double r_scan[4];
     __shared__ float r_abs_p[4];
@@ -643,23 +664,36 @@ __device__ __forceinline__ void router_row_cert(const float *__restrict__ W, con
         const double S = (r_sum[0] + r_sum[1]) + (r_sum[2] + r_sum[3]);
         const double as = (r_abs_s[0] + r_abs_s[1]) + (r_abs_s[2] + r_abs_s[3]);
         const double ap = ((double)r_abs_p[0] + r_abs_p[1]) + ((double)r_abs_p[2] + r_abs_p[3]);
-        cert_finish(S, as, ap, H, E, e, bias, out);
+        cert_finish(S, as, ap, H, E, e, bias, out, ct);
     }
 }
 
 // The certification of the selection, by the router's last block
-// (cert_last): done holds one word per row, set by the row's block once the
-// row is out (zero between launches; the last block clears them), K picks,
-// cctr the counters (or NULL), flag the route's missing flag. done = NULL:
-// the arrays only.
+// (cert_last): sync (or NULL: the arrays only) is the launch counter, 2
+// words, then [E][4] 64-bit tagged values (CertTag): a row's blocks tag its
+// values with the counter plus one, the certifying block takes a row once
+// its four tags are, and then advances the counter (a row a later launch
+// writes can never look done to this one, and a late row of this one never
+// to the next). K picks, cctr the counters (or NULL), flag the route's
+// missing flag.
 struct CertTail {
-    unsigned *done;
+    unsigned *sync;
     int K;
     unsigned long long *cctr;
     int *flag;                  // a wait past CERT_POLLS sets bit 2 (value 4)
     warp_route_args pk;         // pk.idx set: the routing's outputs (idx, w; with pk.table the job lists)
 };
-constexpr unsigned CERT_POLLS = 1u << 16;   // polls of the rows' words before the last block gives up
+constexpr unsigned CERT_POLLS = 1u << 16;   // polls of the rows' values before the last block gives up
+
+// This launch's tag for the rows' values (the block's threads all read it).
+__device__ __forceinline__ CertTag cert_tag(const CertTail &t) {
+    CertTag ct = {nullptr, 0u};
+    if (t.sync) {
+        ct.tg = (unsigned long long *)(t.sync + 2);
+        ct.tag = __hip_atomic_load(t.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    }
+    return ct;
+}
 template <int NT>
 __device__ void cert_last(const float *__restrict__ W, const float *__restrict__ x, int E, int H,
                           const float *__restrict__ bias, float *__restrict__ out, const CertTail &t, float *lds,
@@ -669,8 +703,11 @@ __global__ __launch_bounds__(256) void k_router_cert(const float *__restrict__ W
                                                      int H, const float *__restrict__ bias, float *__restrict__ out,
                                                      CertTail t, int lds_floats) {
     extern __shared__ __attribute__((aligned(16))) float rcg_lds[];
-    if ((int)blockIdx.x < E) router_row_cert(W, x, E, H, blockIdx.x, bias, out);   // (block E: the certifier)
-    if (t.done) cert_last<256>(W, x, E, H, bias, out, t, rcg_lds, lds_floats);
+    if ((int)blockIdx.x < E) {
+        router_row_cert(W, x, E, H, blockIdx.x, bias, out, cert_tag(t));
+        return;
+    }
+    cert_last<256>(W, x, E, H, bias, out, t, rcg_lds, lds_floats);   // block E, with t.sync only
 }
 
 // The same arrays, faster: one 256-thread block per row, W's row and x
@@ -796,14 +833,14 @@ __global__ __launch_bounds__(256) void k_router_cert_b(const float *__restrict__
     if (tid < 64) {                                       // wave 0 (uniform values)
         const double hsum = ((double)(rc_as[0] + rc_as[1]) + (double)(rc_as[2] + rc_as[3])) * g;
         const double B = fmin(B1, hsum * (1.0 + 4.0 * n * CERT_U) + 1e-12 * as + n * 1.4e-45);
+        const CertTag ct = cert_tag(t);
         if (!(fabs(S) + B < 30.0)) {                       // uniform
             if (tid < 3) cert_finish3(S, B / (CERT_U * (1.0 + 4.0 * n * CERT_U) + 1e-12), 0.0, H, E, e, tid,
-                                      bias, out);
+                                      bias, out, ct);
         } else if (tid == 0) {
-            cert_finish1(S, B, E, e, bias, out);
+            cert_finish1(S, B, E, e, bias, out, ct);
         }
     }
-    if (t.done) cert_last<256>(W, x, E, H, bias, out, t, (float *)rc_lds, lds_floats);
 }
 
 // Launches k_router_cert_b<R4> when H / (4 R4) threads of the block make
@@ -822,23 +859,23 @@ static bool router_cert_b(const float *W, const float *x, int E, int H, const fl
     const int n4 = H >> 2;
     if ((H & 3) || n4 % R4 || n4 / R4 > 256 || (n4 / R4) % 64) return false;
     const size_t lds = std::max((size_t)2 * 256 * (R4 + ((R4 & 1) ? 2 : 1)) * sizeof(float4),
-                                t.done ? cert_last_floats(E, H, t.pk.table) * sizeof(float) : (size_t)0);
+                                t.sync ? cert_last_floats(E, H, t.pk.table) * sizeof(float) : (size_t)0);
     if (lds > 160 * 1024) return false;
     static std::atomic<uint64_t> attr{0};
     if (lds_limit((const void *)k_router_cert_b<R4>, (int)lds, attr, s)) return false;
-    hipLaunchKernelGGL(k_router_cert_b<R4>, dim3(E + (t.done ? 1 : 0)), dim3(256), lds, s, W, x, E, H, bias, out,
+    hipLaunchKernelGGL(k_router_cert_b<R4>, dim3(E + (t.sync ? 1 : 0)), dim3(256), lds, s, W, x, E, H, bias, out,
                        t, (int)(lds / sizeof(float)));
     return true;
 }
 
 extern "C" int wk_router_cert(const float *W, const float *x, int E, int H, const float *bias, float *out,
-                              unsigned *done, int K, unsigned long long *cctr, int *flag,
+                              unsigned *sync, int K, unsigned long long *cctr, int *flag,
                               const warp_route_args *pick, void *stream) {
     if (E <= 0 || H <= 0 || (H & 3) || H > 1024 * CERT_MAXV) return -1;
-    if (done && (K <= 0 || K > WARP_MAX_K || K > E || E > CERT_EMAX)) return -1;
-    if (pick && (!done || !pick->idx || !pick->w || (pick->table && (!pick->jobs || !pick->njobs || !flag))))
+    if (sync && (K <= 0 || K > WARP_MAX_K || K > E || E > CERT_EMAX)) return -1;
+    if (pick && (!sync || !pick->idx || !pick->w || (pick->table && (!pick->jobs || !pick->njobs || !flag))))
         return -1;
-    CertTail t = {done, K, cctr, flag, {}};
+    CertTail t = {sync, K, cctr, flag, {}};
     if (pick) t.pk = *pick;
     // hidden sizes of the reference's models (Kimi-Linear 2304, K3 7168) and
     // their neighbours take the staged kernel
@@ -846,11 +883,11 @@ extern "C" int wk_router_cert(const float *W, const float *x, int E, int H, cons
     if (!(router_cert_b<3>(W, x, E, H, bias, out, t, st) || router_cert_b<4>(W, x, E, H, bias, out, t, st) ||
           router_cert_b<5>(W, x, E, H, bias, out, t, st) || router_cert_b<6>(W, x, E, H, bias, out, t, st) ||
           router_cert_b<7>(W, x, E, H, bias, out, t, st) || router_cert_b<8>(W, x, E, H, bias, out, t, st))) {
-        const size_t lds = done ? cert_last_floats(E, H, t.pk.table) * sizeof(float) : 0;
+        const size_t lds = sync ? cert_last_floats(E, H, t.pk.table) * sizeof(float) : 0;
         if (lds > 160 * 1024) return -1;
         static std::atomic<uint64_t> attr{0};
         if (int r_ = lds_limit((const void *)k_router_cert, (int)lds, attr, stream)) return r_;
-        hipLaunchKernelGGL(k_router_cert, dim3(E + (done ? 1 : 0)), dim3(256), lds, st, W, x, E, H, bias, out, t,
+        hipLaunchKernelGGL(k_router_cert, dim3(E + (sync ? 1 : 0)), dim3(256), lds, st, W, x, E, H, bias, out, t,
                            (int)(lds / sizeof(float)));
     }
     CHECK_LAUNCH();
@@ -2291,19 +2328,12 @@ __device__ void cert_last(const float *__restrict__ W, const float *__restrict__
     __shared__ int sel[WARP_MAX_K];
     __shared__ float wsel[WARP_MAX_K];
     const int tid = threadIdx.x;
-    // A row's block writes its row with agent-coherent stores (st_agent),
-    // complete once wait_stores() returns, and then sets the row's word.
     // The certifying block (one more block, gridDim.x - 1 = E, no row of its
-    // own) polls the words and loads each row as soon as it is out, so the
-    // last row's arrival leaves it one load behind; a wait past CERT_POLLS
-    // polls raises bit 2 of the flag (the call reports it) and leaves the
-    // arrays uncertified. It clears the words for the next launch.
-    if ((int)blockIdx.x != E) {
-        wait_stores();
-        __syncthreads();
-        if (tid == 0) __hip_atomic_store(t.done + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        return;
-    }
+    // own) polls the rows' tagged values (CertTag) and takes each row as
+    // soon as its four carry this launch's tag; a wait past CERT_POLLS polls
+    // raises bit 2 of the flag (the call reports it) and leaves the arrays
+    // uncertified. It then advances the launch counter.
+    const CertTag ct = cert_tag(t);
     const int E2 = (E + 1) & ~1, nw = (E + 63) >> 6;
     float *score = lds, *biased = lds + E2, *lo = lds + 2 * E2, *hi = lds + 3 * E2;
     // the expert table, for the job lists, staged while the rows come in;
@@ -2326,12 +2356,19 @@ __device__ void cert_last(const float *__restrict__ W, const float *__restrict__
     for (unsigned n = 0;; n++) {
         for (int i = 0; i < CERT_EMAX / NT; i++) {
             const int e = tid + i * NT;
-            if (((pend >> i) & 1u) && __hip_atomic_load(t.done + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
-                score[e] = ld_agent(out + e);
-                biased[e] = ld_agent(out + E + e);
-                lo[e] = ld_agent(out + 2 * E + e);
-                hi[e] = ld_agent(out + 3 * E + e);
-                pend &= ~(1u << i);
+            if ((pend >> i) & 1u) {
+                unsigned long long v[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    v[k] = __hip_atomic_load(ct.tg + 4 * (size_t)e + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if ((unsigned)(v[0] >> 32) == ct.tag && (unsigned)(v[1] >> 32) == ct.tag &&
+                    (unsigned)(v[2] >> 32) == ct.tag && (unsigned)(v[3] >> 32) == ct.tag) {
+                    score[e] = __uint_as_float((unsigned)v[0]);
+                    biased[e] = __uint_as_float((unsigned)v[1]);
+                    lo[e] = __uint_as_float((unsigned)v[2]);
+                    hi[e] = __uint_as_float((unsigned)v[3]);
+                    pend &= ~(1u << i);
+                }
             }
         }
         if (__syncthreads_and(pend == 0)) break;          // uniform
@@ -2342,11 +2379,11 @@ __device__ void cert_last(const float *__restrict__ W, const float *__restrict__
         __builtin_amdgcn_s_sleep(1);
     }
     __syncthreads();
+    if (tid == 0) __hip_atomic_store(t.sync, ct.tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // the next launch's
     if (!cl_last) {                                       // (never in practice)
         if (tid == 0 && t.flag) __hip_atomic_fetch_or(t.flag, 4, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
-    for (int e = tid; e < E; e += NT) __hip_atomic_store(t.done + e, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     warp_route_args r = {};
     r.bias = bias;
     r.E = E;

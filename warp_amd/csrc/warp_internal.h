@@ -99,7 +99,8 @@ int wk_router_scored(const float *W, const float *x, int E, int H, const float *
 /* Certified routing inputs of one token (sigmoid scores, fp32 router): out
  * [4][E] = point scores, point biased scores, and the lower and upper bounds
  * of the biased score the reference's sequential logit gives. H % 4 == 0,
- * H <= 16384. done (E zeroed words the launch leaves zeroed; or NULL): the
+ * H <= 16384. sync (WK_CERT_SYNC_WORDS(E) words, zeroed before the first
+ * launch and kept between launches; or NULL): the
  * last block also certifies the top-K selection and rewrites the rows whose
  * order the bounds leave open with their exact (sequential) values, so that
  * a routing from [0, 2E) (scored = 1) picks the reference's experts in its
@@ -110,7 +111,8 @@ int wk_router_scored(const float *W, const float *x, int E, int H, const float *
  * and with pick->table the job lists (pick->jobs, njobs, inter; a pick
  * without a record sets *flag) -- so that no routing launch follows. */
 struct warp_route_args_s;
-int wk_router_cert(const float *W, const float *x, int E, int H, const float *bias, float *out, unsigned *done,
+#define WK_CERT_SYNC_WORDS(E) (2 + 8 * (size_t)(E))  /* a launch counter, then [E][4] 64-bit tagged values */
+int wk_router_cert(const float *W, const float *x, int E, int H, const float *bias, float *out, unsigned *sync,
                    int K, unsigned long long *cctr, int *flag, const struct warp_route_args_s *pick, void *stream);
 
 /* Quantised router / dense trunk rows (Q8G, Q4G, Q3G with the reference's
