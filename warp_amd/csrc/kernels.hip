@@ -1950,28 +1950,31 @@ __device__ __forceinline__ float fkey_inv(long long k) {
 }
 
 // v + p[0] + p[1] + ... + p[4 n4 - 1], one fp32 add at a time in that order
-// (the reference's dotf chain), p 16-byte aligned in LDS, the next four
-// float4 read while four are added.
+// (the reference's dotf chain), p 16-byte aligned in LDS, the next 16
+// float4 read while 16 are added: 64 dependent adds cover the LDS latency
+// (4 ahead left it exposed: a K3 routing's recompute, 2.1 rows on average,
+// took 35 us with 4 ahead and 27 us with 16).
 __device__ __forceinline__ float chain_add(float v, const float4 *p, int n4) {
+    constexpr int D = 16;
     int q = 0;
-    if (n4 >= 4) {
-        float4 c[4];
+    if (n4 >= D) {
+        float4 c[D];
 #pragma unroll
-        for (int j = 0; j < 4; j++) c[j] = p[j];
-        for (; q + 4 <= n4; q += 4) {
-            float4 nx[4];
-            const int qn = min(q + 4, n4 - 4);             // (the last group reads itself again)
+        for (int j = 0; j < D; j++) c[j] = p[j];
+        for (; q + D <= n4; q += D) {
+            float4 nx[D];
+            const int qn = min(q + D, n4 - D);             // (the last group reads itself again)
 #pragma unroll
-            for (int j = 0; j < 4; j++) nx[j] = p[qn + j];
+            for (int j = 0; j < D; j++) nx[j] = p[qn + j];
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
+            for (int j = 0; j < D; j++) {
                 v = __fadd_rn(v, c[j].x);
                 v = __fadd_rn(v, c[j].y);
                 v = __fadd_rn(v, c[j].z);
                 v = __fadd_rn(v, c[j].w);
             }
 #pragma unroll
-            for (int j = 0; j < 4; j++) c[j] = nx[j];
+            for (int j = 0; j < D; j++) c[j] = nx[j];
         }
     }
     for (; q < n4; q++) {
