@@ -669,8 +669,8 @@ __device__ __forceinline__ void router_row_cert(const float *__restrict__ W, con
 }
 
 // The certification of the selection, by the router's last block
-// (cert_last): sync (or NULL: the arrays only) is the launch counter, 2
-// words, then [E][4] 64-bit tagged values (CertTag): a row's blocks tag its
+// (cert_last): sync (or NULL: the arrays only; 8-byte aligned) is the launch
+// counter (word 0; word 1 pads), then [E][4] 64-bit tagged values (CertTag): a row's blocks tag its
 // values with the counter plus one, the certifying block takes a row once
 // its four tags are, and then advances the counter (a row a later launch
 // writes can never look done to this one, and a late row of this one never
@@ -872,7 +872,7 @@ extern "C" int wk_router_cert(const float *W, const float *x, int E, int H, cons
                               unsigned *sync, int K, unsigned long long *cctr, int *flag,
                               const warp_route_args *pick, void *stream) {
     if (E <= 0 || H <= 0 || (H & 3) || H > 1024 * CERT_MAXV) return -1;
-    if (sync && (K <= 0 || K > WARP_MAX_K || K > E || E > CERT_EMAX)) return -1;
+    if (sync && (K <= 0 || K > WARP_MAX_K || K > E || E > CERT_EMAX || ((uintptr_t)sync & 7))) return -1;
     if (pick && (!sync || !pick->idx || !pick->w || (pick->table && (!pick->jobs || !pick->njobs || !flag))))
         return -1;
     CertTail t = {sync, K, cctr, flag, {}};

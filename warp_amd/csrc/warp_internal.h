@@ -99,8 +99,8 @@ int wk_router_scored(const float *W, const float *x, int E, int H, const float *
 /* Certified routing inputs of one token (sigmoid scores, fp32 router): out
  * [4][E] = point scores, point biased scores, and the lower and upper bounds
  * of the biased score the reference's sequential logit gives. H % 4 == 0,
- * H <= 16384. sync (WK_CERT_SYNC_WORDS(E) words, zeroed before the first
- * launch and kept between launches; or NULL): the
+ * H <= 16384. sync (WK_CERT_SYNC_WORDS(E) words, 8-byte aligned, zeroed
+ * before the first launch and kept between launches; or NULL): the
  * last block also certifies the top-K selection and rewrites the rows whose
  * order the bounds leave open with their exact (sequential) values, so that
  * a routing from [0, 2E) (scored = 1) picks the reference's experts in its
