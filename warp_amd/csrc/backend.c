@@ -349,7 +349,7 @@ struct warp_hip_ctx {
     /* device scratch */
     float *logits;
     unsigned long long *cert_ctr;  /* certified decode routings that recomputed, rows recomputed */
-    unsigned *cert_done;           /* the certifying router's launch counter and tagged rows (after cert_ctr) */
+    unsigned *cert_sync;           /* the certifying router's launch counter and tagged rows (after cert_ctr) */
     warp_hip_route_stats route_stats;
     int *idx;
     float *w;
@@ -481,7 +481,7 @@ static int ctx_alloc(warp_hip_ctx *c)
      * tagged rows */
     DMALLOC(c, c->cert_ctr, 2 * sizeof(unsigned long long) + WK_CERT_SYNC_WORDS(E) * sizeof(unsigned));
     DEV(c, hipMemset(c->cert_ctr, 0, 2 * sizeof(unsigned long long) + WK_CERT_SYNC_WORDS(E) * sizeof(unsigned)));
-    c->cert_done = (unsigned *)(c->cert_ctr + 2);
+    c->cert_sync = (unsigned *)(c->cert_ctr + 2);
     DMALLOC(c, c->idx, P * 4);
     DMALLOC(c, c->w, P * 4);
     DMALLOC(c, c->jobs, (size_t)3 * c->max_jobs * sizeof(warp_job));
@@ -1892,7 +1892,7 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
     if (cert) {
         const warp_route_args pick = { NULL, NULL, table, E, g->router_act, g->renorm, I, g->routed_scale, c->idx,
                                        c->w, c->jobs, c->njobs, c->missing, 2, NULL, NULL, 0, NULL };
-        KRN(c, wk_router_cert(L->router, x_dev, E, H, L->bias, c->logits, c->cert_done, K, c->cert_ctr, c->missing,
+        KRN(c, wk_router_cert(L->router, x_dev, E, H, L->bias, c->logits, c->cert_sync, K, c->cert_ctr, c->missing,
                               cert_route ? &pick : NULL, c->st));
     }
     else if (fuse_shared && !sh_in_gu) KRN(c, wk_router_shared(L->router, x_dev, E, H, c->logits, &sa, c->st));
