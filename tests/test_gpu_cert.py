@@ -100,8 +100,10 @@ def decode_case(model, ctx, x, paths):
     return ri, rl, got, rw
 
 
-@pytest.mark.parametrize("E", [64, 640])
+@pytest.mark.parametrize("E", [64, 100, 640])
 def test_certified_picks_on_planted_near_ties(E):
+    # (100: rows the certifying block polls in a partial last pass, and masks
+    # of a last 64-expert word that is not full)
     K, n_tok = 8, 4
     rng = np.random.default_rng(900 + E)
     cluster = set(int(i) for i in rng.permutation(E)[:24])
