@@ -498,6 +498,12 @@ int warp_hip_set_matvec_path(warp_hip_ctx *c, int path);
  * certifying them, 0 certifies (the default). For measuring what the
  * certificate costs; no counterpart in the reference. */
 int warp_hip_set_router_fast(warp_hip_ctx *c, int fast);
+/* The certifying router's limit on polls for its rows (0: the default,
+ * 65,536). A launch that reaches it gives up: that layer's outputs are NaN,
+ * and the next synchronising call reports E_DEVICE and resets the router's
+ * launch counter and tagged rows, so later launches certify as before. For
+ * tests of that path; no counterpart in the reference. */
+int warp_hip_set_cert_polls(warp_hip_ctx *c, unsigned polls);
 /* The expert matvec kernel the current path runs for a decode of `layer`
  * (experts = 1: warp_hip_expert_ffn's single expert, else the layer's
  * top_k): "k_vq_lut", "k_vq_rows", "k_moe_fused", "k_vq_mfma" or "k_apply_p6". For

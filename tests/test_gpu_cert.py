@@ -209,3 +209,57 @@ def test_router_bounds_hold_the_reference_scores(H_, scale):
     finally:
         ctx.close()
     log(f"H={H_} scale {scale}: reference biased scores inside the bounds for 6 x {E} experts; widest {worst:.3g}")
+
+
+def test_certifier_give_up_is_reported_and_recovered():
+    """The certifying block's bounded wait for the rows, forced from the
+    host (warp_hip_set_cert_polls: a limit of one poll, far below the rows'
+    time at H 7168): a launch that gives up leaves empty job lists, so the
+    layer's launches skip their work and its outputs are NaN, and the call
+    reports E_DEVICE. The report resets the router's launch counter and
+    tagged rows once the stream is idle: rows written after a give-up carry
+    the next launch's tag, and must not pass for the next launch's rows. With
+    the default limit again, picks and outputs are the oracle's."""
+    import warp_amd
+    E, K, H_ = 384, 8, 7168
+    spec = ct.Spec(hidden=H_, inter=64, experts=E, top_k=K, layers=1, fmt="VQ12", seed=12, bias=True,
+                   shared_bits=0, renorm=True, routed_scale=1.0, subnormals=False, keep_codes=False,
+                   materialize=tuple(range(0, E, 8)), book_std=0.3)
+    model = ct.build(spec)
+    lay = model.layers[0]
+    b = np.zeros(E, np.float32)
+    b[::8] = 1.0                                          # the picks among the materialised experts
+    lay.bias = b
+    ctx = open_ctx(model)
+    rng = np.random.default_rng(12)
+    try:
+        warp_amd.load_container_model(ctx, model)
+        ctx.set_router(0, np.ascontiguousarray(lay.router, np.float32), b)
+        ctx.set_cert_polls(1)
+        gave_up = 0
+        for t in range(4):
+            x = rng.normal(size=H_).astype(np.float32)
+            out = empty(H_)
+            try:
+                idx, _ = ctx.moe_decode(0, dev(x), out, want_route=True)
+            except warp_amd.WarpHipError as e:
+                assert e.code == warp_amd.E_DEVICE, e
+                assert np.isnan(host(out)).all(), "a layer whose certifier gave up was computed"
+                gave_up += 1
+                continue
+            ro, ri, _, _ = po.LayerView(model, 0).moe_layer(x)
+            assert np.array_equal(idx, ri) and rel_err(host(out), ro) <= TOL
+        assert gave_up >= 1, "no launch gave up after one poll"
+        ctx.set_cert_polls(0)
+        for t in range(4):
+            x = rng.normal(size=H_).astype(np.float32)
+            ro, ri, _, _ = po.LayerView(model, 0).moe_layer(x)
+            out = empty(H_)
+            idx, _ = ctx.moe_decode(0, dev(x), out, want_route=True)
+            assert np.array_equal(idx, ri), (t, idx, ri)
+            e = rel_err(host(out), ro)
+            assert e <= TOL, (t, e)
+    finally:
+        ctx.close()
+    log(f"one-poll limit: {gave_up} of 4 launches gave up (E_DEVICE, NaN layer); default limit after: picks and "
+        f"outputs the oracle's on 4 tokens")

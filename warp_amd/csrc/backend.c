@@ -350,6 +350,7 @@ struct warp_hip_ctx {
     float *logits;
     unsigned long long *cert_ctr;  /* certified decode routings that recomputed, rows recomputed */
     unsigned *cert_sync;           /* the certifying router's launch counter and tagged rows (after cert_ctr) */
+    unsigned cert_polls;           /* its poll limit (0: the kernel's default) */
     warp_hip_route_stats route_stats;
     int *idx;
     float *w;
@@ -485,7 +486,11 @@ static int ctx_alloc(warp_hip_ctx *c)
     DMALLOC(c, c->idx, P * 4);
     DMALLOC(c, c->w, P * 4);
     DMALLOC(c, c->jobs, (size_t)3 * c->max_jobs * sizeof(warp_job));
+    /* zeroed, with the counts: lists read before any routing has written
+     * them hold no jobs and NULL records */
+    DEV(c, hipMemset(c->jobs, 0, (size_t)3 * c->max_jobs * sizeof(warp_job)));
     DMALLOC(c, c->njobs, 4 * sizeof(int));
+    DEV(c, hipMemset(c->njobs, 0, 4 * sizeof(int)));
     DMALLOC(c, c->missing, sizeof(int));
     DMALLOC(c, c->xs, (size_t)T * Hm * 2 * 2);
     DMALLOC(c, c->xscale, (size_t)T * 4);
@@ -755,6 +760,14 @@ static int take_missing(warp_hip_ctx *c)
     if (*c->h_missing) {
         const int flag = *c->h_missing;
         DEV(c, hipMemset(c->missing, 0, sizeof(int)));
+        if ((flag & 4) && c->cert_sync) {
+            /* a certifying router that gave up advanced its launch counter
+             * with a row possibly not yet written; written late, that row
+             * carries the next launch's tag: once every launch is done, the
+             * counter and the tagged rows start again from zero */
+            DEV(c, hipStreamSynchronize(c->st));
+            DEV(c, hipMemset(c->cert_sync, 0, WK_CERT_SYNC_WORDS(c->cfg.n_experts) * sizeof(unsigned)));
+        }
         if (flag & 4)
             return set_err(c, WARP_HIP_E_DEVICE, -1, -1,
                            "a decode launch gave up waiting (the fused launch for its work items, or the "
@@ -1566,6 +1579,13 @@ int warp_hip_set_router_fast(warp_hip_ctx *c, int fast)
     return 0;
 }
 
+int warp_hip_set_cert_polls(warp_hip_ctx *c, unsigned polls)
+{
+    if (!c) return WARP_HIP_E_ARG;
+    c->cert_polls = polls;
+    return 0;
+}
+
 int warp_hip_set_timing(warp_hip_ctx *c, int on)
 {
     if (!c) return WARP_HIP_E_ARG;
@@ -1893,7 +1913,7 @@ int warp_hip_moe_decode(warp_hip_ctx *c, int layer, const float *x_dev, float *o
         const warp_route_args pick = { NULL, NULL, table, E, g->router_act, g->renorm, I, g->routed_scale, c->idx,
                                        c->w, c->jobs, c->njobs, c->missing, 2, NULL, NULL, 0, NULL };
         KRN(c, wk_router_cert(L->router, x_dev, E, H, L->bias, c->logits, c->cert_sync, K, c->cert_ctr, c->missing,
-                              cert_route ? &pick : NULL, c->st));
+                              cert_route ? &pick : NULL, c->cert_polls, c->st));
     }
     else if (fuse_shared && !sh_in_gu) KRN(c, wk_router_shared(L->router, x_dev, E, H, c->logits, &sa, c->st));
     else if (scored) KRN(c, wk_router_scored(L->router, x_dev, E, H, L->bias, c->logits, c->st));
@@ -2448,7 +2468,7 @@ int warp_hip_router_cert(warp_hip_ctx *c, int layer, const float *x_dev, float *
     const layer_t *L = &c->L[layer];
     if (!L->router || g->router_act != WARP_HIP_ROUTE_SIGMOID)
         return set_err(c, WARP_HIP_E_ARG, layer, -1, "certified router needs an F32 router and sigmoid scores");
-    KRN(c, wk_router_cert(L->router, x_dev, g->n_experts, g->hidden, L->bias, out_dev, NULL, 0, NULL, NULL, NULL,
+    KRN(c, wk_router_cert(L->router, x_dev, g->n_experts, g->hidden, L->bias, out_dev, NULL, 0, NULL, NULL, NULL, 0,
                           c->st));
     DEV(c, hipStreamSynchronize(c->st));
     return 0;

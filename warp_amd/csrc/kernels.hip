@@ -680,8 +680,9 @@ struct CertTail {
     unsigned *sync;
     int K;
     unsigned long long *cctr;
-    int *flag;                  // a wait past CERT_POLLS sets bit 2 (value 4)
+    int *flag;                  // a wait past the poll limit sets bit 2 (value 4)
     warp_route_args pk;         // pk.idx set: the routing's outputs (idx, w; with pk.table the job lists)
+    unsigned polls;             // the poll limit (0: CERT_POLLS)
 };
 constexpr unsigned CERT_POLLS = 1u << 16;   // polls of the rows' values before the last block gives up
 
@@ -870,12 +871,12 @@ static bool router_cert_b(const float *W, const float *x, int E, int H, const fl
 
 extern "C" int wk_router_cert(const float *W, const float *x, int E, int H, const float *bias, float *out,
                               unsigned *sync, int K, unsigned long long *cctr, int *flag,
-                              const warp_route_args *pick, void *stream) {
+                              const warp_route_args *pick, unsigned polls, void *stream) {
     if (E <= 0 || H <= 0 || (H & 3) || H > 1024 * CERT_MAXV) return -1;
     if (sync && (K <= 0 || K > WARP_MAX_K || K > E || E > CERT_EMAX || ((uintptr_t)sync & 7))) return -1;
     if (pick && (!sync || !pick->idx || !pick->w || (pick->table && (!pick->jobs || !pick->njobs || !flag))))
         return -1;
-    CertTail t = {sync, K, cctr, flag, {}};
+    CertTail t = {sync, K, cctr, flag, {}, polls};
     if (pick) t.pk = *pick;
     // hidden sizes of the reference's models (Kimi-Linear 2304, K3 7168) and
     // their neighbours take the staged kernel
@@ -2375,7 +2376,7 @@ __device__ void cert_last(const float *__restrict__ W, const float *__restrict__
             }
         }
         if (__syncthreads_and(pend == 0)) break;          // uniform
-        if (n >= CERT_POLLS) {
+        if (n >= (t.polls ? t.polls : CERT_POLLS)) {
             if (tid == 0) cl_last = 0;
             break;
         }
@@ -2385,6 +2386,18 @@ __device__ void cert_last(const float *__restrict__ W, const float *__restrict__
     if (tid == 0) __hip_atomic_store(t.sync, ct.tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // the next launch's
     if (!cl_last) {                                       // (never in practice)
         if (tid == 0 && t.flag) __hip_atomic_fetch_or(t.flag, 4, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // empty job lists: the launches after this one skip their work (and
+        // the combine, seeing the flag, writes NaN) rather than read the
+        // lists a previous launch left
+        if (t.pk.idx && t.pk.table) {
+            for (int i = tid; i < 3 * t.K; i += NT) {
+                warp_job *jo = t.pk.jobs + i;
+                jo->idx = nullptr;
+                jo->scale = nullptr;
+                jo->n = 0;
+            }
+            if (tid < 3) t.pk.njobs[tid] = 0;
+        }
         return;
     }
     warp_route_args r = {};

@@ -105,15 +105,18 @@ int wk_router_scored(const float *W, const float *x, int E, int H, const float *
  * order the bounds leave open with their exact (sequential) values, so that
  * a routing from [0, 2E) (scored = 1) picks the reference's experts in its
  * order; cctr as in warp_route_args; flag (or NULL): bit 2 (value 4) set
- * when the last block's wait for the rows gives up. E <= 4096 with done.
- * pick (with done, or NULL): the last block also writes what wk_route
+ * when the last block's wait for the rows gives up, after polls polls (0:
+ * 65,536). E <= 4096 with sync.
+ * pick (with sync, or NULL): the last block also writes what wk_route
  * writes from those arrays -- pick->idx and pick->w (renorm, routed_scale),
  * and with pick->table the job lists (pick->jobs, njobs, inter; a pick
- * without a record sets *flag) -- so that no routing launch follows. */
+ * without a record sets *flag; a wait that gave up leaves them empty) --
+ * so that no routing launch follows. */
 struct warp_route_args_s;
 #define WK_CERT_SYNC_WORDS(E) (2 + 8 * (size_t)(E))  /* a launch counter, then [E][4] 64-bit tagged values */
 int wk_router_cert(const float *W, const float *x, int E, int H, const float *bias, float *out, unsigned *sync,
-                   int K, unsigned long long *cctr, int *flag, const struct warp_route_args_s *pick, void *stream);
+                   int K, unsigned long long *cctr, int *flag, const struct warp_route_args_s *pick, unsigned polls,
+                   void *stream);
 
 /* Quantised router / dense trunk rows (Q8G, Q4G, Q3G with the reference's
  * packing): y [T][M] = dequant(W) [M][N] . x [T][N]. */

@@ -141,6 +141,7 @@ SIGNATURES = {
     "warp_hip_put_expert_synth": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_uint64, C.c_void_p]),
     "warp_hip_set_matvec_path": (C.c_int, [C.c_void_p, C.c_int]),
     "warp_hip_set_router_fast": (C.c_int, [C.c_void_p, C.c_int]),
+    "warp_hip_set_cert_polls": (C.c_int, [C.c_void_p, C.c_uint]),
     "warp_hip_matvec_kernel": (C.c_char_p, [C.c_void_p, C.c_int, C.c_int]),
     "warp_hip_set_timing": (C.c_int, [C.c_void_p, C.c_int]),
     "warp_hip_get_timing": (C.c_int, [C.c_void_p, C.POINTER(C.c_double), C.POINTER(C.c_uint64)]),
@@ -399,6 +400,11 @@ class Context:
         """True: decode from the fast logits' picks uncertified; False: certify."""
         self._check(lib().warp_hip_set_router_fast(self.h, int(bool(fast))))
         self.cfg.router_fast = int(bool(fast))
+
+    def set_cert_polls(self, polls):
+        """The certifying router's poll limit for its rows (0: the default);
+        a launch that reaches it gives up and the next sync reports E_DEVICE."""
+        self._check(lib().warp_hip_set_cert_polls(self.h, int(polls)))
 
     def matvec_kernel(self, layer, expert_ffn=False):
         """The expert matvec kernel a decode of `layer` runs on the current path."""
