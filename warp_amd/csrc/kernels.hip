@@ -3104,7 +3104,10 @@ __global__ __launch_bounds__(1024) void k_vq_run_f16(VqArgs a, const int *__rest
             if (npg_full + k < npg) step(k, npg_full + k);    // uniform
         l = rq_take(rq, lane);                                // returns while the outputs are stored
         // lane (g, jc) holds C[4g + r][jc] of row tile t: block row
-        // 16g + 4r + t, token jc % 8 of job 2 q + jc / 8
+        // 16g + 4r + t, token jc % 8 of job 2 q + jc / 8 -- the 16
+        // consecutive rows 16g .. 16g + 15 of one token, stored as four
+        // 16-byte runs (4-byte stores, 64 B apart across the lanes, left
+        // partial lines in the L2: the down launch wrote 3.9x its output)
 #pragma unroll
         for (int q = 0; q < RB; q++) {
             if (2 * q >= nt) break;                           // uniform
@@ -3113,13 +3116,22 @@ __global__ __launch_bounds__(1024) void k_vq_run_f16(VqArgs a, const int *__rest
             const bool tv = jq_i < nt && tk < jq.n;
             const int yrow = tv ? jq.yi[tk] : 0;
             const float xsc = tv ? a.xscale[yrow] : 0.0f;
+            float *yo = a.y[kind] + (size_t)yrow * M;
 #pragma unroll
-            for (int t = 0; t < 4; t++)
+            for (int r = 0; r < 4; r++) {
+                const int row = rb * 64 + 16 * g + 4 * r;
+                if ((M & 3) == 0) {                           // uniform: rows row .. row + 3 together
+                    if (tv && row < M)
+                        *(float4 *)(yo + row) = make_float4((acc[q][0][r] * xsc) * f16_keep(jq.scale[row]),
+                                                            (acc[q][1][r] * xsc) * f16_keep(jq.scale[row + 1]),
+                                                            (acc[q][2][r] * xsc) * f16_keep(jq.scale[row + 2]),
+                                                            (acc[q][3][r] * xsc) * f16_keep(jq.scale[row + 3]));
+                } else {
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int row = rb * 64 + 16 * g + 4 * r + t;
-                    if (tv && row < M) a.y[kind][(size_t)yrow * M + row] = (acc[q][t][r] * xsc) * f16_keep(jq.scale[row]);
+                    for (int t = 0; t < 4; t++)
+                        if (tv && row + t < M) yo[row + t] = (acc[q][t][r] * xsc) * f16_keep(jq.scale[row + t]);
                 }
+            }
         }
     }
     rq_leave(rq, lane, 1);
@@ -3144,6 +3156,8 @@ extern "C" int wk_vq_runs(int fmt, const warp_job *jobs, const int *njobs, int m
     if (M <= 0 || N <= 0 || (N % 32) || max_jobs <= 0 || !runs || !queue || kind_lo < 0 || nkinds < 1 || kind_lo + nkinds > 3 ||
         fp16_rows < 0 || (size_t)fp16_rows * N * 2 >= ((size_t)1 << 31))
         return -1;
+    for (int k = kind_lo; k < kind_lo + nkinds; k++)
+        if ((uintptr_t)y[k] & 15) return -1;                // (16-byte row stores)
     const int fp16 = fp16_rows > 0;
     VqArgs a{};
     a.jobs = jobs;
