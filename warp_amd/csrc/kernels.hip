@@ -2950,7 +2950,8 @@ __global__ __launch_bounds__(512) void k_vq_mfma_run(VqArgs a, const int *__rest
             if (npg_full + k < npg) step(k, npg_full + k);    // uniform
         l = rq_take(rq, lane);                                // returns while the outputs are stored
         // lane (g, jc) holds C[4g + r][jc] of row tile t: block row 16g + 4r + t,
-        // token slot jc / 2 of the job, half jc % 2
+        // token slot jc / 2 of the job, half jc % 2 -- the 16 consecutive rows
+        // 16g .. 16g + 15, stored as four 16-byte runs
 #pragma unroll
         for (int q = 0; q < RJ; q++) {
             if (q >= nt) break;                               // uniform
@@ -2958,14 +2959,25 @@ __global__ __launch_bounds__(512) void k_vq_mfma_run(VqArgs a, const int *__rest
             const bool tv = hl == 0 && ts < jq.n;
             const float xsc = tv ? a.xscale[jq.xi[ts]] : 0.0f;
             const int yrow = tv ? jq.yi[ts] : 0;
+            float *yo = a.y[kind] + (size_t)yrow * M;
 #pragma unroll
-            for (int t = 0; t < 4; t++)
+            for (int r = 0; r < 4; r++) {
+                float v[4];
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const float v = acc[q][t][r] + __shfl_xor(acc[q][t][r], 1);
-                    const int row = rb * 64 + 16 * g + 4 * r + t;
-                    if (tv && row < M) a.y[kind][(size_t)yrow * M + row] = (v * xsc) * f16_keep(jq.scale[row]);
+                for (int t = 0; t < 4; t++) v[t] = acc[q][t][r] + __shfl_xor(acc[q][t][r], 1);
+                const int row = rb * 64 + 16 * g + 4 * r;
+                if ((M & 3) == 0) {                           // uniform: rows row .. row + 3 together
+                    if (tv && row < M)
+                        *(float4 *)(yo + row) = make_float4((v[0] * xsc) * f16_keep(jq.scale[row]),
+                                                            (v[1] * xsc) * f16_keep(jq.scale[row + 1]),
+                                                            (v[2] * xsc) * f16_keep(jq.scale[row + 2]),
+                                                            (v[3] * xsc) * f16_keep(jq.scale[row + 3]));
+                } else {
+#pragma unroll
+                    for (int t = 0; t < 4; t++)
+                        if (tv && row + t < M) yo[row + t] = (v[t] * xsc) * f16_keep(jq.scale[row + t]);
                 }
+            }
         }
     }
     rq_leave(rq, lane, 1);
