@@ -3117,9 +3117,11 @@ __global__ __launch_bounds__(1024) void k_vq_run_f16(VqArgs a, const int *__rest
         l = rq_take(rq, lane);                                // returns while the outputs are stored
         // lane (g, jc) holds C[4g + r][jc] of row tile t: block row
         // 16g + 4r + t, token jc % 8 of job 2 q + jc / 8 -- the 16
-        // consecutive rows 16g .. 16g + 15 of one token, stored as four
-        // 16-byte runs (4-byte stores, 64 B apart across the lanes, left
-        // partial lines in the L2: the down launch wrote 3.9x its output)
+        // consecutive rows 16g .. 16g + 15 of one token. The four lanes of a
+        // token (g = 0..3) swap their 16-byte runs (a 4 x 4 transpose by
+        // lane xors 16, 32, 48), so that store k writes rows 16k .. 16k + 15
+        // as one 64-byte sector: stored one float at a time the down launch
+        // wrote 3.9x its output, as 16-byte runs 64 B apart 1.75x.
 #pragma unroll
         for (int q = 0; q < RB; q++) {
             if (2 * q >= nt) break;                           // uniform
@@ -3129,20 +3131,40 @@ __global__ __launch_bounds__(1024) void k_vq_run_f16(VqArgs a, const int *__rest
             const int yrow = tv ? jq.yi[tk] : 0;
             const float xsc = tv ? a.xscale[yrow] : 0.0f;
             float *yo = a.y[kind] + (size_t)yrow * M;
+            if ((M & 63) == 0) {                              // uniform: whole 64-row blocks
+                // w[d][t]: what round d brings from lane g ^ d, its row
+                // 16 (g ^ d) + 4 g + t
+                float w[4][4];
+                auto pick = [](const float *u, int i) { return i == 0 ? u[0] : i == 1 ? u[1] : i == 2 ? u[2] : u[3]; };
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int row = rb * 64 + 16 * g + 4 * r;
-                if ((M & 3) == 0) {                           // uniform: rows row .. row + 3 together
-                    if (tv && row < M)
-                        *(float4 *)(yo + row) = make_float4((acc[q][0][r] * xsc) * f16_keep(jq.scale[row]),
-                                                            (acc[q][1][r] * xsc) * f16_keep(jq.scale[row + 1]),
-                                                            (acc[q][2][r] * xsc) * f16_keep(jq.scale[row + 2]),
-                                                            (acc[q][3][r] * xsc) * f16_keep(jq.scale[row + 3]));
-                } else {
+                for (int t = 0; t < 4; t++) {
+                    float v[4];                               // rows 16 g + 4 r + t
 #pragma unroll
-                    for (int t = 0; t < 4; t++)
-                        if (tv && row + t < M) yo[row + t] = (acc[q][t][r] * xsc) * f16_keep(jq.scale[row + t]);
+                    for (int r = 0; r < 4; r++)
+                        v[r] = (acc[q][t][r] * xsc) * f16_keep(jq.scale[rb * 64 + 16 * g + 4 * r + t]);
+#pragma unroll
+                    for (int d = 0; d < 4; d++) {             // round d: v[g ^ d] to lane g ^ d
+                        const float sv = pick(v, g ^ d);
+                        w[d][t] = d == 0 ? sv : __shfl_xor(sv, 16 * d);
+                    }
                 }
+#pragma unroll
+                for (int k = 0; k < 4; k++) {                 // rows 16 k + 4 g .. + 3: round g ^ k's
+                    const int d = g ^ k;
+                    const float4 o = make_float4(d == 0 ? w[0][0] : d == 1 ? w[1][0] : d == 2 ? w[2][0] : w[3][0],
+                                                 d == 0 ? w[0][1] : d == 1 ? w[1][1] : d == 2 ? w[2][1] : w[3][1],
+                                                 d == 0 ? w[0][2] : d == 1 ? w[1][2] : d == 2 ? w[2][2] : w[3][2],
+                                                 d == 0 ? w[0][3] : d == 1 ? w[1][3] : d == 2 ? w[2][3] : w[3][3]);
+                    if (tv) *(float4 *)(yo + rb * 64 + 16 * k + 4 * g) = o;
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+#pragma unroll
+                    for (int t = 0; t < 4; t++) {
+                        const int row = rb * 64 + 16 * g + 4 * r + t;
+                        if (tv && row < M) yo[row] = (acc[q][t][r] * xsc) * f16_keep(jq.scale[row]);
+                    }
             }
         }
     }
