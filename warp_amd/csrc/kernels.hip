@@ -2960,23 +2960,42 @@ __global__ __launch_bounds__(512) void k_vq_mfma_run(VqArgs a, const int *__rest
             const float xsc = tv ? a.xscale[jq.xi[ts]] : 0.0f;
             const int yrow = tv ? jq.yi[ts] : 0;
             float *yo = a.y[kind] + (size_t)yrow * M;
+            if ((M & 63) == 0) {                              // uniform: whole 64-row blocks
+                // the same 4 x 4 transpose as the reduced-precision kernel's:
+                // store k writes rows 16k .. 16k + 15 as one 64-byte sector
+                float w[4][4];
+                auto pick = [](const float *u, int i) { return i == 0 ? u[0] : i == 1 ? u[1] : i == 2 ? u[2] : u[3]; };
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                float v[4];
+                for (int t = 0; t < 4; t++) {
+                    float v[4];                               // rows 16 g + 4 r + t
 #pragma unroll
-                for (int t = 0; t < 4; t++) v[t] = acc[q][t][r] + __shfl_xor(acc[q][t][r], 1);
-                const int row = rb * 64 + 16 * g + 4 * r;
-                if ((M & 3) == 0) {                           // uniform: rows row .. row + 3 together
-                    if (tv && row < M)
-                        *(float4 *)(yo + row) = make_float4((v[0] * xsc) * f16_keep(jq.scale[row]),
-                                                            (v[1] * xsc) * f16_keep(jq.scale[row + 1]),
-                                                            (v[2] * xsc) * f16_keep(jq.scale[row + 2]),
-                                                            (v[3] * xsc) * f16_keep(jq.scale[row + 3]));
-                } else {
+                    for (int r = 0; r < 4; r++)
+                        v[r] = ((acc[q][t][r] + __shfl_xor(acc[q][t][r], 1)) * xsc) *
+                               f16_keep(jq.scale[rb * 64 + 16 * g + 4 * r + t]);
 #pragma unroll
-                    for (int t = 0; t < 4; t++)
-                        if (tv && row + t < M) yo[row + t] = (v[t] * xsc) * f16_keep(jq.scale[row + t]);
+                    for (int d = 0; d < 4; d++) {
+                        const float sv = pick(v, g ^ d);
+                        w[d][t] = d == 0 ? sv : __shfl_xor(sv, 16 * d);
+                    }
                 }
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const int d = g ^ k;
+                    const float4 o = make_float4(d == 0 ? w[0][0] : d == 1 ? w[1][0] : d == 2 ? w[2][0] : w[3][0],
+                                                 d == 0 ? w[0][1] : d == 1 ? w[1][1] : d == 2 ? w[2][1] : w[3][1],
+                                                 d == 0 ? w[0][2] : d == 1 ? w[1][2] : d == 2 ? w[2][2] : w[3][2],
+                                                 d == 0 ? w[0][3] : d == 1 ? w[1][3] : d == 2 ? w[2][3] : w[3][3]);
+                    if (tv) *(float4 *)(yo + rb * 64 + 16 * k + 4 * g) = o;
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+#pragma unroll
+                    for (int t = 0; t < 4; t++) {
+                        const float v = acc[q][t][r] + __shfl_xor(acc[q][t][r], 1);
+                        const int row = rb * 64 + 16 * g + 4 * r + t;
+                        if (tv && row < M) yo[row] = (v * xsc) * f16_keep(jq.scale[row]);
+                    }
             }
         }
     }
