@@ -17,6 +17,8 @@ outside the bar.
 - 512 tokens: token order changes no result bit, and every token stays
   within the bar of the exact mode's chunk output;
 - chunks of 1, 3 and 9 tokens (runs of a single partial job);
+- rows that do not fill 64-row blocks (hidden 160, intermediate 96), both
+  modes;
 - more distinct experts than cache slots (windows), bit-identical to a
   cache that holds them all.
 """
@@ -125,6 +127,31 @@ def test_fp16_small_chunks(T):
         e = rel_err(out, ro)
         assert e <= TOL16, (T, e)
         log(f"fp16 chunk of {T} tokens: rel err {e:.2e}")
+    finally:
+        ctx.close()
+
+
+@pytest.mark.parametrize("fp16", [True, False])
+def test_chunk_rows_not_a_multiple_of_64(fp16):
+    """Hidden 160 and intermediate 96: neither launch's rows fill whole
+    64-row blocks, so the run kernels store their outputs one row at a time
+    instead of as transposed 64-byte sectors; both modes against the oracle
+    (2e-3 reduced precision, 1e-4 exact)."""
+    import warp_amd
+    spec = ct.Spec(hidden=160, inter=96, experts=16, top_k=4, layers=1, fmt="VQ12", seed=29, subnormals=False,
+                   keep_codes=False, **BALANCED)
+    model = ct.build(spec)
+    T = 40
+    ctx = open_ctx(model, max_tokens=T, prefill_fp16=fp16)
+    try:
+        warp_amd.load_container_model(ctx, model)
+        X = np.random.default_rng(29).normal(size=(T, spec.hidden)).astype(np.float32)
+        out, route, _ = ctx.moe_chunk_host(0, X)
+        ro, rr, _ = po.LayerView(model, 0).moe_chunk(X)
+        assert np.array_equal(route, rr)
+        e = rel_err(out, ro)
+        assert e <= (TOL16 if fp16 else 1e-4), (fp16, e)
+        log(f"chunk of {T} tokens at hidden 160 / inter 96 ({'fp16' if fp16 else 'exact'}): rel err {e:.2e}")
     finally:
         ctx.close()
 
